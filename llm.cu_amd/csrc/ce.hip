@@ -1,0 +1,161 @@
+// ce.hip — fused softmax + NLL + dlogits over the 151936-wide vocabulary.
+//
+// Restates src/kernels/loss.cu:13-91 (one block per row, three sweeps over
+// the row, host-side sum) for gfx950: with only T = 128 rows and 256 CUs,
+// each row is split into CE_CHUNK-wide chunks so the grid has T * chunks
+// workgroups.
+//   phase 1: per chunk, an online (max, sum exp(x - max)) pair -> stats.
+//   phase 2: merge the row's pairs into lse = m + ln Z, then for every j
+//            p = exp(x_j - lse), g = p - 1[j = t], and write the fp32 dlogits
+//            g / n_valid and/or the fp16 operand g * 2^14 for the lm_head dX
+//            GEMM (the scale keeps p ~ 1/V out of fp16 subnormals; the GEMM
+//            epilogue divides it out exactly).  The chunk's second read hits
+//            L2 / MALL (the 77.8 MB of logits fit in the 256 MB MALL).
+//   phase 3: one workgroup sums the per-row losses in a fixed order.
+// Rows i with (i % seq_len) == seq_len - 1 have no target inside their
+// window (loss.cu:18-21); their loss is 0 and their dlogits row is written
+// as zeros (the reference leaves it uninitialised).
+#include "ops.h"
+
+namespace llmt {
+
+namespace {
+
+constexpr int CE_THREADS = 256;
+constexpr int CE_CHUNK = 8192;  // floats per workgroup chunk (32 KB)
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LN2 = 0.6931471805599453f;
+
+__device__ __forceinline__ void merge(float& m, float& s, float m2, float s2) {
+  const float mn = fmaxf(m, m2);
+  if (mn == -INFINITY) return;
+  s = s * exp2f((m - mn) * LOG2E) + s2 * exp2f((m2 - mn) * LOG2E);
+  m = mn;
+}
+
+__global__ __launch_bounds__(CE_THREADS) void ce_phase1(const float* __restrict__ logits, int V,
+                                                        int chunks, float2* __restrict__ stats) {
+  const int row = blockIdx.y, ch = blockIdx.x;
+  const float* x = logits + (long long)row * V;
+  const int j0 = ch * CE_CHUNK;
+  const int j1 = min(V, j0 + CE_CHUNK);
+  float m = -INFINITY, s = 0.f;
+  // 16-byte loads; V is a multiple of 4 for every supported vocabulary.
+  for (int j = j0 + threadIdx.x * 4; j < j1; j += CE_THREADS * 4) {
+    const float4 v = *reinterpret_cast<const float4*>(x + j);
+    const float mx = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
+    const float mn = fmaxf(m, mx);
+    s = s * exp2f((m - mn) * LOG2E) + exp2f((v.x - mn) * LOG2E) + exp2f((v.y - mn) * LOG2E) +
+        exp2f((v.z - mn) * LOG2E) + exp2f((v.w - mn) * LOG2E);
+    m = mn;
+  }
+  // wave then block merge of (m, s)
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float m2 = __shfl_xor(m, o, 64), s2 = __shfl_xor(s, o, 64);
+    merge(m, s, m2, s2);
+  }
+  __shared__ float rm[CE_THREADS / 64], rs[CE_THREADS / 64];
+  if ((threadIdx.x & 63) == 0) {
+    rm[threadIdx.x >> 6] = m;
+    rs[threadIdx.x >> 6] = s;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float M = rm[0], S = rs[0];
+    for (int i = 1; i < CE_THREADS / 64; ++i) merge(M, S, rm[i], rs[i]);
+    stats[(long long)row * chunks + ch] = make_float2(M, S);
+  }
+}
+
+__global__ __launch_bounds__(CE_THREADS) void ce_phase2(const float* __restrict__ logits,
+                                                        const int* __restrict__ targets, int V,
+                                                        int seq_len, int chunks, float inv_valid,
+                                                        const float2* __restrict__ stats,
+                                                        float* __restrict__ dlogits,
+                                                        _Float16* __restrict__ grad16,
+                                                        float* __restrict__ loss_rows) {
+  const int row = blockIdx.y, ch = blockIdx.x;
+  const bool valid = (row % seq_len) != seq_len - 1;
+  const int j0 = ch * CE_CHUNK;
+  const int j1 = min(V, j0 + CE_CHUNK);
+  const long long base = (long long)row * V;
+  if (!valid) {
+    for (int j = j0 + threadIdx.x * 4; j < j1; j += CE_THREADS * 4) {
+      if (dlogits) *reinterpret_cast<float4*>(dlogits + base + j) = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (grad16) {
+        half4 z = {(_Float16)0.f, (_Float16)0.f, (_Float16)0.f, (_Float16)0.f};
+        *reinterpret_cast<half4*>(grad16 + base + j) = z;
+      }
+    }
+    if (ch == 0 && threadIdx.x == 0) loss_rows[row] = 0.f;
+    return;
+  }
+  float M = -INFINITY, S = 0.f;
+  for (int c = 0; c < chunks; ++c) {
+    const float2 p = stats[(long long)row * chunks + c];
+    merge(M, S, p.x, p.y);
+  }
+  const float lse = M + __logf(S);
+  // Out-of-range ids are clamped (never read out of bounds); the reference
+  // does not check them.
+  const int t = min(max(targets[row], 0), V - 1);
+  if (ch == 0 && threadIdx.x == 0) loss_rows[row] = lse - logits[base + t];
+  const float* x = logits + base;
+  for (int j = j0 + threadIdx.x * 4; j < j1; j += CE_THREADS * 4) {
+    const float4 v = *reinterpret_cast<const float4*>(x + j);
+    float g[4] = {exp2f((v.x - lse) * LOG2E), exp2f((v.y - lse) * LOG2E),
+                  exp2f((v.z - lse) * LOG2E), exp2f((v.w - lse) * LOG2E)};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (j + i == t) g[i] -= 1.0f;
+    if (dlogits)
+      *reinterpret_cast<float4*>(dlogits + base + j) =
+          make_float4(g[0] * inv_valid, g[1] * inv_valid, g[2] * inv_valid, g[3] * inv_valid);
+    if (grad16) {
+      half4 h = {(_Float16)(g[0] * kGradLogitScale), (_Float16)(g[1] * kGradLogitScale),
+                 (_Float16)(g[2] * kGradLogitScale), (_Float16)(g[3] * kGradLogitScale)};
+      *reinterpret_cast<half4*>(grad16 + base + j) = h;
+    }
+  }
+}
+
+// Deterministic mean over valid rows (fixed summation order).
+__global__ __launch_bounds__(CE_THREADS) void ce_mean(const float* __restrict__ loss_rows, int rows,
+                                                      float inv_valid, float* __restrict__ out) {
+  __shared__ float red[CE_THREADS / 64];
+  float s = 0.f;
+  for (int i = threadIdx.x; i < rows; i += CE_THREADS) s += loss_rows[i];
+  s = block_sum<CE_THREADS / 64>(s, red);
+  if (threadIdx.x == 0) *out = s * inv_valid;
+}
+
+}  // namespace
+
+int ce_chunks(int V) { return (V + CE_CHUNK - 1) / CE_CHUNK; }
+
+hipError_t cross_entropy(const float* logits, const int* targets, int rows, int V, int seq_len,
+                         float2* stats, float* dlogits, _Float16* grad16, float* loss_rows,
+                         float* loss_mean, hipStream_t st) {
+  if (V % 4 || seq_len < 2 || rows % seq_len) {
+    set_error("cross_entropy: unsupported V=%d seq_len=%d rows=%d", V, seq_len, rows);
+    return hipErrorInvalidValue;
+  }
+  const int chunks = ce_chunks(V);
+  const int n_valid = rows / seq_len * (seq_len - 1);
+  const float inv_valid = 1.0f / (float)n_valid;
+  hipLaunchKernelGGL(ce_phase1, dim3(chunks, rows), dim3(CE_THREADS), 0, st, logits, V, chunks,
+                     stats);
+  LLMT_LAUNCH_CHECK();
+  hipLaunchKernelGGL(ce_phase2, dim3(chunks, rows), dim3(CE_THREADS), 0, st, logits, targets, V,
+                     seq_len, chunks, inv_valid, stats, dlogits, grad16, loss_rows);
+  LLMT_LAUNCH_CHECK();
+  if (loss_mean) {
+    hipLaunchKernelGGL(ce_mean, dim3(1), dim3(CE_THREADS), 0, st, loss_rows, rows, inv_valid,
+                       loss_mean);
+    LLMT_LAUNCH_CHECK();
+  }
+  return hipSuccess;
+}
+
+}  // namespace llmt

@@ -1,0 +1,94 @@
+// common.h — shared device/host helpers for the gfx950 kernels of libllmt.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stdio.h>
+
+namespace llmt {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef int8_t int8x8 __attribute__((ext_vector_type(8)));
+
+// Error plumbing: every launcher returns hipError_t; the C ABI maps it to
+// LLMT_ERR_HIP and records a message.
+void set_error(const char* fmt, ...);
+
+#define LLMT_HIP_TRY(expr)                                                     \
+  do {                                                                         \
+    hipError_t e_ = (expr);                                                    \
+    if (e_ != hipSuccess) {                                                    \
+      ::llmt::set_error("%s:%d: %s: %s", __FILE__, __LINE__, #expr,            \
+                        hipGetErrorString(e_));                                \
+      return e_;                                                               \
+    }                                                                          \
+  } while (0)
+
+#define LLMT_LAUNCH_CHECK() LLMT_HIP_TRY(hipGetLastError())
+
+// fp16 MFMA 16x16x32, fp32 accumulate.  Operand k-order only has to agree
+// between A and B: every GEMM here loads both with lane group g = lane/16
+// holding k = 8g..8g+7 of the 32-wide step.  D: lane holds rows
+// 4*(lane/16)+v (v = 0..3) of column lane%16.
+__device__ __forceinline__ floatx4 mfma16(half8 a, half8 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Block-wide reductions for blocks of NW waves; `red` is LDS of >= NW floats.
+// Every thread gets the result.  Contains __syncthreads().
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) t += red[i];
+  __syncthreads();
+  return t;
+}
+
+template <int NW>
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = wave_max(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float t = red[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) t = fmaxf(t, red[i]);
+  __syncthreads();
+  return t;
+}
+
+// Power-of-two scale that maps a row maximum |x| into [2^13, 2^14): the fp16
+// gradient operands carry it per row and GEMM epilogues divide it back out
+// exactly.  amax == 0 gives scale 1.
+__device__ __forceinline__ float pow2_scale_for(float amax) {
+  if (!(amax > 0.f) || !isfinite(amax)) return 1.0f;
+  int e;
+  frexpf(amax, &e);  // amax = f * 2^e, f in [0.5, 1)
+  return ldexpf(1.0f, 14 - e);
+}
+
+__device__ __forceinline__ float h2f(_Float16 h) { return (float)h; }
+__device__ __forceinline__ _Float16 f2h(float f) { return (_Float16)f; }
+
+}  // namespace llmt
