@@ -196,7 +196,9 @@ const char* llmt_last_error(void);
 void llmt_dims_qwen3_1_7b(llmt_dims* out);
 
 /* Context for up to max_batch sequences of seq_len tokens (stashes and
- * workspaces are sized at creation).  stream may be NULL (null stream). */
+ * workspaces are sized at creation).  stream may be NULL: the context then
+ * creates its own stream, blocking with respect to the legacy default stream
+ * (a captured HIP graph needs a non-default stream). */
 int llmt_ctx_create(const llmt_dims* dims, int max_batch, int seq_len, int weight_format,
                     void* stream, llmt_ctx** out);
 int llmt_ctx_destroy(llmt_ctx* ctx);
@@ -258,6 +260,14 @@ int llmt_layer_forward(llmt_ctx* ctx, int layer, const float* x, float* y, int b
 int llmt_layer_backward(llmt_ctx* ctx, int layer, const float* dy, float* dx, int batch);
 /* AdamW over the whole arena (one multi-tensor launch). */
 int llmt_adamw(llmt_ctx* ctx, const llmt_hparams* hp, int step);
+/* One llmt_step run eagerly with a HIP event between consecutive kernels:
+ * cat_ms[c] receives the milliseconds spent in each kernel category
+ * (0 forward GEMMs, 1 backward GEMMs, 2 lm_head GEMMs, 3 attention, 4 row
+ * epilogues, 5 cross-entropy, 6 LoRA grads, 7 AdamW); gemm_flops and
+ * gemm_weight_bytes (may be NULL) the step's GEMM FLOPs and weight bytes. */
+int llmt_profile_step(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
+                      const llmt_hparams* hp, int step, float* cat_ms, int ncat,
+                      double* gemm_flops, double* gemm_weight_bytes);
 
 /* ---- standalone operators (stream may be NULL) ---- */
 

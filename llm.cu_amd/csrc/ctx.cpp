@@ -1,0 +1,490 @@
+// ctx.cpp — context set-up: buffer layout, frozen-weight upload (with the
+// pre-transposed copies the backward GEMMs stream), the reference's on-disk
+// weight and adapter formats, and the single-layer entry points of config C0.
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <vector>
+
+#include "ctx.h"
+
+using namespace llmt;
+
+#define TRY_ARG(cond, ...)    \
+  do {                        \
+    if (!(cond)) {            \
+      set_error(__VA_ARGS__); \
+      return LLMT_ERR_ARG;    \
+    }                         \
+  } while (0)
+
+#define TRY_HIP(expr)                                                   \
+  do {                                                                  \
+    hipError_t e__ = (expr);                                            \
+    if (e__ != hipSuccess) {                                            \
+      if (e__ != hipErrorInvalidValue || !llmt_last_error()[0])         \
+        set_error("%s: %s", #expr, hipGetErrorString(e__));             \
+      return e__ == hipErrorInvalidValue ? LLMT_ERR_ARG : LLMT_ERR_HIP; \
+    }                                                                   \
+  } while (0)
+
+#define TRY_PTR(p)                 \
+  do {                             \
+    if (!(p)) return LLMT_ERR_HIP; \
+  } while (0)
+
+namespace llmt {
+
+int Ctx::init() {
+  H = dims.hidden;
+  nq = dims.n_heads;
+  nkv = dims.n_kv_heads;
+  Q = nq * kHeadDim;
+  KV = nkv * kHeadDim;
+  NT = Q + 2 * KV;
+  I = dims.intermediate;
+  V = dims.vocab;
+  L = dims.n_layers;
+  Tmax = maxB * S;
+  lscale = dims.alpha / (float)dims.rank;
+  const long long R = kRank;
+
+  // adapter arena, per layer: q A, q B, k A, k B, v A, v B, o A, o B
+  const long long sz[8] = {R * H, (long long)Q * R, R * H, (long long)KV * R,
+                           R * H, (long long)KV * R, R * Q, (long long)H * R};
+  long long off = 0;
+  for (int i = 0; i < 8; ++i) {
+    seg_off[i] = off;
+    off += sz[i];
+  }
+  lora_per_layer = (size_t)off;
+  lora_numel = lora_per_layer * L;
+  sh_a_qkv = 0;
+  sh_a_o = 3 * R * H;
+  sh_bt_qkv = sh_a_o + R * Q;
+  sh_bt_o = sh_bt_qkv + 3 * R * NT;
+  shadow_per_layer = sh_bt_o + R * H;
+
+  TRY_PTR(lora_p = alloc_n<float>(lora_numel));
+  TRY_PTR(lora_g = alloc_n<float>(lora_numel));
+  TRY_PTR(lora_m = alloc_n<float>(lora_numel));
+  TRY_PTR(lora_v = alloc_n<float>(lora_numel));
+  TRY_PTR(shadow = alloc_n<_Float16>(shadow_per_layer * L));
+  TRY_PTR(hp_dev = alloc_n<AdamHp>(1));
+  TRY_HIP(hipMemset(lora_p, 0, lora_numel * sizeof(float)));
+  TRY_HIP(hipMemset(lora_g, 0, lora_numel * sizeof(float)));
+  TRY_HIP(hipMemset(lora_m, 0, lora_numel * sizeof(float)));
+  TRY_HIP(hipMemset(lora_v, 0, lora_numel * sizeof(float)));
+  TRY_HIP(hipMemset(shadow, 0, shadow_per_layer * L * sizeof(_Float16)));
+
+  // RoPE tables: angles in double, rounded once to fp32 (src/kernels/rope.cu:15-18).
+  {
+    std::vector<float> c((size_t)S * 64), s((size_t)S * 64);
+    for (int p = 0; p < S; ++p)
+      for (int d = 0; d < 64; ++d) {
+        const double freq = 1.0 / pow((double)dims.theta, 2.0 * d / kHeadDim);
+        const double ang = (double)p * freq;
+        c[(size_t)p * 64 + d] = (float)cos(ang);
+        s[(size_t)p * 64 + d] = (float)sin(ang);
+      }
+    TRY_PTR(cosT = alloc_n<float>(c.size()));
+    TRY_PTR(sinT = alloc_n<float>(s.size()));
+    TRY_HIP(hipMemcpy(cosT, c.data(), c.size() * sizeof(float), hipMemcpyHostToDevice));
+    TRY_HIP(hipMemcpy(sinT, s.data(), s.size() * sizeof(float), hipMemcpyHostToDevice));
+  }
+
+  // frozen weights
+  layers.resize(L);
+  const size_t mats[4][2] = {{(size_t)NT, (size_t)H}, {(size_t)H, (size_t)Q},
+                             {(size_t)2 * I, (size_t)H}, {(size_t)H, (size_t)I}};
+  const int esz = wfmt == LLMT_WEIGHTS_I8 ? 1 : 2;
+  for (int l = 0; l < L; ++l) {
+    Layer& w = layers[l];
+    WMat* fw[4] = {&w.wqkv, &w.wo, &w.wgu, &w.wd};
+    WMat* bw[4] = {&w.wqkvT, &w.woT, &w.wguT, &w.wdT};
+    for (int m = 0; m < 4; ++m) {
+      const size_t rows = mats[m][0], cols = mats[m][1];
+      void* f = alloc(rows * cols * esz);
+      void* b = alloc(rows * cols * esz);
+      TRY_PTR(f);
+      TRY_PTR(b);
+      fw[m]->p = f;
+      fw[m]->rows = (int)rows;
+      fw[m]->ld = (int)cols;
+      fw[m]->i8 = esz == 1;
+      bw[m]->p = b;
+      bw[m]->rows = (int)cols;
+      bw[m]->ld = (int)rows;
+      bw[m]->i8 = esz == 1;
+      if (esz == 1) {
+        _Float16* sc = alloc_n<_Float16>(rows);
+        TRY_PTR(sc);
+        fw[m]->colscale = sc;
+        bw[m]->kscale = sc;
+      }
+    }
+    float* nw = alloc_n<float>(2 * H + 2 * kHeadDim);
+    TRY_PTR(nw);
+    w.attn_norm = nw;
+    w.ffn_norm = nw + H;
+    w.q_norm = nw + 2 * H;
+    w.k_norm = nw + 2 * H + kHeadDim;
+  }
+  TRY_PTR(E = alloc_n<_Float16>((size_t)V * H));
+  TRY_PTR(ET = alloc_n<_Float16>((size_t)V * H));
+  TRY_PTR(final_norm = alloc_n<float>(H));
+
+  // per-layer stashes
+  const size_t T = Tmax;
+  stash.resize(L);
+  for (int l = 0; l < L; ++l) {
+    Stash& s = stash[l];
+    TRY_PTR(s.x_in = alloc_n<float>(T * H));
+    TRY_PTR(s.xn = alloc_n<_Float16>(T * H));
+    TRY_PTR(s.qkraw = alloc_n<float>(T * (Q + KV)));
+    TRY_PTR(s.qkv16 = alloc_n<_Float16>(T * NT));
+    TRY_PTR(s.h = alloc_n<float>(T * 64));
+    TRY_PTR(s.o16 = alloc_n<_Float16>(T * Q));
+    TRY_PTR(s.lse = alloc_n<float>((size_t)maxB * nq * S));
+    TRY_PTR(s.x_mid = alloc_n<float>(T * H));
+    TRY_PTR(s.xn2 = alloc_n<_Float16>(T * H));
+    TRY_PTR(s.gu = alloc_n<float>(T * 2 * I));
+  }
+  TRY_PTR(x_final = alloc_n<float>(T * H));
+  TRY_PTR(xf16 = alloc_n<_Float16>(T * H));
+  TRY_PTR(logits = alloc_n<float>(T * V));
+  TRY_PTR(grad16 = alloc_n<_Float16>(T * V));
+  TRY_PTR(ce_stats = alloc_n<float2>(T * ce_chunks(V)));
+  TRY_PTR(loss_rows = alloc_n<float>(T));
+  TRY_PTR(loss_dev = alloc_n<float>(1));
+  TRY_PTR(tok_buf = alloc_n<int>(T));
+  TRY_PTR(tgt_buf = alloc_n<int>(T));
+  TRY_HIP(hipMemset(tok_buf, 0, T * sizeof(int)));
+  TRY_HIP(hipMemset(tgt_buf, 0, T * sizeof(int)));
+
+  // split-K partials: the largest split * M * N over every GEMM of the step
+  const int shapes[9][2] = {{NT + 3 * kRank, H}, {H + kRank, Q}, {2 * I, H}, {H, I},
+                            {H, V},              {I, H},         {H, 2 * I}, {Q + kRank, H},
+                            {H + 3 * kRank, NT}};
+  part_elems = 0;
+  for (int b = 1; b <= maxB; ++b) {
+    const int M = b * S;
+    if (M % 16) continue;
+    for (auto& sh : shapes) {
+      const size_t e = (size_t)gemm_pick_split(M, sh[0], sh[1], 64) * M * sh[0];
+      if (e > part_elems) part_elems = e;
+    }
+  }
+  if (part_elems == 0) part_elems = 1;
+  TRY_PTR(part = alloc_n<float>(part_elems));
+  TRY_PTR(a16 = alloc_n<_Float16>(T * I));
+  TRY_PTR(d_res = alloc_n<float>(T * H));
+  TRY_PTR(dmid = alloc_n<float>(T * H));
+  TRY_PTR(g16 = alloc_n<_Float16>(T * (H > NT ? H : NT)));
+  TRY_PTR(rinv = alloc_n<float>(T));
+  TRY_PTR(rinv2 = alloc_n<float>(T));
+  TRY_PTR(dgu16 = alloc_n<_Float16>(T * 2 * I));
+  TRY_PTR(dO = alloc_n<float>(T * Q));
+  TRY_PTR(delta = alloc_n<float>((size_t)maxB * nq * S));
+  TRY_PTR(damax = alloc_n<float>(T));
+  TRY_PTR(dqkv32 = alloc_n<float>(T * NT));
+  TRY_PTR(dy32 = alloc_n<float>(T * NT));
+  TRY_PTR(dh = alloc_n<float>(T * 64));
+
+  TRY_HIP(hipHostMalloc((void**)&host_loss, sizeof(float), hipHostMallocDefault));
+  TRY_HIP(hipHostMalloc((void**)&host_hp, sizeof(AdamHp), hipHostMallocDefault));
+  *host_loss = 0.f;
+  TRY_HIP(hipDeviceSynchronize());
+  return LLMT_OK;
+}
+
+}  // namespace llmt
+
+static Ctx* C_(llmt_ctx* c) { return reinterpret_cast<Ctx*>(c); }
+
+// Copy a [rows, cols] fp16 matrix into rows [r0, r0 + rows) of dst (ld cols)
+// and its transpose into columns [r0, r0 + rows) of dstT (ld ldT).
+static hipError_t put_f16(Ctx* c, const void* src, int rows, int cols, const WMat& f, int r0,
+                          const WMat& b) {
+  _Float16* d = (_Float16*)f.p + (size_t)r0 * f.ld;
+  LLMT_HIP_TRY(hipMemcpyAsync(d, src, (size_t)rows * cols * 2, hipMemcpyDefault, c->st));
+  return transpose_f16((const _Float16*)src, rows, cols, cols, (_Float16*)b.p + r0, b.ld, c->st);
+}
+
+static hipError_t put_i8(Ctx* c, const int8_t* src, const void* scale, int rows, int cols,
+                         const WMat& f, int r0, const WMat& b) {
+  int8_t* d = (int8_t*)f.p + (size_t)r0 * f.ld;
+  LLMT_HIP_TRY(hipMemcpyAsync(d, src, (size_t)rows * cols, hipMemcpyDefault, c->st));
+  LLMT_HIP_TRY(hipMemcpyAsync((_Float16*)f.colscale + r0, scale, (size_t)rows * 2,
+                              hipMemcpyDefault, c->st));
+  return transpose_i8(src, rows, cols, cols, (int8_t*)b.p + r0, b.ld, c->st);
+}
+
+static int put_norms(Ctx* c, Layer& w, const float* attn_norm, const float* ffn_norm,
+                     const float* q_norm, const float* k_norm) {
+  TRY_ARG(attn_norm && ffn_norm && q_norm && k_norm, "norm weights must be given");
+  TRY_HIP(hipMemcpyAsync(w.attn_norm, attn_norm, c->H * 4, hipMemcpyDefault, c->st));
+  TRY_HIP(hipMemcpyAsync(w.ffn_norm, ffn_norm, c->H * 4, hipMemcpyDefault, c->st));
+  TRY_HIP(hipMemcpyAsync(w.q_norm, q_norm, kHeadDim * 4, hipMemcpyDefault, c->st));
+  TRY_HIP(hipMemcpyAsync(w.k_norm, k_norm, kHeadDim * 4, hipMemcpyDefault, c->st));
+  return LLMT_OK;
+}
+
+extern "C" {
+
+int llmt_set_layer_f16(llmt_ctx* ctx, int layer, const void* wq, const void* wk, const void* wv,
+                       const void* wo, const void* w_gate, const void* w_up, const void* w_down,
+                       const float* attn_norm, const float* ffn_norm, const float* q_norm,
+                       const float* k_norm) {
+  set_error("");
+  Ctx* c = C_(ctx);
+  TRY_ARG(c && layer >= 0 && layer < c->L, "llmt_set_layer_f16: bad ctx/layer");
+  TRY_ARG(c->wfmt == LLMT_WEIGHTS_F16, "context was created for int8 weights");
+  TRY_ARG(wq && wk && wv && wo && w_gate && w_up && w_down, "NULL weight");
+  Layer& w = c->layers[layer];
+  const int H = c->H, Q = c->Q, KV = c->KV, I = c->I;
+  TRY_HIP(put_f16(c, wq, Q, H, w.wqkv, 0, w.wqkvT));
+  TRY_HIP(put_f16(c, wk, KV, H, w.wqkv, Q, w.wqkvT));
+  TRY_HIP(put_f16(c, wv, KV, H, w.wqkv, Q + KV, w.wqkvT));
+  TRY_HIP(put_f16(c, wo, H, Q, w.wo, 0, w.woT));
+  TRY_HIP(put_f16(c, w_gate, I, H, w.wgu, 0, w.wguT));
+  TRY_HIP(put_f16(c, w_up, I, H, w.wgu, I, w.wguT));
+  TRY_HIP(put_f16(c, w_down, H, I, w.wd, 0, w.wdT));
+  int rc = put_norms(c, w, attn_norm, ffn_norm, q_norm, k_norm);
+  if (rc) return rc;
+  TRY_HIP(hipStreamSynchronize(c->st));
+  w.ready = true;
+  return LLMT_OK;
+}
+
+int llmt_set_layer_i8(llmt_ctx* ctx, int layer, const int8_t* const q[7],
+                      const void* const scale[7], const float* attn_norm, const float* ffn_norm,
+                      const float* q_norm, const float* k_norm) {
+  set_error("");
+  Ctx* c = C_(ctx);
+  TRY_ARG(c && layer >= 0 && layer < c->L, "llmt_set_layer_i8: bad ctx/layer");
+  TRY_ARG(c->wfmt == LLMT_WEIGHTS_I8, "context was created for fp16 weights");
+  TRY_ARG(q && scale, "NULL weight array");
+  for (int i = 0; i < 7; ++i) TRY_ARG(q[i] && scale[i], "NULL weight %d", i);
+  Layer& w = c->layers[layer];
+  const int H = c->H, Q = c->Q, KV = c->KV, I = c->I;
+  TRY_HIP(put_i8(c, q[0], scale[0], Q, H, w.wqkv, 0, w.wqkvT));
+  TRY_HIP(put_i8(c, q[1], scale[1], KV, H, w.wqkv, Q, w.wqkvT));
+  TRY_HIP(put_i8(c, q[2], scale[2], KV, H, w.wqkv, Q + KV, w.wqkvT));
+  TRY_HIP(put_i8(c, q[3], scale[3], H, Q, w.wo, 0, w.woT));
+  TRY_HIP(put_i8(c, q[4], scale[4], I, H, w.wgu, 0, w.wguT));
+  TRY_HIP(put_i8(c, q[5], scale[5], I, H, w.wgu, I, w.wguT));
+  TRY_HIP(put_i8(c, q[6], scale[6], H, I, w.wd, 0, w.wdT));
+  int rc = put_norms(c, w, attn_norm, ffn_norm, q_norm, k_norm);
+  if (rc) return rc;
+  TRY_HIP(hipStreamSynchronize(c->st));
+  w.ready = true;
+  return LLMT_OK;
+}
+
+int llmt_set_embed_f16(llmt_ctx* ctx, const void* embed_lm_head, const float* final_norm) {
+  set_error("");
+  Ctx* c = C_(ctx);
+  TRY_ARG(c && embed_lm_head && final_norm, "llmt_set_embed_f16: NULL argument");
+  TRY_HIP(hipMemcpyAsync(c->E, embed_lm_head, (size_t)c->V * c->H * 2, hipMemcpyDefault, c->st));
+  TRY_HIP(transpose_f16((const _Float16*)embed_lm_head, c->V, c->H, c->H, c->ET, c->V, c->st));
+  TRY_HIP(hipMemcpyAsync(c->final_norm, final_norm, c->H * 4, hipMemcpyDefault, c->st));
+  TRY_HIP(hipStreamSynchronize(c->st));
+  c->embed_ready = true;
+  return LLMT_OK;
+}
+
+// ---------------------------------------------------------------- file formats
+
+// Raw little-endian fp32, no header (python/export_weights.py:19-26); the
+// size must match exactly (the reference only checks for short reads,
+// src/train.cu:42-54).
+static int read_f32(const char* path, size_t n, std::vector<float>& buf) {
+  FILE* f = fopen(path, "rb");
+  if (!f) {
+    set_error("cannot open %s", path);
+    return LLMT_ERR_IO;
+  }
+  fseek(f, 0, SEEK_END);
+  const long sz = ftell(f);
+  fseek(f, 0, SEEK_SET);
+  if (sz != (long)(n * sizeof(float))) {
+    fclose(f);
+    set_error("%s: %ld bytes, expected %zu", path, sz, n * sizeof(float));
+    return LLMT_ERR_IO;
+  }
+  buf.resize(n);
+  const size_t got = fread(buf.data(), sizeof(float), n, f);
+  fclose(f);
+  if (got != n) {
+    set_error("short read %s", path);
+    return LLMT_ERR_IO;
+  }
+  return LLMT_OK;
+}
+
+int llmt_load_weights_dir(llmt_ctx* ctx, const char* dir) {
+  set_error("");
+  Ctx* c = C_(ctx);
+  TRY_ARG(c && dir, "llmt_load_weights_dir: NULL argument");
+  const int H = c->H, Q = c->Q, KV = c->KV, I = c->I, V = c->V;
+  const size_t big = (size_t)V * H;
+  float* f32 = nullptr;
+  _Float16* f16 = nullptr;
+  int8_t* q8 = nullptr;
+  float* s32 = nullptr;
+  _Float16* s16 = nullptr;
+  TRY_HIP(hipMalloc((void**)&f32, big * 4));
+  int rc = LLMT_OK;
+  std::vector<float> host;
+  char path[1024];
+  auto fail = [&](int r) {
+    hipFree(f32);
+    hipFree(f16);
+    hipFree(q8);
+    hipFree(s32);
+    hipFree(s16);
+    return r;
+  };
+  if (hipMalloc((void**)&f16, big * 2) != hipSuccess ||
+      hipMalloc((void**)&q8, (size_t)I * H * 7) != hipSuccess ||
+      hipMalloc((void**)&s32, (size_t)(I * 2 + Q + 2 * KV + 2 * H) * 4) != hipSuccess ||
+      hipMalloc((void**)&s16, (size_t)(I * 2 + Q + 2 * KV + 2 * H) * 2) != hipSuccess) {
+    set_error("llmt_load_weights_dir: out of device memory");
+    return fail(LLMT_ERR_HIP);
+  }
+  // Upload one fp32 file into f32 at element offset off.
+  auto up = [&](const char* name, size_t n, size_t off) -> int {
+    snprintf(path, sizeof(path), "%s/%s", dir, name);
+    int r = read_f32(path, n, host);
+    if (r) return r;
+    if (hipMemcpy(f32 + off, host.data(), n * 4, hipMemcpyHostToDevice) != hipSuccess) {
+      set_error("upload %s failed", path);
+      return LLMT_ERR_HIP;
+    }
+    return LLMT_OK;
+  };
+  const char* names[7] = {"self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj",
+                          "self_attn.o_proj", "mlp.gate_proj",    "mlp.up_proj",
+                          "mlp.down_proj"};
+  const size_t rows[7] = {(size_t)Q, (size_t)KV, (size_t)KV, (size_t)H,
+                          (size_t)I, (size_t)I,  (size_t)H};
+  const size_t cols[7] = {(size_t)H, (size_t)H, (size_t)H, (size_t)Q,
+                          (size_t)H, (size_t)H, (size_t)I};
+  for (int l = 0; l < c->L && rc == LLMT_OK; ++l) {
+    size_t off[7], o = 0;
+    for (int m = 0; m < 7; ++m) {
+      off[m] = o;
+      o += rows[m] * cols[m];
+      char nm[256];
+      snprintf(nm, sizeof(nm), "model.layers.%d.%s.weight.bin", l, names[m]);
+      if ((rc = up(nm, rows[m] * cols[m], off[m]))) return fail(rc);
+    }
+    const size_t nrm = o;
+    char nm[256];
+    const char* nn[4] = {"input_layernorm", "post_attention_layernorm", "self_attn.q_norm",
+                         "self_attn.k_norm"};
+    const size_t nsz[4] = {(size_t)H, (size_t)H, (size_t)kHeadDim, (size_t)kHeadDim};
+    size_t noff[4], no = nrm;
+    for (int k = 0; k < 4; ++k) {
+      noff[k] = no;
+      snprintf(nm, sizeof(nm), "model.layers.%d.%s.weight.bin", l, nn[k]);
+      if ((rc = up(nm, nsz[k], no))) return fail(rc);
+      no += nsz[k];
+    }
+    if (c->wfmt == LLMT_WEIGHTS_F16) {
+      if (f32_to_f16(f32, f16, nrm, c->st) != hipSuccess) return fail(LLMT_ERR_HIP);
+      rc = llmt_set_layer_f16(ctx, l, f16 + off[0], f16 + off[1], f16 + off[2], f16 + off[3],
+                              f16 + off[4], f16 + off[5], f16 + off[6], f32 + noff[0],
+                              f32 + noff[1], f32 + noff[2], f32 + noff[3]);
+    } else {
+      // src/kernels/quantize.cu:8-44 on the device, scales kept as fp16.
+      const int8_t* qp[7];
+      const void* sp[7];
+      size_t so = 0;
+      for (int m = 0; m < 7; ++m) {
+        if (quantize_rows_i8(f32 + off[m], (int)rows[m], (int)cols[m], q8 + off[m], s32 + so,
+                             c->st) != hipSuccess ||
+            f32_scale_to_f16(s32 + so, s16 + so, (int)rows[m], c->st) != hipSuccess)
+          return fail(LLMT_ERR_HIP);
+        qp[m] = q8 + off[m];
+        sp[m] = s16 + so;
+        so += rows[m];
+      }
+      rc = llmt_set_layer_i8(ctx, l, qp, sp, f32 + noff[0], f32 + noff[1], f32 + noff[2],
+                             f32 + noff[3]);
+    }
+    if (rc) return fail(rc);
+  }
+  // Tied embedding / lm_head: the reference's scripts write lm_head.weight.bin
+  // as a copy of the embedding (scripts/run.sh:19); the embedding file is used.
+  std::vector<float> fn;
+  snprintf(path, sizeof(path), "%s/model.norm.weight.bin", dir);
+  if ((rc = read_f32(path, H, fn))) return fail(rc);
+  if ((rc = up("model.embed_tokens.weight.bin", big, 0))) return fail(rc);
+  if (f32_to_f16(f32, f16, big, c->st) != hipSuccess || hipStreamSynchronize(c->st) != hipSuccess ||
+      hipMemcpy(f32, fn.data(), H * 4, hipMemcpyHostToDevice) != hipSuccess)
+    return fail(LLMT_ERR_HIP);
+  rc = llmt_set_embed_f16(ctx, f16, f32);
+  return fail(rc);
+}
+
+// src/train.cu:146-170: <dir>/lora_step{N}_layer{L}_{wq|wk|wv|wo}_{A|B}.bin,
+// raw fp32, A [16, d_in], B [d_out, 16].
+static const char* kProjNames[4] = {"wq", "wk", "wv", "wo"};
+
+int llmt_lora_save(llmt_ctx* ctx, const char* dir, int step) {
+  set_error("");
+  Ctx* c = C_(ctx);
+  TRY_ARG(c && dir, "llmt_lora_save: NULL argument");
+  std::vector<float> host(c->lora_numel);
+  TRY_HIP(hipMemcpyAsync(host.data(), c->lora_p, c->lora_numel * 4, hipMemcpyDeviceToHost, c->st));
+  TRY_HIP(hipStreamSynchronize(c->st));
+  char path[1024];
+  for (int l = 0; l < c->L; ++l)
+    for (int p = 0; p < 4; ++p)
+      for (int b = 0; b < 2; ++b) {
+        const int s = 2 * p + b;
+        const size_t n = (size_t)(s + 1 < 8 ? c->seg_off[s + 1] : (long long)c->lora_per_layer) -
+                         (size_t)c->seg_off[s];
+        snprintf(path, sizeof(path), "%s/lora_step%d_layer%d_%s_%c.bin", dir, step, l,
+                 kProjNames[p], b ? 'B' : 'A');
+        FILE* f = fopen(path, "wb");
+        if (!f) {
+          set_error("cannot write %s", path);
+          return LLMT_ERR_IO;
+        }
+        const size_t w = fwrite(host.data() + (size_t)l * c->lora_per_layer + c->seg_off[s], 4, n, f);
+        fclose(f);
+        if (w != n) {
+          set_error("short write %s", path);
+          return LLMT_ERR_IO;
+        }
+      }
+  return LLMT_OK;
+}
+
+int llmt_lora_load(llmt_ctx* ctx, const char* dir, int step) {
+  set_error("");
+  Ctx* c = C_(ctx);
+  TRY_ARG(c && dir, "llmt_lora_load: NULL argument");
+  std::vector<float> host(c->lora_numel), tmp;
+  char path[1024];
+  for (int l = 0; l < c->L; ++l)
+    for (int p = 0; p < 4; ++p)
+      for (int b = 0; b < 2; ++b) {
+        const int s = 2 * p + b;
+        const size_t n = (size_t)(s + 1 < 8 ? c->seg_off[s + 1] : (long long)c->lora_per_layer) -
+                         (size_t)c->seg_off[s];
+        snprintf(path, sizeof(path), "%s/lora_step%d_layer%d_%s_%c.bin", dir, step, l,
+                 kProjNames[p], b ? 'B' : 'A');
+        int rc = read_f32(path, n, tmp);
+        if (rc) return rc;
+        memcpy(host.data() + (size_t)l * c->lora_per_layer + c->seg_off[s], tmp.data(), n * 4);
+      }
+  return llmt_lora_copy(ctx, LLMT_LORA_PARAM, host.data(), 1);
+}
+
+}  // extern "C"

@@ -1,0 +1,162 @@
+// ctx.h — the training-step context behind the llmt_ctx handle.
+#pragma once
+
+#include <vector>
+
+#include "../../include/llmt.h"
+#include "ops.h"
+
+namespace llmt {
+
+constexpr int kHeadDim = 128;
+constexpr int kRank = 16;
+
+// Categories of the per-kernel profile (llmt_profile_step).
+enum {
+  CAT_GEMM_FWD = 0,
+  CAT_GEMM_BWD = 1,
+  CAT_GEMM_HEAD = 2,
+  CAT_ATTN = 3,
+  CAT_ROWS = 4,
+  CAT_CE = 5,
+  CAT_LORA = 6,
+  CAT_ADAM = 7,
+  CAT_END = 8,
+  CAT_COUNT = 8
+};
+
+// One frozen weight matrix as a GEMM B operand: fp16 or int8 rows of length
+// ld (the reduction dimension), with the int8 scale either per row
+// (colscale, forward layout [out, in]) or per reduction index (kscale,
+// transposed layout [in, out]).
+struct WMat {
+  const void* p = nullptr;
+  const _Float16* colscale = nullptr;
+  const _Float16* kscale = nullptr;
+  int rows = 0, ld = 0, i8 = 0;
+};
+
+struct Layer {
+  WMat wqkv, wqkvT;  // [Q + 2 KV, H] and [H, Q + 2 KV]
+  WMat wo, woT;      // [H, Q] and [Q, H]
+  WMat wgu, wguT;    // [2 I, H] (gate rows, then up rows) and [H, 2 I]
+  WMat wd, wdT;      // [H, I] and [I, H]
+  float* attn_norm = nullptr;
+  float* ffn_norm = nullptr;
+  float* q_norm = nullptr;
+  float* k_norm = nullptr;
+  bool ready = false;
+};
+
+// What the backward of one layer needs from its forward (sized for maxB*S).
+struct Stash {
+  float* x_in;       // [T, H] residual stream at the layer input
+  _Float16* xn;      // [T, H] attention-norm output (GEMM / LoRA-A input)
+  float* qkraw;      // [T, Q + KV] q, k before the QK-norm
+  _Float16* qkv16;   // [T, Q + 2 KV] normed + rotated q, k and v
+  float* h;          // [T, 64] LoRA h = x A^T for q, k, v, o
+  _Float16* o16;     // [T, Q] attention output
+  float* lse;        // [B, nq, S]
+  float* x_mid;      // [T, H] residual after attention
+  _Float16* xn2;     // [T, H] FFN-norm output
+  float* gu;         // [T, 2 I] gate, up pre-activations
+};
+
+struct GemmOut {
+  float* part;
+  int split;
+  long long ss;
+  int ldp;
+};
+
+struct Ctx {
+  llmt_dims dims{};
+  int maxB = 1, S = 0, wfmt = 0;
+  hipStream_t st = nullptr;
+  bool own_stream = false;
+  int H = 0, Q = 0, KV = 0, NT = 0, I = 0, V = 0, L = 0, nq = 0, nkv = 0, Tmax = 0;
+  float lscale = 2.0f;
+
+  std::vector<void*> blocks;
+  size_t device_bytes = 0;
+
+  std::vector<Layer> layers;
+  _Float16* E = nullptr;   // [V, H] tied embedding / lm_head
+  _Float16* ET = nullptr;  // [H, V]
+  float* final_norm = nullptr;
+  bool embed_ready = false;
+
+  // adapters: fp32 arenas + fp16 operand shadows
+  size_t lora_per_layer = 0, lora_numel = 0;
+  long long seg_off[8] = {};
+  float *lora_p = nullptr, *lora_g = nullptr, *lora_m = nullptr, *lora_v = nullptr;
+  _Float16* shadow = nullptr;
+  long long shadow_per_layer = 0, sh_a_qkv = 0, sh_a_o = 0, sh_bt_qkv = 0, sh_bt_o = 0;
+  AdamHp* hp_dev = nullptr;
+  AdamHp* host_hp = nullptr;
+
+  float *cosT = nullptr, *sinT = nullptr;
+  std::vector<Stash> stash;
+  float* x_final = nullptr;
+  _Float16* xf16 = nullptr;
+  float* logits = nullptr;
+  _Float16* grad16 = nullptr;
+  float2* ce_stats = nullptr;
+  float* loss_rows = nullptr;
+  float* loss_dev = nullptr;
+  float* host_loss = nullptr;
+  int* tok_buf = nullptr;
+  int* tgt_buf = nullptr;
+
+  float* part = nullptr;
+  size_t part_elems = 0;
+  _Float16* a16 = nullptr;
+  float *d_res = nullptr, *dmid = nullptr;
+  _Float16* g16 = nullptr;
+  float *rinv = nullptr, *rinv2 = nullptr;
+  _Float16* dgu16 = nullptr;
+  float *dO = nullptr, *delta = nullptr, *damax = nullptr;
+  float *dqkv32 = nullptr, *dy32 = nullptr, *dh = nullptr;
+
+  // graph + profiling
+  bool use_graph = false;
+  hipGraphExec_t graph_exec = nullptr;
+  int graph_batch = 0, graph_adam = -1;
+  bool profiling = false;
+  std::vector<hipEvent_t> prof_ev;
+  std::vector<int> prof_cat;
+  int prof_n = 0;
+  double gemm_flops = 0, gemm_wbytes = 0;
+
+  ~Ctx();
+  int init();
+  void* alloc(size_t bytes);
+  template <class T>
+  T* alloc_n(size_t n) {
+    return static_cast<T*>(alloc(n * sizeof(T)));
+  }
+  bool weights_ready() const {
+    if (!embed_ready) return false;
+    for (const Layer& l : layers)
+      if (!l.ready) return false;
+    return true;
+  }
+
+  hipError_t mark(int cat);
+  hipError_t gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int nseg, int M, int K,
+                  float* direct, int ldc, GemmOut* out);
+  BSeg wseg(const WMat& w) const;
+  BSeg hseg(const _Float16* p, int rows, int ld) const;
+  float* lora_ptr(float* arena, int l, int proj, int is_b) const;
+  _Float16* shadow_ptr(int l, long long off) const;
+  AdamShadow shadow_desc() const;
+  AttnArgs attn_args(const Stash& s) const;
+
+  hipError_t forward(const int* tok, const int* tgt, int B, float* dlogits_out);
+  hipError_t backward(int B, int accumulate);
+  hipError_t optimizer();
+  hipError_t refresh_shadows();
+  hipError_t device_step(int B, int with_adam);
+};
+
+}  // namespace llmt

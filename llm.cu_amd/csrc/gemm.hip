@@ -28,12 +28,17 @@ namespace {
 constexpr int BK = 64;
 constexpr int LDA_S = BK + 8;  // padded LDS row, in halves (144 B)
 
-__device__ __forceinline__ half8 load_b_frag(const void* p, int is_i8) {
+// One MFMA B fragment (8 consecutive k of one row).  int8 rows are
+// dequantised exactly to fp16 (|q| <= 127); a per-k scale (transposed int8
+// weights, where the quantisation channel is the reduction index) is then
+// applied as an fp16 multiply.
+__device__ __forceinline__ half8 load_b_frag(const void* p, int is_i8, const _Float16* ks) {
   if (!is_i8) return *reinterpret_cast<const half8*>(p);
   const int8x8 q = *reinterpret_cast<const int8x8*>(p);
   half8 h;
 #pragma unroll
   for (int i = 0; i < 8; ++i) h[i] = (_Float16)(float)q[i];
+  if (ks) h = h * *reinterpret_cast<const half8*>(ks);
   return h;
 }
 
@@ -58,6 +63,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
   int bi8[NF];
   int ncol[NF];
   const _Float16* cscale[NF];
+  const _Float16* kscale[NF];
   bool valid[NF];
 #pragma unroll
   for (int f = 0; f < NF; ++f) {
@@ -74,6 +80,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
     bptr[f] = (const char*)sg.ptr + ((long long)row * sg.ld + (lane >> 4) * 8) * esz;
     bi8[f] = sg.is_i8;
     cscale[f] = sg.colscale ? sg.colscale + (n - g.seg_start[s]) : nullptr;
+    kscale[f] = sg.kscale ? sg.kscale + (lane >> 4) * 8 : nullptr;
     if (!valid[f]) bptr[f] = nullptr;
   }
 
@@ -113,7 +120,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
         const int esz = bi8[f] ? 1 : 2;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
-          dst[f][kk] = load_b_frag(bptr[f] + (long long)(kc * BK + kk * 32) * esz, bi8[f]);
+          dst[f][kk] = load_b_frag(bptr[f] + (long long)(kc * BK + kk * 32) * esz, bi8[f],
+                                   kscale[f] ? kscale[f] + kc * BK + kk * 32 : nullptr);
       }
     }
   };
@@ -206,19 +214,19 @@ __global__ void transpose_f16_kernel(const _Float16* __restrict__ src, int rows,
   }
 }
 
-__global__ void transpose_i8_kernel(const int8_t* __restrict__ src, int rows, int cols,
-                                    int8_t* __restrict__ dst) {
+__global__ void transpose_i8_kernel(const int8_t* __restrict__ src, int rows, int cols, int lds,
+                                    int8_t* __restrict__ dst, int ldd) {
   __shared__ int8_t tile[64][68];
   const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   for (int r = ty; r < 64; r += 4) {
     const int gr = r0 + r, gc = c0 + tx;
-    if (gr < rows && gc < cols) tile[r][tx] = src[(long long)gr * cols + gc];
+    if (gr < rows && gc < cols) tile[r][tx] = src[(long long)gr * lds + gc];
   }
   __syncthreads();
   for (int c = ty; c < 64; c += 4) {
     const int gc = c0 + c, gr = r0 + tx;
-    if (gc < cols && gr < rows) dst[(long long)gc * rows + gr] = tile[tx][c];
+    if (gc < cols && gr < rows) dst[(long long)gc * ldd + gr] = tile[tx][c];
   }
 }
 
@@ -334,9 +342,10 @@ hipError_t transpose_f16(const _Float16* src, int rows, int cols, int lds, _Floa
   return hipSuccess;
 }
 
-hipError_t transpose_i8(const int8_t* src, int rows, int cols, int8_t* dst, hipStream_t st) {
+hipError_t transpose_i8(const int8_t* src, int rows, int cols, int lds, int8_t* dst, int ldd,
+                        hipStream_t st) {
   dim3 grid((cols + 63) / 64, (rows + 63) / 64);
-  hipLaunchKernelGGL(transpose_i8_kernel, grid, dim3(256), 0, st, src, rows, cols, dst);
+  hipLaunchKernelGGL(transpose_i8_kernel, grid, dim3(256), 0, st, src, rows, cols, lds, dst, ldd);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }

@@ -1,0 +1,187 @@
+// lora.hip — rank-16 adapter kernels: the dA/dB reductions over tokens, one
+// multi-tensor AdamW over the whole fp32 adapter arena (which also refreshes
+// the fp16 operand copies the GEMMs read), and the seeded initialiser.
+//
+// Reference: LoRA grads src/kernels/lora_backward.cu:50-90 (two TN GEMMs per
+// adapter through matmul_tn_forward, src/kernels/matmul.cu:102-138, plus
+// scale_add_inplace, src/kernels/lora.cu:10-18); AdamW
+// src/kernels/lora.cu:206-246 (224 launches per step); init
+// src/kernels/lora.cu:32-62 (cuRAND, not reproduced: this library draws its
+// own seeded normals).
+#include "ops.h"
+
+namespace llmt {
+
+namespace {
+
+constexpr int R = 16;
+constexpr int NTH = 256;
+constexpr int TCH = 64;  // tokens staged per LDS chunk
+
+// One adapter-gradient job: out = (acc ? out : 0) + lscale * X^T G over the T
+// token rows, for the ncols columns of X and the 16 columns of G.
+//   dA [16, d_in]:  X = adapter input (xn or o, fp16), G = dh  -> out[r][c]
+//   dB [d_out, 16]: X = upstream grad dy (fp32),       G = h   -> out[c][r]
+__global__ __launch_bounds__(NTH) void lora_grad_kernel(const LoraGradJobs J, int T, float lscale,
+                                                        int accumulate) {
+  __shared__ float Gs[TCH][R + 1];
+  int j = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxLoraJobs; ++i)
+    if (i < J.n && (int)blockIdx.x >= J.block_start[i]) j = i;
+  const LoraGradJob& jb = J.job[j];
+  const int c = ((int)blockIdx.x - J.block_start[j]) * NTH + threadIdx.x;
+  const bool active = c < jb.ncols;
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+  for (int t0 = 0; t0 < T; t0 += TCH) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < TCH * R; i += NTH) {
+      const int tt = i / R, r = i % R;
+      Gs[tt][r] = t0 + tt < T ? jb.G[(long long)(t0 + tt) * jb.ldg + r] : 0.f;
+    }
+    __syncthreads();
+    if (active) {
+      const int n = min(TCH, T - t0);
+      for (int tt = 0; tt < n; ++tt) {
+        const long long off = (long long)(t0 + tt) * jb.ldx + c;
+        const float x = jb.x_f16 ? (float)((const _Float16*)jb.X)[off] : ((const float*)jb.X)[off];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] += x * Gs[tt][r];
+      }
+    }
+  }
+  if (!active) return;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float* o = jb.out_is_B ? jb.out + (long long)c * R + r : jb.out + (long long)r * jb.ncols + c;
+    *o = (accumulate ? *o : 0.f) + lscale * acc[r];
+  }
+}
+
+// Shadow index of arena element i (fp16 operand copy), or -1.
+__device__ __forceinline__ long long shadow_index(const AdamShadow& sh, long long i) {
+  const long long l = i / sh.per_layer;
+  long long j = i - l * sh.per_layer;
+  int s = 0;
+#pragma unroll
+  for (int k = 1; k < 8; ++k)
+    if (j >= sh.seg_off[k]) s = k;
+  j -= sh.seg_off[s];
+  const int p = s >> 1;  // q, k, v, o
+  const long long base = l * sh.shadow_per_layer;
+  if ((s & 1) == 0) {  // A [16, d_in]: row r, column cc
+    const int d_in = sh.d_in[p];
+    const long long r = j / d_in, cc = j - r * d_in;
+    if (p < 3) return base + sh.a_qkv + (p * R + r) * d_in + cc;
+    return base + sh.a_o + r * d_in + cc;
+  }
+  // B [d_out, 16]: element (o, r) -> transposed row r
+  const long long o = j / R, r = j - o * R;
+  if (p < 3) return base + sh.bt_qkv + (p * R + r) * sh.nt + sh.col_off[p] + o;
+  return base + sh.bt_o + r * sh.d_out[3] + o;
+}
+
+// src/kernels/lora.cu:206-220, one launch over the arena.  update = 0 only
+// refreshes the fp16 shadows from the parameters.
+__global__ __launch_bounds__(NTH) void adamw_kernel(float* __restrict__ p,
+                                                    const float* __restrict__ g,
+                                                    float* __restrict__ m, float* __restrict__ v,
+                                                    long long n,
+                                                    const AdamHp* __restrict__ hpp, int update,
+                                                    const AdamShadow sh) {
+  const AdamHp hp = *hpp;
+  for (long long i = (long long)blockIdx.x * NTH + threadIdx.x; i < n;
+       i += (long long)gridDim.x * NTH) {
+    float pi = p[i];
+    if (update) {
+      const float gi = g[i];
+      const float mi = hp.beta1 * m[i] + (1.0f - hp.beta1) * gi;
+      const float vi = hp.beta2 * v[i] + (1.0f - hp.beta2) * gi * gi;
+      m[i] = mi;
+      v[i] = vi;
+      const float m_hat = mi / hp.bc1;
+      const float v_hat = vi / hp.bc2;
+      pi = pi * (1.0f - hp.lr * hp.wd) - hp.lr * m_hat / (sqrtf(v_hat) + hp.eps);
+      p[i] = pi;
+    }
+    if (sh.shadow) sh.shadow[shadow_index(sh, i)] = (_Float16)pi;
+  }
+}
+
+// Counter-based normal draws: SplitMix64 of (seed, index) -> two 24-bit
+// uniforms -> Box-Muller.  Deterministic for a given seed regardless of the
+// launch shape.
+__device__ __forceinline__ unsigned long long splitmix64(unsigned long long x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+__global__ __launch_bounds__(NTH) void lora_init_kernel(float* __restrict__ p,
+                                                        float* __restrict__ m,
+                                                        float* __restrict__ v, long long n,
+                                                        unsigned long long seed, float a_std,
+                                                        float b_std, const AdamShadow sh) {
+  for (long long i = (long long)blockIdx.x * NTH + threadIdx.x; i < n;
+       i += (long long)gridDim.x * NTH) {
+    const unsigned long long z = splitmix64(seed * 0x100000001B3ull + (unsigned long long)i);
+    const float u1 = ((float)(z >> 40) + 1.0f) * (1.0f / 16777216.0f);  // (0, 1]
+    const float u2 = (float)((z >> 16) & 0xFFFFFF) * (1.0f / 16777216.0f);
+    const float nrm = sqrtf(-2.0f * logf(u1)) * cospif(2.0f * u2);
+    const long long j = i % sh.per_layer;
+    int s = 0;
+#pragma unroll
+    for (int k = 1; k < 8; ++k)
+      if (j >= sh.seg_off[k]) s = k;
+    const float val = nrm * ((s & 1) ? b_std : a_std);
+    p[i] = val;
+    m[i] = 0.f;
+    v[i] = 0.f;
+    if (sh.shadow) sh.shadow[shadow_index(sh, i)] = (_Float16)val;
+  }
+}
+
+inline unsigned grid_for(long long n) {
+  long long g = (n + NTH - 1) / NTH;
+  return (unsigned)(g > 8192 ? 8192 : (g < 1 ? 1 : g));
+}
+
+}  // namespace
+
+hipError_t lora_grad(const LoraGradJobs& jobs_in, int T, float lscale, int accumulate,
+                     hipStream_t st) {
+  LoraGradJobs J = jobs_in;
+  if (J.n < 1 || J.n > kMaxLoraJobs) {
+    set_error("lora_grad: %d jobs", J.n);
+    return hipErrorInvalidValue;
+  }
+  int blocks = 0;
+  for (int i = 0; i < J.n; ++i) {
+    J.block_start[i] = blocks;
+    blocks += (J.job[i].ncols + NTH - 1) / NTH;
+  }
+  hipLaunchKernelGGL(lora_grad_kernel, dim3(blocks), dim3(NTH), 0, st, J, T, lscale, accumulate);
+  LLMT_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+hipError_t adamw(float* p, const float* g, float* m, float* v, long long n, const AdamHp* hp,
+                 int update, const AdamShadow& sh, hipStream_t st) {
+  hipLaunchKernelGGL(adamw_kernel, dim3(grid_for(n)), dim3(NTH), 0, st, p, g, m, v, n, hp, update,
+                     sh);
+  LLMT_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+hipError_t lora_init(float* p, float* m, float* v, long long n, unsigned long long seed,
+                     float a_std, float b_std, const AdamShadow& sh, hipStream_t st) {
+  hipLaunchKernelGGL(lora_init_kernel, dim3(grid_for(n)), dim3(NTH), 0, st, p, m, v, n, seed,
+                     a_std, b_std, sh);
+  LLMT_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+}  // namespace llmt

@@ -15,7 +15,8 @@ namespace llmt {
 // optional fp16 colscale[rows] multiplies the result columns).
 struct BSeg {
   const void* ptr;
-  const _Float16* colscale;
+  const _Float16* colscale;  // int8 [out, in] layout: per output row n
+  const _Float16* kscale;    // int8 [in, out] layout: per reduction index k
   int rows;
   int ld;
   int is_i8;
@@ -45,7 +46,8 @@ hipError_t sum_splits(const float* part, int split, long long split_stride, int 
 // ---------------------------------------------------------------- layout
 hipError_t transpose_f16(const _Float16* src, int rows, int cols, int lds, _Float16* dst, int ldd,
                          hipStream_t st);
-hipError_t transpose_i8(const int8_t* src, int rows, int cols, int8_t* dst, hipStream_t st);
+hipError_t transpose_i8(const int8_t* src, int rows, int cols, int lds, int8_t* dst, int ldd,
+                        hipStream_t st);
 hipError_t f32_to_f16(const float* src, _Float16* dst, size_t n, hipStream_t st);
 hipError_t copy_rows_f16(const _Float16* src, int rows, int cols, int lds, _Float16* dst, int ldd,
                          hipStream_t st);
@@ -64,5 +66,154 @@ hipError_t cross_entropy(const float* logits, const int* targets, int rows, int 
                          float2* stats, float* dlogits, _Float16* grad16, float* loss_rows,
                          float* loss_mean, hipStream_t st);
 constexpr float kGradLogitScale = 16384.0f;  // 2^14
+
+// ---------------------------------------------------------------- row kernels
+struct QkvPostArgs {
+  const float* part;
+  int split;
+  long long ss;
+  int ldp;
+  const float* Bq;
+  const float* Bk;
+  const float* Bv;  // LoRA B fp32 [d_out, 16]
+  float lscale;
+  const float* qn;
+  const float* kn;
+  const float* cosT;
+  const float* sinT;  // [S, 64]
+  int S, nq, nkv;
+  float eps;
+  float* qkraw;      // [T, Q + KV] fp32
+  _Float16* qkv16;   // [T, Q + 2 KV]
+  float* hbuf;       // [T, 64]: h columns 0..47
+};
+
+struct NormBwdArgs {
+  const float* part;
+  int split;
+  long long ss;
+  int ldp;
+  const float* rinv_in;  // per-row, may be NULL
+  float gscale;
+  int nlora;             // 0..3 adapters whose dh sits at columns H + 16 p
+  const float* A[3];     // LoRA A fp32 [16, H]
+  float lscale;
+  float* dh_out;         // [T, 64]
+  int dh_col;
+  const float* x;        // RMSNorm input [T, H]
+  const float* w;
+  float eps;
+  int H;
+  const float* dres_in;  // may be NULL (= 0); may alias dres_out
+  float* dres_out;
+  float* dmid_out;       // may be NULL
+  _Float16* g16;
+  float* rinv_out;
+};
+
+struct QkBwdArgs {
+  const float* dqkv;  // attention grads [T, ld] (dq | dk | dv)
+  int ld_dqkv;
+  const float* qkraw;
+  const float* qn;
+  const float* kn;
+  const float* cosT;
+  const float* sinT;
+  int S, nq, nkv;
+  float eps;
+  float* dy32;        // [T, NT]
+  _Float16* g16;      // [T, NT]
+  float* rinv_out;
+};
+
+hipError_t embed_norm(const int* tok, const _Float16* E, int V, int H, const float* w, float eps,
+                      int T, float* x, _Float16* xn, hipStream_t st);
+hipError_t qkv_post(const QkvPostArgs& a, int T, hipStream_t st);
+hipError_t o_post(const float* part, int split, long long ss, int ldp, const float* Bo,
+                  float lscale, const float* x_in, const float* w, float eps, int H, int T,
+                  float* hbuf, float* x_mid, _Float16* xn2, hipStream_t st);
+hipError_t gu_post(const float* part, int split, long long ss, int ldp, int I, int T, float* gu,
+                   _Float16* a16, hipStream_t st);
+hipError_t resid_norm(const float* part, int split, long long ss, int ldp, const float* x_res,
+                      const float* w, float eps, int H, int T, float* x_out, _Float16* xn,
+                      hipStream_t st);
+hipError_t qk_norm_rope(const _Float16* raw, const float* qn, const float* kn, const float* cosT,
+                        const float* sinT, int S, int nq, int nkv, float eps, int T, _Float16* out,
+                        hipStream_t st);
+hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st);
+hipError_t swiglu_bwd(const float* part, int split, long long ss, int ldp, const float* rinv_in,
+                      const float* gu, int I, int T, _Float16* dgu16, float* rinv_out,
+                      hipStream_t st);
+hipError_t o_dx_post(const float* part, int split, long long ss, int ldp, const float* rinv_in,
+                     const float* Ao, float lscale, const _Float16* o16, int nq, int S, int T,
+                     float* dh_out, float* dO, float* delta, float* damax, hipStream_t st);
+hipError_t qk_bwd(const QkBwdArgs& a, int T, hipStream_t st);
+
+// ---------------------------------------------------------------- attention
+struct AttnArgs {
+  const _Float16* qkv;  // q, k, v columns of one fp16 [T, ldq] buffer
+  long long ldq;
+  int qcol, kcol, vcol;
+  int nq, nkv, S;
+  float sm_scale;
+  _Float16* o;          // forward output [T, ldo]
+  long long ldo;
+  float* lse;           // [B, nq, S] natural-log LSE of the scaled scores
+  const float* dO;      // backward: dO fp32 [T, lddo]
+  long long lddo;
+  const float* delta;   // [B, nq, S] rowsum(dO * O)
+  const float* damax;   // [T] max |dO| per row
+  float* dq;
+  float* dk;
+  float* dv;            // fp32 [T, ldg] at their head offsets
+  long long ldg;
+};
+hipError_t attn_fwd(const AttnArgs& a, int B, hipStream_t st);
+hipError_t attn_bwd(const AttnArgs& a, int B, hipStream_t st);
+
+// ---------------------------------------------------------------- LoRA / AdamW
+constexpr int kMaxLoraJobs = 8;
+struct LoraGradJob {
+  const void* X;     // [T, ldx] fp16 or fp32
+  int x_f16;
+  long long ldx;
+  int ncols;
+  const float* G;    // [T, ldg] (16 columns used)
+  long long ldg;
+  float* out;
+  int out_is_B;      // 0: out[16][ncols] (dA), 1: out[ncols][16] (dB)
+};
+struct LoraGradJobs {
+  LoraGradJob job[kMaxLoraJobs];
+  int block_start[kMaxLoraJobs];
+  int n;
+};
+hipError_t lora_grad(const LoraGradJobs& jobs, int T, float lscale, int accumulate,
+                     hipStream_t st);
+
+struct AdamHp {
+  float lr, beta1, beta2, eps, wd, bc1, bc2;
+};
+// Where the fp16 operand copies of an arena element live.  Arena layout per
+// layer: q A, q B, k A, k B, v A, v B, o A, o B (seg_off = start of each).
+// Shadow layout per layer (halves): A_qkv [48][H] at a_qkv, A_o [16][Q] at
+// a_o, B^T_qkv [48][nt] at bt_qkv (block-diagonal, zero elsewhere), B^T_o
+// [16][H] at bt_o.
+struct AdamShadow {
+  _Float16* shadow;  // NULL: no shadow writes
+  long long per_layer;
+  long long seg_off[8];
+  int d_in[4];
+  int d_out[4];
+  int col_off[3];
+  int nt;
+  long long shadow_per_layer;
+  long long a_qkv, a_o, bt_qkv, bt_o;
+};
+// hp is a device pointer (so a captured graph picks up new step counts).
+hipError_t adamw(float* p, const float* g, float* m, float* v, long long n, const AdamHp* hp,
+                 int update, const AdamShadow& sh, hipStream_t st);
+hipError_t lora_init(float* p, float* m, float* v, long long n, unsigned long long seed,
+                     float a_std, float b_std, const AdamShadow& sh, hipStream_t st);
 
 }  // namespace llmt

@@ -1,0 +1,630 @@
+// step.cpp — the native layer of include/llmt.h: one context owns every
+// device buffer of the LoRA training step (frozen weights with their
+// pre-transposed copies, the fp32 adapter arenas and their fp16 operand
+// shadows, the per-layer stashes, the workspaces), sequences the kernels of
+// one step on one stream, optionally captures the step into a HIP graph, and
+// reads the loss back with the step's single host synchronisation.
+//
+// Step order follows src/train.cu:251-288: forward
+// (src/kernels/lora_forward.cu:169-305), fused cross-entropy
+// (src/kernels/loss.cu:74-91), backward (src/kernels/lora_backward.cu:212-408),
+// AdamW (src/kernels/lora.cu:235-246).
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "../../include/llmt.h"
+#include "ctx.h"
+
+using namespace llmt;
+
+namespace llmt {
+
+// ------------------------------------------------------------------ memory
+
+void* Ctx::alloc(size_t bytes) {
+  bytes = (bytes + 255) & ~(size_t)255;
+  void* p = nullptr;
+  if (hipMalloc(&p, bytes) != hipSuccess) {
+    set_error("hipMalloc(%zu) failed", bytes);
+    return nullptr;
+  }
+  blocks.push_back(p);
+  device_bytes += bytes;
+  return p;
+}
+
+Ctx::~Ctx() {
+  if (graph_exec) hipGraphExecDestroy(graph_exec);
+  for (auto& e : prof_ev) hipEventDestroy(e);
+  for (void* p : blocks) hipFree(p);
+  if (host_loss) hipHostFree(host_loss);
+  if (host_hp) hipHostFree(host_hp);
+  if (own_stream) hipStreamDestroy(st);
+}
+
+// ------------------------------------------------------------------ launches
+
+hipError_t Ctx::mark(int cat) {
+  if (!profiling) return hipSuccess;
+  if (prof_n >= (int)prof_ev.size()) {
+    hipEvent_t e;
+    LLMT_HIP_TRY(hipEventCreate(&e));
+    prof_ev.push_back(e);
+  }
+  prof_cat.resize(prof_n + 1);
+  prof_cat[prof_n] = cat;
+  LLMT_HIP_TRY(hipEventRecord(prof_ev[prof_n], st));
+  ++prof_n;
+  return hipSuccess;
+}
+
+hipError_t Ctx::gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int nseg, int M, int K,
+                     float* direct, int ldc, GemmOut* out) {
+  GemmArgs g{};
+  g.A = A;
+  g.lda = lda;
+  g.nseg = nseg;
+  for (int i = 0; i < nseg; ++i) g.seg[i] = segs[i];
+  gemm_finalize_segments(g);
+  g.M = M;
+  g.K = K;
+  if (direct) {
+    g.split = 1;
+    g.C = direct;
+    g.ldc = ldc;
+    g.split_stride = 0;
+  } else {
+    g.split = gemm_pick_split(M, g.N, K, 64);
+    g.C = part;
+    g.ldc = g.N;
+    g.split_stride = (long long)M * g.N;
+    if ((size_t)g.split * M * g.N > part_elems) {
+      set_error("gemm: partial workspace too small (%d x %d x %d > %zu)", g.split, M, g.N,
+                part_elems);
+      return hipErrorInvalidValue;
+    }
+  }
+  LLMT_HIP_TRY(mark(cat));
+  LLMT_HIP_TRY(gemm_nt(g, st));
+  gemm_flops += 2.0 * M * g.N * K;
+  double wbytes = 0;
+  for (int i = 0; i < nseg; ++i) wbytes += (double)segs[i].rows * K * (segs[i].is_i8 ? 1 : 2);
+  gemm_wbytes += wbytes;
+  if (out) {
+    out->part = g.C;
+    out->split = g.split;
+    out->ss = g.split_stride;
+    out->ldp = g.ldc;
+  }
+  return hipSuccess;
+}
+
+// ------------------------------------------------------------------ layout helpers
+
+BSeg Ctx::wseg(const WMat& w) const {
+  BSeg s{};
+  s.ptr = w.p;
+  s.colscale = w.colscale;
+  s.kscale = w.kscale;
+  s.rows = w.rows;
+  s.ld = w.ld;
+  s.is_i8 = w.i8;
+  return s;
+}
+
+BSeg Ctx::hseg(const _Float16* p, int rows, int ld) const {
+  BSeg s{};
+  s.ptr = p;
+  s.rows = rows;
+  s.ld = ld;
+  return s;
+}
+
+float* Ctx::lora_ptr(float* arena, int l, int proj, int is_b) const {
+  return arena + (size_t)l * lora_per_layer + seg_off[2 * proj + is_b];
+}
+
+_Float16* Ctx::shadow_ptr(int l, long long off) const {
+  return shadow + (size_t)l * shadow_per_layer + off;
+}
+
+AdamShadow Ctx::shadow_desc() const {
+  AdamShadow sh{};
+  sh.shadow = shadow;
+  sh.per_layer = lora_per_layer;
+  for (int i = 0; i < 8; ++i) sh.seg_off[i] = seg_off[i];
+  sh.d_in[0] = sh.d_in[1] = sh.d_in[2] = H;
+  sh.d_in[3] = Q;
+  sh.d_out[0] = Q;
+  sh.d_out[1] = sh.d_out[2] = KV;
+  sh.d_out[3] = H;
+  sh.col_off[0] = 0;
+  sh.col_off[1] = Q;
+  sh.col_off[2] = Q + KV;
+  sh.nt = NT;
+  sh.shadow_per_layer = shadow_per_layer;
+  sh.a_qkv = sh_a_qkv;
+  sh.a_o = sh_a_o;
+  sh.bt_qkv = sh_bt_qkv;
+  sh.bt_o = sh_bt_o;
+  return sh;
+}
+
+// ------------------------------------------------------------------ forward
+
+hipError_t Ctx::forward(const int* tok, const int* tgt, int B, float* dlogits_out) {
+  const int T = B * S;
+  const float eps = dims.eps, ls = lscale;
+  LLMT_HIP_TRY(mark(CAT_ROWS));
+  LLMT_HIP_TRY(embed_norm(tok, E, V, H, layers[0].attn_norm, eps, T, stash[0].x_in, stash[0].xn, st));
+  for (int l = 0; l < L; ++l) {
+    Layer& w = layers[l];
+    Stash& s = stash[l];
+    GemmOut go;
+    // Q/K/V (+ the three LoRA A) projections in one GEMM.
+    BSeg sq[2] = {wseg(w.wqkv), hseg(shadow_ptr(l, sh_a_qkv), 3 * kRank, H)};
+    LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn, H, sq, 2, T, H, nullptr, 0, &go));
+    QkvPostArgs qa{};
+    qa.part = go.part; qa.split = go.split; qa.ss = go.ss; qa.ldp = go.ldp;
+    qa.Bq = lora_ptr(lora_p, l, 0, 1);
+    qa.Bk = lora_ptr(lora_p, l, 1, 1);
+    qa.Bv = lora_ptr(lora_p, l, 2, 1);
+    qa.lscale = ls;
+    qa.qn = w.q_norm; qa.kn = w.k_norm;
+    qa.cosT = cosT; qa.sinT = sinT;
+    qa.S = S; qa.nq = nq; qa.nkv = nkv; qa.eps = eps;
+    qa.qkraw = s.qkraw; qa.qkv16 = s.qkv16; qa.hbuf = s.h;
+    LLMT_HIP_TRY(mark(CAT_ROWS));
+    LLMT_HIP_TRY(qkv_post(qa, T, st));
+    // attention
+    AttnArgs aa = attn_args(s);
+    LLMT_HIP_TRY(mark(CAT_ATTN));
+    LLMT_HIP_TRY(attn_fwd(aa, B, st));
+    // O (+ LoRA A) projection, residual, FFN norm
+    BSeg so[2] = {wseg(w.wo), hseg(shadow_ptr(l, sh_a_o), kRank, Q)};
+    LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.o16, Q, so, 2, T, Q, nullptr, 0, &go));
+    LLMT_HIP_TRY(mark(CAT_ROWS));
+    LLMT_HIP_TRY(o_post(go.part, go.split, go.ss, go.ldp, lora_ptr(lora_p, l, 3, 1), ls, s.x_in,
+                        w.ffn_norm, eps, H, T, s.h, s.x_mid, s.xn2, st));
+    // gate/up, SwiGLU
+    BSeg sg[1] = {wseg(w.wgu)};
+    LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn2, H, sg, 1, T, H, nullptr, 0, &go));
+    LLMT_HIP_TRY(mark(CAT_ROWS));
+    LLMT_HIP_TRY(gu_post(go.part, go.split, go.ss, go.ldp, I, T, s.gu, a16, st));
+    // down, residual, next norm
+    BSeg sd[1] = {wseg(w.wd)};
+    LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, a16, I, sd, 1, T, I, nullptr, 0, &go));
+    const bool last = l + 1 == L;
+    LLMT_HIP_TRY(mark(CAT_ROWS));
+    LLMT_HIP_TRY(resid_norm(go.part, go.split, go.ss, go.ldp, s.x_mid,
+                            last ? final_norm : layers[l + 1].attn_norm, eps, H, T,
+                            last ? x_final : stash[l + 1].x_in, last ? xf16 : stash[l + 1].xn, st));
+  }
+  // lm_head logits (tied embedding) and the fused cross-entropy
+  BSeg se[1] = {hseg(E, V, H)};
+  LLMT_HIP_TRY(gemm(CAT_GEMM_HEAD, xf16, H, se, 1, T, H, logits, V, nullptr));
+  LLMT_HIP_TRY(mark(CAT_CE));
+  LLMT_HIP_TRY(cross_entropy(logits, tgt, T, V, S, ce_stats, dlogits_out, grad16, loss_rows,
+                             loss_dev, st));
+  return hipSuccess;
+}
+
+AttnArgs Ctx::attn_args(const Stash& s) const {
+  AttnArgs a{};
+  a.qkv = s.qkv16;
+  a.ldq = NT;
+  a.qcol = 0;
+  a.kcol = Q;
+  a.vcol = Q + KV;
+  a.nq = nq;
+  a.nkv = nkv;
+  a.S = S;
+  a.sm_scale = 1.0f / sqrtf((float)kHeadDim);
+  a.o = s.o16;
+  a.ldo = Q;
+  a.lse = s.lse;
+  a.dO = dO;
+  a.lddo = Q;
+  a.delta = delta;
+  a.damax = damax;
+  a.dq = dqkv32;
+  a.dk = dqkv32 + Q;
+  a.dv = dqkv32 + Q + KV;
+  a.ldg = NT;
+  return a;
+}
+
+// ------------------------------------------------------------------ backward
+
+hipError_t Ctx::backward(int B, int accumulate) {
+  const int T = B * S;
+  const float eps = dims.eps, ls = lscale;
+  const int n_valid = B * (S - 1);
+  GemmOut go;
+  // lm_head dX over the vocabulary, then the final RMSNorm backward.
+  BSeg sh_[1] = {hseg(ET, H, V)};
+  LLMT_HIP_TRY(gemm(CAT_GEMM_HEAD, grad16, V, sh_, 1, T, V, nullptr, 0, &go));
+  NormBwdArgs nb{};
+  nb.part = go.part; nb.split = go.split; nb.ss = go.ss; nb.ldp = go.ldp;
+  nb.rinv_in = nullptr;
+  nb.gscale = 1.0f / (kGradLogitScale * (float)n_valid);
+  nb.nlora = 0;
+  nb.lscale = ls;
+  nb.dh_out = dh;
+  nb.x = x_final;
+  nb.w = final_norm;
+  nb.eps = eps;
+  nb.H = H;
+  nb.dres_in = nullptr;
+  nb.dres_out = d_res;
+  nb.dmid_out = nullptr;
+  nb.g16 = g16;
+  nb.rinv_out = rinv;
+  LLMT_HIP_TRY(mark(CAT_ROWS));
+  LLMT_HIP_TRY(norm_bwd(nb, T, st));
+
+  for (int l = L - 1; l >= 0; --l) {
+    Layer& w = layers[l];
+    Stash& s = stash[l];
+    // MLP: down dX -> SwiGLU bwd -> gate/up dX -> FFN norm bwd (+ residual)
+    BSeg sd[1] = {wseg(w.wdT)};
+    LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, sd, 1, T, H, nullptr, 0, &go));
+    LLMT_HIP_TRY(mark(CAT_ROWS));
+    LLMT_HIP_TRY(swiglu_bwd(go.part, go.split, go.ss, go.ldp, rinv, s.gu, I, T, dgu16, rinv2, st));
+    BSeg sg[1] = {wseg(w.wguT)};
+    LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, dgu16, 2 * I, sg, 1, T, 2 * I, nullptr, 0, &go));
+    nb = NormBwdArgs{};
+    nb.part = go.part; nb.split = go.split; nb.ss = go.ss; nb.ldp = go.ldp;
+    nb.rinv_in = rinv2;
+    nb.gscale = 1.0f;
+    nb.nlora = 0;
+    nb.lscale = ls;
+    nb.dh_out = dh;
+    nb.x = s.x_mid;
+    nb.w = w.ffn_norm;
+    nb.eps = eps;
+    nb.H = H;
+    nb.dres_in = d_res;
+    nb.dres_out = d_res;
+    nb.dmid_out = dmid;
+    nb.g16 = g16;
+    nb.rinv_out = rinv;
+    LLMT_HIP_TRY(mark(CAT_ROWS));
+    LLMT_HIP_TRY(norm_bwd(nb, T, st));
+    // O projection dX (+ dh_o through the B_o^T rows)
+    BSeg so[2] = {wseg(w.woT), hseg(shadow_ptr(l, sh_bt_o), kRank, H)};
+    LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, so, 2, T, H, nullptr, 0, &go));
+    LLMT_HIP_TRY(mark(CAT_ROWS));
+    LLMT_HIP_TRY(o_dx_post(go.part, go.split, go.ss, go.ldp, rinv, lora_ptr(lora_p, l, 3, 0), ls,
+                           s.o16, nq, S, T, dh, dO, delta, damax, st));
+    // attention backward
+    AttnArgs aa = attn_args(s);
+    LLMT_HIP_TRY(mark(CAT_ATTN));
+    LLMT_HIP_TRY(attn_bwd(aa, B, st));
+    // RoPE + QK-norm backward
+    QkBwdArgs qb{};
+    qb.dqkv = dqkv32; qb.ld_dqkv = NT;
+    qb.qkraw = s.qkraw;
+    qb.qn = w.q_norm; qb.kn = w.k_norm;
+    qb.cosT = cosT; qb.sinT = sinT;
+    qb.S = S; qb.nq = nq; qb.nkv = nkv; qb.eps = eps;
+    qb.dy32 = dy32; qb.g16 = g16; qb.rinv_out = rinv;
+    LLMT_HIP_TRY(mark(CAT_ROWS));
+    LLMT_HIP_TRY(qk_bwd(qb, T, st));
+    // Q/K/V dX (+ dh_q, dh_k, dh_v through the B^T rows), attention norm bwd
+    BSeg sq[2] = {wseg(w.wqkvT), hseg(shadow_ptr(l, sh_bt_qkv), 3 * kRank, NT)};
+    LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, NT, sq, 2, T, NT, nullptr, 0, &go));
+    nb = NormBwdArgs{};
+    nb.part = go.part; nb.split = go.split; nb.ss = go.ss; nb.ldp = go.ldp;
+    nb.rinv_in = rinv;
+    nb.gscale = 1.0f;
+    nb.nlora = 3;
+    nb.A[0] = lora_ptr(lora_p, l, 0, 0);
+    nb.A[1] = lora_ptr(lora_p, l, 1, 0);
+    nb.A[2] = lora_ptr(lora_p, l, 2, 0);
+    nb.lscale = ls;
+    nb.dh_out = dh;
+    nb.dh_col = 0;
+    nb.x = s.x_in;
+    nb.w = w.attn_norm;
+    nb.eps = eps;
+    nb.H = H;
+    nb.dres_in = d_res;
+    nb.dres_out = d_res;
+    nb.dmid_out = nullptr;
+    nb.g16 = g16;
+    nb.rinv_out = rinv;
+    LLMT_HIP_TRY(mark(CAT_ROWS));
+    LLMT_HIP_TRY(norm_bwd(nb, T, st));
+    // adapter gradients of this layer
+    LoraGradJobs J{};
+    J.n = 8;
+    const LoraGradJob jobs[8] = {
+        {s.xn, 1, H, H, dh + 0, 64, lora_ptr(lora_g, l, 0, 0), 0},
+        {s.xn, 1, H, H, dh + 16, 64, lora_ptr(lora_g, l, 1, 0), 0},
+        {s.xn, 1, H, H, dh + 32, 64, lora_ptr(lora_g, l, 2, 0), 0},
+        {s.o16, 1, Q, Q, dh + 48, 64, lora_ptr(lora_g, l, 3, 0), 0},
+        {dy32, 0, NT, Q, s.h + 0, 64, lora_ptr(lora_g, l, 0, 1), 1},
+        {dy32 + Q, 0, NT, KV, s.h + 16, 64, lora_ptr(lora_g, l, 1, 1), 1},
+        {dy32 + Q + KV, 0, NT, KV, s.h + 32, 64, lora_ptr(lora_g, l, 2, 1), 1},
+        {dmid, 0, H, H, s.h + 48, 64, lora_ptr(lora_g, l, 3, 1), 1},
+    };
+    for (int i = 0; i < 8; ++i) J.job[i] = jobs[i];
+    LLMT_HIP_TRY(mark(CAT_LORA));
+    LLMT_HIP_TRY(lora_grad(J, T, ls, accumulate, st));
+  }
+  return hipSuccess;
+}
+
+hipError_t Ctx::optimizer() {
+  LLMT_HIP_TRY(mark(CAT_ADAM));
+  LLMT_HIP_TRY(adamw(lora_p, lora_g, lora_m, lora_v, (long long)lora_numel, hp_dev, 1,
+                     shadow_desc(), st));
+  return hipSuccess;
+}
+
+hipError_t Ctx::refresh_shadows() {
+  LLMT_HIP_TRY(adamw(lora_p, nullptr, nullptr, nullptr, (long long)lora_numel, hp_dev, 0,
+                     shadow_desc(), st));
+  return hipSuccess;
+}
+
+hipError_t Ctx::device_step(int B, int with_adam) {
+  LLMT_HIP_TRY(forward(tok_buf, tgt_buf, B, nullptr));
+  LLMT_HIP_TRY(backward(B, 0));
+  if (with_adam) LLMT_HIP_TRY(optimizer());
+  LLMT_HIP_TRY(mark(CAT_END));
+  return hipSuccess;
+}
+
+}  // namespace llmt
+
+// ====================================================================== C ABI
+
+#define TRY_ARG(cond, ...)          \
+  do {                              \
+    if (!(cond)) {                  \
+      set_error(__VA_ARGS__);       \
+      return LLMT_ERR_ARG;          \
+    }                               \
+  } while (0)
+
+#define TRY_HIP(expr)                                                         \
+  do {                                                                        \
+    hipError_t e__ = (expr);                                                  \
+    if (e__ != hipSuccess) {                                                  \
+      if (e__ != hipErrorInvalidValue || !llmt_last_error()[0])               \
+        set_error("%s: %s", #expr, hipGetErrorString(e__));                   \
+      return e__ == hipErrorInvalidValue ? LLMT_ERR_ARG : LLMT_ERR_HIP;       \
+    }                                                                         \
+  } while (0)
+
+static Ctx* C_(llmt_ctx* c) { return reinterpret_cast<Ctx*>(c); }
+static const Ctx* C_(const llmt_ctx* c) { return reinterpret_cast<const Ctx*>(c); }
+
+extern "C" {
+
+int llmt_ctx_create(const llmt_dims* dims, int max_batch, int seq_len, int weight_format,
+                    void* stream, llmt_ctx** out) {
+  set_error("");
+  TRY_ARG(dims && out, "llmt_ctx_create: NULL argument");
+  TRY_ARG(dims->head_dim == kHeadDim, "head_dim must be %d (got %d)", kHeadDim, dims->head_dim);
+  TRY_ARG(dims->rank == kRank, "LoRA rank must be %d (got %d)", kRank, dims->rank);
+  TRY_ARG(dims->n_heads > 0 && dims->n_kv_heads > 0 && dims->n_heads % dims->n_kv_heads == 0,
+          "n_heads must be a multiple of n_kv_heads");
+  TRY_ARG(dims->hidden % 64 == 0 && dims->intermediate % 64 == 0 && dims->vocab % 64 == 0,
+          "hidden, intermediate and vocab must be multiples of 64");
+  TRY_ARG(dims->n_layers >= 1, "n_layers >= 1");
+  TRY_ARG(max_batch >= 1 && seq_len >= 2, "max_batch >= 1 and seq_len >= 2");
+  TRY_ARG(weight_format == LLMT_WEIGHTS_F16 || weight_format == LLMT_WEIGHTS_I8,
+          "weight_format");
+  Ctx* c = new Ctx();
+  c->dims = *dims;
+  c->maxB = max_batch;
+  c->S = seq_len;
+  c->wfmt = weight_format;
+  c->st = (hipStream_t)stream;
+  if (!c->st) {
+    // A stream of its own (graph capture needs one); created blocking, so it
+    // stays ordered with work on the legacy default stream.
+    if (hipStreamCreate(&c->st) != hipSuccess) {
+      delete c;
+      set_error("llmt_ctx_create: hipStreamCreate failed");
+      return LLMT_ERR_HIP;
+    }
+    c->own_stream = true;
+  }
+  int rc = c->init();
+  if (rc != LLMT_OK) {
+    delete c;
+    return rc;
+  }
+  *out = reinterpret_cast<llmt_ctx*>(c);
+  return LLMT_OK;
+}
+
+int llmt_ctx_destroy(llmt_ctx* ctx) {
+  if (ctx) {
+    hipStreamSynchronize(C_(ctx)->st);
+    delete C_(ctx);
+  }
+  return LLMT_OK;
+}
+
+size_t llmt_ctx_device_bytes(const llmt_ctx* ctx) { return ctx ? C_(ctx)->device_bytes : 0; }
+
+size_t llmt_lora_numel(const llmt_ctx* ctx) { return ctx ? C_(ctx)->lora_numel : 0; }
+
+size_t llmt_lora_offset(const llmt_ctx* ctx, int layer, int proj, int is_b) {
+  const Ctx* c = C_(ctx);
+  if (!c || layer < 0 || layer >= c->L || proj < 0 || proj > 3) return (size_t)-1;
+  return (size_t)layer * c->lora_per_layer + c->seg_off[2 * proj + (is_b ? 1 : 0)];
+}
+
+int llmt_lora_copy(llmt_ctx* ctx, int kind, float* buf, int to_ctx) {
+  set_error("");
+  Ctx* c = C_(ctx);
+  TRY_ARG(c && buf && kind >= 0 && kind <= 3, "llmt_lora_copy: bad arguments");
+  float* arena[4] = {c->lora_p, c->lora_g, c->lora_m, c->lora_v};
+  const size_t bytes = c->lora_numel * sizeof(float);
+  if (to_ctx) {
+    TRY_HIP(hipMemcpyAsync(arena[kind], buf, bytes, hipMemcpyDefault, c->st));
+    if (kind == LLMT_LORA_PARAM) TRY_HIP(c->refresh_shadows());
+  } else {
+    TRY_HIP(hipMemcpyAsync(buf, arena[kind], bytes, hipMemcpyDefault, c->st));
+  }
+  TRY_HIP(hipStreamSynchronize(c->st));
+  return LLMT_OK;
+}
+
+int llmt_lora_init(llmt_ctx* ctx, uint64_t seed, float a_std, float b_std) {
+  set_error("");
+  Ctx* c = C_(ctx);
+  TRY_ARG(c, "llmt_lora_init: NULL ctx");
+  TRY_HIP(lora_init(c->lora_p, c->lora_m, c->lora_v, (long long)c->lora_numel, seed, a_std, b_std,
+                    c->shadow_desc(), c->st));
+  TRY_HIP(hipMemsetAsync(c->lora_g, 0, c->lora_numel * sizeof(float), c->st));
+  TRY_HIP(hipStreamSynchronize(c->st));
+  return LLMT_OK;
+}
+
+static int check_tokens(Ctx* c, const int* tokens, const int* targets, int batch) {
+  TRY_ARG(c && tokens && targets, "NULL argument");
+  TRY_ARG(batch >= 1 && batch <= c->maxB, "batch %d outside [1, %d]", batch, c->maxB);
+  TRY_ARG(c->weights_ready(), "frozen weights not set (llmt_set_layer_* / llmt_set_embed_f16)");
+  TRY_ARG((batch * c->S) % 16 == 0, "batch*seq_len must be a multiple of 16");
+  return LLMT_OK;
+}
+
+static int stage_inputs(Ctx* c, const int* tokens, const int* targets, int batch) {
+  const size_t n = (size_t)batch * c->S * sizeof(int);
+  TRY_HIP(hipMemcpyAsync(c->tok_buf, tokens, n, hipMemcpyDefault, c->st));
+  TRY_HIP(hipMemcpyAsync(c->tgt_buf, targets, n, hipMemcpyDefault, c->st));
+  return LLMT_OK;
+}
+
+static int set_hp(Ctx* c, const llmt_hparams* hp, int step) {
+  TRY_ARG(hp && step >= 1, "llmt_step: hparams NULL or step < 1");
+  AdamHp h{};
+  h.lr = hp->lr;
+  h.beta1 = hp->beta1;
+  h.beta2 = hp->beta2;
+  h.eps = hp->eps;
+  h.wd = hp->wd;
+  // src/kernels/lora.cu:238-239: bias corrections in fp32 with powf.
+  h.bc1 = 1.0f - powf(hp->beta1, (float)step);
+  h.bc2 = 1.0f - powf(hp->beta2, (float)step);
+  // The pinned staging slot may still be read by an in-flight copy of the
+  // previous step; the stream is idle here (every step ends synchronised).
+  *c->host_hp = h;
+  TRY_HIP(hipMemcpyAsync(c->hp_dev, c->host_hp, sizeof(AdamHp), hipMemcpyHostToDevice, c->st));
+  return LLMT_OK;
+}
+
+static int run_step(Ctx* c, int batch, int with_adam, float* loss_host) {
+  if (c->use_graph && !c->profiling) {
+    if (!c->graph_exec || c->graph_batch != batch || c->graph_adam != with_adam) {
+      if (c->graph_exec) {
+        hipGraphExecDestroy(c->graph_exec);
+        c->graph_exec = nullptr;
+      }
+      hipGraph_t g;
+      TRY_HIP(hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
+      hipError_t e = c->device_step(batch, with_adam);
+      hipError_t e2 = hipStreamEndCapture(c->st, &g);
+      TRY_HIP(e);
+      TRY_HIP(e2);
+      e = hipGraphInstantiate(&c->graph_exec, g, nullptr, nullptr, 0);
+      hipGraphDestroy(g);
+      TRY_HIP(e);
+      c->graph_batch = batch;
+      c->graph_adam = with_adam;
+    }
+    TRY_HIP(hipGraphLaunch(c->graph_exec, c->st));
+  } else {
+    c->prof_n = 0;
+    c->gemm_flops = c->gemm_wbytes = 0;
+    TRY_HIP(c->device_step(batch, with_adam));
+  }
+  TRY_HIP(hipMemcpyAsync(c->host_loss, c->loss_dev, sizeof(float), hipMemcpyDeviceToHost, c->st));
+  TRY_HIP(hipStreamSynchronize(c->st));
+  if (loss_host) *loss_host = *c->host_loss;
+  return LLMT_OK;
+}
+
+int llmt_step(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
+              const llmt_hparams* hp, int step, float* loss_host) {
+  set_error("");
+  Ctx* c = C_(ctx);
+  int rc = check_tokens(c, tokens, targets, batch);
+  if (rc) return rc;
+  if ((rc = set_hp(c, hp, step))) return rc;
+  if ((rc = stage_inputs(c, tokens, targets, batch))) return rc;
+  return run_step(c, batch, 1, loss_host);
+}
+
+int llmt_forward_backward(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
+                          float* loss_host) {
+  set_error("");
+  Ctx* c = C_(ctx);
+  int rc = check_tokens(c, tokens, targets, batch);
+  if (rc) return rc;
+  if ((rc = stage_inputs(c, tokens, targets, batch))) return rc;
+  return run_step(c, batch, 0, loss_host);
+}
+
+int llmt_adamw(llmt_ctx* ctx, const llmt_hparams* hp, int step) {
+  set_error("");
+  Ctx* c = C_(ctx);
+  TRY_ARG(c, "NULL ctx");
+  int rc = set_hp(c, hp, step);
+  if (rc) return rc;
+  TRY_HIP(c->optimizer());
+  TRY_HIP(hipStreamSynchronize(c->st));
+  return LLMT_OK;
+}
+
+int llmt_set_graph(llmt_ctx* ctx, int enable) {
+  Ctx* c = C_(ctx);
+  if (!c) return LLMT_ERR_ARG;
+  c->use_graph = enable != 0;
+  if (!c->use_graph && c->graph_exec) {
+    hipGraphExecDestroy(c->graph_exec);
+    c->graph_exec = nullptr;
+  }
+  return LLMT_OK;
+}
+
+const float* llmt_logits(const llmt_ctx* ctx) { return ctx ? C_(ctx)->logits : nullptr; }
+
+int llmt_profile_step(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
+                      const llmt_hparams* hp, int step, float* cat_ms, int ncat,
+                      double* gemm_flops, double* gemm_weight_bytes) {
+  set_error("");
+  Ctx* c = C_(ctx);
+  int rc = check_tokens(c, tokens, targets, batch);
+  if (rc) return rc;
+  TRY_ARG(cat_ms && ncat >= 1, "llmt_profile_step: cat_ms");
+  if ((rc = set_hp(c, hp, step))) return rc;
+  if ((rc = stage_inputs(c, tokens, targets, batch))) return rc;
+  c->profiling = true;
+  rc = run_step(c, batch, 1, nullptr);
+  c->profiling = false;
+  if (rc) return rc;
+  for (int i = 0; i < ncat; ++i) cat_ms[i] = 0.f;
+  for (int i = 0; i + 1 < c->prof_n; ++i) {
+    float ms = 0.f;
+    TRY_HIP(hipEventElapsedTime(&ms, c->prof_ev[i], c->prof_ev[i + 1]));
+    const int cat = c->prof_cat[i];
+    if (cat >= 0 && cat < ncat) cat_ms[cat] += ms;
+  }
+  if (gemm_flops) *gemm_flops = c->gemm_flops;
+  if (gemm_weight_bytes) *gemm_weight_bytes = c->gemm_wbytes;
+  return LLMT_OK;
+}
+
+}  // extern "C"

@@ -72,6 +72,8 @@ _PROTOS = {
     "llmt_layer_forward": (i32, [vp, i32, vp, vp, i32]),
     "llmt_layer_backward": (i32, [vp, i32, vp, vp, i32]),
     "llmt_adamw": (i32, [vp, C.POINTER(HParams), i32]),
+    "llmt_profile_step": (i32, [vp, vp, vp, i32, C.POINTER(HParams), i32, fp, i32,
+                                C.POINTER(C.c_double), C.POINTER(C.c_double)]),
 }
 
 _lib = None
@@ -174,3 +176,150 @@ def cross_entropy(logits, targets, seq_len, want_dlogits=True, stream=None):
     check(lib().llmt_cross_entropy(ptr(logits), ptr(targets), rows, V, seq_len, ptr(dl), ptr(lr),
                                    ptr(lm), stream_ptr(stream)))
     return lm, lr, dl
+
+
+# ------------------------------------------------------------------ training context
+
+PROFILE_CATEGORIES = ("gemm_fwd", "gemm_bwd", "gemm_lm_head", "attention", "row_epilogues",
+                      "cross_entropy", "lora_grad", "adamw")
+
+
+def hparams(lr=3e-4, beta1=0.9, beta2=0.999, eps=1e-8, wd=0.01) -> HParams:
+    """AdamW hyper-parameters; defaults are src/train.cu:174-182."""
+    return HParams(lr, beta1, beta2, eps, wd)
+
+
+class Context:
+    """One llmt_ctx: frozen weights, adapters, stashes and workspaces of the
+    LoRA training step for up to ``max_batch`` sequences of ``seq_len``."""
+
+    def __init__(self, dims: Dims, max_batch: int, seq_len: int, int8: bool = False, stream=None):
+        self.dims = dims
+        self.max_batch = max_batch
+        self.seq_len = seq_len
+        h = vp()
+        sp = None if stream is None else C.c_void_p(stream.cuda_stream)
+        check(lib().llmt_ctx_create(C.byref(dims), max_batch, seq_len, 1 if int8 else 0, sp,
+                                    C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().llmt_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def device_bytes(self) -> int:
+        return lib().llmt_ctx_device_bytes(self.h)
+
+    # -- weights
+    def set_layer_f16(self, layer, wq, wk, wv, wo, w_gate, w_up, w_down, attn_norm, ffn_norm,
+                      q_norm, k_norm):
+        check(lib().llmt_set_layer_f16(self.h, layer, *(ptr(t) for t in (
+            wq, wk, wv, wo, w_gate, w_up, w_down, attn_norm, ffn_norm, q_norm, k_norm))))
+
+    def set_layer_i8(self, layer, qs, scales16, attn_norm, ffn_norm, q_norm, k_norm):
+        qa = (vp * 7)(*(t.data_ptr() for t in qs))
+        sa = (vp * 7)(*(t.data_ptr() for t in scales16))
+        check(lib().llmt_set_layer_i8(self.h, layer, qa, sa, ptr(attn_norm), ptr(ffn_norm),
+                                      ptr(q_norm), ptr(k_norm)))
+
+    def set_embed_f16(self, embed, final_norm):
+        check(lib().llmt_set_embed_f16(self.h, ptr(embed), ptr(final_norm)))
+
+    def load_weights_dir(self, path):
+        check(lib().llmt_load_weights_dir(self.h, str(path).encode()))
+
+    # -- adapters
+    @property
+    def lora_numel(self) -> int:
+        return lib().llmt_lora_numel(self.h)
+
+    def lora_offset(self, layer, proj, is_b) -> int:
+        return lib().llmt_lora_offset(self.h, layer, PROJ[proj] if isinstance(proj, str) else proj,
+                                      int(is_b))
+
+    def lora_set(self, kind: str, flat):
+        """Copy a flat fp32 tensor (device or host) into an arena."""
+        flat = flat.contiguous()
+        assert flat.numel() == self.lora_numel and flat.dtype.is_floating_point
+        check(lib().llmt_lora_copy(self.h, KIND[kind], ptr(flat), 1))
+
+    def lora_get(self, kind: str, device="cuda"):
+        import torch
+        out = torch.empty(self.lora_numel, dtype=torch.float32, device=device)
+        check(lib().llmt_lora_copy(self.h, KIND[kind], ptr(out), 0))
+        return out
+
+    def lora_init(self, seed: int, a_std: float, b_std: float):
+        check(lib().llmt_lora_init(self.h, seed, a_std, b_std))
+
+    def lora_save(self, path, step: int):
+        check(lib().llmt_lora_save(self.h, str(path).encode(), step))
+
+    def lora_load(self, path, step: int):
+        check(lib().llmt_lora_load(self.h, str(path).encode(), step))
+
+    # -- the step
+    def set_graph(self, enable: bool):
+        check(lib().llmt_set_graph(self.h, int(enable)))
+
+    def step(self, tokens, targets, hp: HParams, step: int) -> float:
+        loss = C.c_float()
+        check(lib().llmt_step(self.h, ptr(tokens), ptr(targets), tokens.shape[0], C.byref(hp),
+                              step, C.byref(loss)))
+        return loss.value
+
+    def forward_backward(self, tokens, targets) -> float:
+        loss = C.c_float()
+        check(lib().llmt_forward_backward(self.h, ptr(tokens), ptr(targets), tokens.shape[0],
+                                          C.byref(loss)))
+        return loss.value
+
+    def profile_step(self, tokens, targets, hp: HParams, step: int):
+        """Per-category kernel milliseconds of one eager step, plus the step's
+        GEMM FLOPs and weight bytes."""
+        n = len(PROFILE_CATEGORIES)
+        ms = (C.c_float * n)()
+        fl, wb = C.c_double(), C.c_double()
+        check(lib().llmt_profile_step(self.h, ptr(tokens), ptr(targets), tokens.shape[0],
+                                      C.byref(hp), step, ms, n, C.byref(fl), C.byref(wb)))
+        return dict(zip(PROFILE_CATEGORIES, list(ms))), fl.value, wb.value
+
+
+def flatten_adapters(adapters, attr=("A", "B")):
+    """Adapters as list-of-dicts (layer -> proj -> object with A, B) -> one
+    flat fp32 tensor in the arena order: layer by layer, q, k, v, o, A then B."""
+    import torch
+    parts = []
+    for d in adapters:
+        for p in ("wq", "wk", "wv", "wo"):
+            for a in attr:
+                parts.append(getattr(d[p], a).reshape(-1).float())
+    return torch.cat(parts)
+
+
+def unflatten_adapters(flat, dims):
+    """Inverse of flatten_adapters: list of {proj: (A, B)} tensors (views)."""
+    r = dims.rank
+    q, kv, hd = dims.n_heads * dims.head_dim, dims.n_kv_heads * dims.head_dim, dims.hidden
+    shapes = {"wq": (q, hd), "wk": (kv, hd), "wv": (kv, hd), "wo": (hd, q)}
+    out, off = [], 0
+    for _ in range(dims.n_layers):
+        d = {}
+        for p in ("wq", "wk", "wv", "wo"):
+            d_out, d_in = shapes[p]
+            A = flat[off:off + r * d_in].view(r, d_in)
+            off += r * d_in
+            B = flat[off:off + d_out * r].view(d_out, r)
+            off += d_out * r
+            d[p] = (A, B)
+        out.append(d)
+    assert off == flat.numel()
+    return out
