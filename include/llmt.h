@@ -263,7 +263,8 @@ int llmt_adamw(llmt_ctx* ctx, const llmt_hparams* hp, int step);
 /* One llmt_step run eagerly with a HIP event between consecutive kernels:
  * cat_ms[c] receives the milliseconds spent in each kernel category
  * (0 forward GEMMs, 1 backward GEMMs, 2 lm_head GEMMs, 3 attention, 4 row
- * epilogues, 5 cross-entropy, 6 LoRA grads, 7 AdamW); gemm_flops and
+ * epilogues, 5 cross-entropy, 6 LoRA grads, 7 AdamW, 8 split-K reductions);
+ * gemm_flops and
  * gemm_weight_bytes (may be NULL) the step's GEMM FLOPs and weight bytes. */
 int llmt_profile_step(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
                       const llmt_hparams* hp, int step, float* cat_ms, int ncat,

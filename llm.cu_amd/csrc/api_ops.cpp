@@ -50,20 +50,30 @@ void llmt_dims_qwen3_1_7b(llmt_dims* d) {
   d->theta = LLMT_ROPE_THETA;
 }
 
+// The standalone GEMMs take a row-major B; it is packed into a temporary
+// fragment-packed copy first (the training step packs its frozen weights once).
 static int gemm_common(const void* A, int lda, const void* B, int ldb, int is_i8,
                        const void* scale, float* C, int ldc, int M, int N, int K, void* stream) {
   g_err[0] = 0;
-  if (!A || !B || !C || M <= 0 || N <= 0 || K <= 0 || M % 16 || K % 64 || N % 16 ||
-      lda < K || ldb < K || ldc < N) {
-    set_error("llmt_gemm: unsupported shape M=%d N=%d K=%d (M%%16, N%%16, K%%64 must be 0)", M, N, K);
+  if (!A || !B || !C || M <= 0 || N <= 0 || K <= 0 || M % 16 || K % 32 || N % 16 ||
+      lda < K || ldb < K || ldc < N || lda % 8 || ldc % 4) {
+    set_error("llmt_gemm: unsupported shape M=%d N=%d K=%d (M%%16, N%%16, K%%32, lda%%8, ldc%%4 "
+              "must be 0)", M, N, K);
     return LLMT_ERR_ARG;
   }
   hipStream_t st = (hipStream_t)stream;
+  void* packed = nullptr;
+  const size_t esz = is_i8 ? 1 : 2;
+  API_TRY(hipMallocAsync(&packed, (size_t)N * K * esz, st));
+  if (is_i8)
+    API_TRY(pack_i8((const int8_t*)B, ldb, 0, N, K, (int8_t*)packed, K, 0, 0, st));
+  else
+    API_TRY(pack_f16((const _Float16*)B, ldb, 0, N, K, (_Float16*)packed, K, 0, 0, st));
   GemmArgs g{};
   g.A = (const _Float16*)A;
   g.lda = lda;
   g.nseg = 1;
-  g.seg[0] = BSeg{B, (const _Float16*)scale, nullptr, N, ldb, is_i8};
+  g.seg[0] = BSeg{packed, (const _Float16*)scale, nullptr, N, K, is_i8};
   gemm_finalize_segments(g);
   g.M = M;
   g.K = K;
@@ -81,9 +91,19 @@ static int gemm_common(const void* A, int lda, const void* B, int ldb, int is_i8
   }
   API_TRY(gemm_nt(g, st));
   if (part) {
-    API_TRY(sum_splits(part, g.split, (long long)M * N, N, C, ldc, M, N, st));
+    ReduceArgs ra{};
+    ra.part = part;
+    ra.split = g.split;
+    ra.ss = (long long)M * N;
+    ra.ldp = N;
+    ra.out = C;
+    ra.ldo = ldc;
+    ra.M = M;
+    ra.N = N;
+    API_TRY(reduce_lora(ra, st));
     API_TRY(hipFreeAsync(part, st));
   }
+  API_TRY(hipFreeAsync(packed, st));
   return LLMT_OK;
 }
 

@@ -88,6 +88,15 @@ __device__ __forceinline__ float pow2_scale_for(float amax) {
   return ldexpf(1.0f, 14 - e);
 }
 
+// Fragment-packed layout of a GEMM B operand [rows, K] (rows % 16 == 0,
+// K % 32 == 0): 16-row x 32-k blocks of 512 elements, ordered by row block
+// then k block; inside a block, lane l = 16 g + c of a wave holds row c,
+// k = 8 g .. 8 g + 7 contiguously.  One MFMA B fragment is therefore one
+// contiguous 1 KB (fp16) or 512 B (int8) load per wave.
+__host__ __device__ __forceinline__ long long packed_index(long long r, long long k, long long K) {
+  return (((r >> 4) * (K >> 5) + (k >> 5)) << 9) + ((((k >> 3) & 3) << 4) + (r & 15)) * 8 + (k & 7);
+}
+
 __device__ __forceinline__ float h2f(_Float16 h) { return (float)h; }
 __device__ __forceinline__ _Float16 f2h(float f) { return (_Float16)f; }
 

@@ -6,6 +6,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <vector>
 
 #include "ctx.h"
@@ -179,6 +180,11 @@ int Ctx::init() {
   }
   if (part_elems == 0) part_elems = 1;
   TRY_PTR(part = alloc_n<float>(part_elems));
+  red_elems = 0;
+  for (auto& sh : shapes)
+    if (sh[0] != H || sh[1] != V) red_elems = std::max(red_elems, (size_t)T * sh[0]);
+  red_elems = std::max(red_elems, (size_t)T * H);
+  TRY_PTR(red = alloc_n<float>(red_elems));
   TRY_PTR(a16 = alloc_n<_Float16>(T * I));
   TRY_PTR(d_res = alloc_n<float>(T * H));
   TRY_PTR(dmid = alloc_n<float>(T * H));
@@ -204,22 +210,22 @@ int Ctx::init() {
 
 static Ctx* C_(llmt_ctx* c) { return reinterpret_cast<Ctx*>(c); }
 
-// Copy a [rows, cols] fp16 matrix into rows [r0, r0 + rows) of dst (ld cols)
-// and its transpose into columns [r0, r0 + rows) of dstT (ld ldT).
+// Pack a row-major [rows, cols] matrix into rows [r0, r0 + rows) of the
+// forward operand f (row length cols) and, transposed, into k range
+// [r0, r0 + rows) of the backward operand b (row length = f's row count).
 static hipError_t put_f16(Ctx* c, const void* src, int rows, int cols, const WMat& f, int r0,
                           const WMat& b) {
-  _Float16* d = (_Float16*)f.p + (size_t)r0 * f.ld;
-  LLMT_HIP_TRY(hipMemcpyAsync(d, src, (size_t)rows * cols * 2, hipMemcpyDefault, c->st));
-  return transpose_f16((const _Float16*)src, rows, cols, cols, (_Float16*)b.p + r0, b.ld, c->st);
+  LLMT_HIP_TRY(pack_f16((const _Float16*)src, cols, 0, rows, cols, (_Float16*)f.p, f.ld, r0, 0,
+                        c->st));
+  return pack_f16((const _Float16*)src, cols, 1, cols, rows, (_Float16*)b.p, b.ld, 0, r0, c->st);
 }
 
 static hipError_t put_i8(Ctx* c, const int8_t* src, const void* scale, int rows, int cols,
                          const WMat& f, int r0, const WMat& b) {
-  int8_t* d = (int8_t*)f.p + (size_t)r0 * f.ld;
-  LLMT_HIP_TRY(hipMemcpyAsync(d, src, (size_t)rows * cols, hipMemcpyDefault, c->st));
+  LLMT_HIP_TRY(pack_i8(src, cols, 0, rows, cols, (int8_t*)f.p, f.ld, r0, 0, c->st));
   LLMT_HIP_TRY(hipMemcpyAsync((_Float16*)f.colscale + r0, scale, (size_t)rows * 2,
                               hipMemcpyDefault, c->st));
-  return transpose_i8(src, rows, cols, cols, (int8_t*)b.p + r0, b.ld, c->st);
+  return pack_i8(src, cols, 1, cols, rows, (int8_t*)b.p, b.ld, 0, r0, c->st);
 }
 
 static int put_norms(Ctx* c, Layer& w, const float* attn_norm, const float* ffn_norm,
@@ -288,8 +294,9 @@ int llmt_set_embed_f16(llmt_ctx* ctx, const void* embed_lm_head, const float* fi
   set_error("");
   Ctx* c = C_(ctx);
   TRY_ARG(c && embed_lm_head && final_norm, "llmt_set_embed_f16: NULL argument");
-  TRY_HIP(hipMemcpyAsync(c->E, embed_lm_head, (size_t)c->V * c->H * 2, hipMemcpyDefault, c->st));
-  TRY_HIP(transpose_f16((const _Float16*)embed_lm_head, c->V, c->H, c->H, c->ET, c->V, c->st));
+  const _Float16* e = (const _Float16*)embed_lm_head;
+  TRY_HIP(pack_f16(e, c->H, 0, c->V, c->H, c->E, c->H, 0, 0, c->st));
+  TRY_HIP(pack_f16(e, c->H, 1, c->H, c->V, c->ET, c->V, 0, 0, c->st));
   TRY_HIP(hipMemcpyAsync(c->final_norm, final_norm, c->H * 4, hipMemcpyDefault, c->st));
   TRY_HIP(hipStreamSynchronize(c->st));
   c->embed_ready = true;

@@ -21,13 +21,14 @@ enum {
   CAT_CE = 5,
   CAT_LORA = 6,
   CAT_ADAM = 7,
-  CAT_END = 8,
-  CAT_COUNT = 8
+  CAT_REDUCE = 8,
+  CAT_END = 9,
+  CAT_COUNT = 9
 };
 
-// One frozen weight matrix as a GEMM B operand: fp16 or int8 rows of length
-// ld (the reduction dimension), with the int8 scale either per row
-// (colscale, forward layout [out, in]) or per reduction index (kscale,
+// One frozen weight matrix as a GEMM B operand: fragment-packed fp16 or int8
+// rows of length ld (the reduction dimension), with the int8 scale either per
+// row (colscale, forward layout [out, in]) or per reduction index (kscale,
 // transposed layout [in, out]).
 struct WMat {
   const void* p = nullptr;
@@ -81,8 +82,8 @@ struct Ctx {
   size_t device_bytes = 0;
 
   std::vector<Layer> layers;
-  _Float16* E = nullptr;   // [V, H] tied embedding / lm_head
-  _Float16* ET = nullptr;  // [H, V]
+  _Float16* E = nullptr;   // [V, H] tied embedding / lm_head (packed, K = H)
+  _Float16* ET = nullptr;  // [H, V] (packed, K = V)
   float* final_norm = nullptr;
   bool embed_ready = false;
 
@@ -108,8 +109,10 @@ struct Ctx {
   int* tok_buf = nullptr;
   int* tgt_buf = nullptr;
 
-  float* part = nullptr;
+  float* part = nullptr;   // split-K partials
   size_t part_elems = 0;
+  float* red = nullptr;    // reduced GEMM output (+ LoRA up-projection)
+  size_t red_elems = 0;
   _Float16* a16 = nullptr;
   float *d_res = nullptr, *dmid = nullptr;
   _Float16* g16 = nullptr;
@@ -143,8 +146,12 @@ struct Ctx {
   }
 
   hipError_t mark(int cat);
+  // C = A B^T over the segments.  direct: split 1 into `direct` (ld ldc).
+  // Otherwise the result lands in `red` (reduced in fixed split order, plus
+  // the nlora LoRA up-projections) and *out describes it (split 1).
   hipError_t gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int nseg, int M, int K,
-                  float* direct, int ldc, GemmOut* out);
+                  float* direct, int ldc, GemmOut* out, int nlora = 0,
+                  const LoraUp* ups = nullptr);
   BSeg wseg(const WMat& w) const;
   BSeg hseg(const _Float16* p, int rows, int ld) const;
   float* lora_ptr(float* arena, int l, int proj, int is_b) const;

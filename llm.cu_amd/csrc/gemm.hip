@@ -1,6 +1,6 @@
 // gemm.hip — skinny "NT" GEMM on fp16 MFMA (v_mfma_f32_16x16x32_f16) for
-// gfx950, plus the layout kernels (transposes, conversions, the bit-exact
-// int8 quantizer).
+// gfx950, plus the layout kernels (fragment packing, transposes,
+// conversions, the bit-exact int8 quantizer) and the split-K reduction.
 //
 // Every frozen-weight product of the training step is expressed as
 // C = A * B^T with both operands contiguous along the reduction dimension:
@@ -12,53 +12,69 @@
 //
 // Work decomposition.  The step's activations have few rows (T = 128 at the
 // headline shape), so every weight element is used T times: the kernel is
-// HBM-bound on the weight stream.  A workgroup of NW waves owns an
-// (MF*16) x (NW*NF*16) output tile over a K range (split-K); the A tile
-// [MF*16 x 64] is staged through LDS (double-buffered, padded rows: no bank
-// conflicts for ds_read_b128) and shared by the waves; each wave streams its
-// own NF*16 weight rows straight from HBM into MFMA operand registers with
-// 16-byte loads, one 64-wide K chunk ahead.  Split partials go to an fp32
-// workspace and are summed by the consuming epilogue kernel.
+// HBM-bound on the weight stream.  B operands are stored fragment-packed
+// (packed_index in common.h): each wave streams its NF*16 weight rows as
+// contiguous 1 KB loads straight into MFMA operand registers through a
+// four-slot register ring (three k-steps of 32 ahead).  The A tile of all
+// MF*16 rows is staged through LDS in 64-wide K chunks (double-buffered, in
+// MFMA fragment order so every ds_read_b128 is a contiguous conflict-free
+// 1 KB) and shared by the NW waves; the next chunk's A loads are issued a
+// chunk of MFMA work before they are stored.  The small LDS footprint (32 KB)
+// lets two 8-wave workgroups share a CU, which measured faster than larger
+// chunks, wider tiles or deeper B prefetch on MI355X.  K is split across workgroups (split-K) so a
+// launch fills the 256 CUs; split partials are fp32 and are reduced in a
+// fixed order by reduce_splits.
+#include <stdlib.h>
+#include <type_traits>
+
 #include "ops.h"
 
 namespace llmt {
 
-namespace {
-
-constexpr int BK = 64;
-constexpr int LDA_S = BK + 8;  // padded LDS row, in halves (144 B)
-
-// One MFMA B fragment (8 consecutive k of one row).  int8 rows are
-// dequantised exactly to fp16 (|q| <= 127); a per-k scale (transposed int8
-// weights, where the quantisation channel is the reduction index) is then
-// applied as an fp16 multiply.
-__device__ __forceinline__ half8 load_b_frag(const void* p, int is_i8, const _Float16* ks) {
-  if (!is_i8) return *reinterpret_cast<const half8*>(p);
-  const int8x8 q = *reinterpret_cast<const int8x8*>(p);
-  half8 h;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) h[i] = (_Float16)(float)q[i];
-  if (ks) h = h * *reinterpret_cast<const half8*>(ks);
-  return h;
+static int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return v && *v ? atoi(v) : dflt;
 }
 
-template <int MF, int NF, int NW>
+namespace {
+
+constexpr int KSTEP = 32;               // k per MFMA
+constexpr int CH_STEPS = 2;             // k-steps per LDS chunk
+constexpr int CH = CH_STEPS * KSTEP;    // 64
+constexpr int RING = 4;                 // B register slots (prefetch distance 3)
+static_assert((2 * CH_STEPS) % RING == 0, "ring slots must be static over two chunks");
+
+template <int V>
+using IC = std::integral_constant<int, V>;
+
+// One workgroup: output tile (MF*16) x (NW*NF*16) over k-steps [s0, s1) of
+// its split.  Chunk c covers k-steps s0 + 8c .. s0 + 8c + 7; steps past s1
+// multiply a zeroed B fragment (branch-free: the compiler then keeps the
+// ring's newer loads in flight across every wait), and every address is
+// clamped into the operand.  With I8 a segment may be int8 (dequantised in
+// registers at MFMA time, optionally times a per-k scale loaded alongside).
+template <int MF, int NF, int NW, bool I8>
 __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
   constexpr int MT = MF * 16;
-  constexpr int PIECES = MT * (BK / 8);  // 16-byte pieces per A chunk
   constexpr int NT = NW * 64;
+  constexpr int PIECES = MT * (CH / 8);  // 16-byte A pieces per chunk
   constexpr int APT = (PIECES + NT - 1) / NT;
-  __shared__ __attribute__((aligned(16))) _Float16 As[2][MT * LDA_S];
+  // A chunk in LDS in MFMA fragment order: fragment (k-step q, m-tile mi) is
+  // 1 KB at (q * MF + mi) * 512 halves with lane l's 8 halves at l * 8, so
+  // every ds_read_b128 of a wave is one contiguous, conflict-free 1 KB, and
+  // the staging writes (thread i -> piece i) are contiguous too.
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][MT * CH];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int m0 = blockIdx.z * MT;
-  const int nchunks = g.K / BK;
-  const int kc0 = (int)((long long)blockIdx.y * nchunks / g.split);
-  const int kc1 = (int)((long long)(blockIdx.y + 1) * nchunks / g.split);
+  const int ksteps = g.K / KSTEP;
+  const int s0 = (int)((long long)blockIdx.y * ksteps / g.split);
+  const int s1 = (int)((long long)(blockIdx.y + 1) * ksteps / g.split);
+  const int nst = s1 - s0;
+  const int nch = (nst + CH_STEPS - 1) / CH_STEPS;
 
-  // Per-fragment B row pointers (a fragment's 16 rows lie in one segment).
   const char* bptr[NF];
   int bi8[NF];
   int ncol[NF];
@@ -67,21 +83,22 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
   bool valid[NF];
 #pragma unroll
   for (int f = 0; f < NF; ++f) {
-    const int n = (blockIdx.x * NW + wave) * NF * 16 + f * 16;
-    ncol[f] = n;
-    valid[f] = n < g.N;
+    const int nn = (blockIdx.x * NW + wave) * NF * 16 + f * 16;
+    ncol[f] = nn;
+    valid[f] = nn < g.N;
     int s = 0;
 #pragma unroll
     for (int i = 1; i < 4; ++i)
-      if (i < g.nseg && n >= g.seg_start[i]) s = i;
+      if (i < g.nseg && nn >= g.seg_start[i]) s = i;
     const BSeg& sg = g.seg[s];
-    const int row = n - g.seg_start[s] + (lane & 15);
-    const int esz = sg.is_i8 ? 1 : 2;
-    bptr[f] = (const char*)sg.ptr + ((long long)row * sg.ld + (lane >> 4) * 8) * esz;
-    bi8[f] = sg.is_i8;
-    cscale[f] = sg.colscale ? sg.colscale + (n - g.seg_start[s]) : nullptr;
-    kscale[f] = sg.kscale ? sg.kscale + (lane >> 4) * 8 : nullptr;
-    if (!valid[f]) bptr[f] = nullptr;
+    // Invalid fragments read row block 0 of their segment (in bounds) and
+    // are never stored.
+    const long long rb16 = valid[f] ? (nn - g.seg_start[s]) >> 4 : 0;
+    const int i8 = I8 ? sg.is_i8 : 0;
+    bptr[f] = (const char*)sg.ptr + ((rb16 * ksteps) * 512 + lane * 8) * (i8 ? 1 : 2);
+    bi8[f] = i8;
+    cscale[f] = sg.colscale ? sg.colscale + (nn - g.seg_start[s]) : nullptr;
+    kscale[f] = (I8 && sg.kscale) ? sg.kscale + (lane >> 4) * 8 : nullptr;
   }
 
   floatx4 acc[MF][NF];
@@ -90,16 +107,21 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
 #pragma unroll
     for (int f = 0; f < NF; ++f) acc[i][f] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  half8 breg[NF][2], bnext[NF][2];
-  uint4 astage[APT];
+  uint4 ra[APT];
+  uint4 rb[RING][NF];
+  uint4 rk[RING][NF];
 
-  auto load_a = [&](int kc) {
+  auto load_a = [&](int c) {
+    const int kb = (s0 + c * CH_STEPS) * KSTEP;
 #pragma unroll
     for (int i = 0; i < APT; ++i) {
-      const int idx = tid + i * NT;
-      if (idx < PIECES) {
-        const int r = idx >> 3, c = idx & 7;
-        astage[i] = *reinterpret_cast<const uint4*>(g.A + (long long)(m0 + r) * g.lda + kc * BK + c * 8);
+      const int idx = tid + i * NT;  // LDS piece: fragment idx / 64, lane idx % 64
+      if (PIECES % NT == 0 || idx < PIECES) {
+        const int fr = idx >> 6, l = idx & 63;
+        const int q = fr / MF, mi = fr % MF;
+        const int r = mi * 16 + (l & 15);
+        const int k = min(kb + q * KSTEP + (l >> 4) * 8, g.K - 8);
+        ra[i] = *reinterpret_cast<const uint4*>(g.A + (long long)(m0 + r) * g.lda + k);
       }
     }
   };
@@ -107,58 +129,94 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < APT; ++i) {
       const int idx = tid + i * NT;
-      if (idx < PIECES) {
-        const int r = idx >> 3, c = idx & 7;
-        *reinterpret_cast<uint4*>(&As[buf][r * LDA_S + c * 8]) = astage[i];
-      }
+      if (PIECES % NT == 0 || idx < PIECES)
+        *reinterpret_cast<uint4*>(&As[buf][idx * 8]) = ra[i];
     }
   };
-  auto load_b = [&](int kc, half8 (&dst)[NF][2]) {
+  auto load_b = [&](int j, auto S) {
+    constexpr int st = decltype(S)::value;
+    const long long ss = s0 + min(j, nst - 1);
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
-      if (valid[f]) {
-        const int esz = bi8[f] ? 1 : 2;
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-          dst[f][kk] = load_b_frag(bptr[f] + (long long)(kc * BK + kk * 32) * esz, bi8[f],
-                                   kscale[f] ? kscale[f] + kc * BK + kk * 32 : nullptr);
+      if (I8 && bi8[f]) {
+        const uint2 q = *reinterpret_cast<const uint2*>(bptr[f] + ss * 512);
+        rb[st][f] = make_uint4(q.x, q.y, 0u, 0u);
+        if (kscale[f]) rk[st][f] = *reinterpret_cast<const uint4*>(kscale[f] + ss * KSTEP);
+      } else {
+        rb[st][f] = *reinterpret_cast<const uint4*>(bptr[f] + ss * 1024);
       }
     }
   };
+  auto bfrag = [&](int f, auto S) -> half8 {
+    constexpr int st = decltype(S)::value;
+    half8 h;
+    if (I8 && bi8[f]) {
+      const uint4 raw = rb[st][f];
+      int8x8 q;
+      __builtin_memcpy(&q, &raw, 8);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) h[i] = (_Float16)(float)q[i];
+      if (kscale[f]) {
+        half8 sc;
+        __builtin_memcpy(&sc, &rk[st][f], 16);
+        h = h * sc;
+      }
+    } else {
+      __builtin_memcpy(&h, &rb[st][f], 16);
+    }
+    return h;
+  };
+  // k-step q of the chunk pair starting at chunk c (q < CH_STEPS: chunk c in
+  // LDS buffer 0, else chunk c + 1 in buffer 1); ring slot q % RING is static.
+  auto kstep = [&](int c, auto Q) {
+    constexpr int q = decltype(Q)::value;
+    constexpr int buf = q / CH_STEPS;
+    const int j = c * CH_STEPS + q;
+    load_b(j + RING - 1, IC<(q + RING - 1) % RING>{});
+    const bool live = j < nst;
+    half8 b[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      b[f] = bfrag(f, IC<q % RING>{});
+      if (!live) b[f] = half8{};
+    }
+#pragma unroll
+    for (int mi = 0; mi < MF; ++mi) {
+      const half8 a =
+          *reinterpret_cast<const half8*>(&As[buf][(((q % CH_STEPS) * MF + mi) * 64 + lane) * 8]);
+#pragma unroll
+      for (int f = 0; f < NF; ++f) acc[mi][f] = mfma16(a, b[f], acc[mi][f]);
+    }
+  };
+  auto ksteps_of = [&](int c, auto Q0) {
+    constexpr int q0 = decltype(Q0)::value;
+    kstep(c, IC<q0>{});
+    kstep(c, IC<q0 + 1>{});
+  };
+  static_assert(CH_STEPS == 2, "ksteps_of covers two k-steps per chunk");
 
-  if (kc0 < kc1) {
-    load_a(kc0);
+  if (nst > 0) {
+    load_a(0);
+    load_b(0, IC<0>{});
+    load_b(1, IC<1>{});
+    load_b(2, IC<2>{});
     store_a(0);
-    load_b(kc0, breg);
-  }
-  int cur = 0;
-  for (int kc = kc0; kc < kc1; ++kc) {
     __syncthreads();
-    const bool more = kc + 1 < kc1;
-    if (more) {
-      load_a(kc + 1);
-      load_b(kc + 1, bnext);
+    // Two chunks per trip: compute from buffer 0 while chunk c+1 lands in
+    // buffer 1, then the reverse.  Chunks past the end are clamped loads
+    // multiplied by zero B fragments.
+    for (int c = 0; c < nch; c += 2) {
+      load_a(min(c + 1, nch - 1));
+      __builtin_amdgcn_sched_barrier(0);
+      ksteps_of(c, IC<0>{});
+      store_a(1);
+      __syncthreads();
+      load_a(min(c + 2, nch - 1));
+      __builtin_amdgcn_sched_barrier(0);
+      ksteps_of(c, IC<CH_STEPS>{});
+      store_a(0);
+      __syncthreads();
     }
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-#pragma unroll
-      for (int mi = 0; mi < MF; ++mi) {
-        const half8 a = *reinterpret_cast<const half8*>(
-            &As[cur][(mi * 16 + (lane & 15)) * LDA_S + kk * 32 + (lane >> 4) * 8]);
-#pragma unroll
-        for (int f = 0; f < NF; ++f)
-          if (valid[f]) acc[mi][f] = mfma16(a, breg[f][kk], acc[mi][f]);
-      }
-    }
-    if (more) {
-      store_a(cur ^ 1);
-#pragma unroll
-      for (int f = 0; f < NF; ++f) {
-        breg[f][0] = bnext[f][0];
-        breg[f][1] = bnext[f][1];
-      }
-    }
-    cur ^= 1;
   }
 
   float* C = g.C + (long long)blockIdx.y * g.split_stride;
@@ -178,23 +236,145 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
   }
 }
 
-template <int MF>
-hipError_t launch_mf(const GemmArgs& g, hipStream_t st) {
-  constexpr int NF = 2, NW = 4;
+template <int MF, int NF, int NW>
+hipError_t launch_cfg(const GemmArgs& g, hipStream_t st) {
   const int ncols = NW * NF * 16;
   dim3 grid((g.N + ncols - 1) / ncols, g.split, g.M / (MF * 16));
-  hipLaunchKernelGGL((gemm_nt_kernel<MF, NF, NW>), grid, dim3(NW * 64), 0, st, g);
+  bool i8 = false;
+  for (int i = 0; i < g.nseg; ++i) i8 = i8 || g.seg[i].is_i8;
+  if (i8)
+    hipLaunchKernelGGL((gemm_nt_kernel<MF, NF, NW, true>), grid, dim3(NW * 64), 0, st, g);
+  else
+    hipLaunchKernelGGL((gemm_nt_kernel<MF, NF, NW, false>), grid, dim3(NW * 64), 0, st, g);
   return hipGetLastError();
 }
 
-__global__ void sum_splits_kernel(const float* __restrict__ part, int split, long long sstride,
-                                  int ldp, float* __restrict__ out, int ldo, int M, int N) {
-  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (long long)M * N) return;
-  const int m = (int)(i / N), n = (int)(i % N);
-  float s = 0.f;
-  for (int k = 0; k < split; ++k) s += part[k * sstride + (long long)m * ldp + n];
-  out[(long long)m * ldo + n] = s;
+constexpr int kNW = 8, kNF = 2;  // 256-column tiles
+
+template <int MF>
+hipError_t launch_mf(const GemmArgs& g, hipStream_t st) {
+  return launch_cfg<MF, kNF, kNW>(g, st);
+}
+
+// Fixed-order split-K reduction fused with the LoRA up-projections:
+//   out[m][n] = sum_s part[s][m][n] + lscale * sum_r h[m][r] * M_p(r, n - c0_p)
+// for n inside adapter p's column range (adapters may share columns: each
+// one covering n adds its term), where h (the rank-16 LoRA activations,
+// x A^T forward or dy B backward) is itself a set of extra columns of the same
+// GEMM, reduced here first, per 16-row block, into LDS.  M_p is B [n, 16]
+// (forward: y += s h B^T) or A [16, n] (backward: dx += s dh A).
+// Workgroup: 16 rows x 64 columns; thread = one row x four columns (float4
+// loads, splits added in order, four partial loads in flight).
+__global__ __launch_bounds__(256) void reduce_lora_kernel(const ReduceArgs a) {
+  __shared__ float hs[16][3 * 16 + 1];
+  __shared__ float ms[3][16][64 + 1];  // this block's 64 columns of each adapter matrix
+  const int m0 = blockIdx.y * 16;
+  const int cb = blockIdx.x * 64;
+  const int tid = threadIdx.x;
+  // Adapter column ranges are multiples of 64 wide and aligned: a block is
+  // entirely inside or outside each of them.
+  int inside = 0;
+  for (int q = 0; q < a.nlora; ++q) {
+    const LoraUp& u = a.up[q];
+    if (cb < u.c0 || cb >= u.c0 + u.n) continue;
+    inside |= 1 << q;
+    const int jb = cb - u.c0;
+    for (int i = tid; i < 16 * 64; i += 256) {
+      if (u.is_B) {  // B [n, 16]: 64 rows of 16 contiguous floats
+        const int cc = i >> 4, r = i & 15;
+        ms[q][r][cc] = u.M[(long long)(jb + cc) * 16 + r];
+      } else {       // A [16, n]: 16 rows, 64 contiguous floats each
+        const int r = i >> 6, cc = i & 63;
+        ms[q][r][cc] = u.M[(long long)r * u.n + jb + cc];
+      }
+    }
+  }
+  const int nh = 16 * a.nlora;
+  if (inside) {
+    for (int e = tid; e < 16 * nh; e += 256) {
+      const int t = e / nh, j = e % nh;
+      const float* p = a.part + (long long)(m0 + t) * a.ldp + a.up[j >> 4].hcol + (j & 15);
+      float v = p[0];
+      int k = 1;
+      for (; k + 4 <= a.split; k += 4) {
+        const float x0 = p[k * a.ss], x1 = p[(k + 1) * a.ss], x2 = p[(k + 2) * a.ss],
+                    x3 = p[(k + 3) * a.ss];
+        v += x0;
+        v += x1;
+        v += x2;
+        v += x3;
+      }
+      for (; k < a.split; ++k) v += p[k * a.ss];
+      hs[t][j] = v;
+    }
+  }
+  __syncthreads();
+  const int t = tid >> 4;
+  const int cc = (tid & 15) * 4;
+  const int c = cb + cc;
+  if (c >= a.N) return;
+  const float* p = a.part + (long long)(m0 + t) * a.ldp + c;
+  float4 v = *reinterpret_cast<const float4*>(p);
+  int k = 1;
+  for (; k + 4 <= a.split; k += 4) {
+    const float4 x0 = *reinterpret_cast<const float4*>(p + k * a.ss);
+    const float4 x1 = *reinterpret_cast<const float4*>(p + (k + 1) * a.ss);
+    const float4 x2 = *reinterpret_cast<const float4*>(p + (k + 2) * a.ss);
+    const float4 x3 = *reinterpret_cast<const float4*>(p + (k + 3) * a.ss);
+    v.x += x0.x; v.y += x0.y; v.z += x0.z; v.w += x0.w;
+    v.x += x1.x; v.y += x1.y; v.z += x1.z; v.w += x1.w;
+    v.x += x2.x; v.y += x2.y; v.z += x2.z; v.w += x2.w;
+    v.x += x3.x; v.y += x3.y; v.z += x3.z; v.w += x3.w;
+  }
+  for (; k < a.split; ++k) {
+    const float4 x = *reinterpret_cast<const float4*>(p + k * a.ss);
+    v.x += x.x; v.y += x.y; v.z += x.z; v.w += x.w;
+  }
+  for (int q = 0; q < a.nlora; ++q) {
+    if (!(inside >> q & 1)) continue;
+    float l0 = 0.f, l1 = 0.f, l2 = 0.f, l3 = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float h = hs[t][q * 16 + r];
+      l0 += h * ms[q][r][cc];
+      l1 += h * ms[q][r][cc + 1];
+      l2 += h * ms[q][r][cc + 2];
+      l3 += h * ms[q][r][cc + 3];
+    }
+    v.x += a.lscale * l0;
+    v.y += a.lscale * l1;
+    v.z += a.lscale * l2;
+    v.w += a.lscale * l3;
+  }
+  *reinterpret_cast<float4*>(a.out + (long long)(m0 + t) * a.ldo + c) = v;
+}
+
+// Pack rows [row0, row0 + R) x k [k0, k0 + C) of a fragment-packed B operand
+// (row length K) from a row-major source (leading dimension lds): if
+// transpose, element (i, j) of the destination block is src[j][i], else
+// src[i][j].  One thread per 8-element piece; C % 8 == 0, k0 % 8 == 0.
+template <typename T>
+__global__ void pack_kernel(const T* __restrict__ src, long long lds, int transpose, int R, int C,
+                            T* __restrict__ dst, long long K, int row0, int k0) {
+  const long long np = (long long)R * (C / 8);
+  for (long long p = (long long)blockIdx.x * blockDim.x + threadIdx.x; p < np;
+       p += (long long)gridDim.x * blockDim.x) {
+    int i, jp;
+    if (transpose) {  // consecutive threads: consecutive destination rows
+      i = (int)(p % R);
+      jp = (int)(p / R);
+    } else {
+      i = (int)(p / (C / 8));
+      jp = (int)(p % (C / 8));
+    }
+    T v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      v[e] = transpose ? src[(long long)(jp * 8 + e) * lds + i] : src[(long long)i * lds + jp * 8 + e];
+    T* d = dst + packed_index(row0 + i, k0 + jp * 8, K);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d[e] = v[e];
+  }
 }
 
 // 64x64 tiles through LDS; 256 threads.
@@ -292,13 +472,20 @@ void gemm_finalize_segments(GemmArgs& g) {
   g.N = s;
 }
 
+// Split-K factor: enough (column tiles x splits) workgroups for about one
+// per CU (tunable with LLMT_GEMM_TARGET_WG), without splits shorter than
+// LLMT_GEMM_MIN_STEPS k-steps of 32.  Fewer splits means fewer fp32
+// partials to reduce.
+int gemm_tile_n() { return kNW * kNF * 16; }
+
 int gemm_pick_split(int M, int N, int K, int max_split) {
-  // Aim for >= 2 workgroups per CU on 256 CUs while keeping >= 4 K chunks
-  // per split.
+  const int target = env_int("LLMT_GEMM_TARGET_WG", 256);
+  const int min_steps = env_int("LLMT_GEMM_MIN_STEPS", 4);
   const int mt = (M % 128 == 0) ? M / 128 : 1;
-  const int ntiles = (N + 127) / 128 * mt;
-  int split = (512 + ntiles - 1) / ntiles;
-  const int kmax = (K / BK) / 4;
+  const int tn = gemm_tile_n();
+  const int ntiles = (N + tn - 1) / tn * mt;
+  int split = (target + ntiles / 2) / ntiles;
+  const int kmax = (K / KSTEP) / min_steps;
   if (split > kmax) split = kmax;
   if (split > max_split) split = max_split;
   if (split < 1) split = 1;
@@ -306,7 +493,8 @@ int gemm_pick_split(int M, int N, int K, int max_split) {
 }
 
 hipError_t gemm_nt(const GemmArgs& g, hipStream_t st) {
-  if (g.M <= 0 || g.N <= 0 || g.M % 16 || g.K % BK || g.split < 1 || g.nseg < 1 || g.nseg > 4) {
+  if (g.M <= 0 || g.N <= 0 || g.M % 16 || g.K % KSTEP || g.K < KSTEP || g.split < 1 ||
+      g.split > g.K / KSTEP || g.nseg < 1 || g.nseg > 4) {
     set_error("gemm_nt: unsupported shape M=%d N=%d K=%d split=%d", g.M, g.N, g.K, g.split);
     return hipErrorInvalidValue;
   }
@@ -325,11 +513,45 @@ hipError_t gemm_nt(const GemmArgs& g, hipStream_t st) {
   return e;
 }
 
-hipError_t sum_splits(const float* part, int split, long long sstride, int ldp, float* out, int ldo,
-                      int M, int N, hipStream_t st) {
-  const long long n = (long long)M * N;
-  hipLaunchKernelGGL(sum_splits_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, part,
-                     split, sstride, ldp, out, ldo, M, N);
+hipError_t reduce_lora(const ReduceArgs& a, hipStream_t st) {
+  if (a.M % 16 || a.N % 4 || a.ldp % 4 || a.ldo % 4 || a.nlora < 0 || a.nlora > 3 ||
+      a.out == a.part) {
+    set_error("reduce_lora: M %% 16, N/ldp/ldo %% 4, nlora <= 3 and out != part required");
+    return hipErrorInvalidValue;
+  }
+  for (int q = 0; q < a.nlora; ++q)
+    if (a.up[q].c0 % 64 || a.up[q].n % 64) {
+      set_error("reduce_lora: adapter column ranges must be 64-aligned");
+      return hipErrorInvalidValue;
+    }
+  dim3 grid((a.N + 63) / 64, a.M / 16);
+  hipLaunchKernelGGL(reduce_lora_kernel, grid, dim3(256), 0, st, a);
+  LLMT_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+hipError_t pack_f16(const _Float16* src, long long lds, int transpose, int R, int C, _Float16* dst,
+                    long long K, int row0, int k0, hipStream_t st) {
+  if (C % 8 || k0 % 8 || K % 32) {
+    set_error("pack_f16: C, k0 must be multiples of 8 and K of 32");
+    return hipErrorInvalidValue;
+  }
+  const long long np = (long long)R * (C / 8);
+  hipLaunchKernelGGL(pack_kernel<_Float16>, dim3(grid1d(np, 256)), dim3(256), 0, st, src, lds,
+                     transpose, R, C, dst, K, row0, k0);
+  LLMT_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+hipError_t pack_i8(const int8_t* src, long long lds, int transpose, int R, int C, int8_t* dst,
+                   long long K, int row0, int k0, hipStream_t st) {
+  if (C % 8 || k0 % 8 || K % 32) {
+    set_error("pack_i8: C, k0 must be multiples of 8 and K of 32");
+    return hipErrorInvalidValue;
+  }
+  const long long np = (long long)R * (C / 8);
+  hipLaunchKernelGGL(pack_kernel<int8_t>, dim3(grid1d(np, 256)), dim3(256), 0, st, src, lds,
+                     transpose, R, C, dst, K, row0, k0);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }

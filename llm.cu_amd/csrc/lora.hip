@@ -22,15 +22,20 @@ constexpr int TCH = 64;  // tokens staged per LDS chunk
 // token rows, for the ncols columns of X and the 16 columns of G.
 //   dA [16, d_in]:  X = adapter input (xn or o, fp16), G = dh  -> out[r][c]
 //   dB [d_out, 16]: X = upstream grad dy (fp32),       G = h   -> out[c][r]
+// A workgroup owns GC columns; its four waves take interleaved quarters of
+// every 64-token chunk and their partial sums are added in LDS in wave order.
+constexpr int GC = 64;
 __global__ __launch_bounds__(NTH) void lora_grad_kernel(const LoraGradJobs J, int T, float lscale,
                                                         int accumulate) {
   __shared__ float Gs[TCH][R + 1];
+  __shared__ float red[NTH / 64][GC][R + 1];
   int j = 0;
 #pragma unroll
   for (int i = 1; i < kMaxLoraJobs; ++i)
     if (i < J.n && (int)blockIdx.x >= J.block_start[i]) j = i;
   const LoraGradJob& jb = J.job[j];
-  const int c = ((int)blockIdx.x - J.block_start[j]) * NTH + threadIdx.x;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c = ((int)blockIdx.x - J.block_start[j]) * GC + lane;
   const bool active = c < jb.ncols;
   float acc[R];
 #pragma unroll
@@ -44,7 +49,8 @@ __global__ __launch_bounds__(NTH) void lora_grad_kernel(const LoraGradJobs J, in
     __syncthreads();
     if (active) {
       const int n = min(TCH, T - t0);
-      for (int tt = 0; tt < n; ++tt) {
+#pragma unroll 4
+      for (int tt = w; tt < n; tt += NTH / 64) {
         const long long off = (long long)(t0 + tt) * jb.ldx + c;
         const float x = jb.x_f16 ? (float)((const _Float16*)jb.X)[off] : ((const float*)jb.X)[off];
 #pragma unroll
@@ -52,11 +58,19 @@ __global__ __launch_bounds__(NTH) void lora_grad_kernel(const LoraGradJobs J, in
       }
     }
   }
+#pragma unroll
+  for (int r = 0; r < R; ++r) red[w][lane][r] = acc[r];
+  __syncthreads();
+  // thread (lane, w) finishes rows r = 4 w .. 4 w + 3 of column lane
   if (!active) return;
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
+  for (int rr = 0; rr < R / 4; ++rr) {
+    const int r = w * (R / 4) + rr;
+    float v = red[0][lane][r];
+#pragma unroll
+    for (int q = 1; q < NTH / 64; ++q) v += red[q][lane][r];
     float* o = jb.out_is_B ? jb.out + (long long)c * R + r : jb.out + (long long)r * jb.ncols + c;
-    *o = (accumulate ? *o : 0.f) + lscale * acc[r];
+    *o = (accumulate ? *o : 0.f) + lscale * v;
   }
 }
 
@@ -71,16 +85,17 @@ __device__ __forceinline__ long long shadow_index(const AdamShadow& sh, long lon
   j -= sh.seg_off[s];
   const int p = s >> 1;  // q, k, v, o
   const long long base = l * sh.shadow_per_layer;
+  // The shadows are GEMM B operands, stored fragment-packed.
   if ((s & 1) == 0) {  // A [16, d_in]: row r, column cc
     const int d_in = sh.d_in[p];
     const long long r = j / d_in, cc = j - r * d_in;
-    if (p < 3) return base + sh.a_qkv + (p * R + r) * d_in + cc;
-    return base + sh.a_o + r * d_in + cc;
+    if (p < 3) return base + sh.a_qkv + packed_index(p * R + r, cc, d_in);
+    return base + sh.a_o + packed_index(r, cc, d_in);
   }
-  // B [d_out, 16]: element (o, r) -> transposed row r
+  // B [d_out, 16]: element (o, r) -> row r, column o of B^T
   const long long o = j / R, r = j - o * R;
-  if (p < 3) return base + sh.bt_qkv + (p * R + r) * sh.nt + sh.col_off[p] + o;
-  return base + sh.bt_o + r * sh.d_out[3] + o;
+  if (p < 3) return base + sh.bt_qkv + packed_index(p * R + r, sh.col_off[p] + o, sh.nt);
+  return base + sh.bt_o + packed_index(r, o, sh.d_out[3]);
 }
 
 // src/kernels/lora.cu:206-220, one launch over the arena.  update = 0 only
@@ -161,7 +176,7 @@ hipError_t lora_grad(const LoraGradJobs& jobs_in, int T, float lscale, int accum
   int blocks = 0;
   for (int i = 0; i < J.n; ++i) {
     J.block_start[i] = blocks;
-    blocks += (J.job[i].ncols + NTH - 1) / NTH;
+    blocks += (J.job[i].ncols + GC - 1) / GC;
   }
   hipLaunchKernelGGL(lora_grad_kernel, dim3(blocks), dim3(NTH), 0, st, J, T, lscale, accumulate);
   LLMT_LAUNCH_CHECK();

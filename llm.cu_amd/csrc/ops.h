@@ -34,14 +34,39 @@ struct GemmArgs {
   int M, N, K, split;
 };
 
+// Every B segment is fragment-packed (packed_index, common.h) with row
+// length K; rows a multiple of 16.  A is row-major fp16 [M, lda], K % 32 == 0.
 // Fills seg_start/N from seg[0..nseg).
 void gemm_finalize_segments(GemmArgs& g);
 // Split factor for a GEMM of this shape on this device (>=1, bounded by K).
 int gemm_pick_split(int M, int N, int K, int max_split);
 hipError_t gemm_nt(const GemmArgs& g, hipStream_t st);
-// out[m][n] = sum_s part[s][m][n] (ld = ldp for parts, ldo for out).
-hipError_t sum_splits(const float* part, int split, long long split_stride, int ldp, float* out,
-                      int ldo, int M, int N, hipStream_t st);
+// out[m][n] = sum_s part[s][m][n] in split order, plus for output columns
+// [c0, c0 + n) of each LoRA adapter lscale * sum_r part-sum[m][hcol + r] *
+// M(r, n') (M = B [n, 16] if is_B, else A [16, n]).  out != part; M % 16 == 0.
+struct LoraUp {
+  const float* M;
+  int c0, n, hcol, is_B;
+};
+struct ReduceArgs {
+  const float* part;
+  int split;
+  long long ss;
+  int ldp;
+  float* out;
+  int ldo;
+  int M, N;
+  int nlora;
+  LoraUp up[3];
+  float lscale;
+};
+hipError_t reduce_lora(const ReduceArgs& a, hipStream_t st);
+// Pack a row-major block into rows [row0, row0 + R) x k [k0, k0 + C) of a
+// fragment-packed operand with row length K (transpose: the block is src^T).
+hipError_t pack_f16(const _Float16* src, long long lds, int transpose, int R, int C, _Float16* dst,
+                    long long K, int row0, int k0, hipStream_t st);
+hipError_t pack_i8(const int8_t* src, long long lds, int transpose, int R, int C, int8_t* dst,
+                   long long K, int row0, int k0, hipStream_t st);
 
 // ---------------------------------------------------------------- layout
 hipError_t transpose_f16(const _Float16* src, int rows, int cols, int lds, _Float16* dst, int ldd,
@@ -73,10 +98,6 @@ struct QkvPostArgs {
   int split;
   long long ss;
   int ldp;
-  const float* Bq;
-  const float* Bk;
-  const float* Bv;  // LoRA B fp32 [d_out, 16]
-  float lscale;
   const float* qn;
   const float* kn;
   const float* cosT;
@@ -96,8 +117,6 @@ struct NormBwdArgs {
   const float* rinv_in;  // per-row, may be NULL
   float gscale;
   int nlora;             // 0..3 adapters whose dh sits at columns H + 16 p
-  const float* A[3];     // LoRA A fp32 [16, H]
-  float lscale;
   float* dh_out;         // [T, 64]
   int dh_col;
   const float* x;        // RMSNorm input [T, H]
@@ -129,9 +148,9 @@ struct QkBwdArgs {
 hipError_t embed_norm(const int* tok, const _Float16* E, int V, int H, const float* w, float eps,
                       int T, float* x, _Float16* xn, hipStream_t st);
 hipError_t qkv_post(const QkvPostArgs& a, int T, hipStream_t st);
-hipError_t o_post(const float* part, int split, long long ss, int ldp, const float* Bo,
-                  float lscale, const float* x_in, const float* w, float eps, int H, int T,
-                  float* hbuf, float* x_mid, _Float16* xn2, hipStream_t st);
+hipError_t o_post(const float* part, int split, long long ss, int ldp, const float* x_in,
+                  const float* w, float eps, int H, int T, float* hbuf, float* x_mid,
+                  _Float16* xn2, hipStream_t st);
 hipError_t gu_post(const float* part, int split, long long ss, int ldp, int I, int T, float* gu,
                    _Float16* a16, hipStream_t st);
 hipError_t resid_norm(const float* part, int split, long long ss, int ldp, const float* x_res,
@@ -145,8 +164,8 @@ hipError_t swiglu_bwd(const float* part, int split, long long ss, int ldp, const
                       const float* gu, int I, int T, _Float16* dgu16, float* rinv_out,
                       hipStream_t st);
 hipError_t o_dx_post(const float* part, int split, long long ss, int ldp, const float* rinv_in,
-                     const float* Ao, float lscale, const _Float16* o16, int nq, int S, int T,
-                     float* dh_out, float* dO, float* delta, float* damax, hipStream_t st);
+                     const _Float16* o16, int nq, int S, int T, float* dh_out, float* dO,
+                     float* delta, float* damax, hipStream_t st);
 hipError_t qk_bwd(const QkBwdArgs& a, int T, hipStream_t st);
 
 // ---------------------------------------------------------------- attention

@@ -27,9 +27,19 @@ constexpr int RW = RT / 64;
 constexpr int HD = 128;  // head_dim
 constexpr int R = 16;    // LoRA rank
 
+// Sum of the split-K partials of one element, in split order (deterministic);
+// four loads are issued before they are added.
 __device__ __forceinline__ float split_sum(const float* __restrict__ p, int split, long long ss) {
   float s = p[0];
-  for (int k = 1; k < split; ++k) s += p[k * ss];
+  int k = 1;
+  for (; k + 4 <= split; k += 4) {
+    const float a = p[k * ss], b = p[(k + 1) * ss], c = p[(k + 2) * ss], d = p[(k + 3) * ss];
+    s += a;
+    s += b;
+    s += c;
+    s += d;
+  }
+  for (; k < split; ++k) s += p[k * ss];
   return s;
 }
 
@@ -67,49 +77,38 @@ __global__ __launch_bounds__(RT) void embed_norm_kernel(const int* __restrict__ 
   __shared__ float red[2 * RW];
   const int t = blockIdx.x;
   const int id = min(max(tok[t], 0), V - 1);
-  const _Float16* e = E + (long long)id * H;
+  // E is fragment-packed (K = H): the row's 8-element pieces are contiguous.
   float ss = 0.f;
-  for (int c = threadIdx.x; c < H; c += RT) {
-    const float v = (float)e[c];
-    x[(long long)t * H + c] = v;
-    ss += v * v;
+  for (int c = threadIdx.x * 8; c < H; c += RT * 8) {
+    const half8 v = *reinterpret_cast<const half8*>(E + packed_index(id, c, H));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float f = (float)v[i];
+      x[(long long)t * H + c + i] = f;
+      ss += f * f;
+    }
   }
   const float r = rsqrtf(block_sum2(ss, 0.f, red).x / H + eps);
   for (int c = threadIdx.x; c < H; c += RT)
-    xn[(long long)t * H + c] = (_Float16)((float)e[c] * r * w[c]);
+    xn[(long long)t * H + c] = (_Float16)(x[(long long)t * H + c] * r * w[c]);
 }
 
-// After the fused Q/K/V(+LoRA-A) GEMM: y = xW^T + s * (x A^T) B^T per
-// projection (src/kernels/lora.cu:181-202), stash q_raw/k_raw (fp32, the
-// QK-norm backward input) and h = x A^T, then per head QK-RMSNorm
+// After the fused Q/K/V(+LoRA-A) GEMM, whose reduction already added
+// s * (x A^T) B^T per projection (src/kernels/lora.cu:181-202): stash
+// q_raw/k_raw (fp32, the QK-norm backward input) and h = x A^T, then per head
+// QK-RMSNorm
 // (src/kernels/rmsnorm.cu:36-41 with 128-wide rows) and half-split RoPE
 // (src/kernels/rope.cu:7-27): lane l of a wave owns the rotation pair
 // (l, l + 64).  Writes q, k (normed, rotated) and v as fp16 [T, Q + 2 KV].
 __global__ __launch_bounds__(RT) void qkv_post_kernel(const QkvPostArgs a) {
   extern __shared__ float ys[];  // [NT]
-  __shared__ float hs[3 * R];
   const int t = blockIdx.x;
   const int Q = a.nq * HD, KV = a.nkv * HD, NT = Q + 2 * KV;
   const float* prow = a.part + (long long)t * a.ldp;
-  if (threadIdx.x < 3 * R) {
-    const float h = split_sum(prow + NT + threadIdx.x, a.split, a.ss);
-    hs[threadIdx.x] = h;
-    a.hbuf[(long long)t * 64 + threadIdx.x] = h;
-  }
-  __syncthreads();
+  if (threadIdx.x < 3 * R)
+    a.hbuf[(long long)t * 64 + threadIdx.x] = split_sum(prow + NT + threadIdx.x, a.split, a.ss);
   for (int c = threadIdx.x; c < NT; c += RT) {
-    const int p = c < Q ? 0 : (c < Q + KV ? 1 : 2);
-    const int row = c - (p == 0 ? 0 : (p == 1 ? Q : Q + KV));
-    const float* B = p == 0 ? a.Bq : (p == 1 ? a.Bk : a.Bv);
-    const float4* b4 = reinterpret_cast<const float4*>(B + (long long)row * R);
-    float l = 0.f;
-#pragma unroll
-    for (int i = 0; i < R / 4; ++i) {
-      const float4 b = b4[i];
-      l += hs[p * R + 4 * i] * b.x + hs[p * R + 4 * i + 1] * b.y + hs[p * R + 4 * i + 2] * b.z +
-           hs[p * R + 4 * i + 3] * b.w;
-    }
-    const float y = split_sum(prow + c, a.split, a.ss) + a.lscale * l;
+    const float y = split_sum(prow + c, a.split, a.ss);
     ys[c] = y;
     if (c < Q + KV)
       a.qkraw[(long long)t * (Q + KV) + c] = y;
@@ -131,37 +130,25 @@ __global__ __launch_bounds__(RT) void qkv_post_kernel(const QkvPostArgs a) {
   }
 }
 
-// After the O(+LoRA-A) GEMM: x_mid = x_in + oW^T + s (o A^T) B^T (residual,
-// src/kernels/elementwise.cu:4-15), stash h_o, then the FFN RMSNorm -> fp16.
+// After the O(+LoRA-A) GEMM (LoRA term added by its reduction):
+// x_mid = x_in + oW^T + s (o A^T) B^T (residual, src/kernels/elementwise.cu:
+// 4-15), stash h_o, then the FFN RMSNorm -> fp16.
 __global__ __launch_bounds__(RT) void o_post_kernel(const float* __restrict__ part, int split,
                                                     long long ss_, int ldp,
-                                                    const float* __restrict__ Bo, float lscale,
                                                     const float* __restrict__ x_in,
                                                     const float* __restrict__ w, float eps, int H,
                                                     float* __restrict__ hbuf,
                                                     float* __restrict__ x_mid,
                                                     _Float16* __restrict__ xn2) {
   extern __shared__ float ys[];  // [H]
-  __shared__ float hs[R];
   __shared__ float red[2 * RW];
   const int t = blockIdx.x;
   const float* prow = part + (long long)t * ldp;
-  if (threadIdx.x < R) {
-    const float h = split_sum(prow + H + threadIdx.x, split, ss_);
-    hs[threadIdx.x] = h;
-    hbuf[(long long)t * 64 + 3 * R + threadIdx.x] = h;
-  }
-  __syncthreads();
+  if (threadIdx.x < R)
+    hbuf[(long long)t * 64 + 3 * R + threadIdx.x] = split_sum(prow + H + threadIdx.x, split, ss_);
   float ssq = 0.f;
   for (int c = threadIdx.x; c < H; c += RT) {
-    const float4* b4 = reinterpret_cast<const float4*>(Bo + (long long)c * R);
-    float l = 0.f;
-#pragma unroll
-    for (int i = 0; i < R / 4; ++i) {
-      const float4 b = b4[i];
-      l += hs[4 * i] * b.x + hs[4 * i + 1] * b.y + hs[4 * i + 2] * b.z + hs[4 * i + 3] * b.w;
-    }
-    const float xm = x_in[(long long)t * H + c] + split_sum(prow + c, split, ss_) + lscale * l;
+    const float xm = x_in[(long long)t * H + c] + split_sum(prow + c, split, ss_);
     x_mid[(long long)t * H + c] = xm;
     ys[c] = xm;
     ssq += xm * xm;
@@ -249,36 +236,26 @@ __global__ __launch_bounds__(RT) void qk_norm_rope_kernel(const _Float16* __rest
 // Generic "GEMM dX -> RMSNorm backward -> residual" row epilogue
 // (src/kernels/rmsnorm.cu:53-95 plus the caller's residual adds,
 // src/kernels/lora_backward.cu:297-300, 400-403).  d = GEMM row * rinv_in[t]
-// * gscale, plus for nlora adapters the LoRA input gradient
-// s * (dh_p A_p) (src/kernels/lora_backward.cu:87 with the layout fixed),
-// where dh_p sits in the GEMM's extra columns [H + 16p, H + 16p + 16).
+// * gscale; for nlora adapters the GEMM's reduction already added the LoRA
+// input gradient s * (dh_p A_p) (src/kernels/lora_backward.cu:87 with the
+// layout fixed), and dh_p, in the extra columns [H + 16p, H + 16p + 16), is
+// stashed (unscaled) for the adapter gradients.
 // dres_out = dres_in + rmsnorm_bwd(d, x, w); also written to dmid_out when
 // given, and as the next fp16 gradient operand (g16, rinv_out).
 __global__ __launch_bounds__(RT) void norm_bwd_kernel(const NormBwdArgs a) {
   extern __shared__ float ds[];  // [H]
-  __shared__ float dhs[3 * R];
   __shared__ float red[2 * RW];
   const int t = blockIdx.x;
   const int H = a.H;
   const float* prow = a.part + (long long)t * a.ldp;
   const float rs = (a.rinv_in ? a.rinv_in[t] : 1.0f) * a.gscale;
-  if (threadIdx.x < R * a.nlora) {
-    const float dh = split_sum(prow + H + threadIdx.x, a.split, a.ss) * rs;
-    dhs[threadIdx.x] = dh;
-    a.dh_out[(long long)t * 64 + a.dh_col + threadIdx.x] = dh;
-  }
-  __syncthreads();
+  if (threadIdx.x < R * a.nlora)
+    a.dh_out[(long long)t * 64 + a.dh_col + threadIdx.x] =
+        split_sum(prow + H + threadIdx.x, a.split, a.ss) * rs;
   const float* x = a.x + (long long)t * H;
   float dot = 0.f, ssx = 0.f;
   for (int c = threadIdx.x; c < H; c += RT) {
-    float d = split_sum(prow + c, a.split, a.ss) * rs;
-    float l = 0.f;
-    for (int p = 0; p < a.nlora; ++p) {
-      const float* A = a.A[p];
-#pragma unroll
-      for (int r = 0; r < R; ++r) l += dhs[p * R + r] * A[(long long)r * H + c];
-    }
-    d += a.lscale * l;
+    const float d = split_sum(prow + c, a.split, a.ss) * rs;
     ds[c] = d;
     const float xv = x[c];
     dot += d * a.w[c] * xv;
@@ -335,37 +312,30 @@ __global__ __launch_bounds__(RT) void swiglu_bwd_kernel(const float* __restrict_
     dgu16[(long long)t * 2 * I + c] = (_Float16)(ds[c] * sc);
 }
 
-// dX of the O projection (+ dh_o in the LoRA-B^T columns): d_o = row * rinv
-// + s (dh_o A_o); writes d_o fp32 (attention dO), the row's max |d_o| and the
-// flash-backward row statistic delta[b, h, s] = sum_d dO * O.
+// dX of the O projection (+ dh_o in the LoRA-B^T columns; the reduction
+// already added s (dh_o A_o)): d_o = row * rinv; writes d_o fp32 (attention
+// dO), dh_o, the row's max |d_o| and the flash-backward row statistic
+// delta[b, h, s] = sum_d dO * O.
 __global__ __launch_bounds__(RT) void o_dx_post_kernel(const float* __restrict__ part, int split,
                                                        long long ss_, int ldp,
                                                        const float* __restrict__ rinv_in,
-                                                       const float* __restrict__ Ao, float lscale,
                                                        const _Float16* __restrict__ o16, int nq,
                                                        int S, float* __restrict__ dh_out,
                                                        float* __restrict__ dO,
                                                        float* __restrict__ delta,
                                                        float* __restrict__ damax) {
   extern __shared__ float ds[];  // [Q]
-  __shared__ float dhs[R];
   __shared__ float red[2 * RW];
   const int t = blockIdx.x;
   const int Q = nq * HD;
   const float* prow = part + (long long)t * ldp;
   const float rs = rinv_in[t];
-  if (threadIdx.x < R) {
-    const float dh = split_sum(prow + Q + threadIdx.x, split, ss_) * rs;
-    dhs[threadIdx.x] = dh;
-    dh_out[(long long)t * 64 + 3 * R + threadIdx.x] = dh;
-  }
-  __syncthreads();
+  if (threadIdx.x < R)
+    dh_out[(long long)t * 64 + 3 * R + threadIdx.x] =
+        split_sum(prow + Q + threadIdx.x, split, ss_) * rs;
   float amax = 0.f;
   for (int c = threadIdx.x; c < Q; c += RT) {
-    float l = 0.f;
-#pragma unroll
-    for (int r = 0; r < R; ++r) l += dhs[r] * Ao[(long long)r * Q + c];
-    const float d = split_sum(prow + c, split, ss_) * rs + lscale * l;
+    const float d = split_sum(prow + c, split, ss_) * rs;
     dO[(long long)t * Q + c] = d;
     ds[c] = d;
     amax = fmaxf(amax, fabsf(d));
@@ -445,11 +415,11 @@ hipError_t qkv_post(const QkvPostArgs& a, int T, hipStream_t st) {
   return hipSuccess;
 }
 
-hipError_t o_post(const float* part, int split, long long ss, int ldp, const float* Bo,
-                  float lscale, const float* x_in, const float* w, float eps, int H, int T,
-                  float* hbuf, float* x_mid, _Float16* xn2, hipStream_t st) {
+hipError_t o_post(const float* part, int split, long long ss, int ldp, const float* x_in,
+                  const float* w, float eps, int H, int T, float* hbuf, float* x_mid,
+                  _Float16* xn2, hipStream_t st) {
   hipLaunchKernelGGL(o_post_kernel, dim3(T), dim3(RT), H * sizeof(float), st, part, split, ss, ldp,
-                     Bo, lscale, x_in, w, eps, H, hbuf, x_mid, xn2);
+                     x_in, w, eps, H, hbuf, x_mid, xn2);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
@@ -501,10 +471,10 @@ hipError_t swiglu_bwd(const float* part, int split, long long ss, int ldp, const
 }
 
 hipError_t o_dx_post(const float* part, int split, long long ss, int ldp, const float* rinv_in,
-                     const float* Ao, float lscale, const _Float16* o16, int nq, int S, int T,
-                     float* dh_out, float* dO, float* delta, float* damax, hipStream_t st) {
+                     const _Float16* o16, int nq, int S, int T, float* dh_out, float* dO,
+                     float* delta, float* damax, hipStream_t st) {
   hipLaunchKernelGGL(o_dx_post_kernel, dim3(T), dim3(RT), nq * HD * sizeof(float), st, part, split,
-                     ss, ldp, rinv_in, Ao, lscale, o16, nq, S, dh_out, dO, delta, damax);
+                     ss, ldp, rinv_in, o16, nq, S, dh_out, dO, delta, damax);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }

@@ -63,7 +63,7 @@ hipError_t Ctx::mark(int cat) {
 }
 
 hipError_t Ctx::gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int nseg, int M, int K,
-                     float* direct, int ldc, GemmOut* out) {
+                     float* direct, int ldc, GemmOut* out, int nlora, const LoraUp* ups) {
   GemmArgs g{};
   g.A = A;
   g.lda = lda;
@@ -82,9 +82,8 @@ hipError_t Ctx::gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int 
     g.C = part;
     g.ldc = g.N;
     g.split_stride = (long long)M * g.N;
-    if ((size_t)g.split * M * g.N > part_elems) {
-      set_error("gemm: partial workspace too small (%d x %d x %d > %zu)", g.split, M, g.N,
-                part_elems);
+    if ((size_t)g.split * M * g.N > part_elems || (size_t)M * g.N > red_elems) {
+      set_error("gemm: workspace too small (%d x %d x %d > %zu)", g.split, M, g.N, part_elems);
       return hipErrorInvalidValue;
     }
   }
@@ -94,11 +93,29 @@ hipError_t Ctx::gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int 
   double wbytes = 0;
   for (int i = 0; i < nseg; ++i) wbytes += (double)segs[i].rows * K * (segs[i].is_i8 ? 1 : 2);
   gemm_wbytes += wbytes;
-  if (out) {
-    out->part = g.C;
-    out->split = g.split;
-    out->ss = g.split_stride;
-    out->ldp = g.ldc;
+  if (!out) return hipSuccess;
+  out->part = g.C;
+  out->split = g.split;
+  out->ss = g.split_stride;
+  out->ldp = g.ldc;
+  if (!direct && (g.split > 1 || nlora > 0)) {
+    ReduceArgs ra{};
+    ra.part = g.C;
+    ra.split = g.split;
+    ra.ss = g.split_stride;
+    ra.ldp = g.ldc;
+    ra.out = red;
+    ra.ldo = g.N;
+    ra.M = M;
+    ra.N = g.N;
+    ra.nlora = nlora;
+    for (int i = 0; i < nlora; ++i) ra.up[i] = ups[i];
+    ra.lscale = lscale;
+    LLMT_HIP_TRY(mark(CAT_REDUCE));
+    LLMT_HIP_TRY(reduce_lora(ra, st));
+    out->part = red;
+    out->split = 1;
+    out->ss = 0;
   }
   return hipSuccess;
 }
@@ -167,13 +184,12 @@ hipError_t Ctx::forward(const int* tok, const int* tgt, int B, float* dlogits_ou
     GemmOut go;
     // Q/K/V (+ the three LoRA A) projections in one GEMM.
     BSeg sq[2] = {wseg(w.wqkv), hseg(shadow_ptr(l, sh_a_qkv), 3 * kRank, H)};
-    LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn, H, sq, 2, T, H, nullptr, 0, &go));
+    const LoraUp uq[3] = {{lora_ptr(lora_p, l, 0, 1), 0, Q, NT, 1},
+                          {lora_ptr(lora_p, l, 1, 1), Q, KV, NT + kRank, 1},
+                          {lora_ptr(lora_p, l, 2, 1), Q + KV, KV, NT + 2 * kRank, 1}};
+    LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn, H, sq, 2, T, H, nullptr, 0, &go, 3, uq));
     QkvPostArgs qa{};
     qa.part = go.part; qa.split = go.split; qa.ss = go.ss; qa.ldp = go.ldp;
-    qa.Bq = lora_ptr(lora_p, l, 0, 1);
-    qa.Bk = lora_ptr(lora_p, l, 1, 1);
-    qa.Bv = lora_ptr(lora_p, l, 2, 1);
-    qa.lscale = ls;
     qa.qn = w.q_norm; qa.kn = w.k_norm;
     qa.cosT = cosT; qa.sinT = sinT;
     qa.S = S; qa.nq = nq; qa.nkv = nkv; qa.eps = eps;
@@ -186,10 +202,11 @@ hipError_t Ctx::forward(const int* tok, const int* tgt, int B, float* dlogits_ou
     LLMT_HIP_TRY(attn_fwd(aa, B, st));
     // O (+ LoRA A) projection, residual, FFN norm
     BSeg so[2] = {wseg(w.wo), hseg(shadow_ptr(l, sh_a_o), kRank, Q)};
-    LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.o16, Q, so, 2, T, Q, nullptr, 0, &go));
+    const LoraUp uo[1] = {{lora_ptr(lora_p, l, 3, 1), 0, H, H, 1}};
+    LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.o16, Q, so, 2, T, Q, nullptr, 0, &go, 1, uo));
     LLMT_HIP_TRY(mark(CAT_ROWS));
-    LLMT_HIP_TRY(o_post(go.part, go.split, go.ss, go.ldp, lora_ptr(lora_p, l, 3, 1), ls, s.x_in,
-                        w.ffn_norm, eps, H, T, s.h, s.x_mid, s.xn2, st));
+    LLMT_HIP_TRY(o_post(go.part, go.split, go.ss, go.ldp, s.x_in, w.ffn_norm, eps, H, T, s.h,
+                        s.x_mid, s.xn2, st));
     // gate/up, SwiGLU
     BSeg sg[1] = {wseg(w.wgu)};
     LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn2, H, sg, 1, T, H, nullptr, 0, &go));
@@ -253,7 +270,6 @@ hipError_t Ctx::backward(int B, int accumulate) {
   nb.rinv_in = nullptr;
   nb.gscale = 1.0f / (kGradLogitScale * (float)n_valid);
   nb.nlora = 0;
-  nb.lscale = ls;
   nb.dh_out = dh;
   nb.x = x_final;
   nb.w = final_norm;
@@ -282,7 +298,6 @@ hipError_t Ctx::backward(int B, int accumulate) {
     nb.rinv_in = rinv2;
     nb.gscale = 1.0f;
     nb.nlora = 0;
-    nb.lscale = ls;
     nb.dh_out = dh;
     nb.x = s.x_mid;
     nb.w = w.ffn_norm;
@@ -297,10 +312,11 @@ hipError_t Ctx::backward(int B, int accumulate) {
     LLMT_HIP_TRY(norm_bwd(nb, T, st));
     // O projection dX (+ dh_o through the B_o^T rows)
     BSeg so[2] = {wseg(w.woT), hseg(shadow_ptr(l, sh_bt_o), kRank, H)};
-    LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, so, 2, T, H, nullptr, 0, &go));
+    const LoraUp ubo[1] = {{lora_ptr(lora_p, l, 3, 0), 0, Q, Q, 0}};
+    LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, so, 2, T, H, nullptr, 0, &go, 1, ubo));
     LLMT_HIP_TRY(mark(CAT_ROWS));
-    LLMT_HIP_TRY(o_dx_post(go.part, go.split, go.ss, go.ldp, rinv, lora_ptr(lora_p, l, 3, 0), ls,
-                           s.o16, nq, S, T, dh, dO, delta, damax, st));
+    LLMT_HIP_TRY(o_dx_post(go.part, go.split, go.ss, go.ldp, rinv, s.o16, nq, S, T, dh, dO, delta,
+                           damax, st));
     // attention backward
     AttnArgs aa = attn_args(s);
     LLMT_HIP_TRY(mark(CAT_ATTN));
@@ -317,16 +333,15 @@ hipError_t Ctx::backward(int B, int accumulate) {
     LLMT_HIP_TRY(qk_bwd(qb, T, st));
     // Q/K/V dX (+ dh_q, dh_k, dh_v through the B^T rows), attention norm bwd
     BSeg sq[2] = {wseg(w.wqkvT), hseg(shadow_ptr(l, sh_bt_qkv), 3 * kRank, NT)};
-    LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, NT, sq, 2, T, NT, nullptr, 0, &go));
+    const LoraUp ubq[3] = {{lora_ptr(lora_p, l, 0, 0), 0, H, H, 0},
+                           {lora_ptr(lora_p, l, 1, 0), 0, H, H + kRank, 0},
+                           {lora_ptr(lora_p, l, 2, 0), 0, H, H + 2 * kRank, 0}};
+    LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, NT, sq, 2, T, NT, nullptr, 0, &go, 3, ubq));
     nb = NormBwdArgs{};
     nb.part = go.part; nb.split = go.split; nb.ss = go.ss; nb.ldp = go.ldp;
     nb.rinv_in = rinv;
     nb.gscale = 1.0f;
     nb.nlora = 3;
-    nb.A[0] = lora_ptr(lora_p, l, 0, 0);
-    nb.A[1] = lora_ptr(lora_p, l, 1, 0);
-    nb.A[2] = lora_ptr(lora_p, l, 2, 0);
-    nb.lscale = ls;
     nb.dh_out = dh;
     nb.dh_col = 0;
     nb.x = s.x_in;

@@ -181,7 +181,7 @@ def cross_entropy(logits, targets, seq_len, want_dlogits=True, stream=None):
 # ------------------------------------------------------------------ training context
 
 PROFILE_CATEGORIES = ("gemm_fwd", "gemm_bwd", "gemm_lm_head", "attention", "row_epilogues",
-                      "cross_entropy", "lora_grad", "adamw")
+                      "cross_entropy", "lora_grad", "adamw", "split_reduce")
 
 
 def hparams(lr=3e-4, beta1=0.9, beta2=0.999, eps=1e-8, wd=0.01) -> HParams:
