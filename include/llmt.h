@@ -145,9 +145,11 @@ void adamw_step_lora(LoraWeights* lora, const LoraGrads* grads, float lr, float 
 void scale_add_inplace(float* dst, const float* src, float scale, int n);
 void gpu_zero(float* buf, int n);
 
-/* src/kernels/lora_forward.cu:169-186.  The workspaces are accepted for ABI
- * compatibility; hidden receives the final-normed hidden state and logits
- * the fp32 logits [seq, V]. */
+/* src/kernels/lora_forward.cu:169-186.  The workspaces and acts are accepted
+ * for ABI compatibility and not touched (the stashes live in the library's
+ * context); logits receives the fp32 logits [seq, V].  Frozen weights are
+ * uploaded (fp16 pads when set, else the fp32 fields converted) on the first
+ * call for a given MW, adapters on every call.  seq_len % 16 == 0. */
 void transformer_forward_lora(const int* token_ids, const MW* model, const LoraWeights* lora,
                               float* hidden, float* residual, float* norm_out,
                               float* q, float* k, float* v, float* k_exp, float* v_exp,
@@ -288,9 +290,16 @@ int llmt_quantize_rows_i8(const float* w, int rows, int cols, int8_t* q, float* 
 int llmt_cross_entropy(const float* logits, const int* targets, int rows, int V, int seq_len,
                        float* dlogits, float* loss_rows, float* loss_mean, void* stream);
 /* Config C1: logits = hidden W^T, fused CE, dlogits, dhidden = dlogits W.
- * hidden [T, H] fp16, W [V, H] fp16; outputs fp32. */
+ * hidden [T, H] fp16, W [V, H] fp16 row-major (packed into temporaries on
+ * every call); outputs fp32; *loss_mean is a device float; dlogits may be
+ * NULL.  T % 16 == 0, T % seq_len == 0. */
 int llmt_lm_head_ce(const void* hidden, const void* W, const int* targets, int T, int seq_len,
                     int H, int V, float* loss_mean, float* dlogits, float* dhidden, void* stream);
+/* Config C1 on a context's tied embedding (already packed by
+ * llmt_set_embed_f16): hidden fp16 [batch*seq_len, H], dlogits (may be
+ * NULL) and dhidden fp32 device buffers; *loss_host after one host sync. */
+int llmt_head_ce(llmt_ctx* ctx, const void* hidden16, const int* targets, int batch,
+                 float* loss_host, float* dlogits, float* dhidden);
 /* Causal GQA flash attention (config C3).  q [B,S,nq,128], k/v [B,S,nkv,128]
  * fp16, o fp16 [B,S,nq,128], lse fp32 [B,nq,S]. */
 int llmt_attention_fwd(const void* q, const void* k, const void* v, void* o, float* lse,

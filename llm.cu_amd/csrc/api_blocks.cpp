@@ -1,0 +1,345 @@
+// api_blocks.cpp — C ABI for the benchmark configurations that exercise one
+// block of the step in isolation:
+//   C0  one decoder layer forward / backward through a context
+//       (llmt_layer_forward / llmt_layer_backward);
+//   C1  lm_head logits + fused cross-entropy + lm_head dX
+//       (llmt_head_ce on a context's packed tied embedding, llmt_lm_head_ce
+//       standalone);
+//   C3  causal GQA flash attention forward / backward and the whole
+//       QK-norm + RoPE + attention backward block
+//       (llmt_attention_fwd / _bwd / _block_bwd).
+// Every entry point validates shapes on the host before launching.
+#include <math.h>
+#include <string.h>
+
+#include <vector>
+
+#include "ctx.h"
+
+using namespace llmt;
+
+#define TRY_ARG(cond, ...)    \
+  do {                        \
+    if (!(cond)) {            \
+      set_error(__VA_ARGS__); \
+      return LLMT_ERR_ARG;    \
+    }                         \
+  } while (0)
+
+#define TRY_HIP(expr)                                                   \
+  do {                                                                  \
+    hipError_t e__ = (expr);                                            \
+    if (e__ != hipSuccess) {                                            \
+      if (e__ != hipErrorInvalidValue || !llmt_last_error()[0])         \
+        set_error("%s: %s", #expr, hipGetErrorString(e__));             \
+      return e__ == hipErrorInvalidValue ? LLMT_ERR_ARG : LLMT_ERR_HIP; \
+    }                                                                   \
+  } while (0)
+
+static Ctx* C_(llmt_ctx* c) { return reinterpret_cast<Ctx*>(c); }
+
+// Temporary device buffers released (stream-ordered) on scope exit.
+struct Temps {
+  hipStream_t st;
+  std::vector<void*> ptrs;
+  explicit Temps(hipStream_t s) : st(s) {}
+  template <class T>
+  T* get(size_t n) {
+    void* p = nullptr;
+    if (hipMallocAsync(&p, n * sizeof(T) + 256, st) != hipSuccess) return nullptr;
+    ptrs.push_back(p);
+    return static_cast<T*>(p);
+  }
+  ~Temps() {
+    for (void* p : ptrs) (void)hipFreeAsync(p, st);
+  }
+};
+
+extern "C" {
+
+// ------------------------------------------------------------------ C0
+
+int llmt_layer_forward(llmt_ctx* ctx, int layer, const float* x, float* y, int batch) {
+  set_error("");
+  Ctx* c = C_(ctx);
+  TRY_ARG(c && x && y && layer >= 0 && layer < c->L, "llmt_layer_forward: bad arguments");
+  TRY_ARG(batch >= 1 && batch <= c->maxB && (batch * c->S) % 16 == 0, "batch");
+  TRY_ARG(c->layers[layer].ready, "layer %d weights not set", layer);
+  const int T = batch * c->S;
+  Stash& s = c->stash[layer];
+  Layer& w = c->layers[layer];
+  TRY_HIP(copy_norm(x, w.attn_norm, c->dims.eps, c->H, T, s.x_in, s.xn, c->st));
+  TRY_HIP(c->layer_fwd(layer, batch, w.attn_norm, y, c->xf16));
+  TRY_HIP(hipStreamSynchronize(c->st));
+  return LLMT_OK;
+}
+
+int llmt_layer_backward(llmt_ctx* ctx, int layer, const float* dy, float* dx, int batch) {
+  set_error("");
+  Ctx* c = C_(ctx);
+  TRY_ARG(c && dy && dx && layer >= 0 && layer < c->L, "llmt_layer_backward: bad arguments");
+  TRY_ARG(batch >= 1 && batch <= c->maxB && (batch * c->S) % 16 == 0, "batch");
+  const int T = batch * c->S;
+  TRY_HIP(grad_rows(dy, c->H, T, c->d_res, c->g16, c->rinv, c->st));
+  TRY_HIP(c->layer_bwd(layer, batch, 0));
+  TRY_HIP(hipMemcpyAsync(dx, c->d_res, (size_t)T * c->H * 4, hipMemcpyDeviceToDevice, c->st));
+  TRY_HIP(hipStreamSynchronize(c->st));
+  return LLMT_OK;
+}
+
+// ------------------------------------------------------------------ C1
+
+// lm_head GEMMs on packed operands E (K = H) and ET (K = V), fused CE between.
+static int head_ce_packed(hipStream_t st, const _Float16* hidden, const _Float16* E,
+                          const _Float16* ET, const int* targets, int T, int seq_len, int H,
+                          int V, float* logits, _Float16* grad16, float2* stats,
+                          float* loss_rows, float* loss_mean, float* dlogits, float* dhidden,
+                          float* part, size_t part_elems) {
+  GemmArgs g{};
+  g.A = hidden;
+  g.lda = H;
+  g.nseg = 1;
+  g.seg[0] = BSeg{E, nullptr, nullptr, V, H, 0};
+  gemm_finalize_segments(g);
+  g.M = T;
+  g.K = H;
+  g.split = 1;
+  g.C = logits;
+  g.ldc = V;
+  TRY_HIP(gemm_nt(g, st));
+  TRY_HIP(cross_entropy(logits, targets, T, V, seq_len, stats, dlogits, grad16, loss_rows,
+                        loss_mean, st));
+  GemmArgs d{};
+  d.A = grad16;
+  d.lda = V;
+  d.nseg = 1;
+  d.seg[0] = BSeg{ET, nullptr, nullptr, H, V, 0};
+  gemm_finalize_segments(d);
+  d.M = T;
+  d.K = V;
+  d.split = gemm_pick_split(T, H, V, 64);
+  TRY_ARG((size_t)d.split * T * H <= part_elems, "head_ce: partial workspace");
+  d.C = part;
+  d.ldc = H;
+  d.split_stride = (long long)T * H;
+  TRY_HIP(gemm_nt(d, st));
+  ReduceArgs ra{};
+  ra.part = part;
+  ra.split = d.split;
+  ra.ss = d.split_stride;
+  ra.ldp = H;
+  ra.out = dhidden;
+  ra.ldo = H;
+  ra.M = T;
+  ra.N = H;
+  const int n_valid = T / seq_len * (seq_len - 1);
+  ra.out_scale = 1.0f / (kGradLogitScale * (float)n_valid);
+  TRY_HIP(reduce_lora(ra, st));
+  return LLMT_OK;
+}
+
+int llmt_head_ce(llmt_ctx* ctx, const void* hidden16, const int* targets, int batch,
+                 float* loss_host, float* dlogits, float* dhidden) {
+  set_error("");
+  Ctx* c = C_(ctx);
+  TRY_ARG(c && hidden16 && targets && dhidden, "llmt_head_ce: NULL argument");
+  TRY_ARG(c->embed_ready, "embedding not set");
+  TRY_ARG(batch >= 1 && batch <= c->maxB && (batch * c->S) % 16 == 0, "batch");
+  const int T = batch * c->S;
+  int rc = head_ce_packed(c->st, (const _Float16*)hidden16, c->E, c->ET, targets, T, c->S, c->H,
+                          c->V, c->logits, c->grad16, c->ce_stats, c->loss_rows, c->loss_dev,
+                          dlogits, dhidden, c->part, c->part_elems);
+  if (rc) return rc;
+  TRY_HIP(hipMemcpyAsync(c->host_loss, c->loss_dev, 4, hipMemcpyDeviceToHost, c->st));
+  TRY_HIP(hipStreamSynchronize(c->st));
+  if (loss_host) *loss_host = *c->host_loss;
+  return LLMT_OK;
+}
+
+int llmt_lm_head_ce(const void* hidden, const void* W, const int* targets, int T, int seq_len,
+                    int H, int V, float* loss_mean, float* dlogits, float* dhidden, void* stream) {
+  set_error("");
+  TRY_ARG(hidden && W && targets && loss_mean && dhidden, "llmt_lm_head_ce: NULL argument");
+  TRY_ARG(T > 0 && T % 16 == 0 && seq_len >= 2 && T % seq_len == 0 && H % 32 == 0 &&
+              V % 32 == 0 && H % 8 == 0,
+          "llmt_lm_head_ce: T %% 16, T %% seq_len, H %% 32, V %% 32 must be 0");
+  hipStream_t st = (hipStream_t)stream;
+  Temps tmp(st);
+  _Float16* E = tmp.get<_Float16>((size_t)V * H);
+  _Float16* ET = tmp.get<_Float16>((size_t)V * H);
+  float* logits = tmp.get<float>((size_t)T * V);
+  _Float16* g16 = tmp.get<_Float16>((size_t)T * V);
+  float2* stats = tmp.get<float2>((size_t)T * ce_chunks(V));
+  float* rows = tmp.get<float>(T);
+  const size_t pe = (size_t)gemm_pick_split(T, H, V, 64) * T * H;
+  float* part = tmp.get<float>(pe);
+  TRY_ARG(E && ET && logits && g16 && stats && rows && part, "llmt_lm_head_ce: out of memory");
+  TRY_HIP(pack_f16((const _Float16*)W, H, 0, V, H, E, H, 0, 0, st));
+  TRY_HIP(pack_f16((const _Float16*)W, H, 1, H, V, ET, V, 0, 0, st));
+  return head_ce_packed(st, (const _Float16*)hidden, E, ET, targets, T, seq_len, H, V, logits, g16,
+                        stats, rows, loss_mean, dlogits, dhidden, part, pe);
+}
+
+// ------------------------------------------------------------------ C3
+
+static int attn_shape_ok(int B, int S, int nq, int nkv) {
+  return B > 0 && S > 0 && nq > 0 && nkv > 0 && nq % nkv == 0;
+}
+
+int llmt_attention_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int B,
+                       int S, int nq, int nkv, void* stream) {
+  set_error("");
+  TRY_ARG(q && k && v && o && lse && attn_shape_ok(B, S, nq, nkv),
+          "llmt_attention_fwd: bad arguments");
+  AttnArgs a{};
+  a.q = (const _Float16*)q;
+  a.ldq = (long long)nq * kHeadDim;
+  a.k = (const _Float16*)k;
+  a.ldk = (long long)nkv * kHeadDim;
+  a.v = (const _Float16*)v;
+  a.ldv = (long long)nkv * kHeadDim;
+  a.nq = nq;
+  a.nkv = nkv;
+  a.S = S;
+  a.sm_scale = 1.0f / sqrtf((float)kHeadDim);
+  a.o = (_Float16*)o;
+  a.ldo = (long long)nq * kHeadDim;
+  a.lse = lse;
+  TRY_HIP(attn_fwd(a, B, (hipStream_t)stream));
+  return LLMT_OK;
+}
+
+int llmt_attention_bwd(const void* q, const void* k, const void* v, const void* o,
+                       const float* lse, const float* dout, float* dq, float* dk, float* dv,
+                       int B, int S, int nq, int nkv, void* stream) {
+  set_error("");
+  TRY_ARG(q && k && v && o && lse && dout && dq && dk && dv && attn_shape_ok(B, S, nq, nkv),
+          "llmt_attention_bwd: bad arguments");
+  hipStream_t st = (hipStream_t)stream;
+  const int T = B * S;
+  Temps tmp(st);
+  float* delta = tmp.get<float>((size_t)B * nq * S);
+  float* damax = tmp.get<float>(T);
+  TRY_ARG(delta && damax, "llmt_attention_bwd: out of memory");
+  const long long ldq = (long long)nq * kHeadDim, ldkv = (long long)nkv * kHeadDim;
+  TRY_HIP(attn_delta(dout, ldq, (const _Float16*)o, ldq, nq, S, T, delta, damax, st));
+  AttnArgs a{};
+  a.q = (const _Float16*)q;
+  a.ldq = ldq;
+  a.k = (const _Float16*)k;
+  a.ldk = ldkv;
+  a.v = (const _Float16*)v;
+  a.ldv = ldkv;
+  a.nq = nq;
+  a.nkv = nkv;
+  a.S = S;
+  a.sm_scale = 1.0f / sqrtf((float)kHeadDim);
+  a.lse = const_cast<float*>(lse);  // read-only in the backward
+  a.dO = dout;
+  a.lddo = ldq;
+  a.delta = delta;
+  a.damax = damax;
+  a.dq = dq;
+  a.ldgq = ldq;
+  a.dk = dk;
+  a.dv = dv;
+  a.ldgkv = ldkv;
+  TRY_HIP(attn_bwd(a, B, st));
+  return LLMT_OK;
+}
+
+int llmt_attention_block_bwd(const void* q_raw, const void* k_raw, const void* v,
+                             const float* q_norm, const float* k_norm, const void* dout,
+                             float* dq_raw, float* dk_raw, float* dv, int B, int S, int nq,
+                             int nkv, float theta, float eps, void* stream) {
+  set_error("");
+  TRY_ARG(q_raw && k_raw && v && q_norm && k_norm && dout && dq_raw && dk_raw && dv &&
+              attn_shape_ok(B, S, nq, nkv),
+          "llmt_attention_block_bwd: bad arguments");
+  hipStream_t st = (hipStream_t)stream;
+  const int T = B * S, Q = nq * kHeadDim, KV = nkv * kHeadDim, NT = Q + 2 * KV;
+  Temps tmp(st);
+  _Float16* raw16 = tmp.get<_Float16>((size_t)T * NT);
+  _Float16* qkv16 = tmp.get<_Float16>((size_t)T * NT);
+  float* qkraw = tmp.get<float>((size_t)T * (Q + KV));
+  _Float16* o16 = tmp.get<_Float16>((size_t)T * Q);
+  float* lse = tmp.get<float>((size_t)B * nq * S);
+  float* dO = tmp.get<float>((size_t)T * Q);
+  float* delta = tmp.get<float>((size_t)B * nq * S);
+  float* damax = tmp.get<float>(T);
+  float* dqkv = tmp.get<float>((size_t)T * NT);
+  float* dy = tmp.get<float>((size_t)T * NT);
+  _Float16* g16 = tmp.get<_Float16>((size_t)T * NT);
+  float* rinv = tmp.get<float>(T);
+  float* cosT = tmp.get<float>((size_t)S * 64);
+  float* sinT = tmp.get<float>((size_t)S * 64);
+  TRY_ARG(raw16 && qkv16 && qkraw && o16 && lse && dO && delta && damax && dqkv && dy && g16 &&
+              rinv && cosT && sinT,
+          "llmt_attention_block_bwd: out of memory");
+  // RoPE tables (src/kernels/rope.cu:15-18), angles in double rounded to fp32.
+  std::vector<float> hc((size_t)S * 64), hs((size_t)S * 64);
+  for (int p = 0; p < S; ++p)
+    for (int d = 0; d < 64; ++d) {
+      const double ang = (double)p / pow((double)theta, 2.0 * d / kHeadDim);
+      hc[(size_t)p * 64 + d] = (float)cos(ang);
+      hs[(size_t)p * 64 + d] = (float)sin(ang);
+    }
+  TRY_HIP(hipMemcpyAsync(cosT, hc.data(), hc.size() * 4, hipMemcpyHostToDevice, st));
+  TRY_HIP(hipMemcpyAsync(sinT, hs.data(), hs.size() * 4, hipMemcpyHostToDevice, st));
+  // [q_raw | k_raw | v] rows
+  TRY_HIP(hipMemcpy2DAsync(raw16, NT * 2, q_raw, Q * 2, Q * 2, T, hipMemcpyDeviceToDevice, st));
+  TRY_HIP(hipMemcpy2DAsync(raw16 + Q, NT * 2, k_raw, KV * 2, KV * 2, T, hipMemcpyDeviceToDevice, st));
+  TRY_HIP(hipMemcpy2DAsync(raw16 + Q + KV, NT * 2, v, KV * 2, KV * 2, T, hipMemcpyDeviceToDevice,
+                           st));
+  TRY_HIP(f16_to_f32_rows(raw16, NT, T, Q + KV, qkraw, Q + KV, st));
+  TRY_HIP(qk_norm_rope(raw16, q_norm, k_norm, cosT, sinT, S, nq, nkv, eps, T, qkv16, st));
+  AttnArgs a{};
+  a.q = qkv16;
+  a.ldq = NT;
+  a.k = qkv16 + Q;
+  a.ldk = NT;
+  a.v = qkv16 + Q + KV;
+  a.ldv = NT;
+  a.nq = nq;
+  a.nkv = nkv;
+  a.S = S;
+  a.sm_scale = 1.0f / sqrtf((float)kHeadDim);
+  a.o = o16;
+  a.ldo = Q;
+  a.lse = lse;
+  TRY_HIP(attn_fwd(a, B, st));
+  TRY_HIP(f16_to_f32_rows((const _Float16*)dout, Q, T, Q, dO, Q, st));
+  TRY_HIP(attn_delta(dO, Q, o16, Q, nq, S, T, delta, damax, st));
+  a.dO = dO;
+  a.lddo = Q;
+  a.delta = delta;
+  a.damax = damax;
+  a.dq = dqkv;
+  a.ldgq = NT;
+  a.dk = dqkv + Q;
+  a.dv = dqkv + Q + KV;
+  a.ldgkv = NT;
+  TRY_HIP(attn_bwd(a, B, st));
+  QkBwdArgs qb{};
+  qb.dqkv = dqkv;
+  qb.ld_dqkv = NT;
+  qb.qkraw = qkraw;
+  qb.qn = q_norm;
+  qb.kn = k_norm;
+  qb.cosT = cosT;
+  qb.sinT = sinT;
+  qb.S = S;
+  qb.nq = nq;
+  qb.nkv = nkv;
+  qb.eps = eps;
+  qb.dy32 = dy;
+  qb.g16 = g16;
+  qb.rinv_out = rinv;
+  TRY_HIP(qk_bwd(qb, T, st));
+  TRY_HIP(hipMemcpy2DAsync(dq_raw, Q * 4, dy, NT * 4, Q * 4, T, hipMemcpyDeviceToDevice, st));
+  TRY_HIP(hipMemcpy2DAsync(dk_raw, KV * 4, dy + Q, NT * 4, KV * 4, T, hipMemcpyDeviceToDevice, st));
+  TRY_HIP(hipMemcpy2DAsync(dv, KV * 4, dy + Q + KV, NT * 4, KV * 4, T, hipMemcpyDeviceToDevice, st));
+  return LLMT_OK;
+}
+
+}  // extern "C"

@@ -154,20 +154,20 @@ __global__ __launch_bounds__(NTH) void attn_fwd_kernel(const AttnArgs a) {
   half8 qf[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
-    qf[ks] = frag_global(a.qkv + rowb * a.ldq + a.qcol + h * HD, a.ldq, q, S, ks, lane);
+    qf[ks] = frag_global(a.q + rowb * a.ldq + h * HD, a.ldq, q, S, ks, lane);
 
   floatx4 ot[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) ot[i] = floatx4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f;
 
-  const _Float16* kbase = a.qkv + rowb * a.ldq + a.kcol + kvh * HD;
-  const _Float16* vbase = a.qkv + rowb * a.ldq + a.vcol + kvh * HD;
+  const _Float16* kbase = a.k + rowb * a.ldk + kvh * HD;
+  const _Float16* vbase = a.v + rowb * a.ldv + kvh * HD;
   const int nkb = min(qb, (S - 1) / BLK) + 1;
   for (int kb = 0; kb < nkb; ++kb) {
     __syncthreads();
-    stage_f16(kbase, a.ldq, kb * BLK, S, Ks, nullptr);
-    stage_f16(vbase, a.ldq, kb * BLK, S, nullptr, VT);
+    stage_f16(kbase, a.ldk, kb * BLK, S, Ks, nullptr);
+    stage_f16(vbase, a.ldv, kb * BLK, S, nullptr, VT);
     __syncthreads();
     floatx4 st[4];
 #pragma unroll
@@ -249,8 +249,8 @@ __global__ __launch_bounds__(NTH) void attn_bwd_dkdv_kernel(const AttnArgs a) {
   half8 kf[4], vf[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
-    kf[ks] = frag_global(a.qkv + rowb * a.ldq + a.kcol + kvh * HD, a.ldq, key, S, ks, lane);
-    vf[ks] = frag_global(a.qkv + rowb * a.ldq + a.vcol + kvh * HD, a.ldq, key, S, ks, lane);
+    kf[ks] = frag_global(a.k + rowb * a.ldk + kvh * HD, a.ldk, key, S, ks, lane);
+    vf[ks] = frag_global(a.v + rowb * a.ldv + kvh * HD, a.ldv, key, S, ks, lane);
   }
   floatx4 dkT[8], dvT[8];
 #pragma unroll
@@ -265,7 +265,7 @@ __global__ __launch_bounds__(NTH) void attn_bwd_dkdv_kernel(const AttnArgs a) {
     const float* del_h = a.delta + ((long long)b * a.nq + h) * S;
     for (int qb = kb; qb < nqb; ++qb) {
       __syncthreads();
-      stage_f16(a.qkv + rowb * a.ldq + a.qcol + h * HD, a.ldq, qb * BLK, S, Qs, QT);
+      stage_f16(a.q + rowb * a.ldq + h * HD, a.ldq, qb * BLK, S, Qs, QT);
       stage_f32(a.dO + rowb * a.lddo + h * HD, a.lddo, qb * BLK, S, gs, Ds, DT);
       if (threadIdx.x < BLK) {
         const int qq = qb * BLK + threadIdx.x;
@@ -309,8 +309,8 @@ __global__ __launch_bounds__(NTH) void attn_bwd_dkdv_kernel(const AttnArgs a) {
   }
   if (key < S) {
     const float inv = 1.0f / gs;
-    float* dk = a.dk + (rowb + key) * a.ldg + kvh * HD;
-    float* dv = a.dv + (rowb + key) * a.ldg + kvh * HD;
+    float* dk = a.dk + (rowb + key) * a.ldgkv + kvh * HD;
+    float* dv = a.dv + (rowb + key) * a.ldgkv + kvh * HD;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       *reinterpret_cast<float4*>(dk + dt * 16 + 4 * g) =
@@ -342,7 +342,7 @@ __global__ __launch_bounds__(NTH) void attn_bwd_dq_kernel(const AttnArgs a) {
   half8 qf[4], df[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
-    qf[ks] = frag_global(a.qkv + rowb * a.ldq + a.qcol + h * HD, a.ldq, q, S, ks, lane);
+    qf[ks] = frag_global(a.q + rowb * a.ldq + h * HD, a.ldq, q, S, ks, lane);
     df[ks] = frag_global_f32(a.dO + rowb * a.lddo + h * HD, a.lddo, q, S, ks, lane, gs);
   }
   const bool qok = q < S;
@@ -352,13 +352,13 @@ __global__ __launch_bounds__(NTH) void attn_bwd_dq_kernel(const AttnArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) dqT[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  const _Float16* kbase = a.qkv + rowb * a.ldq + a.kcol + kvh * HD;
-  const _Float16* vbase = a.qkv + rowb * a.ldq + a.vcol + kvh * HD;
+  const _Float16* kbase = a.k + rowb * a.ldk + kvh * HD;
+  const _Float16* vbase = a.v + rowb * a.ldv + kvh * HD;
   const int nkb = min(qb, (S - 1) / BLK) + 1;
   for (int kb = 0; kb < nkb; ++kb) {
     __syncthreads();
-    stage_f16(kbase, a.ldq, kb * BLK, S, Ks, KT);
-    stage_f16(vbase, a.ldq, kb * BLK, S, Vs, nullptr);
+    stage_f16(kbase, a.ldk, kb * BLK, S, Ks, KT);
+    stage_f16(vbase, a.ldv, kb * BLK, S, Vs, nullptr);
     __syncthreads();
     floatx4 pt[4], dt_[4];
 #pragma unroll
@@ -389,7 +389,7 @@ __global__ __launch_bounds__(NTH) void attn_bwd_dq_kernel(const AttnArgs a) {
   }
   if (qok) {
     const float f = a.sm_scale / gs;
-    float* dq = a.dq + (rowb + q) * a.ldg + h * HD;
+    float* dq = a.dq + (rowb + q) * a.ldgq + h * HD;
 #pragma unroll
     for (int d = 0; d < 8; ++d)
       *reinterpret_cast<float4*>(dq + d * 16 + 4 * g) =
@@ -397,7 +397,39 @@ __global__ __launch_bounds__(NTH) void attn_bwd_dq_kernel(const AttnArgs a) {
   }
 }
 
+// Per token row: delta[b, h, s] = sum_d dO[t, h, d] * O[t, h, d] (one wave
+// per head) and damax[t] = max |dO[t, :]|.
+__global__ __launch_bounds__(NTH) void attn_delta_kernel(const float* __restrict__ dO, long long ldd,
+                                                         const _Float16* __restrict__ o,
+                                                         long long ldo, int nq, int S,
+                                                         float* __restrict__ delta,
+                                                         float* __restrict__ damax) {
+  __shared__ float red[NTH / 64];
+  const int t = blockIdx.x;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int b = t / S, s = t - b * S;
+  float amax = 0.f;
+  for (int h = w; h < nq; h += NTH / 64) {
+    const float* d = dO + (long long)t * ldd + h * HD;
+    const _Float16* oo = o + (long long)t * ldo + h * HD;
+    const float d0 = d[lane], d1 = d[lane + 64];
+    amax = fmaxf(amax, fmaxf(fabsf(d0), fabsf(d1)));
+    const float v = wave_sum(d0 * (float)oo[lane] + d1 * (float)oo[lane + 64]);
+    if (lane == 0) delta[((long long)b * nq + h) * S + s] = v;
+  }
+  amax = block_max<NTH / 64>(amax, red);
+  if (threadIdx.x == 0) damax[t] = amax;
+}
+
 }  // namespace
+
+hipError_t attn_delta(const float* dO, long long ldd, const _Float16* o, long long ldo, int nq,
+                      int S, int T, float* delta, float* damax, hipStream_t st) {
+  hipLaunchKernelGGL(attn_delta_kernel, dim3(T), dim3(NTH), 0, st, dO, ldd, o, ldo, nq, S, delta,
+                     damax);
+  LLMT_LAUNCH_CHECK();
+  return hipSuccess;
+}
 
 hipError_t attn_fwd(const AttnArgs& a, int B, hipStream_t st) {
   if (a.nq % a.nkv || a.S <= 0) {

@@ -159,7 +159,13 @@ struct Ctx {
   AdamShadow shadow_desc() const;
   AttnArgs attn_args(const Stash& s) const;
 
-  hipError_t forward(const int* tok, const int* tgt, int B, float* dlogits_out);
+  hipError_t layer_fwd(int l, int B, const float* next_w, float* x_out, _Float16* xn_out);
+  // Embedding + layers + lm_head logits (into logits_out, or the context's).
+  hipError_t forward(const int* tok, int B, float* logits_out);
+  // Fused CE over lg (NULL: the context's logits): loss, grad16, optional fp32 dlogits.
+  hipError_t ce(const float* lg, const int* tgt, int B, float* dlogits_out);
+  hipError_t head_bwd(int B);
+  hipError_t layer_bwd(int l, int B, int accumulate);
   hipError_t backward(int B, int accumulate);
   hipError_t optimizer();
   hipError_t refresh_shadows();

@@ -346,6 +346,12 @@ __global__ __launch_bounds__(256) void reduce_lora_kernel(const ReduceArgs a) {
     v.z += a.lscale * l2;
     v.w += a.lscale * l3;
   }
+  if (a.out_scale != 0.f && a.out_scale != 1.f) {
+    v.x *= a.out_scale;
+    v.y *= a.out_scale;
+    v.z *= a.out_scale;
+    v.w *= a.out_scale;
+  }
   *reinterpret_cast<float4*>(a.out + (long long)(m0 + t) * a.ldo + c) = v;
 }
 

@@ -59,6 +59,7 @@ struct ReduceArgs {
   int nlora;
   LoraUp up[3];
   float lscale;
+  float out_scale;  // 0 is read as 1
 };
 hipError_t reduce_lora(const ReduceArgs& a, hipStream_t st);
 // Pack a row-major block into rows [row0, row0 + R) x k [k0, k0 + C) of a
@@ -167,12 +168,28 @@ hipError_t o_dx_post(const float* part, int split, long long ss, int ldp, const 
                      const _Float16* o16, int nq, int S, int T, float* dh_out, float* dO,
                      float* delta, float* damax, hipStream_t st);
 hipError_t qk_bwd(const QkBwdArgs& a, int T, hipStream_t st);
+// x_out = x (may alias), xn = fp16(rmsnorm(x) * w): a layer input from fp32.
+hipError_t copy_norm(const float* x, const float* w, float eps, int H, int T, float* x_out,
+                     _Float16* xn, hipStream_t st);
+// A gradient row as the fp16 GEMM operand: dres = dy (may alias), g16 =
+// fp16(dy * sc), rinv = 1 / sc with sc the row's power-of-two scale.
+hipError_t grad_rows(const float* dy, int H, int T, float* dres, _Float16* g16, float* rinv,
+                     hipStream_t st);
+// dst[r][c] = (float) src[r][c] for a [rows, cols] block (lds, ldd).
+hipError_t f16_to_f32_rows(const _Float16* src, long long lds, int rows, int cols, float* dst,
+                           long long ldd, hipStream_t st);
+// dst = fp16(src * scale) elementwise.
+hipError_t f32_to_f16_scaled(const float* src, _Float16* dst, size_t n, float scale,
+                             hipStream_t st);
 
 // ---------------------------------------------------------------- attention
 struct AttnArgs {
-  const _Float16* qkv;  // q, k, v columns of one fp16 [T, ldq] buffer
+  const _Float16* q;    // [T, ldq] (head h at column h * 128)
   long long ldq;
-  int qcol, kcol, vcol;
+  const _Float16* k;    // [T, ldk]
+  long long ldk;
+  const _Float16* v;    // [T, ldv]
+  long long ldv;
   int nq, nkv, S;
   float sm_scale;
   _Float16* o;          // forward output [T, ldo]
@@ -182,13 +199,19 @@ struct AttnArgs {
   long long lddo;
   const float* delta;   // [B, nq, S] rowsum(dO * O)
   const float* damax;   // [T] max |dO| per row
-  float* dq;
+  float* dq;            // fp32 [T, ldgq]
+  long long ldgq;
   float* dk;
-  float* dv;            // fp32 [T, ldg] at their head offsets
-  long long ldg;
+  float* dv;            // fp32 [T, ldgkv]
+  long long ldgkv;
 };
 hipError_t attn_fwd(const AttnArgs& a, int B, hipStream_t st);
 hipError_t attn_bwd(const AttnArgs& a, int B, hipStream_t st);
+// Row statistics of a standalone attention backward: delta[b, h, s] =
+// sum_d dO * O and damax[t] = max |dO| over the row (dO fp32 [T, ldd],
+// O fp16 [T, ldo]).
+hipError_t attn_delta(const float* dO, long long ldd, const _Float16* o, long long ldo, int nq,
+                      int S, int T, float* delta, float* damax, hipStream_t st);
 
 // ---------------------------------------------------------------- LoRA / AdamW
 constexpr int kMaxLoraJobs = 8;

@@ -394,12 +394,97 @@ __global__ __launch_bounds__(RT) void qk_bwd_kernel(const QkBwdArgs a) {
   for (int c = threadIdx.x; c < NT; c += RT) a.g16[(long long)t * NT + c] = (_Float16)(ds[c] * sc);
 }
 
+// x_out = x; xn = fp16(rmsnorm(x) * w).
+__global__ __launch_bounds__(RT) void copy_norm_kernel(const float* __restrict__ x,
+                                                       const float* __restrict__ w, float eps,
+                                                       int H, float* x_out,
+                                                       _Float16* __restrict__ xn) {
+  __shared__ float red[2 * RW];
+  const int t = blockIdx.x;
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < H; c += RT) {
+    const float v = x[(long long)t * H + c];
+    ss += v * v;
+  }
+  const float r = rsqrtf(block_sum2(ss, 0.f, red).x / H + eps);
+  for (int c = threadIdx.x; c < H; c += RT) {
+    const float v = x[(long long)t * H + c];
+    x_out[(long long)t * H + c] = v;
+    xn[(long long)t * H + c] = (_Float16)(v * r * w[c]);
+  }
+}
+
+// dres = dy; g16 = fp16(dy * sc); rinv = 1 / sc (sc: the row's power-of-two scale).
+__global__ __launch_bounds__(RT) void grad_rows_kernel(const float* dy, int H, float* dres,
+                                                       _Float16* __restrict__ g16,
+                                                       float* __restrict__ rinv) {
+  __shared__ float red[2 * RW];
+  const int t = blockIdx.x;
+  float amax = 0.f;
+  for (int c = threadIdx.x; c < H; c += RT) amax = fmaxf(amax, fabsf(dy[(long long)t * H + c]));
+  amax = block_max<RW>(amax, red);
+  const float sc = pow2_scale_for(amax);
+  if (threadIdx.x == 0) rinv[t] = 1.0f / sc;
+  for (int c = threadIdx.x; c < H; c += RT) {
+    const float v = dy[(long long)t * H + c];
+    dres[(long long)t * H + c] = v;
+    g16[(long long)t * H + c] = (_Float16)(v * sc);
+  }
+}
+
+__global__ void f16_to_f32_rows_kernel(const _Float16* __restrict__ s, long long lds, int rows,
+                                       int cols, float* __restrict__ d, long long ldd) {
+  const long long n = (long long)rows * cols;
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (long long)gridDim.x * blockDim.x) {
+    const long long r = i / cols, c = i - r * cols;
+    d[r * ldd + c] = (float)s[r * lds + c];
+  }
+}
+
+__global__ void f32_to_f16_scaled_kernel(const float* __restrict__ s, _Float16* __restrict__ d,
+                                         size_t n, float scale) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    d[i] = (_Float16)(s[i] * scale);
+}
+
 inline unsigned grid_elems(long long n) {
   long long g = (n + RT - 1) / RT;
   return (unsigned)(g > 65536 ? 65536 : (g < 1 ? 1 : g));
 }
 
 }  // namespace
+
+hipError_t copy_norm(const float* x, const float* w, float eps, int H, int T, float* x_out,
+                     _Float16* xn, hipStream_t st) {
+  hipLaunchKernelGGL(copy_norm_kernel, dim3(T), dim3(RT), 0, st, x, w, eps, H, x_out, xn);
+  LLMT_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+hipError_t grad_rows(const float* dy, int H, int T, float* dres, _Float16* g16, float* rinv,
+                     hipStream_t st) {
+  hipLaunchKernelGGL(grad_rows_kernel, dim3(T), dim3(RT), 0, st, dy, H, dres, g16, rinv);
+  LLMT_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+hipError_t f16_to_f32_rows(const _Float16* src, long long lds, int rows, int cols, float* dst,
+                           long long ldd, hipStream_t st) {
+  hipLaunchKernelGGL(f16_to_f32_rows_kernel, dim3(grid_elems((long long)rows * cols)), dim3(RT), 0,
+                     st, src, lds, rows, cols, dst, ldd);
+  LLMT_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+hipError_t f32_to_f16_scaled(const float* src, _Float16* dst, size_t n, float scale,
+                             hipStream_t st) {
+  hipLaunchKernelGGL(f32_to_f16_scaled_kernel, dim3(grid_elems((long long)n)), dim3(RT), 0, st, src,
+                     dst, n, scale);
+  LLMT_LAUNCH_CHECK();
+  return hipSuccess;
+}
 
 hipError_t embed_norm(const int* tok, const _Float16* E, int V, int H, const float* w, float eps,
                       int T, float* x, _Float16* xn, hipStream_t st) {

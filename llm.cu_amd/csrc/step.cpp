@@ -173,70 +173,87 @@ AdamShadow Ctx::shadow_desc() const {
 
 // ------------------------------------------------------------------ forward
 
-hipError_t Ctx::forward(const int* tok, const int* tgt, int B, float* dlogits_out) {
+// One decoder layer's forward (src/kernels/lora_forward.cu:198-298) from
+// stash[l].x_in / stash[l].xn; writes the layer output to x_out and its
+// RMSNorm with next_w (the next layer's attention norm, or the final norm)
+// to xn_out.
+hipError_t Ctx::layer_fwd(int l, int B, const float* next_w, float* x_out, _Float16* xn_out) {
   const int T = B * S;
-  const float eps = dims.eps, ls = lscale;
+  const float eps = dims.eps;
+  Layer& w = layers[l];
+  Stash& s = stash[l];
+  GemmOut go;
+  // Q/K/V (+ the three LoRA A) projections in one GEMM; the reduction adds
+  // s (x A^T) B^T per projection.
+  BSeg sq[2] = {wseg(w.wqkv), hseg(shadow_ptr(l, sh_a_qkv), 3 * kRank, H)};
+  const LoraUp uq[3] = {{lora_ptr(lora_p, l, 0, 1), 0, Q, NT, 1},
+                        {lora_ptr(lora_p, l, 1, 1), Q, KV, NT + kRank, 1},
+                        {lora_ptr(lora_p, l, 2, 1), Q + KV, KV, NT + 2 * kRank, 1}};
+  LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn, H, sq, 2, T, H, nullptr, 0, &go, 3, uq));
+  QkvPostArgs qa{};
+  qa.part = go.part; qa.split = go.split; qa.ss = go.ss; qa.ldp = go.ldp;
+  qa.qn = w.q_norm; qa.kn = w.k_norm;
+  qa.cosT = cosT; qa.sinT = sinT;
+  qa.S = S; qa.nq = nq; qa.nkv = nkv; qa.eps = eps;
+  qa.qkraw = s.qkraw; qa.qkv16 = s.qkv16; qa.hbuf = s.h;
   LLMT_HIP_TRY(mark(CAT_ROWS));
-  LLMT_HIP_TRY(embed_norm(tok, E, V, H, layers[0].attn_norm, eps, T, stash[0].x_in, stash[0].xn, st));
+  LLMT_HIP_TRY(qkv_post(qa, T, st));
+  AttnArgs aa = attn_args(s);
+  LLMT_HIP_TRY(mark(CAT_ATTN));
+  LLMT_HIP_TRY(attn_fwd(aa, B, st));
+  // O (+ LoRA A) projection, residual, FFN norm
+  BSeg so[2] = {wseg(w.wo), hseg(shadow_ptr(l, sh_a_o), kRank, Q)};
+  const LoraUp uo[1] = {{lora_ptr(lora_p, l, 3, 1), 0, H, H, 1}};
+  LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.o16, Q, so, 2, T, Q, nullptr, 0, &go, 1, uo));
+  LLMT_HIP_TRY(mark(CAT_ROWS));
+  LLMT_HIP_TRY(o_post(go.part, go.split, go.ss, go.ldp, s.x_in, w.ffn_norm, eps, H, T, s.h,
+                      s.x_mid, s.xn2, st));
+  // gate/up, SwiGLU
+  BSeg sg[1] = {wseg(w.wgu)};
+  LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn2, H, sg, 1, T, H, nullptr, 0, &go));
+  LLMT_HIP_TRY(mark(CAT_ROWS));
+  LLMT_HIP_TRY(gu_post(go.part, go.split, go.ss, go.ldp, I, T, s.gu, a16, st));
+  // down, residual, next norm
+  BSeg sd[1] = {wseg(w.wd)};
+  LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, a16, I, sd, 1, T, I, nullptr, 0, &go));
+  LLMT_HIP_TRY(mark(CAT_ROWS));
+  LLMT_HIP_TRY(resid_norm(go.part, go.split, go.ss, go.ldp, s.x_mid, next_w, eps, H, T, x_out,
+                          xn_out, st));
+  return hipSuccess;
+}
+
+hipError_t Ctx::forward(const int* tok, int B, float* logits_out) {
+  const int T = B * S;
+  LLMT_HIP_TRY(mark(CAT_ROWS));
+  LLMT_HIP_TRY(embed_norm(tok, E, V, H, layers[0].attn_norm, dims.eps, T, stash[0].x_in,
+                          stash[0].xn, st));
   for (int l = 0; l < L; ++l) {
-    Layer& w = layers[l];
-    Stash& s = stash[l];
-    GemmOut go;
-    // Q/K/V (+ the three LoRA A) projections in one GEMM.
-    BSeg sq[2] = {wseg(w.wqkv), hseg(shadow_ptr(l, sh_a_qkv), 3 * kRank, H)};
-    const LoraUp uq[3] = {{lora_ptr(lora_p, l, 0, 1), 0, Q, NT, 1},
-                          {lora_ptr(lora_p, l, 1, 1), Q, KV, NT + kRank, 1},
-                          {lora_ptr(lora_p, l, 2, 1), Q + KV, KV, NT + 2 * kRank, 1}};
-    LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn, H, sq, 2, T, H, nullptr, 0, &go, 3, uq));
-    QkvPostArgs qa{};
-    qa.part = go.part; qa.split = go.split; qa.ss = go.ss; qa.ldp = go.ldp;
-    qa.qn = w.q_norm; qa.kn = w.k_norm;
-    qa.cosT = cosT; qa.sinT = sinT;
-    qa.S = S; qa.nq = nq; qa.nkv = nkv; qa.eps = eps;
-    qa.qkraw = s.qkraw; qa.qkv16 = s.qkv16; qa.hbuf = s.h;
-    LLMT_HIP_TRY(mark(CAT_ROWS));
-    LLMT_HIP_TRY(qkv_post(qa, T, st));
-    // attention
-    AttnArgs aa = attn_args(s);
-    LLMT_HIP_TRY(mark(CAT_ATTN));
-    LLMT_HIP_TRY(attn_fwd(aa, B, st));
-    // O (+ LoRA A) projection, residual, FFN norm
-    BSeg so[2] = {wseg(w.wo), hseg(shadow_ptr(l, sh_a_o), kRank, Q)};
-    const LoraUp uo[1] = {{lora_ptr(lora_p, l, 3, 1), 0, H, H, 1}};
-    LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.o16, Q, so, 2, T, Q, nullptr, 0, &go, 1, uo));
-    LLMT_HIP_TRY(mark(CAT_ROWS));
-    LLMT_HIP_TRY(o_post(go.part, go.split, go.ss, go.ldp, s.x_in, w.ffn_norm, eps, H, T, s.h,
-                        s.x_mid, s.xn2, st));
-    // gate/up, SwiGLU
-    BSeg sg[1] = {wseg(w.wgu)};
-    LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn2, H, sg, 1, T, H, nullptr, 0, &go));
-    LLMT_HIP_TRY(mark(CAT_ROWS));
-    LLMT_HIP_TRY(gu_post(go.part, go.split, go.ss, go.ldp, I, T, s.gu, a16, st));
-    // down, residual, next norm
-    BSeg sd[1] = {wseg(w.wd)};
-    LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, a16, I, sd, 1, T, I, nullptr, 0, &go));
     const bool last = l + 1 == L;
-    LLMT_HIP_TRY(mark(CAT_ROWS));
-    LLMT_HIP_TRY(resid_norm(go.part, go.split, go.ss, go.ldp, s.x_mid,
-                            last ? final_norm : layers[l + 1].attn_norm, eps, H, T,
-                            last ? x_final : stash[l + 1].x_in, last ? xf16 : stash[l + 1].xn, st));
+    LLMT_HIP_TRY(layer_fwd(l, B, last ? final_norm : layers[l + 1].attn_norm,
+                           last ? x_final : stash[l + 1].x_in, last ? xf16 : stash[l + 1].xn));
   }
-  // lm_head logits (tied embedding) and the fused cross-entropy
+  // lm_head logits (tied embedding)
   BSeg se[1] = {hseg(E, V, H)};
-  LLMT_HIP_TRY(gemm(CAT_GEMM_HEAD, xf16, H, se, 1, T, H, logits, V, nullptr));
+  LLMT_HIP_TRY(gemm(CAT_GEMM_HEAD, xf16, H, se, 1, T, H, logits_out ? logits_out : logits, V,
+                    nullptr));
+  return hipSuccess;
+}
+
+hipError_t Ctx::ce(const float* lg, const int* tgt, int B, float* dlogits_out) {
   LLMT_HIP_TRY(mark(CAT_CE));
-  LLMT_HIP_TRY(cross_entropy(logits, tgt, T, V, S, ce_stats, dlogits_out, grad16, loss_rows,
-                             loss_dev, st));
+  LLMT_HIP_TRY(cross_entropy(lg ? lg : logits, tgt, B * S, V, S, ce_stats, dlogits_out, grad16,
+                             loss_rows, loss_dev, st));
   return hipSuccess;
 }
 
 AttnArgs Ctx::attn_args(const Stash& s) const {
   AttnArgs a{};
-  a.qkv = s.qkv16;
+  a.q = s.qkv16;
   a.ldq = NT;
-  a.qcol = 0;
-  a.kcol = Q;
-  a.vcol = Q + KV;
+  a.k = s.qkv16 + Q;
+  a.ldk = NT;
+  a.v = s.qkv16 + Q + KV;
+  a.ldv = NT;
   a.nq = nq;
   a.nkv = nkv;
   a.S = S;
@@ -249,17 +266,21 @@ AttnArgs Ctx::attn_args(const Stash& s) const {
   a.delta = delta;
   a.damax = damax;
   a.dq = dqkv32;
+  a.ldgq = NT;
   a.dk = dqkv32 + Q;
   a.dv = dqkv32 + Q + KV;
-  a.ldg = NT;
+  a.ldgkv = NT;
   return a;
 }
 
 // ------------------------------------------------------------------ backward
 
-hipError_t Ctx::backward(int B, int accumulate) {
+// lm_head dX over the vocabulary (from the fp16 grad16 = (p - onehot) * 2^14)
+// and the final RMSNorm backward: leaves the residual-stream gradient in
+// d_res and its fp16 operand in g16 / rinv.
+hipError_t Ctx::head_bwd(int B) {
   const int T = B * S;
-  const float eps = dims.eps, ls = lscale;
+  const float eps = dims.eps;
   const int n_valid = B * (S - 1);
   GemmOut go;
   // lm_head dX over the vocabulary, then the final RMSNorm backward.
@@ -282,96 +303,112 @@ hipError_t Ctx::backward(int B, int accumulate) {
   nb.rinv_out = rinv;
   LLMT_HIP_TRY(mark(CAT_ROWS));
   LLMT_HIP_TRY(norm_bwd(nb, T, st));
+  return hipSuccess;
+}
 
-  for (int l = L - 1; l >= 0; --l) {
-    Layer& w = layers[l];
-    Stash& s = stash[l];
-    // MLP: down dX -> SwiGLU bwd -> gate/up dX -> FFN norm bwd (+ residual)
-    BSeg sd[1] = {wseg(w.wdT)};
-    LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, sd, 1, T, H, nullptr, 0, &go));
-    LLMT_HIP_TRY(mark(CAT_ROWS));
-    LLMT_HIP_TRY(swiglu_bwd(go.part, go.split, go.ss, go.ldp, rinv, s.gu, I, T, dgu16, rinv2, st));
-    BSeg sg[1] = {wseg(w.wguT)};
-    LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, dgu16, 2 * I, sg, 1, T, 2 * I, nullptr, 0, &go));
-    nb = NormBwdArgs{};
-    nb.part = go.part; nb.split = go.split; nb.ss = go.ss; nb.ldp = go.ldp;
-    nb.rinv_in = rinv2;
-    nb.gscale = 1.0f;
-    nb.nlora = 0;
-    nb.dh_out = dh;
-    nb.x = s.x_mid;
-    nb.w = w.ffn_norm;
-    nb.eps = eps;
-    nb.H = H;
-    nb.dres_in = d_res;
-    nb.dres_out = d_res;
-    nb.dmid_out = dmid;
-    nb.g16 = g16;
-    nb.rinv_out = rinv;
-    LLMT_HIP_TRY(mark(CAT_ROWS));
-    LLMT_HIP_TRY(norm_bwd(nb, T, st));
-    // O projection dX (+ dh_o through the B_o^T rows)
-    BSeg so[2] = {wseg(w.woT), hseg(shadow_ptr(l, sh_bt_o), kRank, H)};
-    const LoraUp ubo[1] = {{lora_ptr(lora_p, l, 3, 0), 0, Q, Q, 0}};
-    LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, so, 2, T, H, nullptr, 0, &go, 1, ubo));
-    LLMT_HIP_TRY(mark(CAT_ROWS));
-    LLMT_HIP_TRY(o_dx_post(go.part, go.split, go.ss, go.ldp, rinv, s.o16, nq, S, T, dh, dO, delta,
-                           damax, st));
-    // attention backward
-    AttnArgs aa = attn_args(s);
-    LLMT_HIP_TRY(mark(CAT_ATTN));
-    LLMT_HIP_TRY(attn_bwd(aa, B, st));
-    // RoPE + QK-norm backward
-    QkBwdArgs qb{};
-    qb.dqkv = dqkv32; qb.ld_dqkv = NT;
-    qb.qkraw = s.qkraw;
-    qb.qn = w.q_norm; qb.kn = w.k_norm;
-    qb.cosT = cosT; qb.sinT = sinT;
-    qb.S = S; qb.nq = nq; qb.nkv = nkv; qb.eps = eps;
-    qb.dy32 = dy32; qb.g16 = g16; qb.rinv_out = rinv;
-    LLMT_HIP_TRY(mark(CAT_ROWS));
-    LLMT_HIP_TRY(qk_bwd(qb, T, st));
-    // Q/K/V dX (+ dh_q, dh_k, dh_v through the B^T rows), attention norm bwd
-    BSeg sq[2] = {wseg(w.wqkvT), hseg(shadow_ptr(l, sh_bt_qkv), 3 * kRank, NT)};
-    const LoraUp ubq[3] = {{lora_ptr(lora_p, l, 0, 0), 0, H, H, 0},
-                           {lora_ptr(lora_p, l, 1, 0), 0, H, H + kRank, 0},
-                           {lora_ptr(lora_p, l, 2, 0), 0, H, H + 2 * kRank, 0}};
-    LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, NT, sq, 2, T, NT, nullptr, 0, &go, 3, ubq));
-    nb = NormBwdArgs{};
-    nb.part = go.part; nb.split = go.split; nb.ss = go.ss; nb.ldp = go.ldp;
-    nb.rinv_in = rinv;
-    nb.gscale = 1.0f;
-    nb.nlora = 3;
-    nb.dh_out = dh;
-    nb.dh_col = 0;
-    nb.x = s.x_in;
-    nb.w = w.attn_norm;
-    nb.eps = eps;
-    nb.H = H;
-    nb.dres_in = d_res;
-    nb.dres_out = d_res;
-    nb.dmid_out = nullptr;
-    nb.g16 = g16;
-    nb.rinv_out = rinv;
-    LLMT_HIP_TRY(mark(CAT_ROWS));
-    LLMT_HIP_TRY(norm_bwd(nb, T, st));
-    // adapter gradients of this layer
-    LoraGradJobs J{};
-    J.n = 8;
-    const LoraGradJob jobs[8] = {
-        {s.xn, 1, H, H, dh + 0, 64, lora_ptr(lora_g, l, 0, 0), 0},
-        {s.xn, 1, H, H, dh + 16, 64, lora_ptr(lora_g, l, 1, 0), 0},
-        {s.xn, 1, H, H, dh + 32, 64, lora_ptr(lora_g, l, 2, 0), 0},
-        {s.o16, 1, Q, Q, dh + 48, 64, lora_ptr(lora_g, l, 3, 0), 0},
-        {dy32, 0, NT, Q, s.h + 0, 64, lora_ptr(lora_g, l, 0, 1), 1},
-        {dy32 + Q, 0, NT, KV, s.h + 16, 64, lora_ptr(lora_g, l, 1, 1), 1},
-        {dy32 + Q + KV, 0, NT, KV, s.h + 32, 64, lora_ptr(lora_g, l, 2, 1), 1},
-        {dmid, 0, H, H, s.h + 48, 64, lora_ptr(lora_g, l, 3, 1), 1},
-    };
-    for (int i = 0; i < 8; ++i) J.job[i] = jobs[i];
-    LLMT_HIP_TRY(mark(CAT_LORA));
-    LLMT_HIP_TRY(lora_grad(J, T, ls, accumulate, st));
-  }
+// One decoder layer's backward (src/kernels/lora_backward.cu:271-406) from
+// d_res / g16 / rinv (the gradient at the layer output); leaves the gradient
+// at the layer input there and writes (or adds, accumulate) the layer's
+// adapter gradients into the GRAD arena.
+hipError_t Ctx::layer_bwd(int l, int B, int accumulate) {
+  const int T = B * S;
+  const float eps = dims.eps, ls = lscale;
+  GemmOut go;
+  NormBwdArgs nb{};
+
+  Layer& w = layers[l];
+  Stash& s = stash[l];
+  // MLP: down dX -> SwiGLU bwd -> gate/up dX -> FFN norm bwd (+ residual)
+  BSeg sd[1] = {wseg(w.wdT)};
+  LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, sd, 1, T, H, nullptr, 0, &go));
+  LLMT_HIP_TRY(mark(CAT_ROWS));
+  LLMT_HIP_TRY(swiglu_bwd(go.part, go.split, go.ss, go.ldp, rinv, s.gu, I, T, dgu16, rinv2, st));
+  BSeg sg[1] = {wseg(w.wguT)};
+  LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, dgu16, 2 * I, sg, 1, T, 2 * I, nullptr, 0, &go));
+  nb = NormBwdArgs{};
+  nb.part = go.part; nb.split = go.split; nb.ss = go.ss; nb.ldp = go.ldp;
+  nb.rinv_in = rinv2;
+  nb.gscale = 1.0f;
+  nb.nlora = 0;
+  nb.dh_out = dh;
+  nb.x = s.x_mid;
+  nb.w = w.ffn_norm;
+  nb.eps = eps;
+  nb.H = H;
+  nb.dres_in = d_res;
+  nb.dres_out = d_res;
+  nb.dmid_out = dmid;
+  nb.g16 = g16;
+  nb.rinv_out = rinv;
+  LLMT_HIP_TRY(mark(CAT_ROWS));
+  LLMT_HIP_TRY(norm_bwd(nb, T, st));
+  // O projection dX (+ dh_o through the B_o^T rows)
+  BSeg so[2] = {wseg(w.woT), hseg(shadow_ptr(l, sh_bt_o), kRank, H)};
+  const LoraUp ubo[1] = {{lora_ptr(lora_p, l, 3, 0), 0, Q, Q, 0}};
+  LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, so, 2, T, H, nullptr, 0, &go, 1, ubo));
+  LLMT_HIP_TRY(mark(CAT_ROWS));
+  LLMT_HIP_TRY(o_dx_post(go.part, go.split, go.ss, go.ldp, rinv, s.o16, nq, S, T, dh, dO, delta,
+                         damax, st));
+  // attention backward
+  AttnArgs aa = attn_args(s);
+  LLMT_HIP_TRY(mark(CAT_ATTN));
+  LLMT_HIP_TRY(attn_bwd(aa, B, st));
+  // RoPE + QK-norm backward
+  QkBwdArgs qb{};
+  qb.dqkv = dqkv32; qb.ld_dqkv = NT;
+  qb.qkraw = s.qkraw;
+  qb.qn = w.q_norm; qb.kn = w.k_norm;
+  qb.cosT = cosT; qb.sinT = sinT;
+  qb.S = S; qb.nq = nq; qb.nkv = nkv; qb.eps = eps;
+  qb.dy32 = dy32; qb.g16 = g16; qb.rinv_out = rinv;
+  LLMT_HIP_TRY(mark(CAT_ROWS));
+  LLMT_HIP_TRY(qk_bwd(qb, T, st));
+  // Q/K/V dX (+ dh_q, dh_k, dh_v through the B^T rows), attention norm bwd
+  BSeg sq[2] = {wseg(w.wqkvT), hseg(shadow_ptr(l, sh_bt_qkv), 3 * kRank, NT)};
+  const LoraUp ubq[3] = {{lora_ptr(lora_p, l, 0, 0), 0, H, H, 0},
+                         {lora_ptr(lora_p, l, 1, 0), 0, H, H + kRank, 0},
+                         {lora_ptr(lora_p, l, 2, 0), 0, H, H + 2 * kRank, 0}};
+  LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, NT, sq, 2, T, NT, nullptr, 0, &go, 3, ubq));
+  nb = NormBwdArgs{};
+  nb.part = go.part; nb.split = go.split; nb.ss = go.ss; nb.ldp = go.ldp;
+  nb.rinv_in = rinv;
+  nb.gscale = 1.0f;
+  nb.nlora = 3;
+  nb.dh_out = dh;
+  nb.dh_col = 0;
+  nb.x = s.x_in;
+  nb.w = w.attn_norm;
+  nb.eps = eps;
+  nb.H = H;
+  nb.dres_in = d_res;
+  nb.dres_out = d_res;
+  nb.dmid_out = nullptr;
+  nb.g16 = g16;
+  nb.rinv_out = rinv;
+  LLMT_HIP_TRY(mark(CAT_ROWS));
+  LLMT_HIP_TRY(norm_bwd(nb, T, st));
+  // adapter gradients of this layer
+  LoraGradJobs J{};
+  J.n = 8;
+  const LoraGradJob jobs[8] = {
+      {s.xn, 1, H, H, dh + 0, 64, lora_ptr(lora_g, l, 0, 0), 0},
+      {s.xn, 1, H, H, dh + 16, 64, lora_ptr(lora_g, l, 1, 0), 0},
+      {s.xn, 1, H, H, dh + 32, 64, lora_ptr(lora_g, l, 2, 0), 0},
+      {s.o16, 1, Q, Q, dh + 48, 64, lora_ptr(lora_g, l, 3, 0), 0},
+      {dy32, 0, NT, Q, s.h + 0, 64, lora_ptr(lora_g, l, 0, 1), 1},
+      {dy32 + Q, 0, NT, KV, s.h + 16, 64, lora_ptr(lora_g, l, 1, 1), 1},
+      {dy32 + Q + KV, 0, NT, KV, s.h + 32, 64, lora_ptr(lora_g, l, 2, 1), 1},
+      {dmid, 0, H, H, s.h + 48, 64, lora_ptr(lora_g, l, 3, 1), 1},
+  };
+  for (int i = 0; i < 8; ++i) J.job[i] = jobs[i];
+  LLMT_HIP_TRY(mark(CAT_LORA));
+  LLMT_HIP_TRY(lora_grad(J, T, ls, accumulate, st));
+  return hipSuccess;
+}
+
+hipError_t Ctx::backward(int B, int accumulate) {
+  LLMT_HIP_TRY(head_bwd(B));
+  for (int l = L - 1; l >= 0; --l) LLMT_HIP_TRY(layer_bwd(l, B, accumulate));
   return hipSuccess;
 }
 
@@ -389,7 +426,8 @@ hipError_t Ctx::refresh_shadows() {
 }
 
 hipError_t Ctx::device_step(int B, int with_adam) {
-  LLMT_HIP_TRY(forward(tok_buf, tgt_buf, B, nullptr));
+  LLMT_HIP_TRY(forward(tok_buf, B, nullptr));
+  LLMT_HIP_TRY(ce(nullptr, tgt_buf, B, nullptr));
   LLMT_HIP_TRY(backward(B, 0));
   if (with_adam) LLMT_HIP_TRY(optimizer());
   LLMT_HIP_TRY(mark(CAT_END));

@@ -72,6 +72,7 @@ _PROTOS = {
     "llmt_layer_forward": (i32, [vp, i32, vp, vp, i32]),
     "llmt_layer_backward": (i32, [vp, i32, vp, vp, i32]),
     "llmt_adamw": (i32, [vp, C.POINTER(HParams), i32]),
+    "llmt_head_ce": (i32, [vp, vp, vp, i32, fp, vp, vp]),
     "llmt_profile_step": (i32, [vp, vp, vp, i32, C.POINTER(HParams), i32, fp, i32,
                                 C.POINTER(C.c_double), C.POINTER(C.c_double)]),
 }
@@ -282,6 +283,30 @@ class Context:
                                           C.byref(loss)))
         return loss.value
 
+    def head_ce(self, hidden16, targets, want_dlogits=False):
+        """C1 on the context's tied embedding: (loss, dlogits or None, dhidden)."""
+        import torch
+        T = hidden16.shape[0]
+        loss = C.c_float()
+        dl = torch.empty(T, self.dims.vocab, dtype=torch.float32, device=hidden16.device) \
+            if want_dlogits else None
+        dh = torch.empty(T, self.dims.hidden, dtype=torch.float32, device=hidden16.device)
+        check(lib().llmt_head_ce(self.h, ptr(hidden16), ptr(targets), T // self.seq_len,
+                                 C.byref(loss), ptr(dl), ptr(dh)))
+        return loss.value, dl, dh
+
+    def layer_forward(self, layer, x, batch):
+        import torch
+        y = torch.empty_like(x)
+        check(lib().llmt_layer_forward(self.h, layer, ptr(x), ptr(y), batch))
+        return y
+
+    def layer_backward(self, layer, dy, batch):
+        import torch
+        dx = torch.empty_like(dy)
+        check(lib().llmt_layer_backward(self.h, layer, ptr(dy), ptr(dx), batch))
+        return dx
+
     def profile_step(self, tokens, targets, hp: HParams, step: int):
         """Per-category kernel milliseconds of one eager step, plus the step's
         GEMM FLOPs and weight bytes."""
@@ -323,3 +348,55 @@ def unflatten_adapters(flat, dims):
         out.append(d)
     assert off == flat.numel()
     return out
+
+
+def lm_head_ce(hidden16, W16, targets, seq_len, want_dlogits=True, stream=None):
+    """Standalone C1: (loss_mean [1], dlogits or None, dhidden [T, H])."""
+    import torch
+    T, H = hidden16.shape
+    V = W16.shape[0]
+    lm = torch.empty(1, dtype=torch.float32, device=hidden16.device)
+    dl = torch.empty(T, V, dtype=torch.float32, device=hidden16.device) if want_dlogits else None
+    dh = torch.empty(T, H, dtype=torch.float32, device=hidden16.device)
+    check(lib().llmt_lm_head_ce(ptr(hidden16), ptr(W16), ptr(targets), T, seq_len, H, V, ptr(lm),
+                                ptr(dl), ptr(dh), stream_ptr(stream)))
+    return lm, dl, dh
+
+
+def attention_fwd(q, k, v, stream=None):
+    """q [B,S,nq,128], k/v [B,S,nkv,128] fp16 -> (o fp16 like q, lse fp32 [B,nq,S])."""
+    import torch
+    B, S, nq, _ = q.shape
+    nkv = k.shape[2]
+    o = torch.empty_like(q)
+    lse = torch.empty(B, nq, S, dtype=torch.float32, device=q.device)
+    check(lib().llmt_attention_fwd(ptr(q), ptr(k), ptr(v), ptr(o), ptr(lse), B, S, nq, nkv,
+                                   stream_ptr(stream)))
+    return o, lse
+
+
+def attention_bwd(q, k, v, o, lse, dout32, stream=None):
+    """Gradients (fp32) w.r.t. q, k, v of the causal GQA attention."""
+    import torch
+    B, S, nq, _ = q.shape
+    nkv = k.shape[2]
+    dq = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    dk = torch.empty(k.shape, dtype=torch.float32, device=q.device)
+    dv = torch.empty(v.shape, dtype=torch.float32, device=q.device)
+    check(lib().llmt_attention_bwd(ptr(q), ptr(k), ptr(v), ptr(o), ptr(lse), ptr(dout32), ptr(dq),
+                                   ptr(dk), ptr(dv), B, S, nq, nkv, stream_ptr(stream)))
+    return dq, dk, dv
+
+
+def attention_block_bwd(q_raw, k_raw, v, q_norm, k_norm, dout16, theta=1e6, eps=1e-6, stream=None):
+    """Config C3: QK-norm + RoPE + flash attention forward and backward."""
+    import torch
+    B, S, nq, _ = q_raw.shape
+    nkv = k_raw.shape[2]
+    dq = torch.empty(q_raw.shape, dtype=torch.float32, device=q_raw.device)
+    dk = torch.empty(k_raw.shape, dtype=torch.float32, device=q_raw.device)
+    dv = torch.empty(v.shape, dtype=torch.float32, device=q_raw.device)
+    check(lib().llmt_attention_block_bwd(ptr(q_raw), ptr(k_raw), ptr(v), ptr(q_norm), ptr(k_norm),
+                                         ptr(dout16), ptr(dq), ptr(dk), ptr(dv), B, S, nq, nkv,
+                                         theta, eps, stream_ptr(stream)))
+    return dq, dk, dv

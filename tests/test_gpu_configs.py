@@ -1,0 +1,364 @@
+"""GPU parity of the benchmark configurations C0-C4 against the
+exact fp32 CPU oracle, through the C ABI.
+
+Tolerances (north star): loss within 1e-3 absolute; every gradient tensor
+within 1e-2 relative L2; integer work bit-exact.  C2 is checked at full size
+(28 layers, vocabulary 151936, batch 1 x seq 128); C4 at full width with
+2 layers and B2 x S256 against the oracle, and at full size through
+size-independent properties (finite, loss near ln V, bit-identical reruns)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import llmt
+from helpers import grad_errors, oracle_grads, rel_l2, upload_model
+from oracle import lora_step as ref
+from oracle.configs import config0, config1, config3, config_model
+
+pytestmark = pytest.mark.gpu
+
+LOSS_TOL = 1e-3
+GRAD_TOL = 1e-2
+Q3 = ref.QWEN3_1_7B
+
+
+@pytest.fixture(scope="module")
+def c2(dev):
+    torch.set_num_threads(16)
+    print("case: C2 full model, seed 1002, B1 x S128", flush=True)
+    W, ad, tok, tgt, _ = config_model(Q3, 1, 128, 1002)
+    loss_ref, grads_ref, _ = oracle_grads(W, ad, tok, tgt, Q3)
+    return dict(W=W, ad=ad, tok=tok, tgt=tgt, loss_ref=float(loss_ref), grads_ref=grads_ref)
+
+
+def test_c2_full_step_parity(c2, dev):
+    ctx = llmt.Context(llmt.make_dims(Q3), 1, 128)
+    try:
+        upload_model(ctx, c2["W"], dev)
+        ctx.lora_set("param", llmt.flatten_adapters(c2["ad"]).to(dev))
+        loss = ctx.forward_backward(c2["tok"].to(dev), c2["tgt"].to(dev))
+        print(f"C2 loss {loss:.6f} oracle {c2['loss_ref']:.6f}", flush=True)
+        assert abs(loss - c2["loss_ref"]) < LOSS_TOL
+        errs = grad_errors(ctx.lora_get("grad"), c2["grads_ref"], Q3)
+        worst = max(errs.items(), key=lambda kv: kv[1])
+        print("C2 worst grad rel-L2", worst, flush=True)
+        assert worst[1] < GRAD_TOL
+        # the step through a captured graph: same loss, then AdamW
+        ctx.set_graph(True)
+        loss_g = ctx.step(c2["tok"].to(dev), c2["tgt"].to(dev), llmt.hparams(), 1)
+        assert loss_g == loss
+    finally:
+        ctx.close()
+
+
+# ------------------------------------------------------------------ compat layer
+
+import ctypes as C
+
+
+class LoraAdapterC(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("A", "B", "mA", "vA", "mB", "vB")] + \
+               [("d_in", C.c_int), ("d_out", C.c_int)]
+
+
+class LoraWeightsC(C.Structure):
+    _fields_ = [(p, LoraAdapterC * 28) for p in ("wq", "wk", "wv", "wo")]
+
+
+class LoraGradC(C.Structure):
+    _fields_ = [("dA", C.c_void_p), ("dB", C.c_void_p)]
+
+
+class LoraGradsC(C.Structure):
+    _fields_ = [(p, LoraGradC * 28) for p in ("wq", "wk", "wv", "wo")]
+
+
+class LoraActsC(C.Structure):
+    _fields_ = [(n, C.c_void_p * 28) for n in (
+        "layer_in", "attn_norm_out", "q_raw", "k_raw", "q_rope", "k_rope", "v_raw", "attn_w",
+        "pre_o", "post_attn", "ffn_norm_out", "gate_raw", "up_raw", "hq", "hk", "hv", "ho")]
+
+
+class LWC(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("attn_norm", "ffn_norm", "wq", "wk", "wv", "wo", "q_norm",
+                                          "k_norm", "w_gate", "w_up", "w_down")] + \
+               [("_pad", C.c_void_p * 21)]
+
+
+class MWC(C.Structure):
+    _fields_ = [("embed_table", C.c_void_p), ("layers", LWC * 28), ("final_norm", C.c_void_p),
+                ("lm_head", C.c_void_p), ("_pad", C.c_void_p * 3)]
+
+
+def test_compat_struct_sizes():
+    assert C.sizeof(LWC) == 32 * 8 and C.sizeof(LoraAdapterC) == 56
+    assert C.sizeof(MWC) == 8 * (1 + 32 * 28 + 5)
+
+
+def test_compat_reference_api_matches_oracle(c2, dev):
+    """The reference's own step API (src/train.cu:261-287 call sequence) with
+    fp16 weights in the MW pad slots (src/main.cu:40-55 map)."""
+    L = llmt.lib()
+    L.lora_weights_init.argtypes = [C.POINTER(LoraWeightsC)]
+    L.lora_grads_alloc.argtypes = [C.POINTER(LoraGradsC), C.POINTER(LoraWeightsC)]
+    L.lora_grads_zero.argtypes = [C.POINTER(LoraGradsC)]
+    L.lora_acts_alloc.argtypes = [C.POINTER(LoraActsC), C.c_int]
+    L.transformer_forward_lora.argtypes = [C.c_void_p, C.POINTER(MWC), C.POINTER(LoraWeightsC)] + \
+        [C.c_void_p] * 12 + [C.POINTER(LoraActsC), C.c_int]
+    L.cross_entropy_forward.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int]
+    L.cross_entropy_forward.restype = C.c_float
+    L.transformer_backward_lora.argtypes = [C.c_void_p, C.POINTER(MWC), C.POINTER(LoraWeightsC),
+                                            C.POINTER(LoraActsC), C.POINTER(LoraGradsC)] + \
+        [C.c_void_p] * 14 + [C.c_int]
+    L.adamw_step_lora.argtypes = [C.POINTER(LoraWeightsC), C.POINTER(LoraGradsC)] + \
+        [C.c_float] * 5 + [C.c_int]
+    L.lora_weights_free.argtypes = [C.POINTER(LoraWeightsC)]
+    L.lora_grads_free.argtypes = [C.POINTER(LoraGradsC)]
+
+    W, S = c2["W"], 128
+    keep = []
+
+    def dev16(t):
+        x = t.to(torch.float16).to(dev).contiguous()
+        keep.append(x)
+        return x.data_ptr()
+
+    def dev32(t):
+        x = t.to(torch.float32).to(dev).contiguous()
+        keep.append(x)
+        return x.data_ptr()
+
+    mw = MWC()
+    for l, lw in enumerate(W.layers):
+        d = mw.layers[l]
+        d.attn_norm, d.ffn_norm = dev32(lw.attn_norm), dev32(lw.ffn_norm)
+        d.q_norm, d.k_norm = dev32(lw.q_norm), dev32(lw.k_norm)
+        for i, name in enumerate(("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")):
+            d._pad[i] = dev16(getattr(lw, name))
+    mw._pad[0] = dev16(W.embed)
+    mw.final_norm = dev32(W.final_norm)
+    lora = LoraWeightsC()
+    L.lora_weights_init(C.byref(lora))
+    # the oracle's adapters into the library-allocated buffers
+    for l in range(28):
+        for p in ref.PROJS:
+            a = getattr(lora, p)[l]
+            for addr, t in ((a.A, c2["ad"][l][p].A), (a.B, c2["ad"][l][p].B)):
+                _ptr_tensor(addr, t.numel(), dev).copy_(t.reshape(-1).float().to(dev))
+    grads = LoraGradsC()
+    L.lora_grads_alloc(C.byref(grads), C.byref(lora))
+    acts = LoraActsC()
+    L.lora_acts_alloc(C.byref(acts), S)
+    tok = c2["tok"].reshape(-1).to(dev)
+    tgt = c2["tgt"].reshape(-1).to(dev)
+    logits = torch.empty(S, Q3.vocab, device=dev)
+    dlogits = torch.empty(S, Q3.vocab, device=dev)
+    ws = [torch.empty(1, device=dev) for _ in range(15)]
+    torch.cuda.synchronize()
+    L.transformer_forward_lora(tok.data_ptr(), C.byref(mw), C.byref(lora),
+                               *[w.data_ptr() for w in ws[:11]], logits.data_ptr(), C.byref(acts), S)
+    loss = L.cross_entropy_forward(logits.data_ptr(), tgt.data_ptr(), dlogits.data_ptr(), S)
+    assert abs(loss - c2["loss_ref"]) < LOSS_TOL
+    assert float(dlogits[-1].abs().max()) == 0.0       # Q4: last row written as zeros
+    L.lora_grads_zero(C.byref(grads))
+    L.transformer_backward_lora(dlogits.data_ptr(), C.byref(mw), C.byref(lora), C.byref(acts),
+                                C.byref(grads), *[w.data_ptr() for w in ws[:14]], S)
+    torch.cuda.synchronize()
+    worst = 0.0
+    for l in range(28):
+        for p in ref.PROJS:
+            gg = getattr(grads, p)[l]
+            dA = _ptr_tensor(gg.dA, c2["grads_ref"][l][p][0].numel(), dev)
+            dB = _ptr_tensor(gg.dB, c2["grads_ref"][l][p][1].numel(), dev)
+            worst = max(worst, rel_l2(dA.cpu().view_as(c2["grads_ref"][l][p][0]), c2["grads_ref"][l][p][0]),
+                        rel_l2(dB.cpu().view_as(c2["grads_ref"][l][p][1]), c2["grads_ref"][l][p][1]))
+    print("compat worst grad rel-L2", worst, flush=True)
+    assert worst < GRAD_TOL
+    L.adamw_step_lora(C.byref(lora), C.byref(grads), 3e-4, 0.9, 0.999, 1e-8, 0.01, 1)
+    torch.cuda.synchronize()
+    a0 = lora.wq[0]
+    got = _ptr_tensor(a0.A, 16 * 2048, dev).cpu().view(16, 2048)
+    want, _, _ = ref.adamw(c2["ad"][0]["wq"].A, c2["grads_ref"][0]["wq"][0], torch.zeros(16, 2048),
+                           torch.zeros(16, 2048), 3e-4, 0.9, 0.999, 1e-8, 0.01, 1)
+    assert rel_l2(got, want) < GRAD_TOL
+    L.lora_grads_free(C.byref(grads))
+    L.lora_weights_free(C.byref(lora))
+
+
+def _ptr_tensor(addr, n, dev):
+    """A float32 torch view of n floats at device address addr."""
+    class _Holder:
+        __cuda_array_interface__ = {"shape": (n,), "typestr": "<f4", "data": (addr, False),
+                                    "version": 3, "strides": None}
+    return torch.as_tensor(_Holder(), device=dev)
+
+
+# ------------------------------------------------------------------ C0
+
+def test_c0_single_layer(dev):
+    print("case: C0 one layer fp32 weights, B1 x S128", flush=True)
+    d1, lw, ad, x, dy = config0()
+    cos, sin = ref.rope_tables(128, d1.head_dim, d1.theta)
+    y_ref, st = ref.layer_forward(x, lw, ad, d1, 1, 128, cos, sin)
+    dx_ref, grads_ref = ref.layer_backward(dy, st, lw, ad, d1, 1, 128, cos, sin)
+    ctx = llmt.Context(llmt.make_dims(d1), 1, 128)
+    try:
+        h = lambda t: t.to(torch.float16).to(dev).contiguous()
+        f = lambda t: t.to(torch.float32).to(dev).contiguous()
+        ctx.set_layer_f16(0, h(lw.wq), h(lw.wk), h(lw.wv), h(lw.wo), h(lw.w_gate), h(lw.w_up),
+                          h(lw.w_down), f(lw.attn_norm), f(lw.ffn_norm), f(lw.q_norm), f(lw.k_norm))
+        ctx.lora_set("param", llmt.flatten_adapters([ad]).to(dev))
+        y = ctx.layer_forward(0, x.to(dev), 1)
+        assert rel_l2(y.cpu(), y_ref) < GRAD_TOL
+        dx = ctx.layer_backward(0, dy.to(dev), 1)
+        assert rel_l2(dx.cpu(), dx_ref) < GRAD_TOL
+        errs = grad_errors(ctx.lora_get("grad"), [grads_ref], d1)
+        print("C0 worst", max(errs.items(), key=lambda kv: kv[1]), flush=True)
+        assert max(errs.values()) < GRAD_TOL
+    finally:
+        ctx.close()
+
+
+# ------------------------------------------------------------------ C1
+
+@pytest.mark.parametrize("via_ctx", [False, True])
+def test_c1_head_ce(dev, via_ctx):
+    print(f"case: C1 lm_head + CE, ctx={via_ctx}", flush=True)
+    x, W, tgt = config1()
+    S = 128
+    logits = x.float() @ W.float().t()
+    valid = ref.valid_rows(1, S)
+    loss_ref, dl_ref, _ = ref.cross_entropy(logits, tgt, valid)
+    dh_ref = dl_ref @ W.float()
+    if via_ctx:
+        d = ref.Dims(n_layers=1)
+        ctx = llmt.Context(llmt.make_dims(d), 1, S)
+        try:
+            ctx.set_embed_f16(W.to(dev), torch.ones(2048, device=dev))
+            loss, dl, dh = ctx.head_ce(x.to(dev), tgt.to(dev), want_dlogits=True)
+        finally:
+            ctx.close()
+    else:
+        lm, dl, dh = llmt.lm_head_ce(x.to(dev), W.to(dev), tgt.to(dev), S)
+        loss = float(lm)
+    assert abs(loss - float(loss_ref)) < LOSS_TOL
+    assert rel_l2(dl.cpu(), dl_ref) < GRAD_TOL
+    assert float(dl[-1].abs().max()) == 0.0
+    assert rel_l2(dh.cpu(), dh_ref) < GRAD_TOL
+
+
+# ------------------------------------------------------------------ C3
+
+def _attn_block_ref(q_raw, k_raw, v, do, eps=1e-6, theta=1e6):
+    """Oracle: QK-RMSNorm (weights 1) + RoPE + causal GQA attention fwd/bwd,
+    returning gradients w.r.t. q_raw, k_raw, v (fp32 on the CPU)."""
+    B, S, nq, hd = q_raw.shape
+    cos, sin = ref.rope_tables(S, hd, theta)
+    w = torch.ones(hd)
+    qr, kr, vv, dd = (t.float() for t in (q_raw, k_raw, v, do))
+    qn = ref.rope_fwd(ref.rmsnorm(qr, w, eps), cos, sin)
+    kn = ref.rope_fwd(ref.rmsnorm(kr, w, eps), cos, sin)
+    # the GPU rounds the normed q, k to fp16 before the attention
+    qn, kn = qn.half().float(), kn.half().float()
+    o, lse = ref.attention_fwd(qn, kn, vv)
+    dq, dk, dv = ref.attention_bwd(dd, qn, kn, vv, o, lse)
+    dq = ref.rmsnorm_bwd(ref.rope_bwd(dq, cos, sin), qr, w, eps)
+    dk = ref.rmsnorm_bwd(ref.rope_bwd(dk, cos, sin), kr, w, eps)
+    return dq, dk, dv
+
+
+@pytest.mark.parametrize("B,S", [(4, 2048), (1, 200)])
+def test_c3_attention_block(dev, B, S):
+    print(f"case: C3 attention block B{B} S{S}", flush=True)
+    q, k, v, do = config3(batch=B, seq_len=S)
+    dq_ref, dk_ref, dv_ref = _attn_block_ref(q, k, v, do)
+    one = torch.ones(128, device=dev)
+    dq, dk, dv = llmt.attention_block_bwd(q.to(dev), k.to(dev), v.to(dev), one, one, do.to(dev))
+    for got, want in ((dq, dq_ref), (dk, dk_ref), (dv, dv_ref)):
+        assert torch.isfinite(got).all()
+        assert rel_l2(got.cpu(), want) < GRAD_TOL
+
+
+@pytest.mark.parametrize("B,S,nq,nkv", [(2, 256, 16, 8), (1, 77, 4, 1), (3, 64, 2, 2)])
+def test_attention_fwd_bwd(dev, B, S, nq, nkv):
+    g = torch.Generator().manual_seed(S + nq)
+    q = torch.randn(B, S, nq, 128, generator=g).half()
+    k = torch.randn(B, S, nkv, 128, generator=g).half()
+    v = torch.randn(B, S, nkv, 128, generator=g).half()
+    do = torch.randn(B, S, nq, 128, generator=g) * 1e-3   # small dO: exercises the dO scale
+    o_ref, lse_ref = ref.attention_fwd(q.float(), k.float(), v.float())
+    o, lse = llmt.attention_fwd(q.to(dev), k.to(dev), v.to(dev))
+    assert rel_l2(o.float().cpu(), o_ref) < 2e-3
+    assert (lse.cpu() - lse_ref).abs().max() < 1e-3
+    dq_ref, dk_ref, dv_ref = ref.attention_bwd(do, q.float(), k.float(), v.float(),
+                                               o.float().cpu(), lse.cpu())
+    dq, dk, dv = llmt.attention_bwd(q.to(dev), k.to(dev), v.to(dev), o, lse, do.to(dev))
+    for got, want in ((dq, dq_ref), (dk, dk_ref), (dv, dv_ref)):
+        assert rel_l2(got.cpu(), want) < GRAD_TOL
+
+
+# ------------------------------------------------------------------ C4 (int8 weights)
+
+def _upload_i8(ctx, W, qs, dev):
+    f = lambda t: t.to(torch.float32).to(dev).contiguous()
+    for l, lw in enumerate(W.layers):
+        names = ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")
+        q8 = [torch.from_numpy(qs[(l, n)][0]).to(dev) for n in names]
+        s16 = [torch.from_numpy(qs[(l, n)][1]).to(dev) for n in names]
+        ctx.set_layer_i8(l, q8, s16, f(lw.attn_norm), f(lw.ffn_norm), f(lw.q_norm), f(lw.k_norm))
+    ctx.set_embed_f16(W.embed.half().to(dev), f(W.final_norm))
+
+
+def test_c4_int8_reduced_matches_oracle(dev):
+    """C4's int8 path (fused dequant in every frozen GEMM) at full width,
+    2 layers, B2 x S256, against the oracle on the dequantised weights."""
+    print("case: C4 reduced (2 layers, B2 S256, int8)", flush=True)
+    d = ref.Dims(n_layers=2)
+    W, ad, tok, tgt, qs = config_model(d, batch=2, seq_len=256, seed=1004, int8=True)
+    loss_ref, grads_ref, _ = oracle_grads(W, ad, tok, tgt, d)
+    ctx = llmt.Context(llmt.make_dims(d), 2, 256, int8=True)
+    try:
+        _upload_i8(ctx, W, qs, dev)
+        ctx.lora_set("param", llmt.flatten_adapters(ad).to(dev))
+        loss = ctx.forward_backward(tok.to(dev), tgt.to(dev))
+        assert abs(loss - float(loss_ref)) < LOSS_TOL
+        errs = grad_errors(ctx.lora_get("grad"), grads_ref, d)
+        print("C4-reduced worst", max(errs.items(), key=lambda kv: kv[1]), flush=True)
+        assert max(errs.values()) < GRAD_TOL
+    finally:
+        ctx.close()
+
+
+def test_device_quantizer_matches_oracle_on_c4_weights(dev):
+    g = torch.Generator().manual_seed(1004)
+    w = torch.randn(2048, 2048, generator=g) * 0.02
+    from oracle.quant import quantize_rows
+    q_ref, s_ref = quantize_rows(w.numpy())
+    q, s = llmt.quantize_rows_i8(w.to(dev))
+    assert np.array_equal(q.cpu().numpy(), q_ref)                 # bit-exact
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+
+
+def test_c4_full_size_properties(dev):
+    """Full C4 (28 layers, int8 weights, B8 x S512): finite loss near ln V,
+    finite gradients, bit-identical reruns (fixed reduction order)."""
+    print("case: C4 full size (B8 S512 int8)", flush=True)
+    import bench
+    ctx = llmt.Context(llmt.make_dims(Q3), 8, 512, int8=True)
+    try:
+        bench.build_model(ctx, Q3, 1004, dev, int8=True)
+        ctx.lora_init(1004, 2048 ** -0.5, 0.01)
+        g = torch.Generator(device=dev).manual_seed(1005)
+        win = torch.randint(0, Q3.vocab, (8, 513), generator=g, device=dev, dtype=torch.int32)
+        tok, tgt = win[:, :-1].contiguous(), win[:, 1:].contiguous()
+        l1 = ctx.forward_backward(tok, tgt)
+        g1 = ctx.lora_get("grad").clone()
+        l2 = ctx.forward_backward(tok, tgt)
+        g2 = ctx.lora_get("grad")
+        assert math.isfinite(l1) and abs(l1 - math.log(Q3.vocab)) < 2.0
+        assert torch.isfinite(g1).all() and g1.abs().max() > 0
+        assert l1 == l2 and torch.equal(g1, g2)
+    finally:
+        ctx.close()

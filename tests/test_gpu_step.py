@@ -105,3 +105,18 @@ def test_lora_save_load_roundtrip(small, tmp_path, dev):
     ctx.lora_set("param", torch.zeros_like(before))
     ctx.lora_load(tmp_path, 5)
     assert torch.equal(ctx.lora_get("param"), before)
+
+
+def test_small_model_matches_golden_fixture(small, dev):
+    """Same step against the committed fixture (tests/golden/small_step.npz)."""
+    import numpy as np
+    from pathlib import Path
+    want = np.load(Path(__file__).resolve().parent / "golden" / "small_step.npz")
+    ctx = small["ctx"]
+    ad = small["ad"]
+    ctx.lora_set("param", llmt.flatten_adapters(ad).to(dev))
+    loss = ctx.forward_backward(small["tok"], small["tgt"])
+    assert abs(loss - float(want["loss"])) < LOSS_TOL
+    got = ctx.lora_get("grad").cpu().double()
+    w = torch.from_numpy(want["grads"]).double()
+    assert float((got - w).norm() / w.norm()) < GRAD_TOL
