@@ -262,7 +262,9 @@ int llmt_layer_forward(llmt_ctx* ctx, int layer, const float* x, float* y, int b
 int llmt_layer_backward(llmt_ctx* ctx, int layer, const float* dy, float* dx, int batch);
 /* AdamW over the whole arena (one multi-tensor launch). */
 int llmt_adamw(llmt_ctx* ctx, const llmt_hparams* hp, int step);
-/* One llmt_step run eagerly with a HIP event between consecutive kernels:
+/* One llmt_step with a HIP event recorded between consecutive kernels (the
+ * step is captured into a graph with event-record nodes and replayed; if
+ * capture fails it runs eagerly, *profile_graph (may be NULL) says which):
  * cat_ms[c] receives the milliseconds spent in each kernel category
  * (0 forward GEMMs, 1 backward GEMMs, 2 lm_head GEMMs, 3 attention, 4 row
  * epilogues, 5 cross-entropy, 6 LoRA grads, 7 AdamW, 8 split-K reductions);
@@ -270,7 +272,15 @@ int llmt_adamw(llmt_ctx* ctx, const llmt_hparams* hp, int step);
  * gemm_weight_bytes (may be NULL) the step's GEMM FLOPs and weight bytes. */
 int llmt_profile_step(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
                       const llmt_hparams* hp, int step, float* cat_ms, int ncat,
-                      double* gemm_flops, double* gemm_weight_bytes);
+                      double* gemm_flops, double* gemm_weight_bytes, int* profile_graph);
+/* The frozen-weight GEMM launches of one llmt_step (same shapes, operands and
+ * workspaces, the other kernels left out) replayed `reps` times as one HIP
+ * graph timed with HIP events on the context's stream: *avg_us = average
+ * duration of one GEMM launch; *launches, *weight_bytes, *flops describe one
+ * step's GEMMs (any may be NULL).  Leaves the adapters stepped once. */
+int llmt_profile_gemms(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
+                       const llmt_hparams* hp, int step, int reps, float* avg_us,
+                       int* launches, double* weight_bytes, double* flops);
 
 /* ---- standalone operators (stream may be NULL) ---- */
 

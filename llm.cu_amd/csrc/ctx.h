@@ -130,6 +130,8 @@ struct Ctx {
   std::vector<int> prof_cat;
   int prof_n = 0;
   double gemm_flops = 0, gemm_wbytes = 0;
+  bool record_gemms = false;       // keep the GemmArgs of every GEMM launched
+  std::vector<GemmArgs> recorded;
 
   ~Ctx();
   int init();

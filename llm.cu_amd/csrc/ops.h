@@ -213,6 +213,10 @@ hipError_t attn_bwd(const AttnArgs& a, int B, hipStream_t st);
 hipError_t attn_delta(const float* dO, long long ldd, const _Float16* o, long long ldo, int nq,
                       int S, int T, float* delta, float* damax, hipStream_t st);
 
+// A one-thread kernel that returns after about `us` microseconds of device
+// wall clock (never more than a few times that: the wait loop is bounded).
+hipError_t gpu_delay(int us, hipStream_t st);
+
 // ---------------------------------------------------------------- LoRA / AdamW
 constexpr int kMaxLoraJobs = 8;
 struct LoraGradJob {

@@ -89,6 +89,7 @@ hipError_t Ctx::gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int 
   }
   LLMT_HIP_TRY(mark(cat));
   LLMT_HIP_TRY(gemm_nt(g, st));
+  if (record_gemms) recorded.push_back(g);
   gemm_flops += 2.0 * M * g.N * K;
   double wbytes = 0;
   for (int i = 0; i < nseg; ++i) wbytes += (double)segs[i].rows * K * (segs[i].is_i8 ? 1 : 2);
@@ -654,9 +655,64 @@ int llmt_set_graph(llmt_ctx* ctx, int enable) {
 
 const float* llmt_logits(const llmt_ctx* ctx) { return ctx ? C_(ctx)->logits : nullptr; }
 
+// Replays exactly the GEMM launches of one step (same shapes, operands and
+// workspaces; the other kernels left out) `reps` times as one captured graph
+// and returns the average duration of one GEMM launch.
+int llmt_profile_gemms(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
+                       const llmt_hparams* hp, int step, int reps, float* avg_us,
+                       int* launches, double* weight_bytes, double* flops) {
+  set_error("");
+  Ctx* c = C_(ctx);
+  int rc = check_tokens(c, tokens, targets, batch);
+  if (rc) return rc;
+  TRY_ARG(avg_us && reps >= 1, "llmt_profile_gemms: avg_us, reps");
+  if ((rc = set_hp(c, hp, step))) return rc;
+  if ((rc = stage_inputs(c, tokens, targets, batch))) return rc;
+  const bool was_graph = c->use_graph;
+  c->use_graph = false;
+  c->record_gemms = true;
+  c->recorded.clear();
+  rc = run_step(c, batch, 1, nullptr);
+  c->record_gemms = false;
+  c->use_graph = was_graph;
+  if (rc) return rc;
+  const double fl = c->gemm_flops, wb = c->gemm_wbytes;
+  std::vector<GemmArgs> gs = c->recorded;
+  hipGraph_t gph = nullptr;
+  hipGraphExec_t ex = nullptr;
+  TRY_HIP(hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
+  hipError_t e = hipSuccess;
+  for (const GemmArgs& g : gs)
+    if (e == hipSuccess) e = gemm_nt(g, c->st);
+  hipError_t e2 = hipStreamEndCapture(c->st, &gph);
+  TRY_HIP(e);
+  TRY_HIP(e2);
+  e = hipGraphInstantiate(&ex, gph, nullptr, nullptr, 0);
+  hipGraphDestroy(gph);
+  TRY_HIP(e);
+  hipEvent_t e0, e1;
+  TRY_HIP(hipEventCreate(&e0));
+  TRY_HIP(hipEventCreate(&e1));
+  TRY_HIP(hipGraphLaunch(ex, c->st));  // warm
+  TRY_HIP(hipEventRecord(e0, c->st));
+  for (int r = 0; r < reps; ++r) TRY_HIP(hipGraphLaunch(ex, c->st));
+  TRY_HIP(hipEventRecord(e1, c->st));
+  TRY_HIP(hipEventSynchronize(e1));
+  float ms = 0.f;
+  TRY_HIP(hipEventElapsedTime(&ms, e0, e1));
+  hipEventDestroy(e0);
+  hipEventDestroy(e1);
+  hipGraphExecDestroy(ex);
+  *avg_us = gs.empty() ? 0.f : ms * 1e3f / (float)(reps * gs.size());
+  if (launches) *launches = (int)gs.size();
+  if (weight_bytes) *weight_bytes = wb;
+  if (flops) *flops = fl;
+  return LLMT_OK;
+}
+
 int llmt_profile_step(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
                       const llmt_hparams* hp, int step, float* cat_ms, int ncat,
-                      double* gemm_flops, double* gemm_weight_bytes) {
+                      double* gemm_flops, double* gemm_weight_bytes, int* profile_graph) {
   set_error("");
   Ctx* c = C_(ctx);
   int rc = check_tokens(c, tokens, targets, batch);
@@ -664,10 +720,48 @@ int llmt_profile_step(llmt_ctx* ctx, const int* tokens, const int* targets, int 
   TRY_ARG(cat_ms && ncat >= 1, "llmt_profile_step: cat_ms");
   if ((rc = set_hp(c, hp, step))) return rc;
   if ((rc = stage_inputs(c, tokens, targets, batch))) return rc;
+  // Events between consecutive kernels.  The profiled step is captured into
+  // a graph (event-record nodes) and replayed, so the kernels run back to
+  // back as in the timed loop; an eager run is the fallback.
   c->profiling = true;
-  rc = run_step(c, batch, 1, nullptr);
+  c->prof_n = 0;
+  c->gemm_flops = c->gemm_wbytes = 0;
+  bool captured = false;
+  {
+    hipGraph_t gph = nullptr;
+    hipGraphExec_t ex = nullptr;
+    if (hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal) == hipSuccess) {
+      hipError_t e = c->device_step(batch, 1);
+      hipError_t e2 = hipStreamEndCapture(c->st, &gph);
+      if (e == hipSuccess && e2 == hipSuccess &&
+          hipGraphInstantiate(&ex, gph, nullptr, nullptr, 0) == hipSuccess &&
+          hipGraphLaunch(ex, c->st) == hipSuccess && hipGraphLaunch(ex, c->st) == hipSuccess &&
+          hipStreamSynchronize(c->st) == hipSuccess) {
+        // Event-record nodes only help if their timestamps can be read back.
+        float ms = 0.f;
+        captured = c->prof_n > 1 &&
+                   hipEventElapsedTime(&ms, c->prof_ev[0], c->prof_ev[1]) == hipSuccess;
+      }
+      if (ex) hipGraphExecDestroy(ex);
+      if (gph) hipGraphDestroy(gph);
+    }
+    (void)hipGetLastError();
+  }
+  if (!captured) {
+    // Eager fallback: a bounded delay kernel first keeps the GPU busy while
+    // the host enqueues the whole step, so the kernels (and the events
+    // between them) then run back to back without host launch gaps.
+    TRY_HIP(gpu_delay(20000, c->st));
+    c->prof_n = 0;
+    c->gemm_flops = c->gemm_wbytes = 0;
+    rc = run_step(c, batch, 1, nullptr);
+    if (rc) {
+      c->profiling = false;
+      return rc;
+    }
+  }
   c->profiling = false;
-  if (rc) return rc;
+  if (profile_graph) *profile_graph = captured ? 1 : 0;
   for (int i = 0; i < ncat; ++i) cat_ms[i] = 0.f;
   for (int i = 0; i + 1 < c->prof_n; ++i) {
     float ms = 0.f;

@@ -73,8 +73,12 @@ _PROTOS = {
     "llmt_layer_backward": (i32, [vp, i32, vp, vp, i32]),
     "llmt_adamw": (i32, [vp, C.POINTER(HParams), i32]),
     "llmt_head_ce": (i32, [vp, vp, vp, i32, fp, vp, vp]),
+    "llmt_profile_gemms": (i32, [vp, vp, vp, i32, C.POINTER(HParams), i32, i32, fp,
+                                 C.POINTER(C.c_int), C.POINTER(C.c_double),
+                                 C.POINTER(C.c_double)]),
     "llmt_profile_step": (i32, [vp, vp, vp, i32, C.POINTER(HParams), i32, fp, i32,
-                                C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+                                C.POINTER(C.c_double), C.POINTER(C.c_double),
+                                C.POINTER(C.c_int)]),
 }
 
 _lib = None
@@ -307,14 +311,24 @@ class Context:
         check(lib().llmt_layer_backward(self.h, layer, ptr(dy), ptr(dx), batch))
         return dx
 
+    def profile_gemms(self, tokens, targets, hp: HParams, step: int, reps: int = 5):
+        """(average GEMM launch us, launches per step, weight bytes, flops per step)."""
+        us, n, wb, fl = C.c_float(), C.c_int(), C.c_double(), C.c_double()
+        check(lib().llmt_profile_gemms(self.h, ptr(tokens), ptr(targets), tokens.shape[0],
+                                       C.byref(hp), step, reps, C.byref(us), C.byref(n),
+                                       C.byref(wb), C.byref(fl)))
+        return us.value, n.value, wb.value, fl.value
+
     def profile_step(self, tokens, targets, hp: HParams, step: int):
         """Per-category kernel milliseconds of one eager step, plus the step's
         GEMM FLOPs and weight bytes."""
         n = len(PROFILE_CATEGORIES)
         ms = (C.c_float * n)()
-        fl, wb = C.c_double(), C.c_double()
+        fl, wb, gr = C.c_double(), C.c_double(), C.c_int()
         check(lib().llmt_profile_step(self.h, ptr(tokens), ptr(targets), tokens.shape[0],
-                                      C.byref(hp), step, ms, n, C.byref(fl), C.byref(wb)))
+                                      C.byref(hp), step, ms, n, C.byref(fl), C.byref(wb),
+                                      C.byref(gr)))
+        self.last_profile_graph = bool(gr.value)
         return dict(zip(PROFILE_CATEGORIES, list(ms))), fl.value, wb.value
 
 
