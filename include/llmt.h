@@ -282,6 +282,14 @@ int llmt_profile_gemms(llmt_ctx* ctx, const int* tokens, const int* targets, int
                        const llmt_hparams* hp, int step, int reps, float* avg_us,
                        int* launches, double* weight_bytes, double* flops);
 
+/* The step's GEMM launches grouped by shape (N, K, split, int8), each group
+ * replayed `reps` times as its own HIP graph.  Per group s < *nshapes
+ * (<= max_shapes): shape_info[5s..5s+4] = N, K, split, launches per step,
+ * int8; shape_us[s] = average launch duration in microseconds. */
+int llmt_profile_gemm_shapes(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
+                             const llmt_hparams* hp, int step, int reps, int max_shapes,
+                             int* nshapes, int* shape_info, float* shape_us);
+
 /* ---- standalone operators (stream may be NULL) ---- */
 
 /* C = A B^T: A [M, K] fp16 (lda), B [N, K] fp16 (ldb), C [M, N] fp32 (ldc).

@@ -28,7 +28,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # The packed-fp32 feature is disabled for every device compile: hipcc -O3
 # otherwise forms v_pk_*_f32 from plain float code on gfx950.
 CFLAGS = [
-    f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
+    f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++20", "-Wall", "-Wno-unused-function",
     "-Wno-unused-variable", "-Wno-unused-but-set-variable",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{ROOT / 'include'}", f"-I{CSRC}",

@@ -180,11 +180,6 @@ int Ctx::init() {
   }
   if (part_elems == 0) part_elems = 1;
   TRY_PTR(part = alloc_n<float>(part_elems));
-  red_elems = 0;
-  for (auto& sh : shapes)
-    if (sh[0] != H || sh[1] != V) red_elems = std::max(red_elems, (size_t)T * sh[0]);
-  red_elems = std::max(red_elems, (size_t)T * H);
-  TRY_PTR(red = alloc_n<float>(red_elems));
   TRY_PTR(a16 = alloc_n<_Float16>(T * I));
   TRY_PTR(d_res = alloc_n<float>(T * H));
   TRY_PTR(dmid = alloc_n<float>(T * H));

@@ -111,8 +111,6 @@ struct Ctx {
 
   float* part = nullptr;   // split-K partials
   size_t part_elems = 0;
-  float* red = nullptr;    // reduced GEMM output (+ LoRA up-projection)
-  size_t red_elems = 0;
   _Float16* a16 = nullptr;
   float *d_res = nullptr, *dmid = nullptr;
   _Float16* g16 = nullptr;
@@ -149,11 +147,14 @@ struct Ctx {
 
   hipError_t mark(int cat);
   // C = A B^T over the segments.  direct: split 1 into `direct` (ld ldc).
-  // Otherwise the result lands in `red` (reduced in fixed split order, plus
-  // the nlora LoRA up-projections) and *out describes it (split 1).
+  // Otherwise the fp32 split-K partials land in `part` and *out describes
+  // them; the consuming row epilogue sums them in split order.
   hipError_t gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int nseg, int M, int K,
-                  float* direct, int ldc, GemmOut* out, int nlora = 0,
-                  const LoraUp* ups = nullptr);
+                  float* direct, int ldc, GemmOut* out);
+  // A GEMM's partials as a row-epilogue input with raw h columns
+  // [hcol, hcol + nh) and LoRA up-projection terms.
+  RowIn row_in(const GemmOut& go, int hcol = 0, int nh = 0, int nterm = 0,
+               const LoraTerm* terms = nullptr) const;
   BSeg wseg(const WMat& w) const;
   BSeg hseg(const _Float16* p, int rows, int ld) const;
   float* lora_ptr(float* arena, int l, int proj, int is_b) const;

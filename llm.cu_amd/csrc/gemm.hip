@@ -38,27 +38,36 @@ static int env_int(const char* name, int dflt) {
 
 namespace {
 
-constexpr int KSTEP = 32;               // k per MFMA
-constexpr int CH_STEPS = 2;             // k-steps per LDS chunk
-constexpr int CH = CH_STEPS * KSTEP;    // 64
-constexpr int RING = 4;                 // B register slots (prefetch distance 3)
-static_assert((2 * CH_STEPS) % RING == 0, "ring slots must be static over two chunks");
+#define LLMT_INLINE __attribute__((always_inline))
+
+constexpr int KSTEP = 32;  // k per MFMA
 
 template <int V>
 using IC = std::integral_constant<int, V>;
 
+constexpr int gcd_c(int a, int b) { return b == 0 ? a : gcd_c(b, a % b); }
+constexpr int lcm_c(int a, int b) { return a / gcd_c(a, b) * b; }
+
 // One workgroup: output tile (MF*16) x (NW*NF*16) over k-steps [s0, s1) of
-// its split.  Chunk c covers k-steps s0 + 8c .. s0 + 8c + 7; steps past s1
-// multiply a zeroed B fragment (branch-free: the compiler then keeps the
-// ring's newer loads in flight across every wait), and every address is
-// clamped into the operand.  With I8 a segment may be int8 (dequantised in
+// its split.  The A tile goes through LDS in chunks of CHS k-steps (two LDS
+// buffers); chunk c + ADIST is loaded into registers while chunk c is
+// multiplied, so an A load has ADIST chunks of MFMA work to land.  B
+// fragments stream through a RING-slot register ring, RING - 1 k-steps
+// ahead.  The main loop body covers UC chunks so that every LDS buffer,
+// A register set and ring slot index is a compile-time constant.  Chunks
+// and k-steps past the end are clamped loads multiplied by zeroed B
+// fragments (branch-free: the compiler then keeps the newer loads in flight
+// across every wait).  With I8 a segment may be int8 (dequantised in
 // registers at MFMA time, optionally times a per-k scale loaded alongside).
-template <int MF, int NF, int NW, bool I8>
+template <int MF, int NF, int NW, int CHS, int RING, int ADIST, bool I8>
 __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
   constexpr int MT = MF * 16;
   constexpr int NT = NW * 64;
+  constexpr int CH = CHS * KSTEP;
   constexpr int PIECES = MT * (CH / 8);  // 16-byte A pieces per chunk
   constexpr int APT = (PIECES + NT - 1) / NT;
+  constexpr int UC = lcm_c(lcm_c(2, ADIST), lcm_c(RING, CHS) / CHS);
+  static_assert(ADIST == 1 || ADIST == 2, "A prefetch distance is one or two chunks");
   // A chunk in LDS in MFMA fragment order: fragment (k-step q, m-tile mi) is
   // 1 KB at (q * MF + mi) * 512 halves with lane l's 8 halves at l * 8, so
   // every ds_read_b128 of a wave is one contiguous, conflict-free 1 KB, and
@@ -73,7 +82,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
   const int s0 = (int)((long long)blockIdx.y * ksteps / g.split);
   const int s1 = (int)((long long)(blockIdx.y + 1) * ksteps / g.split);
   const int nst = s1 - s0;
-  const int nch = (nst + CH_STEPS - 1) / CH_STEPS;
+  const int nch = (nst + CHS - 1) / CHS;
 
   const char* bptr[NF];
   int bi8[NF];
@@ -107,12 +116,13 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
 #pragma unroll
     for (int f = 0; f < NF; ++f) acc[i][f] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  uint4 ra[APT];
-  uint4 rb[RING][NF];
-  uint4 rk[RING][NF];
+  u32x4 ra[ADIST][APT];
+  u32x4 rb[RING][NF];
+  u32x4 rk[RING][NF];
 
-  auto load_a = [&](int c) {
-    const int kb = (s0 + c * CH_STEPS) * KSTEP;
+  auto load_a = [&](int c, auto R) LLMT_INLINE {
+    constexpr int set = decltype(R)::value;
+    const int kb = (s0 + min(c, nch - 1) * CHS) * KSTEP;
 #pragma unroll
     for (int i = 0; i < APT; ++i) {
       const int idx = tid + i * NT;  // LDS piece: fragment idx / 64, lane idx % 64
@@ -121,101 +131,98 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
         const int q = fr / MF, mi = fr % MF;
         const int r = mi * 16 + (l & 15);
         const int k = min(kb + q * KSTEP + (l >> 4) * 8, g.K - 8);
-        ra[i] = *reinterpret_cast<const uint4*>(g.A + (long long)(m0 + r) * g.lda + k);
+        ra[set][i] = *reinterpret_cast<const u32x4*>(g.A + (long long)(m0 + r) * g.lda + k);
       }
     }
   };
-  auto store_a = [&](int buf) {
+  auto store_a = [&](auto R, auto BUF) LLMT_INLINE {
+    constexpr int set = decltype(R)::value;
+    constexpr int buf = decltype(BUF)::value;
 #pragma unroll
     for (int i = 0; i < APT; ++i) {
       const int idx = tid + i * NT;
       if (PIECES % NT == 0 || idx < PIECES)
-        *reinterpret_cast<uint4*>(&As[buf][idx * 8]) = ra[i];
+        *reinterpret_cast<u32x4*>(&As[buf][idx * 8]) = ra[set][i];
     }
   };
-  auto load_b = [&](int j, auto S) {
+  auto load_b = [&](int j, auto S) LLMT_INLINE {
     constexpr int st = decltype(S)::value;
     const long long ss = s0 + min(j, nst - 1);
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
       if (I8 && bi8[f]) {
-        const uint2 q = *reinterpret_cast<const uint2*>(bptr[f] + ss * 512);
-        rb[st][f] = make_uint4(q.x, q.y, 0u, 0u);
-        if (kscale[f]) rk[st][f] = *reinterpret_cast<const uint4*>(kscale[f] + ss * KSTEP);
+        const u32x2 q = *reinterpret_cast<const u32x2*>(bptr[f] + ss * 512);
+        rb[st][f] = u32x4{q[0], q[1], 0u, 0u};
+        if (kscale[f]) rk[st][f] = *reinterpret_cast<const u32x4*>(kscale[f] + ss * KSTEP);
       } else {
-        rb[st][f] = *reinterpret_cast<const uint4*>(bptr[f] + ss * 1024);
+        rb[st][f] = *reinterpret_cast<const u32x4*>(bptr[f] + ss * 1024);
       }
     }
   };
-  auto bfrag = [&](int f, auto S) -> half8 {
+  auto bfrag = [&](int f, auto S) LLMT_INLINE -> half8 {
     constexpr int st = decltype(S)::value;
     half8 h;
     if (I8 && bi8[f]) {
-      const uint4 raw = rb[st][f];
-      int8x8 q;
-      __builtin_memcpy(&q, &raw, 8);
+      const u32x2 raw = {rb[st][f][0], rb[st][f][1]};
+      const int8x8 q = __builtin_bit_cast(int8x8, raw);
 #pragma unroll
       for (int i = 0; i < 8; ++i) h[i] = (_Float16)(float)q[i];
       if (kscale[f]) {
-        half8 sc;
-        __builtin_memcpy(&sc, &rk[st][f], 16);
-        h = h * sc;
+        h = h * __builtin_bit_cast(half8, rk[st][f]);
       }
     } else {
-      __builtin_memcpy(&h, &rb[st][f], 16);
+      h = __builtin_bit_cast(half8, rb[st][f]);
     }
     return h;
   };
-  // k-step q of the chunk pair starting at chunk c (q < CH_STEPS: chunk c in
-  // LDS buffer 0, else chunk c + 1 in buffer 1); ring slot q % RING is static.
-  auto kstep = [&](int c, auto Q) {
+  // k-step j = (chunk base cb + u) * CHS + q: ring slot (u * CHS + q) % RING
+  // and LDS buffer u % 2 are static within the unrolled body.
+  auto kstep = [&](int cb, auto U, auto Q) LLMT_INLINE {
+    constexpr int u = decltype(U)::value;
     constexpr int q = decltype(Q)::value;
-    constexpr int buf = q / CH_STEPS;
-    const int j = c * CH_STEPS + q;
-    load_b(j + RING - 1, IC<(q + RING - 1) % RING>{});
+    constexpr int pos = u * CHS + q;
+    const int j = (cb + u) * CHS + q;
+    load_b(j + RING - 1, IC<(pos + RING - 1) % RING>{});
     const bool live = j < nst;
     half8 b[NF];
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
-      b[f] = bfrag(f, IC<q % RING>{});
+      b[f] = bfrag(f, IC<pos % RING>{});
       if (!live) b[f] = half8{};
     }
 #pragma unroll
     for (int mi = 0; mi < MF; ++mi) {
       const half8 a =
-          *reinterpret_cast<const half8*>(&As[buf][(((q % CH_STEPS) * MF + mi) * 64 + lane) * 8]);
+          *reinterpret_cast<const half8*>(&As[u % 2][((q * MF + mi) * 64 + lane) * 8]);
 #pragma unroll
       for (int f = 0; f < NF; ++f) acc[mi][f] = mfma16(a, b[f], acc[mi][f]);
     }
   };
-  auto ksteps_of = [&](int c, auto Q0) {
-    constexpr int q0 = decltype(Q0)::value;
-    kstep(c, IC<q0>{});
-    kstep(c, IC<q0 + 1>{});
+  auto chunk = [&](int cb, auto U) LLMT_INLINE {
+    constexpr int u = decltype(U)::value;
+    // chunk cb + u + ADIST goes to register set (u + ADIST) % ADIST = u % ADIST
+    load_a(cb + u + ADIST, IC<u % ADIST>{});
+    __builtin_amdgcn_sched_barrier(0);
+    [&]<int... Q>(std::integer_sequence<int, Q...>) LLMT_INLINE {
+      (kstep(cb, IC<u>{}, IC<Q>{}), ...);
+    }(std::make_integer_sequence<int, CHS>{});
+    // chunk cb + u + 1 was loaded ADIST - 1 chunks ago into set (u + 1) % ADIST
+    store_a(IC<(u + 1) % ADIST>{}, IC<(u + 1) % 2>{});
+    __syncthreads();
   };
-  static_assert(CH_STEPS == 2, "ksteps_of covers two k-steps per chunk");
 
   if (nst > 0) {
-    load_a(0);
-    load_b(0, IC<0>{});
-    load_b(1, IC<1>{});
-    load_b(2, IC<2>{});
-    store_a(0);
+    load_a(0, IC<0>{});
+    if constexpr (ADIST == 2) load_a(1, IC<1>{});
+    [&]<int... P>(std::integer_sequence<int, P...>) LLMT_INLINE {
+      (load_b(P, IC<P>{}), ...);
+    }(std::make_integer_sequence<int, RING - 1>{});
+    store_a(IC<0>{}, IC<0>{});
     __syncthreads();
-    // Two chunks per trip: compute from buffer 0 while chunk c+1 lands in
-    // buffer 1, then the reverse.  Chunks past the end are clamped loads
-    // multiplied by zero B fragments.
-    for (int c = 0; c < nch; c += 2) {
-      load_a(min(c + 1, nch - 1));
-      __builtin_amdgcn_sched_barrier(0);
-      ksteps_of(c, IC<0>{});
-      store_a(1);
-      __syncthreads();
-      load_a(min(c + 2, nch - 1));
-      __builtin_amdgcn_sched_barrier(0);
-      ksteps_of(c, IC<CH_STEPS>{});
-      store_a(0);
-      __syncthreads();
+    for (int c = 0; c < nch; c += UC) {
+      [&]<int... U>(std::integer_sequence<int, U...>) LLMT_INLINE {
+        (chunk(c, IC<U>{}), ...);
+      }(std::make_integer_sequence<int, UC>{});
     }
   }
 
@@ -236,24 +243,58 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
   }
 }
 
-template <int MF, int NF, int NW>
+template <int MF, int NF, int NW, int CHS, int RING, int ADIST>
 hipError_t launch_cfg(const GemmArgs& g, hipStream_t st) {
   const int ncols = NW * NF * 16;
   dim3 grid((g.N + ncols - 1) / ncols, g.split, g.M / (MF * 16));
   bool i8 = false;
   for (int i = 0; i < g.nseg; ++i) i8 = i8 || g.seg[i].is_i8;
   if (i8)
-    hipLaunchKernelGGL((gemm_nt_kernel<MF, NF, NW, true>), grid, dim3(NW * 64), 0, st, g);
+    hipLaunchKernelGGL((gemm_nt_kernel<MF, NF, NW, CHS, RING, ADIST, true>), grid, dim3(NW * 64), 0,
+                       st, g);
   else
-    hipLaunchKernelGGL((gemm_nt_kernel<MF, NF, NW, false>), grid, dim3(NW * 64), 0, st, g);
+    hipLaunchKernelGGL((gemm_nt_kernel<MF, NF, NW, CHS, RING, ADIST, false>), grid, dim3(NW * 64),
+                       0, st, g);
   return hipGetLastError();
 }
 
-constexpr int kNW = 8, kNF = 2;  // 256-column tiles
+// Pipeline variants (waves per workgroup, LDS chunk k-steps, B ring slots,
+// A prefetch distance); LLMT_GEMM_CFG selects one for tuning.
+struct GemmCfg {
+  int nw, chs, ring, adist;
+};
+constexpr GemmCfg kCfgs[] = {
+    {8, 2, 4, 1}, {8, 2, 4, 2}, {8, 2, 8, 2}, {8, 4, 8, 1}, {8, 4, 8, 2},
+    {4, 2, 4, 1}, {4, 2, 4, 2}, {4, 2, 8, 2}, {4, 4, 8, 1}, {4, 4, 8, 2},
+};
+constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
+constexpr int kNF = 2;
+
+int gemm_cfg() {
+  const int c = env_int("LLMT_GEMM_CFG", 5);
+  return c >= 0 && c < kNumCfgs ? c : 0;
+}
+
+template <int MF, int C>
+hipError_t launch_c(const GemmArgs& g, hipStream_t st) {
+  constexpr GemmCfg k = kCfgs[C];
+  return launch_cfg<MF, kNF, k.nw, k.chs, k.ring, k.adist>(g, st);
+}
 
 template <int MF>
 hipError_t launch_mf(const GemmArgs& g, hipStream_t st) {
-  return launch_cfg<MF, kNF, kNW>(g, st);
+  switch (gemm_cfg()) {
+    case 1: return launch_c<MF, 1>(g, st);
+    case 2: return launch_c<MF, 2>(g, st);
+    case 3: return launch_c<MF, 3>(g, st);
+    case 4: return launch_c<MF, 4>(g, st);
+    case 5: return launch_c<MF, 5>(g, st);
+    case 6: return launch_c<MF, 6>(g, st);
+    case 7: return launch_c<MF, 7>(g, st);
+    case 8: return launch_c<MF, 8>(g, st);
+    case 9: return launch_c<MF, 9>(g, st);
+    default: return launch_c<MF, 0>(g, st);
+  }
 }
 
 // Fixed-order split-K reduction fused with the LoRA up-projections:
@@ -263,10 +304,33 @@ hipError_t launch_mf(const GemmArgs& g, hipStream_t st) {
 // x A^T forward or dy B backward) is itself a set of extra columns of the same
 // GEMM, reduced here first, per 16-row block, into LDS.  M_p is B [n, 16]
 // (forward: y += s h B^T) or A [16, n] (backward: dx += s dh A).
-// Workgroup: 16 rows x 64 columns; thread = one row x four columns (float4
-// loads, splits added in order, four partial loads in flight).
+// Workgroup: 16 rows x 64 columns; thread = one row x four columns.  The
+// kernel is latency-bound (the partials were just written), so every load
+// it needs (adapter block, h partials, column partials; RB splits at a time)
+// is issued before the first sum; sums run in split order (deterministic).
+constexpr int RB = 16;  // partial loads in flight per thread
+
+__device__ __forceinline__ float4 add4(float4 a, float4 b) {
+  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
+// sum_s p[s * ss] for s < split, in order, RB loads in flight
+__device__ __forceinline__ float4 sum_splits(const float* p, int split, long long ss) {
+  float4 v = *reinterpret_cast<const float4*>(p);
+  for (int k = 1; k < split; k += RB) {
+    float4 x[RB];
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+      x[i] = *reinterpret_cast<const float4*>(p + (long long)min(k + i, split - 1) * ss);
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+      if (k + i < split) v = add4(v, x[i]);
+  }
+  return v;
+}
+
 __global__ __launch_bounds__(256) void reduce_lora_kernel(const ReduceArgs a) {
-  __shared__ float hs[16][3 * 16 + 1];
+  __shared__ float hs[16][3 * 16 + 4];
   __shared__ float ms[3][16][64 + 1];  // this block's 64 columns of each adapter matrix
   const int m0 = blockIdx.y * 16;
   const int cb = blockIdx.x * 64;
@@ -274,62 +338,53 @@ __global__ __launch_bounds__(256) void reduce_lora_kernel(const ReduceArgs a) {
   // Adapter column ranges are multiples of 64 wide and aligned: a block is
   // entirely inside or outside each of them.
   int inside = 0;
-  for (int q = 0; q < a.nlora; ++q) {
+  for (int q = 0; q < a.nlora; ++q)
+    if (cb >= a.up[q].c0 && cb < a.up[q].c0 + a.up[q].n) inside |= 1 << q;
+  // adapter blocks -> registers (12 values per thread per adapter)
+  float mreg[3][4];
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    if (!(inside >> q & 1)) continue;
     const LoraUp& u = a.up[q];
-    if (cb < u.c0 || cb >= u.c0 + u.n) continue;
-    inside |= 1 << q;
     const int jb = cb - u.c0;
-    for (int i = tid; i < 16 * 64; i += 256) {
-      if (u.is_B) {  // B [n, 16]: 64 rows of 16 contiguous floats
-        const int cc = i >> 4, r = i & 15;
-        ms[q][r][cc] = u.M[(long long)(jb + cc) * 16 + r];
-      } else {       // A [16, n]: 16 rows, 64 contiguous floats each
-        const int r = i >> 6, cc = i & 63;
-        ms[q][r][cc] = u.M[(long long)r * u.n + jb + cc];
-      }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = tid + 256 * e;  // 0..1023
+      mreg[q][e] = u.is_B ? u.M[(long long)(jb + (i >> 4)) * 16 + (i & 15)]
+                          : u.M[(long long)(i >> 6) * u.n + jb + (i & 63)];
     }
   }
-  const int nh = 16 * a.nlora;
-  if (inside) {
-    for (int e = tid; e < 16 * nh; e += 256) {
-      const int t = e / nh, j = e % nh;
-      const float* p = a.part + (long long)(m0 + t) * a.ldp + a.up[j >> 4].hcol + (j & 15);
-      float v = p[0];
-      int k = 1;
-      for (; k + 4 <= a.split; k += 4) {
-        const float x0 = p[k * a.ss], x1 = p[(k + 1) * a.ss], x2 = p[(k + 2) * a.ss],
-                    x3 = p[(k + 3) * a.ss];
-        v += x0;
-        v += x1;
-        v += x2;
-        v += x3;
-      }
-      for (; k < a.split; ++k) v += p[k * a.ss];
-      hs[t][j] = v;
-    }
-  }
-  __syncthreads();
+  // h partials: thread -> (row tid / 12, 4 h columns), 192 threads
+  const int nh4 = 4 * a.nlora;  // float4 groups of h per row
+  float4 hv = make_float4(0.f, 0.f, 0.f, 0.f);
+  const bool hthread = inside && tid < 16 * nh4;
+  const int hr = hthread ? tid / nh4 : 0, hg = hthread ? tid % nh4 : 0;
+  if (hthread)
+    hv = sum_splits(a.part + (long long)(m0 + hr) * a.ldp + a.up[hg >> 2].hcol + (hg & 3) * 4,
+                    a.split, a.ss);
   const int t = tid >> 4;
   const int cc = (tid & 15) * 4;
   const int c = cb + cc;
-  if (c >= a.N) return;
-  const float* p = a.part + (long long)(m0 + t) * a.ldp + c;
-  float4 v = *reinterpret_cast<const float4*>(p);
-  int k = 1;
-  for (; k + 4 <= a.split; k += 4) {
-    const float4 x0 = *reinterpret_cast<const float4*>(p + k * a.ss);
-    const float4 x1 = *reinterpret_cast<const float4*>(p + (k + 1) * a.ss);
-    const float4 x2 = *reinterpret_cast<const float4*>(p + (k + 2) * a.ss);
-    const float4 x3 = *reinterpret_cast<const float4*>(p + (k + 3) * a.ss);
-    v.x += x0.x; v.y += x0.y; v.z += x0.z; v.w += x0.w;
-    v.x += x1.x; v.y += x1.y; v.z += x1.z; v.w += x1.w;
-    v.x += x2.x; v.y += x2.y; v.z += x2.z; v.w += x2.w;
-    v.x += x3.x; v.y += x3.y; v.z += x3.z; v.w += x3.w;
+  const bool live = c < a.N;
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (live) v = sum_splits(a.part + (long long)(m0 + t) * a.ldp + c, a.split, a.ss);
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    if (!(inside >> q & 1)) continue;
+    const bool isB = a.up[q].is_B;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = tid + 256 * e;
+      if (isB) ms[q][i & 15][i >> 4] = mreg[q][e];
+      else ms[q][i >> 6][i & 63] = mreg[q][e];
+    }
   }
-  for (; k < a.split; ++k) {
-    const float4 x = *reinterpret_cast<const float4*>(p + k * a.ss);
-    v.x += x.x; v.y += x.y; v.z += x.z; v.w += x.w;
+  if (hthread) {
+    float* h = &hs[hr][(hg >> 2) * 16 + (hg & 3) * 4];
+    h[0] = hv.x; h[1] = hv.y; h[2] = hv.z; h[3] = hv.w;
   }
+  __syncthreads();
+  if (!live) return;
   for (int q = 0; q < a.nlora; ++q) {
     if (!(inside >> q & 1)) continue;
     float l0 = 0.f, l1 = 0.f, l2 = 0.f, l3 = 0.f;
@@ -482,10 +537,12 @@ void gemm_finalize_segments(GemmArgs& g) {
 // per CU (tunable with LLMT_GEMM_TARGET_WG), without splits shorter than
 // LLMT_GEMM_MIN_STEPS k-steps of 32.  Fewer splits means fewer fp32
 // partials to reduce.
-int gemm_tile_n() { return kNW * kNF * 16; }
+int gemm_tile_n() { return kCfgs[gemm_cfg()].nw * kNF * 16; }
 
 int gemm_pick_split(int M, int N, int K, int max_split) {
-  const int target = env_int("LLMT_GEMM_TARGET_WG", 256);
+  // Partials grow with the workgroup count: about 3/4 of the CUs for the
+  // layer GEMMs, two waves of CUs for the very long lm_head dX reduction.
+  const int target = env_int("LLMT_GEMM_TARGET_WG", K > 16384 ? 512 : 192);
   const int min_steps = env_int("LLMT_GEMM_MIN_STEPS", 4);
   const int mt = (M % 128 == 0) ? M / 128 : 1;
   const int tn = gemm_tile_n();
@@ -526,8 +583,8 @@ hipError_t reduce_lora(const ReduceArgs& a, hipStream_t st) {
     return hipErrorInvalidValue;
   }
   for (int q = 0; q < a.nlora; ++q)
-    if (a.up[q].c0 % 64 || a.up[q].n % 64) {
-      set_error("reduce_lora: adapter column ranges must be 64-aligned");
+    if (a.up[q].c0 % 64 || a.up[q].n % 64 || a.up[q].hcol % 4) {
+      set_error("reduce_lora: adapter column ranges must be 64-aligned, h columns 4-aligned");
       return hipErrorInvalidValue;
     }
   dim3 grid((a.N + 63) / 64, a.M / 16);

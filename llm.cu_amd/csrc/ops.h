@@ -94,11 +94,30 @@ hipError_t cross_entropy(const float* logits, const int* targets, int rows, int 
 constexpr float kGradLogitScale = 16384.0f;  // 2^14
 
 // ---------------------------------------------------------------- row kernels
-struct QkvPostArgs {
+// A token row of a split-K GEMM output as the input of a row epilogue: the
+// fp32 partials (summed in split order by the consumer) plus the LoRA
+// up-projection terms, taken from the fragment-packed fp16 adapter shadows:
+//   y[c] += lscale * sum_r h[hidx + r] * shadow(row0 + r, c)   for c in [c0, c0 + n)
+// where h are the raw extra columns [hcol, hcol + nh) of the same GEMM.
+struct LoraTerm {
+  const _Float16* sh;  // element (row0 + r, c) at packed_index(row0 + r, c, kp)
+  int row0, kp;
+  int c0, n;           // multiples of 8
+  int hidx;
+};
+struct RowIn {
   const float* part;
   int split;
   long long ss;
   int ldp;
+  int hcol, nh;  // nh % 4 == 0, nh <= 64 (0: none)
+  int nterm;     // <= 3
+  LoraTerm term[3];
+  float lscale;
+};
+
+struct QkvPostArgs {
+  RowIn in;
   const float* qn;
   const float* kn;
   const float* cosT;
@@ -111,14 +130,10 @@ struct QkvPostArgs {
 };
 
 struct NormBwdArgs {
-  const float* part;
-  int split;
-  long long ss;
-  int ldp;
+  RowIn in;
   const float* rinv_in;  // per-row, may be NULL
   float gscale;
-  int nlora;             // 0..3 adapters whose dh sits at columns H + 16 p
-  float* dh_out;         // [T, 64]
+  float* dh_out;         // [T, 64]: the in.nh raw h columns times the row scale
   int dh_col;
   const float* x;        // RMSNorm input [T, H]
   const float* w;
@@ -149,24 +164,19 @@ struct QkBwdArgs {
 hipError_t embed_norm(const int* tok, const _Float16* E, int V, int H, const float* w, float eps,
                       int T, float* x, _Float16* xn, hipStream_t st);
 hipError_t qkv_post(const QkvPostArgs& a, int T, hipStream_t st);
-hipError_t o_post(const float* part, int split, long long ss, int ldp, const float* x_in,
-                  const float* w, float eps, int H, int T, float* hbuf, float* x_mid,
-                  _Float16* xn2, hipStream_t st);
-hipError_t gu_post(const float* part, int split, long long ss, int ldp, int I, int T, float* gu,
-                   _Float16* a16, hipStream_t st);
-hipError_t resid_norm(const float* part, int split, long long ss, int ldp, const float* x_res,
-                      const float* w, float eps, int H, int T, float* x_out, _Float16* xn,
-                      hipStream_t st);
+hipError_t o_post(const RowIn& in, const float* x_in, const float* w, float eps, int H, int T,
+                  float* hbuf, float* x_mid, _Float16* xn2, hipStream_t st);
+hipError_t gu_post(const RowIn& in, int I, int T, float* gu, _Float16* a16, hipStream_t st);
+hipError_t resid_norm(const RowIn& in, const float* x_res, const float* w, float eps, int H, int T,
+                      float* x_out, _Float16* xn, hipStream_t st);
 hipError_t qk_norm_rope(const _Float16* raw, const float* qn, const float* kn, const float* cosT,
                         const float* sinT, int S, int nq, int nkv, float eps, int T, _Float16* out,
                         hipStream_t st);
 hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st);
-hipError_t swiglu_bwd(const float* part, int split, long long ss, int ldp, const float* rinv_in,
-                      const float* gu, int I, int T, _Float16* dgu16, float* rinv_out,
-                      hipStream_t st);
-hipError_t o_dx_post(const float* part, int split, long long ss, int ldp, const float* rinv_in,
-                     const _Float16* o16, int nq, int S, int T, float* dh_out, float* dO,
-                     float* delta, float* damax, hipStream_t st);
+hipError_t swiglu_bwd(const RowIn& in, const float* rinv_in, const float* gu, int I, int T,
+                      _Float16* dgu16, float* rinv_out, hipStream_t st);
+hipError_t o_dx_post(const RowIn& in, const float* rinv_in, const _Float16* o16, int nq, int S,
+                     int T, float* dh_out, float* dO, float* delta, float* damax, hipStream_t st);
 hipError_t qk_bwd(const QkBwdArgs& a, int T, hipStream_t st);
 // x_out = x (may alias), xn = fp16(rmsnorm(x) * w): a layer input from fp32.
 hipError_t copy_norm(const float* x, const float* w, float eps, int H, int T, float* x_out,

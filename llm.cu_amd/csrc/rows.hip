@@ -27,20 +27,92 @@ constexpr int RW = RT / 64;
 constexpr int HD = 128;  // head_dim
 constexpr int R = 16;    // LoRA rank
 
-// Sum of the split-K partials of one element, in split order (deterministic);
-// four loads are issued before they are added.
-__device__ __forceinline__ float split_sum(const float* __restrict__ p, int split, long long ss) {
-  float s = p[0];
-  int k = 1;
-  for (; k + 4 <= split; k += 4) {
-    const float a = p[k * ss], b = p[(k + 1) * ss], c = p[(k + 2) * ss], d = p[(k + 3) * ss];
-    s += a;
-    s += b;
-    s += c;
-    s += d;
+// Split-K partial sums, in split order (deterministic), with RB8 splits'
+// loads in flight per thread: row epilogues are latency-bound, so every
+// load of a batch is issued before the first add.
+constexpr int RB8 = 8;
+
+__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 add4(float4 a, float4 b) {
+  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
+__device__ __forceinline__ float4 sum_splits4(const float* p, int split, long long ss) {
+  float4 v = ld4(p);
+  for (int k = 1; k < split; k += 2 * RB8) {
+    float4 x[2 * RB8];
+#pragma unroll
+    for (int i = 0; i < 2 * RB8; ++i) x[i] = ld4(p + (long long)min(k + i, split - 1) * ss);
+#pragma unroll
+    for (int i = 0; i < 2 * RB8; ++i)
+      if (k + i < split) v = add4(v, x[i]);
   }
-  for (; k < split; ++k) s += p[k * ss];
-  return s;
+  return v;
+}
+
+__device__ __forceinline__ void sum_splits8(const float* p, int split, long long ss, float4& a,
+                                            float4& b) {
+  a = ld4(p);
+  b = ld4(p + 4);
+  for (int k = 1; k < split; k += RB8) {
+    float4 x[RB8], y[RB8];
+#pragma unroll
+    for (int i = 0; i < RB8; ++i) {
+      const float* q = p + (long long)min(k + i, split - 1) * ss;
+      x[i] = ld4(q);
+      y[i] = ld4(q + 4);
+    }
+#pragma unroll
+    for (int i = 0; i < RB8; ++i)
+      if (k + i < split) {
+        a = add4(a, x[i]);
+        b = add4(b, y[i]);
+      }
+  }
+}
+
+// Row t of a split-K GEMM output into LDS: ys[c] (c < n, n % 8 == 0) = the
+// split sum plus the LoRA up-projection terms covering c; hs[j] (j < in.nh)
+// = the raw h columns.  Thread -> 8-column pieces.  Ends with a barrier.
+__device__ void fetch_row(const RowIn& in, int t, int n, float* ys, float* hs) {
+  const float* prow = in.part + (long long)t * in.ldp;
+  const int tid = threadIdx.x;
+  if (tid < in.nh / 4) {
+    const float4 h = sum_splits4(prow + in.hcol + 4 * tid, in.split, in.ss);
+    hs[4 * tid] = h.x;
+    hs[4 * tid + 1] = h.y;
+    hs[4 * tid + 2] = h.z;
+    hs[4 * tid + 3] = h.w;
+  }
+  for (int pc = tid; pc < n / 8; pc += RT) {
+    float4 a, b;
+    sum_splits8(prow + 8 * pc, in.split, in.ss, a, b);
+    *reinterpret_cast<float4*>(ys + 8 * pc) = a;
+    *reinterpret_cast<float4*>(ys + 8 * pc + 4) = b;
+  }
+  __syncthreads();
+  if (in.nterm == 0) return;
+  for (int pc = tid; pc < n / 8; pc += RT) {
+    const int c = 8 * pc;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < in.nterm; ++q) {
+      const LoraTerm& m = in.term[q];
+      if (c < m.c0 || c >= m.c0 + m.n) continue;
+      half8 wv[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        wv[r] = *reinterpret_cast<const half8*>(m.sh + packed_index(m.row0 + r, c, m.kp));
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float h = hs[m.hidx + r];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += h * (float)wv[r][e];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ys[c + e] += in.lscale * acc[e];
+  }
+  __syncthreads();
 }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
@@ -102,20 +174,18 @@ __global__ __launch_bounds__(RT) void embed_norm_kernel(const int* __restrict__ 
 // (l, l + 64).  Writes q, k (normed, rotated) and v as fp16 [T, Q + 2 KV].
 __global__ __launch_bounds__(RT) void qkv_post_kernel(const QkvPostArgs a) {
   extern __shared__ float ys[];  // [NT]
+  __shared__ float hs[64];
   const int t = blockIdx.x;
   const int Q = a.nq * HD, KV = a.nkv * HD, NT = Q + 2 * KV;
-  const float* prow = a.part + (long long)t * a.ldp;
-  if (threadIdx.x < 3 * R)
-    a.hbuf[(long long)t * 64 + threadIdx.x] = split_sum(prow + NT + threadIdx.x, a.split, a.ss);
+  fetch_row(a.in, t, NT, ys, hs);
+  if (threadIdx.x < a.in.nh) a.hbuf[(long long)t * 64 + threadIdx.x] = hs[threadIdx.x];
   for (int c = threadIdx.x; c < NT; c += RT) {
-    const float y = split_sum(prow + c, a.split, a.ss);
-    ys[c] = y;
+    const float y = ys[c];
     if (c < Q + KV)
       a.qkraw[(long long)t * (Q + KV) + c] = y;
     else
       a.qkv16[(long long)t * NT + c] = (_Float16)y;
   }
-  __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int pos = t % a.S;
   const float cs = a.cosT[pos * (HD / 2) + lane], sn = a.sinT[pos * (HD / 2) + lane];
@@ -133,8 +203,7 @@ __global__ __launch_bounds__(RT) void qkv_post_kernel(const QkvPostArgs a) {
 // After the O(+LoRA-A) GEMM (LoRA term added by its reduction):
 // x_mid = x_in + oW^T + s (o A^T) B^T (residual, src/kernels/elementwise.cu:
 // 4-15), stash h_o, then the FFN RMSNorm -> fp16.
-__global__ __launch_bounds__(RT) void o_post_kernel(const float* __restrict__ part, int split,
-                                                    long long ss_, int ldp,
+__global__ __launch_bounds__(RT) void o_post_kernel(const RowIn in,
                                                     const float* __restrict__ x_in,
                                                     const float* __restrict__ w, float eps, int H,
                                                     float* __restrict__ hbuf,
@@ -142,13 +211,13 @@ __global__ __launch_bounds__(RT) void o_post_kernel(const float* __restrict__ pa
                                                     _Float16* __restrict__ xn2) {
   extern __shared__ float ys[];  // [H]
   __shared__ float red[2 * RW];
+  __shared__ float hs[64];
   const int t = blockIdx.x;
-  const float* prow = part + (long long)t * ldp;
-  if (threadIdx.x < R)
-    hbuf[(long long)t * 64 + 3 * R + threadIdx.x] = split_sum(prow + H + threadIdx.x, split, ss_);
+  fetch_row(in, t, H, ys, hs);
+  if (threadIdx.x < in.nh) hbuf[(long long)t * 64 + 3 * R + threadIdx.x] = hs[threadIdx.x];
   float ssq = 0.f;
   for (int c = threadIdx.x; c < H; c += RT) {
-    const float xm = x_in[(long long)t * H + c] + split_sum(prow + c, split, ss_);
+    const float xm = x_in[(long long)t * H + c] + ys[c];
     x_mid[(long long)t * H + c] = xm;
     ys[c] = xm;
     ssq += xm * xm;
@@ -160,37 +229,42 @@ __global__ __launch_bounds__(RT) void o_post_kernel(const float* __restrict__ pa
 
 // After the fused gate/up GEMM: stash g, u (fp32) and a = silu(g) * u
 // (src/kernels/activation.cu:5-18) as the fp16 operand of the down GEMM.
-__global__ __launch_bounds__(RT) void gu_post_kernel(const float* __restrict__ part, int split,
-                                                     long long ss_, int ldp, int I, long long n,
+__global__ __launch_bounds__(RT) void gu_post_kernel(const RowIn in, int I, long long n4,
                                                      float* __restrict__ gu,
                                                      _Float16* __restrict__ a16) {
-  for (long long i = (long long)blockIdx.x * RT + threadIdx.x; i < n;
+  for (long long i = (long long)blockIdx.x * RT + threadIdx.x; i < n4;
        i += (long long)gridDim.x * RT) {
-    const long long t = i / I;
-    const int c = (int)(i - t * I);
-    const float g = split_sum(part + t * ldp + c, split, ss_);
-    const float u = split_sum(part + t * ldp + I + c, split, ss_);
-    gu[t * 2 * I + c] = g;
-    gu[t * 2 * I + I + c] = u;
-    a16[i] = (_Float16)(silu(g) * u);
+    const long long t = i / (I / 4);
+    const int c = (int)(i - t * (I / 4)) * 4;
+    const float* p = in.part + t * in.ldp + c;
+    const float4 g = sum_splits4(p, in.split, in.ss);
+    const float4 u = sum_splits4(p + I, in.split, in.ss);
+    *reinterpret_cast<float4*>(gu + t * 2 * I + c) = g;
+    *reinterpret_cast<float4*>(gu + t * 2 * I + I + c) = u;
+    half4 o;
+    o[0] = (_Float16)(silu(g.x) * u.x);
+    o[1] = (_Float16)(silu(g.y) * u.y);
+    o[2] = (_Float16)(silu(g.z) * u.z);
+    o[3] = (_Float16)(silu(g.w) * u.w);
+    *reinterpret_cast<half4*>(a16 + t * I + c) = o;
   }
 }
 
 // After the down GEMM: x_out = x_mid + aW_down^T, then the next RMSNorm
 // (the next layer's attention norm, or the final norm) -> fp16.
-__global__ __launch_bounds__(RT) void resid_norm_kernel(const float* __restrict__ part, int split,
-                                                        long long ss_, int ldp,
+__global__ __launch_bounds__(RT) void resid_norm_kernel(const RowIn in,
                                                         const float* __restrict__ x_res,
                                                         const float* __restrict__ w, float eps,
                                                         int H, float* __restrict__ x_out,
                                                         _Float16* __restrict__ xn) {
   extern __shared__ float ys[];
   __shared__ float red[2 * RW];
+  __shared__ float hs[64];
   const int t = blockIdx.x;
-  const float* prow = part + (long long)t * ldp;
+  fetch_row(in, t, H, ys, hs);
   float ssq = 0.f;
   for (int c = threadIdx.x; c < H; c += RT) {
-    const float v = x_res[(long long)t * H + c] + split_sum(prow + c, split, ss_);
+    const float v = x_res[(long long)t * H + c] + ys[c];
     x_out[(long long)t * H + c] = v;
     ys[c] = v;
     ssq += v * v;
@@ -245,17 +319,17 @@ __global__ __launch_bounds__(RT) void qk_norm_rope_kernel(const _Float16* __rest
 __global__ __launch_bounds__(RT) void norm_bwd_kernel(const NormBwdArgs a) {
   extern __shared__ float ds[];  // [H]
   __shared__ float red[2 * RW];
+  __shared__ float hs[64];
   const int t = blockIdx.x;
   const int H = a.H;
-  const float* prow = a.part + (long long)t * a.ldp;
+  fetch_row(a.in, t, H, ds, hs);
   const float rs = (a.rinv_in ? a.rinv_in[t] : 1.0f) * a.gscale;
-  if (threadIdx.x < R * a.nlora)
-    a.dh_out[(long long)t * 64 + a.dh_col + threadIdx.x] =
-        split_sum(prow + H + threadIdx.x, a.split, a.ss) * rs;
+  if (threadIdx.x < a.in.nh)
+    a.dh_out[(long long)t * 64 + a.dh_col + threadIdx.x] = hs[threadIdx.x] * rs;
   const float* x = a.x + (long long)t * H;
   float dot = 0.f, ssx = 0.f;
   for (int c = threadIdx.x; c < H; c += RT) {
-    const float d = split_sum(prow + c, a.split, a.ss) * rs;
+    const float d = ds[c] * rs;
     ds[c] = d;
     const float xv = x[c];
     dot += d * a.w[c] * xv;
@@ -282,21 +356,21 @@ __global__ __launch_bounds__(RT) void norm_bwd_kernel(const NormBwdArgs a) {
 // dX of the down projection -> SwiGLU backward (src/kernels/activation.cu:
 // 26-43 with d_up = dy * silu(g), i.e. without the reference's aliasing of
 // d_gate and d_swiglu at src/kernels/lora_backward.cu:287) -> [dg | du] fp16.
-__global__ __launch_bounds__(RT) void swiglu_bwd_kernel(const float* __restrict__ part, int split,
-                                                        long long ss_, int ldp,
+__global__ __launch_bounds__(RT) void swiglu_bwd_kernel(const RowIn in,
                                                         const float* __restrict__ rinv_in,
                                                         const float* __restrict__ gu, int I,
                                                         _Float16* __restrict__ dgu16,
                                                         float* __restrict__ rinv_out) {
   extern __shared__ float ds[];  // [2 I]
   __shared__ float red[2 * RW];
+  __shared__ float hs[64];
   const int t = blockIdx.x;
-  const float* prow = part + (long long)t * ldp;
+  fetch_row(in, t, I, ds, hs);
   const float rs = rinv_in[t];
   const float* gr = gu + (long long)t * 2 * I;
   float amax = 0.f;
   for (int c = threadIdx.x; c < I; c += RT) {
-    const float da = split_sum(prow + c, split, ss_) * rs;
+    const float da = ds[c] * rs;
     const float g = gr[c], u = gr[I + c];
     const float sg = 1.0f / (1.0f + __expf(-g));
     const float dg = da * u * (sg * (1.0f + g * (1.0f - sg)));
@@ -316,8 +390,7 @@ __global__ __launch_bounds__(RT) void swiglu_bwd_kernel(const float* __restrict_
 // already added s (dh_o A_o)): d_o = row * rinv; writes d_o fp32 (attention
 // dO), dh_o, the row's max |d_o| and the flash-backward row statistic
 // delta[b, h, s] = sum_d dO * O.
-__global__ __launch_bounds__(RT) void o_dx_post_kernel(const float* __restrict__ part, int split,
-                                                       long long ss_, int ldp,
+__global__ __launch_bounds__(RT) void o_dx_post_kernel(const RowIn in,
                                                        const float* __restrict__ rinv_in,
                                                        const _Float16* __restrict__ o16, int nq,
                                                        int S, float* __restrict__ dh_out,
@@ -326,16 +399,15 @@ __global__ __launch_bounds__(RT) void o_dx_post_kernel(const float* __restrict__
                                                        float* __restrict__ damax) {
   extern __shared__ float ds[];  // [Q]
   __shared__ float red[2 * RW];
+  __shared__ float hs[64];
   const int t = blockIdx.x;
   const int Q = nq * HD;
-  const float* prow = part + (long long)t * ldp;
+  fetch_row(in, t, Q, ds, hs);
   const float rs = rinv_in[t];
-  if (threadIdx.x < R)
-    dh_out[(long long)t * 64 + 3 * R + threadIdx.x] =
-        split_sum(prow + Q + threadIdx.x, split, ss_) * rs;
+  if (threadIdx.x < in.nh) dh_out[(long long)t * 64 + 3 * R + threadIdx.x] = hs[threadIdx.x] * rs;
   float amax = 0.f;
   for (int c = threadIdx.x; c < Q; c += RT) {
-    const float d = split_sum(prow + c, split, ss_) * rs;
+    const float d = ds[c] * rs;
     dO[(long long)t * Q + c] = d;
     ds[c] = d;
     amax = fmaxf(amax, fabsf(d));
@@ -456,6 +528,16 @@ inline unsigned grid_elems(long long n) {
 
 }  // namespace
 
+static bool row_in_ok(const RowIn& in, int n, const char* who) {
+  bool ok = in.nh % 4 == 0 && in.nh >= 0 && in.nh <= 64 && in.nterm >= 0 && in.nterm <= 3 &&
+            n % 8 == 0 && in.ldp % 4 == 0 && in.split >= 1 && (in.split == 1 || in.ss % 4 == 0) &&
+            in.hcol % 4 == 0;
+  for (int q = 0; q < in.nterm && ok; ++q)
+    ok = in.term[q].c0 % 8 == 0 && in.term[q].n % 8 == 0 && in.term[q].hidx + R <= in.nh;
+  if (!ok) set_error("%s: unsupported row-input layout (n=%d nh=%d nterm=%d)", who, n, in.nh, in.nterm);
+  return ok;
+}
+
 hipError_t copy_norm(const float* x, const float* w, float eps, int H, int T, float* x_out,
                      _Float16* xn, hipStream_t st) {
   hipLaunchKernelGGL(copy_norm_kernel, dim3(T), dim3(RT), 0, st, x, w, eps, H, x_out, xn);
@@ -495,34 +577,35 @@ hipError_t embed_norm(const int* tok, const _Float16* E, int V, int H, const flo
 
 hipError_t qkv_post(const QkvPostArgs& a, int T, hipStream_t st) {
   const int NT = (a.nq + 2 * a.nkv) * HD;
+  if (!row_in_ok(a.in, NT, "qkv_post")) return hipErrorInvalidValue;
   hipLaunchKernelGGL(qkv_post_kernel, dim3(T), dim3(RT), NT * sizeof(float), st, a);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
 
-hipError_t o_post(const float* part, int split, long long ss, int ldp, const float* x_in,
-                  const float* w, float eps, int H, int T, float* hbuf, float* x_mid,
-                  _Float16* xn2, hipStream_t st) {
-  hipLaunchKernelGGL(o_post_kernel, dim3(T), dim3(RT), H * sizeof(float), st, part, split, ss, ldp,
-                     x_in, w, eps, H, hbuf, x_mid, xn2);
+
+hipError_t o_post(const RowIn& in, const float* x_in, const float* w, float eps, int H, int T,
+                  float* hbuf, float* x_mid, _Float16* xn2, hipStream_t st) {
+  if (!row_in_ok(in, H, "o_post")) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(o_post_kernel, dim3(T), dim3(RT), H * sizeof(float), st, in, x_in, w, eps, H,
+                     hbuf, x_mid, xn2);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
 
-hipError_t gu_post(const float* part, int split, long long ss, int ldp, int I, int T, float* gu,
-                   _Float16* a16, hipStream_t st) {
-  const long long n = (long long)T * I;
-  hipLaunchKernelGGL(gu_post_kernel, dim3(grid_elems(n)), dim3(RT), 0, st, part, split, ss, ldp, I,
-                     n, gu, a16);
+hipError_t gu_post(const RowIn& in, int I, int T, float* gu, _Float16* a16, hipStream_t st) {
+  if (!row_in_ok(in, I, "gu_post") || in.nterm) return hipErrorInvalidValue;
+  const long long n4 = (long long)T * (I / 4);
+  hipLaunchKernelGGL(gu_post_kernel, dim3(grid_elems(n4)), dim3(RT), 0, st, in, I, n4, gu, a16);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
 
-hipError_t resid_norm(const float* part, int split, long long ss, int ldp, const float* x_res,
-                      const float* w, float eps, int H, int T, float* x_out, _Float16* xn,
-                      hipStream_t st) {
-  hipLaunchKernelGGL(resid_norm_kernel, dim3(T), dim3(RT), H * sizeof(float), st, part, split, ss,
-                     ldp, x_res, w, eps, H, x_out, xn);
+hipError_t resid_norm(const RowIn& in, const float* x_res, const float* w, float eps, int H, int T,
+                      float* x_out, _Float16* xn, hipStream_t st) {
+  if (!row_in_ok(in, H, "resid_norm")) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(resid_norm_kernel, dim3(T), dim3(RT), H * sizeof(float), st, in, x_res, w, eps,
+                     H, x_out, xn);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
@@ -537,29 +620,26 @@ hipError_t qk_norm_rope(const _Float16* raw, const float* qn, const float* kn, c
 }
 
 hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st) {
-  if (a.nlora < 0 || a.nlora > 3) {
-    set_error("norm_bwd: nlora=%d", a.nlora);
-    return hipErrorInvalidValue;
-  }
+  if (!row_in_ok(a.in, a.H, "norm_bwd")) return hipErrorInvalidValue;
   hipLaunchKernelGGL(norm_bwd_kernel, dim3(T), dim3(RT), a.H * sizeof(float), st, a);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
 
-hipError_t swiglu_bwd(const float* part, int split, long long ss, int ldp, const float* rinv_in,
-                      const float* gu, int I, int T, _Float16* dgu16, float* rinv_out,
-                      hipStream_t st) {
-  hipLaunchKernelGGL(swiglu_bwd_kernel, dim3(T), dim3(RT), 2 * I * sizeof(float), st, part, split,
-                     ss, ldp, rinv_in, gu, I, dgu16, rinv_out);
+hipError_t swiglu_bwd(const RowIn& in, const float* rinv_in, const float* gu, int I, int T,
+                      _Float16* dgu16, float* rinv_out, hipStream_t st) {
+  if (!row_in_ok(in, I, "swiglu_bwd")) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(swiglu_bwd_kernel, dim3(T), dim3(RT), 2 * I * sizeof(float), st, in, rinv_in,
+                     gu, I, dgu16, rinv_out);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
 
-hipError_t o_dx_post(const float* part, int split, long long ss, int ldp, const float* rinv_in,
-                     const _Float16* o16, int nq, int S, int T, float* dh_out, float* dO,
-                     float* delta, float* damax, hipStream_t st) {
-  hipLaunchKernelGGL(o_dx_post_kernel, dim3(T), dim3(RT), nq * HD * sizeof(float), st, part, split,
-                     ss, ldp, rinv_in, o16, nq, S, dh_out, dO, delta, damax);
+hipError_t o_dx_post(const RowIn& in, const float* rinv_in, const _Float16* o16, int nq, int S,
+                     int T, float* dh_out, float* dO, float* delta, float* damax, hipStream_t st) {
+  if (!row_in_ok(in, nq * HD, "o_dx_post")) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(o_dx_post_kernel, dim3(T), dim3(RT), nq * HD * sizeof(float), st, in, rinv_in,
+                     o16, nq, S, dh_out, dO, delta, damax);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }

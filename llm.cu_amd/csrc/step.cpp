@@ -14,6 +14,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <array>
 #include <vector>
 
 #include "../../include/llmt.h"
@@ -63,7 +64,7 @@ hipError_t Ctx::mark(int cat) {
 }
 
 hipError_t Ctx::gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int nseg, int M, int K,
-                     float* direct, int ldc, GemmOut* out, int nlora, const LoraUp* ups) {
+                     float* direct, int ldc, GemmOut* out) {
   GemmArgs g{};
   g.A = A;
   g.lda = lda;
@@ -82,7 +83,7 @@ hipError_t Ctx::gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int 
     g.C = part;
     g.ldc = g.N;
     g.split_stride = (long long)M * g.N;
-    if ((size_t)g.split * M * g.N > part_elems || (size_t)M * g.N > red_elems) {
+    if ((size_t)g.split * M * g.N > part_elems) {
       set_error("gemm: workspace too small (%d x %d x %d > %zu)", g.split, M, g.N, part_elems);
       return hipErrorInvalidValue;
     }
@@ -99,26 +100,21 @@ hipError_t Ctx::gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int 
   out->split = g.split;
   out->ss = g.split_stride;
   out->ldp = g.ldc;
-  if (!direct && (g.split > 1 || nlora > 0)) {
-    ReduceArgs ra{};
-    ra.part = g.C;
-    ra.split = g.split;
-    ra.ss = g.split_stride;
-    ra.ldp = g.ldc;
-    ra.out = red;
-    ra.ldo = g.N;
-    ra.M = M;
-    ra.N = g.N;
-    ra.nlora = nlora;
-    for (int i = 0; i < nlora; ++i) ra.up[i] = ups[i];
-    ra.lscale = lscale;
-    LLMT_HIP_TRY(mark(CAT_REDUCE));
-    LLMT_HIP_TRY(reduce_lora(ra, st));
-    out->part = red;
-    out->split = 1;
-    out->ss = 0;
-  }
   return hipSuccess;
+}
+
+RowIn Ctx::row_in(const GemmOut& go, int hcol, int nh, int nterm, const LoraTerm* terms) const {
+  RowIn r{};
+  r.part = go.part;
+  r.split = go.split;
+  r.ss = go.ss;
+  r.ldp = go.ldp;
+  r.hcol = hcol;
+  r.nh = nh;
+  r.nterm = nterm;
+  for (int i = 0; i < nterm; ++i) r.term[i] = terms[i];
+  r.lscale = lscale;
+  return r;
 }
 
 // ------------------------------------------------------------------ layout helpers
@@ -184,15 +180,16 @@ hipError_t Ctx::layer_fwd(int l, int B, const float* next_w, float* x_out, _Floa
   Layer& w = layers[l];
   Stash& s = stash[l];
   GemmOut go;
-  // Q/K/V (+ the three LoRA A) projections in one GEMM; the reduction adds
-  // s (x A^T) B^T per projection.
+  // Q/K/V (+ the three LoRA A) projections in one GEMM; the epilogue adds
+  // s (x A^T) B^T per projection from the h columns.
   BSeg sq[2] = {wseg(w.wqkv), hseg(shadow_ptr(l, sh_a_qkv), 3 * kRank, H)};
-  const LoraUp uq[3] = {{lora_ptr(lora_p, l, 0, 1), 0, Q, NT, 1},
-                        {lora_ptr(lora_p, l, 1, 1), Q, KV, NT + kRank, 1},
-                        {lora_ptr(lora_p, l, 2, 1), Q + KV, KV, NT + 2 * kRank, 1}};
-  LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn, H, sq, 2, T, H, nullptr, 0, &go, 3, uq));
+  const _Float16* bt_qkv = shadow_ptr(l, sh_bt_qkv);
+  const LoraTerm tq[3] = {{bt_qkv, 0, NT, 0, Q, 0},
+                          {bt_qkv, kRank, NT, Q, KV, kRank},
+                          {bt_qkv, 2 * kRank, NT, Q + KV, KV, 2 * kRank}};
+  LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn, H, sq, 2, T, H, nullptr, 0, &go));
   QkvPostArgs qa{};
-  qa.part = go.part; qa.split = go.split; qa.ss = go.ss; qa.ldp = go.ldp;
+  qa.in = row_in(go, NT, 3 * kRank, 3, tq);
   qa.qn = w.q_norm; qa.kn = w.k_norm;
   qa.cosT = cosT; qa.sinT = sinT;
   qa.S = S; qa.nq = nq; qa.nkv = nkv; qa.eps = eps;
@@ -204,22 +201,21 @@ hipError_t Ctx::layer_fwd(int l, int B, const float* next_w, float* x_out, _Floa
   LLMT_HIP_TRY(attn_fwd(aa, B, st));
   // O (+ LoRA A) projection, residual, FFN norm
   BSeg so[2] = {wseg(w.wo), hseg(shadow_ptr(l, sh_a_o), kRank, Q)};
-  const LoraUp uo[1] = {{lora_ptr(lora_p, l, 3, 1), 0, H, H, 1}};
-  LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.o16, Q, so, 2, T, Q, nullptr, 0, &go, 1, uo));
+  const LoraTerm to[1] = {{shadow_ptr(l, sh_bt_o), 0, H, 0, H, 0}};
+  LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.o16, Q, so, 2, T, Q, nullptr, 0, &go));
   LLMT_HIP_TRY(mark(CAT_ROWS));
-  LLMT_HIP_TRY(o_post(go.part, go.split, go.ss, go.ldp, s.x_in, w.ffn_norm, eps, H, T, s.h,
-                      s.x_mid, s.xn2, st));
+  LLMT_HIP_TRY(o_post(row_in(go, H, kRank, 1, to), s.x_in, w.ffn_norm, eps, H, T, s.h, s.x_mid,
+                      s.xn2, st));
   // gate/up, SwiGLU
   BSeg sg[1] = {wseg(w.wgu)};
   LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn2, H, sg, 1, T, H, nullptr, 0, &go));
   LLMT_HIP_TRY(mark(CAT_ROWS));
-  LLMT_HIP_TRY(gu_post(go.part, go.split, go.ss, go.ldp, I, T, s.gu, a16, st));
+  LLMT_HIP_TRY(gu_post(row_in(go), I, T, s.gu, a16, st));
   // down, residual, next norm
   BSeg sd[1] = {wseg(w.wd)};
   LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, a16, I, sd, 1, T, I, nullptr, 0, &go));
   LLMT_HIP_TRY(mark(CAT_ROWS));
-  LLMT_HIP_TRY(resid_norm(go.part, go.split, go.ss, go.ldp, s.x_mid, next_w, eps, H, T, x_out,
-                          xn_out, st));
+  LLMT_HIP_TRY(resid_norm(row_in(go), s.x_mid, next_w, eps, H, T, x_out, xn_out, st));
   return hipSuccess;
 }
 
@@ -288,10 +284,9 @@ hipError_t Ctx::head_bwd(int B) {
   BSeg sh_[1] = {hseg(ET, H, V)};
   LLMT_HIP_TRY(gemm(CAT_GEMM_HEAD, grad16, V, sh_, 1, T, V, nullptr, 0, &go));
   NormBwdArgs nb{};
-  nb.part = go.part; nb.split = go.split; nb.ss = go.ss; nb.ldp = go.ldp;
+  nb.in = row_in(go);
   nb.rinv_in = nullptr;
   nb.gscale = 1.0f / (kGradLogitScale * (float)n_valid);
-  nb.nlora = 0;
   nb.dh_out = dh;
   nb.x = x_final;
   nb.w = final_norm;
@@ -323,14 +318,13 @@ hipError_t Ctx::layer_bwd(int l, int B, int accumulate) {
   BSeg sd[1] = {wseg(w.wdT)};
   LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, sd, 1, T, H, nullptr, 0, &go));
   LLMT_HIP_TRY(mark(CAT_ROWS));
-  LLMT_HIP_TRY(swiglu_bwd(go.part, go.split, go.ss, go.ldp, rinv, s.gu, I, T, dgu16, rinv2, st));
+  LLMT_HIP_TRY(swiglu_bwd(row_in(go), rinv, s.gu, I, T, dgu16, rinv2, st));
   BSeg sg[1] = {wseg(w.wguT)};
   LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, dgu16, 2 * I, sg, 1, T, 2 * I, nullptr, 0, &go));
   nb = NormBwdArgs{};
-  nb.part = go.part; nb.split = go.split; nb.ss = go.ss; nb.ldp = go.ldp;
+  nb.in = row_in(go);
   nb.rinv_in = rinv2;
   nb.gscale = 1.0f;
-  nb.nlora = 0;
   nb.dh_out = dh;
   nb.x = s.x_mid;
   nb.w = w.ffn_norm;
@@ -345,11 +339,11 @@ hipError_t Ctx::layer_bwd(int l, int B, int accumulate) {
   LLMT_HIP_TRY(norm_bwd(nb, T, st));
   // O projection dX (+ dh_o through the B_o^T rows)
   BSeg so[2] = {wseg(w.woT), hseg(shadow_ptr(l, sh_bt_o), kRank, H)};
-  const LoraUp ubo[1] = {{lora_ptr(lora_p, l, 3, 0), 0, Q, Q, 0}};
-  LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, so, 2, T, H, nullptr, 0, &go, 1, ubo));
+  const LoraTerm tbo[1] = {{shadow_ptr(l, sh_a_o), 0, Q, 0, Q, 0}};
+  LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, so, 2, T, H, nullptr, 0, &go));
   LLMT_HIP_TRY(mark(CAT_ROWS));
-  LLMT_HIP_TRY(o_dx_post(go.part, go.split, go.ss, go.ldp, rinv, s.o16, nq, S, T, dh, dO, delta,
-                         damax, st));
+  LLMT_HIP_TRY(o_dx_post(row_in(go, Q, kRank, 1, tbo), rinv, s.o16, nq, S, T, dh, dO, delta, damax,
+                         st));
   // attention backward
   AttnArgs aa = attn_args(s);
   LLMT_HIP_TRY(mark(CAT_ATTN));
@@ -366,15 +360,15 @@ hipError_t Ctx::layer_bwd(int l, int B, int accumulate) {
   LLMT_HIP_TRY(qk_bwd(qb, T, st));
   // Q/K/V dX (+ dh_q, dh_k, dh_v through the B^T rows), attention norm bwd
   BSeg sq[2] = {wseg(w.wqkvT), hseg(shadow_ptr(l, sh_bt_qkv), 3 * kRank, NT)};
-  const LoraUp ubq[3] = {{lora_ptr(lora_p, l, 0, 0), 0, H, H, 0},
-                         {lora_ptr(lora_p, l, 1, 0), 0, H, H + kRank, 0},
-                         {lora_ptr(lora_p, l, 2, 0), 0, H, H + 2 * kRank, 0}};
-  LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, NT, sq, 2, T, NT, nullptr, 0, &go, 3, ubq));
+  const _Float16* a_qkv = shadow_ptr(l, sh_a_qkv);
+  const LoraTerm tbq[3] = {{a_qkv, 0, H, 0, H, 0},
+                           {a_qkv, kRank, H, 0, H, kRank},
+                           {a_qkv, 2 * kRank, H, 0, H, 2 * kRank}};
+  LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, NT, sq, 2, T, NT, nullptr, 0, &go));
   nb = NormBwdArgs{};
-  nb.part = go.part; nb.split = go.split; nb.ss = go.ss; nb.ldp = go.ldp;
+  nb.in = row_in(go, H, 3 * kRank, 3, tbq);
   nb.rinv_in = rinv;
   nb.gscale = 1.0f;
-  nb.nlora = 3;
   nb.dh_out = dh;
   nb.dh_col = 0;
   nb.x = s.x_in;
@@ -707,6 +701,81 @@ int llmt_profile_gemms(llmt_ctx* ctx, const int* tokens, const int* targets, int
   if (launches) *launches = (int)gs.size();
   if (weight_bytes) *weight_bytes = wb;
   if (flops) *flops = fl;
+  return LLMT_OK;
+}
+
+int llmt_profile_gemm_shapes(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
+                             const llmt_hparams* hp, int step, int reps, int max_shapes,
+                             int* nshapes, int* shape_info, float* shape_us) {
+  set_error("");
+  Ctx* c = C_(ctx);
+  int rc = check_tokens(c, tokens, targets, batch);
+  if (rc) return rc;
+  TRY_ARG(nshapes && shape_info && shape_us && reps >= 1 && max_shapes >= 1,
+          "llmt_profile_gemm_shapes: outputs, reps");
+  if ((rc = set_hp(c, hp, step))) return rc;
+  if ((rc = stage_inputs(c, tokens, targets, batch))) return rc;
+  const bool was_graph = c->use_graph;
+  c->use_graph = false;
+  c->record_gemms = true;
+  c->recorded.clear();
+  rc = run_step(c, batch, 1, nullptr);
+  c->record_gemms = false;
+  c->use_graph = was_graph;
+  if (rc) return rc;
+  // group launches by (N, K, split), in first-seen order
+  std::vector<std::vector<int>> groups;
+  std::vector<std::array<int, 4>> keys;
+  for (size_t i = 0; i < c->recorded.size(); ++i) {
+    const GemmArgs& g = c->recorded[i];
+    const std::array<int, 4> k{g.N, g.K, g.split, g.seg[0].is_i8};
+    size_t j = 0;
+    while (j < keys.size() && keys[j] != k) ++j;
+    if (j == keys.size()) {
+      keys.push_back(k);
+      groups.emplace_back();
+    }
+    groups[j].push_back((int)i);
+  }
+  const int ns = (int)std::min<size_t>(groups.size(), (size_t)max_shapes);
+  hipEvent_t e0, e1;
+  TRY_HIP(hipEventCreate(&e0));
+  TRY_HIP(hipEventCreate(&e1));
+  for (int s = 0; s < ns; ++s) {
+    {
+      hipGraph_t gph = nullptr;
+      hipGraphExec_t ex = nullptr;
+      TRY_HIP(hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
+      hipError_t e = hipSuccess;
+      for (int i : groups[s])
+        if (e == hipSuccess) e = gemm_nt(c->recorded[i], c->st);
+      hipError_t e2 = hipStreamEndCapture(c->st, &gph);
+      TRY_HIP(e);
+      TRY_HIP(e2);
+      e = hipGraphInstantiate(&ex, gph, nullptr, nullptr, 0);
+      hipGraphDestroy(gph);
+      TRY_HIP(e);
+      TRY_HIP(hipGraphLaunch(ex, c->st));
+      TRY_HIP(hipEventRecord(e0, c->st));
+      for (int r = 0; r < reps; ++r) TRY_HIP(hipGraphLaunch(ex, c->st));
+      TRY_HIP(hipEventRecord(e1, c->st));
+      TRY_HIP(hipEventSynchronize(e1));
+      float ms = 0.f;
+      TRY_HIP(hipEventElapsedTime(&ms, e0, e1));
+      hipGraphExecDestroy(ex);
+      shape_us[s] = ms * 1e3f / (float)(reps * groups[s].size());
+    }
+    const GemmArgs& g = c->recorded[groups[s][0]];
+    int* inf = shape_info + 5 * s;
+    inf[0] = g.N;
+    inf[1] = g.K;
+    inf[2] = g.split;
+    inf[3] = (int)groups[s].size();
+    inf[4] = g.seg[0].is_i8;
+  }
+  hipEventDestroy(e0);
+  hipEventDestroy(e1);
+  *nshapes = ns;
   return LLMT_OK;
 }
 

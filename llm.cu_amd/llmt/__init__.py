@@ -73,6 +73,8 @@ _PROTOS = {
     "llmt_layer_backward": (i32, [vp, i32, vp, vp, i32]),
     "llmt_adamw": (i32, [vp, C.POINTER(HParams), i32]),
     "llmt_head_ce": (i32, [vp, vp, vp, i32, fp, vp, vp]),
+    "llmt_profile_gemm_shapes": (i32, [vp, vp, vp, i32, C.POINTER(HParams), i32, i32, i32,
+                                       C.POINTER(C.c_int), C.POINTER(C.c_int), fp]),
     "llmt_profile_gemms": (i32, [vp, vp, vp, i32, C.POINTER(HParams), i32, i32, fp,
                                  C.POINTER(C.c_int), C.POINTER(C.c_double),
                                  C.POINTER(C.c_double)]),
@@ -318,6 +320,18 @@ class Context:
                                        C.byref(hp), step, reps, C.byref(us), C.byref(n),
                                        C.byref(wb), C.byref(fl)))
         return us.value, n.value, wb.value, fl.value
+
+    def profile_gemm_shapes(self, tokens, targets, hp: HParams, step: int, reps: int = 5):
+        """Per GEMM shape of the step: dicts with N, K, split, launches, int8
+        and us (average launch duration)."""
+        mx = 32
+        ns = C.c_int()
+        info = (C.c_int * (5 * mx))()
+        us = (C.c_float * mx)()
+        check(lib().llmt_profile_gemm_shapes(self.h, ptr(tokens), ptr(targets), tokens.shape[0],
+                                             C.byref(hp), step, reps, mx, C.byref(ns), info, us))
+        keys = ("N", "K", "split", "launches", "int8")
+        return [dict(zip(keys, info[5 * s:5 * s + 5]), us=us[s]) for s in range(ns.value)]
 
     def profile_step(self, tokens, targets, hp: HParams, step: int):
         """Per-category kernel milliseconds of one eager step, plus the step's
