@@ -220,7 +220,8 @@ int llmt_attention_bwd(const void* q, const void* k, const void* v, const void* 
   Temps tmp(st);
   float* delta = tmp.get<float>((size_t)B * nq * S);
   float* damax = tmp.get<float>(T);
-  TRY_ARG(delta && damax, "llmt_attention_bwd: out of memory");
+  float* dkvp = tmp.get<float>((size_t)T * 2 * nq * kHeadDim);
+  TRY_ARG(delta && damax && dkvp, "llmt_attention_bwd: out of memory");
   const long long ldq = (long long)nq * kHeadDim, ldkv = (long long)nkv * kHeadDim;
   TRY_HIP(attn_delta(dout, ldq, (const _Float16*)o, ldq, nq, S, T, delta, damax, st));
   AttnArgs a{};
@@ -241,6 +242,7 @@ int llmt_attention_bwd(const void* q, const void* k, const void* v, const void* 
   a.damax = damax;
   a.dq = dq;
   a.ldgq = ldq;
+  a.dkvp = dkvp;
   a.dk = dk;
   a.dv = dv;
   a.ldgkv = ldkv;
@@ -268,13 +270,14 @@ int llmt_attention_block_bwd(const void* q_raw, const void* k_raw, const void* v
   float* delta = tmp.get<float>((size_t)B * nq * S);
   float* damax = tmp.get<float>(T);
   float* dqkv = tmp.get<float>((size_t)T * NT);
+  float* dkvp = tmp.get<float>((size_t)T * 2 * Q);
   float* dy = tmp.get<float>((size_t)T * NT);
   _Float16* g16 = tmp.get<_Float16>((size_t)T * NT);
   float* rinv = tmp.get<float>(T);
   float* cosT = tmp.get<float>((size_t)S * 64);
   float* sinT = tmp.get<float>((size_t)S * 64);
-  TRY_ARG(raw16 && qkv16 && qkraw && o16 && lse && dO && delta && damax && dqkv && dy && g16 &&
-              rinv && cosT && sinT,
+  TRY_ARG(raw16 && qkv16 && qkraw && o16 && lse && dO && delta && damax && dqkv && dkvp && dy &&
+              g16 && rinv && cosT && sinT,
           "llmt_attention_block_bwd: out of memory");
   // RoPE tables (src/kernels/rope.cu:15-18), angles in double rounded to fp32.
   std::vector<float> hc((size_t)S * 64), hs((size_t)S * 64);
@@ -316,13 +319,14 @@ int llmt_attention_block_bwd(const void* q_raw, const void* k_raw, const void* v
   a.damax = damax;
   a.dq = dqkv;
   a.ldgq = NT;
-  a.dk = dqkv + Q;
-  a.dv = dqkv + Q + KV;
-  a.ldgkv = NT;
+  a.dkvp = dkvp;
+  a.dk = nullptr;  // qk_bwd sums the per-query-head shares
+  a.dv = nullptr;
   TRY_HIP(attn_bwd(a, B, st));
   QkBwdArgs qb{};
   qb.dqkv = dqkv;
   qb.ld_dqkv = NT;
+  qb.dkvp = dkvp;
   qb.qkraw = qkraw;
   qb.qn = q_norm;
   qb.kn = k_norm;

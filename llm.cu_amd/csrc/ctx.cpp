@@ -191,6 +191,7 @@ int Ctx::init() {
   TRY_PTR(delta = alloc_n<float>((size_t)maxB * nq * S));
   TRY_PTR(damax = alloc_n<float>(T));
   TRY_PTR(dqkv32 = alloc_n<float>(T * NT));
+  TRY_PTR(dkvp = alloc_n<float>((size_t)T * 2 * Q));
   TRY_PTR(dy32 = alloc_n<float>(T * NT));
   TRY_PTR(dh = alloc_n<float>(T * 64));
 

@@ -118,6 +118,7 @@ struct Ctx {
   _Float16* dgu16 = nullptr;
   float *dO = nullptr, *delta = nullptr, *damax = nullptr;
   float *dqkv32 = nullptr, *dy32 = nullptr, *dh = nullptr;
+  float* dkvp = nullptr;  // [T, 2 Q]: per-query-head dK | dV shares
 
   // graph + profiling
   bool use_graph = false;

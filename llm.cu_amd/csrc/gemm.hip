@@ -1,6 +1,7 @@
 // gemm.hip — skinny "NT" GEMM on fp16 MFMA (v_mfma_f32_16x16x32_f16) for
 // gfx950, plus the layout kernels (fragment packing, transposes,
-// conversions, the bit-exact int8 quantizer) and the split-K reduction.
+// conversions, the bit-exact int8 quantizer) and the split-K reduction used
+// by the standalone GEMM entry points.
 //
 // Every frozen-weight product of the training step is expressed as
 // C = A * B^T with both operands contiguous along the reduction dimension:
@@ -15,15 +16,19 @@
 // HBM-bound on the weight stream.  B operands are stored fragment-packed
 // (packed_index in common.h): each wave streams its NF*16 weight rows as
 // contiguous 1 KB loads straight into MFMA operand registers through a
-// four-slot register ring (three k-steps of 32 ahead).  The A tile of all
-// MF*16 rows is staged through LDS in 64-wide K chunks (double-buffered, in
-// MFMA fragment order so every ds_read_b128 is a contiguous conflict-free
-// 1 KB) and shared by the NW waves; the next chunk's A loads are issued a
-// chunk of MFMA work before they are stored.  The small LDS footprint (32 KB)
-// lets two 8-wave workgroups share a CU, which measured faster than larger
-// chunks, wider tiles or deeper B prefetch on MI355X.  K is split across workgroups (split-K) so a
-// launch fills the 256 CUs; split partials are fp32 and are reduced in a
-// fixed order by reduce_splits.
+// register ring (RING - 1 k-steps of 32 ahead).  The A tile of all MF*16 rows
+// is staged through LDS in 64-wide K chunks (double-buffered, in MFMA
+// fragment order so every ds_read_b128 is a contiguous conflict-free 1 KB)
+// and shared by the NW waves; the next chunk's A loads are issued a chunk of
+// MFMA work before they are stored.  K is split across workgroups (split-K)
+// so a launch fills the CUs; the fp32 split partials are summed in split
+// order by the consuming row epilogue (deterministic), and the standalone
+// GEMM entry points reduce them with reduce_lora.  Measured on MI355X
+// (per-workgroup timestamps): the in-loop weight stream runs at 2.6-3.8 TB/s,
+// and each launch pays ~5 us of fixed latency (launch, the first A/B round
+// trip, the partial stores), which four-wave 128-column tiles at about 3/4 of
+// a workgroup per CU balance best against the partial traffic; deeper B
+// rings and A prefetch distances measured no faster.
 #include <stdlib.h>
 #include <type_traits>
 
@@ -219,9 +224,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
     }(std::make_integer_sequence<int, RING - 1>{});
     store_a(IC<0>{}, IC<0>{});
     __syncthreads();
+    // The unrolled body stops at the last chunk (uniform exit), so a deep
+    // ring costs no padded MFMA work on short K ranges.
     for (int c = 0; c < nch; c += UC) {
       [&]<int... U>(std::integer_sequence<int, U...>) LLMT_INLINE {
-        (chunk(c, IC<U>{}), ...);
+        ((c + U < nch ? (chunk(c, IC<U>{}), true) : false) && ...);
       }(std::make_integer_sequence<int, UC>{});
     }
   }
@@ -264,8 +271,8 @@ struct GemmCfg {
   int nw, chs, ring, adist;
 };
 constexpr GemmCfg kCfgs[] = {
-    {8, 2, 4, 1}, {8, 2, 4, 2}, {8, 2, 8, 2}, {8, 4, 8, 1}, {8, 4, 8, 2},
-    {4, 2, 4, 1}, {4, 2, 4, 2}, {4, 2, 8, 2}, {4, 4, 8, 1}, {4, 4, 8, 2},
+    {8, 2, 4, 1}, {8, 2, 4, 2}, {8, 2, 8, 2}, {8, 2, 6, 1}, {4, 2, 6, 2},
+    {4, 2, 4, 1}, {4, 2, 4, 2}, {4, 2, 8, 2}, {4, 2, 8, 1}, {4, 2, 6, 1},
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 constexpr int kNF = 2;

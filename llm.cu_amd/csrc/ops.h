@@ -149,6 +149,8 @@ struct NormBwdArgs {
 struct QkBwdArgs {
   const float* dqkv;  // attention grads [T, ld] (dq | dk | dv)
   int ld_dqkv;
+  const float* dkvp;  // if set: dk, dv are the group sums of these per-query-head shares
+                      // [T, 2 nq 128] (attn_bwd's dkvp) instead of dqkv's columns
   const float* qkraw;
   const float* qn;
   const float* kn;
@@ -211,8 +213,9 @@ struct AttnArgs {
   const float* damax;   // [T] max |dO| per row
   float* dq;            // fp32 [T, ldgq]
   long long ldgq;
-  float* dk;
-  float* dv;            // fp32 [T, ldgkv]
+  float* dkvp;          // [T, 2 nq 128]: each query head's share of dK | dV
+  float* dk;            // optional: dK, dV summed over each GQA group,
+  float* dv;            //   fp32 [T, ldgkv] (NULL: the consumer sums dkvp)
   long long ldgkv;
 };
 hipError_t attn_fwd(const AttnArgs& a, int B, hipStream_t st);

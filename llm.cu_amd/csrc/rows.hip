@@ -2,8 +2,12 @@
 // epilogues that consume split-K GEMM partials and fuse everything that lives
 // on one token row (LoRA up-projection, QK-RMSNorm + RoPE, residual adds,
 // RMSNorm forward/backward, SwiGLU forward/backward, the attention-backward
-// row statistics).  One workgroup of 256 threads (4 waves) per token row
-// unless noted; rows are staged in LDS so each input is read from HBM once.
+// row statistics).  One workgroup of 512 threads (8 waves) per token row
+// unless noted.  At the headline shape these kernels are latency-bound (128
+// rows, a few hundred KB each), so a thread owns 4-column pieces of the row
+// in registers and issues every independent load (split-K partials, h
+// columns, side inputs) before the first use: one memory round trip, then
+// LDS-only block reductions.
 //
 // The reference runs these as separate fp32 kernels on the default stream
 // (src/kernels/rmsnorm.cu, rope.cu, activation.cu, elementwise.cu, embed.cu,
@@ -22,97 +26,148 @@ namespace llmt {
 
 namespace {
 
-constexpr int RT = 256;  // threads per row workgroup
+constexpr int RT = 512;  // threads per row workgroup
 constexpr int RW = RT / 64;
 constexpr int HD = 128;  // head_dim
 constexpr int R = 16;    // LoRA rank
-
-// Split-K partial sums, in split order (deterministic), with RB8 splits'
-// loads in flight per thread: row epilogues are latency-bound, so every
-// load of a batch is issued before the first add.
-constexpr int RB8 = 8;
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 __device__ __forceinline__ float4 add4(float4 a, float4 b) {
   return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
+__device__ __forceinline__ float4 mul4(float4 a, float s) {
+  return make_float4(a.x * s, a.y * s, a.z * s, a.w * s);
+}
+__device__ __forceinline__ void st_h4(_Float16* p, float4 v) {
+  half4 h;
+  h[0] = (_Float16)v.x;
+  h[1] = (_Float16)v.y;
+  h[2] = (_Float16)v.z;
+  h[3] = (_Float16)v.w;
+  *reinterpret_cast<half4*>(p) = h;
+}
+__device__ __forceinline__ float amax4(float4 v) {
+  return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
 
+// Split-K partial sums in split order (deterministic), every load of a
+// batch issued before the first add.
 __device__ __forceinline__ float4 sum_splits4(const float* p, int split, long long ss) {
+  constexpr int SB = 16;
   float4 v = ld4(p);
-  for (int k = 1; k < split; k += 2 * RB8) {
-    float4 x[2 * RB8];
+  for (int k = 1; k < split; k += SB) {
+    float4 x[SB];
 #pragma unroll
-    for (int i = 0; i < 2 * RB8; ++i) x[i] = ld4(p + (long long)min(k + i, split - 1) * ss);
+    for (int i = 0; i < SB; ++i) x[i] = ld4(p + (long long)min(k + i, split - 1) * ss);
 #pragma unroll
-    for (int i = 0; i < 2 * RB8; ++i)
-      if (k + i < split) v = add4(v, x[i]);
+    for (int i = 0; i < SB; ++i) v = k + i < split ? add4(v, x[i]) : v;
   }
   return v;
 }
 
-__device__ __forceinline__ void sum_splits8(const float* p, int split, long long ss, float4& a,
-                                            float4& b) {
-  a = ld4(p);
-  b = ld4(p + 4);
-  for (int k = 1; k < split; k += RB8) {
-    float4 x[RB8], y[RB8];
+// This thread's pieces of row t of a split-K GEMM output: piece p is columns
+// 4 (tid + p RT) .. + 3 (live when < n; dead pieces hold column 0's values),
+// plus (HH) this thread's four raw h columns when tid < nh / 4 (others hold
+// group 0's).  One loop for both, with up to 24 loads in flight per batch
+// and branch-free in-order adds, so a row costs one memory round trip per
+// batch of splits.
+template <int P, bool HH>
+__device__ __forceinline__ void load_row(const RowIn& in, int t, int n, float4 (&v)[P], float4& h) {
+  const float* prow = in.part + (long long)t * in.ldp;
+  int off[P];
 #pragma unroll
-    for (int i = 0; i < RB8; ++i) {
-      const float* q = p + (long long)min(k + i, split - 1) * ss;
-      x[i] = ld4(q);
-      y[i] = ld4(q + 4);
+  for (int p = 0; p < P; ++p) {
+    const int c = 4 * ((int)threadIdx.x + p * RT);
+    off[p] = c < n ? c : 0;
+    v[p] = ld4(prow + off[p]);
+  }
+  const int hoff = in.hcol + 4 * ((int)threadIdx.x < in.nh / 4 ? (int)threadIdx.x : 0);
+  if (HH) h = ld4(prow + hoff);
+  constexpr int SB = 24 / (P + (HH ? 1 : 0));
+  for (int k = 1; k < in.split; k += SB) {
+    float4 x[SB][P], y[SB];
+#pragma unroll
+    for (int i = 0; i < SB; ++i) {
+      const float* q = prow + (long long)min(k + i, in.split - 1) * in.ss;
+#pragma unroll
+      for (int p = 0; p < P; ++p) x[i][p] = ld4(q + off[p]);
+      if (HH) y[i] = ld4(q + hoff);
     }
 #pragma unroll
-    for (int i = 0; i < RB8; ++i)
-      if (k + i < split) {
-        a = add4(a, x[i]);
-        b = add4(b, y[i]);
-      }
+    for (int i = 0; i < SB; ++i) {
+      const bool ok = k + i < in.split;
+#pragma unroll
+      for (int p = 0; p < P; ++p) v[p] = ok ? add4(v[p], x[i][p]) : v[p];
+      if (HH) h = ok ? add4(h, y[i]) : h;
+    }
   }
 }
 
-// Row t of a split-K GEMM output into LDS: ys[c] (c < n, n % 8 == 0) = the
-// split sum plus the LoRA up-projection terms covering c; hs[j] (j < in.nh)
-// = the raw h columns.  Thread -> 8-column pieces.  Ends with a barrier.
-__device__ void fetch_row(const RowIn& in, int t, int n, float* ys, float* hs) {
-  const float* prow = in.part + (long long)t * in.ldp;
-  const int tid = threadIdx.x;
-  if (tid < in.nh / 4) {
-    const float4 h = sum_splits4(prow + in.hcol + 4 * tid, in.split, in.ss);
-    hs[4 * tid] = h.x;
-    hs[4 * tid + 1] = h.y;
-    hs[4 * tid + 2] = h.z;
-    hs[4 * tid + 3] = h.w;
-  }
-  for (int pc = tid; pc < n / 8; pc += RT) {
-    float4 a, b;
-    sum_splits8(prow + 8 * pc, in.split, in.ss, a, b);
-    *reinterpret_cast<float4*>(ys + 8 * pc) = a;
-    *reinterpret_cast<float4*>(ys + 8 * pc + 4) = b;
-  }
-  __syncthreads();
-  if (in.nterm == 0) return;
-  for (int pc = tid; pc < n / 8; pc += RT) {
-    const int c = 8 * pc;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int q = 0; q < in.nterm; ++q) {
-      const LoraTerm& m = in.term[q];
-      if (c < m.c0 || c >= m.c0 + m.n) continue;
-      half8 wv[R];
+template <int P>
+__device__ __forceinline__ void load_partials(const RowIn& in, int t, int n, float4 (&v)[P]) {
+  float4 h;
+  load_row<P, false>(in, t, n, v, h);
+}
+
+__device__ __forceinline__ void store_h(const RowIn& in, float4 h, float* hs) {
+  if ((int)threadIdx.x < in.nh / 4) *reinterpret_cast<float4*>(hs + 4 * threadIdx.x) = h;
+}
+
+// LoRA up-projection of this thread's pieces, split into a load phase (no
+// dependence on h, issued with the partials) and an apply phase:
+//   v[p] += lscale * sum over the terms covering the piece (at most NTM, in
+//   term order) of sum_r hs[hidx + r] * shadow(row0 + r, c .. c + 3).
+template <int P, int NTM>
+struct LoraRegs {
+  half4 w[P][NTM][R];
+  int hidx[P][NTM];  // -1: unused slot
+};
+
+// NTM == 1: the piece is covered by at most one term (the forward q/k/v
+// column ranges); NTM == 3: term q goes to slot q.
+template <int P, int NTM>
+__device__ __forceinline__ void lora_load(const RowIn& in, int n, LoraRegs<P, NTM>& L) {
+  static_assert(NTM == 1 || NTM == 3, "one covering term, or one slot per term");
 #pragma unroll
-      for (int r = 0; r < R; ++r)
-        wv[r] = *reinterpret_cast<const half8*>(m.sh + packed_index(m.row0 + r, c, m.kp));
+  for (int p = 0; p < P; ++p) {
+    const int c = 4 * ((int)threadIdx.x + p * RT);
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const float h = hs[m.hidx + r];
+    for (int s = 0; s < NTM; ++s) L.hidx[p][s] = -1;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] += h * (float)wv[r][e];
+    for (int q = 0; q < 3; ++q) {
+      const int s = NTM == 1 ? 0 : q;
+      const bool use = q < in.nterm && c < n && c >= in.term[q].c0 && c < in.term[q].c0 + in.term[q].n;
+      if (use) {
+        const LoraTerm& m = in.term[q];
+        L.hidx[p][s] = m.hidx;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          L.w[p][s][r] = *reinterpret_cast<const half4*>(m.sh + packed_index(m.row0 + r, c, m.kp));
       }
     }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ys[c + e] += in.lscale * acc[e];
   }
-  __syncthreads();
+}
+
+template <int P, int NTM>
+__device__ __forceinline__ void lora_apply(const RowIn& in, const float* hs,
+                                           const LoraRegs<P, NTM>& L, float4 (&v)[P]) {
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int s = 0; s < NTM; ++s) {
+      if (L.hidx[p][s] < 0) continue;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float h = hs[L.hidx[p][s] + r];
+        acc.x += h * (float)L.w[p][s][r][0];
+        acc.y += h * (float)L.w[p][s][r][1];
+        acc.z += h * (float)L.w[p][s][r][2];
+        acc.w += h * (float)L.w[p][s][r][3];
+      }
+    }
+    v[p] = add4(v[p], mul4(acc, in.lscale));
+  }
 }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
@@ -172,20 +227,32 @@ __global__ __launch_bounds__(RT) void embed_norm_kernel(const int* __restrict__ 
 // (src/kernels/rmsnorm.cu:36-41 with 128-wide rows) and half-split RoPE
 // (src/kernels/rope.cu:7-27): lane l of a wave owns the rotation pair
 // (l, l + 64).  Writes q, k (normed, rotated) and v as fp16 [T, Q + 2 KV].
+template <int P>
 __global__ __launch_bounds__(RT) void qkv_post_kernel(const QkvPostArgs a) {
   extern __shared__ float ys[];  // [NT]
   __shared__ float hs[64];
   const int t = blockIdx.x;
   const int Q = a.nq * HD, KV = a.nkv * HD, NT = Q + 2 * KV;
-  fetch_row(a.in, t, NT, ys, hs);
-  if (threadIdx.x < a.in.nh) a.hbuf[(long long)t * 64 + threadIdx.x] = hs[threadIdx.x];
-  for (int c = threadIdx.x; c < NT; c += RT) {
-    const float y = ys[c];
+  float4 v[P], hv;
+  load_row<P, true>(a.in, t, NT, v, hv);
+  LoraRegs<P, 1> L;
+  lora_load<P, 1>(a.in, NT, L);
+  store_h(a.in, hv, hs);
+  if ((int)threadIdx.x < a.in.nh / 4)
+    *reinterpret_cast<float4*>(a.hbuf + (long long)t * 64 + 4 * threadIdx.x) = hv;
+  __syncthreads();
+  lora_apply<P, 1>(a.in, hs, L, v);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int c = 4 * ((int)threadIdx.x + p * RT);
+    if (c >= NT) continue;
+    *reinterpret_cast<float4*>(ys + c) = v[p];
     if (c < Q + KV)
-      a.qkraw[(long long)t * (Q + KV) + c] = y;
+      *reinterpret_cast<float4*>(a.qkraw + (long long)t * (Q + KV) + c) = v[p];
     else
-      a.qkv16[(long long)t * NT + c] = (_Float16)y;
+      st_h4(a.qkv16 + (long long)t * NT + c, v[p]);
   }
+  __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int pos = t % a.S;
   const float cs = a.cosT[pos * (HD / 2) + lane], sn = a.sinT[pos * (HD / 2) + lane];
@@ -203,28 +270,50 @@ __global__ __launch_bounds__(RT) void qkv_post_kernel(const QkvPostArgs a) {
 // After the O(+LoRA-A) GEMM (LoRA term added by its reduction):
 // x_mid = x_in + oW^T + s (o A^T) B^T (residual, src/kernels/elementwise.cu:
 // 4-15), stash h_o, then the FFN RMSNorm -> fp16.
+template <int P>
 __global__ __launch_bounds__(RT) void o_post_kernel(const RowIn in,
                                                     const float* __restrict__ x_in,
                                                     const float* __restrict__ w, float eps, int H,
                                                     float* __restrict__ hbuf,
                                                     float* __restrict__ x_mid,
                                                     _Float16* __restrict__ xn2) {
-  extern __shared__ float ys[];  // [H]
   __shared__ float red[2 * RW];
   __shared__ float hs[64];
   const int t = blockIdx.x;
-  fetch_row(in, t, H, ys, hs);
-  if (threadIdx.x < in.nh) hbuf[(long long)t * 64 + 3 * R + threadIdx.x] = hs[threadIdx.x];
+  float4 xi[P], wv[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int c = min(4 * ((int)threadIdx.x + p * RT), H - 4);
+    xi[p] = ld4(x_in + (long long)t * H + c);
+    wv[p] = ld4(w + c);
+  }
+  float4 v[P], hv;
+  load_row<P, true>(in, t, H, v, hv);
+  LoraRegs<P, 1> L;
+  lora_load<P, 1>(in, H, L);
+  store_h(in, hv, hs);
+  if ((int)threadIdx.x < in.nh / 4)
+    *reinterpret_cast<float4*>(hbuf + (long long)t * 64 + 3 * R + 4 * threadIdx.x) = hv;
+  __syncthreads();
+  lora_apply<P, 1>(in, hs, L, v);
   float ssq = 0.f;
-  for (int c = threadIdx.x; c < H; c += RT) {
-    const float xm = x_in[(long long)t * H + c] + ys[c];
-    x_mid[(long long)t * H + c] = xm;
-    ys[c] = xm;
-    ssq += xm * xm;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int c = 4 * ((int)threadIdx.x + p * RT);
+    if (c >= H) continue;
+    v[p] = add4(xi[p], v[p]);
+    *reinterpret_cast<float4*>(x_mid + (long long)t * H + c) = v[p];
+    ssq += v[p].x * v[p].x + v[p].y * v[p].y + v[p].z * v[p].z + v[p].w * v[p].w;
   }
   const float r = rsqrtf(block_sum2(ssq, 0.f, red).x / H + eps);
-  for (int c = threadIdx.x; c < H; c += RT)
-    xn2[(long long)t * H + c] = (_Float16)(ys[c] * r * w[c]);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int c = 4 * ((int)threadIdx.x + p * RT);
+    if (c >= H) continue;
+    st_h4(xn2 + (long long)t * H + c,
+          make_float4(v[p].x * r * wv[p].x, v[p].y * r * wv[p].y, v[p].z * r * wv[p].z,
+                      v[p].w * r * wv[p].w));
+  }
 }
 
 // After the fused gate/up GEMM: stash g, u (fp32) and a = silu(g) * u
@@ -252,25 +341,41 @@ __global__ __launch_bounds__(RT) void gu_post_kernel(const RowIn in, int I, long
 
 // After the down GEMM: x_out = x_mid + aW_down^T, then the next RMSNorm
 // (the next layer's attention norm, or the final norm) -> fp16.
+template <int P>
 __global__ __launch_bounds__(RT) void resid_norm_kernel(const RowIn in,
                                                         const float* __restrict__ x_res,
                                                         const float* __restrict__ w, float eps,
                                                         int H, float* __restrict__ x_out,
                                                         _Float16* __restrict__ xn) {
-  extern __shared__ float ys[];
   __shared__ float red[2 * RW];
-  __shared__ float hs[64];
   const int t = blockIdx.x;
-  fetch_row(in, t, H, ys, hs);
+  float4 xr[P], wv[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int c = min(4 * ((int)threadIdx.x + p * RT), H - 4);
+    xr[p] = ld4(x_res + (long long)t * H + c);
+    wv[p] = ld4(w + c);
+  }
+  float4 v[P];
+  load_partials<P>(in, t, H, v);
   float ssq = 0.f;
-  for (int c = threadIdx.x; c < H; c += RT) {
-    const float v = x_res[(long long)t * H + c] + ys[c];
-    x_out[(long long)t * H + c] = v;
-    ys[c] = v;
-    ssq += v * v;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int c = 4 * ((int)threadIdx.x + p * RT);
+    if (c >= H) continue;
+    v[p] = add4(xr[p], v[p]);
+    *reinterpret_cast<float4*>(x_out + (long long)t * H + c) = v[p];
+    ssq += v[p].x * v[p].x + v[p].y * v[p].y + v[p].z * v[p].z + v[p].w * v[p].w;
   }
   const float r = rsqrtf(block_sum2(ssq, 0.f, red).x / H + eps);
-  for (int c = threadIdx.x; c < H; c += RT) xn[(long long)t * H + c] = (_Float16)(ys[c] * r * w[c]);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int c = 4 * ((int)threadIdx.x + p * RT);
+    if (c >= H) continue;
+    st_h4(xn + (long long)t * H + c,
+          make_float4(v[p].x * r * wv[p].x, v[p].y * r * wv[p].y, v[p].z * r * wv[p].z,
+                      v[p].w * r * wv[p].w));
+  }
 }
 
 // QK-RMSNorm + RoPE forward from fp16 raw q/k (the standalone attention
@@ -316,80 +421,125 @@ __global__ __launch_bounds__(RT) void qk_norm_rope_kernel(const _Float16* __rest
 // stashed (unscaled) for the adapter gradients.
 // dres_out = dres_in + rmsnorm_bwd(d, x, w); also written to dmid_out when
 // given, and as the next fp16 gradient operand (g16, rinv_out).
+template <int P>
 __global__ __launch_bounds__(RT) void norm_bwd_kernel(const NormBwdArgs a) {
-  extern __shared__ float ds[];  // [H]
   __shared__ float red[2 * RW];
   __shared__ float hs[64];
   const int t = blockIdx.x;
   const int H = a.H;
-  fetch_row(a.in, t, H, ds, hs);
+  float4 xv[P], wv[P], dr[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int c = min(4 * ((int)threadIdx.x + p * RT), H - 4);
+    xv[p] = ld4(a.x + (long long)t * H + c);
+    wv[p] = ld4(a.w + c);
+    dr[p] = a.dres_in ? ld4(a.dres_in + (long long)t * H + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   const float rs = (a.rinv_in ? a.rinv_in[t] : 1.0f) * a.gscale;
-  if (threadIdx.x < a.in.nh)
-    a.dh_out[(long long)t * 64 + a.dh_col + threadIdx.x] = hs[threadIdx.x] * rs;
-  const float* x = a.x + (long long)t * H;
+  float4 v[P], hv;
+  load_row<P, true>(a.in, t, H, v, hv);
+  store_h(a.in, hv, hs);
+  if ((int)threadIdx.x < a.in.nh / 4)
+    *reinterpret_cast<float4*>(a.dh_out + (long long)t * 64 + a.dh_col + 4 * threadIdx.x) =
+        mul4(hv, rs);
+  if (a.in.nterm) {
+    LoraRegs<P, 3> L;
+    lora_load<P, 3>(a.in, H, L);
+    __syncthreads();
+    lora_apply<P, 3>(a.in, hs, L, v);
+  }
   float dot = 0.f, ssx = 0.f;
-  for (int c = threadIdx.x; c < H; c += RT) {
-    const float d = ds[c] * rs;
-    ds[c] = d;
-    const float xv = x[c];
-    dot += d * a.w[c] * xv;
-    ssx += xv * xv;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int c = 4 * ((int)threadIdx.x + p * RT);
+    if (c >= H) continue;
+    v[p] = mul4(v[p], rs);
+    dot += v[p].x * wv[p].x * xv[p].x + v[p].y * wv[p].y * xv[p].y + v[p].z * wv[p].z * xv[p].z +
+           v[p].w * wv[p].w * xv[p].w;
+    ssx += xv[p].x * xv[p].x + xv[p].y * xv[p].y + xv[p].z * xv[p].z + xv[p].w * xv[p].w;
   }
   const float2 s2 = block_sum2(dot, ssx, red);
   const float r = rsqrtf(s2.y / H + a.eps);
   const float coef = r * r / H * s2.x;
   float amax = 0.f;
-  for (int c = threadIdx.x; c < H; c += RT) {
-    const float dx = r * (ds[c] * a.w[c] - coef * x[c]);
-    const float v = (a.dres_in ? a.dres_in[(long long)t * H + c] : 0.f) + dx;
-    a.dres_out[(long long)t * H + c] = v;
-    if (a.dmid_out) a.dmid_out[(long long)t * H + c] = v;
-    ds[c] = v;
-    amax = fmaxf(amax, fabsf(v));
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int c = 4 * ((int)threadIdx.x + p * RT);
+    if (c >= H) continue;
+    const float4 d = v[p], x = xv[p], ww = wv[p];
+    v[p] = make_float4(dr[p].x + r * (d.x * ww.x - coef * x.x), dr[p].y + r * (d.y * ww.y - coef * x.y),
+                       dr[p].z + r * (d.z * ww.z - coef * x.z), dr[p].w + r * (d.w * ww.w - coef * x.w));
+    *reinterpret_cast<float4*>(a.dres_out + (long long)t * H + c) = v[p];
+    if (a.dmid_out) *reinterpret_cast<float4*>(a.dmid_out + (long long)t * H + c) = v[p];
+    amax = fmaxf(amax, amax4(v[p]));
   }
   amax = block_max<RW>(amax, red);
   const float sc = pow2_scale_for(amax);
   if (threadIdx.x == 0) a.rinv_out[t] = 1.0f / sc;
-  for (int c = threadIdx.x; c < H; c += RT) a.g16[(long long)t * H + c] = (_Float16)(ds[c] * sc);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int c = 4 * ((int)threadIdx.x + p * RT);
+    if (c < H) st_h4(a.g16 + (long long)t * H + c, mul4(v[p], sc));
+  }
 }
 
 // dX of the down projection -> SwiGLU backward (src/kernels/activation.cu:
 // 26-43 with d_up = dy * silu(g), i.e. without the reference's aliasing of
 // d_gate and d_swiglu at src/kernels/lora_backward.cu:287) -> [dg | du] fp16.
+template <int P>
 __global__ __launch_bounds__(RT) void swiglu_bwd_kernel(const RowIn in,
                                                         const float* __restrict__ rinv_in,
                                                         const float* __restrict__ gu, int I,
                                                         _Float16* __restrict__ dgu16,
                                                         float* __restrict__ rinv_out) {
-  extern __shared__ float ds[];  // [2 I]
   __shared__ float red[2 * RW];
-  __shared__ float hs[64];
   const int t = blockIdx.x;
-  fetch_row(in, t, I, ds, hs);
-  const float rs = rinv_in[t];
   const float* gr = gu + (long long)t * 2 * I;
+  float4 g4[P], u4[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int c = min(4 * ((int)threadIdx.x + p * RT), I - 4);
+    g4[p] = ld4(gr + c);
+    u4[p] = ld4(gr + I + c);
+  }
+  const float rs = rinv_in[t];
+  float4 v[P];
+  load_partials<P>(in, t, I, v);
+  float4 dg[P], du[P];
   float amax = 0.f;
-  for (int c = threadIdx.x; c < I; c += RT) {
-    const float da = ds[c] * rs;
-    const float g = gr[c], u = gr[I + c];
-    const float sg = 1.0f / (1.0f + __expf(-g));
-    const float dg = da * u * (sg * (1.0f + g * (1.0f - sg)));
-    const float du = da * (g * sg);
-    ds[c] = dg;
-    ds[I + c] = du;
-    amax = fmaxf(amax, fmaxf(fabsf(dg), fabsf(du)));
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const float da[4] = {v[p].x * rs, v[p].y * rs, v[p].z * rs, v[p].w * rs};
+    const float g[4] = {g4[p].x, g4[p].y, g4[p].z, g4[p].w};
+    const float u[4] = {u4[p].x, u4[p].y, u4[p].z, u4[p].w};
+    float o1[4], o2[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float sg = 1.0f / (1.0f + __expf(-g[e]));
+      o1[e] = da[e] * u[e] * (sg * (1.0f + g[e] * (1.0f - sg)));
+      o2[e] = da[e] * (g[e] * sg);
+    }
+    dg[p] = make_float4(o1[0], o1[1], o1[2], o1[3]);
+    du[p] = make_float4(o2[0], o2[1], o2[2], o2[3]);
+    if (4 * ((int)threadIdx.x + p * RT) < I) amax = fmaxf(amax, fmaxf(amax4(dg[p]), amax4(du[p])));
   }
   amax = block_max<RW>(amax, red);
   const float sc = pow2_scale_for(amax);
   if (threadIdx.x == 0) rinv_out[t] = 1.0f / sc;
-  for (int c = threadIdx.x; c < 2 * I; c += RT)
-    dgu16[(long long)t * 2 * I + c] = (_Float16)(ds[c] * sc);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int c = 4 * ((int)threadIdx.x + p * RT);
+    if (c >= I) continue;
+    st_h4(dgu16 + (long long)t * 2 * I + c, mul4(dg[p], sc));
+    st_h4(dgu16 + (long long)t * 2 * I + I + c, mul4(du[p], sc));
+  }
 }
 
 // dX of the O projection (+ dh_o in the LoRA-B^T columns; the reduction
 // already added s (dh_o A_o)): d_o = row * rinv; writes d_o fp32 (attention
 // dO), dh_o, the row's max |d_o| and the flash-backward row statistic
 // delta[b, h, s] = sum_d dO * O.
+template <int P>
 __global__ __launch_bounds__(RT) void o_dx_post_kernel(const RowIn in,
                                                        const float* __restrict__ rinv_in,
                                                        const _Float16* __restrict__ o16, int nq,
@@ -397,32 +547,47 @@ __global__ __launch_bounds__(RT) void o_dx_post_kernel(const RowIn in,
                                                        float* __restrict__ dO,
                                                        float* __restrict__ delta,
                                                        float* __restrict__ damax) {
-  extern __shared__ float ds[];  // [Q]
   __shared__ float red[2 * RW];
   __shared__ float hs[64];
   const int t = blockIdx.x;
   const int Q = nq * HD;
-  fetch_row(in, t, Q, ds, hs);
+  half4 ov[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int c = min(4 * ((int)threadIdx.x + p * RT), Q - 4);
+    ov[p] = *reinterpret_cast<const half4*>(o16 + (long long)t * Q + c);
+  }
   const float rs = rinv_in[t];
-  if (threadIdx.x < in.nh) dh_out[(long long)t * 64 + 3 * R + threadIdx.x] = hs[threadIdx.x] * rs;
-  float amax = 0.f;
-  for (int c = threadIdx.x; c < Q; c += RT) {
-    const float d = ds[c] * rs;
-    dO[(long long)t * Q + c] = d;
-    ds[c] = d;
-    amax = fmaxf(amax, fabsf(d));
-  }
-  amax = block_max<RW>(amax, red);  // (also orders the ds[] writes)
-  if (threadIdx.x == 0) damax[t] = amax;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float4 v[P], hv;
+  load_row<P, true>(in, t, Q, v, hv);
+  LoraRegs<P, 1> L;
+  lora_load<P, 1>(in, Q, L);
+  store_h(in, hv, hs);
+  if ((int)threadIdx.x < in.nh / 4)
+    *reinterpret_cast<float4*>(dh_out + (long long)t * 64 + 3 * R + 4 * threadIdx.x) = mul4(hv, rs);
+  __syncthreads();
+  lora_apply<P, 1>(in, hs, L, v);
   const int b = t / S, s = t - b * S;
-  const _Float16* o = o16 + (long long)t * Q;
-  for (int h = wave; h < nq; h += RW) {
-    const int base = h * HD;
-    const float v = wave_sum(ds[base + lane] * (float)o[base + lane] +
-                             ds[base + 64 + lane] * (float)o[base + 64 + lane]);
-    if (lane == 0) delta[((long long)b * nq + h) * S + s] = v;
+  float amax = 0.f;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int c = 4 * ((int)threadIdx.x + p * RT);
+    const bool live = c < Q;
+    const float4 d = mul4(v[p], rs);
+    if (live) {
+      *reinterpret_cast<float4*>(dO + (long long)t * Q + c) = d;
+      amax = fmaxf(amax, amax4(d));
+    }
+    // delta = sum over a head's 128 columns = 32 consecutive threads
+    float part = live ? d.x * (float)ov[p][0] + d.y * (float)ov[p][1] + d.z * (float)ov[p][2] +
+                            d.w * (float)ov[p][3]
+                      : 0.f;
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) part += __shfl_xor(part, o, 64);
+    if (live && (threadIdx.x & 31) == 0) delta[((long long)b * nq + c / HD) * S + s] = part;
   }
+  amax = block_max<RW>(amax, red);
+  if (threadIdx.x == 0) damax[t] = amax;
 }
 
 // Attention gradients (w.r.t. the normed, rotated q/k and v) -> RoPE
@@ -434,13 +599,25 @@ __global__ __launch_bounds__(RT) void qk_bwd_kernel(const QkBwdArgs a) {
   __shared__ float red[2 * RW];
   const int t = blockIdx.x;
   const int Q = a.nq * HD, KV = a.nkv * HD, NT = Q + 2 * KV;
+  const int group = a.nq / a.nkv;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int pos = t % a.S;
   const float cs = a.cosT[pos * (HD / 2) + lane], sn = a.sinT[pos * (HD / 2) + lane];
   const float* g = a.dqkv + (long long)t * a.ld_dqkv;
+  const float* sh = a.dkvp ? a.dkvp + (long long)t * 2 * Q : nullptr;
+  // gradient at column c of [dq | dk | dv] (the K/V ones summed over the
+  // query heads of their group, in order, when given as shares)
+  auto grad = [&](int c) -> float {
+    if (!sh || c < Q) return g[c];
+    const int kv = c < Q + KV ? 0 : 1;
+    const int cc = c - Q - kv * KV, j = cc / HD, d = cc - j * HD;
+    float s = 0.f;
+    for (int gi = 0; gi < group; ++gi) s += sh[(kv * a.nq + j * group + gi) * HD + d];
+    return s;
+  };
   for (int hh = wave; hh < a.nq + a.nkv; hh += RW) {
     const int base = hh * HD;
-    const float d0 = g[base + lane], d1 = g[base + 64 + lane];
+    const float d0 = grad(base + lane), d1 = grad(base + 64 + lane);
     const float n0 = d0 * cs + d1 * sn, n1 = d1 * cs - d0 * sn;
     const float* w = hh < a.nq ? a.qn : a.kn;
     const float w0 = w[lane], w1 = w[lane + 64];
@@ -452,7 +629,7 @@ __global__ __launch_bounds__(RT) void qk_bwd_kernel(const QkBwdArgs a) {
     ds[base + lane] = r * (n0 * w0 - coef * x0);
     ds[base + 64 + lane] = r * (n1 * w1 - coef * x1);
   }
-  for (int c = Q + KV + threadIdx.x; c < NT; c += RT) ds[c] = g[c];
+  for (int c = Q + KV + threadIdx.x; c < NT; c += RT) ds[c] = grad(c);
   __syncthreads();
   float amax = 0.f;
   for (int c = threadIdx.x; c < NT; c += RT) {
@@ -530,10 +707,10 @@ inline unsigned grid_elems(long long n) {
 
 static bool row_in_ok(const RowIn& in, int n, const char* who) {
   bool ok = in.nh % 4 == 0 && in.nh >= 0 && in.nh <= 64 && in.nterm >= 0 && in.nterm <= 3 &&
-            n % 8 == 0 && in.ldp % 4 == 0 && in.split >= 1 && (in.split == 1 || in.ss % 4 == 0) &&
+            n % 4 == 0 && in.ldp % 4 == 0 && in.split >= 1 && (in.split == 1 || in.ss % 4 == 0) &&
             in.hcol % 4 == 0;
   for (int q = 0; q < in.nterm && ok; ++q)
-    ok = in.term[q].c0 % 8 == 0 && in.term[q].n % 8 == 0 && in.term[q].hidx + R <= in.nh;
+    ok = in.term[q].c0 % 4 == 0 && in.term[q].n % 4 == 0 && in.term[q].hidx + R <= in.nh;
   if (!ok) set_error("%s: unsupported row-input layout (n=%d nh=%d nterm=%d)", who, n, in.nh, in.nterm);
   return ok;
 }
@@ -578,7 +755,16 @@ hipError_t embed_norm(const int* tok, const _Float16* E, int V, int H, const flo
 hipError_t qkv_post(const QkvPostArgs& a, int T, hipStream_t st) {
   const int NT = (a.nq + 2 * a.nkv) * HD;
   if (!row_in_ok(a.in, NT, "qkv_post")) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(qkv_post_kernel, dim3(T), dim3(RT), NT * sizeof(float), st, a);
+  const int P = (NT + 4 * RT - 1) / (4 * RT);
+  switch (P) {
+    case 1: hipLaunchKernelGGL(qkv_post_kernel<1>, dim3(T), dim3(RT), NT * sizeof(float), st, a); break;
+    case 2: hipLaunchKernelGGL(qkv_post_kernel<2>, dim3(T), dim3(RT), NT * sizeof(float), st, a); break;
+    case 3: hipLaunchKernelGGL(qkv_post_kernel<3>, dim3(T), dim3(RT), NT * sizeof(float), st, a); break;
+    case 4: hipLaunchKernelGGL(qkv_post_kernel<4>, dim3(T), dim3(RT), NT * sizeof(float), st, a); break;
+    default:
+      set_error("qkv_post: row width %d above %d", NT, 16 * RT);
+      return hipErrorInvalidValue;
+  }
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
@@ -587,8 +773,16 @@ hipError_t qkv_post(const QkvPostArgs& a, int T, hipStream_t st) {
 hipError_t o_post(const RowIn& in, const float* x_in, const float* w, float eps, int H, int T,
                   float* hbuf, float* x_mid, _Float16* xn2, hipStream_t st) {
   if (!row_in_ok(in, H, "o_post")) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(o_post_kernel, dim3(T), dim3(RT), H * sizeof(float), st, in, x_in, w, eps, H,
-                     hbuf, x_mid, xn2);
+  const int P = (H + 4 * RT - 1) / (4 * RT);
+  switch (P) {
+    case 1: hipLaunchKernelGGL(o_post_kernel<1>, dim3(T), dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2); break;
+    case 2: hipLaunchKernelGGL(o_post_kernel<2>, dim3(T), dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2); break;
+    case 3: hipLaunchKernelGGL(o_post_kernel<3>, dim3(T), dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2); break;
+    case 4: hipLaunchKernelGGL(o_post_kernel<4>, dim3(T), dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2); break;
+    default:
+      set_error("o_post: row width %d above %d", H, 16 * RT);
+      return hipErrorInvalidValue;
+  }
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
@@ -604,8 +798,16 @@ hipError_t gu_post(const RowIn& in, int I, int T, float* gu, _Float16* a16, hipS
 hipError_t resid_norm(const RowIn& in, const float* x_res, const float* w, float eps, int H, int T,
                       float* x_out, _Float16* xn, hipStream_t st) {
   if (!row_in_ok(in, H, "resid_norm")) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(resid_norm_kernel, dim3(T), dim3(RT), H * sizeof(float), st, in, x_res, w, eps,
-                     H, x_out, xn);
+  const int P = (H + 4 * RT - 1) / (4 * RT);
+  switch (P) {
+    case 1: hipLaunchKernelGGL(resid_norm_kernel<1>, dim3(T), dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn); break;
+    case 2: hipLaunchKernelGGL(resid_norm_kernel<2>, dim3(T), dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn); break;
+    case 3: hipLaunchKernelGGL(resid_norm_kernel<3>, dim3(T), dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn); break;
+    case 4: hipLaunchKernelGGL(resid_norm_kernel<4>, dim3(T), dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn); break;
+    default:
+      set_error("resid_norm: row width %d above %d", H, 16 * RT);
+      return hipErrorInvalidValue;
+  }
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
@@ -620,8 +822,17 @@ hipError_t qk_norm_rope(const _Float16* raw, const float* qn, const float* kn, c
 }
 
 hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st) {
-  if (!row_in_ok(a.in, a.H, "norm_bwd")) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(norm_bwd_kernel, dim3(T), dim3(RT), a.H * sizeof(float), st, a);
+  if (!row_in_ok(a.in, a.H, "norm_bwd") || a.dh_col % 4) return hipErrorInvalidValue;
+  const int P = (a.H + 4 * RT - 1) / (4 * RT);
+  switch (P) {
+    case 1: hipLaunchKernelGGL(norm_bwd_kernel<1>, dim3(T), dim3(RT), 0, st, a); break;
+    case 2: hipLaunchKernelGGL(norm_bwd_kernel<2>, dim3(T), dim3(RT), 0, st, a); break;
+    case 3: hipLaunchKernelGGL(norm_bwd_kernel<3>, dim3(T), dim3(RT), 0, st, a); break;
+    case 4: hipLaunchKernelGGL(norm_bwd_kernel<4>, dim3(T), dim3(RT), 0, st, a); break;
+    default:
+      set_error("norm_bwd: row width %d above %d", a.H, 16 * RT);
+      return hipErrorInvalidValue;
+  }
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
@@ -629,17 +840,34 @@ hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st) {
 hipError_t swiglu_bwd(const RowIn& in, const float* rinv_in, const float* gu, int I, int T,
                       _Float16* dgu16, float* rinv_out, hipStream_t st) {
   if (!row_in_ok(in, I, "swiglu_bwd")) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(swiglu_bwd_kernel, dim3(T), dim3(RT), 2 * I * sizeof(float), st, in, rinv_in,
-                     gu, I, dgu16, rinv_out);
+  const int P = (I + 4 * RT - 1) / (4 * RT);
+  switch (P) {
+    case 1: hipLaunchKernelGGL(swiglu_bwd_kernel<1>, dim3(T), dim3(RT), 0, st, in, rinv_in, gu, I, dgu16, rinv_out); break;
+    case 2: hipLaunchKernelGGL(swiglu_bwd_kernel<2>, dim3(T), dim3(RT), 0, st, in, rinv_in, gu, I, dgu16, rinv_out); break;
+    case 3: hipLaunchKernelGGL(swiglu_bwd_kernel<3>, dim3(T), dim3(RT), 0, st, in, rinv_in, gu, I, dgu16, rinv_out); break;
+    case 4: hipLaunchKernelGGL(swiglu_bwd_kernel<4>, dim3(T), dim3(RT), 0, st, in, rinv_in, gu, I, dgu16, rinv_out); break;
+    default:
+      set_error("swiglu_bwd: row width %d above %d", I, 16 * RT);
+      return hipErrorInvalidValue;
+  }
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
 
 hipError_t o_dx_post(const RowIn& in, const float* rinv_in, const _Float16* o16, int nq, int S,
                      int T, float* dh_out, float* dO, float* delta, float* damax, hipStream_t st) {
-  if (!row_in_ok(in, nq * HD, "o_dx_post")) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(o_dx_post_kernel, dim3(T), dim3(RT), nq * HD * sizeof(float), st, in, rinv_in,
-                     o16, nq, S, dh_out, dO, delta, damax);
+  const int Q = nq * HD;
+  if (!row_in_ok(in, Q, "o_dx_post")) return hipErrorInvalidValue;
+  const int P = (Q + 4 * RT - 1) / (4 * RT);
+  switch (P) {
+    case 1: hipLaunchKernelGGL(o_dx_post_kernel<1>, dim3(T), dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO, delta, damax); break;
+    case 2: hipLaunchKernelGGL(o_dx_post_kernel<2>, dim3(T), dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO, delta, damax); break;
+    case 3: hipLaunchKernelGGL(o_dx_post_kernel<3>, dim3(T), dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO, delta, damax); break;
+    case 4: hipLaunchKernelGGL(o_dx_post_kernel<4>, dim3(T), dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO, delta, damax); break;
+    default:
+      set_error("o_dx_post: row width %d above %d", Q, 16 * RT);
+      return hipErrorInvalidValue;
+  }
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }

@@ -264,8 +264,9 @@ AttnArgs Ctx::attn_args(const Stash& s) const {
   a.damax = damax;
   a.dq = dqkv32;
   a.ldgq = NT;
-  a.dk = dqkv32 + Q;
-  a.dv = dqkv32 + Q + KV;
+  a.dkvp = dkvp;
+  a.dk = nullptr;  // qk_bwd sums the per-query-head shares
+  a.dv = nullptr;
   a.ldgkv = NT;
   return a;
 }
@@ -351,6 +352,7 @@ hipError_t Ctx::layer_bwd(int l, int B, int accumulate) {
   // RoPE + QK-norm backward
   QkBwdArgs qb{};
   qb.dqkv = dqkv32; qb.ld_dqkv = NT;
+  qb.dkvp = dkvp;
   qb.qkraw = s.qkraw;
   qb.qn = w.q_norm; qb.kn = w.k_norm;
   qb.cosT = cosT; qb.sinT = sinT;
