@@ -23,8 +23,9 @@
 // Tiles: a workgroup owns NW waves x 16 rows (queries, or keys for dK/dV)
 // and iterates over 64-row tiles of the other side, staged through LDS; the
 // next tile's global loads are issued before the current tile is computed.
-// Fewer waves per workgroup give more workgroups at short sequences.  Rows
-// and keys beyond S are zero-filled and masked, so any S works.
+// Rows and keys beyond S are zero-filled and masked, so any S works.
+#include <stdlib.h>
+
 #include <algorithm>
 
 #include "ops.h"
@@ -507,13 +508,14 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(const float* __restrict
   if (threadIdx.x == 0) damax[t] = amax;
 }
 
-// Waves per workgroup for a sequence length: fewer at short sequences so
-// that the launch still has several hundred workgroups.
-int attn_waves(int S, int B, int nheads) {
-  const long long wg4 = (long long)((S + 63) / 64) * nheads * B;
-  if (wg4 >= 512) return 4;
-  if (2 * wg4 >= 512 || S > 256) return 2;
-  return 1;
+// Waves per workgroup (16 query or key rows each).  Four measured fastest on
+// MI355X at S = 128 as well as at S = 2048 (fewer, longer workgroups beat more
+// single-wave ones); LLMT_ATTN_FWD_WAVES / LLMT_ATTN_BWD_WAVES = 1, 2 or 4
+// override it for tuning.
+int attn_waves(const char* env) {
+  const char* e = getenv(env);
+  if (e && (e[0] == '1' || e[0] == '2' || e[0] == '4') && !e[1]) return e[0] - '0';
+  return 4;
 }
 
 }  // namespace
@@ -544,7 +546,7 @@ hipError_t attn_fwd(const AttnArgs& a, int B, hipStream_t st) {
     set_error("attn_fwd: nq=%d nkv=%d S=%d", a.nq, a.nkv, a.S);
     return hipErrorInvalidValue;
   }
-  switch (attn_waves(a.S, B, a.nq)) {
+  switch (attn_waves("LLMT_ATTN_FWD_WAVES")) {
     case 1: launch_fwd<1>(a, B, st); break;
     case 2: launch_fwd<2>(a, B, st); break;
     default: launch_fwd<4>(a, B, st); break;
@@ -558,7 +560,7 @@ hipError_t attn_bwd(const AttnArgs& a, int B, hipStream_t st) {
     set_error("attn_bwd: nq=%d nkv=%d S=%d (dK/dV share buffer required)", a.nq, a.nkv, a.S);
     return hipErrorInvalidValue;
   }
-  switch (attn_waves(a.S, B, 2 * a.nq)) {
+  switch (attn_waves("LLMT_ATTN_BWD_WAVES")) {
     case 1: launch_bwd<1>(a, B, st); break;
     case 2: launch_bwd<2>(a, B, st); break;
     default: launch_bwd<4>(a, B, st); break;

@@ -112,12 +112,22 @@ struct Ctx {
   float* part = nullptr;   // split-K partials
   size_t part_elems = 0;
   _Float16* a16 = nullptr;
-  float *d_res = nullptr, *dmid = nullptr;
+  float* d_res = nullptr;
   _Float16* g16 = nullptr;
   float *rinv = nullptr, *rinv2 = nullptr;
   _Float16* dgu16 = nullptr;
   float *dO = nullptr, *delta = nullptr, *damax = nullptr;
-  float *dqkv32 = nullptr, *dy32 = nullptr, *dh = nullptr;
+  float* dqkv32 = nullptr;
+  // Per layer (kept until the adapter gradients of all layers run in one
+  // launch after the backward): dy of the q/k/v projections [T, NT], dy of
+  // the o projection [T, H], the LoRA dh columns [T, 64].
+  float *dy32_all = nullptr, *dmid_all = nullptr, *dh_all = nullptr;
+  float* dy32(int l) const { return dy32_all + (size_t)l * Tmax * NT; }
+  float* dmid(int l) const { return dmid_all + (size_t)l * Tmax * H; }
+  float* dh(int l) const { return dh_all + (size_t)l * Tmax * 64; }
+  LoraGradJob* lora_jobs = nullptr;  // device [L][kLoraJobs]
+  LoraGradPlan lora_plan{};
+  hipError_t lora_grads(int l0, int nl, int B, int accumulate);
   float* dkvp = nullptr;  // [T, 2 Q]: per-query-head dK | dV shares
 
   // graph + profiling
@@ -169,7 +179,7 @@ struct Ctx {
   // Fused CE over lg (NULL: the context's logits): loss, grad16, optional fp32 dlogits.
   hipError_t ce(const float* lg, const int* tgt, int B, float* dlogits_out);
   hipError_t head_bwd(int B);
-  hipError_t layer_bwd(int l, int B, int accumulate);
+  hipError_t layer_bwd(int l, int B);
   hipError_t backward(int B, int accumulate);
   hipError_t optimizer();
   hipError_t refresh_shadows();

@@ -16,48 +16,65 @@ namespace {
 
 constexpr int R = 16;
 constexpr int NTH = 256;
-constexpr int TCH = 64;  // tokens staged per LDS chunk
 
 // One adapter-gradient job: out = (acc ? out : 0) + lscale * X^T G over the T
 // token rows, for the ncols columns of X and the 16 columns of G.
 //   dA [16, d_in]:  X = adapter input (xn or o, fp16), G = dh  -> out[r][c]
 //   dB [d_out, 16]: X = upstream grad dy (fp32),       G = h   -> out[c][r]
-// A workgroup owns GC columns; its four waves take interleaved quarters of
-// every 64-token chunk and their partial sums are added in LDS in wave order.
+// A workgroup owns GC columns (a lane per column); its four waves take
+// interleaved batches of TB tokens, issue the batch's X loads together and
+// read the batch's G rows (uniform across the wave) through scalar loads,
+// then their partial sums are added in LDS in wave order.  Latency-bound at
+// T = 128: one memory round trip per batch.
 constexpr int GC = 64;
-__global__ __launch_bounds__(NTH) void lora_grad_kernel(const LoraGradJobs J, int T, float lscale,
+constexpr int TB = 32;
+template <bool F16>
+__device__ __forceinline__ void lora_grad_acc(const LoraGradJob& jb, int T, int cc, int w,
+                                              float (&acc)[R]) {
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  for (int t0 = wu * TB; t0 < T; t0 += (NTH / 64) * TB) {
+    float x[TB];
+#pragma unroll
+    for (int i = 0; i < TB; ++i) {
+      const long long off = (long long)min(t0 + i, T - 1) * jb.ldx + cc;
+      x[i] = F16 ? (float)((const _Float16*)jb.X)[off] : ((const float*)jb.X)[off];
+    }
+#pragma unroll
+    for (int i = 0; i < TB; ++i) {
+      if (t0 + i >= T) break;
+      const float* g = jb.G + (long long)(t0 + i) * jb.ldg;
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] += x[i] * g[r];
+    }
+  }
+}
+
+struct LoraGradGrid {
+  int block_start[kLoraJobs + 1];  // column blocks of each job within a layer
+};
+
+__global__ __launch_bounds__(NTH) void lora_grad_kernel(const LoraGradJob* __restrict__ jobs,
+                                                        const LoraGradGrid G, int T, float lscale,
                                                         int accumulate) {
-  __shared__ float Gs[TCH][R + 1];
   __shared__ float red[NTH / 64][GC][R + 1];
+  const int bpl = G.block_start[kLoraJobs];
+  const int layer = (int)blockIdx.x / bpl, lb = (int)blockIdx.x - layer * bpl;
   int j = 0;
 #pragma unroll
-  for (int i = 1; i < kMaxLoraJobs; ++i)
-    if (i < J.n && (int)blockIdx.x >= J.block_start[i]) j = i;
-  const LoraGradJob& jb = J.job[j];
+  for (int i = 1; i < kLoraJobs; ++i)
+    if (lb >= G.block_start[i]) j = i;
+  const LoraGradJob jb = jobs[layer * kLoraJobs + j];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int c = ((int)blockIdx.x - J.block_start[j]) * GC + lane;
+  const int c = (lb - G.block_start[j]) * GC + lane;
   const bool active = c < jb.ncols;
+  const int cc = active ? c : 0;
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
-  for (int t0 = 0; t0 < T; t0 += TCH) {
-    __syncthreads();
-    for (int i = threadIdx.x; i < TCH * R; i += NTH) {
-      const int tt = i / R, r = i % R;
-      Gs[tt][r] = t0 + tt < T ? jb.G[(long long)(t0 + tt) * jb.ldg + r] : 0.f;
-    }
-    __syncthreads();
-    if (active) {
-      const int n = min(TCH, T - t0);
-#pragma unroll 4
-      for (int tt = w; tt < n; tt += NTH / 64) {
-        const long long off = (long long)(t0 + tt) * jb.ldx + c;
-        const float x = jb.x_f16 ? (float)((const _Float16*)jb.X)[off] : ((const float*)jb.X)[off];
-#pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] += x * Gs[tt][r];
-      }
-    }
-  }
+  if (jb.x_f16)
+    lora_grad_acc<true>(jb, T, cc, w, acc);
+  else
+    lora_grad_acc<false>(jb, T, cc, w, acc);
 #pragma unroll
   for (int r = 0; r < R; ++r) red[w][lane][r] = acc[r];
   __syncthreads();
@@ -176,19 +193,17 @@ inline unsigned grid_for(long long n) {
 
 }  // namespace
 
-hipError_t lora_grad(const LoraGradJobs& jobs_in, int T, float lscale, int accumulate,
-                     hipStream_t st) {
-  LoraGradJobs J = jobs_in;
-  if (J.n < 1 || J.n > kMaxLoraJobs) {
-    set_error("lora_grad: %d jobs", J.n);
+hipError_t lora_grad(const LoraGradJob* jobs, const LoraGradPlan& plan, int layers, int T,
+                     float lscale, int accumulate, hipStream_t st) {
+  if (layers < 1 || T < 1) {
+    set_error("lora_grad: %d layers, T=%d", layers, T);
     return hipErrorInvalidValue;
   }
-  int blocks = 0;
-  for (int i = 0; i < J.n; ++i) {
-    J.block_start[i] = blocks;
-    blocks += (J.job[i].ncols + GC - 1) / GC;
-  }
-  hipLaunchKernelGGL(lora_grad_kernel, dim3(blocks), dim3(NTH), 0, st, J, T, lscale, accumulate);
+  LoraGradGrid G{};
+  for (int i = 0; i < kLoraJobs; ++i)
+    G.block_start[i + 1] = G.block_start[i] + (plan.ncols[i] + GC - 1) / GC;
+  hipLaunchKernelGGL(lora_grad_kernel, dim3(layers * G.block_start[kLoraJobs]), dim3(NTH), 0, st,
+                     jobs, G, T, lscale, accumulate);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }

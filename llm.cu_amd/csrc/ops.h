@@ -231,7 +231,6 @@ hipError_t attn_delta(const float* dO, long long ldd, const _Float16* o, long lo
 hipError_t gpu_delay(int us, hipStream_t st);
 
 // ---------------------------------------------------------------- LoRA / AdamW
-constexpr int kMaxLoraJobs = 8;
 struct LoraGradJob {
   const void* X;     // [T, ldx] fp16 or fp32
   int x_f16;
@@ -242,13 +241,15 @@ struct LoraGradJob {
   float* out;
   int out_is_B;      // 0: out[16][ncols] (dA), 1: out[ncols][16] (dB)
 };
-struct LoraGradJobs {
-  LoraGradJob job[kMaxLoraJobs];
-  int block_start[kMaxLoraJobs];
-  int n;
+// The adapter-gradient jobs of `layers` consecutive layers (kLoraJobs per
+// layer, same order and column counts in every layer) in one launch; `jobs`
+// is a device table [layer][kLoraJobs], starting at the first layer.
+constexpr int kLoraJobs = 8;
+struct LoraGradPlan {
+  int ncols[kLoraJobs];  // columns of each job (identical across layers)
 };
-hipError_t lora_grad(const LoraGradJobs& jobs, int T, float lscale, int accumulate,
-                     hipStream_t st);
+hipError_t lora_grad(const LoraGradJob* jobs, const LoraGradPlan& plan, int layers, int T,
+                     float lscale, int accumulate, hipStream_t st);
 
 struct AdamHp {
   float lr, beta1, beta2, eps, wd, bc1, bc2;

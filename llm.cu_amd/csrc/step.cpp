@@ -288,7 +288,7 @@ hipError_t Ctx::head_bwd(int B) {
   nb.in = row_in(go);
   nb.rinv_in = nullptr;
   nb.gscale = 1.0f / (kGradLogitScale * (float)n_valid);
-  nb.dh_out = dh;
+  nb.dh_out = nullptr;
   nb.x = x_final;
   nb.w = final_norm;
   nb.eps = eps;
@@ -305,16 +305,19 @@ hipError_t Ctx::head_bwd(int B) {
 
 // One decoder layer's backward (src/kernels/lora_backward.cu:271-406) from
 // d_res / g16 / rinv (the gradient at the layer output); leaves the gradient
-// at the layer input there and writes (or adds, accumulate) the layer's
-// adapter gradients into the GRAD arena.
-hipError_t Ctx::layer_bwd(int l, int B, int accumulate) {
+// at the layer input there and the layer's adapter-gradient inputs (dh, dy)
+// in its per-layer slots for lora_grads.
+hipError_t Ctx::layer_bwd(int l, int B) {
   const int T = B * S;
-  const float eps = dims.eps, ls = lscale;
+  const float eps = dims.eps;
   GemmOut go;
   NormBwdArgs nb{};
 
   Layer& w = layers[l];
   Stash& s = stash[l];
+  float* const dh = this->dh(l);
+  float* const dmid = this->dmid(l);
+  float* const dy32 = this->dy32(l);
   // MLP: down dX -> SwiGLU bwd -> gate/up dX -> FFN norm bwd (+ residual)
   BSeg sd[1] = {wseg(w.wdT)};
   LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, sd, 1, T, H, nullptr, 0, &go));
@@ -326,7 +329,7 @@ hipError_t Ctx::layer_bwd(int l, int B, int accumulate) {
   nb.in = row_in(go);
   nb.rinv_in = rinv2;
   nb.gscale = 1.0f;
-  nb.dh_out = dh;
+  nb.dh_out = nullptr;
   nb.x = s.x_mid;
   nb.w = w.ffn_norm;
   nb.eps = eps;
@@ -384,28 +387,19 @@ hipError_t Ctx::layer_bwd(int l, int B, int accumulate) {
   nb.rinv_out = rinv;
   LLMT_HIP_TRY(mark(CAT_ROWS));
   LLMT_HIP_TRY(norm_bwd(nb, T, st));
-  // adapter gradients of this layer
-  LoraGradJobs J{};
-  J.n = 8;
-  const LoraGradJob jobs[8] = {
-      {s.xn, 1, H, H, dh + 0, 64, lora_ptr(lora_g, l, 0, 0), 0},
-      {s.xn, 1, H, H, dh + 16, 64, lora_ptr(lora_g, l, 1, 0), 0},
-      {s.xn, 1, H, H, dh + 32, 64, lora_ptr(lora_g, l, 2, 0), 0},
-      {s.o16, 1, Q, Q, dh + 48, 64, lora_ptr(lora_g, l, 3, 0), 0},
-      {dy32, 0, NT, Q, s.h + 0, 64, lora_ptr(lora_g, l, 0, 1), 1},
-      {dy32 + Q, 0, NT, KV, s.h + 16, 64, lora_ptr(lora_g, l, 1, 1), 1},
-      {dy32 + Q + KV, 0, NT, KV, s.h + 32, 64, lora_ptr(lora_g, l, 2, 1), 1},
-      {dmid, 0, H, H, s.h + 48, 64, lora_ptr(lora_g, l, 3, 1), 1},
-  };
-  for (int i = 0; i < 8; ++i) J.job[i] = jobs[i];
-  LLMT_HIP_TRY(mark(CAT_LORA));
-  LLMT_HIP_TRY(lora_grad(J, T, ls, accumulate, st));
   return hipSuccess;
+}
+
+hipError_t Ctx::lora_grads(int l0, int nl, int B, int accumulate) {
+  LLMT_HIP_TRY(mark(CAT_LORA));
+  return lora_grad(lora_jobs + (size_t)l0 * kLoraJobs, lora_plan, nl, B * S, lscale, accumulate, st);
 }
 
 hipError_t Ctx::backward(int B, int accumulate) {
   LLMT_HIP_TRY(head_bwd(B));
-  for (int l = L - 1; l >= 0; --l) LLMT_HIP_TRY(layer_bwd(l, B, accumulate));
+  for (int l = L - 1; l >= 0; --l) LLMT_HIP_TRY(layer_bwd(l, B));
+  // every layer's adapter gradients in one launch
+  LLMT_HIP_TRY(lora_grads(0, L, B, accumulate));
   return hipSuccess;
 }
 
