@@ -29,6 +29,7 @@
 // trip, the partial stores), which four-wave 128-column tiles at about 3/4 of
 // a workgroup per CU balance best against the partial traffic; deeper B
 // rings and A prefetch distances measured no faster.
+#include <math.h>
 #include <stdlib.h>
 #include <type_traits>
 
@@ -247,6 +248,468 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
         C[(long long)row * g.ldc + col] = acc[mi][f][v] * cs;
       }
     }
+  }
+}
+
+// Large-M kernel (the T = 4096 configurations, where the GEMMs are
+// MFMA-bound): a 256 x BN output tile per workgroup of WN x 2 waves (each
+// 128 x 64: 32 accumulator fragments), both operands staged through LDS in
+// MFMA fragment order in 64-wide K chunks (double-buffered; the next chunk's
+// global loads are issued before the current chunk is multiplied).  int8 B
+// pieces are dequantised (times the per-k scale, if any) on their way into
+// LDS; per-row scales are applied in the epilogue.  Split-K over blockIdx.y
+// (partials summed by the consumer).  Wider tiles raise the flops per byte
+// fetched from L2 / MALL, which bounds this kernel before the MFMA rate does.
+constexpr int BM = 256, BCH = 2;  // BCH k-steps per chunk
+template <int WN>
+__global__ __launch_bounds__(WN * 128) void gemm_big_kernel(const GemmArgs g, int g_order) {
+  constexpr int BN = WN * 64, NT = WN * 128;
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * BCH * KSTEP];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * BCH * KSTEP];
+  constexpr int AP = BM * BCH * KSTEP / 8 / NT;  // 16-byte A pieces per thread
+  constexpr int BP = BN * BCH * KSTEP / 8 / NT;  // B pieces per thread
+  constexpr int NFB = BN / 16;                    // column fragments per k-step
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  // Tile order: workgroup i runs on XCD i % 8, so tiles are renumbered to
+  // give each XCD a contiguous run of them (operand reuse in its L2).
+  const int ntn = (g.N + BN - 1) / BN, ntm = g.M / BM, nwg = ntn * ntm;
+  int t = blockIdx.x;
+  if (g_order >= 1 && nwg % 8 == 0) t = (t % 8) * (nwg / 8) + t / 8;
+  int tn = t % ntn, tm = t / ntn;
+  const int gmx = g_order >= 2 ? g_order : 1;  // groups of gmx row tiles
+  if (gmx > 1 && ntm % gmx == 0) {
+    const int grp = t / (gmx * ntn), r = t % (gmx * ntn);
+    tm = grp * gmx + r % gmx;
+    tn = r / gmx;
+  }
+  const int n0 = tn * BN, m0 = tm * BM;
+  const int ksteps = g.K / KSTEP;
+  const int c0 = (int)((long long)blockIdx.y * (ksteps / BCH) / g.split);
+  const int c1 = (int)((long long)(blockIdx.y + 1) * (ksteps / BCH) / g.split);
+
+  // B pieces of this thread: piece idx = tid + NT p -> fragment fr = idx >> 6
+  // (wave-uniform: k-step q = fr / NFB, row block ni = fr % NFB), lane idx & 63.
+  const char* bptr[BP];
+  int bi8[BP];
+  const _Float16* bks[BP];
+#pragma unroll
+  for (int p = 0; p < BP; ++p) {
+    const int fr = (tid + NT * p) >> 6, ni = fr % NFB;
+    const int nn = min(n0 + ni * 16, g.N - 16);
+    int sgi = 0;
+#pragma unroll
+    for (int i = 1; i < 4; ++i)
+      if (i < g.nseg && nn >= g.seg_start[i]) sgi = i;
+    const BSeg& sg = g.seg[sgi];
+    const long long rb16 = (nn - g.seg_start[sgi]) >> 4;
+    bi8[p] = sg.is_i8;
+    bptr[p] = (const char*)sg.ptr + ((rb16 * ksteps) * 512 + lane * 8) * (sg.is_i8 ? 1 : 2);
+    bks[p] = sg.is_i8 && sg.kscale ? sg.kscale + (lane >> 4) * 8 : nullptr;
+  }
+  u32x4 ra[AP], rbv[BP];
+  half8 rks[BP];
+  auto load = [&](int c) LLMT_INLINE {
+    const int kb = c * BCH;
+#pragma unroll
+    for (int p = 0; p < AP; ++p) {
+      const int idx = tid + NT * p, fr = idx >> 6, l = idx & 63;
+      const int q = fr / 16, mi = fr % 16;
+      const int r = mi * 16 + (l & 15);
+      const int k = (kb + q) * KSTEP + (l >> 4) * 8;
+      ra[p] = *reinterpret_cast<const u32x4*>(g.A + (long long)(m0 + r) * g.lda + k);
+    }
+#pragma unroll
+    for (int p = 0; p < BP; ++p) {
+      const int q = ((tid + NT * p) >> 6) / NFB;
+      const long long ks = kb + q;
+      if (bi8[p]) {
+        const u32x2 v = *reinterpret_cast<const u32x2*>(bptr[p] + ks * 512);
+        rbv[p] = u32x4{v[0], v[1], 0u, 0u};
+        if (bks[p]) rks[p] = *reinterpret_cast<const half8*>(bks[p] + ks * KSTEP);
+      } else {
+        rbv[p] = *reinterpret_cast<const u32x4*>(bptr[p] + ks * 1024);
+      }
+    }
+  };
+  auto store = [&](int buf) LLMT_INLINE {
+#pragma unroll
+    for (int p = 0; p < AP; ++p)
+      *reinterpret_cast<u32x4*>(&As[buf][(tid + NT * p) * 8]) = ra[p];
+#pragma unroll
+    for (int p = 0; p < BP; ++p) {
+      half8 h;
+      if (bi8[p]) {
+        const int8x8 q8 = __builtin_bit_cast(int8x8, u32x2{rbv[p][0], rbv[p][1]});
+#pragma unroll
+        for (int i = 0; i < 8; ++i) h[i] = (_Float16)(float)q8[i];
+        if (bks[p]) h = h * rks[p];
+      } else {
+        h = __builtin_bit_cast(half8, rbv[p]);
+      }
+      *reinterpret_cast<half8*>(&Bs[buf][(tid + NT * p) * 8]) = h;
+    }
+  };
+
+  floatx4 acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  if (c1 > c0) {
+    load(c0);
+    store(0);
+    __syncthreads();
+  }
+  for (int c = c0; c < c1; ++c) {
+    const int buf = (c - c0) & 1;
+    if (c + 1 < c1) load(c + 1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < BCH; ++q) {
+      half8 b[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        b[j] = *reinterpret_cast<const half8*>(&Bs[buf][((q * NFB + wn * 4 + j) * 64 + lane) * 8]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const half8 a =
+            *reinterpret_cast<const half8*>(&As[buf][((q * 16 + wm * 8 + i) * 64 + lane) * 8]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16(a, b[j], acc[i][j]);
+      }
+    }
+    if (c + 1 < c1) store(buf ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue: D[4 g + v][c] of fragment (i, j)
+  float* C = g.C + (long long)blockIdx.y * g.split_stride;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int col = n0 + wn * 64 + j * 16 + (lane & 15);
+    if (col >= g.N) continue;
+    int sgi = 0;
+#pragma unroll
+    for (int i = 1; i < 4; ++i)
+      if (i < g.nseg && col >= g.seg_start[i]) sgi = i;
+    const _Float16* cs = g.seg[sgi].colscale;
+    const float sc = cs ? (float)cs[col - g.seg_start[sgi]] : 1.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = m0 + wm * 128 + i * 16 + (lane >> 4) * 4 + v;
+        C[(long long)row * g.ldc + col] = acc[i][j][v] * sc;
+      }
+  }
+}
+
+// Four-wave variant of the same 256 x 256 tile: each wave owns 128 x 128
+// (64 accumulator fragments, held in the accumulation registers), which halves
+// the LDS fragment reads per MFMA, and frees enough registers for two chunks
+// of global loads in flight (prefetch distance 2), so a chunk's L2 / MALL
+// latency is covered by two chunks of MFMA work.
+template <bool I8, bool KS, int PD>
+__global__ __launch_bounds__(256) void gemm_big4_kernel(const GemmArgs g, int g_order) {
+  constexpr int BN = 256, NT = 256;
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * BCH * KSTEP];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * BCH * KSTEP];
+  constexpr int AP = BM * BCH * KSTEP / 8 / NT;  // 8
+  constexpr int BP = BN * BCH * KSTEP / 8 / NT;  // 8
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int ntn = (g.N + BN - 1) / BN, ntm = g.M / BM, nwg = ntn * ntm;
+  int t = blockIdx.x;
+  if (g_order >= 1 && nwg % 8 == 0) t = (t % 8) * (nwg / 8) + t / 8;
+  const int tn = t % ntn, tm = t / ntn;
+  const int n0 = tn * BN, m0 = tm * BM;
+  const int ksteps = g.K / KSTEP;
+  const int c0 = (int)((long long)blockIdx.y * (ksteps / BCH) / g.split);
+  const int c1 = (int)((long long)(blockIdx.y + 1) * (ksteps / BCH) / g.split);
+
+  // Thread pieces (one segment, uniform element type): piece p of the chunk
+  // is fragment wave + 4 p, i.e. k-step p / 4 and 16-row block
+  // wave + 4 (p % 4) of the tile; lane l carries row (l & 15), k (l >> 4) * 8.
+  const _Float16* abase = g.A + (long long)(m0 + wave * 16 + (lane & 15)) * g.lda + (lane >> 4) * 8;
+  const long long astep = 64LL * g.lda;  // 4 row blocks
+  const BSeg& sg = g.seg[0];
+  constexpr int ES = I8 ? 1 : 2;
+  const char* bbase = (const char*)sg.ptr + (long long)lane * 8 * ES;
+  long long boff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int rb = min((n0 >> 4) + wave + 4 * j, (g.N >> 4) - 1);
+    boff[j] = (long long)rb * ksteps * 512 * ES;
+  }
+  const _Float16* kscale = KS ? sg.kscale + (lane >> 4) * 8 : nullptr;
+  using BRaw = std::conditional_t<I8, u32x2, u32x4>;
+  u32x4 ra[PD][AP];
+  BRaw rbv[PD][BP];
+  half8 rks[PD][BCH];
+  auto load = [&](int c, auto R) LLMT_INLINE {
+    constexpr int r = decltype(R)::value;
+    const int kb = min(c, c1 - 1) * BCH;
+#pragma unroll
+    for (int p = 0; p < AP; ++p)
+      ra[r][p] = *reinterpret_cast<const u32x4*>(abase + (p % 4) * astep + (kb + p / 4) * KSTEP);
+#pragma unroll
+    for (int p = 0; p < BP; ++p)
+      rbv[r][p] = *reinterpret_cast<const BRaw*>(bbase + boff[p % 4] + (long long)(kb + p / 4) * 512 * ES);
+    if constexpr (KS) {
+#pragma unroll
+      for (int q = 0; q < BCH; ++q)
+        rks[r][q] = *reinterpret_cast<const half8*>(kscale + (long long)(kb + q) * KSTEP);
+    }
+  };
+  auto store = [&](int buf, auto R) LLMT_INLINE {
+    constexpr int r = decltype(R)::value;
+#pragma unroll
+    for (int p = 0; p < AP; ++p)
+      *reinterpret_cast<u32x4*>(&As[buf][(tid + NT * p) * 8]) = ra[r][p];
+#pragma unroll
+    for (int p = 0; p < BP; ++p) {
+      half8 h;
+      if constexpr (I8) {
+        const int8x8 q8 = __builtin_bit_cast(int8x8, rbv[r][p]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) h[i] = (_Float16)(float)q8[i];
+        if constexpr (KS) h = h * rks[r][p / 4];
+      } else {
+        h = __builtin_bit_cast(half8, rbv[r][p]);
+      }
+      *reinterpret_cast<half8*>(&Bs[buf][(tid + NT * p) * 8]) = h;
+    }
+  };
+
+  floatx4 acc[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int buf) LLMT_INLINE {
+#pragma unroll
+    for (int q = 0; q < BCH; ++q) {
+      half8 b[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        b[j] = *reinterpret_cast<const half8*>(&Bs[buf][((q * 16 + wn * 8 + j) * 64 + lane) * 8]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const half8 a =
+            *reinterpret_cast<const half8*>(&As[buf][((q * 16 + wm * 8 + i) * 64 + lane) * 8]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = mfma16(a, b[j], acc[i][j]);
+      }
+    }
+  };
+  // Chunk x of this split lives in register set (x - c0) % PD while in
+  // flight and in LDS buffer (x - c0) % 2 while multiplied; with PD = 2 a
+  // loop trip covers two chunks so every set index is static; loads past the
+  // end are clamped re-reads that are never multiplied.
+  const int nck = c1 - c0;
+  if constexpr (PD == 1) {
+    if (nck > 0) {
+      load(c0, IC<0>{});
+      store(0, IC<0>{});
+      __syncthreads();
+    }
+    for (int c = c0; c < c1; ++c) {
+      const int buf = (c - c0) & 1;
+      load(c + 1, IC<0>{});
+      __builtin_amdgcn_sched_barrier(0);
+      compute(buf);
+      store(buf ^ 1, IC<0>{});
+      __syncthreads();
+    }
+  } else if (nck > 0) {
+    load(c0, IC<0>{});
+    load(c0 + 1, IC<1>{});
+    store(0, IC<0>{});
+    __syncthreads();
+    for (int pr = 0; pr < nck / 2; ++pr) {
+      const int c = c0 + 2 * pr;
+      load(c + 2, IC<0>{});
+      __builtin_amdgcn_sched_barrier(0);
+      compute(0);
+      store(1, IC<1>{});
+      __syncthreads();
+      load(c + 3, IC<1>{});
+      __builtin_amdgcn_sched_barrier(0);
+      compute(1);
+      store(0, IC<0>{});
+      __syncthreads();
+    }
+    if (nck & 1) compute(0);
+  }
+
+  float* C = g.C + (long long)blockIdx.y * g.split_stride;
+  const _Float16* cs = sg.colscale;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int col = n0 + wn * 128 + j * 16 + (lane & 15);
+    if (col >= g.N) continue;
+    const float sc = cs ? (float)cs[col] : 1.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = m0 + wm * 128 + i * 16 + (lane >> 4) * 4 + v;
+        C[(long long)row * g.ldc + col] = acc[i][j][v] * sc;
+      }
+  }
+}
+
+// LDS-DMA kernel for the large-M GEMMs: the operands go from global memory
+// straight into LDS (global_load_lds: lane l's 16 bytes land at offset 16 l
+// of the wave's block; a fragment-packed fp16 fragment is 1 KB in lane order
+// and an int8 one 512 B, moved by the first 32 lanes, so both arrive in MFMA
+// fragment order with no register staging and no LDS store phase), through
+// an S-stage ring of 32-wide K chunks: chunk c + S - 1 is in flight while
+// chunk c is multiplied, so S - 1 chunks of MFMA work cover the memory
+// latency.  Each workgroup of four waves owns a 256 x 256 tile (128 x 128
+// per wave, the 64 accumulator fragments in the accumulation registers).
+// int8 B fragments are dequantised at read time (exact int8 -> fp16 through
+// the 1024 + x bias trick, times the per-k scale if any).  The waits are
+// explicit: vmcnt counts this thread's DMA issues, which complete in order,
+// and a plain s_barrier (no fence, which would drain every load) publishes
+// the chunk to the other waves.
+__device__ __forceinline__ void dma16(const void* src, _Float16* lds_blk) {
+  __builtin_amdgcn_global_load_lds(src, (void __attribute__((address_space(3)))*)lds_blk, 16, 0, 0);
+}
+// s_waitcnt with vmcnt = N (lgkmcnt and expcnt left free), gfx9 encoding.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// fp16 from 8 int8 values: (1024 + (x + 128)) - 1152, exact.
+__device__ __forceinline__ half8 i8x8_to_h8(u32x2 raw) {
+  const unsigned lo = raw[0] ^ 0x80808080u, hi = raw[1] ^ 0x80808080u;
+  u32x4 bits;
+  bits[0] = 0x64006400u | (lo & 0xFFu) | ((lo & 0xFF00u) << 8);
+  bits[1] = 0x64006400u | ((lo >> 16) & 0xFFu) | ((lo >> 8) & 0xFF0000u);
+  bits[2] = 0x64006400u | (hi & 0xFFu) | ((hi & 0xFF00u) << 8);
+  bits[3] = 0x64006400u | ((hi >> 16) & 0xFFu) | ((hi >> 8) & 0xFF0000u);
+  const half8 h = __builtin_bit_cast(half8, bits);
+  return h - (_Float16)1152.0f;
+}
+
+template <bool I8, bool KS, int S, int WNN>
+__global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, int g_order) {
+  // WNN waves across N (2: four waves of 128 x 128; 4: eight waves of 128 x 64)
+  constexpr int NW = 2 * WNN, WC = 256 / WNN, NFR = WC / 16;  // wave columns, fragments
+  constexpr int FPW = 16 / NW;                                 // A (and B) fragments each wave moves
+  constexpr int ABYTES = 256 * KSTEP * 2;
+  constexpr int BBYTES = 256 * KSTEP * (I8 ? 1 : 2);
+  constexpr int SBYTES = ABYTES + BBYTES + (KS ? 256 : 0);
+  constexpr int OPS = 2 * FPW + (KS ? 1 : 0);                  // DMA issues per chunk per thread
+  __shared__ __attribute__((aligned(1024))) char smem[S * SBYTES];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WNN, wn = wave % WNN;
+  const int ntn = (g.N + 255) / 256, ntm = g.M / 256, nwg = ntn * ntm;
+  int t = blockIdx.x;
+  if (g_order >= 1 && nwg % 8 == 0) t = (t % 8) * (nwg / 8) + t / 8;
+  const int tn = t % ntn, tm = t / ntn;
+  const int n0 = tn * 256, m0 = tm * 256;
+  const int ksteps = g.K / KSTEP;
+  const int c0 = (int)((long long)blockIdx.y * ksteps / g.split);
+  const int c1 = (int)((long long)(blockIdx.y + 1) * ksteps / g.split);
+
+  // issue pointers: wave w moves A fragments FPW w .. and B fragments FPW w ..
+  // of every chunk (plus, with KS, k-scales through lane 0 of waves 0-3)
+  const _Float16* asrc =
+      g.A + (long long)(m0 + wave * FPW * 16 + (lane & 15)) * g.lda + (lane >> 4) * 8;
+  const long long astep = 16LL * g.lda;
+  const BSeg& sg = g.seg[0];
+  constexpr int ES = I8 ? 1 : 2;
+  const char* bsrc = (const char*)sg.ptr + (long long)lane * 16;  // lanes < 32 for int8
+  long long boff[FPW];
+#pragma unroll
+  for (int j = 0; j < FPW; ++j) {
+    const int rb = min((n0 >> 4) + wave * FPW + j, (g.N >> 4) - 1);
+    boff[j] = (long long)rb * ksteps * 512 * ES;
+  }
+  const _Float16* ksrc = KS ? sg.kscale + (wave & 3) * 8 : nullptr;
+  auto issue = [&](int c) LLMT_INLINE {
+    const int cc = min(c, c1 - 1);
+    char* st = smem + (c % S) * SBYTES;
+#pragma unroll
+    for (int j = 0; j < FPW; ++j)
+      dma16(asrc + j * astep + cc * KSTEP, reinterpret_cast<_Float16*>(st + (wave * FPW + j) * 1024));
+#pragma unroll
+    for (int j = 0; j < FPW; ++j) {
+      const char* src = bsrc + boff[j] + (long long)cc * 512 * ES;
+      _Float16* dst = reinterpret_cast<_Float16*>(st + ABYTES + (wave * FPW + j) * 512 * ES);
+      if constexpr (I8) {
+        if (lane < 32) dma16(src, dst);
+      } else {
+        dma16(src, dst);
+      }
+    }
+    if constexpr (KS) {
+      if (lane == 0 && wave < 4)
+        dma16(ksrc + (long long)cc * KSTEP, reinterpret_cast<_Float16*>(st + ABYTES + BBYTES + wave * 16));
+      else if (lane == 0)  // keep the per-thread DMA count uniform (a harmless re-read)
+        dma16(ksrc + (long long)cc * KSTEP, reinterpret_cast<_Float16*>(st + ABYTES + BBYTES + 64 + (wave & 3) * 16));
+    }
+  };
+
+  floatx4 acc[8][NFR];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < NFR; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int c = 0; c < S - 1; ++c) issue(c0 + c);
+  for (int c = c0; c < c1; ++c) {
+    wait_vm<(S - 2) * OPS>();
+    __builtin_amdgcn_s_barrier();
+    issue(c + S - 1);
+    const char* st = smem + (c % S) * SBYTES;
+    half8 b[NFR];
+    half8 ksc;
+    if constexpr (KS) ksc = *reinterpret_cast<const half8*>(st + ABYTES + BBYTES + (lane >> 4) * 16);
+#pragma unroll
+    for (int j = 0; j < NFR; ++j) {
+      const int fr = wn * NFR + j;
+      if constexpr (I8) {
+        const u32x2 raw = *reinterpret_cast<const u32x2*>(st + ABYTES + fr * 512 + lane * 8);
+        b[j] = i8x8_to_h8(raw);
+        if constexpr (KS) b[j] = b[j] * ksc;
+      } else {
+        b[j] = *reinterpret_cast<const half8*>(st + ABYTES + fr * 1024 + lane * 16);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const half8 a = *reinterpret_cast<const half8*>(st + (wm * 8 + i) * 1024 + lane * 16);
+#pragma unroll
+      for (int j = 0; j < NFR; ++j) acc[i][j] = mfma16(a, b[j], acc[i][j]);
+    }
+  }
+  wait_vm<0>();
+
+  float* C = g.C + (long long)blockIdx.y * g.split_stride;
+  const _Float16* cs = sg.colscale;
+#pragma unroll
+  for (int j = 0; j < NFR; ++j) {
+    const int col = n0 + wn * WC + j * 16 + (lane & 15);
+    if (col >= g.N) continue;
+    const float sc = cs ? (float)cs[col] : 1.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = m0 + wm * 128 + i * 16 + (lane >> 4) * 4 + v;
+        C[(long long)row * g.ldc + col] = acc[i][j][v] * sc;
+      }
   }
 }
 
@@ -546,7 +1009,38 @@ void gemm_finalize_segments(GemmArgs& g) {
 // partials to reduce.
 int gemm_tile_n() { return kCfgs[gemm_cfg()].nw * kNF * 16; }
 
+// The 256 x 128 tile kernel takes GEMMs with many rows (no split-K); the
+// skinny kernel everything else.
+static bool big_tiles(int M, int K) { return M >= 1024 && M % BM == 0 && K % (BCH * KSTEP) == 0; }
+static bool use_big_tiles(const GemmArgs& g) {
+  return big_tiles(g.M, g.K) && g.N >= 16 && g.split <= (g.K / (BCH * KSTEP));
+}
+// waves across the tile width: 256-wide tiles (4) unless LLMT_GEMM_BIG_WN=2
+static int big_wn(int N) {
+  (void)N;
+  return env_int("LLMT_GEMM_BIG_WN", 4) == 2 ? 2 : 4;
+}
+
+// Large-tile split-K: the smallest of 1, 2, 4 whose workgroup count fills
+// the 256 CUs in whole waves to >= 85% (partials cost traffic, so no more).
+// A trailing LoRA segment of <= 64 columns runs as its own skinny launch
+// (gemm_nt), so it is left out of the tile count.
+static int big_split(int M, int N, int K, int max_split) {
+  const int nmain = (N % 256 != 0 && N % 64 != 0) ? N - N % 64 : N;
+  const int bn = big_wn(nmain) * 64;
+  const int tiles = (nmain + bn - 1) / bn * (M / BM);
+  int best = 1;
+  for (int split = 1; split <= 4 && split <= max_split && split <= K / (BCH * KSTEP) / 4;
+       split *= 2) {
+    best = split;
+    const double waves = tiles * split / 256.0;
+    if (waves / ceil(waves) >= 0.85) break;
+  }
+  return best;
+}
+
 int gemm_pick_split(int M, int N, int K, int max_split) {
+  if (big_tiles(M, K)) return big_split(M, N, K, max_split);
   // Partials grow with the workgroup count: about 3/4 of the CUs for the
   // layer GEMMs, two waves of CUs for the very long lm_head dX reduction.
   const int target = env_int("LLMT_GEMM_TARGET_WG", K > 16384 ? 512 : 192);
@@ -575,7 +1069,58 @@ hipError_t gemm_nt(const GemmArgs& g, hipStream_t st) {
     }
   hipError_t e;
   const int m16 = g.M / 16;
-  if (m16 % 8 == 0) e = launch_mf<8>(g, st);
+  if (use_big_tiles(g)) {
+    GemmArgs gm = g;
+    const int last = g.nseg - 1;
+    const bool lora_tail = g.nseg > 1 && g.seg[last].rows <= 64 && g.seg_start[last] % 64 == 0;
+    if (lora_tail) {  // the main segments on big tiles, the LoRA rows skinny
+      gm.nseg = last;
+      gemm_finalize_segments(gm);
+    }
+    const int wn = big_wn(gm.N);
+    const int nwg = (gm.N + wn * 64 - 1) / (wn * 64) * (gm.M / BM);
+    const int order = env_int("LLMT_GEMM_BIG_ORDER", 0);
+    const bool i8 = gm.seg[0].is_i8, ks = gm.seg[0].kscale != nullptr;
+    const int kind = env_int("LLMT_GEMM_BIG_KIND", 2);  // 0: 8-wave, 1: 4-wave, 2: DMA
+    if (kind == 2 && wn == 4 && gm.nseg == 1 && gm.N % 16 == 0) {
+      const dim3 gr(nwg, gm.split);
+      if (env_int("LLMT_GEMM_DMA_WAVES", 8) == 4) {
+        if (!i8)
+          hipLaunchKernelGGL((gemm_dma_kernel<false, false, 4, 2>), gr, dim3(256), 0, st, gm, order);
+        else if (ks)
+          hipLaunchKernelGGL((gemm_dma_kernel<true, true, 5, 2>), gr, dim3(256), 0, st, gm, order);
+        else
+          hipLaunchKernelGGL((gemm_dma_kernel<true, false, 5, 2>), gr, dim3(256), 0, st, gm, order);
+      } else {
+        if (!i8)
+          hipLaunchKernelGGL((gemm_dma_kernel<false, false, 4, 4>), gr, dim3(512), 0, st, gm, order);
+        else if (ks)
+          hipLaunchKernelGGL((gemm_dma_kernel<true, true, 5, 4>), gr, dim3(512), 0, st, gm, order);
+        else
+          hipLaunchKernelGGL((gemm_dma_kernel<true, false, 5, 4>), gr, dim3(512), 0, st, gm, order);
+      }
+    } else if (kind == 1 && wn == 4 && gm.nseg == 1 && gm.N % 16 == 0) {
+      const dim3 gr(nwg, gm.split);
+      if (!i8)
+        hipLaunchKernelGGL((gemm_big4_kernel<false, false, 1>), gr, dim3(256), 0, st, gm, order);
+      else if (ks)
+        hipLaunchKernelGGL((gemm_big4_kernel<true, true, 1>), gr, dim3(256), 0, st, gm, order);
+      else
+        hipLaunchKernelGGL((gemm_big4_kernel<true, false, 1>), gr, dim3(256), 0, st, gm, order);
+    } else if (wn == 4)
+      hipLaunchKernelGGL(gemm_big_kernel<4>, dim3(nwg, gm.split), dim3(512), 0, st, gm, order);
+    else
+      hipLaunchKernelGGL(gemm_big_kernel<2>, dim3(nwg, gm.split), dim3(256), 0, st, gm, order);
+    e = hipGetLastError();
+    if (e == hipSuccess && lora_tail) {
+      GemmArgs gl = g;
+      gl.nseg = 1;
+      gl.seg[0] = g.seg[last];
+      gemm_finalize_segments(gl);
+      gl.C = g.C + g.seg_start[last];
+      e = launch_mf<8>(gl, st);
+    }
+  } else if (m16 % 8 == 0) e = launch_mf<8>(g, st);
   else if (m16 % 4 == 0) e = launch_mf<4>(g, st);
   else if (m16 % 2 == 0) e = launch_mf<2>(g, st);
   else e = launch_mf<1>(g, st);

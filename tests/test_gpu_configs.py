@@ -362,3 +362,35 @@ def test_c4_full_size_properties(dev):
         assert l1 == l2 and torch.equal(g1, g2)
     finally:
         ctx.close()
+
+
+# ------------------------------------------------------------------ large-T path
+# T = B x S >= 1024 runs every frozen-weight GEMM on the 256 x 128 tile kernel
+# (fp16 and int8 B operands, LoRA segments in the last column tile, per-row
+# and per-k int8 scales); checked against the oracle on the small model.
+
+def _small_dims():
+    from helpers import SMALL
+    return SMALL
+
+
+@pytest.mark.parametrize("int8", [False, True])
+def test_large_tile_step_matches_oracle(dev, int8):
+    d = _small_dims()
+    print(f"case: small model, B4 S256 (T=1024), int8={int8}", flush=True)
+    W, ad, tok, tgt, qs = config_model(d, batch=4, seq_len=256, seed=1011, int8=int8)
+    loss_ref, grads_ref, _ = oracle_grads(W, ad, tok, tgt, d)
+    ctx = llmt.Context(llmt.make_dims(d), 4, 256, int8=int8)
+    try:
+        if int8:
+            _upload_i8(ctx, W, qs, dev)
+        else:
+            upload_model(ctx, W, dev)
+        ctx.lora_set("param", llmt.flatten_adapters(ad).to(dev))
+        loss = ctx.forward_backward(tok.to(dev), tgt.to(dev))
+        assert abs(loss - float(loss_ref)) < LOSS_TOL
+        errs = grad_errors(ctx.lora_get("grad"), grads_ref, d)
+        print("large-T worst", max(errs.items(), key=lambda kv: kv[1]), flush=True)
+        assert max(errs.values()) < GRAD_TOL
+    finally:
+        ctx.close()

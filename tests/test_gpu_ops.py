@@ -16,9 +16,12 @@ def _seed(s):
     return torch.Generator().manual_seed(s)
 
 
+# M >= 1024 (a multiple of 256) takes the 256 x 128 tile kernel, including
+# partial last column tiles (2064, 4144 = 4096 + 48).
 @pytest.mark.parametrize("M,N,K", [(16, 64, 64), (32, 2064, 2048), (128, 4096 + 48, 2048),
                                    (128, 2048, 6144), (64, 12288, 2048), (256, 1024, 2048),
-                                   (128, 2048, 12288), (48, 160, 320)])
+                                   (128, 2048, 12288), (48, 160, 320), (1024, 2064, 2048),
+                                   (2048, 4096 + 48, 512), (1024, 384, 4096)])
 def test_gemm_f16_matches_fp32(dev, L, M, N, K):
     g = _seed(M * 7 + N + K)
     A = torch.randn(M, K, generator=g).half()
@@ -52,9 +55,10 @@ def test_gemm_strided_operands(dev, L):
     assert (out[:, 48:] == -7.0).all()
 
 
-def test_gemm_i8_matches_dequant(dev, L):
+@pytest.mark.parametrize("M", [128, 1024])
+def test_gemm_i8_matches_dequant(dev, L, M):
     g = _seed(13)
-    M, N, K = 128, 1024, 2048
+    N, K = 1024, 2048
     A = torch.randn(M, K, generator=g).half()
     w = torch.randn(N, K, generator=g) * 0.02
     q, sc = quantize_rows(w.numpy())
