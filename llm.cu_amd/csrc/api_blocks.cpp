@@ -222,7 +222,8 @@ int llmt_attention_bwd(const void* q, const void* k, const void* v, const void* 
   float* delta = tmp.get<float>((size_t)B * nq * S);
   float* damax = tmp.get<float>(T);
   float* dkvp = tmp.get<float>((size_t)T * 2 * nq * kHeadDim);
-  TRY_ARG(delta && damax && dkvp, "llmt_attention_bwd: out of memory");
+  _Float16* dO16 = tmp.get<_Float16>((size_t)T * nq * kHeadDim);
+  TRY_ARG(delta && damax && dkvp && dO16, "llmt_attention_bwd: out of memory");
   const long long ldq = (long long)nq * kHeadDim, ldkv = (long long)nkv * kHeadDim;
   TRY_HIP(attn_delta(dout, ldq, (const _Float16*)o, ldq, nq, S, T, delta, damax, st));
   AttnArgs a{};
@@ -241,6 +242,8 @@ int llmt_attention_bwd(const void* q, const void* k, const void* v, const void* 
   a.lddo = ldq;
   a.delta = delta;
   a.damax = damax;
+  a.dO16 = dO16;
+  a.ld16 = ldq;
   a.dq = dq;
   a.ldgq = ldq;
   a.dkvp = dkvp;
@@ -272,13 +275,14 @@ int llmt_attention_block_bwd(const void* q_raw, const void* k_raw, const void* v
   float* damax = tmp.get<float>(T);
   float* dqkv = tmp.get<float>((size_t)T * NT);
   float* dkvp = tmp.get<float>((size_t)T * 2 * Q);
+  _Float16* dO16 = tmp.get<_Float16>((size_t)T * Q);
   float* dy = tmp.get<float>((size_t)T * NT);
   _Float16* g16 = tmp.get<_Float16>((size_t)T * NT);
   float* rinv = tmp.get<float>(T);
   float* cosT = tmp.get<float>((size_t)S * 64);
   float* sinT = tmp.get<float>((size_t)S * 64);
-  TRY_ARG(raw16 && qkv16 && qkraw && o16 && lse && dO && delta && damax && dqkv && dkvp && dy &&
-              g16 && rinv && cosT && sinT,
+  TRY_ARG(raw16 && qkv16 && qkraw && o16 && lse && dO && delta && damax && dqkv && dkvp && dO16 &&
+              dy && g16 && rinv && cosT && sinT,
           "llmt_attention_block_bwd: out of memory");
   // RoPE tables (src/kernels/rope.cu:15-18), angles in double rounded to fp32.
   std::vector<float> hc((size_t)S * 64), hs((size_t)S * 64);
@@ -318,6 +322,8 @@ int llmt_attention_block_bwd(const void* q_raw, const void* k_raw, const void* v
   a.lddo = Q;
   a.delta = delta;
   a.damax = damax;
+  a.dO16 = dO16;
+  a.ld16 = Q;
   a.dq = dqkv;
   a.ldgq = NT;
   a.dkvp = dkvp;

@@ -1,8 +1,9 @@
 // attn.hip — causal GQA flash attention (head_dim 128) on fp16 MFMA for
 // gfx950: forward (keeps the fp32 log-sum-exp instead of P) and a
-// deterministic backward (dK/dV per key block and query head, dQ per query
-// block, both in one launch; the query heads of a GQA group are summed by
-// the consumer in a fixed order), recomputing P from Q, K and the LSE.
+// deterministic backward in two launches (dQ per query block, which also
+// writes the scaled fp16 dO; then dK/dV per key block and query head, the
+// query heads of a GQA group summed by the consumer in a fixed order), both
+// recomputing P from Q, K and the LSE.
 //
 // Replaces the reference's naive_attn_kernel (src/kernels/lora_forward.cu:
 // 48-135, which stores P [heads, S, S] in fp32), attn_backward_kernel
@@ -16,14 +17,19 @@
 // an A fragment holds A[c][k-slot (g, i)], a B fragment B[k-slot (g, i)][c],
 // the accumulator D[4 g + v][c].  An accumulator is reused as the B operand
 // of the next product by pairing two 16-row tiles: k-slot (g, i) <-> row
-// 4 g + i of tile 2j (i < 4) or of tile 2j + 1 (i >= 4); the A operand then
-// reads the same row order from a transposed LDS copy.  Any fixed slot
-// permutation is valid as long as A and B agree.
+// 4 g + i of tile 2j (i < 4) or of tile 2j + 1 (i >= 4).  The matching A
+// operand is a column of a row-major LDS tile, read with the gfx950
+// transposing load ds_read_b64_tr_b16 (in each 16-lane group, lane l gets
+// element l % 4 of the 8-byte blocks addressed by lanes 4 e + l / 4, e = 0..3).
 //
-// Tiles: a workgroup owns NW waves x 16 rows (queries, or keys for dK/dV)
-// and iterates over 64-row tiles of the other side, staged through LDS; the
-// next tile's global loads are issued before the current tile is computed.
-// Rows and keys beyond S are zero-filled and masked, so any S works.
+// Tiles: 64 rows x 128 halves (16 KB), moved global -> LDS by buffer loads
+// with an LDS destination (16 bytes a lane) into two buffers, so tile i + 1
+// lands while tile i is computed; one barrier per tile.  No padding: the
+// 16-byte piece p of tile row r sits in slot p ^ swz(r), which keeps the
+// row-fragment reads (16 rows, one piece) and the transposed reads (8 rows,
+// two pieces per half-wave) free of bank conflicts.  Rows past S read as
+// zeros (buffer range check); causality and the sequence end are masked in
+// the diagonal / last tiles only, chosen per wave with scalar branches.
 #include <stdlib.h>
 
 #include <algorithm>
@@ -35,86 +41,102 @@ namespace llmt {
 namespace {
 
 constexpr int HD = 128;
-constexpr int BLK = 64;
-constexpr int RP = HD + 8;   // LDS pitch (halves) of a [64][128] row-major tile
-constexpr int TP = BLK + 8;  // LDS pitch (halves) of a [128][64] transposed tile
+constexpr int BLK = 64;           // rows per LDS tile
+constexpr int TILE = BLK * HD;    // halves per LDS tile
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 
+typedef short short4v __attribute__((ext_vector_type(4)));
 typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4;
+typedef __attribute__((address_space(3))) void lds_void;
 
-// A 64 x 128 fp16 tile (rows r0.., row pitch ld, rows >= nrows zero) in
-// registers: thread i of NT holds 16-byte pieces idx = i + NT j.
-template <int NT>
-struct Tile16 {
-  half8 x[1024 / NT];
-};
+__device__ __forceinline__ int swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+// Offset (halves) of halves 8 p .. 8 p + 7 of tile row r.
+__device__ __forceinline__ int toff(int r, int p) { return r * HD + ((p ^ swz(r)) << 3); }
 
-template <int NT>
-__device__ __forceinline__ void load_tile(const _Float16* __restrict__ src, long long ld, int r0,
-                                          int nrows, Tile16<NT>& t) {
-#pragma unroll
-  for (int i = 0; i < 1024 / NT; ++i) {
-    const int idx = threadIdx.x + NT * i;
-    const int row = idx >> 4, d0 = (idx & 15) * 8;
-    // branch-free: clamped load, zeroed past the end (keeps every load in flight)
-    const half8 x = *reinterpret_cast<const half8*>(src + (long long)min(r0 + row, nrows - 1) * ld + d0);
-    t.x[i] = r0 + row < nrows ? x : half8{};
-  }
+// s_waitcnt vmcnt(N), lgkmcnt/expcnt left free (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Same from fp32 with a scale (the attention dO operand).
-template <int NT>
-__device__ __forceinline__ void load_tile_f32(const float* __restrict__ src, long long ld, int r0,
-                                              int nrows, float scale, Tile16<NT>& t) {
-#pragma unroll
-  for (int i = 0; i < 1024 / NT; ++i) {
-    const int idx = threadIdx.x + NT * i;
-    const int row = idx >> 4, d0 = (idx & 15) * 8;
-    const float4* p =
-        reinterpret_cast<const float4*>(src + (long long)min(r0 + row, nrows - 1) * ld + d0);
-    const float4 a = p[0], b = p[1];
-    half8 x;
-    x[0] = (_Float16)(a.x * scale); x[1] = (_Float16)(a.y * scale);
-    x[2] = (_Float16)(a.z * scale); x[3] = (_Float16)(a.w * scale);
-    x[4] = (_Float16)(b.x * scale); x[5] = (_Float16)(b.y * scale);
-    x[6] = (_Float16)(b.z * scale); x[7] = (_Float16)(b.w * scale);
-    t.x[i] = r0 + row < nrows ? x : half8{};
-  }
+// Workgroup barrier that also keeps the compiler from moving LDS accesses
+// across it (the DMA completion is covered by the wait_vm before it).
+__device__ __forceinline__ void tile_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
-// Registers -> LDS: row-major copy `rm` (pitch RP) and/or transposed copy
-// `tr` (pitch TP).
-template <int NT>
-__device__ __forceinline__ void store_tile(const Tile16<NT>& t, _Float16* rm, _Float16* tr) {
+// DMA of 64-row tiles through buffer loads with an LDS destination: rows
+// past the end of the matrix fall outside the buffer and arrive as zeros.
+// Wave w moves the 1 KB chunks w, w + NW, ...: chunk ch holds tile rows
+// 4 ch .. 4 ch + 3; lane l fills slot l % 16 of row 4 ch + l / 16.  The
+// per-lane byte offsets are fixed for a given row pitch, so a tile costs
+// one descriptor (scalar) and 16 / NW loads a wave.
+constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format
+
+// (non-template wrappers: the host pass drops kernel stubs when templates
+// call the LDS-destination buffer load directly)
+__device__ __forceinline__ void buffer_lds16(__amdgpu_buffer_rsrc_t rs, void* lds, unsigned off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)lds, 16, off, 0, 0, 0);
+}
+__device__ __forceinline__ void buffer_lds4(__amdgpu_buffer_rsrc_t rs, void* lds, unsigned off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)lds, 4, off, 0, 0, 0);
+}
+
+template <int NW>
+struct TileDma {
+  unsigned off[16 / NW];
+  __device__ __forceinline__ void init(long long ld, int w) {
+    const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int i = 0; i < 1024 / NT; ++i) {
-    const int idx = threadIdx.x + NT * i;
-    const int row = idx >> 4, d0 = (idx & 15) * 8;
-    if (rm) *reinterpret_cast<half8*>(rm + row * RP + d0) = t.x[i];
-    if (tr) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) tr[(d0 + e) * TP + row] = t.x[i][e];
+    for (int i = 0; i < 16 / NW; ++i) {
+      const int r = 4 * (w + NW * i) + (lane >> 4);
+      off[i] = (unsigned)(r * ld * 2 + (((lane & 15) ^ swz(r)) << 4));
     }
   }
+  // Rows r0 .. r0 + 63 of `src` ([nrows, ld] fp16) into `tile`.
+  __device__ __forceinline__ void issue(const _Float16* src, long long ld, int r0, int nrows,
+                                        _Float16* tile, int w) const {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(src + (long long)r0 * ld), (short)0, (int)((long long)(nrows - r0) * ld * 2),
+        kRsrcWord3);
+#pragma unroll
+    for (int i = 0; i < 16 / NW; ++i)
+      buffer_lds16(rs, tile + (w + NW * i) * 512, off[i]);
+  }
+};
+
+// src[i0 .. i0 + 63] (fp32, zeros past n) into LDS by one wave.
+__device__ __forceinline__ void dma_vec64(const float* src, int i0, int n, float* dst) {
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(src + i0), (short)0, (n - i0) * 4, kRsrcWord3);
+  buffer_lds4(rs, dst, (threadIdx.x & 63) * 4);
 }
 
-// A fragment from a row-major LDS tile: rows m0 + c, k = 32 ks + 8 g + i.
+// Row fragment: rows m0 + c, halves 32 ks + 8 g .. + 7 (piece 4 ks + g).
 __device__ __forceinline__ half8 frag_rm(const _Float16* t, int m0, int ks, int lane) {
-  return *reinterpret_cast<const half8*>(t + (m0 + (lane & 15)) * RP + ks * 32 + (lane >> 4) * 8);
+  return *reinterpret_cast<const half8*>(t + toff(m0 + (lane & 15), 4 * ks + (lane >> 4)));
 }
 
-// A fragment from a transposed LDS tile [d][row] for the paired-accumulator
-// k-slot order: rows d0 + c, k-slots (g, i) -> row 32 j + 4 g + i (i < 4),
-// 32 j + 16 + 4 g + i - 4 (i >= 4).
+// Column fragment for the paired-accumulator k order: lane (c, g) gets
+// tile[32 j + 4 g + i][d0 + c] (i < 4) and tile[32 j + 16 + 4 g + i - 4][d0 + c].
 __device__ __forceinline__ half8 frag_tr(const _Float16* t, int d0, int j, int lane) {
-  const _Float16* p = t + (d0 + (lane & 15)) * TP + 32 * j + 4 * (lane >> 4);
-  const half4v lo = *reinterpret_cast<const half4v*>(p);
-  const half4v hi = *reinterpret_cast<const half4v*>(p + 16);
-  half8 r;
-  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
-  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
-  return r;
+  const int jl = lane & 15;
+  const int r = 32 * j + 4 * (lane >> 4) + (jl >> 2);
+  const int col = d0 + 4 * (jl & 3);
+  const int off = (col & 7);
+  const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(t + toff(r, col >> 3) + off));
+  const short4v hi =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(t + toff(r + 16, col >> 3) + off));
+  const half4v l4 = __builtin_bit_cast(half4v, lo), h4 = __builtin_bit_cast(half4v, hi);
+  half8 x;
+  x[0] = l4[0]; x[1] = l4[1]; x[2] = l4[2]; x[3] = l4[3];
+  x[4] = h4[0]; x[5] = h4[1]; x[6] = h4[2]; x[7] = h4[3];
+  return x;
 }
 
 // B fragment built from two accumulator tiles (see the file comment).
@@ -126,7 +148,7 @@ __device__ __forceinline__ half8 pair_frag(const floatx4& a, const floatx4& b) {
 }
 
 // Operand fragment straight from global memory: row `row` (zero if >= n),
-// k = 32 ks + 8 g .. + 7.
+// halves 32 ks + 8 g .. + 7.
 __device__ __forceinline__ half8 frag_global(const _Float16* base, long long ld, int row, int n,
                                              int ks, int lane) {
   const half8 x =
@@ -158,136 +180,359 @@ __device__ float batch_do_scale(const float* __restrict__ damax, int b, int S, f
 }
 
 // ---------------------------------------------------------------- forward
-// grid (ceil(S / (16 NW)), nq, B).  Wave w owns queries q0 + 16 w + c.
-template <int NW>
-__global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnArgs a) {
-  constexpr int NT = NW * 64, QB = NW * 16;
-  __shared__ __attribute__((aligned(16))) _Float16 Ks[BLK * RP];
-  __shared__ __attribute__((aligned(16))) _Float16 VT[HD * TP];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+// One 64-key tile of the online softmax for RW 16-query tiles of a wave:
+// st holds the raw scores (rows key, column query); on return the fp32
+// probabilities relative to the running max, with m, l and the output
+// accumulators rescaled.  MASK: apply causality / sequence end.
+template <int RW, bool MASK>
+__device__ __forceinline__ void softmax_tile(floatx4 (&st)[RW][4], float (&m)[RW], float (&l)[RW],
+                                             floatx4 (&ot)[RW][8], float sl2, int key0, int q0,
+                                             int S, int lane) {
   const int c = lane & 15, g = lane >> 4;
-  const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int S = a.S;
-  const int kvh = h / (a.nq / a.nkv);
-  const long long rowb = (long long)b * S;
-  const int q = qb * QB + w * 16 + c;  // this lane's query (B-operand column)
-  const float sl2 = a.sm_scale * LOG2E;
-
-  const _Float16* kbase = a.k + rowb * a.ldk + kvh * HD;
-  const _Float16* vbase = a.v + rowb * a.ldv + kvh * HD;
-  const int nkb = min((qb * QB + QB - 1) / BLK, (S - 1) / BLK) + 1;
-  Tile16<NT> tk, tv;
-  load_tile<NT>(kbase, a.ldk, 0, S, tk);
-  load_tile<NT>(vbase, a.ldv, 0, S, tv);
-  half8 qf[4];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
-    qf[ks] = frag_global(a.q + rowb * a.ldq + h * HD, a.ldq, q, S, ks, lane);
-
-  floatx4 ot[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) ot[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY, l = 0.f;
-
-  for (int kb = 0; kb < nkb; ++kb) {
-    __syncthreads();
-    store_tile<NT>(tk, Ks, nullptr);
-    store_tile<NT>(tv, nullptr, VT);
-    __syncthreads();
-    if (kb + 1 < nkb) {
-      load_tile<NT>(kbase, a.ldk, (kb + 1) * BLK, S, tk);
-      load_tile<NT>(vbase, a.ldv, (kb + 1) * BLK, S, tv);
-    }
-    floatx4 st[4];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      st[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) st[mt] = mfma16(frag_rm(Ks, mt * 16, ks, lane), qf[ks], st[mt]);
-    }
+  for (int r = 0; r < RW; ++r) {
+    const int q = q0 + 16 * r + c;
     float bm = -INFINITY;
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int key = kb * BLK + mt * 16 + 4 * g + v;
-        const float s = (key <= q && key < S) ? st[mt][v] * sl2 : -INFINITY;
-        st[mt][v] = s;
+        float s = st[r][mt][v];
+        if (MASK) {
+          const int key = key0 + mt * 16 + 4 * g + v;
+          s = (key <= q && key < S) ? s : -INFINITY;
+          st[r][mt][v] = s;
+        }
         bm = fmaxf(bm, s);
       }
     bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
     bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-    const float mn = fmaxf(m, bm);
+    const float mn = fmaxf(m[r], bm * sl2);  // sl2 > 0: max commutes with the scale
     const float mu = mn == -INFINITY ? 0.f : mn;
-    const float alpha = exp2f(m - mu);
-    m = mn;
+    const float alpha = __builtin_amdgcn_exp2f(m[r] - mu);
+    m[r] = mn;
     float ps = 0.f;
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const float p = exp2f(st[mt][v] - mu);
-        st[mt][v] = p;
+        const float p = __builtin_amdgcn_exp2f(fmaf(st[r][mt][v], sl2, -mu));
+        st[r][mt][v] = p;
         ps += p;
       }
-    l = l * alpha + ps;
+    l[r] = l[r] * alpha + ps;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) ot[dt] *= alpha;
+    for (int dt = 0; dt < 8; ++dt) ot[r][dt] *= alpha;
+  }
+}
+
+// grid (ceil(S / QB), nq, B), QB = 16 NW RW queries; blockIdx.x runs the
+// longest (last) query blocks first.  Wave w owns queries q0 + 16 r + c
+// (r < RW).  LDS: two buffers of (K tile, V tile).
+template <int NW, int RW>
+__global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnArgs a) {
+  constexpr int QB = NW * RW * 16;
+  __shared__ __attribute__((aligned(1024))) _Float16 smem[4 * TILE];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, g = lane >> 4;
+  const int qb = gridDim.x - 1 - blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int S = a.S;
+  const int kvh = h / (a.nq / a.nkv);
+  const long long rowb = (long long)b * S;
+  const int q0 = qb * QB + w * RW * 16;
+  const int qlast = min(q0 + RW * 16, S) - 1;  // last valid query of the wave
+  const float sl2 = a.sm_scale * LOG2E;
+
+  const _Float16* kbase = a.k + rowb * a.ldk + kvh * HD;
+  const _Float16* vbase = a.v + rowb * a.ldv + kvh * HD;
+  const int nkb = min((qb * QB + QB - 1) / BLK, (S - 1) / BLK) + 1;
+  TileDma<NW> dk, dv;
+  dk.init(a.ldk, w);
+  dv.init(a.ldv, w);
+  dk.issue(kbase, a.ldk, 0, S, smem, w);
+  dv.issue(vbase, a.ldv, 0, S, smem + TILE, w);
+  half8 qf[RW][4];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      qf[r][ks] = frag_global(a.q + rowb * a.ldq + h * HD, a.ldq, q0 + 16 * r + c, S, ks, lane);
+
+  floatx4 ot[RW][8];
+  float m[RW], l[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    m[r] = -INFINITY;
+    l[r] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ot[r][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  for (int kb = 0; kb < nkb; ++kb) {
+    wait_vm<0>();
+    tile_barrier();
+    if (kb + 1 < nkb) {
+      _Float16* nb = smem + ((kb + 1) & 1) * 2 * TILE;
+      dk.issue(kbase, a.ldk, (kb + 1) * BLK, S, nb, w);
+      dv.issue(vbase, a.ldv, (kb + 1) * BLK, S, nb + TILE, w);
+    }
+    if (kb * BLK > qlast) continue;  // every key after every query of the wave
+    const _Float16* Ks = smem + (kb & 1) * 2 * TILE;
+    const _Float16* Vs = Ks + TILE;
+    floatx4 st[RW][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+      for (int r = 0; r < RW; ++r) st[r][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const half8 kf = frag_rm(Ks, mt * 16, ks, lane);
+#pragma unroll
+        for (int r = 0; r < RW; ++r) st[r][mt] = mfma16(kf, qf[r][ks], st[r][mt]);
+      }
+    }
+    // keys of the tile all <= every query of the wave and < S: no mask
+    if (kb * BLK + BLK - 1 <= q0 && kb * BLK + BLK <= S)
+      softmax_tile<RW, false>(st, m, l, ot, sl2, kb * BLK, q0, S, lane);
+    else
+      softmax_tile<RW, true>(st, m, l, ot, sl2, kb * BLK, q0, S, lane);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const half8 pb = pair_frag(st[2 * j], st[2 * j + 1]);
+      half8 pb[RW];
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) ot[dt] = mfma16(frag_tr(VT, dt * 16, j, lane), pb, ot[dt]);
+      for (int r = 0; r < RW; ++r) pb[r] = pair_frag(st[r][2 * j], st[r][2 * j + 1]);
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const half8 vf = frag_tr(Vs, dt * 16, j, lane);
+#pragma unroll
+        for (int r = 0; r < RW; ++r) ot[r][dt] = mfma16(vf, pb[r], ot[r][dt]);
+      }
     }
   }
-  l += __shfl_xor(l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
-  if (q < S) {
-    const float inv = 1.0f / l;
-    _Float16* o = a.o + (rowb + q) * a.ldo + h * HD;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      half4v r;
+  for (int r = 0; r < RW; ++r) {
+    float lr = l[r];
+    lr += __shfl_xor(lr, 16, 64);
+    lr += __shfl_xor(lr, 32, 64);
+    const int q = q0 + 16 * r + c;
+    if (q < S) {
+      const float inv = 1.0f / lr;
+      _Float16* o = a.o + (rowb + q) * a.ldo + h * HD;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) r[v] = (_Float16)(ot[dt][v] * inv);
-      *reinterpret_cast<half4v*>(o + dt * 16 + 4 * g) = r;
+      for (int dt = 0; dt < 8; ++dt) {
+        half4v x;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) x[v] = (_Float16)(ot[r][dt][v] * inv);
+        *reinterpret_cast<half4v*>(o + dt * 16 + 4 * g) = x;
+      }
+      if (g == 0) a.lse[((long long)b * a.nq + h) * S + q] = (m[r] + __log2f(lr)) * LN2;
     }
-    if (g == 0) a.lse[((long long)b * a.nq + h) * S + q] = (m + __log2f(l)) * LN2;
+  }
+}
+
+// ---------------------------------------------------------------- dQ
+// dS^T for one 64-key tile: dp (rows key, column query) = dP^T in, dS^T out.
+template <int RW, bool MASK>
+__device__ __forceinline__ void ds_tile_q(const floatx4 (&pt)[RW][4], floatx4 (&dp)[RW][4],
+                                          const float (&lse2)[RW], const float (&del)[RW],
+                                          float sl2, int key0, int q0, int S, int lane) {
+  const int c = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int q = q0 + 16 * r + c;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float pv = __builtin_amdgcn_exp2f(fmaf(pt[r][mt][v], sl2, -lse2[r]));
+        if (MASK) {
+          const int key = key0 + mt * 16 + 4 * g + v;
+          pv = (key <= q && key < S && q < S) ? pv : 0.f;
+        }
+        dp[r][mt][v] = pv * (dp[r][mt][v] - del[r]);
+      }
+  }
+}
+
+// Same tiling as the forward.  Also writes dO * gs in fp16 (gs the batch's
+// power-of-two dO scale) to a.dO16 for the dK/dV launch.
+template <int NW, int RW>
+__global__ __launch_bounds__(NW * 64) void attn_dq_kernel(const AttnArgs a) {
+  constexpr int NT = NW * 64, QB = NW * RW * 16;
+  __shared__ __attribute__((aligned(1024))) _Float16 smem[4 * TILE];
+  __shared__ float red[NW];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, g = lane >> 4;
+  const int qb = gridDim.x - 1 - blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int S = a.S;
+  const int kvh = h / (a.nq / a.nkv);
+  const long long rowb = (long long)b * S;
+  const int q0 = qb * QB + w * RW * 16;
+  const int qlast = min(q0 + RW * 16, S) - 1;
+  const float sl2 = a.sm_scale * LOG2E;
+  const _Float16* kbase = a.k + rowb * a.ldk + kvh * HD;
+  const _Float16* vbase = a.v + rowb * a.ldv + kvh * HD;
+  const int nkb = min((qb * QB + QB - 1) / BLK, (S - 1) / BLK) + 1;
+  TileDma<NW> dk, dv;
+  dk.init(a.ldk, w);
+  dv.init(a.ldv, w);
+  dk.issue(kbase, a.ldk, 0, S, smem, w);
+  dv.issue(vbase, a.ldv, 0, S, smem + TILE, w);
+  const float gs = batch_do_scale<NT>(a.damax, b, S, red);
+
+  half8 qf[RW][4], df[RW][4];
+  float lse2[RW], del[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int q = q0 + 16 * r + c;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      qf[r][ks] = frag_global(a.q + rowb * a.ldq + h * HD, a.ldq, q, S, ks, lane);
+      df[r][ks] = frag_global_f32(a.dO + rowb * a.lddo + h * HD, a.lddo, q, S, ks, lane, gs);
+    }
+    const bool ok = q < S;
+    if (ok) {
+      _Float16* d16 = a.dO16 + (rowb + q) * a.ld16 + h * HD + (lane >> 4) * 8;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) *reinterpret_cast<half8*>(d16 + ks * 32) = df[r][ks];
+    }
+    lse2[r] = ok ? a.lse[((long long)b * a.nq + h) * S + q] * LOG2E : 0.f;
+    del[r] = ok ? a.delta[((long long)b * a.nq + h) * S + q] * gs : 0.f;
+  }
+  floatx4 dqT[RW][8];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dqT[r][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  for (int kb = 0; kb < nkb; ++kb) {
+    wait_vm<0>();
+    tile_barrier();
+    if (kb + 1 < nkb) {
+      _Float16* nb = smem + ((kb + 1) & 1) * 2 * TILE;
+      dk.issue(kbase, a.ldk, (kb + 1) * BLK, S, nb, w);
+      dv.issue(vbase, a.ldv, (kb + 1) * BLK, S, nb + TILE, w);
+    }
+    if (kb * BLK > qlast) continue;
+    const _Float16* Ks = smem + (kb & 1) * 2 * TILE;
+    const _Float16* Vs = Ks + TILE;
+    floatx4 pt[RW][4], dp[RW][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        pt[r][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+        dp[r][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const half8 kf = frag_rm(Ks, mt * 16, ks, lane);
+        const half8 vf = frag_rm(Vs, mt * 16, ks, lane);
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+          pt[r][mt] = mfma16(kf, qf[r][ks], pt[r][mt]);
+          dp[r][mt] = mfma16(vf, df[r][ks], dp[r][mt]);
+        }
+      }
+    }
+    if (kb * BLK + BLK - 1 <= q0 && kb * BLK + BLK <= S && qlast == q0 + RW * 16 - 1)
+      ds_tile_q<RW, false>(pt, dp, lse2, del, sl2, kb * BLK, q0, S, lane);
+    else
+      ds_tile_q<RW, true>(pt, dp, lse2, del, sl2, kb * BLK, q0, S, lane);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      half8 db[RW];
+#pragma unroll
+      for (int r = 0; r < RW; ++r) db[r] = pair_frag(dp[r][2 * j], dp[r][2 * j + 1]);
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        const half8 kt = frag_tr(Ks, d * 16, j, lane);
+#pragma unroll
+        for (int r = 0; r < RW; ++r) dqT[r][d] = mfma16(kt, db[r], dqT[r][d]);
+      }
+    }
+  }
+  const float f = a.sm_scale / gs;
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int q = q0 + 16 * r + c;
+    if (q < S) {
+      float* dq = a.dq + (rowb + q) * a.ldgq + h * HD;
+#pragma unroll
+      for (int d = 0; d < 8; ++d)
+        *reinterpret_cast<float4*>(dq + d * 16 + 4 * g) =
+            make_float4(dqT[r][d][0] * f, dqT[r][d][1] * f, dqT[r][d][2] * f, dqT[r][d][3] * f);
+    }
   }
 }
 
 // ---------------------------------------------------------------- dK, dV
-// Workgroup (key block kb of 16 NW keys, query head h): wave w owns keys
-// k0 + 16 w + c; loops over the 64-query tiles at or after the block.
-// Writes this query head's share of dK, dV (fp32) to a.dkvp.
+// P and dS for one 64-query tile (rows query, column key).
+template <bool MASK>
+__device__ __forceinline__ void ds_tile_kv(floatx4 (&p)[4], floatx4 (&ds)[4], const float* lse_s,
+                                           const float* del_s, float sl2, float gs, int qq0, int key,
+                                           int S, int lane) {
+  const int g = lane >> 4;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const float4 ls = *reinterpret_cast<const float4*>(lse_s + mt * 16 + 4 * g);
+    const float4 dl = *reinterpret_cast<const float4*>(del_s + mt * 16 + 4 * g);
+    const float lv[4] = {ls.x, ls.y, ls.z, ls.w};
+    const float dv[4] = {dl.x, dl.y, dl.z, dl.w};
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float pv = __builtin_amdgcn_exp2f(fmaf(p[mt][v], sl2, -lv[v] * LOG2E));
+      if (MASK) {
+        const int qq = qq0 + mt * 16 + 4 * g + v;
+        pv = (key <= qq && qq < S) ? pv : 0.f;
+      }
+      p[mt][v] = pv;
+      ds[mt][v] = pv * fmaf(-dv[v], gs, ds[mt][v]);
+    }
+  }
+}
+
+// grid (ceil(S / (16 NW)), nq, B): workgroup (key block kb of 16 NW keys,
+// query head h); wave w owns keys k0 + 16 w + c and loops over the 64-query
+// tiles at or after the block.  LDS: two buffers of (Q tile, dO16 tile,
+// lse[64], delta[64]).  Writes this query head's share of dK, dV (fp32) to
+// a.dkvp.
 template <int NW>
-__device__ void attn_dkdv(const AttnArgs& a, int kb, int h, int b, char* smem) {
+__global__ __launch_bounds__(NW * 64) void attn_dkdv_kernel(const AttnArgs a) {
   constexpr int NT = NW * 64, KB = NW * 16;
-  _Float16* Qs = reinterpret_cast<_Float16*>(smem);
-  _Float16* QT = Qs + BLK * RP;
-  _Float16* Ds = QT + HD * TP;
-  _Float16* DT = Ds + BLK * RP;
-  float* lse_s = reinterpret_cast<float*>(DT + HD * TP);
-  float* del_s = lse_s + BLK;
-  float* red = del_s + BLK;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  constexpr int BUF = 2 * TILE + 2 * BLK * 2;  // halves per buffer
+  __shared__ __attribute__((aligned(1024))) _Float16 smem[2 * BUF];
+  __shared__ float red[NW];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, g = lane >> 4;
+  const int kb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int S = a.S;
   const int kvh = h / (a.nq / a.nkv);
   const long long rowb = (long long)b * S;
-  const int key = kb * KB + w * 16 + c;
+  const int k0 = kb * KB + w * 16;  // first key of the wave
+  const int key = k0 + c;
   const float sl2 = a.sm_scale * LOG2E;
   const float* lse_h = a.lse + ((long long)b * a.nq + h) * S;
   const float* del_h = a.delta + ((long long)b * a.nq + h) * S;
   const _Float16* qbase = a.q + rowb * a.ldq + h * HD;
-  const float* dbase = a.dO + rowb * a.lddo + h * HD;
+  const _Float16* dbase = a.dO16 + rowb * a.ld16 + h * HD;
   const int qb0 = (kb * KB) / BLK;
   const int nqb = (S + BLK - 1) / BLK;
+  TileDma<NW> dq_, dd_;
+  dq_.init(a.ldq, w);
+  dd_.init(a.ld16, w);
+  auto issue = [&](int qb, _Float16* buf) {
+    dq_.issue(qbase, a.ldq, qb * BLK, S, buf, w);
+    dd_.issue(dbase, a.ld16, qb * BLK, S, buf + TILE, w);
+    float* vec = reinterpret_cast<float*>(buf + 2 * TILE);
+    if (w == 0) dma_vec64(lse_h, qb * BLK, S, vec);
+    if (w == NW - 1) dma_vec64(del_h, qb * BLK, S, vec + BLK);
+  };
+  issue(qb0, smem);
   const float gs = batch_do_scale<NT>(a.damax, b, S, red);
-
-  Tile16<NT> tq, td;
-  load_tile<NT>(qbase, a.ldq, qb0 * BLK, S, tq);
-  load_tile_f32<NT>(dbase, a.lddo, qb0 * BLK, S, gs, td);
   half8 kf[4], vf[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
@@ -301,19 +546,15 @@ __device__ void attn_dkdv(const AttnArgs& a, int kb, int h, int b, char* smem) {
     dvT[i] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
   for (int qb = qb0; qb < nqb; ++qb) {
-    __syncthreads();
-    store_tile<NT>(tq, Qs, QT);
-    store_tile<NT>(td, Ds, DT);
-    for (int i = threadIdx.x; i < BLK; i += NT) {
-      const int qq = qb * BLK + i;
-      lse_s[i] = qq < S ? lse_h[qq] * LOG2E : 0.f;
-      del_s[i] = qq < S ? del_h[qq] * gs : 0.f;
-    }
-    __syncthreads();
-    if (qb + 1 < nqb) {
-      load_tile<NT>(qbase, a.ldq, (qb + 1) * BLK, S, tq);
-      load_tile_f32<NT>(dbase, a.lddo, (qb + 1) * BLK, S, gs, td);
-    }
+    wait_vm<0>();
+    tile_barrier();
+    if (qb + 1 < nqb) issue(qb + 1, smem + ((qb + 1 - qb0) & 1) * BUF);
+    const _Float16* buf = smem + ((qb - qb0) & 1) * BUF;
+    if (qb * BLK + BLK - 1 < k0) continue;  // every query before every key of the wave
+    const _Float16* Qs = buf;
+    const _Float16* Ds = buf + TILE;
+    const float* lse_s = reinterpret_cast<const float*>(buf + 2 * TILE);
+    const float* del_s = lse_s + BLK;
     floatx4 p[4], ds[4];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
@@ -325,141 +566,36 @@ __device__ void attn_dkdv(const AttnArgs& a, int kb, int h, int b, char* smem) {
         ds[mt] = mfma16(frag_rm(Ds, mt * 16, ks, lane), vf[ks], ds[mt]);
       }
     }
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int ql = mt * 16 + 4 * g + v;
-        const int qq = qb * BLK + ql;
-        const bool ok = key <= qq && qq < S && key < S;
-        const float pv = ok ? exp2f(p[mt][v] * sl2 - lse_s[ql]) : 0.f;
-        p[mt][v] = pv;
-        ds[mt][v] = pv * (ds[mt][v] - del_s[ql]);
-      }
+    // every query of the tile >= every key of the wave and < S: no mask
+    if (qb * BLK >= k0 + 15 && qb * BLK + BLK <= S)
+      ds_tile_kv<false>(p, ds, lse_s, del_s, sl2, gs, qb * BLK, key, S, lane);
+    else
+      ds_tile_kv<true>(p, ds, lse_s, del_s, sl2, gs, qb * BLK, key, S, lane);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const half8 pb = pair_frag(p[2 * j], p[2 * j + 1]);
       const half8 db = pair_frag(ds[2 * j], ds[2 * j + 1]);
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        dvT[dt] = mfma16(frag_tr(DT, dt * 16, j, lane), pb, dvT[dt]);
-        dkT[dt] = mfma16(frag_tr(QT, dt * 16, j, lane), db, dkT[dt]);
+        dvT[dt] = mfma16(frag_tr(Ds, dt * 16, j, lane), pb, dvT[dt]);
+        dkT[dt] = mfma16(frag_tr(Qs, dt * 16, j, lane), db, dkT[dt]);
       }
     }
   }
   if (key < S) {
     const float inv = 1.0f / gs;
+    const float fk = a.sm_scale * inv;
     const long long ldp = 2LL * a.nq * HD;
     float* dk = a.dkvp + (rowb + key) * ldp + h * HD;
     float* dv = a.dkvp + (rowb + key) * ldp + (a.nq + h) * HD;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       *reinterpret_cast<float4*>(dk + dt * 16 + 4 * g) =
-          make_float4(dkT[dt][0] * a.sm_scale * inv, dkT[dt][1] * a.sm_scale * inv,
-                      dkT[dt][2] * a.sm_scale * inv, dkT[dt][3] * a.sm_scale * inv);
+          make_float4(dkT[dt][0] * fk, dkT[dt][1] * fk, dkT[dt][2] * fk, dkT[dt][3] * fk);
       *reinterpret_cast<float4*>(dv + dt * 16 + 4 * g) =
           make_float4(dvT[dt][0] * inv, dvT[dt][1] * inv, dvT[dt][2] * inv, dvT[dt][3] * inv);
     }
   }
-}
-
-// ---------------------------------------------------------------- dQ
-// Workgroup (query block qb of 16 NW queries, head h): wave w owns queries
-// q0 + 16 w + c.
-template <int NW>
-__device__ void attn_dq(const AttnArgs& a, int qb, int h, int b, char* smem) {
-  constexpr int NT = NW * 64, QB = NW * 16;
-  _Float16* Ks = reinterpret_cast<_Float16*>(smem);
-  _Float16* Vs = Ks + BLK * RP;
-  _Float16* KT = Vs + BLK * RP;
-  float* red = reinterpret_cast<float*>(KT + HD * TP);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int c = lane & 15, g = lane >> 4;
-  const int S = a.S;
-  const int kvh = h / (a.nq / a.nkv);
-  const long long rowb = (long long)b * S;
-  const int q = qb * QB + w * 16 + c;
-  const float sl2 = a.sm_scale * LOG2E;
-  const _Float16* kbase = a.k + rowb * a.ldk + kvh * HD;
-  const _Float16* vbase = a.v + rowb * a.ldv + kvh * HD;
-  const int nkb = min((qb * QB + QB - 1) / BLK, (S - 1) / BLK) + 1;
-  Tile16<NT> tk, tv;
-  load_tile<NT>(kbase, a.ldk, 0, S, tk);
-  load_tile<NT>(vbase, a.ldv, 0, S, tv);
-  const float gs = batch_do_scale<NT>(a.damax, b, S, red);
-
-  half8 qf[4], df[4];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    qf[ks] = frag_global(a.q + rowb * a.ldq + h * HD, a.ldq, q, S, ks, lane);
-    df[ks] = frag_global_f32(a.dO + rowb * a.lddo + h * HD, a.lddo, q, S, ks, lane, gs);
-  }
-  const bool qok = q < S;
-  const float lse2 = qok ? a.lse[((long long)b * a.nq + h) * S + q] * LOG2E : 0.f;
-  const float del = qok ? a.delta[((long long)b * a.nq + h) * S + q] * gs : 0.f;
-  floatx4 dqT[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) dqT[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-  for (int kb = 0; kb < nkb; ++kb) {
-    __syncthreads();
-    store_tile<NT>(tk, Ks, KT);
-    store_tile<NT>(tv, Vs, nullptr);
-    __syncthreads();
-    if (kb + 1 < nkb) {
-      load_tile<NT>(kbase, a.ldk, (kb + 1) * BLK, S, tk);
-      load_tile<NT>(vbase, a.ldv, (kb + 1) * BLK, S, tv);
-    }
-    floatx4 pt[4], dt_[4];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      pt[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
-      dt_[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        pt[mt] = mfma16(frag_rm(Ks, mt * 16, ks, lane), qf[ks], pt[mt]);
-        dt_[mt] = mfma16(frag_rm(Vs, mt * 16, ks, lane), df[ks], dt_[mt]);
-      }
-    }
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int key = kb * BLK + mt * 16 + 4 * g + v;
-        const bool ok = key <= q && key < S && qok;
-        const float pv = ok ? exp2f(pt[mt][v] * sl2 - lse2) : 0.f;
-        dt_[mt][v] = pv * (dt_[mt][v] - del);
-      }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const half8 db = pair_frag(dt_[2 * j], dt_[2 * j + 1]);
-#pragma unroll
-      for (int d = 0; d < 8; ++d) dqT[d] = mfma16(frag_tr(KT, d * 16, j, lane), db, dqT[d]);
-    }
-  }
-  if (qok) {
-    const float f = a.sm_scale / gs;
-    float* dq = a.dq + (rowb + q) * a.ldgq + h * HD;
-#pragma unroll
-    for (int d = 0; d < 8; ++d)
-      *reinterpret_cast<float4*>(dq + d * 16 + 4 * g) =
-          make_float4(dqT[d][0] * f, dqT[d][1] * f, dqT[d][2] * f, dqT[d][3] * f);
-  }
-}
-
-constexpr size_t kDkdvLds = (size_t)(2 * BLK * RP + 2 * HD * TP) * 2 + (2 * BLK + 16) * 4;
-constexpr size_t kDqLds = (size_t)(2 * BLK * RP + HD * TP) * 2 + 16 * 4;
-
-// One launch for both backward halves: blockIdx.x < nkb_blocks are dK/dV
-// workgroups (key block, query head), the rest dQ workgroups.
-template <int NW>
-__global__ __launch_bounds__(NW * 64) void attn_bwd_kernel(const AttnArgs a, int n_kv_blocks) {
-  __shared__ __attribute__((aligned(16))) char smem[kDkdvLds > kDqLds ? kDkdvLds : kDqLds];
-  const int h = blockIdx.y, b = blockIdx.z;
-  if ((int)blockIdx.x < n_kv_blocks)
-    attn_dkdv<NW>(a, blockIdx.x, h, b, smem);
-  else
-    attn_dq<NW>(a, blockIdx.x - n_kv_blocks, h, b, smem);
 }
 
 // dK, dV = sum over the query heads of each group of the per-head shares
@@ -508,14 +644,44 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(const float* __restrict
   if (threadIdx.x == 0) damax[t] = amax;
 }
 
-// Waves per workgroup (16 query or key rows each).  Four measured fastest on
-// MI355X at S = 128 as well as at S = 2048 (fewer, longer workgroups beat more
-// single-wave ones); LLMT_ATTN_FWD_WAVES / LLMT_ATTN_BWD_WAVES = 1, 2 or 4
-// override it for tuning.
-int attn_waves(const char* env) {
-  const char* e = getenv(env);
-  if (e && (e[0] == '1' || e[0] == '2' || e[0] == '4') && !e[1]) return e[0] - '0';
-  return 4;
+// Launch shape: NW waves of RW 16-row tiles.  Two tiles a wave halve the LDS
+// operand reads per MFMA; fewer, smaller workgroups keep short sequences
+// spread over the CUs.  LLMT_ATTN_CFG = "NW,RW" (NW 2 or 4, RW 1 or 2)
+// overrides the forward / dQ shape for tuning.
+struct AttnShape {
+  int nw, rw;
+};
+AttnShape attn_shape(int B, int S, int nq) {
+  const char* e = getenv("LLMT_ATTN_CFG");
+  if (e && (e[0] == '2' || e[0] == '4') && e[1] == ',' && (e[2] == '1' || e[2] == '2') && !e[3])
+    return {e[0] - '0', e[2] - '0'};
+  const long long heads = (long long)B * nq;
+  if (heads * ((S + 127) / 128) >= 512) return {4, 2};
+  if (heads * ((S + 63) / 64) >= 256) return {4, 1};
+  return {2, 1};
+}
+int dkdv_waves(int B, int S, int nq) {
+  const char* e = getenv("LLMT_ATTN_DKDV_WAVES");
+  if (e && (e[0] == '2' || e[0] == '4') && !e[1]) return e[0] - '0';
+  return (long long)B * nq * ((S + 63) / 64) >= 256 ? 4 : 2;
+}
+
+template <int NW, int RW>
+void launch_fwd(const AttnArgs& a, int B, hipStream_t st) {
+  constexpr int QB = NW * RW * 16;
+  hipLaunchKernelGGL((attn_fwd_kernel<NW, RW>), dim3((a.S + QB - 1) / QB, a.nq, B), dim3(NW * 64),
+                     0, st, a);
+}
+template <int NW, int RW>
+void launch_dq(const AttnArgs& a, int B, hipStream_t st) {
+  constexpr int QB = NW * RW * 16;
+  hipLaunchKernelGGL((attn_dq_kernel<NW, RW>), dim3((a.S + QB - 1) / QB, a.nq, B), dim3(NW * 64),
+                     0, st, a);
+}
+template <int NW>
+void launch_dkdv(const AttnArgs& a, int B, hipStream_t st) {
+  hipLaunchKernelGGL((attn_dkdv_kernel<NW>), dim3((a.S + NW * 16 - 1) / (NW * 16), a.nq, B),
+                     dim3(NW * 64), 0, st, a);
 }
 
 }  // namespace
@@ -528,43 +694,40 @@ hipError_t attn_delta(const float* dO, long long ldd, const _Float16* o, long lo
   return hipSuccess;
 }
 
-template <int NW>
-static void launch_fwd(const AttnArgs& a, int B, hipStream_t st) {
-  dim3 grid((a.S + NW * 16 - 1) / (NW * 16), a.nq, B);
-  hipLaunchKernelGGL(attn_fwd_kernel<NW>, grid, dim3(NW * 64), 0, st, a);
-}
-
-template <int NW>
-static void launch_bwd(const AttnArgs& a, int B, hipStream_t st) {
-  const int nkvb = (a.S + NW * 16 - 1) / (NW * 16);
-  dim3 grid(2 * nkvb, a.nq, B);
-  hipLaunchKernelGGL(attn_bwd_kernel<NW>, grid, dim3(NW * 64), 0, st, a, nkvb);
-}
-
 hipError_t attn_fwd(const AttnArgs& a, int B, hipStream_t st) {
   if (a.nq % a.nkv || a.S <= 0) {
     set_error("attn_fwd: nq=%d nkv=%d S=%d", a.nq, a.nkv, a.S);
     return hipErrorInvalidValue;
   }
-  switch (attn_waves("LLMT_ATTN_FWD_WAVES")) {
-    case 1: launch_fwd<1>(a, B, st); break;
-    case 2: launch_fwd<2>(a, B, st); break;
-    default: launch_fwd<4>(a, B, st); break;
+  const AttnShape s = attn_shape(B, a.S, a.nq);
+  switch (s.nw * 10 + s.rw) {
+    case 42: launch_fwd<4, 2>(a, B, st); break;
+    case 41: launch_fwd<4, 1>(a, B, st); break;
+    case 22: launch_fwd<2, 2>(a, B, st); break;
+    default: launch_fwd<2, 1>(a, B, st); break;
   }
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
 
 hipError_t attn_bwd(const AttnArgs& a, int B, hipStream_t st) {
-  if (a.nq % a.nkv || a.S <= 0 || !a.dkvp) {
-    set_error("attn_bwd: nq=%d nkv=%d S=%d (dK/dV share buffer required)", a.nq, a.nkv, a.S);
+  if (a.nq % a.nkv || a.S <= 0 || !a.dkvp || !a.dO16) {
+    set_error("attn_bwd: nq=%d nkv=%d S=%d (dK/dV share and fp16 dO buffers required)", a.nq,
+              a.nkv, a.S);
     return hipErrorInvalidValue;
   }
-  switch (attn_waves("LLMT_ATTN_BWD_WAVES")) {
-    case 1: launch_bwd<1>(a, B, st); break;
-    case 2: launch_bwd<2>(a, B, st); break;
-    default: launch_bwd<4>(a, B, st); break;
+  const AttnShape s = attn_shape(B, a.S, a.nq);
+  switch (s.nw * 10 + s.rw) {
+    case 42: launch_dq<4, 2>(a, B, st); break;
+    case 41: launch_dq<4, 1>(a, B, st); break;
+    case 22: launch_dq<2, 2>(a, B, st); break;
+    default: launch_dq<2, 1>(a, B, st); break;
   }
+  LLMT_LAUNCH_CHECK();
+  if (dkdv_waves(B, a.S, a.nq) == 4)
+    launch_dkdv<4>(a, B, st);
+  else
+    launch_dkdv<2>(a, B, st);
   LLMT_LAUNCH_CHECK();
   if (a.dk && a.dv) {
     const long long n = (long long)B * a.S * a.nkv * HD;

@@ -192,6 +192,7 @@ int Ctx::init() {
   TRY_PTR(damax = alloc_n<float>(T));
   TRY_PTR(dqkv32 = alloc_n<float>(T * NT));
   TRY_PTR(dkvp = alloc_n<float>((size_t)T * 2 * Q));
+  TRY_PTR(dO16 = alloc_n<_Float16>((size_t)T * Q));
   TRY_PTR(dy32_all = alloc_n<float>((size_t)L * T * NT));
   TRY_PTR(dh_all = alloc_n<float>((size_t)L * T * 64));
   // adapter-gradient jobs (src/kernels/lora_backward.cu:50-90): per layer

@@ -129,6 +129,7 @@ struct Ctx {
   LoraGradPlan lora_plan{};
   hipError_t lora_grads(int l0, int nl, int B, int accumulate);
   float* dkvp = nullptr;  // [T, 2 Q]: per-query-head dK | dV shares
+  _Float16* dO16 = nullptr;  // [T, Q]: scaled fp16 dO of the attention backward
 
   // graph + profiling
   bool use_graph = false;

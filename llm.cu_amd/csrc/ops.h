@@ -211,6 +211,8 @@ struct AttnArgs {
   long long lddo;
   const float* delta;   // [B, nq, S] rowsum(dO * O)
   const float* damax;   // [T] max |dO| per row
+  _Float16* dO16;       // backward scratch: dO times the batch's power-of-two
+  long long ld16;       //   scale, fp16 [T, ld16] (written by the dQ launch)
   float* dq;            // fp32 [T, ldgq]
   long long ldgq;
   float* dkvp;          // [T, 2 nq 128]: each query head's share of dK | dV

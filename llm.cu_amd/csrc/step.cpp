@@ -262,6 +262,8 @@ AttnArgs Ctx::attn_args(const Stash& s) const {
   a.lddo = Q;
   a.delta = delta;
   a.damax = damax;
+  a.dO16 = dO16;
+  a.ld16 = Q;
   a.dq = dqkv32;
   a.ldgq = NT;
   a.dkvp = dkvp;

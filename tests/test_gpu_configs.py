@@ -299,6 +299,30 @@ def test_attention_fwd_bwd(dev, B, S, nq, nkv):
         assert rel_l2(got.cpu(), want) < GRAD_TOL
 
 
+@pytest.mark.parametrize("cfg,dkdv", [("2,1", "2"), ("2,2", "4"), ("4,1", "4"), ("4,2", "2")])
+@pytest.mark.parametrize("B,S,nq,nkv", [(1, 200, 4, 2), (2, 128, 2, 1)])
+def test_attention_launch_shapes(dev, monkeypatch, cfg, dkdv, B, S, nq, nkv):
+    """Every workgroup shape of the attention kernels (waves x 16-row tiles
+    per wave for the forward and dQ, waves for dK/dV) against the oracle."""
+    monkeypatch.setenv("LLMT_ATTN_CFG", cfg)
+    monkeypatch.setenv("LLMT_ATTN_DKDV_WAVES", dkdv)
+    print(f"case: attention shape {cfg}/{dkdv} B{B} S{S} nq{nq} nkv{nkv}", flush=True)
+    g = torch.Generator().manual_seed(7 * S + nq)
+    q = torch.randn(B, S, nq, 128, generator=g).half()
+    k = torch.randn(B, S, nkv, 128, generator=g).half()
+    v = torch.randn(B, S, nkv, 128, generator=g).half()
+    do = torch.randn(B, S, nq, 128, generator=g)
+    o_ref, lse_ref = ref.attention_fwd(q.float(), k.float(), v.float())
+    o, lse = llmt.attention_fwd(q.to(dev), k.to(dev), v.to(dev))
+    assert rel_l2(o.float().cpu(), o_ref) < 2e-3
+    assert (lse.cpu() - lse_ref).abs().max() < 1e-3
+    dq_ref, dk_ref, dv_ref = ref.attention_bwd(do, q.float(), k.float(), v.float(),
+                                               o.float().cpu(), lse.cpu())
+    dq, dk, dv = llmt.attention_bwd(q.to(dev), k.to(dev), v.to(dev), o, lse, do.to(dev))
+    for got, want in ((dq, dq_ref), (dk, dk_ref), (dv, dv_ref)):
+        assert rel_l2(got.cpu(), want) < GRAD_TOL
+
+
 # ------------------------------------------------------------------ C4 (int8 weights)
 
 def _upload_i8(ctx, W, qs, dev):
