@@ -713,6 +713,158 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
   }
 }
 
+// Skinny fp16 kernel fed by DMA (the T = 128 training step): a 128 x BN
+// output tile (BN = 16 NB) per workgroup of four waves (wave w: rows
+// 32 w .. 32 w + 31, all BN columns), K split over blockIdx.y in 64-wide
+// stages.  Both operands move global -> LDS with buffer loads that have an
+// LDS destination, 16 bytes a lane: A as 128-byte row pieces (8 lanes a row,
+// so each stage touches every A cache line once; the 16-byte pieces are
+// XOR-swizzled by row so the fragment reads are bank-conflict free), B as
+// the two consecutive 1 KB fragments of each fragment-packed row block (one
+// wave-uniform descriptor per row block; the stage offset is a scalar).  An
+// S-stage ring (A 16 KB + B 2 NB KB a stage) keeps S - 1 stages in flight.
+// Stage c is waited for with an explicit vmcnt (the loads of later stages
+// stay in flight) and a plain barrier; the last S - 1 stages wait for all.
+// Measured on MI355X (per-workgroup timestamps, C2 shapes): the partial
+// tiles and the first round trip, not the MFMA work, set the cost at this M;
+// A pieces of a whole cache line cut the first-data latency.  Columns past N
+// load row block 0 of the first segment (in bounds) and are not stored.
+constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ void buffer_lds16(__amdgpu_buffer_rsrc_t rs, void* lds, unsigned voff,
+                                             unsigned soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)lds, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kRsrcWord3);
+}
+// slot of 16-byte piece p (0..7) of A row r in a stage
+__device__ __forceinline__ int a_slot(int r, int p) { return p ^ ((r >> 1) & 7); }
+
+template <int S, int NB>
+__global__ __launch_bounds__(256) void gemm_skinny_kernel(const GemmArgs g) {
+  constexpr int AB = 16384;                  // A bytes per stage
+  constexpr int SB = AB + NB * 2048;         // bytes per stage
+  constexpr int BPW = NB >= 4 ? NB / 4 : 1;  // B row blocks a loading wave moves
+  constexpr int BW = NB >= 4 ? 4 : NB;       // waves that move B
+  __shared__ __attribute__((aligned(1024))) char smem[S * SB];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n0 = blockIdx.x * (NB * 16), m0 = blockIdx.z * 128;
+  const int ksteps = g.K / KSTEP;
+  const int nst = g.K / 64;
+  const int c0 = (int)((long long)blockIdx.y * nst / g.split);
+  const int c1 = (int)((long long)(blockIdx.y + 1) * nst / g.split);
+
+  // A: wave w moves rows 32 w .. 32 w + 31 (four 1 KB pieces of 8 rows)
+  const __amdgpu_buffer_rsrc_t ars =
+      make_rsrc(g.A + (long long)m0 * g.lda, (unsigned)(128u * g.lda * 2u));
+  unsigned aoff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 8 * (4 * wave + i) + (lane >> 3);
+    aoff[i] = (unsigned)((r * g.lda + a_slot(r, lane & 7) * 8) * 2);
+  }
+  __amdgpu_buffer_rsrc_t brs[BPW];
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) {
+    const int nn = n0 + 16 * (wave * BPW + i);
+    int s = 0;
+#pragma unroll
+    for (int q = 1; q < 4; ++q)
+      if (q < g.nseg && nn >= g.seg_start[q]) s = q;
+    const long long rb16 = nn < g.N ? (nn - g.seg_start[s]) >> 4 : 0;
+    brs[i] = make_rsrc((const _Float16*)g.seg[s].ptr + rb16 * ksteps * 512, (unsigned)(ksteps * 1024u));
+  }
+  const bool bwave = wave < BW;
+  auto issue = [&](int c) LLMT_INLINE {
+    char* st = smem + (c % S) * SB;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) buffer_lds16(ars, st + (4 * wave + i) * 1024, aoff[i], c * 128u);
+    if (bwave) {
+#pragma unroll
+      for (int i = 0; i < BPW; ++i)
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+          buffer_lds16(brs[i], st + AB + ((wave * BPW + i) * 2 + q) * 1024, lane * 16u + q * 1024u,
+                       c * 2048u);
+    }
+  };
+  // stage c complete: only the later stages' loads may be pending
+  auto wait_stage = [&]() LLMT_INLINE {
+    if (bwave)
+      wait_vm<(S - 2) * (4 + 2 * BPW)>();
+    else
+      wait_vm<(S - 2) * 4>();
+  };
+  // A fragment reads: row 16 f + c of the stage, k-step q, halves 8 g..
+  int aread[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = 16 * (2 * wave + i) + (lane & 15);
+    aread[i] = r * 128;
+  }
+  const int arow0 = 16 * (2 * wave) + (lane & 15);
+
+  floatx4 acc[2][NB];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  for (int c = c0; c < c1 && c < c0 + S - 1; ++c) issue(c);
+  for (int c = c0; c < c1; ++c) {
+    if (c + S - 1 < c1) {
+      wait_stage();
+      __builtin_amdgcn_s_barrier();
+      issue(c + S - 1);
+    } else {
+      wait_vm<0>();
+      __builtin_amdgcn_s_barrier();
+    }
+    asm volatile("" ::: "memory");
+    const char* st = smem + (c % S) * SB;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      half8 a[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int r = arow0 + 16 * i;
+        a[i] = *reinterpret_cast<const half8*>(st + aread[i] + a_slot(r, 4 * q + (lane >> 4)) * 16);
+      }
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const half8 b = *reinterpret_cast<const half8*>(st + AB + (j * 2 + q) * 1024 + lane * 16);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) acc[i][j] = mfma16(a[i], b, acc[i][j]);
+      }
+    }
+    asm volatile("" ::: "memory");
+  }
+
+  float* C = g.C + (long long)blockIdx.y * g.split_stride;
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int nn = n0 + 16 * j;
+    if (nn >= g.N) continue;
+    int s = 0;
+#pragma unroll
+    for (int q = 1; q < 4; ++q)
+      if (q < g.nseg && nn >= g.seg_start[q]) s = q;
+    const _Float16* cs = g.seg[s].colscale;
+    const int col = nn + (lane & 15);
+    const float sc = cs ? (float)cs[col - g.seg_start[s]] : 1.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = m0 + (2 * wave + i) * 16 + (lane >> 4) * 4 + v;
+        C[(long long)row * g.ldc + col] = acc[i][j][v] * sc;
+      }
+  }
+}
+
 template <int MF, int NF, int NW, int CHS, int RING, int ADIST>
 hipError_t launch_cfg(const GemmArgs& g, hipStream_t st) {
   const int ncols = NW * NF * 16;
@@ -1007,7 +1159,14 @@ void gemm_finalize_segments(GemmArgs& g) {
 // per CU (tunable with LLMT_GEMM_TARGET_WG), without splits shorter than
 // LLMT_GEMM_MIN_STEPS k-steps of 32.  Fewer splits means fewer fp32
 // partials to reduce.
-int gemm_tile_n() { return kCfgs[gemm_cfg()].nw * kNF * 16; }
+// DMA skinny kernel tiles (LLMT_GEMM_SKINNY_BN 32, 64 or 128;
+// LLMT_GEMM_SKINNY_STAGES 0 selects the register-staged kernel).
+static int skinny_stages() { return env_int("LLMT_GEMM_SKINNY_STAGES", 4); }
+static int skinny_bn() {
+  const int b = env_int("LLMT_GEMM_SKINNY_BN", 64);
+  return b == 32 || b == 128 ? b : 64;
+}
+int gemm_tile_n() { return skinny_stages() ? skinny_bn() : kCfgs[gemm_cfg()].nw * kNF * 16; }
 
 // The 256 x 128 tile kernel takes GEMMs with many rows (no split-K); the
 // skinny kernel everything else.
@@ -1054,6 +1213,30 @@ int gemm_pick_split(int M, int N, int K, int max_split) {
   if (split > max_split) split = max_split;
   if (split < 1) split = 1;
   return split;
+}
+
+// M % 128 == 0 with fp16 weights: the DMA-fed skinny kernel, 128 x BN tiles.
+template <int S>
+static void launch_skinny(const GemmArgs& g, hipStream_t st) {
+  const int bn = skinny_bn();
+  const dim3 grid((g.N + bn - 1) / bn, g.split, g.M / 128);
+  if (bn == 32)
+    hipLaunchKernelGGL((gemm_skinny_kernel<S, 2>), grid, dim3(256), 0, st, g);
+  else if (bn == 64)
+    hipLaunchKernelGGL((gemm_skinny_kernel<S, 4>), grid, dim3(256), 0, st, g);
+  else
+    hipLaunchKernelGGL((gemm_skinny_kernel<S, 8>), grid, dim3(256), 0, st, g);
+}
+static hipError_t launch_m128(const GemmArgs& g, hipStream_t st) {
+  bool i8 = false;
+  for (int i = 0; i < g.nseg; ++i) i8 = i8 || g.seg[i].is_i8;
+  const int stages = skinny_stages();
+  if (i8 || g.M % 128 || g.K % 64 || g.split > g.K / 64 || stages == 0) return launch_mf<8>(g, st);
+  if (stages == 3)
+    launch_skinny<3>(g, st);
+  else
+    launch_skinny<4>(g, st);
+  return hipGetLastError();
 }
 
 hipError_t gemm_nt(const GemmArgs& g, hipStream_t st) {
@@ -1118,9 +1301,9 @@ hipError_t gemm_nt(const GemmArgs& g, hipStream_t st) {
       gl.seg[0] = g.seg[last];
       gemm_finalize_segments(gl);
       gl.C = g.C + g.seg_start[last];
-      e = launch_mf<8>(gl, st);
+      e = launch_m128(gl, st);
     }
-  } else if (m16 % 8 == 0) e = launch_mf<8>(g, st);
+  } else if (m16 % 8 == 0) e = launch_m128(g, st);
   else if (m16 % 4 == 0) e = launch_mf<4>(g, st);
   else if (m16 % 2 == 0) e = launch_mf<2>(g, st);
   else e = launch_mf<1>(g, st);
