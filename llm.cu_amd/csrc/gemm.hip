@@ -746,8 +746,7 @@ template <int S, int NB>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(const GemmArgs g) {
   constexpr int AB = 16384;                  // A bytes per stage
   constexpr int SB = AB + NB * 2048;         // bytes per stage
-  constexpr int BPW = NB >= 4 ? NB / 4 : 1;  // B row blocks a loading wave moves
-  constexpr int BW = NB >= 4 ? 4 : NB;       // waves that move B
+  constexpr int BPW = (NB + 3) / 4;  // B row blocks a wave moves at most (w, w + 4, ..)
   __shared__ __attribute__((aligned(1024))) char smem[S * SB];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -766,10 +765,11 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const GemmArgs g) {
     const int r = 8 * (4 * wave + i) + (lane >> 3);
     aoff[i] = (unsigned)((r * g.lda + a_slot(r, lane & 7) * 8) * 2);
   }
+  const int nbw = (NB - wave + 3) / 4;  // row blocks this wave moves
   __amdgpu_buffer_rsrc_t brs[BPW];
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
-    const int nn = n0 + 16 * (wave * BPW + i);
+    const int nn = n0 + 16 * min(wave + 4 * i, NB - 1);
     int s = 0;
 #pragma unroll
     for (int q = 1; q < 4; ++q)
@@ -777,26 +777,28 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const GemmArgs g) {
     const long long rb16 = nn < g.N ? (nn - g.seg_start[s]) >> 4 : 0;
     brs[i] = make_rsrc((const _Float16*)g.seg[s].ptr + rb16 * ksteps * 512, (unsigned)(ksteps * 1024u));
   }
-  const bool bwave = wave < BW;
   auto issue = [&](int c) LLMT_INLINE {
     char* st = smem + (c % S) * SB;
 #pragma unroll
     for (int i = 0; i < 4; ++i) buffer_lds16(ars, st + (4 * wave + i) * 1024, aoff[i], c * 128u);
-    if (bwave) {
 #pragma unroll
-      for (int i = 0; i < BPW; ++i)
+    for (int i = 0; i < BPW; ++i)
+      if (i < nbw) {
 #pragma unroll
         for (int q = 0; q < 2; ++q)
-          buffer_lds16(brs[i], st + AB + ((wave * BPW + i) * 2 + q) * 1024, lane * 16u + q * 1024u,
+          buffer_lds16(brs[i], st + AB + ((wave + 4 * i) * 2 + q) * 1024, lane * 16u + q * 1024u,
                        c * 2048u);
-    }
+      }
   };
-  // stage c complete: only the later stages' loads may be pending
+  // stage c complete: only the later stages' loads (4 + 2 nbw a stage) may be pending
   auto wait_stage = [&]() LLMT_INLINE {
-    if (bwave)
-      wait_vm<(S - 2) * (4 + 2 * BPW)>();
-    else
-      wait_vm<(S - 2) * 4>();
+    switch (nbw) {
+      case 0: wait_vm<(S - 2) * 4>(); break;
+      case 1: wait_vm<(S - 2) * 6>(); break;
+      case 2: wait_vm<(S - 2) * 8>(); break;
+      case 3: wait_vm<(S - 2) * 10>(); break;
+      default: wait_vm<(S - 2) * 12>(); break;
+    }
   };
   // A fragment reads: row 16 f + c of the stage, k-step q, halves 8 g..
   int aread[2];
@@ -1159,14 +1161,44 @@ void gemm_finalize_segments(GemmArgs& g) {
 // per CU (tunable with LLMT_GEMM_TARGET_WG), without splits shorter than
 // LLMT_GEMM_MIN_STEPS k-steps of 32.  Fewer splits means fewer fp32
 // partials to reduce.
-// DMA skinny kernel tiles (LLMT_GEMM_SKINNY_BN 32, 64 or 128;
-// LLMT_GEMM_SKINNY_STAGES 0 selects the register-staged kernel).
+// DMA skinny kernel (fp16 weights, M % 128 == 0; LLMT_GEMM_SKINNY_STAGES = 0
+// selects the register-staged kernel).  Plan: 64-column tiles (48 when that
+// fills more of the GPU) and the most splits that keep the grid within one
+// wave of the 256 CUs (a second, partial wave costs more than the extra
+// partials); at least two 64-wide stages a split.  Wider tiles at the same
+// grid size write proportionally more fp32 partials and measured slower.  Very wide outputs with no split (the lm_head logits) keep the
+// register-staged kernel, measured faster there.  LLMT_GEMM_SKINNY_NB forces
+// the width for tuning.
 static int skinny_stages() { return env_int("LLMT_GEMM_SKINNY_STAGES", 4); }
-static int skinny_bn() {
-  const int b = env_int("LLMT_GEMM_SKINNY_BN", 64);
-  return b == 32 || b == 128 ? b : 64;
+struct SkinnyPlan {
+  int nb, split;
+};
+static SkinnyPlan skinny_plan(int M, int N, int K) {
+  const int frags = (N + 15) / 16, mt = M / 128;
+  const int forced = env_int("LLMT_GEMM_SKINNY_NB", 0);
+  const int target = env_int("LLMT_GEMM_TARGET_WG", 256);
+  SkinnyPlan best{0, 0};
+  int best_w = 0;
+  for (int nb : {4, 3, 2, 6, 8}) {
+    if (!forced && nb != 4 && nb != 3) continue;
+    if (forced && nb != forced) continue;
+    const int tiles = (frags + nb - 1) / nb * mt;
+    int split = target / tiles;
+    if (split > K / 128) split = K / 128;
+    if (split < 1) split = 1;
+    const int w = tiles * split;
+    if (w <= target && w > best_w) {
+      best = {nb, split};
+      best_w = w;
+    }
+  }
+  if (!best.nb) best = {forced ? forced : 4, 1};
+  return best;
 }
-int gemm_tile_n() { return skinny_stages() ? skinny_bn() : kCfgs[gemm_cfg()].nw * kNF * 16; }
+static bool skinny_ok(int M, int N, int K) {
+  return M % 128 == 0 && K % 64 == 0 && skinny_stages() != 0 && (N + 15) / 16 < 2048;
+}
+int gemm_tile_n() { return kCfgs[gemm_cfg()].nw * kNF * 16; }
 
 // The 256 x 128 tile kernel takes GEMMs with many rows (no split-K); the
 // skinny kernel everything else.
@@ -1200,6 +1232,10 @@ static int big_split(int M, int N, int K, int max_split) {
 
 int gemm_pick_split(int M, int N, int K, int max_split) {
   if (big_tiles(M, K)) return big_split(M, N, K, max_split);
+  if (skinny_ok(M, N, K)) {
+    const int split = skinny_plan(M, N, K).split;
+    return split > max_split ? max_split : split;
+  }
   // Partials grow with the workgroup count: about 3/4 of the CUs for the
   // layer GEMMs, two waves of CUs for the very long lm_head dX reduction.
   const int target = env_int("LLMT_GEMM_TARGET_WG", K > 16384 ? 512 : 192);
@@ -1217,25 +1253,25 @@ int gemm_pick_split(int M, int N, int K, int max_split) {
 
 // M % 128 == 0 with fp16 weights: the DMA-fed skinny kernel, 128 x BN tiles.
 template <int S>
-static void launch_skinny(const GemmArgs& g, hipStream_t st) {
-  const int bn = skinny_bn();
-  const dim3 grid((g.N + bn - 1) / bn, g.split, g.M / 128);
-  if (bn == 32)
-    hipLaunchKernelGGL((gemm_skinny_kernel<S, 2>), grid, dim3(256), 0, st, g);
-  else if (bn == 64)
-    hipLaunchKernelGGL((gemm_skinny_kernel<S, 4>), grid, dim3(256), 0, st, g);
-  else
-    hipLaunchKernelGGL((gemm_skinny_kernel<S, 8>), grid, dim3(256), 0, st, g);
+static void launch_skinny(const GemmArgs& g, int nb, hipStream_t st) {
+  const dim3 grid((g.N + nb * 16 - 1) / (nb * 16), g.split, g.M / 128);
+  switch (nb) {
+    case 2: hipLaunchKernelGGL((gemm_skinny_kernel<S, 2>), grid, dim3(256), 0, st, g); break;
+    case 3: hipLaunchKernelGGL((gemm_skinny_kernel<S, 3>), grid, dim3(256), 0, st, g); break;
+    case 6: hipLaunchKernelGGL((gemm_skinny_kernel<S, 6>), grid, dim3(256), 0, st, g); break;
+    case 8: hipLaunchKernelGGL((gemm_skinny_kernel<S, 8>), grid, dim3(256), 0, st, g); break;
+    default: hipLaunchKernelGGL((gemm_skinny_kernel<S, 4>), grid, dim3(256), 0, st, g); break;
+  }
 }
 static hipError_t launch_m128(const GemmArgs& g, hipStream_t st) {
   bool i8 = false;
   for (int i = 0; i < g.nseg; ++i) i8 = i8 || g.seg[i].is_i8;
-  const int stages = skinny_stages();
-  if (i8 || g.M % 128 || g.K % 64 || g.split > g.K / 64 || stages == 0) return launch_mf<8>(g, st);
-  if (stages == 3)
-    launch_skinny<3>(g, st);
+  if (i8 || !skinny_ok(g.M, g.N, g.K) || g.split > g.K / 64) return launch_mf<8>(g, st);
+  const int nb = skinny_plan(g.M, g.N, g.K).nb;
+  if (skinny_stages() == 3)
+    launch_skinny<3>(g, nb, st);
   else
-    launch_skinny<4>(g, st);
+    launch_skinny<4>(g, nb, st);
   return hipGetLastError();
 }
 

@@ -32,14 +32,16 @@ def test_gemm_f16_matches_fp32(dev, L, M, N, K):
     assert torch.isfinite(got).all()
 
 
-@pytest.mark.parametrize("bn,stages", [("32", "4"), ("64", "3"), ("128", "4"), ("64", "0")])
+@pytest.mark.parametrize("nb,stages", [("2", "4"), ("3", "3"), ("4", "4"), ("6", "3"), ("8", "4"),
+                                       ("4", "0")])
 @pytest.mark.parametrize("M,N,K", [(128, 2048 + 48, 2048), (256, 160, 4096), (128, 12288, 1024)])
-def test_gemm_f16_skinny_tiles(dev, L, monkeypatch, bn, stages, M, N, K):
-    """Every tile width / ring depth of the M % 128 == 0 path (0 stages: the
-    register-staged kernel), including partial last column tiles."""
-    monkeypatch.setenv("LLMT_GEMM_SKINNY_BN", bn)
+def test_gemm_f16_skinny_tiles(dev, L, monkeypatch, nb, stages, M, N, K):
+    """Every tile width (nb 16-column fragments) / ring depth of the
+    M % 128 == 0 path (0 stages: the register-staged kernel), including
+    partial last column tiles."""
+    monkeypatch.setenv("LLMT_GEMM_SKINNY_NB", nb)
     monkeypatch.setenv("LLMT_GEMM_SKINNY_STAGES", stages)
-    g = _seed(M + N + K + int(bn))
+    g = _seed(M + N + K + int(nb))
     A = torch.randn(M, K, generator=g).half()
     B = (torch.randn(N, K, generator=g) * 0.02).half()
     want = A.float() @ B.float().t()
