@@ -6,22 +6,30 @@ seq 128, token ids uniform over the vocabulary, next-token targets.  The step
 runs as one captured HIP graph of libllmt.so kernels (llmt_step); inputs are
 resident in HBM before the timed region.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c4] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c3|c4] [--no-cpu]
+    python bench.py --copy-cal      # plain 512 MiB copies (PMC byte-counter scale)
 
 Prints ONE JSON line.  Besides the contract fields it carries
-  roofline:     the GEMM kernel family (the step's dominant kernel): streamed
-                weight bytes per step / summed GEMM kernel time of one eagerly
-                profiled step (HIP events between kernels, on the step's
-                stream), against 8 TB/s HBM;
+  roofline:     the frozen-weight GEMMs (the step's dominant kernel family):
+                the step's GEMM launches replayed back to back as one HIP
+                graph, timed with HIP events on the context's stream;
+                achieved = streamed weight bytes per launch / average launch
+                time, against 8 TB/s HBM (C4: TFLOP/s against 2.5 PFLOP/s);
+                traffic = measured HBM bytes per launch (rocprofv3 FETCH_SIZE
+                and WRITE_SIZE passes scaled by the copy calibration, read
+                from profiles/gemm_c2_traffic.md);
   cpu_baseline: the CPU oracle (PyTorch fp32, oracle/lora_step.py) on a
-                bounded sample of the same step, extrapolated to a full step;
-  kernels:      per-category kernel milliseconds of that profiled step.
+                bounded sample of the same step;
+  kernels:      per-category kernel milliseconds of one profiled step.
+--config c3 times the attention stress case (QK-norm + RoPE + causal GQA
+flash attention forward and backward, B4 x S2048) instead.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -65,7 +73,7 @@ def build_model(ctx, dims, seed, dev, int8=False):
     torch.cuda.synchronize()
 
 
-def cpu_baseline_sampled(dims, batch, seq_len):
+def cpu_baseline_sampled(batch, seq_len):
     """For configurations too large to run whole on the CPU (C4): the CPU
     oracle step on 1-layer and 2-layer models of the same width, batch and
     sequence; per-layer = t2 - t1, head = t1 - per-layer, and the full step is
@@ -73,6 +81,7 @@ def cpu_baseline_sampled(dims, batch, seq_len):
     import torch
     from oracle import lora_step as ref
     from oracle.configs import make_adapters, make_model
+    dims = ref.QWEN3_1_7B
     torch.set_num_threads(len(os.sched_getaffinity(0)))
     t = {}
     for nl in (1, 2):
@@ -99,7 +108,7 @@ def cpu_baseline_sampled(dims, batch, seq_len):
     }
 
 
-def cpu_baseline(dims, batch, seq_len, min_s=10.0):
+def cpu_baseline(batch, seq_len, min_s=10.0):
     """The CPU oracle (PyTorch fp32, oracle/lora_step.py) running the same
     step -- forward, fused CE, closed-form backward, AdamW -- on the same
     configuration with its own seeded random model: one warm-up step, then
@@ -108,6 +117,7 @@ def cpu_baseline(dims, batch, seq_len, min_s=10.0):
     import torch
     from oracle import lora_step as ref
     from oracle.configs import make_adapters, make_model
+    dims = ref.QWEN3_1_7B
     torch.set_num_threads(len(os.sched_getaffinity(0)))
     g = torch.Generator().manual_seed(4242)
     W = make_model(g, dims)
@@ -133,26 +143,97 @@ def cpu_baseline(dims, batch, seq_len, min_s=10.0):
     }
 
 
+def measured_traffic():
+    """HBM bytes per GEMM launch of the C2 step from the committed rocprofv3
+    counter summary (None if absent)."""
+    f = ROOT / "profiles" / "gemm_c2_traffic.md"
+    if not f.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", f.read_text())
+    return int(m.group(1)) if m else None
+
+
+def copy_calibration():
+    """Three plain device copies of 512 MiB: what FETCH_SIZE / WRITE_SIZE read
+    for a kernel of known traffic (the scale applied to the GEMM passes)."""
+    import torch
+    n = 128 << 20
+    src = torch.ones(n, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration": {"bytes_read": n * 4, "bytes_written": n * 4,
+                                           "copies": 3}}), flush=True)
+
+
+def bench_c3(a):
+    """C3: QK-norm + RoPE + causal GQA attention forward and backward through
+    llmt_attention_block_bwd (fp16 q/k/v/dO, fp32 gradients), B4 x S2048,
+    16 query / 8 KV heads.  Work = 7 causal S x S x 128 products per (batch,
+    query head): forward QK^T, PV; backward recomputed QK^T, dO V^T, P^T dO,
+    dS^T Q, dS K."""
+    import torch
+    import llmt
+    B, S, nq, nkv = 4, 2048, 16, 8
+    g = torch.Generator(device="cuda").manual_seed(1003)
+    rnd = lambda h: torch.randn(B, S, h, 128, generator=g, device="cuda").half()
+    q, k, v, do = rnd(nq), rnd(nkv), rnd(nkv), rnd(nq)
+    one = torch.ones(128, device="cuda")
+    run = lambda: llmt.attention_block_bwd(q, k, v, one, one, do)
+    for _ in range(a.warmup):
+        run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        run()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / a.steps
+    flops = 7 * B * nq * (S * (S + 1) / 2) * 128 * 2
+    tf = flops / dt / 1e12
+    out = {
+        "metric": "attention fwd+bwd (QK-norm, RoPE, causal GQA) tokens/s",
+        "value": round(B * S / dt, 2), "unit": "tokens/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(dt * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic N(0,1)",
+        "config": {"workload": "C3: causal GQA attention block fwd+bwd, 16 Q / 8 KV heads, "
+                               "head_dim 128, QK-norm, RoPE 1e6", "global_batch": B,
+                   "seq_len": S},
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_F16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                     "traffic": None,
+                     "kernel": "attention block (norm/RoPE + flash fwd + dQ + dK/dV launches)"},
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", choices=["c2", "c4"], default="c2")
+    ap.add_argument("--config", choices=["c2", "c3", "c4"], default="c2")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--copy-cal", action="store_true", help="PMC byte-counter calibration")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {a.gpus}); the multi-GPU "
               "sharding is a design note, not a code path.", file=sys.stderr)
         sys.exit(2)
+    if a.copy_cal:
+        copy_calibration()
+        return
+    if a.config == "c3":
+        bench_c3(a)
+        return
 
     import torch
     import llmt
-    from oracle import lora_step as ref
 
     dev = torch.device("cuda:0")
-    dims = ref.QWEN3_1_7B
+    dims = llmt.qwen3_dims()
     if a.config == "c2":
         batch, seq_len, int8, seed = 1, 128, False, 1002
         workload = ("C2: Qwen3-1.7B LoRA training step (28 layers, fp16 frozen weights, rank-16 "
@@ -162,7 +243,7 @@ def main():
         workload = ("C4: Qwen3-1.7B LoRA training step (28 layers, int8 per-channel frozen "
                     "weights, fused dequant), batch 8 x seq 512")
     T = batch * seq_len
-    ctx = llmt.Context(llmt.make_dims(dims), max_batch=batch, seq_len=seq_len, int8=int8)
+    ctx = llmt.Context(dims, max_batch=batch, seq_len=seq_len, int8=int8)
     build_model(ctx, dims, seed, dev, int8=int8)
     ctx.lora_init(seed, 1.0 / 2048 ** 0.5, 0.01)
     g = torch.Generator(device=dev).manual_seed(seed + 1)
@@ -202,12 +283,15 @@ def main():
         bound, ach, peak, unit = "mfma", round(tflops, 2), MFMA_F16_PEAK_TFLOPS, "TFLOP/s"
     roofline = {
         "bound": bound,
-        "kernel": "gemm_nt_kernel (all frozen-weight GEMMs of the step)",
+        "kernel": "frozen-weight GEMMs of the step (gemm_skinny_kernel; gemm_nt_kernel "
+                  "for the logits)" if a.config == "c2" else
+                  "frozen-weight GEMMs of the step (gemm_dma_kernel; gemm_skinny_kernel for "
+                  "the LoRA columns)",
         "achieved": ach,
         "peak": peak,
         "unit": unit,
         "frac": round(ach / peak, 4),
-        "traffic": None,
+        "traffic": measured_traffic() if a.config == "c2" else None,
         "algorithmic_bytes_per_launch": round(bytes_per_launch),
         "launches_per_step": n_gemm,
         "avg_launch_us": round(avg_us, 3),
@@ -236,8 +320,8 @@ def main():
     }
     ctx.close()
     if not a.no_cpu:
-        out["cpu_baseline"] = (cpu_baseline(dims, batch, seq_len) if a.config == "c2"
-                               else cpu_baseline_sampled(dims, batch, seq_len))
+        out["cpu_baseline"] = (cpu_baseline(batch, seq_len) if a.config == "c2"
+                               else cpu_baseline_sampled(batch, seq_len))
     print(json.dumps(out), flush=True)
 
 

@@ -284,16 +284,7 @@ int llmt_attention_block_bwd(const void* q_raw, const void* k_raw, const void* v
   TRY_ARG(raw16 && qkv16 && qkraw && o16 && lse && dO && delta && damax && dqkv && dkvp && dO16 &&
               dy && g16 && rinv && cosT && sinT,
           "llmt_attention_block_bwd: out of memory");
-  // RoPE tables (src/kernels/rope.cu:15-18), angles in double rounded to fp32.
-  std::vector<float> hc((size_t)S * 64), hs((size_t)S * 64);
-  for (int p = 0; p < S; ++p)
-    for (int d = 0; d < 64; ++d) {
-      const double ang = (double)p / pow((double)theta, 2.0 * d / kHeadDim);
-      hc[(size_t)p * 64 + d] = (float)cos(ang);
-      hs[(size_t)p * 64 + d] = (float)sin(ang);
-    }
-  TRY_HIP(hipMemcpyAsync(cosT, hc.data(), hc.size() * 4, hipMemcpyHostToDevice, st));
-  TRY_HIP(hipMemcpyAsync(sinT, hs.data(), hs.size() * 4, hipMemcpyHostToDevice, st));
+  TRY_HIP(rope_tables(S, (double)theta, cosT, sinT, st));
   // [q_raw | k_raw | v] rows
   TRY_HIP(hipMemcpy2DAsync(raw16, NT * 2, q_raw, Q * 2, Q * 2, T, hipMemcpyDeviceToDevice, st));
   TRY_HIP(hipMemcpy2DAsync(raw16 + Q, NT * 2, k_raw, KV * 2, KV * 2, T, hipMemcpyDeviceToDevice, st));

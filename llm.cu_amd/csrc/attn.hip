@@ -25,11 +25,13 @@
 // Tiles: 64 rows x 128 halves (16 KB), moved global -> LDS by buffer loads
 // with an LDS destination (16 bytes a lane) into two buffers, so tile i + 1
 // lands while tile i is computed; one barrier per tile.  No padding: the
-// 16-byte piece p of tile row r sits in slot p ^ swz(r), which keeps the
-// row-fragment reads (16 rows, one piece) and the transposed reads (8 rows,
-// two pieces per half-wave) free of bank conflicts.  Rows past S read as
-// zeros (buffer range check); causality and the sequence end are masked in
-// the diagonal / last tiles only, chosen per wave with scalar branches.
+// 16-byte piece p of tile row r sits in slot p ^ (r % 16).  Measured on
+// MI355X (cycles per wave instruction, four waves): the row-fragment reads
+// (16 rows, one piece) run at the rate of a contiguous ds_read_b128 (28.6;
+// unswizzled 128.0), the transposed reads at that of a contiguous
+// ds_read_b64_tr_b16 (25.8; unswizzled 64.0).  Rows past S read as zeros
+// (buffer range check); causality and the sequence end are masked in the
+// diagonal / last tiles only, chosen per wave with scalar branches.
 #include <stdlib.h>
 
 #include <algorithm>
@@ -51,7 +53,7 @@ typedef _Float16 half4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4v lds_short4;
 typedef __attribute__((address_space(3))) void lds_void;
 
-__device__ __forceinline__ int swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+__device__ __forceinline__ int swz(int r) { return r & 15; }
 // Offset (halves) of halves 8 p .. 8 p + 7 of tile row r.
 __device__ __forceinline__ int toff(int r, int p) { return r * HD + ((p ^ swz(r)) << 3); }
 
@@ -716,7 +718,11 @@ hipError_t attn_bwd(const AttnArgs& a, int B, hipStream_t st) {
               a.nkv, a.S);
     return hipErrorInvalidValue;
   }
-  const AttnShape s = attn_shape(B, a.S, a.nq);
+  // dQ holds twice the accumulators of the forward: one 16-row tile a wave
+  // keeps two waves per SIMD (two tiles spill to one), measured faster at
+  // every S; LLMT_ATTN_CFG still selects any shape for tuning.
+  AttnShape s = attn_shape(B, a.S, a.nq);
+  if (!getenv("LLMT_ATTN_CFG")) s.rw = 1;
   switch (s.nw * 10 + s.rw) {
     case 42: launch_dq<4, 2>(a, B, st); break;
     case 41: launch_dq<4, 1>(a, B, st); break;

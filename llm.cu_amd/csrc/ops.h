@@ -171,6 +171,8 @@ hipError_t o_post(const RowIn& in, const float* x_in, const float* w, float eps,
 hipError_t gu_post(const RowIn& in, int I, int T, float* gu, _Float16* a16, hipStream_t st);
 hipError_t resid_norm(const RowIn& in, const float* x_res, const float* w, float eps, int H, int T,
                       float* x_out, _Float16* xn, hipStream_t st);
+// cos / sin tables of the half-split RoPE, [S, 64] fp32 each, on the device.
+hipError_t rope_tables(int S, double theta, float* cosT, float* sinT, hipStream_t st);
 hipError_t qk_norm_rope(const _Float16* raw, const float* qn, const float* kn, const float* cosT,
                         const float* sinT, int S, int nq, int nkv, float eps, int T, _Float16* out,
                         hipStream_t st);

@@ -812,6 +812,25 @@ hipError_t resid_norm(const RowIn& in, const float* x_res, const float* w, float
   return hipSuccess;
 }
 
+// RoPE tables (src/kernels/rope.cu:15-18): angle p / theta^(2 d / 128) in
+// double, cos and sin rounded to fp32; [S, 64] each.
+__global__ __launch_bounds__(256) void rope_tables_kernel(int S, double theta, float* cosT,
+                                                          float* sinT) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= S * 64) return;
+  const int p = i >> 6, d = i & 63;
+  const double ang = (double)p / pow(theta, 2.0 * d / 128.0);
+  cosT[i] = (float)cos(ang);
+  sinT[i] = (float)sin(ang);
+}
+
+hipError_t rope_tables(int S, double theta, float* cosT, float* sinT, hipStream_t st) {
+  hipLaunchKernelGGL(rope_tables_kernel, dim3((S * 64 + 255) / 256), dim3(256), 0, st, S, theta,
+                     cosT, sinT);
+  LLMT_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
 hipError_t qk_norm_rope(const _Float16* raw, const float* qn, const float* kn, const float* cosT,
                         const float* sinT, int S, int nq, int nkv, float eps, int T, _Float16* out,
                         hipStream_t st) {
