@@ -104,7 +104,7 @@ def cpu_baseline_sampled(batch, seq_len):
         "sample": (f"CPU oracle (PyTorch fp32) LoRA step on 1- and 2-layer models at "
                    f"B{batch}xS{seq_len} ({t[1]:.1f} s, {t[2]:.1f} s, one step each); full "
                    f"{dims.n_layers}-layer step extrapolated = head + {dims.n_layers} x layer = "
-                   f"{total:.1f} s"),
+                   f"{total:.1f} s; {torch.get_num_threads()} threads on {cpu_description()}"),
     }
 
 
@@ -139,7 +139,8 @@ def cpu_baseline(batch, seq_len, min_s=10.0):
         "kind": "port",
         "sample": (f"CPU oracle (PyTorch fp32, oracle/lora_step.py) full {dims.n_layers}-layer "
                    f"LoRA step (fwd + CE + bwd + AdamW) at B{batch}xS{seq_len}, random model; "
-                   f"median of {len(times)} timed steps after 1 warm-up: {med:.3f} s/step"),
+                   f"median of {len(times)} timed steps after 1 warm-up: {med:.3f} s/step; "
+                   f"{torch.get_num_threads()} threads on {cpu_description()}"),
     }
 
 
@@ -151,6 +152,56 @@ def measured_traffic():
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", f.read_text())
     return int(m.group(1)) if m else None
+
+
+def achievable_peaks():
+    """Measured ceilings on this GPU, reported beside the datasheet peaks: a
+    1 GiB device copy (read + write bytes / time) and an 8192^3 fp16 GEMM
+    through torch.mm (hipBLASLt)."""
+    import torch
+    src = torch.ones(256 << 20, device="cuda")
+    dst = torch.empty_like(src)
+    a = torch.randn(8192, 8192, device="cuda").half()
+    b = torch.randn(8192, 8192, device="cuda").half()
+
+    def timed(fn, n):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n
+
+    t_copy = timed(lambda: dst.copy_(src), 10)
+    t_mm = timed(lambda: torch.mm(a, b), 10)
+    out = {"hbm_copy_gbs": round(2 * src.numel() * 4 / t_copy / 1e9, 1),
+           "mfma_f16_tflops_hipblaslt": round(2 * 8192 ** 3 / t_mm / 1e12, 1),
+           "datasheet": {"hbm_gbs": HBM_PEAK_GBS, "mfma_f16_tflops": MFMA_F16_PEAK_TFLOPS}}
+    del src, dst, a, b
+    torch.cuda.empty_cache()
+    return out
+
+
+def cpu_description():
+    """CPU model, sockets and cores of the host (from /proc/cpuinfo)."""
+    model, phys, cores = "unknown", set(), set()
+    try:
+        cur = {}
+        for line in open("/proc/cpuinfo"):
+            if ":" not in line:
+                if cur:
+                    phys.add(cur.get("physical id"))
+                    cores.add((cur.get("physical id"), cur.get("core id")))
+                cur = {}
+                continue
+            k, v = (x.strip() for x in line.split(":", 1))
+            cur[k] = v
+            if k == "model name":
+                model = v
+    except OSError:
+        pass
+    return f"{model}; {len(phys)} socket(s), {len(cores)} physical cores on the host"
 
 
 def copy_calibration():
@@ -319,6 +370,7 @@ def main():
         "loss_first_last": [round(losses[0], 5), round(losses[-1], 5)],
     }
     ctx.close()
+    out["achievable"] = achievable_peaks()
     if not a.no_cpu:
         out["cpu_baseline"] = (cpu_baseline(batch, seq_len) if a.config == "c2"
                                else cpu_baseline_sampled(batch, seq_len))

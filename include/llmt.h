@@ -235,6 +235,11 @@ int llmt_lora_copy(llmt_ctx* ctx, int kind, float* buf, int to_ctx);
  * (src/train.cu:146-170) — raw fp32, A [16, d_in], B [d_out, 16]. */
 int llmt_lora_save(llmt_ctx* ctx, const char* dir, int step);
 int llmt_lora_load(llmt_ctx* ctx, const char* dir, int step);
+/* AdamW moments for resuming a run (no counterpart in the reference, whose
+ * driver cannot resume): <dir>/lora_step{N}_adamw.bin holds "LLMTADAM",
+ * int32 version 1, int32 step, int64 numel, fp32 m, fp32 v. */
+int llmt_lora_save_state(llmt_ctx* ctx, const char* dir, int step);
+int llmt_lora_load_state(llmt_ctx* ctx, const char* dir, int step);
 /* Seeded init on the device (the reference draws A with cuRAND, B = 0:
  * src/kernels/lora.cu:40-62; configs use A std a_std, B std b_std). */
 int llmt_lora_init(llmt_ctx* ctx, uint64_t seed, float a_std, float b_std);

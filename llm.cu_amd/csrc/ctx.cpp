@@ -366,7 +366,9 @@ int llmt_load_weights_dir(llmt_ctx* ctx, const char* dir) {
   Ctx* c = C_(ctx);
   TRY_ARG(c && dir, "llmt_load_weights_dir: NULL argument");
   const int H = c->H, Q = c->Q, KV = c->KV, I = c->I, V = c->V;
-  const size_t big = (size_t)V * H;
+  // staging: the embedding, or one layer's seven matrices and four norms
+  const size_t layer_elems = (size_t)H * (2 * Q + 2 * KV + 3 * (size_t)I);
+  const size_t big = std::max((size_t)V * H, layer_elems + 2 * (size_t)H + 2 * kHeadDim);
   float* f32 = nullptr;
   _Float16* f16 = nullptr;
   int8_t* q8 = nullptr;
@@ -385,7 +387,7 @@ int llmt_load_weights_dir(llmt_ctx* ctx, const char* dir) {
     return r;
   };
   if (hipMalloc((void**)&f16, big * 2) != hipSuccess ||
-      hipMalloc((void**)&q8, (size_t)I * H * 7) != hipSuccess ||
+      hipMalloc((void**)&q8, layer_elems) != hipSuccess ||
       hipMalloc((void**)&s32, (size_t)(I * 2 + Q + 2 * KV + 2 * H) * 4) != hipSuccess ||
       hipMalloc((void**)&s16, (size_t)(I * 2 + Q + 2 * KV + 2 * H) * 2) != hipSuccess) {
     set_error("llmt_load_weights_dir: out of device memory");
@@ -459,8 +461,8 @@ int llmt_load_weights_dir(llmt_ctx* ctx, const char* dir) {
   std::vector<float> fn;
   snprintf(path, sizeof(path), "%s/model.norm.weight.bin", dir);
   if ((rc = read_f32(path, H, fn))) return fail(rc);
-  if ((rc = up("model.embed_tokens.weight.bin", big, 0))) return fail(rc);
-  if (f32_to_f16(f32, f16, big, c->st) != hipSuccess || hipStreamSynchronize(c->st) != hipSuccess ||
+  if ((rc = up("model.embed_tokens.weight.bin", (size_t)V * H, 0))) return fail(rc);
+  if (f32_to_f16(f32, f16, (size_t)V * H, c->st) != hipSuccess || hipStreamSynchronize(c->st) != hipSuccess ||
       hipMemcpy(f32, fn.data(), H * 4, hipMemcpyHostToDevice) != hipSuccess)
     return fail(LLMT_ERR_HIP);
   rc = llmt_set_embed_f16(ctx, f16, f32);
@@ -521,6 +523,70 @@ int llmt_lora_load(llmt_ctx* ctx, const char* dir, int step) {
         memcpy(host.data() + (size_t)l * c->lora_per_layer + c->seg_off[s], tmp.data(), n * 4);
       }
   return llmt_lora_copy(ctx, LLMT_LORA_PARAM, host.data(), 1);
+}
+
+// AdamW state next to the adapter files: <dir>/lora_step{N}_adamw.bin =
+// "LLMTADAM", int32 version 1, int32 step, int64 numel, fp32 m[numel],
+// fp32 v[numel] (little-endian).  The reference has no resume; this is the
+// state a restart at step N + 1 needs besides the adapters themselves.
+static const char kAdamMagic[8] = {'L', 'L', 'M', 'T', 'A', 'D', 'A', 'M'};
+
+int llmt_lora_save_state(llmt_ctx* ctx, const char* dir, int step) {
+  set_error("");
+  Ctx* c = C_(ctx);
+  TRY_ARG(c && dir, "llmt_lora_save_state: NULL argument");
+  const size_t n = c->lora_numel;
+  std::vector<float> mv(2 * n);
+  TRY_HIP(hipMemcpyAsync(mv.data(), c->lora_m, n * 4, hipMemcpyDeviceToHost, c->st));
+  TRY_HIP(hipMemcpyAsync(mv.data() + n, c->lora_v, n * 4, hipMemcpyDeviceToHost, c->st));
+  TRY_HIP(hipStreamSynchronize(c->st));
+  char path[1024];
+  snprintf(path, sizeof(path), "%s/lora_step%d_adamw.bin", dir, step);
+  FILE* f = fopen(path, "wb");
+  if (!f) {
+    set_error("cannot write %s", path);
+    return LLMT_ERR_IO;
+  }
+  const int32_t hdr[2] = {1, step};
+  const int64_t numel = (int64_t)n;
+  bool ok = fwrite(kAdamMagic, 1, 8, f) == 8 && fwrite(hdr, 4, 2, f) == 2 &&
+            fwrite(&numel, 8, 1, f) == 1 && fwrite(mv.data(), 4, 2 * n, f) == 2 * n;
+  ok = (fclose(f) == 0) && ok;
+  if (!ok) {
+    set_error("short write %s", path);
+    return LLMT_ERR_IO;
+  }
+  return LLMT_OK;
+}
+
+int llmt_lora_load_state(llmt_ctx* ctx, const char* dir, int step) {
+  set_error("");
+  Ctx* c = C_(ctx);
+  TRY_ARG(c && dir, "llmt_lora_load_state: NULL argument");
+  const size_t n = c->lora_numel;
+  char path[1024];
+  snprintf(path, sizeof(path), "%s/lora_step%d_adamw.bin", dir, step);
+  FILE* f = fopen(path, "rb");
+  if (!f) {
+    set_error("cannot open %s", path);
+    return LLMT_ERR_IO;
+  }
+  char magic[8];
+  int32_t hdr[2];
+  int64_t numel = 0;
+  std::vector<float> mv(2 * n);
+  const bool ok = fread(magic, 1, 8, f) == 8 && fread(hdr, 4, 2, f) == 2 &&
+                  fread(&numel, 8, 1, f) == 1 && memcmp(magic, kAdamMagic, 8) == 0 &&
+                  hdr[0] == 1 && hdr[1] == step && numel == (int64_t)n &&
+                  fread(mv.data(), 4, 2 * n, f) == 2 * n;
+  fclose(f);
+  if (!ok) {
+    set_error("%s: not an AdamW state of step %d with %zu parameters", path, step, n);
+    return LLMT_ERR_IO;
+  }
+  int rc = llmt_lora_copy(ctx, LLMT_LORA_M, mv.data(), 1);
+  if (rc) return rc;
+  return llmt_lora_copy(ctx, LLMT_LORA_V, mv.data() + n, 1);
 }
 
 }  // extern "C"

@@ -64,6 +64,8 @@ _PROTOS = {
     "llmt_lora_copy": (i32, [vp, i32, vp, i32]),
     "llmt_lora_save": (i32, [vp, C.c_char_p, i32]),
     "llmt_lora_load": (i32, [vp, C.c_char_p, i32]),
+    "llmt_lora_save_state": (i32, [vp, C.c_char_p, i32]),
+    "llmt_lora_load_state": (i32, [vp, C.c_char_p, i32]),
     "llmt_lora_init": (i32, [vp, u64, f32, f32]),
     "llmt_step": (i32, [vp, vp, vp, i32, C.POINTER(HParams), i32, fp]),
     "llmt_forward_backward": (i32, [vp, vp, vp, i32, fp]),
@@ -272,6 +274,13 @@ class Context:
 
     def lora_load(self, path, step: int):
         check(lib().llmt_lora_load(self.h, str(path).encode(), step))
+
+    def lora_save_state(self, path, step: int):
+        """AdamW moments to <path>/lora_step{step}_adamw.bin (for resuming)."""
+        check(lib().llmt_lora_save_state(self.h, str(path).encode(), step))
+
+    def lora_load_state(self, path, step: int):
+        check(lib().llmt_lora_load_state(self.h, str(path).encode(), step))
 
     # -- the step
     def set_graph(self, enable: bool):

@@ -62,3 +62,23 @@ def test_standalone_ops_reject_bad_shapes():
 def test_profile_categories_match_header():
     txt = llmt.HEADER.read_text()
     assert "8 split-K reductions" in txt and len(llmt.PROFILE_CATEGORIES) == 9
+
+
+def test_llm_train_cli_rejects_bad_input(tmp_path):
+    """The driver exits with status 1 and a message before touching the GPU on
+    bad flags, a missing token file or too few tokens (src/train.cu:194-213)."""
+    import subprocess
+    from pathlib import Path
+    import numpy as np
+    exe = Path(__file__).resolve().parent.parent / "llm.cu_amd" / "llm_train"
+    assert exe.exists(), "llm_train not built (python llm.cu_amd/build.py)"
+    run = lambda *a: subprocess.run([str(exe), *a], capture_output=True, text=True, timeout=60)
+    r = run("--bogus")
+    assert r.returncode == 1 and "unknown" in r.stderr
+    r = run("--data", str(tmp_path / "missing.bin"))
+    assert r.returncode == 1 and "not found" in r.stderr
+    tok = tmp_path / "few.bin"
+    np.array([3, 1, 2, 3], dtype="<i4").tofile(tok)
+    r = run("--data", str(tok), "--seq-len", "8")
+    assert r.returncode == 1 and "need at least 9 tokens, got 3" in r.stderr
+    assert "Training config: lr=3.00e-04 steps=1000 seq_len=8" in r.stdout
