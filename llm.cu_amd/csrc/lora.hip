@@ -21,30 +21,42 @@ constexpr int NTH = 256;
 // token rows, for the ncols columns of X and the 16 columns of G.
 //   dA [16, d_in]:  X = adapter input (xn or o, fp16), G = dh  -> out[r][c]
 //   dB [d_out, 16]: X = upstream grad dy (fp32),       G = h   -> out[c][r]
-// A workgroup owns GC columns (a lane per column); its four waves take
-// interleaved batches of TB tokens, issue the batch's X loads together and
-// read the batch's G rows (uniform across the wave) through scalar loads,
-// then their partial sums are added in LDS in wave order.  Latency-bound at
-// T = 128: one memory round trip per batch.
-constexpr int GC = 64;
-constexpr int TB = 32;
+// A workgroup owns GC columns, four per lane (one 8- or 16-byte load of X per
+// token); its four waves take interleaved batches of TB tokens, issue the
+// batch's X loads together and read the batch's G rows (uniform across the
+// wave) through scalar loads, accumulating a 16 x 4 block per lane; the four
+// partial blocks are then added in LDS in wave order (deterministic).
+constexpr int GC = 256;
+constexpr int TB = 16;
+template <bool F16>
+__device__ __forceinline__ float4 load_x4(const void* X, long long off) {
+  if (F16) {
+    const half4 h = *reinterpret_cast<const half4*>((const _Float16*)X + off);
+    return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+  }
+  return *reinterpret_cast<const float4*>((const float*)X + off);
+}
+
 template <bool F16>
 __device__ __forceinline__ void lora_grad_acc(const LoraGradJob& jb, int T, int cc, int w,
-                                              float (&acc)[R]) {
+                                              float4 (&acc)[R]) {
   const int wu = __builtin_amdgcn_readfirstlane(w);
   for (int t0 = wu * TB; t0 < T; t0 += (NTH / 64) * TB) {
-    float x[TB];
+    float4 x[TB];
 #pragma unroll
-    for (int i = 0; i < TB; ++i) {
-      const long long off = (long long)min(t0 + i, T - 1) * jb.ldx + cc;
-      x[i] = F16 ? (float)((const _Float16*)jb.X)[off] : ((const float*)jb.X)[off];
-    }
+    for (int i = 0; i < TB; ++i) x[i] = load_x4<F16>(jb.X, (long long)min(t0 + i, T - 1) * jb.ldx + cc);
 #pragma unroll
     for (int i = 0; i < TB; ++i) {
       if (t0 + i >= T) break;
       const float* g = jb.G + (long long)(t0 + i) * jb.ldg;
 #pragma unroll
-      for (int r = 0; r < R; ++r) acc[r] += x[i] * g[r];
+      for (int r = 0; r < R; ++r) {
+        const float gr = g[r];
+        acc[r].x += x[i].x * gr;
+        acc[r].y += x[i].y * gr;
+        acc[r].z += x[i].z * gr;
+        acc[r].w += x[i].w * gr;
+      }
     }
   }
 }
@@ -56,7 +68,7 @@ struct LoraGradGrid {
 __global__ __launch_bounds__(NTH) void lora_grad_kernel(const LoraGradJob* __restrict__ jobs,
                                                         const LoraGradGrid G, int T, float lscale,
                                                         int accumulate) {
-  __shared__ float red[NTH / 64][GC][R + 1];
+  __shared__ float red[NTH / 64][R][GC];  // 64 KB
   const int bpl = G.block_start[kLoraJobs];
   const int layer = (int)blockIdx.x / bpl, lb = (int)blockIdx.x - layer * bpl;
   int j = 0;
@@ -65,28 +77,28 @@ __global__ __launch_bounds__(NTH) void lora_grad_kernel(const LoraGradJob* __res
     if (lb >= G.block_start[i]) j = i;
   const LoraGradJob jb = jobs[layer * kLoraJobs + j];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int c = (lb - G.block_start[j]) * GC + lane;
-  const bool active = c < jb.ncols;
-  const int cc = active ? c : 0;
-  float acc[R];
+  const int cb = (lb - G.block_start[j]) * GC;  // first column of the block
+  const int c = cb + 4 * lane;                  // this lane's first column
+  const int cc = c < jb.ncols ? c : 0;
+  float4 acc[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+  for (int r = 0; r < R; ++r) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
   if (jb.x_f16)
     lora_grad_acc<true>(jb, T, cc, w, acc);
   else
     lora_grad_acc<false>(jb, T, cc, w, acc);
 #pragma unroll
-  for (int r = 0; r < R; ++r) red[w][lane][r] = acc[r];
+  for (int r = 0; r < R; ++r) *reinterpret_cast<float4*>(&red[w][r][4 * lane]) = acc[r];
   __syncthreads();
-  // thread (lane, w) finishes rows r = 4 w .. 4 w + 3 of column lane
-  if (!active) return;
+  // thread i finishes column cb + i (all 16 r), summing the waves in order
+  const int col = cb + (int)threadIdx.x;
+  if (col >= jb.ncols) return;
 #pragma unroll
-  for (int rr = 0; rr < R / 4; ++rr) {
-    const int r = w * (R / 4) + rr;
-    float v = red[0][lane][r];
+  for (int r = 0; r < R; ++r) {
+    float v = red[0][r][threadIdx.x];
 #pragma unroll
-    for (int q = 1; q < NTH / 64; ++q) v += red[q][lane][r];
-    float* o = jb.out_is_B ? jb.out + (long long)c * R + r : jb.out + (long long)r * jb.ncols + c;
+    for (int q = 1; q < NTH / 64; ++q) v += red[q][r][threadIdx.x];
+    float* o = jb.out_is_B ? jb.out + (long long)col * R + r : jb.out + (long long)r * jb.ncols + col;
     *o = (accumulate ? *o : 0.f) + lscale * v;
   }
 }
@@ -199,6 +211,11 @@ hipError_t lora_grad(const LoraGradJob* jobs, const LoraGradPlan& plan, int laye
     set_error("lora_grad: %d layers, T=%d", layers, T);
     return hipErrorInvalidValue;
   }
+  for (int i = 0; i < kLoraJobs; ++i)
+    if (plan.ncols[i] % 4) {
+      set_error("lora_grad: job %d has %d columns (a multiple of 4 is required)", i, plan.ncols[i]);
+      return hipErrorInvalidValue;
+    }
   LoraGradGrid G{};
   for (int i = 0; i < kLoraJobs; ++i)
     G.block_start[i + 1] = G.block_start[i] + (plan.ncols[i] + GC - 1) / GC;

@@ -20,6 +20,8 @@
 // next to the operand and the consuming epilogue multiplies the GEMM result
 // row by it.  The scale is a power of two, so applying and removing it is
 // exact in fp32.
+#include <stdlib.h>
+
 #include "ops.h"
 
 namespace llmt {
@@ -227,16 +229,21 @@ __global__ __launch_bounds__(RT) void embed_norm_kernel(const int* __restrict__ 
 // (src/kernels/rmsnorm.cu:36-41 with 128-wide rows) and half-split RoPE
 // (src/kernels/rope.cu:7-27): lane l of a wave owns the rotation pair
 // (l, l + 64).  Writes q, k (normed, rotated) and v as fp16 [T, Q + 2 KV].
-template <int P>
-__global__ __launch_bounds__(RT) void qkv_post_kernel(const QkvPostArgs a) {
+template <int P, bool MULTI>
+__global__ __launch_bounds__(RT) void qkv_post_kernel(const QkvPostArgs a, int T, int rpw) {
   extern __shared__ float ys[];  // [NT]
   __shared__ float hs[64];
-  const int t = blockIdx.x;
   const int Q = a.nq * HD, KV = a.nkv * HD, NT = Q + 2 * KV;
+  LoraRegs<P, 1> L;
+  if constexpr (MULTI) lora_load<P, 1>(a.in, NT, L);
+  const int nrows = MULTI ? rpw : 1;
+  for (int it = 0; it < nrows; ++it) {
+  const int t = blockIdx.x * nrows + it;
+  if (t >= T) break;
+  if (it) __syncthreads();
   float4 v[P], hv;
   load_row<P, true>(a.in, t, NT, v, hv);
-  LoraRegs<P, 1> L;
-  lora_load<P, 1>(a.in, NT, L);
+  if constexpr (!MULTI) lora_load<P, 1>(a.in, NT, L);
   store_h(a.in, hv, hs);
   if ((int)threadIdx.x < a.in.nh / 4)
     *reinterpret_cast<float4*>(a.hbuf + (long long)t * 64 + 4 * threadIdx.x) = hv;
@@ -265,32 +272,38 @@ __global__ __launch_bounds__(RT) void qkv_post_kernel(const QkvPostArgs a) {
     a.qkv16[(long long)t * NT + base + lane] = (_Float16)(y0 * cs - y1 * sn);
     a.qkv16[(long long)t * NT + base + 64 + lane] = (_Float16)(y1 * cs + y0 * sn);
   }
+  }
 }
 
 // After the O(+LoRA-A) GEMM (LoRA term added by its reduction):
 // x_mid = x_in + oW^T + s (o A^T) B^T (residual, src/kernels/elementwise.cu:
 // 4-15), stash h_o, then the FFN RMSNorm -> fp16.
-template <int P>
+template <int P, bool MULTI>
 __global__ __launch_bounds__(RT) void o_post_kernel(const RowIn in,
                                                     const float* __restrict__ x_in,
                                                     const float* __restrict__ w, float eps, int H,
                                                     float* __restrict__ hbuf,
                                                     float* __restrict__ x_mid,
-                                                    _Float16* __restrict__ xn2) {
+                                                    _Float16* __restrict__ xn2, int T, int rpw) {
   __shared__ float red[2 * RW];
   __shared__ float hs[64];
-  const int t = blockIdx.x;
-  float4 xi[P], wv[P];
+  float4 wv[P];
 #pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int c = min(4 * ((int)threadIdx.x + p * RT), H - 4);
-    xi[p] = ld4(x_in + (long long)t * H + c);
-    wv[p] = ld4(w + c);
-  }
+  for (int p = 0; p < P; ++p) wv[p] = ld4(w + min(4 * ((int)threadIdx.x + p * RT), H - 4));
+  LoraRegs<P, 1> L;
+  if constexpr (MULTI) lora_load<P, 1>(in, H, L);
+  const int nrows = MULTI ? rpw : 1;
+  for (int it = 0; it < nrows; ++it) {
+  const int t = blockIdx.x * nrows + it;
+  if (t >= T) break;
+  if (it) __syncthreads();
+  float4 xi[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+    xi[p] = ld4(x_in + (long long)t * H + min(4 * ((int)threadIdx.x + p * RT), H - 4));
   float4 v[P], hv;
   load_row<P, true>(in, t, H, v, hv);
-  LoraRegs<P, 1> L;
-  lora_load<P, 1>(in, H, L);
+  if constexpr (!MULTI) lora_load<P, 1>(in, H, L);
   store_h(in, hv, hs);
   if ((int)threadIdx.x < in.nh / 4)
     *reinterpret_cast<float4*>(hbuf + (long long)t * 64 + 3 * R + 4 * threadIdx.x) = hv;
@@ -313,6 +326,7 @@ __global__ __launch_bounds__(RT) void o_post_kernel(const RowIn in,
     st_h4(xn2 + (long long)t * H + c,
           make_float4(v[p].x * r * wv[p].x, v[p].y * r * wv[p].y, v[p].z * r * wv[p].z,
                       v[p].w * r * wv[p].w));
+  }
   }
 }
 
@@ -539,18 +553,25 @@ __global__ __launch_bounds__(RT) void swiglu_bwd_kernel(const RowIn in,
 // already added s (dh_o A_o)): d_o = row * rinv; writes d_o fp32 (attention
 // dO), dh_o, the row's max |d_o| and the flash-backward row statistic
 // delta[b, h, s] = sum_d dO * O.
-template <int P>
+template <int P, bool MULTI>
 __global__ __launch_bounds__(RT) void o_dx_post_kernel(const RowIn in,
                                                        const float* __restrict__ rinv_in,
                                                        const _Float16* __restrict__ o16, int nq,
                                                        int S, float* __restrict__ dh_out,
                                                        float* __restrict__ dO,
                                                        float* __restrict__ delta,
-                                                       float* __restrict__ damax) {
+                                                       float* __restrict__ damax, int T,
+                                                       int rpw) {
   __shared__ float red[2 * RW];
   __shared__ float hs[64];
-  const int t = blockIdx.x;
   const int Q = nq * HD;
+  LoraRegs<P, 1> L;
+  if constexpr (MULTI) lora_load<P, 1>(in, Q, L);
+  const int nrows = MULTI ? rpw : 1;
+  for (int it = 0; it < nrows; ++it) {
+  const int t = blockIdx.x * nrows + it;
+  if (t >= T) break;
+  if (it) __syncthreads();
   half4 ov[P];
 #pragma unroll
   for (int p = 0; p < P; ++p) {
@@ -560,8 +581,7 @@ __global__ __launch_bounds__(RT) void o_dx_post_kernel(const RowIn in,
   const float rs = rinv_in[t];
   float4 v[P], hv;
   load_row<P, true>(in, t, Q, v, hv);
-  LoraRegs<P, 1> L;
-  lora_load<P, 1>(in, Q, L);
+  if constexpr (!MULTI) lora_load<P, 1>(in, Q, L);
   store_h(in, hv, hs);
   if ((int)threadIdx.x < in.nh / 4)
     *reinterpret_cast<float4*>(dh_out + (long long)t * 64 + 3 * R + 4 * threadIdx.x) = mul4(hv, rs);
@@ -588,6 +608,7 @@ __global__ __launch_bounds__(RT) void o_dx_post_kernel(const RowIn in,
   }
   amax = block_max<RW>(amax, red);
   if (threadIdx.x == 0) damax[t] = amax;
+  }
 }
 
 // Attention gradients (w.r.t. the normed, rotated q/k and v) -> RoPE
@@ -705,6 +726,24 @@ inline unsigned grid_elems(long long n) {
 
 }  // namespace
 
+// Token rows per workgroup of the one-term LoRA epilogues: the adapter
+// shadows (16 x 4 fp16 values per column piece) are loaded into registers
+// once per workgroup and reused for every row, keeping at least 512
+// workgroups.  Only for rows of at most 2 pieces per thread (P): wider rows
+// kept beside the shadows across the loop spill.  1 selects the one-row
+// kernel (shadows loaded per row).  LLMT_ROWS_PER_WG overrides for tuning.
+static int rows_per_wg(int T, int P) {
+  if (P > 2) return 1;
+  const char* e = getenv("LLMT_ROWS_PER_WG");
+  if (e && *e) {
+    const int v = atoi(e);
+    if (v >= 1 && v <= 64) return v;
+  }
+  int r = 1;
+  while (r < 8 && T / (2 * r) >= 512) r *= 2;
+  return r;
+}
+
 static bool row_in_ok(const RowIn& in, int n, const char* who) {
   bool ok = in.nh % 4 == 0 && in.nh >= 0 && in.nh <= 64 && in.nterm >= 0 && in.nterm <= 3 &&
             n % 4 == 0 && in.ldp % 4 == 0 && in.split >= 1 && (in.split == 1 || in.ss % 4 == 0) &&
@@ -756,11 +795,19 @@ hipError_t qkv_post(const QkvPostArgs& a, int T, hipStream_t st) {
   const int NT = (a.nq + 2 * a.nkv) * HD;
   if (!row_in_ok(a.in, NT, "qkv_post")) return hipErrorInvalidValue;
   const int P = (NT + 4 * RT - 1) / (4 * RT);
+  const int rpw = rows_per_wg(T, P);
+  const dim3 g((T + rpw - 1) / rpw);
   switch (P) {
-    case 1: hipLaunchKernelGGL(qkv_post_kernel<1>, dim3(T), dim3(RT), NT * sizeof(float), st, a); break;
-    case 2: hipLaunchKernelGGL(qkv_post_kernel<2>, dim3(T), dim3(RT), NT * sizeof(float), st, a); break;
-    case 3: hipLaunchKernelGGL(qkv_post_kernel<3>, dim3(T), dim3(RT), NT * sizeof(float), st, a); break;
-    case 4: hipLaunchKernelGGL(qkv_post_kernel<4>, dim3(T), dim3(RT), NT * sizeof(float), st, a); break;
+    case 1:
+      if (rpw > 1) hipLaunchKernelGGL((qkv_post_kernel<1, true>), g, dim3(RT), NT * sizeof(float), st, a, T, rpw);
+      else hipLaunchKernelGGL((qkv_post_kernel<1, false>), g, dim3(RT), NT * sizeof(float), st, a, T, rpw);
+      break;
+    case 2:
+      if (rpw > 1) hipLaunchKernelGGL((qkv_post_kernel<2, true>), g, dim3(RT), NT * sizeof(float), st, a, T, rpw);
+      else hipLaunchKernelGGL((qkv_post_kernel<2, false>), g, dim3(RT), NT * sizeof(float), st, a, T, rpw);
+      break;
+    case 3: hipLaunchKernelGGL((qkv_post_kernel<3, false>), g, dim3(RT), NT * sizeof(float), st, a, T, rpw); break;
+    case 4: hipLaunchKernelGGL((qkv_post_kernel<4, false>), g, dim3(RT), NT * sizeof(float), st, a, T, rpw); break;
     default:
       set_error("qkv_post: row width %d above %d", NT, 16 * RT);
       return hipErrorInvalidValue;
@@ -774,11 +821,19 @@ hipError_t o_post(const RowIn& in, const float* x_in, const float* w, float eps,
                   float* hbuf, float* x_mid, _Float16* xn2, hipStream_t st) {
   if (!row_in_ok(in, H, "o_post")) return hipErrorInvalidValue;
   const int P = (H + 4 * RT - 1) / (4 * RT);
+  const int rpw = rows_per_wg(T, P);
+  const dim3 g((T + rpw - 1) / rpw);
   switch (P) {
-    case 1: hipLaunchKernelGGL(o_post_kernel<1>, dim3(T), dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2); break;
-    case 2: hipLaunchKernelGGL(o_post_kernel<2>, dim3(T), dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2); break;
-    case 3: hipLaunchKernelGGL(o_post_kernel<3>, dim3(T), dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2); break;
-    case 4: hipLaunchKernelGGL(o_post_kernel<4>, dim3(T), dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2); break;
+    case 1:
+      if (rpw > 1) hipLaunchKernelGGL((o_post_kernel<1, true>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T, rpw);
+      else hipLaunchKernelGGL((o_post_kernel<1, false>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T, rpw);
+      break;
+    case 2:
+      if (rpw > 1) hipLaunchKernelGGL((o_post_kernel<2, true>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T, rpw);
+      else hipLaunchKernelGGL((o_post_kernel<2, false>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T, rpw);
+      break;
+    case 3: hipLaunchKernelGGL((o_post_kernel<3, false>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T, rpw); break;
+    case 4: hipLaunchKernelGGL((o_post_kernel<4, false>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T, rpw); break;
     default:
       set_error("o_post: row width %d above %d", H, 16 * RT);
       return hipErrorInvalidValue;
@@ -878,11 +933,19 @@ hipError_t o_dx_post(const RowIn& in, const float* rinv_in, const _Float16* o16,
   const int Q = nq * HD;
   if (!row_in_ok(in, Q, "o_dx_post")) return hipErrorInvalidValue;
   const int P = (Q + 4 * RT - 1) / (4 * RT);
+  const int rpw = rows_per_wg(T, P);
+  const dim3 g((T + rpw - 1) / rpw);
   switch (P) {
-    case 1: hipLaunchKernelGGL(o_dx_post_kernel<1>, dim3(T), dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO, delta, damax); break;
-    case 2: hipLaunchKernelGGL(o_dx_post_kernel<2>, dim3(T), dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO, delta, damax); break;
-    case 3: hipLaunchKernelGGL(o_dx_post_kernel<3>, dim3(T), dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO, delta, damax); break;
-    case 4: hipLaunchKernelGGL(o_dx_post_kernel<4>, dim3(T), dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO, delta, damax); break;
+    case 1:
+      if (rpw > 1) hipLaunchKernelGGL((o_dx_post_kernel<1, true>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO, delta, damax, T, rpw);
+      else hipLaunchKernelGGL((o_dx_post_kernel<1, false>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO, delta, damax, T, rpw);
+      break;
+    case 2:
+      if (rpw > 1) hipLaunchKernelGGL((o_dx_post_kernel<2, true>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO, delta, damax, T, rpw);
+      else hipLaunchKernelGGL((o_dx_post_kernel<2, false>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO, delta, damax, T, rpw);
+      break;
+    case 3: hipLaunchKernelGGL((o_dx_post_kernel<3, false>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO, delta, damax, T, rpw); break;
+    case 4: hipLaunchKernelGGL((o_dx_post_kernel<4, false>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO, delta, damax, T, rpw); break;
     default:
       set_error("o_dx_post: row width %d above %d", Q, 16 * RT);
       return hipErrorInvalidValue;

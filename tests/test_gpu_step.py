@@ -120,3 +120,17 @@ def test_small_model_matches_golden_fixture(small, dev):
     got = ctx.lora_get("grad").cpu().double()
     w = torch.from_numpy(want["grads"]).double()
     assert float((got - w).norm() / w.norm()) < GRAD_TOL
+
+
+@pytest.mark.parametrize("rows", ["3", "8"])
+def test_rows_per_workgroup(small, monkeypatch, rows):
+    """The row epilogues with LoRA terms looping over several token rows per
+    workgroup (adapter shadows loaded once), including a partial last group
+    (128 rows / 3), give the same step as the oracle."""
+    monkeypatch.setenv("LLMT_ROWS_PER_WG", rows)
+    ctx = small["ctx"]
+    ctx.set_graph(False)
+    loss = ctx.forward_backward(small["tok"], small["tgt"])
+    assert abs(loss - small["loss_ref"]) < LOSS_TOL
+    errs = grad_errors(ctx.lora_get("grad"), small["grads_ref"], SMALL)
+    assert max(errs.values()) < GRAD_TOL
