@@ -220,12 +220,12 @@ int llmt_attention_bwd(const void* q, const void* k, const void* v, const void* 
   const int T = B * S;
   Temps tmp(st);
   float* delta = tmp.get<float>((size_t)B * nq * S);
-  float* damax = tmp.get<float>(T);
+  float* dsc = tmp.get<float>(T);
   float* dkvp = tmp.get<float>((size_t)T * 2 * nq * kHeadDim);
   _Float16* dO16 = tmp.get<_Float16>((size_t)T * nq * kHeadDim);
-  TRY_ARG(delta && damax && dkvp && dO16, "llmt_attention_bwd: out of memory");
+  TRY_ARG(delta && dsc && dkvp && dO16, "llmt_attention_bwd: out of memory");
   const long long ldq = (long long)nq * kHeadDim, ldkv = (long long)nkv * kHeadDim;
-  TRY_HIP(attn_delta(dout, ldq, (const _Float16*)o, ldq, nq, S, T, delta, damax, st));
+  TRY_HIP(attn_delta(dout, ldq, (const _Float16*)o, ldq, nq, S, T, delta, dO16, ldq, dsc, st));
   AttnArgs a{};
   a.q = (const _Float16*)q;
   a.ldq = ldq;
@@ -238,12 +238,10 @@ int llmt_attention_bwd(const void* q, const void* k, const void* v, const void* 
   a.S = S;
   a.sm_scale = 1.0f / sqrtf((float)kHeadDim);
   a.lse = const_cast<float*>(lse);  // read-only in the backward
-  a.dO = dout;
-  a.lddo = ldq;
-  a.delta = delta;
-  a.damax = damax;
   a.dO16 = dO16;
   a.ld16 = ldq;
+  a.dsc = dsc;
+  a.delta = delta;
   a.dq = dq;
   a.ldgq = ldq;
   a.dkvp = dkvp;
@@ -272,7 +270,7 @@ int llmt_attention_block_bwd(const void* q_raw, const void* k_raw, const void* v
   float* lse = tmp.get<float>((size_t)B * nq * S);
   float* dO = tmp.get<float>((size_t)T * Q);
   float* delta = tmp.get<float>((size_t)B * nq * S);
-  float* damax = tmp.get<float>(T);
+  float* dsc = tmp.get<float>(T);
   float* dqkv = tmp.get<float>((size_t)T * NT);
   float* dkvp = tmp.get<float>((size_t)T * 2 * Q);
   _Float16* dO16 = tmp.get<_Float16>((size_t)T * Q);
@@ -281,7 +279,7 @@ int llmt_attention_block_bwd(const void* q_raw, const void* k_raw, const void* v
   float* rinv = tmp.get<float>(T);
   float* cosT = tmp.get<float>((size_t)S * 64);
   float* sinT = tmp.get<float>((size_t)S * 64);
-  TRY_ARG(raw16 && qkv16 && qkraw && o16 && lse && dO && delta && damax && dqkv && dkvp && dO16 &&
+  TRY_ARG(raw16 && qkv16 && qkraw && o16 && lse && dO && delta && dsc && dqkv && dkvp && dO16 &&
               dy && g16 && rinv && cosT && sinT,
           "llmt_attention_block_bwd: out of memory");
   TRY_HIP(rope_tables(S, (double)theta, cosT, sinT, st));
@@ -308,13 +306,11 @@ int llmt_attention_block_bwd(const void* q_raw, const void* k_raw, const void* v
   a.lse = lse;
   TRY_HIP(attn_fwd(a, B, st));
   TRY_HIP(f16_to_f32_rows((const _Float16*)dout, Q, T, Q, dO, Q, st));
-  TRY_HIP(attn_delta(dO, Q, o16, Q, nq, S, T, delta, damax, st));
-  a.dO = dO;
-  a.lddo = Q;
-  a.delta = delta;
-  a.damax = damax;
+  TRY_HIP(attn_delta(dO, Q, o16, Q, nq, S, T, delta, dO16, Q, dsc, st));
   a.dO16 = dO16;
   a.ld16 = Q;
+  a.dsc = dsc;
+  a.delta = delta;
   a.dq = dqkv;
   a.ldgq = NT;
   a.dkvp = dkvp;

@@ -1,9 +1,12 @@
 // attn.hip — causal GQA flash attention (head_dim 128) on fp16 MFMA for
 // gfx950: forward (keeps the fp32 log-sum-exp instead of P) and a
-// deterministic backward in two launches (dQ per query block, which also
-// writes the scaled fp16 dO; then dK/dV per key block and query head, the
-// query heads of a GQA group summed by the consumer in a fixed order), both
-// recomputing P from Q, K and the LSE.
+// deterministic backward in one launch (dQ per query block beside dK/dV per
+// key block and query head, the query heads of a GQA group summed by the
+// consumer in a fixed order), recomputing P from Q, K and the LSE.  The
+// backward takes dO as fp16 rows each scaled by its own power of two (the
+// producer's row epilogue writes them with the inverse scales): dQ works in
+// each row's own scale, dK and dV, which mix rows, bring each row to its
+// batch's common scale on the fly.
 //
 // Replaces the reference's naive_attn_kernel (src/kernels/lora_forward.cu:
 // 48-135, which stores P [heads, S, S] in fp32), attn_backward_kernel
@@ -158,27 +161,16 @@ __device__ __forceinline__ half8 frag_global(const _Float16* base, long long ld,
   return row < n ? x : half8{};
 }
 
-__device__ __forceinline__ half8 frag_global_f32(const float* base, long long ld, int row, int n,
-                                                 int ks, int lane, float scale) {
-  const float4* p =
-      reinterpret_cast<const float4*>(base + (long long)min(row, n - 1) * ld + ks * 32 + (lane >> 4) * 8);
-  const float4 a = p[0], b = p[1];
-  half8 r;
-  r[0] = (_Float16)(a.x * scale); r[1] = (_Float16)(a.y * scale);
-  r[2] = (_Float16)(a.z * scale); r[3] = (_Float16)(a.w * scale);
-  r[4] = (_Float16)(b.x * scale); r[5] = (_Float16)(b.y * scale);
-  r[6] = (_Float16)(b.z * scale); r[7] = (_Float16)(b.w * scale);
-  return row < n ? r : half8{};
-}
-
-// Power-of-two scale for the fp16 dO operand of batch b: from the per-row
-// max |dO| of the batch's S rows.  Identical in every workgroup of b.
+// Common power-of-two scale of batch b's fp16 dO rows: the reciprocal of the
+// largest per-row inverse scale (all-zero rows store 0), 1 when every row is
+// zero.  Identical in every workgroup of b.  Row t enters the products
+// times r_t = gs * dsc[t] <= 1, which brings it to this common scale.
 template <int NT>
-__device__ float batch_do_scale(const float* __restrict__ damax, int b, int S, float* red) {
+__device__ float batch_do_scale(const float* __restrict__ dsc, int b, int S, float* red) {
   float m = 0.f;
-  for (int s = threadIdx.x; s < S; s += NT) m = fmaxf(m, damax[(long long)b * S + s]);
+  for (int s = threadIdx.x; s < S; s += NT) m = fmaxf(m, dsc[(long long)b * S + s]);
   m = block_max<NT / 64>(m, red);
-  return pow2_scale_for(m);
+  return m > 0.f ? 1.0f / m : 1.0f;
 }
 
 // ---------------------------------------------------------------- forward
@@ -357,17 +349,15 @@ __device__ __forceinline__ void ds_tile_q(const floatx4 (&pt)[RW][4], floatx4 (&
   }
 }
 
-// Same tiling as the forward.  Also writes dO * gs in fp16 (gs the batch's
-// power-of-two dO scale) to a.dO16 for the dK/dV launch.
+// Query block qb of head h, batch b: the forward's tiling (LDS: two
+// buffers of K and V tiles, 4 TILE halves).  dQ row q depends on dO row q
+// only, so each row stays in its own dO scale 1 / dsc[q] throughout.
 template <int NW, int RW>
-__global__ __launch_bounds__(NW * 64) void attn_dq_kernel(const AttnArgs a) {
-  constexpr int NT = NW * 64, QB = NW * RW * 16;
-  __shared__ __attribute__((aligned(1024))) _Float16 smem[4 * TILE];
-  __shared__ float red[NW];
+__device__ __forceinline__ void dq_block(const AttnArgs& a, _Float16* smem, int qb, int h, int b) {
+  constexpr int QB = NW * RW * 16;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, g = lane >> 4;
-  const int qb = gridDim.x - 1 - blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int S = a.S;
   const int kvh = h / (a.nq / a.nkv);
   const long long rowb = (long long)b * S;
@@ -382,26 +372,21 @@ __global__ __launch_bounds__(NW * 64) void attn_dq_kernel(const AttnArgs a) {
   dv.init(a.ldv, w);
   dk.issue(kbase, a.ldk, 0, S, smem, w);
   dv.issue(vbase, a.ldv, 0, S, smem + TILE, w);
-  const float gs = batch_do_scale<NT>(a.damax, b, S, red);
-
   half8 qf[RW][4], df[RW][4];
-  float lse2[RW], del[RW];
+  float lse2[RW], del[RW], fq[RW];
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
     const int q = q0 + 16 * r + c;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       qf[r][ks] = frag_global(a.q + rowb * a.ldq + h * HD, a.ldq, q, S, ks, lane);
-      df[r][ks] = frag_global_f32(a.dO + rowb * a.lddo + h * HD, a.lddo, q, S, ks, lane, gs);
+      df[r][ks] = frag_global(a.dO16 + rowb * a.ld16 + h * HD, a.ld16, q, S, ks, lane);
     }
     const bool ok = q < S;
-    if (ok) {
-      _Float16* d16 = a.dO16 + (rowb + q) * a.ld16 + h * HD + (lane >> 4) * 8;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) *reinterpret_cast<half8*>(d16 + ks * 32) = df[r][ks];
-    }
     lse2[r] = ok ? a.lse[((long long)b * a.nq + h) * S + q] * LOG2E : 0.f;
-    del[r] = ok ? a.delta[((long long)b * a.nq + h) * S + q] * gs : 0.f;
+    const float dsc = ok ? a.dsc[rowb + q] : 0.f;
+    del[r] = dsc > 0.f ? a.delta[((long long)b * a.nq + h) * S + q] / dsc : 0.f;
+    fq[r] = a.sm_scale * dsc;
   }
   floatx4 dqT[RW][8];
 #pragma unroll
@@ -456,10 +441,10 @@ __global__ __launch_bounds__(NW * 64) void attn_dq_kernel(const AttnArgs a) {
       }
     }
   }
-  const float f = a.sm_scale / gs;
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
     const int q = q0 + 16 * r + c;
+    const float f = fq[r];
     if (q < S) {
       float* dq = a.dq + (rowb + q) * a.ldgq + h * HD;
 #pragma unroll
@@ -471,18 +456,23 @@ __global__ __launch_bounds__(NW * 64) void attn_dq_kernel(const AttnArgs a) {
 }
 
 // ---------------------------------------------------------------- dK, dV
-// P and dS for one 64-query tile (rows query, column key).
+// P and dS for one 64-query tile (rows query, column key), both in the
+// batch's dO scale gs: ds arrives in each query row's own dO scale, so row
+// q's factor r = gs * dsc[q] brings dP there, and P times r is the operand
+// against the row-scaled dO16 of dV.
 template <bool MASK>
 __device__ __forceinline__ void ds_tile_kv(floatx4 (&p)[4], floatx4 (&ds)[4], const float* lse_s,
-                                           const float* del_s, float sl2, float gs, int qq0, int key,
-                                           int S, int lane) {
+                                           const float* del_s, const float* dsc_s, float sl2,
+                                           float gs, int qq0, int key, int S, int lane) {
   const int g = lane >> 4;
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
     const float4 ls = *reinterpret_cast<const float4*>(lse_s + mt * 16 + 4 * g);
     const float4 dl = *reinterpret_cast<const float4*>(del_s + mt * 16 + 4 * g);
+    const float4 sc = *reinterpret_cast<const float4*>(dsc_s + mt * 16 + 4 * g);
     const float lv[4] = {ls.x, ls.y, ls.z, ls.w};
     const float dv[4] = {dl.x, dl.y, dl.z, dl.w};
+    const float rv[4] = {sc.x * gs, sc.y * gs, sc.z * gs, sc.w * gs};
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       float pv = __builtin_amdgcn_exp2f(fmaf(p[mt][v], sl2, -lv[v] * LOG2E));
@@ -490,8 +480,8 @@ __device__ __forceinline__ void ds_tile_kv(floatx4 (&p)[4], floatx4 (&ds)[4], co
         const int qq = qq0 + mt * 16 + 4 * g + v;
         pv = (key <= qq && qq < S) ? pv : 0.f;
       }
-      p[mt][v] = pv;
-      ds[mt][v] = pv * fmaf(-dv[v], gs, ds[mt][v]);
+      p[mt][v] = pv * rv[v];
+      ds[mt][v] = pv * fmaf(ds[mt][v], rv[v], -dv[v] * gs);
     }
   }
 }
@@ -499,18 +489,18 @@ __device__ __forceinline__ void ds_tile_kv(floatx4 (&p)[4], floatx4 (&ds)[4], co
 // grid (ceil(S / (16 NW)), nq, B): workgroup (key block kb of 16 NW keys,
 // query head h); wave w owns keys k0 + 16 w + c and loops over the 64-query
 // tiles at or after the block.  LDS: two buffers of (Q tile, dO16 tile,
-// lse[64], delta[64]).  Writes this query head's share of dK, dV (fp32) to
-// a.dkvp.
+// lse[64], delta[64], dsc[64]).  Writes this query head's share of dK, dV
+// (fp32) to a.dkvp.
+constexpr int KV_BUF = 2 * TILE + 3 * BLK * 2;  // halves per dK/dV buffer
+
 template <int NW>
-__global__ __launch_bounds__(NW * 64) void attn_dkdv_kernel(const AttnArgs a) {
+__device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* smem, float* red, int kb,
+                                           int h, int b) {
   constexpr int NT = NW * 64, KB = NW * 16;
-  constexpr int BUF = 2 * TILE + 2 * BLK * 2;  // halves per buffer
-  __shared__ __attribute__((aligned(1024))) _Float16 smem[2 * BUF];
-  __shared__ float red[NW];
+  constexpr int BUF = KV_BUF;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, g = lane >> 4;
-  const int kb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int S = a.S;
   const int kvh = h / (a.nq / a.nkv);
   const long long rowb = (long long)b * S;
@@ -519,6 +509,7 @@ __global__ __launch_bounds__(NW * 64) void attn_dkdv_kernel(const AttnArgs a) {
   const float sl2 = a.sm_scale * LOG2E;
   const float* lse_h = a.lse + ((long long)b * a.nq + h) * S;
   const float* del_h = a.delta + ((long long)b * a.nq + h) * S;
+  const float* dsc_b = a.dsc + rowb;
   const _Float16* qbase = a.q + rowb * a.ldq + h * HD;
   const _Float16* dbase = a.dO16 + rowb * a.ld16 + h * HD;
   const int qb0 = (kb * KB) / BLK;
@@ -532,9 +523,10 @@ __global__ __launch_bounds__(NW * 64) void attn_dkdv_kernel(const AttnArgs a) {
     float* vec = reinterpret_cast<float*>(buf + 2 * TILE);
     if (w == 0) dma_vec64(lse_h, qb * BLK, S, vec);
     if (w == NW - 1) dma_vec64(del_h, qb * BLK, S, vec + BLK);
+    if (w == NW / 2) dma_vec64(dsc_b, qb * BLK, S, vec + 2 * BLK);
   };
   issue(qb0, smem);
-  const float gs = batch_do_scale<NT>(a.damax, b, S, red);
+  const float gs = batch_do_scale<NT>(a.dsc, b, S, red);
   half8 kf[4], vf[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
@@ -557,6 +549,7 @@ __global__ __launch_bounds__(NW * 64) void attn_dkdv_kernel(const AttnArgs a) {
     const _Float16* Ds = buf + TILE;
     const float* lse_s = reinterpret_cast<const float*>(buf + 2 * TILE);
     const float* del_s = lse_s + BLK;
+    const float* dsc_s = lse_s + 2 * BLK;
     floatx4 p[4], ds[4];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
@@ -570,9 +563,9 @@ __global__ __launch_bounds__(NW * 64) void attn_dkdv_kernel(const AttnArgs a) {
     }
     // every query of the tile >= every key of the wave and < S: no mask
     if (qb * BLK >= k0 + 15 && qb * BLK + BLK <= S)
-      ds_tile_kv<false>(p, ds, lse_s, del_s, sl2, gs, qb * BLK, key, S, lane);
+      ds_tile_kv<false>(p, ds, lse_s, del_s, dsc_s, sl2, gs, qb * BLK, key, S, lane);
     else
-      ds_tile_kv<true>(p, ds, lse_s, del_s, sl2, gs, qb * BLK, key, S, lane);
+      ds_tile_kv<true>(p, ds, lse_s, del_s, dsc_s, sl2, gs, qb * BLK, key, S, lane);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const half8 pb = pair_frag(p[2 * j], p[2 * j + 1]);
@@ -600,6 +593,23 @@ __global__ __launch_bounds__(NW * 64) void attn_dkdv_kernel(const AttnArgs a) {
   }
 }
 
+// The whole attention backward of a launch: blocks [0, nkvb) of x are dK/dV
+// key blocks (most work first), the next nqb dQ query blocks (last, i.e.
+// longest, first).  The two halves share no outputs, so one launch runs
+// them side by side; a launch with nkvb or nqb = 0 runs one half.
+constexpr int BWD_SMEM = 2 * KV_BUF > 4 * TILE ? 2 * KV_BUF : 4 * TILE;
+
+template <int NW, int RW>
+__global__ __launch_bounds__(NW * 64) void attn_bwd_kernel(const AttnArgs a, int nkvb, int nqb) {
+  __shared__ __attribute__((aligned(1024))) _Float16 smem[BWD_SMEM];
+  __shared__ float red[NW];
+  const int x = blockIdx.x;
+  if (x < nkvb)
+    dkdv_block<NW>(a, smem, red, x, blockIdx.y, blockIdx.z);
+  else
+    dq_block<NW, RW>(a, smem, nqb - 1 - (x - nkvb), blockIdx.y, blockIdx.z);
+}
+
 // dK, dV = sum over the query heads of each group of the per-head shares
 // (group order, deterministic).
 __global__ __launch_bounds__(256) void gqa_sum_kernel(const float* __restrict__ dkvp, int nq,
@@ -623,12 +633,14 @@ __global__ __launch_bounds__(256) void gqa_sum_kernel(const float* __restrict__ 
 }
 
 // Per token row: delta[b, h, s] = sum_d dO[t, h, d] * O[t, h, d] (one wave
-// per head) and damax[t] = max |dO[t, :]|.
+// per head), then dO16[t] = fp16(dO[t] * sc) with sc the power-of-two scale
+// of max |dO[t, :]| and dsc[t] = 1 / sc (0 for an all-zero row).
 __global__ __launch_bounds__(256) void attn_delta_kernel(const float* __restrict__ dO, long long ldd,
                                                          const _Float16* __restrict__ o,
                                                          long long ldo, int nq, int S,
                                                          float* __restrict__ delta,
-                                                         float* __restrict__ damax) {
+                                                         _Float16* __restrict__ dO16,
+                                                         long long ld16, float* __restrict__ dsc) {
   __shared__ float red[4];
   const int t = blockIdx.x;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -643,7 +655,14 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(const float* __restrict
     if (lane == 0) delta[((long long)b * nq + h) * S + s] = v;
   }
   amax = block_max<4>(amax, red);
-  if (threadIdx.x == 0) damax[t] = amax;
+  const float sc = pow2_scale_for(amax, kDoScaleExp);
+  if (threadIdx.x == 0) dsc[t] = pow2_inv_scale_for(amax, kDoScaleExp);
+  for (int h = w; h < nq; h += 4) {
+    const float* d = dO + (long long)t * ldd + h * HD;
+    _Float16* d16 = dO16 + (long long)t * ld16 + h * HD;
+    d16[lane] = (_Float16)(d[lane] * sc);
+    d16[lane + 64] = (_Float16)(d[lane + 64] * sc);
+  }
 }
 
 // Launch shape: NW waves of RW 16-row tiles.  Two tiles a wave halve the LDS
@@ -675,23 +694,46 @@ void launch_fwd(const AttnArgs& a, int B, hipStream_t st) {
                      0, st, a);
 }
 template <int NW, int RW>
-void launch_dq(const AttnArgs& a, int B, hipStream_t st) {
-  constexpr int QB = NW * RW * 16;
-  hipLaunchKernelGGL((attn_dq_kernel<NW, RW>), dim3((a.S + QB - 1) / QB, a.nq, B), dim3(NW * 64),
-                     0, st, a);
+void launch_bwd(const AttnArgs& a, int B, int nkvb, int nqb, hipStream_t st) {
+  hipLaunchKernelGGL((attn_bwd_kernel<NW, RW>), dim3(nkvb + nqb, a.nq, B), dim3(NW * 64), 0, st, a,
+                     nkvb, nqb);
 }
-template <int NW>
-void launch_dkdv(const AttnArgs& a, int B, hipStream_t st) {
-  hipLaunchKernelGGL((attn_dkdv_kernel<NW>), dim3((a.S + NW * 16 - 1) / (NW * 16), a.nq, B),
-                     dim3(NW * 64), 0, st, a);
+// dK/dV key blocks of nwk waves and dQ query blocks of nwq waves x rw tiles:
+// one launch when the wave counts agree, else one launch each.
+void launch_attn_bwd(const AttnArgs& a, int B, int nwk, int nwq, int rw, hipStream_t st) {
+  const int nkvb = (a.S + nwk * 16 - 1) / (nwk * 16);
+  const int nqb = (a.S + nwq * rw * 16 - 1) / (nwq * rw * 16);
+  auto dq_only = [&](int n) {
+    switch (nwq * 10 + rw) {
+      case 42: launch_bwd<4, 2>(a, B, 0, n, st); break;
+      case 41: launch_bwd<4, 1>(a, B, 0, n, st); break;
+      case 22: launch_bwd<2, 2>(a, B, 0, n, st); break;
+      default: launch_bwd<2, 1>(a, B, 0, n, st); break;
+    }
+  };
+  if (nwk == nwq) {
+    switch (nwq * 10 + rw) {
+      case 42: launch_bwd<4, 2>(a, B, nkvb, nqb, st); break;
+      case 41: launch_bwd<4, 1>(a, B, nkvb, nqb, st); break;
+      case 22: launch_bwd<2, 2>(a, B, nkvb, nqb, st); break;
+      default: launch_bwd<2, 1>(a, B, nkvb, nqb, st); break;
+    }
+    return;
+  }
+  if (nwk == 4)
+    launch_bwd<4, 1>(a, B, nkvb, 0, st);
+  else
+    launch_bwd<2, 1>(a, B, nkvb, 0, st);
+  dq_only(nqb);
 }
 
 }  // namespace
 
 hipError_t attn_delta(const float* dO, long long ldd, const _Float16* o, long long ldo, int nq,
-                      int S, int T, float* delta, float* damax, hipStream_t st) {
+                      int S, int T, float* delta, _Float16* dO16, long long ld16, float* dsc,
+                      hipStream_t st) {
   hipLaunchKernelGGL(attn_delta_kernel, dim3(T), dim3(256), 0, st, dO, ldd, o, ldo, nq, S, delta,
-                     damax);
+                     dO16, ld16, dsc);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
@@ -713,8 +755,8 @@ hipError_t attn_fwd(const AttnArgs& a, int B, hipStream_t st) {
 }
 
 hipError_t attn_bwd(const AttnArgs& a, int B, hipStream_t st) {
-  if (a.nq % a.nkv || a.S <= 0 || !a.dkvp || !a.dO16) {
-    set_error("attn_bwd: nq=%d nkv=%d S=%d (dK/dV share and fp16 dO buffers required)", a.nq,
+  if (a.nq % a.nkv || a.S <= 0 || !a.dkvp || !a.dO16 || !a.dsc) {
+    set_error("attn_bwd: nq=%d nkv=%d S=%d (dK/dV share, fp16 dO and its scales required)", a.nq,
               a.nkv, a.S);
     return hipErrorInvalidValue;
   }
@@ -723,17 +765,7 @@ hipError_t attn_bwd(const AttnArgs& a, int B, hipStream_t st) {
   // every S; LLMT_ATTN_CFG still selects any shape for tuning.
   AttnShape s = attn_shape(B, a.S, a.nq);
   if (!getenv("LLMT_ATTN_CFG")) s.rw = 1;
-  switch (s.nw * 10 + s.rw) {
-    case 42: launch_dq<4, 2>(a, B, st); break;
-    case 41: launch_dq<4, 1>(a, B, st); break;
-    case 22: launch_dq<2, 2>(a, B, st); break;
-    default: launch_dq<2, 1>(a, B, st); break;
-  }
-  LLMT_LAUNCH_CHECK();
-  if (dkdv_waves(B, a.S, a.nq) == 4)
-    launch_dkdv<4>(a, B, st);
-  else
-    launch_dkdv<2>(a, B, st);
+  launch_attn_bwd(a, B, dkdv_waves(B, a.S, a.nq), s.nw, s.rw, st);
   LLMT_LAUNCH_CHECK();
   if (a.dk && a.dv) {
     const long long n = (long long)B * a.S * a.nkv * HD;

@@ -80,14 +80,27 @@ __device__ __forceinline__ float block_max(float v, float* red) {
   return t;
 }
 
-// Power-of-two scale that maps a row maximum |x| into [2^13, 2^14): the fp16
-// gradient operands carry it per row and GEMM epilogues divide it back out
-// exactly.  amax == 0 gives scale 1.
-__device__ __forceinline__ float pow2_scale_for(float amax) {
+// Power-of-two scale that maps a row maximum |x| into [2^(E-1), 2^E): the
+// fp16 operands carry it per row and their consumers divide it back out
+// exactly.  GEMM operands use E = 14 (fp32 accumulation, no fp16 results);
+// amax == 0 or non-finite gives scale 1.
+__device__ __forceinline__ float pow2_scale_for(float amax, int E = 14) {
   if (!(amax > 0.f) || !isfinite(amax)) return 1.0f;
   int e;
   frexpf(amax, &e);  // amax = f * 2^e, f in [0.5, 1)
-  return ldexpf(1.0f, 14 - e);
+  return ldexpf(1.0f, E - e);
+}
+
+// The attention backward's fp16 dO rows: dS = P (dO V^T - delta), a sum of
+// 128 products of a dO row with V, is itself rounded to fp16, so dO rows
+// leave 2^5 of headroom under the GEMM operands' range.
+constexpr int kDoScaleExp = 9;
+
+// Inverse of a row scale as stored beside its scaled fp16 row (0 marks an
+// all-zero row, which contributes nothing whatever its scale); the largest
+// over a set of rows gives their common scale.
+__device__ __forceinline__ float pow2_inv_scale_for(float amax, int E = 14) {
+  return amax > 0.f ? 1.0f / pow2_scale_for(amax, E) : 0.f;
 }
 
 // Fragment-packed layout of a GEMM B operand [rows, K] (rows % 16 == 0,

@@ -116,7 +116,7 @@ struct Ctx {
   _Float16* g16 = nullptr;
   float *rinv = nullptr, *rinv2 = nullptr;
   _Float16* dgu16 = nullptr;
-  float *dO = nullptr, *delta = nullptr, *damax = nullptr;
+  float *delta = nullptr, *dsc = nullptr;
   float* dqkv32 = nullptr;
   // Per layer (kept until the adapter gradients of all layers run in one
   // launch after the backward): dy of the q/k/v projections [T, NT], dy of
@@ -129,7 +129,7 @@ struct Ctx {
   LoraGradPlan lora_plan{};
   hipError_t lora_grads(int l0, int nl, int B, int accumulate);
   float* dkvp = nullptr;  // [T, 2 Q]: per-query-head dK | dV shares
-  _Float16* dO16 = nullptr;  // [T, Q]: scaled fp16 dO of the attention backward
+  _Float16* dO16 = nullptr;  // [T, Q]: row-scaled fp16 dO of the attention backward
 
   // graph + profiling
   bool use_graph = false;

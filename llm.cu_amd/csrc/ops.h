@@ -179,8 +179,12 @@ hipError_t qk_norm_rope(const _Float16* raw, const float* qn, const float* kn, c
 hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st);
 hipError_t swiglu_bwd(const RowIn& in, const float* rinv_in, const float* gu, int I, int T,
                       _Float16* dgu16, float* rinv_out, hipStream_t st);
+// dX of the O projection -> the attention's dO operand: dO16 row t =
+// fp16(dO[t] * 2^k) with 2^k the row's power-of-two scale, dsc[t] = 2^-k (0
+// for an all-zero row), delta[b, h, s] = sum_d dO * O.
 hipError_t o_dx_post(const RowIn& in, const float* rinv_in, const _Float16* o16, int nq, int S,
-                     int T, float* dh_out, float* dO, float* delta, float* damax, hipStream_t st);
+                     int T, float* dh_out, _Float16* dO16, float* delta, float* dsc,
+                     hipStream_t st);
 hipError_t qk_bwd(const QkBwdArgs& a, int T, hipStream_t st);
 // x_out = x (may alias), xn = fp16(rmsnorm(x) * w): a layer input from fp32.
 hipError_t copy_norm(const float* x, const float* w, float eps, int H, int T, float* x_out,
@@ -209,12 +213,10 @@ struct AttnArgs {
   _Float16* o;          // forward output [T, ldo]
   long long ldo;
   float* lse;           // [B, nq, S] natural-log LSE of the scaled scores
-  const float* dO;      // backward: dO fp32 [T, lddo]
-  long long lddo;
+  const _Float16* dO16;  // backward: fp16 [T, ld16], row t = dO[t] / dsc[t]
+  long long ld16;
+  const float* dsc;     // [T] inverse power-of-two scale of dO16 row t (0: zero row)
   const float* delta;   // [B, nq, S] rowsum(dO * O)
-  const float* damax;   // [T] max |dO| per row
-  _Float16* dO16;       // backward scratch: dO times the batch's power-of-two
-  long long ld16;       //   scale, fp16 [T, ld16] (written by the dQ launch)
   float* dq;            // fp32 [T, ldgq]
   long long ldgq;
   float* dkvp;          // [T, 2 nq 128]: each query head's share of dK | dV
@@ -224,11 +226,12 @@ struct AttnArgs {
 };
 hipError_t attn_fwd(const AttnArgs& a, int B, hipStream_t st);
 hipError_t attn_bwd(const AttnArgs& a, int B, hipStream_t st);
-// Row statistics of a standalone attention backward: delta[b, h, s] =
-// sum_d dO * O and damax[t] = max |dO| over the row (dO fp32 [T, ldd],
-// O fp16 [T, ldo]).
+// Operands of a standalone attention backward from dO fp32 [T, ldd] and O
+// fp16 [T, ldo]: delta[b, h, s] = sum_d dO * O, dO16 [T, ld16] and dsc as
+// o_dx_post writes them.
 hipError_t attn_delta(const float* dO, long long ldd, const _Float16* o, long long ldo, int nq,
-                      int S, int T, float* delta, float* damax, hipStream_t st);
+                      int S, int T, float* delta, _Float16* dO16, long long ld16, float* dsc,
+                      hipStream_t st);
 
 // A one-thread kernel that returns after about `us` microseconds of device
 // wall clock (never more than a few times that: the wait loop is bounded).

@@ -550,17 +550,18 @@ __global__ __launch_bounds__(RT) void swiglu_bwd_kernel(const RowIn in,
 }
 
 // dX of the O projection (+ dh_o in the LoRA-B^T columns; the reduction
-// already added s (dh_o A_o)): d_o = row * rinv; writes d_o fp32 (attention
-// dO), dh_o, the row's max |d_o| and the flash-backward row statistic
+// already added s (dh_o A_o)): d_o = row * rinv; writes dh_o, the attention
+// backward's dO operand (fp16, scaled by the row's power of two, with the
+// inverse scale in dsc[t]) and the flash-backward row statistic
 // delta[b, h, s] = sum_d dO * O.
 template <int P, bool MULTI>
 __global__ __launch_bounds__(RT) void o_dx_post_kernel(const RowIn in,
                                                        const float* __restrict__ rinv_in,
                                                        const _Float16* __restrict__ o16, int nq,
                                                        int S, float* __restrict__ dh_out,
-                                                       float* __restrict__ dO,
+                                                       _Float16* __restrict__ dO16,
                                                        float* __restrict__ delta,
-                                                       float* __restrict__ damax, int T,
+                                                       float* __restrict__ dsc, int T,
                                                        int rpw) {
   __shared__ float red[2 * RW];
   __shared__ float hs[64];
@@ -594,10 +595,8 @@ __global__ __launch_bounds__(RT) void o_dx_post_kernel(const RowIn in,
     const int c = 4 * ((int)threadIdx.x + p * RT);
     const bool live = c < Q;
     const float4 d = mul4(v[p], rs);
-    if (live) {
-      *reinterpret_cast<float4*>(dO + (long long)t * Q + c) = d;
-      amax = fmaxf(amax, amax4(d));
-    }
+    v[p] = d;
+    if (live) amax = fmaxf(amax, amax4(d));
     // delta = sum over a head's 128 columns = 32 consecutive threads
     float part = live ? d.x * (float)ov[p][0] + d.y * (float)ov[p][1] + d.z * (float)ov[p][2] +
                             d.w * (float)ov[p][3]
@@ -607,7 +606,13 @@ __global__ __launch_bounds__(RT) void o_dx_post_kernel(const RowIn in,
     if (live && (threadIdx.x & 31) == 0) delta[((long long)b * nq + c / HD) * S + s] = part;
   }
   amax = block_max<RW>(amax, red);
-  if (threadIdx.x == 0) damax[t] = amax;
+  const float sc = pow2_scale_for(amax, kDoScaleExp);
+  if (threadIdx.x == 0) dsc[t] = pow2_inv_scale_for(amax, kDoScaleExp);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int c = 4 * ((int)threadIdx.x + p * RT);
+    if (c < Q) st_h4(dO16 + (long long)t * Q + c, mul4(v[p], sc));
+  }
   }
 }
 
@@ -929,7 +934,8 @@ hipError_t swiglu_bwd(const RowIn& in, const float* rinv_in, const float* gu, in
 }
 
 hipError_t o_dx_post(const RowIn& in, const float* rinv_in, const _Float16* o16, int nq, int S,
-                     int T, float* dh_out, float* dO, float* delta, float* damax, hipStream_t st) {
+                     int T, float* dh_out, _Float16* dO16, float* delta, float* dsc,
+                     hipStream_t st) {
   const int Q = nq * HD;
   if (!row_in_ok(in, Q, "o_dx_post")) return hipErrorInvalidValue;
   const int P = (Q + 4 * RT - 1) / (4 * RT);
@@ -937,15 +943,15 @@ hipError_t o_dx_post(const RowIn& in, const float* rinv_in, const _Float16* o16,
   const dim3 g((T + rpw - 1) / rpw);
   switch (P) {
     case 1:
-      if (rpw > 1) hipLaunchKernelGGL((o_dx_post_kernel<1, true>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO, delta, damax, T, rpw);
-      else hipLaunchKernelGGL((o_dx_post_kernel<1, false>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO, delta, damax, T, rpw);
+      if (rpw > 1) hipLaunchKernelGGL((o_dx_post_kernel<1, true>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO16, delta, dsc, T, rpw);
+      else hipLaunchKernelGGL((o_dx_post_kernel<1, false>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO16, delta, dsc, T, rpw);
       break;
     case 2:
-      if (rpw > 1) hipLaunchKernelGGL((o_dx_post_kernel<2, true>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO, delta, damax, T, rpw);
-      else hipLaunchKernelGGL((o_dx_post_kernel<2, false>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO, delta, damax, T, rpw);
+      if (rpw > 1) hipLaunchKernelGGL((o_dx_post_kernel<2, true>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO16, delta, dsc, T, rpw);
+      else hipLaunchKernelGGL((o_dx_post_kernel<2, false>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO16, delta, dsc, T, rpw);
       break;
-    case 3: hipLaunchKernelGGL((o_dx_post_kernel<3, false>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO, delta, damax, T, rpw); break;
-    case 4: hipLaunchKernelGGL((o_dx_post_kernel<4, false>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO, delta, damax, T, rpw); break;
+    case 3: hipLaunchKernelGGL((o_dx_post_kernel<3, false>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO16, delta, dsc, T, rpw); break;
+    case 4: hipLaunchKernelGGL((o_dx_post_kernel<4, false>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO16, delta, dsc, T, rpw); break;
     default:
       set_error("o_dx_post: row width %d above %d", Q, 16 * RT);
       return hipErrorInvalidValue;

@@ -258,12 +258,10 @@ AttnArgs Ctx::attn_args(const Stash& s) const {
   a.o = s.o16;
   a.ldo = Q;
   a.lse = s.lse;
-  a.dO = dO;
-  a.lddo = Q;
-  a.delta = delta;
-  a.damax = damax;
   a.dO16 = dO16;
   a.ld16 = Q;
+  a.dsc = dsc;
+  a.delta = delta;
   a.dq = dqkv32;
   a.ldgq = NT;
   a.dkvp = dkvp;
@@ -348,7 +346,7 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   const LoraTerm tbo[1] = {{shadow_ptr(l, sh_a_o), 0, Q, 0, Q, 0}};
   LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, so, 2, T, H, nullptr, 0, &go));
   LLMT_HIP_TRY(mark(CAT_ROWS));
-  LLMT_HIP_TRY(o_dx_post(row_in(go, Q, kRank, 1, tbo), rinv, s.o16, nq, S, T, dh, dO, delta, damax,
+  LLMT_HIP_TRY(o_dx_post(row_in(go, Q, kRank, 1, tbo), rinv, s.o16, nq, S, T, dh, dO16, delta, dsc,
                          st));
   // attention backward
   AttnArgs aa = attn_args(s);

@@ -299,6 +299,47 @@ def test_attention_fwd_bwd(dev, B, S, nq, nkv):
         assert rel_l2(got.cpu(), want) < GRAD_TOL
 
 
+@pytest.mark.parametrize("mode", ["pow2_rows", "zero_rows", "zero_batch"])
+def test_attention_bwd_row_scales(dev, mode):
+    """dO reaches the backward as fp16 rows each scaled by its own power of
+    two.  dQ row i depends on dO row i only and is computed in that row's
+    scale: rows multiplied by 2^e (e from -30 to 2) give dQ rows exactly 2^e
+    times those of the unscaled dO (bit-exact).  dK and dV mix rows at the
+    batch's common scale (checked against the oracle).  All-zero rows and an
+    all-zero batch stay finite and give exact zeros where the mathematics
+    does."""
+    B, S, nq, nkv = 2, 96, 4, 2
+    g = torch.Generator().manual_seed(31)
+    q = torch.randn(B, S, nq, 128, generator=g).half()
+    k = torch.randn(B, S, nkv, 128, generator=g).half()
+    v = torch.randn(B, S, nkv, 128, generator=g).half()
+    do = torch.randn(B, S, nq, 128, generator=g)
+    mag = 2.0 ** (torch.arange(S) % 33 - 30).float()
+    if mode == "pow2_rows":
+        do_run = do * mag[None, :, None, None]
+    elif mode == "zero_rows":
+        do_run = do.clone()
+        do_run[:, ::3] = 0.0
+    else:
+        do_run = do.clone()
+        do_run[1] = 0.0
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    o, lse = llmt.attention_fwd(qd, kd, vd)
+    dq_ref, dk_ref, dv_ref = ref.attention_bwd(do_run, q.float(), k.float(), v.float(),
+                                               o.float().cpu(), lse.cpu())
+    dq, dk, dv = (t.cpu() for t in llmt.attention_bwd(qd, kd, vd, o, lse, do_run.to(dev)))
+    for got, want in ((dq, dq_ref), (dk, dk_ref), (dv, dv_ref)):
+        assert torch.isfinite(got).all()
+        assert rel_l2(got, want) < GRAD_TOL
+    if mode == "pow2_rows":
+        dq1 = llmt.attention_bwd(qd, kd, vd, o, lse, do.to(dev))[0].cpu()
+        assert torch.equal(dq, dq1 * mag[None, :, None, None])
+    elif mode == "zero_rows":
+        assert (dq[:, ::3] == 0).all()
+    else:
+        assert (dq[1] == 0).all() and (dk[1] == 0).all() and (dv[1] == 0).all()
+
+
 @pytest.mark.parametrize("cfg,dkdv", [("2,1", "2"), ("2,2", "4"), ("4,1", "4"), ("4,2", "2")])
 @pytest.mark.parametrize("B,S,nq,nkv", [(1, 200, 4, 2), (2, 128, 2, 1)])
 def test_attention_launch_shapes(dev, monkeypatch, cfg, dkdv, B, S, nq, nkv):
