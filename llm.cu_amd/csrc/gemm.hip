@@ -714,21 +714,26 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
 }
 
 // Skinny fp16 kernel fed by DMA (the T = 128 training step): a 128 x BN
-// output tile (BN = 16 NB) per workgroup of four waves (wave w: rows
-// 32 w .. 32 w + 31, all BN columns), K split over blockIdx.y in 64-wide
-// stages.  Both operands move global -> LDS with buffer loads that have an
-// LDS destination, 16 bytes a lane: A as 128-byte row pieces (8 lanes a row,
-// so each stage touches every A cache line once; the 16-byte pieces are
-// XOR-swizzled by row so the fragment reads are bank-conflict free), B as
-// the two consecutive 1 KB fragments of each fragment-packed row block (one
-// wave-uniform descriptor per row block; the stage offset is a scalar).  An
-// S-stage ring (A 16 KB + B 2 NB KB a stage) keeps S - 1 stages in flight.
-// Stage c is waited for with an explicit vmcnt (the loads of later stages
-// stay in flight) and a plain barrier; the last S - 1 stages wait for all.
-// Measured on MI355X (per-workgroup timestamps, C2 shapes): the partial
-// tiles and the first round trip, not the MFMA work, set the cost at this M;
-// A pieces of a whole cache line cut the first-data latency.  Columns past N
-// load row block 0 of the first segment (in bounds) and are not stored.
+// output tile (BN = 16 NB) per workgroup of eight waves, K split over
+// blockIdx.y in 64-wide stages.  Wave w = 4 kg + wr computes rows
+// 32 wr .. 32 wr + 31 x all BN columns over k half kg (32 of the 64) of
+// every stage, so each SIMD runs two waves whose LDS reads and MFMAs
+// interleave; the two halves' sums meet in LDS at the end (kg 1 hands its
+// accumulators to kg 0, which stores).  Both operands move global -> LDS with
+// buffer loads that have an LDS destination, 16 bytes a lane: A as 128-byte
+// row pieces (8 lanes a row, so each stage touches every A cache line once;
+// the 16-byte pieces are XOR-swizzled by row so the fragment reads are
+// bank-conflict free; wave w moves rows 16 w .. 16 w + 15), B as the 1 KB
+// fragment of k half kg of each fragment-packed row block (row blocks wr,
+// wr + 4, ..; one wave-uniform descriptor per row block, the stage offset a
+// scalar).  An S-stage ring (A 16 KB + B 2 NB KB a stage) keeps S - 1 stages
+// in flight; stage c is waited for with an explicit vmcnt (the loads of later
+// stages stay in flight) and a plain barrier, the last S - 1 stages wait for
+// all.  A wave reads all fragments of its stage half before its MFMAs.
+// Measured on MI355X (C2 shapes, back to back): 5-15% below the four-wave
+// form with the same tiles; the partial tiles and the first round trip set
+// the rest of the cost at this M.  Columns past N load row block 0 of the
+// first segment (in bounds) and are not stored.
 constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -743,33 +748,35 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, unsig
 __device__ __forceinline__ int a_slot(int r, int p) { return p ^ ((r >> 1) & 7); }
 
 template <int S, int NB>
-__global__ __launch_bounds__(256) void gemm_skinny_kernel(const GemmArgs g) {
+__global__ __launch_bounds__(512) void gemm_skinny_kernel(const GemmArgs g) {
   constexpr int AB = 16384;                  // A bytes per stage
   constexpr int SB = AB + NB * 2048;         // bytes per stage
-  constexpr int BPW = (NB + 3) / 4;  // B row blocks a wave moves at most (w, w + 4, ..)
+  constexpr int BPW = (NB + 3) / 4;          // B row blocks a wave moves at most (wr, wr + 4, ..)
+  static_assert(4 * 2 * NB * 64 * 16 <= S * SB, "k-half exchange fits in the ring");
   __shared__ __attribute__((aligned(1024))) char smem[S * SB];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wr = wave & 3, kg = wave >> 2;
   const int n0 = blockIdx.x * (NB * 16), m0 = blockIdx.z * 128;
   const int ksteps = g.K / KSTEP;
   const int nst = g.K / 64;
   const int c0 = (int)((long long)blockIdx.y * nst / g.split);
   const int c1 = (int)((long long)(blockIdx.y + 1) * nst / g.split);
 
-  // A: wave w moves rows 32 w .. 32 w + 31 (four 1 KB pieces of 8 rows)
+  // A: wave w moves rows 16 w .. 16 w + 15 (two 1 KB pieces of 8 rows)
   const __amdgpu_buffer_rsrc_t ars =
       make_rsrc(g.A + (long long)m0 * g.lda, (unsigned)(128u * g.lda * 2u));
-  unsigned aoff[4];
+  unsigned aoff[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 8 * (4 * wave + i) + (lane >> 3);
+  for (int i = 0; i < 2; ++i) {
+    const int r = 8 * (2 * wave + i) + (lane >> 3);
     aoff[i] = (unsigned)((r * g.lda + a_slot(r, lane & 7) * 8) * 2);
   }
-  const int nbw = (NB - wave + 3) / 4;  // row blocks this wave moves
+  const int nbw = (NB - wr + 3) / 4;  // row blocks this wave moves
   __amdgpu_buffer_rsrc_t brs[BPW];
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
-    const int nn = n0 + 16 * min(wave + 4 * i, NB - 1);
+    const int nn = n0 + 16 * min(wr + 4 * i, NB - 1);
     int s = 0;
 #pragma unroll
     for (int q = 1; q < 4; ++q)
@@ -780,34 +787,29 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const GemmArgs g) {
   auto issue = [&](int c) LLMT_INLINE {
     char* st = smem + (c % S) * SB;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) buffer_lds16(ars, st + (4 * wave + i) * 1024, aoff[i], c * 128u);
+    for (int i = 0; i < 2; ++i) buffer_lds16(ars, st + (2 * wave + i) * 1024, aoff[i], c * 128u);
 #pragma unroll
     for (int i = 0; i < BPW; ++i)
-      if (i < nbw) {
-#pragma unroll
-        for (int q = 0; q < 2; ++q)
-          buffer_lds16(brs[i], st + AB + ((wave + 4 * i) * 2 + q) * 1024, lane * 16u + q * 1024u,
-                       c * 2048u);
-      }
+      if (i < nbw)
+        buffer_lds16(brs[i], st + AB + ((wr + 4 * i) * 2 + kg) * 1024, lane * 16u + kg * 1024u,
+                     c * 2048u);
   };
-  // stage c complete: only the later stages' loads (4 + 2 nbw a stage) may be pending
+  // stage c complete: only the later stages' loads (2 + nbw a stage) may be pending
   auto wait_stage = [&]() LLMT_INLINE {
     switch (nbw) {
-      case 0: wait_vm<(S - 2) * 4>(); break;
-      case 1: wait_vm<(S - 2) * 6>(); break;
-      case 2: wait_vm<(S - 2) * 8>(); break;
-      case 3: wait_vm<(S - 2) * 10>(); break;
-      default: wait_vm<(S - 2) * 12>(); break;
+      case 0: wait_vm<(S - 2) * 2>(); break;
+      case 1: wait_vm<(S - 2) * 3>(); break;
+      default: wait_vm<(S - 2) * 4>(); break;
     }
   };
-  // A fragment reads: row 16 f + c of the stage, k-step q, halves 8 g..
+  // A fragment reads: row 16 (2 wr + i) + c of the stage, k half kg, halves 8 g..
+  const int arow0 = 16 * (2 * wr) + (lane & 15);
   int aread[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int r = 16 * (2 * wave + i) + (lane & 15);
-    aread[i] = r * 128;
+    const int r = arow0 + 16 * i;
+    aread[i] = r * 128 + a_slot(r, 4 * kg + (lane >> 4)) * 16;
   }
-  const int arow0 = 16 * (2 * wave) + (lane & 15);
 
   floatx4 acc[2][NB];
 #pragma unroll
@@ -827,23 +829,36 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const GemmArgs g) {
     }
     asm volatile("" ::: "memory");
     const char* st = smem + (c % S) * SB;
+    half8 a[2], b[NB];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      half8 a[2];
+    for (int i = 0; i < 2; ++i) a[i] = *reinterpret_cast<const half8*>(st + aread[i]);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int r = arow0 + 16 * i;
-        a[i] = *reinterpret_cast<const half8*>(st + aread[i] + a_slot(r, 4 * q + (lane >> 4)) * 16);
-      }
+    for (int j = 0; j < NB; ++j)
+      b[j] = *reinterpret_cast<const half8*>(st + AB + (j * 2 + kg) * 1024 + lane * 16);
 #pragma unroll
-      for (int j = 0; j < NB; ++j) {
-        const half8 b = *reinterpret_cast<const half8*>(st + AB + (j * 2 + q) * 1024 + lane * 16);
+    for (int j = 0; j < NB; ++j)
 #pragma unroll
-        for (int i = 0; i < 2; ++i) acc[i][j] = mfma16(a[i], b, acc[i][j]);
-      }
-    }
+      for (int i = 0; i < 2; ++i) acc[i][j] = mfma16(a[i], b[j], acc[i][j]);
     asm volatile("" ::: "memory");
   }
+
+  // k half 1 hands its sums to k half 0 (the ring is free: every load has
+  // landed and every wave is past its last fragment read)
+  wait_vm<0>();
+  __syncthreads();
+  floatx4* xch = reinterpret_cast<floatx4*>(smem) + wr * (2 * NB * 64);
+  if (kg == 1) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < NB; ++j) xch[(i * NB + j) * 64 + lane] = acc[i][j];
+  }
+  __syncthreads();
+  if (kg == 1) return;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[i][j] += xch[(i * NB + j) * 64 + lane];
 
   float* C = g.C + (long long)blockIdx.y * g.split_stride;
 #pragma unroll
@@ -861,7 +876,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const GemmArgs g) {
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int row = m0 + (2 * wave + i) * 16 + (lane >> 4) * 4 + v;
+        const int row = m0 + (2 * wr + i) * 16 + (lane >> 4) * 4 + v;
         C[(long long)row * g.ldc + col] = acc[i][j][v] * sc;
       }
   }
@@ -1252,15 +1267,25 @@ int gemm_pick_split(int M, int N, int K, int max_split) {
 }
 
 // M % 128 == 0 with fp16 weights: the DMA-fed skinny kernel, 128 x BN tiles.
+// LDS of an S-stage ring of NB-fragment tiles within the 160 KB of a CU
+template <int S, int NB>
+constexpr bool skinny_fits = S * (16384 + NB * 2048) <= 160 * 1024;
+
 template <int S>
 static void launch_skinny(const GemmArgs& g, int nb, hipStream_t st) {
   const dim3 grid((g.N + nb * 16 - 1) / (nb * 16), g.split, g.M / 128);
   switch (nb) {
-    case 2: hipLaunchKernelGGL((gemm_skinny_kernel<S, 2>), grid, dim3(256), 0, st, g); break;
-    case 3: hipLaunchKernelGGL((gemm_skinny_kernel<S, 3>), grid, dim3(256), 0, st, g); break;
-    case 6: hipLaunchKernelGGL((gemm_skinny_kernel<S, 6>), grid, dim3(256), 0, st, g); break;
-    case 8: hipLaunchKernelGGL((gemm_skinny_kernel<S, 8>), grid, dim3(256), 0, st, g); break;
-    default: hipLaunchKernelGGL((gemm_skinny_kernel<S, 4>), grid, dim3(256), 0, st, g); break;
+    case 2: hipLaunchKernelGGL((gemm_skinny_kernel<S, 2>), grid, dim3(512), 0, st, g); break;
+    case 3: hipLaunchKernelGGL((gemm_skinny_kernel<S, 3>), grid, dim3(512), 0, st, g); break;
+    case 6:
+      if constexpr (skinny_fits<S, 6>)
+        hipLaunchKernelGGL((gemm_skinny_kernel<S, 6>), grid, dim3(512), 0, st, g);
+      break;
+    case 8:
+      if constexpr (skinny_fits<S, 8>)
+        hipLaunchKernelGGL((gemm_skinny_kernel<S, 8>), grid, dim3(512), 0, st, g);
+      break;
+    default: hipLaunchKernelGGL((gemm_skinny_kernel<S, 4>), grid, dim3(512), 0, st, g); break;
   }
 }
 static hipError_t launch_m128(const GemmArgs& g, hipStream_t st) {
@@ -1268,10 +1293,17 @@ static hipError_t launch_m128(const GemmArgs& g, hipStream_t st) {
   for (int i = 0; i < g.nseg; ++i) i8 = i8 || g.seg[i].is_i8;
   if (i8 || !skinny_ok(g.M, g.N, g.K) || g.split > g.K / 64) return launch_mf<8>(g, st);
   const int nb = skinny_plan(g.M, g.N, g.K).nb;
-  if (skinny_stages() == 3)
-    launch_skinny<3>(g, nb, st);
-  else
-    launch_skinny<4>(g, nb, st);
+  const int stages = skinny_stages();
+  if (stages == 6 && nb > 4) {
+    set_error("gemm_nt: %d-stage skinny ring of %d fragments exceeds the LDS", stages, nb);
+    return hipErrorInvalidValue;
+  }
+  switch (stages) {
+    case 3: launch_skinny<3>(g, nb, st); break;
+    case 5: launch_skinny<5>(g, nb, st); break;
+    case 6: launch_skinny<6>(g, nb, st); break;
+    default: launch_skinny<4>(g, nb, st); break;
+  }
   return hipGetLastError();
 }
 

@@ -33,7 +33,8 @@ def test_gemm_f16_matches_fp32(dev, L, M, N, K):
 
 
 @pytest.mark.parametrize("nb,stages", [("2", "4"), ("3", "3"), ("4", "4"), ("6", "3"), ("8", "4"),
-                                       ("4", "0")])
+                                       ("4", "0"), ("3", "5"), ("8", "5"), ("4", "6"),
+                                       ("3", "6")])
 @pytest.mark.parametrize("M,N,K", [(128, 2048 + 48, 2048), (256, 160, 4096), (128, 12288, 1024)])
 def test_gemm_f16_skinny_tiles(dev, L, monkeypatch, nb, stages, M, N, K):
     """Every tile width (nb 16-column fragments) / ring depth of the
