@@ -222,56 +222,108 @@ __global__ __launch_bounds__(RT) void embed_norm_kernel(const int* __restrict__ 
     xn[(long long)t * H + c] = (_Float16)(x[(long long)t * H + c] * r * w[c]);
 }
 
-// After the fused Q/K/V(+LoRA-A) GEMM, whose reduction already added
-// s * (x A^T) B^T per projection (src/kernels/lora.cu:181-202): stash
-// q_raw/k_raw (fp32, the QK-norm backward input) and h = x A^T, then per head
-// QK-RMSNorm
-// (src/kernels/rmsnorm.cu:36-41 with 128-wide rows) and half-split RoPE
-// (src/kernels/rope.cu:7-27): lane l of a wave owns the rotation pair
-// (l, l + 64).  Writes q, k (normed, rotated) and v as fp16 [T, Q + 2 KV].
-template <int P, bool MULTI>
-__global__ __launch_bounds__(RT) void qkv_post_kernel(const QkvPostArgs a, int T, int rpw) {
-  extern __shared__ float ys[];  // [NT]
-  __shared__ float hs[64];
+// After the fused Q/K/V(+LoRA-A) GEMM: y = sum of the split partials plus
+// s (x A^T) B^T per projection (src/kernels/lora.cu:181-202, h = x A^T from
+// the GEMM's extra columns); stash q_raw/k_raw (fp32, the QK-norm backward
+// input) and h, then per head QK-RMSNorm (src/kernels/rmsnorm.cu:36-41 with
+// 128-wide rows) and half-split RoPE (src/kernels/rope.cu:7-27).  Writes q, k
+// (normed, rotated) and v as fp16 [T, Q + 2 KV].
+// Tiled by head: workgroup (head hh of the q | k | v heads, 16 rows), four
+// waves of four rows each; lane l owns columns l and l + 64 of the head (its
+// rotation pair), so the norm is a wave sum and the adapter slice a lane
+// needs is 2 x 16 values held in registers for all its rows.  Every load of
+// a wave's rows (partials of every split, the 16 h columns) is issued before
+// the first use.
+constexpr int QH_ROWS = 16;
+
+__global__ __launch_bounds__(256) void qkv_post_kernel(const QkvPostArgs a, int T) {
+  constexpr int RPW = QH_ROWS / 4;
+  const int hh = blockIdx.x;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int Q = a.nq * HD, KV = a.nkv * HD, NT = Q + 2 * KV;
-  LoraRegs<P, 1> L;
-  if constexpr (MULTI) lora_load<P, 1>(a.in, NT, L);
-  const int nrows = MULTI ? rpw : 1;
-  for (int it = 0; it < nrows; ++it) {
-  const int t = blockIdx.x * nrows + it;
-  if (t >= T) break;
-  if (it) __syncthreads();
-  float4 v[P], hv;
-  load_row<P, true>(a.in, t, NT, v, hv);
-  if constexpr (!MULTI) lora_load<P, 1>(a.in, NT, L);
-  store_h(a.in, hv, hs);
-  if ((int)threadIdx.x < a.in.nh / 4)
-    *reinterpret_cast<float4*>(a.hbuf + (long long)t * 64 + 4 * threadIdx.x) = hv;
-  __syncthreads();
-  lora_apply<P, 1>(a.in, hs, L, v);
+  const int base = hh * HD;
+  const int term = hh < a.nq ? 0 : (hh < a.nq + a.nkv ? 1 : 2);
+  const RowIn& in = a.in;
+  const bool lora = term < in.nterm;
+  const int hcol = in.hcol + R * term;
+  float b0[R], b1[R];
 #pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int c = 4 * ((int)threadIdx.x + p * RT);
-    if (c >= NT) continue;
-    *reinterpret_cast<float4*>(ys + c) = v[p];
-    if (c < Q + KV)
-      *reinterpret_cast<float4*>(a.qkraw + (long long)t * (Q + KV) + c) = v[p];
-    else
-      st_h4(a.qkv16 + (long long)t * NT + c, v[p]);
+  for (int r = 0; r < R; ++r) {
+    b0[r] = 0.f;
+    b1[r] = 0.f;
   }
-  __syncthreads();
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int pos = t % a.S;
-  const float cs = a.cosT[pos * (HD / 2) + lane], sn = a.sinT[pos * (HD / 2) + lane];
-  for (int hh = wave; hh < a.nq + a.nkv; hh += RW) {
-    const int base = hh * HD;
-    const float* w = hh < a.nq ? a.qn : a.kn;
-    const float x0 = ys[base + lane], x1 = ys[base + 64 + lane];
-    const float r = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / HD + a.eps);
-    const float y0 = x0 * r * w[lane], y1 = x1 * r * w[lane + 64];
-    a.qkv16[(long long)t * NT + base + lane] = (_Float16)(y0 * cs - y1 * sn);
-    a.qkv16[(long long)t * NT + base + 64 + lane] = (_Float16)(y1 * cs + y0 * sn);
+  if (lora) {
+    const LoraTerm& m = in.term[term];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      b0[r] = (float)m.sh[packed_index(m.row0 + r, base + lane, m.kp)];
+      b1[r] = (float)m.sh[packed_index(m.row0 + r, base + 64 + lane, m.kp)];
+    }
   }
+  const int t0 = blockIdx.y * QH_ROWS + w;
+  float x0[RPW], x1[RPW], hv[RPW];
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int t = min(t0 + 4 * i, T - 1);
+    const float* prow = in.part + (long long)t * in.ldp;
+    x0[i] = prow[base + lane];
+    x1[i] = prow[base + 64 + lane];
+    hv[i] = lora ? prow[hcol + (lane & 15)] : 0.f;
+  }
+  for (int k = 1; k < in.split; ++k) {
+    float y0[RPW], y1[RPW], yh[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      const int t = min(t0 + 4 * i, T - 1);
+      const float* prow = in.part + (long long)k * in.ss + (long long)t * in.ldp;
+      y0[i] = prow[base + lane];
+      y1[i] = prow[base + 64 + lane];
+      yh[i] = lora ? prow[hcol + (lane & 15)] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      x0[i] += y0[i];
+      x1[i] += y1[i];
+      hv[i] += yh[i];
+    }
+  }
+  const bool qk = hh < a.nq + a.nkv;
+  const float* nw = hh < a.nq ? a.qn : a.kn;
+  const float w0 = qk ? nw[lane] : 0.f, w1 = qk ? nw[lane + 64] : 0.f;
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int t = t0 + 4 * i;
+    if (t >= T) break;
+    float v0 = x0[i], v1 = x1[i];
+    if (lora) {
+      float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float h = __shfl(hv[i], r, 64);
+        acc0 += h * b0[r];
+        acc1 += h * b1[r];
+      }
+      v0 += acc0 * in.lscale;
+      v1 += acc1 * in.lscale;
+      // the first head of each projection stashes its 16 h columns
+      if ((hh == 0 || hh == a.nq || hh == a.nq + a.nkv) && lane < R)
+        a.hbuf[(long long)t * 64 + R * term + lane] = hv[i];
+    }
+    _Float16* out = a.qkv16 + (long long)t * NT + base;
+    if (!qk) {
+      out[lane] = (_Float16)v0;
+      out[64 + lane] = (_Float16)v1;
+      continue;
+    }
+    float* raw = a.qkraw + (long long)t * (Q + KV) + base;
+    raw[lane] = v0;
+    raw[64 + lane] = v1;
+    const float r = rsqrtf(wave_sum(v0 * v0 + v1 * v1) / HD + a.eps);
+    const int pos = t % a.S;
+    const float cs = a.cosT[pos * (HD / 2) + lane], sn = a.sinT[pos * (HD / 2) + lane];
+    const float y0 = v0 * r * w0, y1 = v1 * r * w1;
+    out[lane] = (_Float16)(y0 * cs - y1 * sn);
+    out[64 + lane] = (_Float16)(y1 * cs + y0 * sn);
   }
 }
 
@@ -797,26 +849,19 @@ hipError_t embed_norm(const int* tok, const _Float16* E, int V, int H, const flo
 }
 
 hipError_t qkv_post(const QkvPostArgs& a, int T, hipStream_t st) {
-  const int NT = (a.nq + 2 * a.nkv) * HD;
+  const int Q = a.nq * HD, KV = a.nkv * HD, NT = Q + 2 * KV;
   if (!row_in_ok(a.in, NT, "qkv_post")) return hipErrorInvalidValue;
-  const int P = (NT + 4 * RT - 1) / (4 * RT);
-  const int rpw = rows_per_wg(T, P);
-  const dim3 g((T + rpw - 1) / rpw);
-  switch (P) {
-    case 1:
-      if (rpw > 1) hipLaunchKernelGGL((qkv_post_kernel<1, true>), g, dim3(RT), NT * sizeof(float), st, a, T, rpw);
-      else hipLaunchKernelGGL((qkv_post_kernel<1, false>), g, dim3(RT), NT * sizeof(float), st, a, T, rpw);
-      break;
-    case 2:
-      if (rpw > 1) hipLaunchKernelGGL((qkv_post_kernel<2, true>), g, dim3(RT), NT * sizeof(float), st, a, T, rpw);
-      else hipLaunchKernelGGL((qkv_post_kernel<2, false>), g, dim3(RT), NT * sizeof(float), st, a, T, rpw);
-      break;
-    case 3: hipLaunchKernelGGL((qkv_post_kernel<3, false>), g, dim3(RT), NT * sizeof(float), st, a, T, rpw); break;
-    case 4: hipLaunchKernelGGL((qkv_post_kernel<4, false>), g, dim3(RT), NT * sizeof(float), st, a, T, rpw); break;
-    default:
-      set_error("qkv_post: row width %d above %d", NT, 16 * RT);
-      return hipErrorInvalidValue;
+  // adapter terms q, k, v over their own column ranges, h columns in order
+  bool ok = a.in.nterm == 0 || (a.in.nterm == 3 && a.in.nh == 3 * R);
+  const int c0[3] = {0, Q, Q + KV}, n[3] = {Q, KV, KV};
+  for (int q = 0; q < a.in.nterm && ok; ++q)
+    ok = a.in.term[q].c0 == c0[q] && a.in.term[q].n == n[q] && a.in.term[q].hidx == R * q;
+  if (!ok) {
+    set_error("qkv_post: LoRA terms must be q, k, v over their own columns");
+    return hipErrorInvalidValue;
   }
+  hipLaunchKernelGGL(qkv_post_kernel, dim3(a.nq + 2 * a.nkv, (T + QH_ROWS - 1) / QH_ROWS),
+                     dim3(256), 0, st, a, T);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
