@@ -160,9 +160,11 @@ struct Ctx {
   hipError_t mark(int cat);
   // C = A B^T over the segments.  direct: split 1 into `direct` (ld ldc).
   // Otherwise the fp32 split-K partials land in `part` and *out describes
-  // them; the consuming row epilogue sums them in split order.
+  // them; the consuming row epilogue sums them in split order.  glu16 (with
+  // direct): the fused SwiGLU epilogue also writes fp16(silu(gate) * up)
+  // [M, N / 2] there (gemm_glu_ok shapes only).
   hipError_t gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int nseg, int M, int K,
-                  float* direct, int ldc, GemmOut* out);
+                  float* direct, int ldc, GemmOut* out, _Float16* glu16 = nullptr);
   // A GEMM's partials as a row-epilogue input with raw h columns
   // [hcol, hcol + nh) and LoRA up-projection terms.
   RowIn row_in(const GemmOut& go, int hcol = 0, int nh = 0, int nterm = 0,

@@ -599,7 +599,7 @@ __device__ __forceinline__ half8 i8x8_to_h8(u32x2 raw) {
   return h - (_Float16)1152.0f;
 }
 
-template <bool I8, bool KS, int S, int WNN>
+template <bool I8, bool KS, int S, int WNN, bool GLU = false>
 __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, int g_order) {
   // WNN waves across N (2: four waves of 128 x 128; 4: eight waves of 128 x 64)
   constexpr int NW = 2 * WNN, WC = 256 / WNN, NFR = WC / 16;  // wave columns, fragments
@@ -629,10 +629,14 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
   const BSeg& sg = g.seg[0];
   constexpr int ES = I8 ? 1 : 2;
   const char* bsrc = (const char*)sg.ptr + (long long)lane * 16;  // lanes < 32 for int8
+  // SwiGLU pairs: tile fragment f is gate (f even) or up (f odd) row block
+  // 8 tn + f / 2, so a wave's fragments 2 p and 2 p + 1 cover the same columns
   long long boff[FPW];
 #pragma unroll
   for (int j = 0; j < FPW; ++j) {
-    const int rb = min((n0 >> 4) + wave * FPW + j, (g.N >> 4) - 1);
+    const int f = wave * FPW + j;
+    const int rb = GLU ? (f & 1) * (g.glu >> 4) + tn * 8 + (f >> 1)
+                       : min((n0 >> 4) + f, (g.N >> 4) - 1);
     boff[j] = (long long)rb * ksteps * 512 * ES;
   }
   const _Float16* ksrc = KS ? sg.kscale + (wave & 3) * 8 : nullptr;
@@ -698,6 +702,32 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
 
   float* C = g.C + (long long)blockIdx.y * g.split_stride;
   const _Float16* cs = sg.colscale;
+  if constexpr (GLU) {
+    float sgu[NFR];
+#pragma unroll
+    for (int jj = 0; jj < NFR / 2; ++jj) {
+      const int col = (tn * 8 + ((wn * NFR) >> 1) + jj) * 16 + (lane & 15);
+      sgu[2 * jj] = cs ? (float)cs[col] : 1.0f;
+      sgu[2 * jj + 1] = cs ? (float)cs[g.glu + col] : 1.0f;
+    }
+    const int col0 = (tn * 8 + ((wn * NFR) >> 1)) * 16 + (lane & 15);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const long long row = m0 + wm * 128 + i * 16 + (lane >> 4) * 4 + v;
+        float* crow = C + row * g.ldc + col0;
+        _Float16* arow = g.glu16 + row * g.ldglu + col0;
+#pragma unroll
+        for (int jj = 0; jj < NFR / 2; ++jj) {
+          const float gt = acc[i][2 * jj][v] * sgu[2 * jj], up = acc[i][2 * jj + 1][v] * sgu[2 * jj + 1];
+          crow[16 * jj] = gt;
+          crow[g.glu + 16 * jj] = up;
+          arow[16 * jj] = (_Float16)(gt / (1.0f + __expf(-gt)) * up);
+        }
+      }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < NFR; ++j) {
     const int col = n0 + wn * WC + j * 16 + (lane & 15);
@@ -1245,6 +1275,13 @@ static int big_split(int M, int N, int K, int max_split) {
   return best;
 }
 
+// The DMA large-tile kernel (the default for big tiles) carries the SwiGLU
+// epilogue: 256-wide tiles over 8 waves, gate/up fragment pairs per wave.
+bool gemm_glu_ok(int M, int I, int K) {
+  return big_tiles(M, K) && I % 128 == 0 && env_int("LLMT_GEMM_BIG_KIND", 2) == 2 &&
+         big_wn(2 * I) == 4 && env_int("LLMT_GEMM_DMA_WAVES", 8) == 8 && big_split(M, 2 * I, K, 64) == 1;
+}
+
 int gemm_pick_split(int M, int N, int K, int max_split) {
   if (big_tiles(M, K)) return big_split(M, N, K, max_split);
   if (skinny_ok(M, N, K)) {
@@ -1318,6 +1355,11 @@ hipError_t gemm_nt(const GemmArgs& g, hipStream_t st) {
       set_error("gemm_nt: segment rows must be a multiple of 16 (%d)", g.seg[i].rows);
       return hipErrorInvalidValue;
     }
+  if (g.glu && !(g.glu % 128 == 0 && g.N == 2 * g.glu && g.nseg == 1 && g.split == 1 &&
+                 g.glu16 && gemm_glu_ok(g.M, g.glu, g.K))) {
+    set_error("gemm_nt: SwiGLU epilogue needs the large-tile kernel, split 1, N = 2 x %d", g.glu);
+    return hipErrorInvalidValue;
+  }
   hipError_t e;
   const int m16 = g.M / 16;
   if (use_big_tiles(g)) {
@@ -1342,6 +1384,13 @@ hipError_t gemm_nt(const GemmArgs& g, hipStream_t st) {
           hipLaunchKernelGGL((gemm_dma_kernel<true, true, 5, 2>), gr, dim3(256), 0, st, gm, order);
         else
           hipLaunchKernelGGL((gemm_dma_kernel<true, false, 5, 2>), gr, dim3(256), 0, st, gm, order);
+      } else if (gm.glu) {
+        if (!i8)
+          hipLaunchKernelGGL((gemm_dma_kernel<false, false, 4, 4, true>), gr, dim3(512), 0, st, gm, order);
+        else if (ks)
+          hipLaunchKernelGGL((gemm_dma_kernel<true, true, 5, 4, true>), gr, dim3(512), 0, st, gm, order);
+        else
+          hipLaunchKernelGGL((gemm_dma_kernel<true, false, 5, 4, true>), gr, dim3(512), 0, st, gm, order);
       } else {
         if (!i8)
           hipLaunchKernelGGL((gemm_dma_kernel<false, false, 4, 4>), gr, dim3(512), 0, st, gm, order);

@@ -32,7 +32,15 @@ struct GemmArgs {
   int ldc;
   long long split_stride;  // elements between split partials
   int M, N, K, split;
+  // glu > 0: fused SwiGLU epilogue (split 1, N = 2 glu, one segment whose
+  // rows [0, glu) are the gate and [glu, 2 glu) the up projection): C gets
+  // [gate | up] as without it, and glu16[m][n] = fp16(silu(gate) * up).
+  int glu;
+  _Float16* glu16;
+  int ldglu;
 };
+// The fused SwiGLU epilogue exists for this GEMM shape (the large-tile kernel).
+bool gemm_glu_ok(int M, int I, int K);
 
 // Every B segment is fragment-packed (packed_index, common.h) with row
 // length K; rows a multiple of 16.  A is row-major fp16 [M, lda], K % 32 == 0.

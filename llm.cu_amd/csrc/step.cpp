@@ -64,7 +64,7 @@ hipError_t Ctx::mark(int cat) {
 }
 
 hipError_t Ctx::gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int nseg, int M, int K,
-                     float* direct, int ldc, GemmOut* out) {
+                     float* direct, int ldc, GemmOut* out, _Float16* glu16) {
   GemmArgs g{};
   g.A = A;
   g.lda = lda;
@@ -78,6 +78,11 @@ hipError_t Ctx::gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int 
     g.C = direct;
     g.ldc = ldc;
     g.split_stride = 0;
+    if (glu16) {
+      g.glu = g.N / 2;
+      g.glu16 = glu16;
+      g.ldglu = g.N / 2;
+    }
   } else {
     g.split = gemm_pick_split(M, g.N, K, 64);
     g.C = part;
@@ -206,11 +211,15 @@ hipError_t Ctx::layer_fwd(int l, int B, const float* next_w, float* x_out, _Floa
   LLMT_HIP_TRY(mark(CAT_ROWS));
   LLMT_HIP_TRY(o_post(row_in(go, H, kRank, 1, to), s.x_in, w.ffn_norm, eps, H, T, s.h, s.x_mid,
                       s.xn2, st));
-  // gate/up, SwiGLU
+  // gate/up, SwiGLU (in the GEMM epilogue where the large-tile kernel runs)
   BSeg sg[1] = {wseg(w.wgu)};
-  LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn2, H, sg, 1, T, H, nullptr, 0, &go));
-  LLMT_HIP_TRY(mark(CAT_ROWS));
-  LLMT_HIP_TRY(gu_post(row_in(go), I, T, s.gu, a16, st));
+  if (gemm_glu_ok(T, I, H)) {
+    LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn2, H, sg, 1, T, H, s.gu, 2 * I, nullptr, a16));
+  } else {
+    LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn2, H, sg, 1, T, H, nullptr, 0, &go));
+    LLMT_HIP_TRY(mark(CAT_ROWS));
+    LLMT_HIP_TRY(gu_post(row_in(go), I, T, s.gu, a16, st));
+  }
   // down, residual, next norm
   BSeg sd[1] = {wseg(w.wd)};
   LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, a16, I, sd, 1, T, I, nullptr, 0, &go));
