@@ -182,7 +182,8 @@ int Ctx::init() {
   TRY_PTR(part = alloc_n<float>(part_elems));
   TRY_PTR(a16 = alloc_n<_Float16>(T * I));
   TRY_PTR(d_res = alloc_n<float>(T * H));
-  TRY_PTR(dmid_all = alloc_n<float>((size_t)L * T * H));
+  TRY_PTR(go16_all = alloc_n<_Float16>((size_t)L * T * H));
+  TRY_PTR(ro_all = alloc_n<float>((size_t)L * T));
   TRY_PTR(g16 = alloc_n<_Float16>(T * (H > NT ? H : NT)));
   TRY_PTR(rinv = alloc_n<float>(T));
   TRY_PTR(rinv2 = alloc_n<float>(T));
@@ -192,7 +193,8 @@ int Ctx::init() {
   TRY_PTR(dqkv32 = alloc_n<float>(T * NT));
   TRY_PTR(dkvp = alloc_n<float>((size_t)T * 2 * Q));
   TRY_PTR(dO16 = alloc_n<_Float16>((size_t)T * Q));
-  TRY_PTR(dy32_all = alloc_n<float>((size_t)L * T * NT));
+  TRY_PTR(gq16_all = alloc_n<_Float16>((size_t)L * T * NT));
+  TRY_PTR(rq_all = alloc_n<float>((size_t)L * T));
   TRY_PTR(dh_all = alloc_n<float>((size_t)L * T * 64));
   // adapter-gradient jobs (src/kernels/lora_backward.cu:50-90): per layer
   // dA_p = s dh_p^T x_p and dB_p = s dy_p^T h_p for p = q, k, v, o
@@ -201,19 +203,19 @@ int Ctx::init() {
     for (int l = 0; l < L; ++l) {
       const Stash& s = stash[l];
       float* dhl = dh(l);
-      float* dyl = dy32(l);
+      const _Float16* gql = gq16(l);
       auto g = [&](int proj, int is_b) {
         return lora_g + (size_t)l * lora_per_layer + seg_off[2 * proj + is_b];
       };
       const LoraGradJob js[kLoraJobs] = {
-          {s.xn, 1, H, H, dhl + 0, 64, g(0, 0), 0},
-          {s.xn, 1, H, H, dhl + 16, 64, g(1, 0), 0},
-          {s.xn, 1, H, H, dhl + 32, 64, g(2, 0), 0},
-          {s.o16, 1, Q, Q, dhl + 48, 64, g(3, 0), 0},
-          {dyl, 0, NT, Q, s.h + 0, 64, g(0, 1), 1},
-          {dyl + Q, 0, NT, KV, s.h + 16, 64, g(1, 1), 1},
-          {dyl + Q + KV, 0, NT, KV, s.h + 32, 64, g(2, 1), 1},
-          {dmid(l), 0, H, H, s.h + 48, 64, g(3, 1), 1},
+          {s.xn, 1, H, nullptr, H, dhl + 0, 64, g(0, 0), 0},
+          {s.xn, 1, H, nullptr, H, dhl + 16, 64, g(1, 0), 0},
+          {s.xn, 1, H, nullptr, H, dhl + 32, 64, g(2, 0), 0},
+          {s.o16, 1, Q, nullptr, Q, dhl + 48, 64, g(3, 0), 0},
+          {gql, 1, NT, rq(l), Q, s.h + 0, 64, g(0, 1), 1},
+          {gql + Q, 1, NT, rq(l), KV, s.h + 16, 64, g(1, 1), 1},
+          {gql + Q + KV, 1, NT, rq(l), KV, s.h + 32, 64, g(2, 1), 1},
+          {go16(l), 1, H, ro(l), H, s.h + 48, 64, g(3, 1), 1},
       };
       for (int j = 0; j < kLoraJobs; ++j) jobs[(size_t)l * kLoraJobs + j] = js[j];
       if (l == 0)

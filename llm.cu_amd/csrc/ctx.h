@@ -121,9 +121,15 @@ struct Ctx {
   // Per layer (kept until the adapter gradients of all layers run in one
   // launch after the backward): dy of the q/k/v projections [T, NT], dy of
   // the o projection [T, H], the LoRA dh columns [T, 64].
-  float *dy32_all = nullptr, *dmid_all = nullptr, *dh_all = nullptr;
-  float* dy32(int l) const { return dy32_all + (size_t)l * Tmax * NT; }
-  float* dmid(int l) const { return dmid_all + (size_t)l * Tmax * H; }
+  // Per layer, kept for the adapter gradients: the fp16 gradient operands of
+  // the Q/K/V dX GEMM ([T, NT], the q/k/v projections' upstream gradient) and
+  // of the O dX GEMM ([T, H], the o projection's), with their row factors.
+  _Float16 *gq16_all = nullptr, *go16_all = nullptr;
+  float *rq_all = nullptr, *ro_all = nullptr, *dh_all = nullptr;
+  _Float16* gq16(int l) const { return gq16_all + (size_t)l * Tmax * NT; }
+  _Float16* go16(int l) const { return go16_all + (size_t)l * Tmax * H; }
+  float* rq(int l) const { return rq_all + (size_t)l * Tmax; }
+  float* ro(int l) const { return ro_all + (size_t)l * Tmax; }
   float* dh(int l) const { return dh_all + (size_t)l * Tmax * 64; }
   LoraGradJob* lora_jobs = nullptr;  // device [L][kLoraJobs]
   LoraGradPlan lora_plan{};

@@ -1241,7 +1241,8 @@ static SkinnyPlan skinny_plan(int M, int N, int K) {
   return best;
 }
 static bool skinny_ok(int M, int N, int K) {
-  return M % 128 == 0 && K % 64 == 0 && skinny_stages() != 0 && (N + 15) / 16 < 2048;
+  return M % 128 == 0 && K % 64 == 0 && skinny_stages() != 0 &&
+         (N + 15) / 16 < env_int("LLMT_GEMM_SKINNY_MAX_FRAGS", 2048);
 }
 int gemm_tile_n() { return kCfgs[gemm_cfg()].nw * kNF * 16; }
 

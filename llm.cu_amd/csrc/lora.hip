@@ -20,7 +20,9 @@ constexpr int NTH = 256;
 // One adapter-gradient job: out = (acc ? out : 0) + lscale * X^T G over the T
 // token rows, for the ncols columns of X and the 16 columns of G.
 //   dA [16, d_in]:  X = adapter input (xn or o, fp16), G = dh  -> out[r][c]
-//   dB [d_out, 16]: X = upstream grad dy (fp32),       G = h   -> out[c][r]
+//   dB [d_out, 16]: X = upstream grad dy,              G = h   -> out[c][r]
+// (dy as the fp16 GEMM operand, row t scaled by the power of two 1 / xs[t],
+// which the G row takes back exactly)
 // A workgroup owns GC columns, four per lane (one 8- or 16-byte load of X per
 // token); its four waves take interleaved batches of TB tokens, issue the
 // batch's X loads together and read the batch's G rows (uniform across the
@@ -49,9 +51,10 @@ __device__ __forceinline__ void lora_grad_acc(const LoraGradJob& jb, int T, int 
     for (int i = 0; i < TB; ++i) {
       if (t0 + i >= T) break;
       const float* g = jb.G + (long long)(t0 + i) * jb.ldg;
+      const float xs = jb.xs ? jb.xs[t0 + i] : 1.0f;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const float gr = g[r];
+        const float gr = g[r] * xs;
         acc[r].x += x[i].x * gr;
         acc[r].y += x[i].y * gr;
         acc[r].z += x[i].z * gr;

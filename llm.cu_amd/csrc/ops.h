@@ -166,8 +166,8 @@ struct QkBwdArgs {
   const float* sinT;
   int S, nq, nkv;
   float eps;
-  float* dy32;        // [T, NT]
-  _Float16* g16;      // [T, NT]
+  float* dy32;        // [T, NT], may be NULL
+  _Float16* g16;      // [T, NT], row t scaled by 1 / rinv_out[t]
   float* rinv_out;
 };
 
@@ -250,6 +250,7 @@ struct LoraGradJob {
   const void* X;     // [T, ldx] fp16 or fp32
   int x_f16;
   long long ldx;
+  const float* xs;   // NULL, or row t of X stands for X[t] * xs[t]
   int ncols;
   const float* G;    // [T, ldg] (16 columns used)
   long long ldg;

@@ -712,7 +712,7 @@ __global__ __launch_bounds__(RT) void qk_bwd_kernel(const QkBwdArgs a) {
   float amax = 0.f;
   for (int c = threadIdx.x; c < NT; c += RT) {
     const float v = ds[c];
-    a.dy32[(long long)t * NT + c] = v;
+    if (a.dy32) a.dy32[(long long)t * NT + c] = v;
     amax = fmaxf(amax, fabsf(v));
   }
   amax = block_max<RW>(amax, red);

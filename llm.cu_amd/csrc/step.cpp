@@ -314,28 +314,29 @@ hipError_t Ctx::head_bwd(int B) {
 
 // One decoder layer's backward (src/kernels/lora_backward.cu:271-406) from
 // d_res / g16 / rinv (the gradient at the layer output); leaves the gradient
-// at the layer input there and the layer's adapter-gradient inputs (dh, dy)
-// in its per-layer slots for lora_grads.
+// at the layer input there and the layer's adapter-gradient inputs (dh, and
+// the projections' upstream gradients as the fp16 GEMM operands with their
+// row factors) in its per-layer slots for lora_grads.
 hipError_t Ctx::layer_bwd(int l, int B) {
   const int T = B * S;
   const float eps = dims.eps;
-  GemmOut go;
+  GemmOut go_;
   NormBwdArgs nb{};
 
   Layer& w = layers[l];
   Stash& s = stash[l];
   float* const dh = this->dh(l);
-  float* const dmid = this->dmid(l);
-  float* const dy32 = this->dy32(l);
+  _Float16* const og16 = go16(l);  // o projection upstream gradient (fp16, row factor ro)
+  _Float16* const qg16 = gq16(l);  // q/k/v projections upstream gradient (row factor rq)
   // MLP: down dX -> SwiGLU bwd -> gate/up dX -> FFN norm bwd (+ residual)
   BSeg sd[1] = {wseg(w.wdT)};
-  LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, sd, 1, T, H, nullptr, 0, &go));
+  LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, sd, 1, T, H, nullptr, 0, &go_));
   LLMT_HIP_TRY(mark(CAT_ROWS));
-  LLMT_HIP_TRY(swiglu_bwd(row_in(go), rinv, s.gu, I, T, dgu16, rinv2, st));
+  LLMT_HIP_TRY(swiglu_bwd(row_in(go_), rinv, s.gu, I, T, dgu16, rinv2, st));
   BSeg sg[1] = {wseg(w.wguT)};
-  LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, dgu16, 2 * I, sg, 1, T, 2 * I, nullptr, 0, &go));
+  LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, dgu16, 2 * I, sg, 1, T, 2 * I, nullptr, 0, &go_));
   nb = NormBwdArgs{};
-  nb.in = row_in(go);
+  nb.in = row_in(go_);
   nb.rinv_in = rinv2;
   nb.gscale = 1.0f;
   nb.dh_out = nullptr;
@@ -345,18 +346,18 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   nb.H = H;
   nb.dres_in = d_res;
   nb.dres_out = d_res;
-  nb.dmid_out = dmid;
-  nb.g16 = g16;
-  nb.rinv_out = rinv;
+  nb.dmid_out = nullptr;
+  nb.g16 = og16;
+  nb.rinv_out = ro(l);
   LLMT_HIP_TRY(mark(CAT_ROWS));
   LLMT_HIP_TRY(norm_bwd(nb, T, st));
   // O projection dX (+ dh_o through the B_o^T rows)
   BSeg so[2] = {wseg(w.woT), hseg(shadow_ptr(l, sh_bt_o), kRank, H)};
   const LoraTerm tbo[1] = {{shadow_ptr(l, sh_a_o), 0, Q, 0, Q, 0}};
-  LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, so, 2, T, H, nullptr, 0, &go));
+  LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, og16, H, so, 2, T, H, nullptr, 0, &go_));
   LLMT_HIP_TRY(mark(CAT_ROWS));
-  LLMT_HIP_TRY(o_dx_post(row_in(go, Q, kRank, 1, tbo), rinv, s.o16, nq, S, T, dh, dO16, delta, dsc,
-                         st));
+  LLMT_HIP_TRY(o_dx_post(row_in(go_, Q, kRank, 1, tbo), ro(l), s.o16, nq, S, T, dh, dO16, delta,
+                         dsc, st));
   // attention backward
   AttnArgs aa = attn_args(s);
   LLMT_HIP_TRY(mark(CAT_ATTN));
@@ -369,7 +370,7 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   qb.qn = w.q_norm; qb.kn = w.k_norm;
   qb.cosT = cosT; qb.sinT = sinT;
   qb.S = S; qb.nq = nq; qb.nkv = nkv; qb.eps = eps;
-  qb.dy32 = dy32; qb.g16 = g16; qb.rinv_out = rinv;
+  qb.dy32 = nullptr; qb.g16 = qg16; qb.rinv_out = rq(l);
   LLMT_HIP_TRY(mark(CAT_ROWS));
   LLMT_HIP_TRY(qk_bwd(qb, T, st));
   // Q/K/V dX (+ dh_q, dh_k, dh_v through the B^T rows), attention norm bwd
@@ -378,10 +379,10 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   const LoraTerm tbq[3] = {{a_qkv, 0, H, 0, H, 0},
                            {a_qkv, kRank, H, 0, H, kRank},
                            {a_qkv, 2 * kRank, H, 0, H, 2 * kRank}};
-  LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, NT, sq, 2, T, NT, nullptr, 0, &go));
+  LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, qg16, NT, sq, 2, T, NT, nullptr, 0, &go_));
   nb = NormBwdArgs{};
-  nb.in = row_in(go, H, 3 * kRank, 3, tbq);
-  nb.rinv_in = rinv;
+  nb.in = row_in(go_, H, 3 * kRank, 3, tbq);
+  nb.rinv_in = rq(l);
   nb.gscale = 1.0f;
   nb.dh_out = dh;
   nb.dh_col = 0;
