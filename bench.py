@@ -254,7 +254,7 @@ def bench_c3(a):
         "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_F16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
                      "traffic": None,
-                     "kernel": "attention block (norm/RoPE + flash fwd + dQ + dK/dV launches)"},
+                     "kernel": "attention block (norm/RoPE + flash fwd + flash bwd: dQ and dK/dV blocks)"},
     }
     print(json.dumps(out), flush=True)
 

@@ -456,23 +456,19 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, _Float16* smem, int 
 }
 
 // ---------------------------------------------------------------- dK, dV
-// P and dS for one 64-query tile (rows query, column key), both in the
-// batch's dO scale gs: ds arrives in each query row's own dO scale, so row
-// q's factor r = gs * dsc[q] brings dP there, and P times r is the operand
-// against the row-scaled dO16 of dV.
+// P and dS for one 64-query tile (rows query, column key); the tile's dO16
+// rows are already at the batch's dO scale gs, so dS comes out in it too.
 template <bool MASK>
 __device__ __forceinline__ void ds_tile_kv(floatx4 (&p)[4], floatx4 (&ds)[4], const float* lse_s,
-                                           const float* del_s, const float* dsc_s, float sl2,
-                                           float gs, int qq0, int key, int S, int lane) {
+                                           const float* del_s, float sl2, float gs, int qq0, int key,
+                                           int S, int lane) {
   const int g = lane >> 4;
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
     const float4 ls = *reinterpret_cast<const float4*>(lse_s + mt * 16 + 4 * g);
     const float4 dl = *reinterpret_cast<const float4*>(del_s + mt * 16 + 4 * g);
-    const float4 sc = *reinterpret_cast<const float4*>(dsc_s + mt * 16 + 4 * g);
     const float lv[4] = {ls.x, ls.y, ls.z, ls.w};
     const float dv[4] = {dl.x, dl.y, dl.z, dl.w};
-    const float rv[4] = {sc.x * gs, sc.y * gs, sc.z * gs, sc.w * gs};
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       float pv = __builtin_amdgcn_exp2f(fmaf(p[mt][v], sl2, -lv[v] * LOG2E));
@@ -480,18 +476,24 @@ __device__ __forceinline__ void ds_tile_kv(floatx4 (&p)[4], floatx4 (&ds)[4], co
         const int qq = qq0 + mt * 16 + 4 * g + v;
         pv = (key <= qq && qq < S) ? pv : 0.f;
       }
-      p[mt][v] = pv * rv[v];
-      ds[mt][v] = pv * fmaf(ds[mt][v], rv[v], -dv[v] * gs);
+      p[mt][v] = pv;
+      ds[mt][v] = pv * fmaf(-dv[v], gs, ds[mt][v]);
     }
   }
+}
+
+// s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt left free): this thread's LDS
+// writes are done, the DMA loads of later tiles stay in flight.
+__device__ __forceinline__ void wait_lds() {
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
 }
 
 // grid (ceil(S / (16 NW)), nq, B): workgroup (key block kb of 16 NW keys,
 // query head h); wave w owns keys k0 + 16 w + c and loops over the 64-query
 // tiles at or after the block.  LDS: two buffers of (Q tile, dO16 tile,
-// lse[64], delta[64], dsc[64]).  Writes this query head's share of dK, dV
-// (fp32) to a.dkvp.
-constexpr int KV_BUF = 2 * TILE + 3 * BLK * 2;  // halves per dK/dV buffer
+// lse[64], delta[64]).  Writes this query head's share of dK, dV (fp32) to
+// a.dkvp.
+constexpr int KV_BUF = 2 * TILE + 2 * BLK * 2;  // halves per dK/dV buffer
 
 template <int NW>
 __device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* smem, float* red, int kb,
@@ -523,7 +525,6 @@ __device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* smem, fl
     float* vec = reinterpret_cast<float*>(buf + 2 * TILE);
     if (w == 0) dma_vec64(lse_h, qb * BLK, S, vec);
     if (w == NW - 1) dma_vec64(del_h, qb * BLK, S, vec + BLK);
-    if (w == NW / 2) dma_vec64(dsc_b, qb * BLK, S, vec + 2 * BLK);
   };
   issue(qb0, smem);
   const float gs = batch_do_scale<NT>(a.dsc, b, S, red);
@@ -539,17 +540,33 @@ __device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* smem, fl
     dkT[i] = floatx4{0.f, 0.f, 0.f, 0.f};
     dvT[i] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
+  constexpr int RPT = BLK * 16 / NT;  // 16-byte dO16 pieces a thread rescales per tile
   for (int qb = qb0; qb < nqb; ++qb) {
     wait_vm<0>();
     tile_barrier();
+    // the tile's dO16 rows to the batch scale: row q times gs * dsc[q] (a
+    // power of two <= 1, exact in fp16 short of underflow); the factors are
+    // loaded before the next tile's DMA so their wait leaves it in flight
+    float f[RPT];
+#pragma unroll
+    for (int k = 0; k < RPT; ++k)
+      f[k] = dsc_b[min(qb * BLK + ((int)(threadIdx.x + k * NT) >> 4), S - 1)];
+    asm volatile("" ::: "memory");
     if (qb + 1 < nqb) issue(qb + 1, smem + ((qb + 1 - qb0) & 1) * BUF);
-    const _Float16* buf = smem + ((qb - qb0) & 1) * BUF;
+    _Float16* buf = smem + ((qb - qb0) & 1) * BUF;
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      const int pi = threadIdx.x + k * NT;
+      half8* d = reinterpret_cast<half8*>(buf + TILE + toff(pi >> 4, pi & 15));
+      *d = *d * (_Float16)(f[k] * gs);
+    }
+    wait_lds();
+    tile_barrier();
     if (qb * BLK + BLK - 1 < k0) continue;  // every query before every key of the wave
     const _Float16* Qs = buf;
     const _Float16* Ds = buf + TILE;
     const float* lse_s = reinterpret_cast<const float*>(buf + 2 * TILE);
     const float* del_s = lse_s + BLK;
-    const float* dsc_s = lse_s + 2 * BLK;
     floatx4 p[4], ds[4];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
@@ -563,9 +580,9 @@ __device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* smem, fl
     }
     // every query of the tile >= every key of the wave and < S: no mask
     if (qb * BLK >= k0 + 15 && qb * BLK + BLK <= S)
-      ds_tile_kv<false>(p, ds, lse_s, del_s, dsc_s, sl2, gs, qb * BLK, key, S, lane);
+      ds_tile_kv<false>(p, ds, lse_s, del_s, sl2, gs, qb * BLK, key, S, lane);
     else
-      ds_tile_kv<true>(p, ds, lse_s, del_s, dsc_s, sl2, gs, qb * BLK, key, S, lane);
+      ds_tile_kv<true>(p, ds, lse_s, del_s, sl2, gs, qb * BLK, key, S, lane);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const half8 pb = pair_frag(p[2 * j], p[2 * j + 1]);
@@ -599,15 +616,21 @@ __device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* smem, fl
 // them side by side; a launch with nkvb or nqb = 0 runs one half.
 constexpr int BWD_SMEM = 2 * KV_BUF > 4 * TILE ? 2 * KV_BUF : 4 * TILE;
 
-template <int NW, int RW>
+// PART 0: both halves; 1: dK/dV only (nqb = 0); 2: dQ only (nkvb = 0) --
+// the one-half forms keep their own (smaller) register and LDS budgets.
+template <int NW, int RW, int PART>
 __global__ __launch_bounds__(NW * 64) void attn_bwd_kernel(const AttnArgs a, int nkvb, int nqb) {
-  __shared__ __attribute__((aligned(1024))) _Float16 smem[BWD_SMEM];
+  constexpr int SMEM = PART == 1 ? 2 * KV_BUF : PART == 2 ? 4 * TILE : BWD_SMEM;
+  __shared__ __attribute__((aligned(1024))) _Float16 smem[SMEM];
   __shared__ float red[NW];
   const int x = blockIdx.x;
-  if (x < nkvb)
-    dkdv_block<NW>(a, smem, red, x, blockIdx.y, blockIdx.z);
-  else
-    dq_block<NW, RW>(a, smem, nqb - 1 - (x - nkvb), blockIdx.y, blockIdx.z);
+  if constexpr (PART != 2) {
+    if (PART == 1 || x < nkvb) {
+      dkdv_block<NW>(a, smem, red, x, blockIdx.y, blockIdx.z);
+      return;
+    }
+  }
+  if constexpr (PART != 1) dq_block<NW, RW>(a, smem, nqb - 1 - (x - nkvb), blockIdx.y, blockIdx.z);
 }
 
 // dK, dV = sum over the query heads of each group of the per-head shares
@@ -693,38 +716,39 @@ void launch_fwd(const AttnArgs& a, int B, hipStream_t st) {
   hipLaunchKernelGGL((attn_fwd_kernel<NW, RW>), dim3((a.S + QB - 1) / QB, a.nq, B), dim3(NW * 64),
                      0, st, a);
 }
-template <int NW, int RW>
+template <int NW, int RW, int PART>
 void launch_bwd(const AttnArgs& a, int B, int nkvb, int nqb, hipStream_t st) {
-  hipLaunchKernelGGL((attn_bwd_kernel<NW, RW>), dim3(nkvb + nqb, a.nq, B), dim3(NW * 64), 0, st, a,
-                     nkvb, nqb);
+  hipLaunchKernelGGL((attn_bwd_kernel<NW, RW, PART>), dim3(nkvb + nqb, a.nq, B), dim3(NW * 64), 0,
+                     st, a, nkvb, nqb);
 }
 // dK/dV key blocks of nwk waves and dQ query blocks of nwq waves x rw tiles:
-// one launch when the wave counts agree, else one launch each.
+// one launch when the wave counts agree and the halves are small (each
+// under 2048 workgroups: the second launch would mostly wait on the first's
+// tail), else one launch each (measured 5% faster at B4 x S2048).
 void launch_attn_bwd(const AttnArgs& a, int B, int nwk, int nwq, int rw, hipStream_t st) {
   const int nkvb = (a.S + nwk * 16 - 1) / (nwk * 16);
   const int nqb = (a.S + nwq * rw * 16 - 1) / (nwq * rw * 16);
-  auto dq_only = [&](int n) {
+  const bool small = (long long)nkvb * a.nq * B < 2048;
+  if (nwk == nwq && small) {
     switch (nwq * 10 + rw) {
-      case 42: launch_bwd<4, 2>(a, B, 0, n, st); break;
-      case 41: launch_bwd<4, 1>(a, B, 0, n, st); break;
-      case 22: launch_bwd<2, 2>(a, B, 0, n, st); break;
-      default: launch_bwd<2, 1>(a, B, 0, n, st); break;
-    }
-  };
-  if (nwk == nwq) {
-    switch (nwq * 10 + rw) {
-      case 42: launch_bwd<4, 2>(a, B, nkvb, nqb, st); break;
-      case 41: launch_bwd<4, 1>(a, B, nkvb, nqb, st); break;
-      case 22: launch_bwd<2, 2>(a, B, nkvb, nqb, st); break;
-      default: launch_bwd<2, 1>(a, B, nkvb, nqb, st); break;
+      case 42: launch_bwd<4, 2, 0>(a, B, nkvb, nqb, st); break;
+      case 41: launch_bwd<4, 1, 0>(a, B, nkvb, nqb, st); break;
+      case 22: launch_bwd<2, 2, 0>(a, B, nkvb, nqb, st); break;
+      default: launch_bwd<2, 1, 0>(a, B, nkvb, nqb, st); break;
     }
     return;
   }
+  // dQ first: its sweep leaves Q, K, V and dO warm for the dK/dV launch
+  switch (nwq * 10 + rw) {
+    case 42: launch_bwd<4, 2, 2>(a, B, 0, nqb, st); break;
+    case 41: launch_bwd<4, 1, 2>(a, B, 0, nqb, st); break;
+    case 22: launch_bwd<2, 2, 2>(a, B, 0, nqb, st); break;
+    default: launch_bwd<2, 1, 2>(a, B, 0, nqb, st); break;
+  }
   if (nwk == 4)
-    launch_bwd<4, 1>(a, B, nkvb, 0, st);
+    launch_bwd<4, 1, 1>(a, B, nkvb, 0, st);
   else
-    launch_bwd<2, 1>(a, B, nkvb, 0, st);
-  dq_only(nqb);
+    launch_bwd<2, 1, 1>(a, B, nkvb, 0, st);
 }
 
 }  // namespace
