@@ -93,6 +93,7 @@ struct Ctx {
   float *lora_p = nullptr, *lora_g = nullptr, *lora_m = nullptr, *lora_v = nullptr;
   _Float16* shadow = nullptr;
   long long shadow_per_layer = 0, sh_a_qkv = 0, sh_a_o = 0, sh_bt_qkv = 0, sh_bt_o = 0;
+  _Float16* shadow_rm = nullptr;  // row-major twin of `shadow` (row epilogues)
   AdamHp* hp_dev = nullptr;
   AdamHp* host_hp = nullptr;
 

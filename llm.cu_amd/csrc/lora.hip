@@ -107,7 +107,15 @@ __global__ __launch_bounds__(NTH) void lora_grad_kernel(const LoraGradJob* __res
 }
 
 // Shadow index of arena element i (fp16 operand copy), or -1.
-__device__ __forceinline__ long long shadow_index(const AdamShadow& sh, long long i) {
+// Arena element i -> (shadow block offset within the layer, row, column,
+// row length) of its fp16 copies; the packed copy (a GEMM B operand) holds it
+// at packed_index(row, col, len), the row-major twin at row * len + col.
+struct ShadowPos {
+  long long base;  // layer base + block offset
+  long long row, col;
+  int len;
+};
+__device__ __forceinline__ ShadowPos shadow_pos(const AdamShadow& sh, long long i) {
   const long long l = i / sh.per_layer;
   long long j = i - l * sh.per_layer;
   int s = 0;
@@ -117,17 +125,22 @@ __device__ __forceinline__ long long shadow_index(const AdamShadow& sh, long lon
   j -= sh.seg_off[s];
   const int p = s >> 1;  // q, k, v, o
   const long long base = l * sh.shadow_per_layer;
-  // The shadows are GEMM B operands, stored fragment-packed.
   if ((s & 1) == 0) {  // A [16, d_in]: row r, column cc
     const int d_in = sh.d_in[p];
     const long long r = j / d_in, cc = j - r * d_in;
-    if (p < 3) return base + sh.a_qkv + packed_index(p * R + r, cc, d_in);
-    return base + sh.a_o + packed_index(r, cc, d_in);
+    if (p < 3) return {base + sh.a_qkv, p * R + r, cc, d_in};
+    return {base + sh.a_o, r, cc, d_in};
   }
   // B [d_out, 16]: element (o, r) -> row r, column o of B^T
   const long long o = j / R, r = j - o * R;
-  if (p < 3) return base + sh.bt_qkv + packed_index(p * R + r, sh.col_off[p] + o, sh.nt);
-  return base + sh.bt_o + packed_index(r, o, sh.d_out[3]);
+  if (p < 3) return {base + sh.bt_qkv, p * R + r, sh.col_off[p] + o, sh.nt};
+  return {base + sh.bt_o, r, o, sh.d_out[3]};
+}
+__device__ __forceinline__ void shadow_store(const AdamShadow& sh, long long i, float v) {
+  const ShadowPos q = shadow_pos(sh, i);
+  const _Float16 h = (_Float16)v;
+  sh.shadow[q.base + packed_index(q.row, q.col, q.len)] = h;
+  sh.rm[q.base + q.row * q.len + q.col] = h;
 }
 
 // src/kernels/lora.cu:206-220, one launch over the arena.  update = 0 only
@@ -153,7 +166,7 @@ __global__ __launch_bounds__(NTH) void adamw_kernel(float* __restrict__ p,
       pi = pi * (1.0f - hp.lr * hp.wd) - hp.lr * m_hat / (sqrtf(v_hat) + hp.eps);
       p[i] = pi;
     }
-    if (sh.shadow) sh.shadow[shadow_index(sh, i)] = (_Float16)pi;
+    if (sh.shadow) shadow_store(sh, i, pi);
   }
 }
 
@@ -187,7 +200,7 @@ __global__ __launch_bounds__(NTH) void lora_init_kernel(float* __restrict__ p,
     p[i] = val;
     m[i] = 0.f;
     v[i] = 0.f;
-    if (sh.shadow) sh.shadow[shadow_index(sh, i)] = (_Float16)val;
+    if (sh.shadow) shadow_store(sh, i, val);
   }
 }
 

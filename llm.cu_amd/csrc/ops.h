@@ -104,13 +104,15 @@ constexpr float kGradLogitScale = 16384.0f;  // 2^14
 // ---------------------------------------------------------------- row kernels
 // A token row of a split-K GEMM output as the input of a row epilogue: the
 // fp32 partials (summed in split order by the consumer) plus the LoRA
-// up-projection terms, taken from the fragment-packed fp16 adapter shadows:
+// up-projection terms, taken from the row-major fp16 twin of an adapter
+// shadow block ([rows, kp], the same values as the fragment-packed block the
+// GEMMs read; a row's columns are contiguous, so a wave's loads coalesce):
 //   y[c] += lscale * sum_r h[hidx + r] * shadow(row0 + r, c)   for c in [c0, c0 + n)
 // where h are the raw extra columns [hcol, hcol + nh) of the same GEMM.
 struct LoraTerm {
-  const _Float16* sh;  // element (row0 + r, c) at packed_index(row0 + r, c, kp)
+  const _Float16* shr;  // element (row0 + r, c) at shr[(row0 + r) * kp + c]
   int row0, kp;
-  int c0, n;           // multiples of 8
+  int c0, n;            // multiples of 8
   int hidx;
 };
 struct RowIn {
@@ -277,6 +279,7 @@ struct AdamHp {
 // [16][H] at bt_o.
 struct AdamShadow {
   _Float16* shadow;  // NULL: no shadow writes
+  _Float16* rm;      // row-major twin (same block offsets), written with shadow
   long long per_layer;
   long long seg_off[8];
   int d_in[4];

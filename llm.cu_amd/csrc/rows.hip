@@ -144,7 +144,7 @@ __device__ __forceinline__ void lora_load(const RowIn& in, int n, LoraRegs<P, NT
         L.hidx[p][s] = m.hidx;
 #pragma unroll
         for (int r = 0; r < R; ++r)
-          L.w[p][s][r] = *reinterpret_cast<const half4*>(m.sh + packed_index(m.row0 + r, c, m.kp));
+          L.w[p][s][r] = *reinterpret_cast<const half4*>(m.shr + (long long)(m.row0 + r) * m.kp + c);
       }
     }
   }
@@ -256,8 +256,8 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(const QkvPostArgs a, int 
     const LoraTerm& m = in.term[term];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      b0[r] = (float)m.sh[packed_index(m.row0 + r, base + lane, m.kp)];
-      b1[r] = (float)m.sh[packed_index(m.row0 + r, base + 64 + lane, m.kp)];
+      b0[r] = (float)m.shr[(long long)(m.row0 + r) * m.kp + base + lane];
+      b1[r] = (float)m.shr[(long long)(m.row0 + r) * m.kp + base + 64 + lane];
     }
   }
   const int t0 = blockIdx.y * QH_ROWS + w;

@@ -154,6 +154,7 @@ _Float16* Ctx::shadow_ptr(int l, long long off) const {
 AdamShadow Ctx::shadow_desc() const {
   AdamShadow sh{};
   sh.shadow = shadow;
+  sh.rm = shadow_rm;
   sh.per_layer = lora_per_layer;
   for (int i = 0; i < 8; ++i) sh.seg_off[i] = seg_off[i];
   sh.d_in[0] = sh.d_in[1] = sh.d_in[2] = H;
@@ -188,7 +189,7 @@ hipError_t Ctx::layer_fwd(int l, int B, const float* next_w, float* x_out, _Floa
   // Q/K/V (+ the three LoRA A) projections in one GEMM; the epilogue adds
   // s (x A^T) B^T per projection from the h columns.
   BSeg sq[2] = {wseg(w.wqkv), hseg(shadow_ptr(l, sh_a_qkv), 3 * kRank, H)};
-  const _Float16* bt_qkv = shadow_ptr(l, sh_bt_qkv);
+  const _Float16* bt_qkv = shadow_rm + (size_t)l * shadow_per_layer + sh_bt_qkv;
   const LoraTerm tq[3] = {{bt_qkv, 0, NT, 0, Q, 0},
                           {bt_qkv, kRank, NT, Q, KV, kRank},
                           {bt_qkv, 2 * kRank, NT, Q + KV, KV, 2 * kRank}};
@@ -206,7 +207,7 @@ hipError_t Ctx::layer_fwd(int l, int B, const float* next_w, float* x_out, _Floa
   LLMT_HIP_TRY(attn_fwd(aa, B, st));
   // O (+ LoRA A) projection, residual, FFN norm
   BSeg so[2] = {wseg(w.wo), hseg(shadow_ptr(l, sh_a_o), kRank, Q)};
-  const LoraTerm to[1] = {{shadow_ptr(l, sh_bt_o), 0, H, 0, H, 0}};
+  const LoraTerm to[1] = {{shadow_rm + (size_t)l * shadow_per_layer + sh_bt_o, 0, H, 0, H, 0}};
   LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.o16, Q, so, 2, T, Q, nullptr, 0, &go));
   LLMT_HIP_TRY(mark(CAT_ROWS));
   LLMT_HIP_TRY(o_post(row_in(go, H, kRank, 1, to), s.x_in, w.ffn_norm, eps, H, T, s.h, s.x_mid,
@@ -353,7 +354,7 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   LLMT_HIP_TRY(norm_bwd(nb, T, st));
   // O projection dX (+ dh_o through the B_o^T rows)
   BSeg so[2] = {wseg(w.woT), hseg(shadow_ptr(l, sh_bt_o), kRank, H)};
-  const LoraTerm tbo[1] = {{shadow_ptr(l, sh_a_o), 0, Q, 0, Q, 0}};
+  const LoraTerm tbo[1] = {{shadow_rm + (size_t)l * shadow_per_layer + sh_a_o, 0, Q, 0, Q, 0}};
   LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, og16, H, so, 2, T, H, nullptr, 0, &go_));
   LLMT_HIP_TRY(mark(CAT_ROWS));
   LLMT_HIP_TRY(o_dx_post(row_in(go_, Q, kRank, 1, tbo), ro(l), s.o16, nq, S, T, dh, dO16, delta,
@@ -375,7 +376,7 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   LLMT_HIP_TRY(qk_bwd(qb, T, st));
   // Q/K/V dX (+ dh_q, dh_k, dh_v through the B^T rows), attention norm bwd
   BSeg sq[2] = {wseg(w.wqkvT), hseg(shadow_ptr(l, sh_bt_qkv), 3 * kRank, NT)};
-  const _Float16* a_qkv = shadow_ptr(l, sh_a_qkv);
+  const _Float16* a_qkv = shadow_rm + (size_t)l * shadow_per_layer + sh_a_qkv;
   const LoraTerm tbq[3] = {{a_qkv, 0, H, 0, H, 0},
                            {a_qkv, kRank, H, 0, H, kRank},
                            {a_qkv, 2 * kRank, H, 0, H, 2 * kRank}};
