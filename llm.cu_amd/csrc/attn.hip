@@ -456,19 +456,23 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, _Float16* smem, int 
 }
 
 // ---------------------------------------------------------------- dK, dV
-// P and dS for one 64-query tile (rows query, column key); the tile's dO16
-// rows are already at the batch's dO scale gs, so dS comes out in it too.
+// P and dS for one 64-query tile (rows query, column key), both in the
+// batch's dO scale gs: ds arrives in each query row's own dO scale, so row
+// q's factor r = gs * dsc[q] (<= 1) brings dP there, and P times r is the
+// operand against the row-scaled dO16 of dV.
 template <bool MASK>
 __device__ __forceinline__ void ds_tile_kv(floatx4 (&p)[4], floatx4 (&ds)[4], const float* lse_s,
-                                           const float* del_s, float sl2, float gs, int qq0, int key,
-                                           int S, int lane) {
+                                           const float* del_s, const float* dsc_s, float sl2,
+                                           float gs, int qq0, int key, int S, int lane) {
   const int g = lane >> 4;
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
     const float4 ls = *reinterpret_cast<const float4*>(lse_s + mt * 16 + 4 * g);
     const float4 dl = *reinterpret_cast<const float4*>(del_s + mt * 16 + 4 * g);
+    const float4 sc = *reinterpret_cast<const float4*>(dsc_s + mt * 16 + 4 * g);
     const float lv[4] = {ls.x, ls.y, ls.z, ls.w};
     const float dv[4] = {dl.x, dl.y, dl.z, dl.w};
+    const float rv[4] = {sc.x * gs, sc.y * gs, sc.z * gs, sc.w * gs};
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       float pv = __builtin_amdgcn_exp2f(fmaf(p[mt][v], sl2, -lv[v] * LOG2E));
@@ -476,24 +480,18 @@ __device__ __forceinline__ void ds_tile_kv(floatx4 (&p)[4], floatx4 (&ds)[4], co
         const int qq = qq0 + mt * 16 + 4 * g + v;
         pv = (key <= qq && qq < S) ? pv : 0.f;
       }
-      p[mt][v] = pv;
-      ds[mt][v] = pv * fmaf(-dv[v], gs, ds[mt][v]);
+      p[mt][v] = pv * rv[v];
+      ds[mt][v] = pv * fmaf(ds[mt][v], rv[v], -dv[v] * gs);
     }
   }
-}
-
-// s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt left free): this thread's LDS
-// writes are done, the DMA loads of later tiles stay in flight.
-__device__ __forceinline__ void wait_lds() {
-  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
 }
 
 // grid (ceil(S / (16 NW)), nq, B): workgroup (key block kb of 16 NW keys,
 // query head h); wave w owns keys k0 + 16 w + c and loops over the 64-query
 // tiles at or after the block.  LDS: two buffers of (Q tile, dO16 tile,
-// lse[64], delta[64]).  Writes this query head's share of dK, dV (fp32) to
-// a.dkvp.
-constexpr int KV_BUF = 2 * TILE + 2 * BLK * 2;  // halves per dK/dV buffer
+// lse[64], delta[64], dsc[64]).  Writes this query head's share of dK, dV
+// (fp32) to a.dkvp.
+constexpr int KV_BUF = 2 * TILE + 3 * BLK * 2;  // halves per dK/dV buffer
 
 template <int NW>
 __device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* smem, float* red, int kb,
@@ -525,6 +523,7 @@ __device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* smem, fl
     float* vec = reinterpret_cast<float*>(buf + 2 * TILE);
     if (w == 0) dma_vec64(lse_h, qb * BLK, S, vec);
     if (w == NW - 1) dma_vec64(del_h, qb * BLK, S, vec + BLK);
+    if (w == NW / 2) dma_vec64(dsc_b, qb * BLK, S, vec + 2 * BLK);
   };
   issue(qb0, smem);
   const float gs = batch_do_scale<NT>(a.dsc, b, S, red);
@@ -540,33 +539,17 @@ __device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* smem, fl
     dkT[i] = floatx4{0.f, 0.f, 0.f, 0.f};
     dvT[i] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
-  constexpr int RPT = BLK * 16 / NT;  // 16-byte dO16 pieces a thread rescales per tile
   for (int qb = qb0; qb < nqb; ++qb) {
     wait_vm<0>();
     tile_barrier();
-    // the tile's dO16 rows to the batch scale: row q times gs * dsc[q] (a
-    // power of two <= 1, exact in fp16 short of underflow); the factors are
-    // loaded before the next tile's DMA so their wait leaves it in flight
-    float f[RPT];
-#pragma unroll
-    for (int k = 0; k < RPT; ++k)
-      f[k] = dsc_b[min(qb * BLK + ((int)(threadIdx.x + k * NT) >> 4), S - 1)];
-    asm volatile("" ::: "memory");
     if (qb + 1 < nqb) issue(qb + 1, smem + ((qb + 1 - qb0) & 1) * BUF);
-    _Float16* buf = smem + ((qb - qb0) & 1) * BUF;
-#pragma unroll
-    for (int k = 0; k < RPT; ++k) {
-      const int pi = threadIdx.x + k * NT;
-      half8* d = reinterpret_cast<half8*>(buf + TILE + toff(pi >> 4, pi & 15));
-      *d = *d * (_Float16)(f[k] * gs);
-    }
-    wait_lds();
-    tile_barrier();
+    const _Float16* buf = smem + ((qb - qb0) & 1) * BUF;
     if (qb * BLK + BLK - 1 < k0) continue;  // every query before every key of the wave
     const _Float16* Qs = buf;
     const _Float16* Ds = buf + TILE;
     const float* lse_s = reinterpret_cast<const float*>(buf + 2 * TILE);
     const float* del_s = lse_s + BLK;
+    const float* dsc_s = lse_s + 2 * BLK;
     floatx4 p[4], ds[4];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
@@ -580,9 +563,9 @@ __device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* smem, fl
     }
     // every query of the tile >= every key of the wave and < S: no mask
     if (qb * BLK >= k0 + 15 && qb * BLK + BLK <= S)
-      ds_tile_kv<false>(p, ds, lse_s, del_s, sl2, gs, qb * BLK, key, S, lane);
+      ds_tile_kv<false>(p, ds, lse_s, del_s, dsc_s, sl2, gs, qb * BLK, key, S, lane);
     else
-      ds_tile_kv<true>(p, ds, lse_s, del_s, sl2, gs, qb * BLK, key, S, lane);
+      ds_tile_kv<true>(p, ds, lse_s, del_s, dsc_s, sl2, gs, qb * BLK, key, S, lane);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const half8 pb = pair_frag(p[2 * j], p[2 * j + 1]);
