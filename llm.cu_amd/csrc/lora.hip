@@ -8,6 +8,8 @@
 // src/kernels/lora.cu:206-246 (224 launches per step); init
 // src/kernels/lora.cu:32-62 (cuRAND, not reproduced: this library draws its
 // own seeded normals).
+#include <algorithm>
+
 #include "ops.h"
 
 namespace llmt {
@@ -106,7 +108,6 @@ __global__ __launch_bounds__(NTH) void lora_grad_kernel(const LoraGradJob* __res
   }
 }
 
-// Shadow index of arena element i (fp16 operand copy), or -1.
 // Arena element i -> (shadow block offset within the layer, row, column,
 // row length) of its fp16 copies; the packed copy (a GEMM B operand) holds it
 // at packed_index(row, col, len), the row-major twin at row * len + col.
@@ -143,30 +144,74 @@ __device__ __forceinline__ void shadow_store(const AdamShadow& sh, long long i, 
   sh.rm[q.base + q.row * q.len + q.col] = h;
 }
 
-// src/kernels/lora.cu:206-220, one launch over the arena.  update = 0 only
-// refreshes the fp16 shadows from the parameters.
+// One AdamW element update (src/kernels/lora.cu:206-220); returns the new
+// parameter.
+__device__ __forceinline__ float adamw_elem(float* __restrict__ p, const float* __restrict__ g,
+                                            float* __restrict__ m, float* __restrict__ v,
+                                            long long i, const AdamHp& hp) {
+  const float gi = g[i];
+  const float mi = hp.beta1 * m[i] + (1.0f - hp.beta1) * gi;
+  const float vi = hp.beta2 * v[i] + (1.0f - hp.beta2) * gi * gi;
+  m[i] = mi;
+  v[i] = vi;
+  const float m_hat = mi / hp.bc1;
+  const float v_hat = vi / hp.bc2;
+  const float pi = p[i] * (1.0f - hp.lr * hp.wd) - hp.lr * m_hat / (sqrtf(v_hat) + hp.eps);
+  p[i] = pi;
+  return pi;
+}
+
+// Any contiguous set of parameters, no shadows.
 __global__ __launch_bounds__(NTH) void adamw_kernel(float* __restrict__ p,
                                                     const float* __restrict__ g,
                                                     float* __restrict__ m, float* __restrict__ v,
                                                     long long n,
-                                                    const AdamHp* __restrict__ hpp, int update,
-                                                    const AdamShadow sh) {
+                                                    const AdamHp* __restrict__ hpp) {
   const AdamHp hp = *hpp;
   for (long long i = (long long)blockIdx.x * NTH + threadIdx.x; i < n;
-       i += (long long)gridDim.x * NTH) {
-    float pi = p[i];
-    if (update) {
-      const float gi = g[i];
-      const float mi = hp.beta1 * m[i] + (1.0f - hp.beta1) * gi;
-      const float vi = hp.beta2 * v[i] + (1.0f - hp.beta2) * gi * gi;
-      m[i] = mi;
-      v[i] = vi;
-      const float m_hat = mi / hp.bc1;
-      const float v_hat = vi / hp.bc2;
-      pi = pi * (1.0f - hp.lr * hp.wd) - hp.lr * m_hat / (sqrtf(v_hat) + hp.eps);
-      p[i] = pi;
+       i += (long long)gridDim.x * NTH)
+    adamw_elem(p, g, m, v, i, hp);
+}
+
+// The whole arena with its fp16 shadows, one launch: blockIdx.y = layer x 8
+// + segment (q, k, v, o x A, B), so every block knows where its elements'
+// shadow rows and columns are (32-bit index math only).  update = 0 only
+// refreshes the shadows from the parameters.
+__global__ __launch_bounds__(NTH) void adamw_shadow_kernel(float* __restrict__ p,
+                                                           const float* __restrict__ g,
+                                                           float* __restrict__ m,
+                                                           float* __restrict__ v,
+                                                           const AdamHp* __restrict__ hpp,
+                                                           int update, const AdamShadow sh) {
+  const AdamHp hp = *hpp;
+  const int l = blockIdx.y >> 3, s = blockIdx.y & 7, q = s >> 1;
+  const long long i0 = (long long)l * sh.per_layer + sh.seg_off[s];
+  const int n = (int)((s < 7 ? sh.seg_off[s + 1] : sh.per_layer) - sh.seg_off[s]);
+  const long long lb = (long long)l * sh.shadow_per_layer;
+  // A [16, d_in]: element j = (r, c) -> row row0 + r, column c of a block of
+  // row length d_in; B [d_out, 16]: element j = (o, r) -> row row0 + r,
+  // column col0 + o of B^T (row length len)
+  const bool is_b = s & 1;
+  const int row0 = q < 3 ? q * R : 0;
+  const int len = is_b ? (q < 3 ? sh.nt : sh.d_out[3]) : sh.d_in[q];
+  const int col0 = is_b && q < 3 ? sh.col_off[q] : 0;
+  const long long base = lb + (is_b ? (q < 3 ? sh.bt_qkv : sh.bt_o) : (q < 3 ? sh.a_qkv : sh.a_o));
+  const unsigned ulen = (unsigned)len;
+  for (int j = blockIdx.x * NTH + threadIdx.x; j < n; j += gridDim.x * NTH) {
+    const long long i = i0 + j;
+    const float pi = update ? adamw_elem(p, g, m, v, i, hp) : p[i];
+    int row, col;
+    if (is_b) {
+      row = row0 + (j & (R - 1));
+      col = col0 + (j >> 4);
+    } else {
+      const unsigned r = (unsigned)j / ulen;
+      row = row0 + (int)r;
+      col = j - (int)(r * ulen);
     }
-    if (sh.shadow) shadow_store(sh, i, pi);
+    const _Float16 h = (_Float16)pi;
+    sh.shadow[base + packed_index(row, col, len)] = h;
+    sh.rm[base + (long long)row * len + col] = h;
   }
 }
 
@@ -243,8 +288,22 @@ hipError_t lora_grad(const LoraGradJob* jobs, const LoraGradPlan& plan, int laye
 
 hipError_t adamw(float* p, const float* g, float* m, float* v, long long n, const AdamHp* hp,
                  int update, const AdamShadow& sh, hipStream_t st) {
-  hipLaunchKernelGGL(adamw_kernel, dim3(grid_for(n)), dim3(NTH), 0, st, p, g, m, v, n, hp, update,
-                     sh);
+  if (!sh.shadow) {
+    if (!update) return hipSuccess;
+    hipLaunchKernelGGL(adamw_kernel, dim3(grid_for(n)), dim3(NTH), 0, st, p, g, m, v, n, hp);
+    LLMT_LAUNCH_CHECK();
+    return hipSuccess;
+  }
+  if (sh.per_layer <= 0 || n % sh.per_layer || !sh.rm) {
+    set_error("adamw: %lld parameters are not whole layers of %lld", n, sh.per_layer);
+    return hipErrorInvalidValue;
+  }
+  long long seg = 0;
+  for (int s = 0; s < 8; ++s)
+    seg = std::max(seg, (s < 7 ? sh.seg_off[s + 1] : sh.per_layer) - sh.seg_off[s]);
+  const unsigned bx = (unsigned)std::min<long long>((seg + 4 * NTH - 1) / (4 * NTH), 64);
+  hipLaunchKernelGGL(adamw_shadow_kernel, dim3(bx, (unsigned)(n / sh.per_layer * 8)), dim3(NTH), 0,
+                     st, p, g, m, v, hp, update, sh);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
