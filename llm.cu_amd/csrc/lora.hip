@@ -26,10 +26,11 @@ constexpr int NTH = 256;
 // (dy as the fp16 GEMM operand, row t scaled by the power of two 1 / xs[t],
 // which the G row takes back exactly)
 // A workgroup owns GC columns, four per lane (one 8- or 16-byte load of X per
-// token); its four waves take interleaved batches of TB tokens, issue the
-// batch's X loads together and read the batch's G rows (uniform across the
-// wave) through scalar loads, accumulating a 16 x 4 block per lane; the four
-// partial blocks are then added in LDS in wave order (deterministic).
+// token); its waves (four, or one for short token counts) take interleaved
+// batches of TB tokens, issue the batch's X loads together and stage the
+// batch's G rows in LDS (see lora_grad_acc), accumulating a 16 x 4 block per
+// lane; several waves' partial blocks are then added in LDS in wave order
+// (deterministic).
 constexpr int GC = 256;
 constexpr int TB = 16;
 template <bool F16>
@@ -41,26 +42,45 @@ __device__ __forceinline__ float4 load_x4(const void* X, long long off) {
   return *reinterpret_cast<const float4*>((const float*)X + off);
 }
 
-template <bool F16>
+// One wave's share of the token rows.  Per batch of TB tokens the wave loads
+// the batch's TB x 16 G block with one coalesced 16-byte load a lane (times
+// the row factor xs), stages it in its own 1 KB of LDS and reads each token's
+// 16 values back as broadcast LDS reads (same address in every lane).
+template <bool F16, int NW>
 __device__ __forceinline__ void lora_grad_acc(const LoraGradJob& jb, int T, int cc, int w,
-                                              float4 (&acc)[R]) {
+                                              float* gsw, float4 (&acc)[R]) {
   const int wu = __builtin_amdgcn_readfirstlane(w);
-  for (int t0 = wu * TB; t0 < T; t0 += (NTH / 64) * TB) {
+  const int lane = threadIdx.x & 63;
+  for (int t0 = wu * TB; t0 < T; t0 += NW * TB) {
     float4 x[TB];
 #pragma unroll
     for (int i = 0; i < TB; ++i) x[i] = load_x4<F16>(jb.X, (long long)min(t0 + i, T - 1) * jb.ldx + cc);
+    {
+      const int tok = t0 + (lane >> 2);
+      const int tc = min(tok, T - 1);
+      float4 g4 = *reinterpret_cast<const float4*>(jb.G + (long long)tc * jb.ldg + 4 * (lane & 3));
+      const float f = tok < T ? (jb.xs ? jb.xs[tc] : 1.0f) : 0.f;
+      g4 = make_float4(g4.x * f, g4.y * f, g4.z * f, g4.w * f);
+      *reinterpret_cast<float4*>(gsw + 4 * lane) = g4;
+    }
+    // tokens past T carry G = 0 (f = 0 above), so the batch runs whole
 #pragma unroll
     for (int i = 0; i < TB; ++i) {
-      if (t0 + i >= T) break;
-      const float* g = jb.G + (long long)(t0 + i) * jb.ldg;
-      const float xs = jb.xs ? jb.xs[t0 + i] : 1.0f;
+      float gr[R];
+#pragma unroll
+      for (int k = 0; k < R / 4; ++k) {
+        const float4 q = *reinterpret_cast<const float4*>(gsw + i * R + 4 * k);
+        gr[4 * k] = q.x;
+        gr[4 * k + 1] = q.y;
+        gr[4 * k + 2] = q.z;
+        gr[4 * k + 3] = q.w;
+      }
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const float gr = g[r] * xs;
-        acc[r].x += x[i].x * gr;
-        acc[r].y += x[i].y * gr;
-        acc[r].z += x[i].z * gr;
-        acc[r].w += x[i].w * gr;
+        acc[r].x += x[i].x * gr[r];
+        acc[r].y += x[i].y * gr[r];
+        acc[r].z += x[i].z * gr[r];
+        acc[r].w += x[i].w * gr[r];
       }
     }
   }
@@ -70,10 +90,13 @@ struct LoraGradGrid {
   int block_start[kLoraJobs + 1];  // column blocks of each job within a layer
 };
 
-__global__ __launch_bounds__(NTH) void lora_grad_kernel(const LoraGradJob* __restrict__ jobs,
-                                                        const LoraGradGrid G, int T, float lscale,
-                                                        int accumulate) {
-  __shared__ float red[NTH / 64][R][GC];  // 64 KB
+// NW waves per GC-column block share the token rows (interleaved batches of
+// TB) and add their 16 x GC partial blocks in LDS in wave order; NW = 1 (few
+// tokens) runs every token in order in one wave and stores from registers.
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void lora_grad_kernel(const LoraGradJob* __restrict__ jobs,
+                                                            const LoraGradGrid G, int T,
+                                                            float lscale, int accumulate) {
   const int bpl = G.block_start[kLoraJobs];
   const int layer = (int)blockIdx.x / bpl, lb = (int)blockIdx.x - layer * bpl;
   int j = 0;
@@ -85,26 +108,41 @@ __global__ __launch_bounds__(NTH) void lora_grad_kernel(const LoraGradJob* __res
   const int cb = (lb - G.block_start[j]) * GC;  // first column of the block
   const int c = cb + 4 * lane;                  // this lane's first column
   const int cc = c < jb.ncols ? c : 0;
+  __shared__ __attribute__((aligned(16))) float gsh[NW][TB * R];  // a wave's staged G batch
   float4 acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
   if (jb.x_f16)
-    lora_grad_acc<true>(jb, T, cc, w, acc);
+    lora_grad_acc<true, NW>(jb, T, cc, w, gsh[w], acc);
   else
-    lora_grad_acc<false>(jb, T, cc, w, acc);
+    lora_grad_acc<false, NW>(jb, T, cc, w, gsh[w], acc);
+  if constexpr (NW == 1) {
+    if (c >= jb.ncols) return;
 #pragma unroll
-  for (int r = 0; r < R; ++r) *reinterpret_cast<float4*>(&red[w][r][4 * lane]) = acc[r];
-  __syncthreads();
-  // thread i finishes column cb + i (all 16 r), summing the waves in order
-  const int col = cb + (int)threadIdx.x;
-  if (col >= jb.ncols) return;
+    for (int r = 0; r < R; ++r) {
+      const float a4[4] = {acc[r].x, acc[r].y, acc[r].z, acc[r].w};
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    float v = red[0][r][threadIdx.x];
+      for (int e = 0; e < 4; ++e) {
+        float* o = jb.out_is_B ? jb.out + (long long)(c + e) * R + r : jb.out + (long long)r * jb.ncols + c + e;
+        *o = (accumulate ? *o : 0.f) + lscale * a4[e];
+      }
+    }
+  } else {
+    __shared__ float red[NW][R][GC];  // 16 KB a wave
 #pragma unroll
-    for (int q = 1; q < NTH / 64; ++q) v += red[q][r][threadIdx.x];
-    float* o = jb.out_is_B ? jb.out + (long long)col * R + r : jb.out + (long long)r * jb.ncols + col;
-    *o = (accumulate ? *o : 0.f) + lscale * v;
+    for (int r = 0; r < R; ++r) *reinterpret_cast<float4*>(&red[w][r][4 * lane]) = acc[r];
+    __syncthreads();
+    // thread i finishes column cb + i (all 16 r), summing the waves in order
+    const int col = cb + (int)threadIdx.x;
+    if (col >= jb.ncols) return;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float v = red[0][r][threadIdx.x];
+#pragma unroll
+      for (int q = 1; q < NW; ++q) v += red[q][r][threadIdx.x];
+      float* o = jb.out_is_B ? jb.out + (long long)col * R + r : jb.out + (long long)r * jb.ncols + col;
+      *o = (accumulate ? *o : 0.f) + lscale * v;
+    }
   }
 }
 
@@ -280,8 +318,14 @@ hipError_t lora_grad(const LoraGradJob* jobs, const LoraGradPlan& plan, int laye
   LoraGradGrid G{};
   for (int i = 0; i < kLoraJobs; ++i)
     G.block_start[i + 1] = G.block_start[i] + (plan.ncols[i] + GC - 1) / GC;
-  hipLaunchKernelGGL(lora_grad_kernel, dim3(layers * G.block_start[kLoraJobs]), dim3(NTH), 0, st,
-                     jobs, G, T, lscale, accumulate);
+  // one wave a block while the blocks alone fill the CUs' wave slots at this
+  // token count (a block of four waves then only waits on its LDS sum)
+  const dim3 grid(layers * G.block_start[kLoraJobs]);
+  if (T <= 512)
+    hipLaunchKernelGGL(lora_grad_kernel<1>, grid, dim3(64), 0, st, jobs, G, T, lscale, accumulate);
+  else
+    hipLaunchKernelGGL(lora_grad_kernel<NTH / 64>, grid, dim3(NTH), 0, st, jobs, G, T, lscale,
+                       accumulate);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
