@@ -46,24 +46,37 @@ __device__ __forceinline__ float4 load_x4(const void* X, long long off) {
 // the batch's TB x 16 G block with one coalesced 16-byte load a lane (times
 // the row factor xs), stages it in its own 1 KB of LDS and reads each token's
 // 16 values back as broadcast LDS reads (same address in every lane).
+template <bool F16>
+__device__ __forceinline__ void lora_batch_load(const LoraGradJob& jb, int T, int cc, int t0,
+                                                int lane, float4 (&x)[TB], float4& g4) {
+#pragma unroll
+  for (int i = 0; i < TB; ++i) x[i] = load_x4<F16>(jb.X, (long long)min(t0 + i, T - 1) * jb.ldx + cc);
+  const int tok = t0 + (lane >> 2);
+  const int tc = min(tok, T - 1);
+  g4 = *reinterpret_cast<const float4*>(jb.G + (long long)tc * jb.ldg + 4 * (lane & 3));
+  const float f = tok < T ? (jb.xs ? jb.xs[tc] : 1.0f) : 0.f;
+  g4 = make_float4(g4.x * f, g4.y * f, g4.z * f, g4.w * f);
+}
+
+// One wave's share of the token rows.  Per batch of TB tokens the wave loads
+// the batch's TB x 16 G block with one coalesced 16-byte load a lane (times
+// the row factor xs; 0 past T), stages it in its own 1 KB of LDS and reads
+// each token's 16 values back as broadcast LDS reads (same address in every
+// lane).  The next batch's loads are issued before the current batch's FMAs.
 template <bool F16, int NW>
 __device__ __forceinline__ void lora_grad_acc(const LoraGradJob& jb, int T, int cc, int w,
                                               float* gsw, float4 (&acc)[R]) {
   const int wu = __builtin_amdgcn_readfirstlane(w);
   const int lane = threadIdx.x & 63;
-  for (int t0 = wu * TB; t0 < T; t0 += NW * TB) {
-    float4 x[TB];
-#pragma unroll
-    for (int i = 0; i < TB; ++i) x[i] = load_x4<F16>(jb.X, (long long)min(t0 + i, T - 1) * jb.ldx + cc);
-    {
-      const int tok = t0 + (lane >> 2);
-      const int tc = min(tok, T - 1);
-      float4 g4 = *reinterpret_cast<const float4*>(jb.G + (long long)tc * jb.ldg + 4 * (lane & 3));
-      const float f = tok < T ? (jb.xs ? jb.xs[tc] : 1.0f) : 0.f;
-      g4 = make_float4(g4.x * f, g4.y * f, g4.z * f, g4.w * f);
-      *reinterpret_cast<float4*>(gsw + 4 * lane) = g4;
-    }
-    // tokens past T carry G = 0 (f = 0 above), so the batch runs whole
+  int t0 = wu * TB;
+  if (t0 >= T) return;
+  float4 x[TB], g4;
+  lora_batch_load<F16>(jb, T, cc, t0, lane, x, g4);
+  for (; t0 < T; t0 += NW * TB) {
+    *reinterpret_cast<float4*>(gsw + 4 * lane) = g4;
+    float4 xn[TB], gn = g4;
+    const bool more = t0 + NW * TB < T;
+    if (more) lora_batch_load<F16>(jb, T, cc, t0 + NW * TB, lane, xn, gn);
 #pragma unroll
     for (int i = 0; i < TB; ++i) {
       float gr[R];
@@ -82,6 +95,11 @@ __device__ __forceinline__ void lora_grad_acc(const LoraGradJob& jb, int T, int 
         acc[r].z += x[i].z * gr[r];
         acc[r].w += x[i].w * gr[r];
       }
+    }
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < TB; ++i) x[i] = xn[i];
+      g4 = gn;
     }
   }
 }
