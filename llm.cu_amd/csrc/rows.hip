@@ -783,22 +783,21 @@ inline unsigned grid_elems(long long n) {
 
 }  // namespace
 
-// Token rows per workgroup of the one-term LoRA epilogues: the adapter
-// shadows (16 x 4 fp16 values per column piece) are loaded into registers
-// once per workgroup and reused for every row, keeping at least 512
-// workgroups.  Only for rows of at most 2 pieces per thread (P): wider rows
-// kept beside the shadows across the loop spill.  1 selects the one-row
-// kernel (shadows loaded per row).  LLMT_ROWS_PER_WG overrides for tuning.
+// Token rows per workgroup of the one-term LoRA epilogues.  One: the adapter
+// loads (row-major shadows, coalesced) cost less than serialising rows in a
+// workgroup (C4, 4096 rows: 51-53 us at one row against 57 us at eight).
+// LLMT_ROWS_PER_WG > 1 selects the loop variant (adapter values loaded once
+// per workgroup) for rows of at most 2 pieces per thread (P); wider rows kept
+// beside the adapter values across the loop spill.
 static int rows_per_wg(int T, int P) {
+  (void)T;
   if (P > 2) return 1;
   const char* e = getenv("LLMT_ROWS_PER_WG");
   if (e && *e) {
     const int v = atoi(e);
     if (v >= 1 && v <= 64) return v;
   }
-  int r = 1;
-  while (r < 8 && T / (2 * r) >= 512) r *= 2;
-  return r;
+  return 1;
 }
 
 static bool row_in_ok(const RowIn& in, int n, const char* who) {
