@@ -220,7 +220,7 @@ int llmt_attention_bwd(const void* q, const void* k, const void* v, const void* 
   const int T = B * S;
   Temps tmp(st);
   float* delta = tmp.get<float>((size_t)B * nq * S);
-  float* dsc = tmp.get<float>(T);
+  float* dsc = tmp.get<float>((size_t)T * nq);
   float* dkvp = tmp.get<float>((size_t)T * 2 * nq * kHeadDim);
   _Float16* dO16 = tmp.get<_Float16>((size_t)T * nq * kHeadDim);
   TRY_ARG(delta && dsc && dkvp && dO16, "llmt_attention_bwd: out of memory");
@@ -270,7 +270,7 @@ int llmt_attention_block_bwd(const void* q_raw, const void* k_raw, const void* v
   float* lse = tmp.get<float>((size_t)B * nq * S);
   float* dO = tmp.get<float>((size_t)T * Q);
   float* delta = tmp.get<float>((size_t)B * nq * S);
-  float* dsc = tmp.get<float>(T);
+  float* dsc = tmp.get<float>((size_t)T * nq);
   float* dqkv = tmp.get<float>((size_t)T * NT);
   float* dkvp = tmp.get<float>((size_t)T * 2 * Q);
   _Float16* dO16 = tmp.get<_Float16>((size_t)T * Q);

@@ -166,9 +166,9 @@ __device__ __forceinline__ half8 frag_global(const _Float16* base, long long ld,
 // zero.  Identical in every workgroup of b.  Row t enters the products
 // times r_t = gs * dsc[t] <= 1, which brings it to this common scale.
 template <int NT>
-__device__ float batch_do_scale(const float* __restrict__ dsc, int b, int S, float* red) {
+__device__ float batch_do_scale(const float* __restrict__ dsc_bh, int S, float* red) {
   float m = 0.f;
-  for (int s = threadIdx.x; s < S; s += NT) m = fmaxf(m, dsc[(long long)b * S + s]);
+  for (int s = threadIdx.x; s < S; s += NT) m = fmaxf(m, dsc_bh[s]);
   m = block_max<NT / 64>(m, red);
   return m > 0.f ? 1.0f / m : 1.0f;
 }
@@ -384,7 +384,7 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, _Float16* smem, int 
     }
     const bool ok = q < S;
     lse2[r] = ok ? a.lse[((long long)b * a.nq + h) * S + q] * LOG2E : 0.f;
-    const float dsc = ok ? a.dsc[rowb + q] : 0.f;
+    const float dsc = ok ? a.dsc[((long long)b * a.nq + h) * S + q] : 0.f;
     del[r] = dsc > 0.f ? a.delta[((long long)b * a.nq + h) * S + q] / dsc : 0.f;
     fq[r] = a.sm_scale * dsc;
   }
@@ -509,7 +509,7 @@ __device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* smem, fl
   const float sl2 = a.sm_scale * LOG2E;
   const float* lse_h = a.lse + ((long long)b * a.nq + h) * S;
   const float* del_h = a.delta + ((long long)b * a.nq + h) * S;
-  const float* dsc_b = a.dsc + rowb;
+  const float* dsc_b = a.dsc + ((long long)b * a.nq + h) * S;
   const _Float16* qbase = a.q + rowb * a.ldq + h * HD;
   const _Float16* dbase = a.dO16 + rowb * a.ld16 + h * HD;
   const int qb0 = (kb * KB) / BLK;
@@ -526,7 +526,7 @@ __device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* smem, fl
     if (w == NW / 2) dma_vec64(dsc_b, qb * BLK, S, vec + 2 * BLK);
   };
   issue(qb0, smem);
-  const float gs = batch_do_scale<NT>(a.dsc, b, S, red);
+  const float gs = batch_do_scale<NT>(dsc_b, S, red);
   half8 kf[4], vf[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
@@ -638,36 +638,33 @@ __global__ __launch_bounds__(256) void gqa_sum_kernel(const float* __restrict__ 
   }
 }
 
-// Per token row: delta[b, h, s] = sum_d dO[t, h, d] * O[t, h, d] (one wave
-// per head), then dO16[t] = fp16(dO[t] * sc) with sc the power-of-two scale
-// of max |dO[t, :]| and dsc[t] = 1 / sc (0 for an all-zero row).
+// Per token row, one wave per head: delta[b, h, s] = sum_d dO * O, and
+// dO16 = fp16(dO * sc) with sc the power-of-two scale of the head's max |dO|,
+// dsc[b, h, s] = 1 / sc (0 for an all-zero head row).
 __global__ __launch_bounds__(256) void attn_delta_kernel(const float* __restrict__ dO, long long ldd,
                                                          const _Float16* __restrict__ o,
                                                          long long ldo, int nq, int S,
                                                          float* __restrict__ delta,
                                                          _Float16* __restrict__ dO16,
                                                          long long ld16, float* __restrict__ dsc) {
-  __shared__ float red[4];
   const int t = blockIdx.x;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int b = t / S, s = t - b * S;
-  float amax = 0.f;
   for (int h = w; h < nq; h += 4) {
     const float* d = dO + (long long)t * ldd + h * HD;
     const _Float16* oo = o + (long long)t * ldo + h * HD;
     const float d0 = d[lane], d1 = d[lane + 64];
-    amax = fmaxf(amax, fmaxf(fabsf(d0), fabsf(d1)));
     const float v = wave_sum(d0 * (float)oo[lane] + d1 * (float)oo[lane + 64]);
-    if (lane == 0) delta[((long long)b * nq + h) * S + s] = v;
-  }
-  amax = block_max<4>(amax, red);
-  const float sc = pow2_scale_for(amax, kDoScaleExp);
-  if (threadIdx.x == 0) dsc[t] = pow2_inv_scale_for(amax, kDoScaleExp);
-  for (int h = w; h < nq; h += 4) {
-    const float* d = dO + (long long)t * ldd + h * HD;
+    const float amax = wave_max(fmaxf(fabsf(d0), fabsf(d1)));
+    const float sc = pow2_scale_for(amax, kDoScaleExp);
+    const long long bhs = ((long long)b * nq + h) * S + s;
+    if (lane == 0) {
+      delta[bhs] = v;
+      dsc[bhs] = pow2_inv_scale_for(amax, kDoScaleExp);
+    }
     _Float16* d16 = dO16 + (long long)t * ld16 + h * HD;
-    d16[lane] = (_Float16)(d[lane] * sc);
-    d16[lane + 64] = (_Float16)(d[lane + 64] * sc);
+    d16[lane] = (_Float16)(d0 * sc);
+    d16[lane + 64] = (_Float16)(d1 * sc);
   }
 }
 

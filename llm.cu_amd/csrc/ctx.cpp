@@ -191,7 +191,7 @@ int Ctx::init() {
   TRY_PTR(rinv2 = alloc_n<float>(T));
   TRY_PTR(dgu16 = alloc_n<_Float16>(T * 2 * I));
   TRY_PTR(delta = alloc_n<float>((size_t)maxB * nq * S));
-  TRY_PTR(dsc = alloc_n<float>(T));
+  TRY_PTR(dsc = alloc_n<float>((size_t)maxB * nq * S));
   TRY_PTR(dqkv32 = alloc_n<float>(T * NT));
   TRY_PTR(dkvp = alloc_n<float>((size_t)T * 2 * Q));
   TRY_PTR(dO16 = alloc_n<_Float16>((size_t)T * Q));

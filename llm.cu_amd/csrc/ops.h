@@ -189,9 +189,10 @@ hipError_t qk_norm_rope(const _Float16* raw, const float* qn, const float* kn, c
 hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st);
 hipError_t swiglu_bwd(const RowIn& in, const float* rinv_in, const float* gu, int I, int T,
                       _Float16* dgu16, float* rinv_out, hipStream_t st);
-// dX of the O projection -> the attention's dO operand: dO16 row t =
-// fp16(dO[t] * 2^k) with 2^k the row's power-of-two scale, dsc[t] = 2^-k (0
-// for an all-zero row), delta[b, h, s] = sum_d dO * O.
+// dX of the O projection -> the attention's dO operand: dO16 (row t, head h)
+// = fp16(dO * 2^k) with 2^k the power-of-two scale of that head row,
+// dsc[b, h, s] = 2^-k (0 for an all-zero head row), delta[b, h, s] =
+// sum_d dO * O.
 hipError_t o_dx_post(const RowIn& in, const float* rinv_in, const _Float16* o16, int nq, int S,
                      int T, float* dh_out, _Float16* dO16, float* delta, float* dsc,
                      hipStream_t st);
@@ -223,9 +224,9 @@ struct AttnArgs {
   _Float16* o;          // forward output [T, ldo]
   long long ldo;
   float* lse;           // [B, nq, S] natural-log LSE of the scaled scores
-  const _Float16* dO16;  // backward: fp16 [T, ld16], row t = dO[t] / dsc[t]
+  const _Float16* dO16;  // backward: fp16 [T, ld16], head h of row t = dO / dsc[b, h, s]
   long long ld16;
-  const float* dsc;     // [T] inverse power-of-two scale of dO16 row t (0: zero row)
+  const float* dsc;     // [B, nq, S] inverse power-of-two scale of each dO16 head row (0: zero)
   const float* delta;   // [B, nq, S] rowsum(dO * O)
   float* dq;            // fp32 [T, ldgq]
   long long ldgq;

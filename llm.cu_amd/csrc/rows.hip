@@ -28,6 +28,8 @@ namespace llmt {
 
 namespace {
 
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
 constexpr int RT = 512;  // threads per row workgroup
 constexpr int RW = RT / 64;
 constexpr int HD = 128;  // head_dim
@@ -602,29 +604,123 @@ __global__ __launch_bounds__(RT) void swiglu_bwd_kernel(const RowIn in,
 }
 
 // dX of the O projection (+ dh_o in the LoRA-B^T columns; the reduction
-// already added s (dh_o A_o)): d_o = row * rinv; writes dh_o, the attention
-// backward's dO operand (fp16, scaled by the row's power of two, with the
-// inverse scale in dsc[t]) and the flash-backward row statistic
-// delta[b, h, s] = sum_d dO * O.
-template <int P, bool MULTI>
-__global__ __launch_bounds__(RT) void o_dx_post_kernel(const RowIn in,
-                                                       const float* __restrict__ rinv_in,
-                                                       const _Float16* __restrict__ o16, int nq,
-                                                       int S, float* __restrict__ dh_out,
-                                                       _Float16* __restrict__ dO16,
-                                                       float* __restrict__ delta,
-                                                       float* __restrict__ dsc, int T,
-                                                       int rpw) {
-  __shared__ float red[2 * RW];
+// adds s (dh_o A_o)): d_o = row * rinv; writes dh_o, the attention
+// backward's dO operand and the flash-backward row statistic
+// delta[b, h, s] = sum_d dO * O.  dO goes out as fp16 per (row, head), scaled
+// by the power of two of that head's max |dO| (inverse in dsc[b, h, s]).
+// Tiled by head: workgroup = head h x 8 rows, four waves of two rows, lane l
+// owns columns 2l, 2l + 1 of the head (8-byte loads of every split partial),
+// so delta and the head's max are wave reductions and a lane's adapter slice
+// (2 x 16 values) stays in registers for both its rows.
+constexpr int OD_ROWS = 8;
+
+__global__ __launch_bounds__(256) void o_dx_post_kernel(const RowIn in,
+                                                        const float* __restrict__ rinv_in,
+                                                        const _Float16* __restrict__ o16, int nq,
+                                                        int S, int T, float* __restrict__ dh_out,
+                                                        _Float16* __restrict__ dO16,
+                                                        float* __restrict__ delta,
+                                                        float* __restrict__ dsc) {
+  constexpr int RPW = OD_ROWS / 4;
+  const int h = blockIdx.x;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int Q = nq * HD, col = h * HD + 2 * lane;
+  const bool lora = in.nterm > 0;
+  float b0[R], b1[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    b0[r] = 0.f;
+    b1[r] = 0.f;
+  }
+  if (lora) {
+    const LoraTerm& m = in.term[0];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const half2v bb = *reinterpret_cast<const half2v*>(m.shr + (long long)(m.row0 + r) * m.kp + col);
+      b0[r] = (float)bb[0];
+      b1[r] = (float)bb[1];
+    }
+  }
+  const int t0 = blockIdx.y * OD_ROWS + w;
+  float2 x[RPW];
+  float hv[RPW];
+  half2v oo[RPW];
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int t = min(t0 + 4 * i, T - 1);
+    const float* prow = in.part + (long long)t * in.ldp;
+    x[i] = *reinterpret_cast<const float2*>(prow + col);
+    hv[i] = lora ? prow[in.hcol + (lane & 15)] : 0.f;
+    oo[i] = *reinterpret_cast<const half2v*>(o16 + (long long)t * Q + col);
+  }
+  for (int k = 1; k < in.split; ++k) {
+    float2 y[RPW];
+    float yh[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      const int t = min(t0 + 4 * i, T - 1);
+      const float* prow = in.part + (long long)k * in.ss + (long long)t * in.ldp;
+      y[i] = *reinterpret_cast<const float2*>(prow + col);
+      yh[i] = lora ? prow[in.hcol + (lane & 15)] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      x[i].x += y[i].x;
+      x[i].y += y[i].y;
+      hv[i] += yh[i];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int t = t0 + 4 * i;
+    if (t >= T) break;
+    const float rs = rinv_in[t];
+    float v0 = x[i].x, v1 = x[i].y;
+    if (lora) {
+      float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float hr = __shfl(hv[i], r, 64);
+        acc0 += hr * b0[r];
+        acc1 += hr * b1[r];
+      }
+      v0 += acc0 * in.lscale;
+      v1 += acc1 * in.lscale;
+      if (h == 0 && lane < R) dh_out[(long long)t * 64 + 3 * R + lane] = hv[i] * rs;
+    }
+    const float d0 = v0 * rs, d1 = v1 * rs;
+    const int b = t / S, s = t - b * S;
+    const long long bhs = ((long long)b * nq + h) * S + s;
+    const float dl = wave_sum(d0 * (float)oo[i][0] + d1 * (float)oo[i][1]);
+    const float amax = wave_max(fmaxf(fabsf(d0), fabsf(d1)));
+    const float sc = pow2_scale_for(amax, kDoScaleExp);
+    if (lane == 0) {
+      delta[bhs] = dl;
+      dsc[bhs] = pow2_inv_scale_for(amax, kDoScaleExp);
+    }
+    half2v o2;
+    o2[0] = (_Float16)(d0 * sc);
+    o2[1] = (_Float16)(d1 * sc);
+    *reinterpret_cast<half2v*>(dO16 + (long long)t * Q + col) = o2;
+  }
+}
+
+// The same epilogue with one token row per workgroup, for GEMMs with many
+// split partials (a thread sums 16-byte pieces of every split, one load
+// each): thread i owns columns 4 i .. 4 i + 3 of piece p, so a head is 32
+// consecutive threads and its delta and max are 32-lane shuffle sums.
+template <int P>
+__global__ __launch_bounds__(RT) void o_dx_post_row_kernel(const RowIn in,
+                                                           const float* __restrict__ rinv_in,
+                                                           const _Float16* __restrict__ o16,
+                                                           int nq, int S,
+                                                           float* __restrict__ dh_out,
+                                                           _Float16* __restrict__ dO16,
+                                                           float* __restrict__ delta,
+                                                           float* __restrict__ dsc) {
   __shared__ float hs[64];
+  const int t = blockIdx.x;
   const int Q = nq * HD;
-  LoraRegs<P, 1> L;
-  if constexpr (MULTI) lora_load<P, 1>(in, Q, L);
-  const int nrows = MULTI ? rpw : 1;
-  for (int it = 0; it < nrows; ++it) {
-  const int t = blockIdx.x * nrows + it;
-  if (t >= T) break;
-  if (it) __syncthreads();
   half4 ov[P];
 #pragma unroll
   for (int p = 0; p < P; ++p) {
@@ -634,37 +730,35 @@ __global__ __launch_bounds__(RT) void o_dx_post_kernel(const RowIn in,
   const float rs = rinv_in[t];
   float4 v[P], hv;
   load_row<P, true>(in, t, Q, v, hv);
-  if constexpr (!MULTI) lora_load<P, 1>(in, Q, L);
+  LoraRegs<P, 1> L;
+  lora_load<P, 1>(in, Q, L);
   store_h(in, hv, hs);
   if ((int)threadIdx.x < in.nh / 4)
     *reinterpret_cast<float4*>(dh_out + (long long)t * 64 + 3 * R + 4 * threadIdx.x) = mul4(hv, rs);
   __syncthreads();
   lora_apply<P, 1>(in, hs, L, v);
   const int b = t / S, s = t - b * S;
-  float amax = 0.f;
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int c = 4 * ((int)threadIdx.x + p * RT);
-    const bool live = c < Q;
+    const bool live = c < Q;  // uniform over the head's 32 threads
     const float4 d = mul4(v[p], rs);
-    v[p] = d;
-    if (live) amax = fmaxf(amax, amax4(d));
-    // delta = sum over a head's 128 columns = 32 consecutive threads
     float part = live ? d.x * (float)ov[p][0] + d.y * (float)ov[p][1] + d.z * (float)ov[p][2] +
                             d.w * (float)ov[p][3]
                       : 0.f;
+    float amax = live ? amax4(d) : 0.f;
 #pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) part += __shfl_xor(part, o, 64);
-    if (live && (threadIdx.x & 31) == 0) delta[((long long)b * nq + c / HD) * S + s] = part;
-  }
-  amax = block_max<RW>(amax, red);
-  const float sc = pow2_scale_for(amax, kDoScaleExp);
-  if (threadIdx.x == 0) dsc[t] = pow2_inv_scale_for(amax, kDoScaleExp);
-#pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int c = 4 * ((int)threadIdx.x + p * RT);
-    if (c < Q) st_h4(dO16 + (long long)t * Q + c, mul4(v[p], sc));
-  }
+    for (int o = 16; o >= 1; o >>= 1) {
+      part += __shfl_xor(part, o, 64);
+      amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    }
+    if (!live) continue;
+    st_h4(dO16 + (long long)t * Q + c, mul4(d, pow2_scale_for(amax, kDoScaleExp)));
+    if ((threadIdx.x & 31) == 0) {
+      const long long bhs = ((long long)b * nq + c / HD) * S + s;
+      delta[bhs] = part;
+      dsc[bhs] = pow2_inv_scale_for(amax, kDoScaleExp);
+    }
   }
 }
 
@@ -982,23 +1076,26 @@ hipError_t o_dx_post(const RowIn& in, const float* rinv_in, const _Float16* o16,
                      hipStream_t st) {
   const int Q = nq * HD;
   if (!row_in_ok(in, Q, "o_dx_post")) return hipErrorInvalidValue;
-  const int P = (Q + 4 * RT - 1) / (4 * RT);
-  const int rpw = rows_per_wg(T, P);
-  const dim3 g((T + rpw - 1) / rpw);
-  switch (P) {
-    case 1:
-      if (rpw > 1) hipLaunchKernelGGL((o_dx_post_kernel<1, true>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO16, delta, dsc, T, rpw);
-      else hipLaunchKernelGGL((o_dx_post_kernel<1, false>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO16, delta, dsc, T, rpw);
-      break;
-    case 2:
-      if (rpw > 1) hipLaunchKernelGGL((o_dx_post_kernel<2, true>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO16, delta, dsc, T, rpw);
-      else hipLaunchKernelGGL((o_dx_post_kernel<2, false>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO16, delta, dsc, T, rpw);
-      break;
-    case 3: hipLaunchKernelGGL((o_dx_post_kernel<3, false>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO16, delta, dsc, T, rpw); break;
-    case 4: hipLaunchKernelGGL((o_dx_post_kernel<4, false>), g, dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO16, delta, dsc, T, rpw); break;
-    default:
-      set_error("o_dx_post: row width %d above %d", Q, 16 * RT);
-      return hipErrorInvalidValue;
+  if (in.nterm > 1 || (in.nterm == 1 && (in.term[0].c0 != 0 || in.term[0].n != Q ||
+                                         in.term[0].hidx != 0 || in.nh != R))) {
+    set_error("o_dx_post: one LoRA term over all %d columns with its 16 h columns", Q);
+    return hipErrorInvalidValue;
+  }
+  // up to two split partials: tiled by head; more: one row per workgroup
+  // (16-byte loads of each partial), measured faster at the headline shape
+  if (in.split <= 2) {
+    hipLaunchKernelGGL(o_dx_post_kernel, dim3(nq, (T + OD_ROWS - 1) / OD_ROWS), dim3(256), 0, st,
+                       in, rinv_in, o16, nq, S, T, dh_out, dO16, delta, dsc);
+  } else {
+    switch ((Q + 4 * RT - 1) / (4 * RT)) {
+      case 1: hipLaunchKernelGGL(o_dx_post_row_kernel<1>, dim3(T), dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO16, delta, dsc); break;
+      case 2: hipLaunchKernelGGL(o_dx_post_row_kernel<2>, dim3(T), dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO16, delta, dsc); break;
+      case 3: hipLaunchKernelGGL(o_dx_post_row_kernel<3>, dim3(T), dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO16, delta, dsc); break;
+      case 4: hipLaunchKernelGGL(o_dx_post_row_kernel<4>, dim3(T), dim3(RT), 0, st, in, rinv_in, o16, nq, S, dh_out, dO16, delta, dsc); break;
+      default:
+        set_error("o_dx_post: row width %d above %d", Q, 16 * RT);
+        return hipErrorInvalidValue;
+    }
   }
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
