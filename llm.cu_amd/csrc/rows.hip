@@ -75,7 +75,7 @@ __device__ __forceinline__ float4 sum_splits4(const float* p, int split, long lo
 // group 0's).  One loop for both, with up to 24 loads in flight per batch
 // and branch-free in-order adds, so a row costs one memory round trip per
 // batch of splits.
-template <int P, bool HH>
+template <int P, bool HH, int LOADS = 24>
 __device__ __forceinline__ void load_row(const RowIn& in, int t, int n, float4 (&v)[P], float4& h) {
   const float* prow = in.part + (long long)t * in.ldp;
   int off[P];
@@ -87,7 +87,7 @@ __device__ __forceinline__ void load_row(const RowIn& in, int t, int n, float4 (
   }
   const int hoff = in.hcol + 4 * ((int)threadIdx.x < in.nh / 4 ? (int)threadIdx.x : 0);
   if (HH) h = ld4(prow + hoff);
-  constexpr int SB = 24 / (P + (HH ? 1 : 0));
+  constexpr int SB = LOADS / (P + (HH ? 1 : 0));
   for (int k = 1; k < in.split; k += SB) {
     float4 x[SB][P], y[SB];
 #pragma unroll
@@ -548,6 +548,56 @@ __global__ __launch_bounds__(RT) void norm_bwd_kernel(const NormBwdArgs a) {
   for (int p = 0; p < P; ++p) {
     const int c = 4 * ((int)threadIdx.x + p * RT);
     if (c < H) st_h4(a.g16 + (long long)t * H + c, mul4(v[p], sc));
+  }
+}
+
+// The same for rows of one piece per thread (P = 1) with three adapter terms
+// at large T: the adapter values are loaded once per workgroup and kept in
+// registers for NR rows (their 196 KB at H = 2048 would otherwise be read
+// again for every row).
+template <int NR>
+__global__ __launch_bounds__(RT) void norm_bwd_lora_kernel(const NormBwdArgs a, int T) {
+  __shared__ float red[2 * RW];
+  __shared__ float hs[64];
+  const int H = a.H;
+  const int c = 4 * (int)threadIdx.x;
+  const int cc = min(c, H - 4);
+  LoraRegs<1, 3> L;
+  lora_load<1, 3>(a.in, H, L);
+  const float4 ww = ld4(a.w + cc);
+#pragma unroll 1
+  for (int it = 0; it < NR; ++it) {
+    const int t = blockIdx.x * NR + it;
+    if (t >= T) break;
+    if (it) __syncthreads();
+    const float4 x = ld4(a.x + (long long)t * H + cc);
+    const float4 dr = a.dres_in ? ld4(a.dres_in + (long long)t * H + cc) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float rs = (a.rinv_in ? a.rinv_in[t] : 1.0f) * a.gscale;
+    float4 v[1], hv;
+    load_row<1, true, 4>(a.in, t, H, v, hv);  // 4 loads in flight: the adapter values hold 96 VGPRs
+    store_h(a.in, hv, hs);
+    if ((int)threadIdx.x < a.in.nh / 4)
+      *reinterpret_cast<float4*>(a.dh_out + (long long)t * 64 + a.dh_col + 4 * threadIdx.x) =
+          mul4(hv, rs);
+    __syncthreads();
+    lora_apply<1, 3>(a.in, hs, L, v);
+    const bool live = c < H;
+    const float4 d = mul4(v[0], rs);
+    const float dot = live ? d.x * ww.x * x.x + d.y * ww.y * x.y + d.z * ww.z * x.z + d.w * ww.w * x.w : 0.f;
+    const float ssx = live ? x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w : 0.f;
+    const float2 s2 = block_sum2(dot, ssx, red);
+    const float r = rsqrtf(s2.y / H + a.eps);
+    const float coef = r * r / H * s2.x;
+    const float4 o = make_float4(dr.x + r * (d.x * ww.x - coef * x.x), dr.y + r * (d.y * ww.y - coef * x.y),
+                                 dr.z + r * (d.z * ww.z - coef * x.z), dr.w + r * (d.w * ww.w - coef * x.w));
+    if (live) {
+      *reinterpret_cast<float4*>(a.dres_out + (long long)t * H + c) = o;
+      if (a.dmid_out) *reinterpret_cast<float4*>(a.dmid_out + (long long)t * H + c) = o;
+    }
+    const float amax = block_max<RW>(live ? amax4(o) : 0.f, red);
+    const float sc = pow2_scale_for(amax);
+    if (threadIdx.x == 0) a.rinv_out[t] = 1.0f / sc;
+    if (live) st_h4(a.g16 + (long long)t * H + c, mul4(o, sc));
   }
 }
 
@@ -1041,6 +1091,20 @@ hipError_t qk_norm_rope(const _Float16* raw, const float* qn, const float* kn, c
 hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st) {
   if (!row_in_ok(a.in, a.H, "norm_bwd") || a.dh_col % 4) return hipErrorInvalidValue;
   const int P = (a.H + 4 * RT - 1) / (4 * RT);
+  // three adapter terms over one-piece rows at large T: NR rows a workgroup
+  // (C4, 4096 rows: 89 us at one row, 69 us at four; eight measured best;
+  // LLMT_NORM_LORA_ROWS overrides, 1 = the one-row kernel)
+  const char* e = getenv("LLMT_NORM_LORA_ROWS");
+  const int nr = e && *e ? atoi(e) : (T >= 2048 ? 8 : 1);
+  if (P == 1 && a.in.nterm == 3 && nr > 1) {
+    switch (nr) {
+      case 2: hipLaunchKernelGGL(norm_bwd_lora_kernel<2>, dim3((T + 1) / 2), dim3(RT), 0, st, a, T); break;
+      case 8: hipLaunchKernelGGL(norm_bwd_lora_kernel<8>, dim3((T + 7) / 8), dim3(RT), 0, st, a, T); break;
+      default: hipLaunchKernelGGL(norm_bwd_lora_kernel<4>, dim3((T + 3) / 4), dim3(RT), 0, st, a, T); break;
+    }
+    LLMT_LAUNCH_CHECK();
+    return hipSuccess;
+  }
   switch (P) {
     case 1: hipLaunchKernelGGL(norm_bwd_kernel<1>, dim3(T), dim3(RT), 0, st, a); break;
     case 2: hipLaunchKernelGGL(norm_bwd_kernel<2>, dim3(T), dim3(RT), 0, st, a); break;

@@ -134,3 +134,17 @@ def test_rows_per_workgroup(small, monkeypatch, rows):
     assert abs(loss - small["loss_ref"]) < LOSS_TOL
     errs = grad_errors(ctx.lora_get("grad"), small["grads_ref"], SMALL)
     assert max(errs.values()) < GRAD_TOL
+
+
+@pytest.mark.parametrize("rows", ["2", "4", "8"])
+def test_norm_backward_lora_rows(small, monkeypatch, rows):
+    """The attention-norm backward with its three adapter terms looping over
+    several token rows per workgroup (adapter values held in registers),
+    including a partial last group at 8, gives the oracle's step."""
+    monkeypatch.setenv("LLMT_NORM_LORA_ROWS", rows)
+    ctx = small["ctx"]
+    ctx.set_graph(False)
+    loss = ctx.forward_backward(small["tok"], small["tgt"])
+    assert abs(loss - small["loss_ref"]) < LOSS_TOL
+    errs = grad_errors(ctx.lora_get("grad"), small["grads_ref"], SMALL)
+    assert max(errs.values()) < GRAD_TOL
