@@ -1224,8 +1224,12 @@ static SkinnyPlan skinny_plan(int M, int N, int K) {
   const int target = env_int("LLMT_GEMM_TARGET_WG", 256);
   SkinnyPlan best{0, 0};
   int best_w = 0;
+  // Very long reductions (the logits' dX, K = V): every column tile re-reads
+  // its K range of A, so 128-column tiles halve that traffic (163 -> 141 us
+  // at M = 128, N = 2048, K = 151936); elsewhere 64/48-column tiles.
+  const bool wide = K >= 32768;
   for (int nb : {4, 3, 2, 6, 8}) {
-    if (!forced && nb != 4 && nb != 3) continue;
+    if (!forced && (wide ? nb != 8 : (nb != 4 && nb != 3))) continue;
     if (forced && nb != forced) continue;
     const int tiles = (frags + nb - 1) / nb * mt;
     int split = target / tiles;
