@@ -777,7 +777,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, unsig
 // slot of 16-byte piece p (0..7) of A row r in a stage
 __device__ __forceinline__ int a_slot(int r, int p) { return p ^ ((r >> 1) & 7); }
 
-template <int S, int NB>
+// GLU: fragment f of the tile is the gate (f even) or up (f odd) row block of
+// the same 16 columns (split 1, one segment, N = 2 glu); the epilogue writes
+// [gate | up] and fp16(silu(gate) * up) as the large-tile kernel's.
+template <int S, int NB, bool GLU = false>
 __global__ __launch_bounds__(512) void gemm_skinny_kernel(const GemmArgs g) {
   constexpr int AB = 16384;                  // A bytes per stage
   constexpr int SB = AB + NB * 2048;         // bytes per stage
@@ -806,6 +809,12 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(const GemmArgs g) {
   __amdgpu_buffer_rsrc_t brs[BPW];
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
+    if constexpr (GLU) {
+      const int f = min(wr + 4 * i, NB - 1);
+      const long long rb = (f & 1) * (g.glu >> 4) + (long long)blockIdx.x * (NB / 2) + (f >> 1);
+      brs[i] = make_rsrc((const _Float16*)g.seg[0].ptr + rb * ksteps * 512, (unsigned)(ksteps * 1024u));
+      continue;
+    }
     const int nn = n0 + 16 * min(wr + 4 * i, NB - 1);
     int s = 0;
 #pragma unroll
@@ -891,6 +900,23 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(const GemmArgs g) {
     for (int j = 0; j < NB; ++j) acc[i][j] += xch[(i * NB + j) * 64 + lane];
 
   float* C = g.C + (long long)blockIdx.y * g.split_stride;
+  if constexpr (GLU) {
+#pragma unroll
+    for (int jj = 0; jj < NB / 2; ++jj) {
+      const int col = (blockIdx.x * (NB / 2) + jj) * 16 + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const long long row = m0 + (2 * wr + i) * 16 + (lane >> 4) * 4 + v;
+          const float gt = acc[i][2 * jj][v], up = acc[i][2 * jj + 1][v];
+          C[row * g.ldc + col] = gt;
+          C[row * g.ldc + g.glu + col] = up;
+          g.glu16[row * g.ldglu + col] = (_Float16)(gt / (1.0f + __expf(-gt)) * up);
+        }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
     const int nn = n0 + 16 * j;
@@ -1282,9 +1308,12 @@ static int big_split(int M, int N, int K, int max_split) {
 
 // The DMA large-tile kernel (the default for big tiles) carries the SwiGLU
 // epilogue: 256-wide tiles over 8 waves, gate/up fragment pairs per wave.
-bool gemm_glu_ok(int M, int I, int K) {
-  return big_tiles(M, K) && I % 128 == 0 && env_int("LLMT_GEMM_BIG_KIND", 2) == 2 &&
-         big_wn(2 * I) == 4 && env_int("LLMT_GEMM_DMA_WAVES", 8) == 8 && big_split(M, 2 * I, K, 64) == 1;
+bool gemm_glu_ok(int M, int I, int K, bool i8) {
+  if (big_tiles(M, K))
+    return I % 128 == 0 && env_int("LLMT_GEMM_BIG_KIND", 2) == 2 && big_wn(2 * I) == 4 &&
+           env_int("LLMT_GEMM_DMA_WAVES", 8) == 8 && big_split(M, 2 * I, K, 64) == 1;
+  // the skinny kernel, 32 gate + 32 up columns a workgroup, split 1
+  return !i8 && skinny_ok(M, 2 * I, K) && I % 32 == 0 && env_int("LLMT_GEMM_SKINNY_GLU", 1) != 0;
 }
 
 int gemm_pick_split(int M, int N, int K, int max_split) {
@@ -1360,10 +1389,17 @@ hipError_t gemm_nt(const GemmArgs& g, hipStream_t st) {
       set_error("gemm_nt: segment rows must be a multiple of 16 (%d)", g.seg[i].rows);
       return hipErrorInvalidValue;
     }
-  if (g.glu && !(g.glu % 128 == 0 && g.N == 2 * g.glu && g.nseg == 1 && g.split == 1 &&
-                 g.glu16 && gemm_glu_ok(g.M, g.glu, g.K))) {
-    set_error("gemm_nt: SwiGLU epilogue needs the large-tile kernel, split 1, N = 2 x %d", g.glu);
+  if (g.glu && !(g.N == 2 * g.glu && g.nseg == 1 && g.split == 1 && g.glu16 &&
+                 gemm_glu_ok(g.M, g.glu, g.K, g.seg[0].is_i8))) {
+    set_error("gemm_nt: SwiGLU epilogue needs split 1, one segment, N = 2 x %d", g.glu);
     return hipErrorInvalidValue;
+  }
+  if (g.glu && !use_big_tiles(g)) {
+    hipLaunchKernelGGL((gemm_skinny_kernel<4, 4, true>), dim3(g.glu / 32, 1, g.M / 128), dim3(512),
+                       0, st, g);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) set_error("gemm_nt launch: %s", hipGetErrorString(e));
+    return e;
   }
   hipError_t e;
   const int m16 = g.M / 16;

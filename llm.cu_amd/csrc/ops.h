@@ -39,8 +39,8 @@ struct GemmArgs {
   _Float16* glu16;
   int ldglu;
 };
-// The fused SwiGLU epilogue exists for this GEMM shape (the large-tile kernel).
-bool gemm_glu_ok(int M, int I, int K);
+// The fused SwiGLU epilogue exists for this GEMM shape and weight type.
+bool gemm_glu_ok(int M, int I, int K, bool i8);
 
 // Every B segment is fragment-packed (packed_index, common.h) with row
 // length K; rows a multiple of 16.  A is row-major fp16 [M, lda], K % 32 == 0.

@@ -214,7 +214,7 @@ hipError_t Ctx::layer_fwd(int l, int B, const float* next_w, float* x_out, _Floa
                       s.xn2, st));
   // gate/up, SwiGLU (in the GEMM epilogue where the large-tile kernel runs)
   BSeg sg[1] = {wseg(w.wgu)};
-  if (gemm_glu_ok(T, I, H)) {
+  if (gemm_glu_ok(T, I, H, sg[0].is_i8)) {
     LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn2, H, sg, 1, T, H, s.gu, 2 * I, nullptr, a16));
   } else {
     LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn2, H, sg, 1, T, H, nullptr, 0, &go));
