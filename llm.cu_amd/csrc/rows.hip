@@ -816,6 +816,12 @@ __global__ __launch_bounds__(RT) void o_dx_post_row_kernel(const RowIn in,
 // backward (inverse rotation, src/kernels/rope.cu:57-89) -> QK-RMSNorm
 // backward with x = q_raw/k_raw (src/kernels/rmsnorm.cu:53-95) ->
 // dy = [dq_raw | dk_raw | dv] fp32 (the LoRA dB operand) and fp16 (scaled).
+// HPW > 0: every load of a row (a wave's nq + nkv <= HPW RW heads, then
+// KV <= 2 RT v columns; G = the query heads per KV head when K/V come as
+// shares, 0 when not) is issued before any of the math, the shares summed
+// afterwards in the same order (the rows are latency-bound at small T).
+// HPW = 0: one head at a time, any shape.
+template <int HPW, int G>
 __global__ __launch_bounds__(RT) void qk_bwd_kernel(const QkBwdArgs a) {
   extern __shared__ float ds[];  // [NT]
   __shared__ float red[2 * RW];
@@ -837,21 +843,78 @@ __global__ __launch_bounds__(RT) void qk_bwd_kernel(const QkBwdArgs a) {
     for (int gi = 0; gi < group; ++gi) s += sh[(kv * a.nq + j * group + gi) * HD + d];
     return s;
   };
-  for (int hh = wave; hh < a.nq + a.nkv; hh += RW) {
+  auto head = [&](int hh, float d0, float d1, float x0, float x1, float w0,
+                  float w1) __attribute__((always_inline)) {
     const int base = hh * HD;
-    const float d0 = grad(base + lane), d1 = grad(base + 64 + lane);
     const float n0 = d0 * cs + d1 * sn, n1 = d1 * cs - d0 * sn;
-    const float* w = hh < a.nq ? a.qn : a.kn;
-    const float w0 = w[lane], w1 = w[lane + 64];
-    const float* xr = a.qkraw + (long long)t * (Q + KV) + base;
-    const float x0 = xr[lane], x1 = xr[lane + 64];
     const float r = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / HD + a.eps);
     const float dot = wave_sum(n0 * w0 * x0 + n1 * w1 * x1);
     const float coef = r * r / HD * dot;
     ds[base + lane] = r * (n0 * w0 - coef * x0);
     ds[base + 64 + lane] = r * (n1 * w1 - coef * x1);
+  };
+  const float* xrow = a.qkraw + (long long)t * (Q + KV);
+  if constexpr (HPW > 0) {
+    constexpr int NV = G > 0 ? G : 1;  // loads per gradient value
+    // isq: column c is a q column (its NV loads all read g[c]; the address is
+    // a select, not a branch, so no load waits on another)
+    auto load = [&](int c, bool isq, float* v) __attribute__((always_inline)) {
+      if constexpr (G == 0) {
+        v[0] = g[c];
+      } else {
+        const int kv = c < Q + KV ? 0 : 1;
+        const int cc = c - Q - kv * KV, j = cc / HD, d = cc - j * HD;
+#pragma unroll
+        for (int k = 0; k < NV; ++k)
+          v[k] = *(isq ? g + c : sh + (kv * a.nq + j * NV + k) * HD + d);
+      }
+    };
+    auto sum = [&](const float* v, bool isq) __attribute__((always_inline)) {
+      float x = v[0];
+#pragma unroll
+      for (int k = 1; k < NV; ++k)
+        if (!isq) x += v[k];
+      return x;
+    };
+    const float wq0 = a.qn[lane], wq1 = a.qn[lane + 64], wk0 = a.kn[lane], wk1 = a.kn[lane + 64];
+    float vv[2][NV];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int c = Q + KV + threadIdx.x + u * RT;
+      load(c < NT ? c : Q + KV, false, vv[u]);
+    }
+    float d0[HPW][NV], d1[HPW][NV], x0[HPW], x1[HPW];
+#pragma unroll
+    for (int k = 0; k < HPW; ++k) {
+      const int hh = __builtin_amdgcn_readfirstlane(wave + k * RW);
+      const int base = (hh < a.nq + a.nkv ? hh : 0) * HD;
+      load(base + lane, base < Q, d0[k]);
+      load(base + 64 + lane, base < Q, d1[k]);
+      x0[k] = xrow[base + lane];
+      x1[k] = xrow[base + 64 + lane];
+    }
+#pragma unroll
+    for (int k = 0; k < HPW; ++k)
+      if (wave + k * RW < a.nq + a.nkv) {
+        const bool isq = wave + k * RW < a.nq;
+        head(wave + k * RW, sum(d0[k], isq), sum(d1[k], isq), x0[k], x1[k], isq ? wq0 : wk0,
+             isq ? wq1 : wk1);
+      }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int c = Q + KV + threadIdx.x + u * RT;
+      if (c < NT) ds[c] = sum(vv[u], false);
+    }
+  } else {
+    for (int hh = wave; hh < a.nq + a.nkv; hh += RW) {
+      const int base = hh * HD;
+      const float* w = hh < a.nq ? a.qn : a.kn;
+      head(hh, grad(base + lane), grad(base + 64 + lane), xrow[base + lane], xrow[base + 64 + lane],
+           w[lane], w[lane + 64]);
+    }
   }
-  for (int c = Q + KV + threadIdx.x; c < NT; c += RT) ds[c] = grad(c);
+  if constexpr (HPW == 0)
+    for (int c = Q + KV + threadIdx.x; c < NT; c += RT) ds[c] = grad(c);
   __syncthreads();
   float amax = 0.f;
   for (int c = threadIdx.x; c < NT; c += RT) {
@@ -1167,7 +1230,23 @@ hipError_t o_dx_post(const RowIn& in, const float* rinv_in, const _Float16* o16,
 
 hipError_t qk_bwd(const QkBwdArgs& a, int T, hipStream_t st) {
   const int NT = (a.nq + 2 * a.nkv) * HD;
-  hipLaunchKernelGGL(qk_bwd_kernel, dim3(T), dim3(RT), NT * sizeof(float), st, a);
+  const int hpw = (a.nq + a.nkv + RW - 1) / RW;
+  const int G = a.dkvp ? a.nq / a.nkv : 0;
+  const size_t lds = NT * sizeof(float);
+  const char* e = getenv("LLMT_QK_BWD_HOIST");
+  const bool hoist = (!e || atoi(e) != 0) && hpw <= 4 && a.nkv * HD <= 2 * RT &&
+                     (G == 0 || G == 1 || G == 2 || G == 4);
+  const int key = hoist ? hpw * 8 + G : 0;
+  auto go = [&](auto kern) { hipLaunchKernelGGL(kern, dim3(T), dim3(RT), lds, st, a); };
+  switch (key) {
+#define LLMT_QK_CASE(H, GG) \
+  case H * 8 + GG: go(qk_bwd_kernel<H, GG>); break;
+#define LLMT_QK_CASES(H) LLMT_QK_CASE(H, 0) LLMT_QK_CASE(H, 1) LLMT_QK_CASE(H, 2) LLMT_QK_CASE(H, 4)
+    LLMT_QK_CASES(1) LLMT_QK_CASES(2) LLMT_QK_CASES(3) LLMT_QK_CASES(4)
+#undef LLMT_QK_CASES
+#undef LLMT_QK_CASE
+    default: go(qk_bwd_kernel<0, 0>); break;
+  }
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }

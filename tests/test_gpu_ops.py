@@ -35,11 +35,13 @@ def test_gemm_f16_matches_fp32(dev, L, M, N, K):
 @pytest.mark.parametrize("nb,stages", [("2", "4"), ("3", "3"), ("4", "4"), ("6", "3"), ("8", "4"),
                                        ("4", "0"), ("3", "5"), ("8", "5"), ("4", "6"),
                                        ("3", "6")])
-@pytest.mark.parametrize("M,N,K", [(128, 2048 + 48, 2048), (256, 160, 4096), (128, 12288, 1024)])
+@pytest.mark.parametrize("M,N,K", [(128, 2048 + 48, 2048), (256, 160, 4096), (128, 12288, 1024),
+                                   (128, 512, 64), (128, 256, 192), (128, 4096, 320)])
 def test_gemm_f16_skinny_tiles(dev, L, monkeypatch, nb, stages, M, N, K):
     """Every tile width (nb 16-column fragments) / ring depth of the
     M % 128 == 0 path (0 stages: the register-staged kernel), including
-    partial last column tiles."""
+    partial last column tiles and reductions shorter than the ring
+    (K / 64 = 1, 3, 5 stages)."""
     monkeypatch.setenv("LLMT_GEMM_SKINNY_NB", nb)
     monkeypatch.setenv("LLMT_GEMM_SKINNY_STAGES", stages)
     g = _seed(M + N + K + int(nb))

@@ -148,3 +148,26 @@ def test_norm_backward_lora_rows(small, monkeypatch, rows):
     assert abs(loss - small["loss_ref"]) < LOSS_TOL
     errs = grad_errors(ctx.lora_get("grad"), small["grads_ref"], SMALL)
     assert max(errs.values()) < GRAD_TOL
+
+
+@pytest.mark.parametrize("nq,nkv,hoist", [(2, 2, "1"), (8, 2, "1"), (8, 2, "0"), (16, 8, "1")])
+def test_qk_backward_head_layouts(dev, monkeypatch, nq, nkv, hoist):
+    """The QK-norm / RoPE backward for GQA groups 1, 4 and 2 with one, two
+    and three heads a wave (every load of a row issued before the math) and
+    the one-head-at-a-time form (hoist 0) give the oracle's step."""
+    monkeypatch.setenv("LLMT_QK_BWD_HOIST", hoist)
+    dims = ref.Dims(hidden=256, n_layers=2, n_heads=nq, n_kv_heads=nkv, head_dim=128,
+                    intermediate=512, vocab=2048)
+    print(f"case: heads {nq}/{nkv} hoist {hoist}", flush=True)
+    W, ad, tok, tgt = small_problem(dims)
+    loss_ref, grads_ref, _ = oracle_grads(W, ad, tok, tgt, dims)
+    ctx = llmt.Context(llmt.make_dims(dims), max_batch=2, seq_len=64)
+    try:
+        upload_model(ctx, W, dev)
+        ctx.lora_set("param", llmt.flatten_adapters(ad).to(dev))
+        loss = ctx.forward_backward(tok.to(dev), tgt.to(dev))
+        assert abs(loss - float(loss_ref)) < LOSS_TOL
+        errs = grad_errors(ctx.lora_get("grad"), grads_ref, dims)
+        assert max(errs.values()) < GRAD_TOL, max(errs.items(), key=lambda kv: kv[1])
+    finally:
+        ctx.close()
