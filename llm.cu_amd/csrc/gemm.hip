@@ -901,15 +901,17 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(const GemmArgs g) {
 
   float* C = g.C + (long long)blockIdx.y * g.split_stride;
   if constexpr (GLU) {
+    const _Float16* cs = g.seg[0].colscale;
 #pragma unroll
     for (int jj = 0; jj < NB / 2; ++jj) {
       const int col = (blockIdx.x * (NB / 2) + jj) * 16 + (lane & 15);
+      const float sg = cs ? (float)cs[col] : 1.0f, su = cs ? (float)cs[g.glu + col] : 1.0f;
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const long long row = m0 + (2 * wr + i) * 16 + (lane >> 4) * 4 + v;
-          const float gt = acc[i][2 * jj][v], up = acc[i][2 * jj + 1][v];
+          const float gt = acc[i][2 * jj][v] * sg, up = acc[i][2 * jj + 1][v] * su;
           C[row * g.ldc + col] = gt;
           C[row * g.ldc + g.glu + col] = up;
           g.glu16[row * g.ldglu + col] = (_Float16)(gt / (1.0f + __expf(-gt)) * up);
