@@ -142,6 +142,8 @@ struct Ctx {
   bool use_graph = false;
   hipGraphExec_t graph_exec = nullptr;
   int graph_batch = 0, graph_adam = -1;
+  const int* graph_tok = nullptr;  // input pointers the graph copies from (NULL: none)
+  const int* graph_tgt = nullptr;
   bool profiling = false;
   std::vector<hipEvent_t> prof_ev;
   std::vector<int> prof_cat;

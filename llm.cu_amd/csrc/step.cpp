@@ -562,7 +562,9 @@ static int stage_inputs(Ctx* c, const int* tokens, const int* targets, int batch
   return LLMT_OK;
 }
 
-static int set_hp(Ctx* c, const llmt_hparams* hp, int step) {
+// AdamW hyper-parameters of `step` into the pinned staging slot (copied to
+// the device by set_hp, or by the step graph's own copy node).
+static int set_hp_host(Ctx* c, const llmt_hparams* hp, int step) {
   TRY_ARG(hp && step >= 1, "llmt_step: hparams NULL or step < 1");
   AdamHp h{};
   h.lr = hp->lr;
@@ -576,20 +578,49 @@ static int set_hp(Ctx* c, const llmt_hparams* hp, int step) {
   // The pinned staging slot may still be read by an in-flight copy of the
   // previous step; the stream is idle here (every step ends synchronised).
   *c->host_hp = h;
+  return LLMT_OK;
+}
+
+static int set_hp(Ctx* c, const llmt_hparams* hp, int step) {
+  int rc = set_hp_host(c, hp, step);
+  if (rc) return rc;
   TRY_HIP(hipMemcpyAsync(c->hp_dev, c->host_hp, sizeof(AdamHp), hipMemcpyHostToDevice, c->st));
   return LLMT_OK;
 }
 
-static int run_step(Ctx* c, int batch, int with_adam, float* loss_host) {
+// Graph replays take the input copies (tokens, targets, and the staged
+// hyper-parameters when the step has AdamW) as nodes of the step graph, so a
+// step is one launch; the graph is keyed by the token/target pointers.
+static bool graph_inputs(const Ctx* c) {
+  static const int on = [] {
+    const char* e = getenv("LLMT_GRAPH_INPUTS");
+    return e ? atoi(e) : 1;
+  }();
+  return c->use_graph && !c->profiling && on != 0;
+}
+
+// tokens/targets non-NULL: the inputs (and, with AdamW, the staged
+// hyper-parameters) are copied inside the graph instead of before it.
+static int run_step(Ctx* c, int batch, int with_adam, float* loss_host,
+                    const int* tokens = nullptr, const int* targets = nullptr) {
   if (c->use_graph && !c->profiling) {
-    if (!c->graph_exec || c->graph_batch != batch || c->graph_adam != with_adam) {
+    if (!c->graph_exec || c->graph_batch != batch || c->graph_adam != with_adam ||
+        c->graph_tok != tokens || c->graph_tgt != targets) {
       if (c->graph_exec) {
         hipGraphExecDestroy(c->graph_exec);
         c->graph_exec = nullptr;
       }
       hipGraph_t g;
       TRY_HIP(hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
-      hipError_t e = c->device_step(batch, with_adam);
+      hipError_t e = hipSuccess;
+      if (tokens) {
+        const size_t n = (size_t)batch * c->S * sizeof(int);
+        e = hipMemcpyAsync(c->tok_buf, tokens, n, hipMemcpyDefault, c->st);
+        if (e == hipSuccess) e = hipMemcpyAsync(c->tgt_buf, targets, n, hipMemcpyDefault, c->st);
+        if (e == hipSuccess && with_adam)
+          e = hipMemcpyAsync(c->hp_dev, c->host_hp, sizeof(AdamHp), hipMemcpyHostToDevice, c->st);
+      }
+      if (e == hipSuccess) e = c->device_step(batch, with_adam);
       hipError_t e2 = hipStreamEndCapture(c->st, &g);
       TRY_HIP(e);
       TRY_HIP(e2);
@@ -598,6 +629,8 @@ static int run_step(Ctx* c, int batch, int with_adam, float* loss_host) {
       TRY_HIP(e);
       c->graph_batch = batch;
       c->graph_adam = with_adam;
+      c->graph_tok = tokens;
+      c->graph_tgt = targets;
     }
     TRY_HIP(hipGraphLaunch(c->graph_exec, c->st));
   } else {
@@ -617,6 +650,10 @@ int llmt_step(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
   Ctx* c = C_(ctx);
   int rc = check_tokens(c, tokens, targets, batch);
   if (rc) return rc;
+  if (graph_inputs(c)) {
+    if ((rc = set_hp_host(c, hp, step))) return rc;
+    return run_step(c, batch, 1, loss_host, tokens, targets);
+  }
   if ((rc = set_hp(c, hp, step))) return rc;
   if ((rc = stage_inputs(c, tokens, targets, batch))) return rc;
   return run_step(c, batch, 1, loss_host);
@@ -628,6 +665,7 @@ int llmt_forward_backward(llmt_ctx* ctx, const int* tokens, const int* targets, 
   Ctx* c = C_(ctx);
   int rc = check_tokens(c, tokens, targets, batch);
   if (rc) return rc;
+  if (graph_inputs(c)) return run_step(c, batch, 0, loss_host, tokens, targets);
   if ((rc = stage_inputs(c, tokens, targets, batch))) return rc;
   return run_step(c, batch, 0, loss_host);
 }

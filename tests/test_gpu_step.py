@@ -171,3 +171,51 @@ def test_qk_backward_head_layouts(dev, monkeypatch, nq, nkv, hoist):
         assert max(errs.values()) < GRAD_TOL, max(errs.items(), key=lambda kv: kv[1])
     finally:
         ctx.close()
+
+
+def test_graph_copies_inputs_each_replay(small, dev):
+    """With the input copies inside the step graph: new token contents under
+    the same pointers, then other buffers, give the eager step's loss and
+    gradients on every replay (forward + backward, and the full step whose
+    AdamW hyper-parameters are staged for each step)."""
+    ctx = small["ctx"]
+    g = torch.Generator().manual_seed(99)
+    wins = [torch.randint(0, SMALL.vocab, (2, 65), generator=g, dtype=torch.int32) for _ in range(3)]
+    ref = []
+    ctx.set_graph(False)
+    for w in wins:
+        ref.append((ctx.forward_backward(w[:, :-1].contiguous().to(dev), w[:, 1:].contiguous().to(dev)),
+                    ctx.lora_get("grad").clone()))
+    tok = torch.empty(2, 64, dtype=torch.int32, device=dev)
+    tgt = torch.empty(2, 64, dtype=torch.int32, device=dev)
+    ctx.set_graph(True)
+    try:
+        for i, w in enumerate(wins):          # same pointers, new contents
+            tok.copy_(w[:, :-1])
+            tgt.copy_(w[:, 1:])
+            loss = ctx.forward_backward(tok, tgt)
+            assert loss == ref[i][0]
+            assert torch.equal(ctx.lora_get("grad"), ref[i][1])
+        w = wins[0]                            # other buffers: the graph is rebuilt
+        loss = ctx.forward_backward(w[:, :-1].contiguous().to(dev), w[:, 1:].contiguous().to(dev))
+        assert loss == ref[0][0]
+        # full steps: AdamW with per-step bias corrections, graph vs eager
+        p0 = ctx.lora_get("param").clone()
+        m0, v0 = ctx.lora_get("m").clone(), ctx.lora_get("v").clone()
+        hp = llmt.hparams()
+        tok.copy_(wins[1][:, :-1])
+        tgt.copy_(wins[1][:, 1:])
+        graph_losses = [ctx.step(tok, tgt, hp, s) for s in (1, 2)]
+        p_graph = ctx.lora_get("param").clone()
+        ctx.set_graph(False)
+        ctx.lora_set("param", p0)
+        ctx.lora_set("m", m0)
+        ctx.lora_set("v", v0)
+        eager_losses = [ctx.step(tok, tgt, hp, s) for s in (1, 2)]
+        assert graph_losses == eager_losses
+        assert torch.equal(ctx.lora_get("param"), p_graph)
+        ctx.lora_set("param", p0)
+        ctx.lora_set("m", m0)
+        ctx.lora_set("v", v0)
+    finally:
+        ctx.set_graph(False)
