@@ -144,6 +144,7 @@ struct Ctx {
   int graph_batch = 0, graph_adam = -1;
   const int* graph_tok = nullptr;  // input pointers the graph copies from (NULL: none)
   const int* graph_tgt = nullptr;
+  bool inputs_move = false;  // input pointers changed between steps: copies stay outside the graph
   bool profiling = false;
   std::vector<hipEvent_t> prof_ev;
   std::vector<int> prof_cat;

@@ -590,13 +590,21 @@ static int set_hp(Ctx* c, const llmt_hparams* hp, int step) {
 
 // Graph replays take the input copies (tokens, targets, and the staged
 // hyper-parameters when the step has AdamW) as nodes of the step graph, so a
-// step is one launch; the graph is keyed by the token/target pointers.
-static bool graph_inputs(const Ctx* c) {
+// step is one launch; the graph is keyed by the token/target pointers.  A
+// caller whose pointers change between steps would rebuild it every step, so
+// the first change switches the context to copies outside the graph (one
+// rebuild, then the graph is reused whatever the pointers).
+static bool graph_inputs(Ctx* c, const int* tokens, const int* targets) {
   static const int on = [] {
     const char* e = getenv("LLMT_GRAPH_INPUTS");
     return e ? atoi(e) : 1;
   }();
-  return c->use_graph && !c->profiling && on != 0;
+  if (!c->use_graph || c->profiling || on == 0 || c->inputs_move) return false;
+  if (c->graph_exec && c->graph_tok && (c->graph_tok != tokens || c->graph_tgt != targets)) {
+    c->inputs_move = true;
+    return false;
+  }
+  return true;
 }
 
 // tokens/targets non-NULL: the inputs (and, with AdamW, the staged
@@ -650,7 +658,7 @@ int llmt_step(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
   Ctx* c = C_(ctx);
   int rc = check_tokens(c, tokens, targets, batch);
   if (rc) return rc;
-  if (graph_inputs(c)) {
+  if (graph_inputs(c, tokens, targets)) {
     if ((rc = set_hp_host(c, hp, step))) return rc;
     return run_step(c, batch, 1, loss_host, tokens, targets);
   }
@@ -665,7 +673,7 @@ int llmt_forward_backward(llmt_ctx* ctx, const int* tokens, const int* targets, 
   Ctx* c = C_(ctx);
   int rc = check_tokens(c, tokens, targets, batch);
   if (rc) return rc;
-  if (graph_inputs(c)) return run_step(c, batch, 0, loss_host, tokens, targets);
+  if (graph_inputs(c, tokens, targets)) return run_step(c, batch, 0, loss_host, tokens, targets);
   if ((rc = stage_inputs(c, tokens, targets, batch))) return rc;
   return run_step(c, batch, 0, loss_host);
 }
