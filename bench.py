@@ -6,23 +6,29 @@ seq 128, token ids uniform over the vocabulary, next-token targets.  The step
 runs as one captured HIP graph of libllmt.so kernels (llmt_step); inputs are
 resident in HBM before the timed region.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c3|c4] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c3|c4] [--only] [--no-cpu]
     python bench.py --copy-cal      # plain 512 MiB copies (PMC byte-counter scale)
 
 Prints ONE JSON line.  Besides the contract fields it carries
-  roofline:     the frozen-weight GEMMs (the step's dominant kernel family):
-                the step's GEMM launches replayed back to back as one HIP
-                graph, timed with HIP events on the context's stream;
-                achieved = streamed weight bytes per launch / average launch
-                time, against 8 TB/s HBM (C4: TFLOP/s against 2.5 PFLOP/s);
-                traffic = measured HBM bytes per launch (rocprofv3 FETCH_SIZE
-                and WRITE_SIZE passes scaled by the copy calibration, read
-                from profiles/gemm_c2_traffic.md);
+  roofline:     the frozen-weight GEMMs (the step's dominant kernel family),
+                each GEMM kind of the step replayed back to back as a HIP
+                graph of its own (llmt_profile_kernels), timed with HIP
+                events on the context's stream; achieved = streamed weight
+                bytes per launch / average launch time, against 8 TB/s HBM
+                (C4: TFLOP/s against 2.5 PFLOP/s); traffic = measured HBM
+                bytes per launch (rocprofv3 FETCH_SIZE and WRITE_SIZE passes
+                scaled by the copy calibration, read from
+                profiles/gemm_c2_traffic.md);
+  kernels:      per-category kernel milliseconds of a step from the same
+                replays (kernels only: their sum, kernels_sum_ms, is below
+                ms_per_step by the launch gaps);
+  bandwidth_kernels: AdamW, SwiGLU backward, RMSNorm backward and the fused
+                CE in GB/s of their compulsory bytes;
   cpu_baseline: the CPU oracle (PyTorch fp32, oracle/lora_step.py) on a
                 bounded sample of the same step;
-  kernels:      per-category kernel milliseconds of one profiled step.
---config c3 times the attention stress case (QK-norm + RoPE + causal GQA
-flash attention forward and backward, B4 x S2048) instead.
+  c4, c3:       (default run) the C4 step (B8 x S512, int8 weights) and the
+                C3 attention block measured in the same run.
+--config c3 / c4 --only times one of those alone.
 """
 from __future__ import annotations
 
@@ -219,7 +225,7 @@ def copy_calibration():
                                            "copies": 3}}), flush=True)
 
 
-def bench_c3(a):
+def bench_c3(steps, warmup):
     """C3: QK-norm + RoPE + causal GQA attention forward and backward through
     llmt_attention_block_bwd (fp16 q/k/v/dO, fp32 gradients), B4 x S2048,
     16 query / 8 KV heads.  Work = 7 causal S x S x 128 products per (batch,
@@ -233,59 +239,89 @@ def bench_c3(a):
     q, k, v, do = rnd(nq), rnd(nkv), rnd(nkv), rnd(nq)
     one = torch.ones(128, device="cuda")
     run = lambda: llmt.attention_block_bwd(q, k, v, one, one, do)
-    for _ in range(a.warmup):
+    for _ in range(warmup):
         run()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(a.steps):
+    for _ in range(steps):
         run()
     torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / a.steps
+    dt = (time.perf_counter() - t0) / steps
     flops = 7 * B * nq * (S * (S + 1) / 2) * 128 * 2
     tf = flops / dt / 1e12
-    out = {
+    return {
         "metric": "attention fwd+bwd (QK-norm, RoPE, causal GQA) tokens/s",
-        "value": round(B * S / dt, 2), "unit": "tokens/s", "n_gpus": 1, "steps": a.steps,
-        "warmup": a.warmup, "ms_per_step": round(dt * 1e3, 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic N(0,1)",
-        "config": {"workload": "C3: causal GQA attention block fwd+bwd, 16 Q / 8 KV heads, "
-                               "head_dim 128, QK-norm, RoPE 1e6", "global_batch": B,
-                   "seq_len": S},
+        "value": round(B * S / dt, 2), "unit": "tokens/s", "steps": steps, "warmup": warmup,
+        "ms_per_step": round(dt * 1e3, 4),
+        "workload": "C3: causal GQA attention block fwd+bwd, B4 x S2048, 16 Q / 8 KV heads, "
+                    "head_dim 128, QK-norm, RoPE 1e6",
         "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_F16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
                      "traffic": None,
-                     "kernel": "attention block (norm/RoPE + flash fwd + flash bwd: dQ and dK/dV blocks)"},
+                     "kernel": "attention block (norm/RoPE + flash fwd + flash bwd)"},
     }
-    print(json.dumps(out), flush=True)
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=30)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", choices=["c2", "c3", "c4"], default="c2")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-graph", action="store_true")
-    ap.add_argument("--copy-cal", action="store_true", help="PMC byte-counter calibration")
-    a = ap.parse_args()
-    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print(f"bench.py: this build runs on one GPU only (asked for {a.gpus}); the multi-GPU "
-              "sharding is a design note, not a code path.", file=sys.stderr)
-        sys.exit(2)
-    if a.copy_cal:
-        copy_calibration()
-        return
-    if a.config == "c3":
-        bench_c3(a)
-        return
+def kernel_summary(kinds):
+    """Per-category milliseconds per step from llmt_profile_kernels' per-kind
+    replays (kernels only: no events between kernels, no launch gaps)."""
+    import llmt
+    cats = {c: 0.0 for c in llmt.PROFILE_CATEGORIES}
+    for k in kinds:
+        cats[k["category"]] += k["us"] * k["launches"] / 1e3
+    return {c: round(v, 4) for c, v in cats.items()}
 
+
+def gemm_family(kinds):
+    """The frozen-weight GEMMs of the step as one family: launches, average
+    launch duration, algorithmic weight bytes and FLOPs per launch."""
+    g = [k for k in kinds if k["category"] in ("gemm_fwd", "gemm_bwd", "gemm_lm_head")]
+    n = sum(k["launches"] for k in g)
+    t_us = sum(k["us"] * k["launches"] for k in g)
+    by = sum(k["bytes"] * k["launches"] for k in g)
+    fl = sum(k["flops"] * k["launches"] for k in g)
+    return n, t_us / n, by / n, fl / n
+
+
+def bandwidth_kernels(kinds, dims, T):
+    """The bandwidth-bound kernels of the step (north star: >= 70% of HBM):
+    each kernel's compulsory bytes per launch in the dtypes it reads and
+    writes, divided by its average replayed launch duration.
+      adamw          p, g, m, v read and p, m, v written, fp32, per parameter
+                     (7 x 4 B; the fp16 operand shadows it also writes are
+                     not counted);
+      swiglu_bwd     dY [T, I] fp32 (summed GEMM output), gate and up
+                     [T, 2I] fp32 read, dgate | dup [T, 2I] fp16 written;
+      norm_bwd       dY, x, residual-gradient in [T, H] fp32 read, residual
+                     gradient out fp32 and the fp16 GEMM operand written;
+      cross_entropy  logits [T, V] fp32 read once, the fp16 dlogits operand
+                     [T, V] written."""
+    H, I, V = dims.hidden, dims.intermediate, dims.vocab
+    nparam = dims.n_layers * 16 * (3 * H + 2 * dims.n_heads * dims.head_dim +
+                                   2 * dims.n_kv_heads * dims.head_dim + H)
+    want = {"adamw": 7 * 4 * nparam,
+            "swiglu_bwd": T * I * 4 + T * 2 * I * 4 + T * 2 * I * 2,
+            "norm_bwd": T * H * (4 + 4 + 4 + 4 + 2),
+            "cross_entropy": T * V * (4 + 2)}
+    out = {}
+    for k in kinds:
+        if k["name"] in want:
+            b = want[k["name"]]
+            gbs = b / (k["us"] * 1e-6) / 1e9
+            out[k["name"]] = {"us": round(k["us"], 2), "bytes": b, "gbs": round(gbs, 1),
+                              "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return out
+
+
+def bench_step(cfg, steps, warmup, graph=True):
+    """The LoRA training step of config c2 or c4 through llmt_step (one HIP
+    graph launch a step), then llmt_profile_kernels for the per-kernel
+    breakdown and the GEMM roofline."""
     import torch
     import llmt
-
     dev = torch.device("cuda:0")
     dims = llmt.qwen3_dims()
-    if a.config == "c2":
+    if cfg == "c2":
         batch, seq_len, int8, seed = 1, 128, False, 1002
         workload = ("C2: Qwen3-1.7B LoRA training step (28 layers, fp16 frozen weights, rank-16 "
                     "Q/K/V/O adapters, fwd + fused CE + bwd + AdamW), batch 1 x seq 128")
@@ -302,47 +338,36 @@ def main():
                         dtype=torch.int32)
     tok, tgt = win[:, :-1].contiguous(), win[:, 1:].contiguous()
     hp = llmt.hparams()
-
-    ctx.set_graph(not a.no_graph)
+    ctx.set_graph(graph)
     step = 1
-    for _ in range(a.warmup):
+    for _ in range(warmup):
         ctx.step(tok, tgt, hp, step)
         step += 1
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     losses = []
-    for _ in range(a.steps):
+    for _ in range(steps):
         losses.append(ctx.step(tok, tgt, hp, step))
         step += 1
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    ms = dt / a.steps * 1e3
-    value = T * a.steps / dt
-
-    # per-category kernel time of one step (HIP events between kernels)
-    cats, _, _ = ctx.profile_step(tok, tgt, hp, step)
-    step += 1
-    # the dominant kernel: the step's frozen-weight GEMM launches replayed back
-    # to back in one graph, timed with HIP events on the context's stream
-    avg_us, n_gemm, wbytes, flops = ctx.profile_gemms(tok, tgt, hp, step, reps=5)
-    bytes_per_launch = wbytes / n_gemm
+    print(f"bench: {cfg} timed {steps} steps, {dt / steps * 1e3:.3f} ms/step", file=sys.stderr,
+          flush=True)
+    kinds = ctx.profile_kernels(tok, tgt, hp, step, reps=5 if cfg == "c2" else 2)
+    ctx.close()
+    n_gemm, avg_us, bytes_per_launch, flops_per_launch = gemm_family(kinds)
     achieved = bytes_per_launch / (avg_us * 1e-6) / 1e9
-    tflops = flops / n_gemm / (avg_us * 1e-6) / 1e12
-    if a.config == "c2":  # intensity ~T = 128 flop/byte < ridge ~312: HBM-bound
+    tflops = flops_per_launch / (avg_us * 1e-6) / 1e12
+    if cfg == "c2":  # intensity ~T = 128 flop/byte < ridge ~312: HBM-bound
         bound, ach, peak, unit = "hbm", round(achieved, 1), HBM_PEAK_GBS, "GB/s"
-    else:                 # T = 4096: MFMA-bound
+    else:            # T = 4096: MFMA-bound
         bound, ach, peak, unit = "mfma", round(tflops, 2), MFMA_F16_PEAK_TFLOPS, "TFLOP/s"
     roofline = {
         "bound": bound,
-        "kernel": "frozen-weight GEMMs of the step (gemm_skinny_kernel; gemm_nt_kernel "
-                  "for the logits)" if a.config == "c2" else
-                  "frozen-weight GEMMs of the step (gemm_dma_kernel; gemm_skinny_kernel for "
-                  "the LoRA columns)",
-        "achieved": ach,
-        "peak": peak,
-        "unit": unit,
-        "frac": round(ach / peak, 4),
-        "traffic": measured_traffic() if a.config == "c2" else None,
+        "kernel": "frozen-weight GEMMs of the step (" + ", ".join(sorted(
+            {k["name"].split()[0] for k in kinds if k["category"].startswith("gemm")})) + ")",
+        "achieved": ach, "peak": peak, "unit": unit, "frac": round(ach / peak, 4),
+        "traffic": measured_traffic() if cfg == "c2" else None,
         "algorithmic_bytes_per_launch": round(bytes_per_launch),
         "launches_per_step": n_gemm,
         "avg_launch_us": round(avg_us, 3),
@@ -350,30 +375,81 @@ def main():
         "gemm_tflops": round(tflops, 2),
         "mfma_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
     }
+    ms = dt / steps * 1e3
+    return {
+        "value": round(T * steps / dt, 2), "ms_per_step": round(ms, 4), "steps": steps,
+        "warmup": warmup, "T": T, "batch": batch, "seq_len": seq_len, "workload": workload,
+        "roofline": roofline, "kernels": kernel_summary(kinds),
+        "kernels_sum_ms": round(sum(k["us"] * k["launches"] for k in kinds) / 1e3, 4),
+        "launches_per_step": sum(k["launches"] for k in kinds),
+        "bandwidth_kernels": bandwidth_kernels(kinds, dims, T),
+        "loss_first_last": [round(losses[0], 5), round(losses[-1], 5)],
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", choices=["c2", "c3", "c4"], default="c2")
+    ap.add_argument("--only", action="store_true",
+                    help="the selected config alone (no c3 / c4 sub-objects in the c2 line)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--copy-cal", action="store_true", help="PMC byte-counter calibration")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for {a.gpus}); the multi-GPU "
+              "sharding is a design note, not a code path.", file=sys.stderr)
+        sys.exit(2)
+    if a.copy_cal:
+        copy_calibration()
+        return
+    if a.config == "c3":
+        print(json.dumps(bench_c3(a.steps, a.warmup)), flush=True)
+        return
+
+    r = bench_step(a.config, a.steps, a.warmup, graph=not a.no_graph)
     out = {
         "metric": METRIC,
-        "value": round(value, 2),
+        "value": r["value"],
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
-        "ms_per_step": round(ms, 4),
+        "ms_per_step": r["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16",
         "data": "synthetic (random N(0,0.02) frozen weights, uniform token ids)",
-        "config": {"workload": workload, "global_batch": batch, "seq_len": seq_len,
-                   "tokens_per_step": T, "graph": not a.no_graph},
-        "roofline": roofline,
-        "kernels": {k: round(v, 4) for k, v in cats.items()},
-        "loss_first_last": [round(losses[0], 5), round(losses[-1], 5)],
+        "config": {"workload": r["workload"], "global_batch": r["batch"], "seq_len": r["seq_len"],
+                   "tokens_per_step": r["T"], "graph": not a.no_graph},
+        "roofline": r["roofline"],
+        "kernels": r["kernels"],
+        "kernels_sum_ms": r["kernels_sum_ms"],
+        "launches_per_step": r["launches_per_step"],
+        "bandwidth_kernels": r["bandwidth_kernels"],
+        "loss_first_last": r["loss_first_last"],
     }
-    ctx.close()
+    if a.config == "c2" and not a.only:
+        # the other headline configurations, measured in the same run
+        c4 = bench_step("c4", min(a.steps, 10), 2, graph=not a.no_graph)
+        out["c4"] = {k: c4[k] for k in ("workload", "value", "ms_per_step", "steps", "warmup",
+                                        "roofline", "kernels", "kernels_sum_ms",
+                                        "launches_per_step", "bandwidth_kernels",
+                                        "loss_first_last")}
+        out["c4"]["unit"] = "tokens/s"
+        out["c3"] = bench_c3(min(a.steps, 20), 3)
     out["achievable"] = achievable_peaks()
     if not a.no_cpu:
-        out["cpu_baseline"] = (cpu_baseline(batch, seq_len) if a.config == "c2"
-                               else cpu_baseline_sampled(batch, seq_len))
+        if a.config == "c2":
+            out["cpu_baseline"] = cpu_baseline(r["batch"], r["seq_len"])
+            if "c4" in out:
+                out["c4"]["cpu_baseline"] = cpu_baseline_sampled(8, 512)
+        else:
+            out["cpu_baseline"] = cpu_baseline_sampled(r["batch"], r["seq_len"])
     print(json.dumps(out), flush=True)
 
 

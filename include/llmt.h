@@ -75,12 +75,11 @@ typedef struct {
     LoraGrad wo[LLMT_NUM_LAYERS];
 } LoraGrads;
 
-/* include/lora.h:44-62.  The layout is the reference's; the contents are
- * library-private.  layer_in / post_attn hold the fp32 residual stream at the
- * layer input / after the attention residual and hq..ho hold h = x A^T in
- * fp32 (the reference meanings); the other slots point at the library's
- * fp16 stashes and attn_w holds the softmax log-sum-exp [B, heads, S]
- * instead of P (flash-style recompute). */
+/* include/lora.h:44-62.  The layout is the reference's; the stashes
+ * themselves are library-private (they live in the context, with the
+ * softmax log-sum-exp in place of P), so lora_acts_alloc sets every slot to
+ * NULL and the compat forward/backward never read or write them (the
+ * reference's train.cu never reads acts either). */
 typedef struct {
     float* layer_in[LLMT_NUM_LAYERS];
     float* attn_norm_out[LLMT_NUM_LAYERS];
@@ -221,8 +220,15 @@ int llmt_set_layer_i8(llmt_ctx* ctx, int layer, const int8_t* const q[7], const 
                       const float* k_norm);
 /* Tied embedding / lm_head [V, H] fp16 and the final norm [H] fp32. */
 int llmt_set_embed_f16(llmt_ctx* ctx, const void* embed_lm_head, const float* final_norm);
+/* An untied lm_head [V, H] fp16 (the reference loads lm_head.weight.bin on its
+ * own, src/train.cu:87-88): the logits and the head's dX use it, the token
+ * gather keeps the embedding.  Allocates the head's packed copies on the
+ * first call. */
+int llmt_set_lm_head_f16(llmt_ctx* ctx, const void* lm_head);
 /* Reference on-disk layout (src/train.cu:56-89, python/export_weights.py:19-26):
- * <dir>/<hf_param_name>.bin raw fp32 little-endian [out, in], no header. */
+ * <dir>/<hf_param_name>.bin raw fp32 little-endian [out, in], no header.
+ * lm_head.weight.bin is optional: absent or equal to the embedding means a
+ * tied head, otherwise it is loaded as an untied head. */
 int llmt_load_weights_dir(llmt_ctx* ctx, const char* dir);
 
 /* Adapters live in one fp32 arena per kind (param, grad, m, v), ordered layer
@@ -259,6 +265,12 @@ int llmt_forward_backward(llmt_ctx* ctx, const int* tokens, const int* targets, 
 int llmt_set_graph(llmt_ctx* ctx, int enable);
 /* fp32 logits [batch*seq_len, V] of the last forward (NULL if not kept). */
 const float* llmt_logits(const llmt_ctx* ctx);
+/* fp32 residual stream [batch*seq_len, H] at the input of `layer` (0..L-1)
+ * from the last forward, the reference's LoraActs.layer_in[layer]
+ * (include/lora.h:45, src/kernels/lora_forward.cu:205): layer 0's rows are
+ * the gathered embedding rows E[token] (src/kernels/embed.cu:6-20).  NULL for
+ * a layer outside the model. */
+const float* llmt_layer_in(const llmt_ctx* ctx, int layer);
 
 /* Single-layer forward/backward through layer `layer` (config C0): x, y, dy,
  * dx are fp32 [batch*seq_len, H]. The backward writes the layer's adapter
@@ -267,33 +279,26 @@ int llmt_layer_forward(llmt_ctx* ctx, int layer, const float* x, float* y, int b
 int llmt_layer_backward(llmt_ctx* ctx, int layer, const float* dy, float* dx, int batch);
 /* AdamW over the whole arena (one multi-tensor launch). */
 int llmt_adamw(llmt_ctx* ctx, const llmt_hparams* hp, int step);
-/* One llmt_step with a HIP event recorded between consecutive kernels (the
- * step is captured into a graph with event-record nodes and replayed; if
- * capture fails it runs eagerly, *profile_graph (may be NULL) says which):
- * cat_ms[c] receives the milliseconds spent in each kernel category
+/* Per-kernel timing of one llmt_step (no counterpart in the reference).  The
+ * step (forward, CE, backward, AdamW: the adapters advance by this one step)
+ * runs once eagerly with every kernel launch recorded; then the launches of
+ * each kind (one kernel at one shape) are replayed back to back, `reps`
+ * times, as a HIP graph of their own and timed with HIP events on the
+ * context's stream, so no events sit between kernels and no dependent-launch
+ * gaps are counted (the kinds' totals sum to less than a step).  The
+ * parameter and moment arenas are saved before the replays and restored
+ * after; the GRAD arena and the stashes are left unspecified.  Per kind
+ * k < *nkinds (<= max_kinds), in first-launch order: names[k] (owned by the
+ * context, valid until its next llmt_profile_kernels or destroy), cats[k]
  * (0 forward GEMMs, 1 backward GEMMs, 2 lm_head GEMMs, 3 attention, 4 row
- * epilogues, 5 cross-entropy, 6 LoRA grads, 7 AdamW, 8 split-K reductions);
- * gemm_flops and
- * gemm_weight_bytes (may be NULL) the step's GEMM FLOPs and weight bytes. */
-int llmt_profile_step(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
-                      const llmt_hparams* hp, int step, float* cat_ms, int ncat,
-                      double* gemm_flops, double* gemm_weight_bytes, int* profile_graph);
-/* The frozen-weight GEMM launches of one llmt_step (same shapes, operands and
- * workspaces, the other kernels left out) replayed `reps` times as one HIP
- * graph timed with HIP events on the context's stream: *avg_us = average
- * duration of one GEMM launch; *launches, *weight_bytes, *flops describe one
- * step's GEMMs (any may be NULL).  Leaves the adapters stepped once. */
-int llmt_profile_gemms(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
-                       const llmt_hparams* hp, int step, int reps, float* avg_us,
-                       int* launches, double* weight_bytes, double* flops);
-
-/* The step's GEMM launches grouped by shape (N, K, split, int8), each group
- * replayed `reps` times as its own HIP graph.  Per group s < *nshapes
- * (<= max_shapes): shape_info[5s..5s+4] = N, K, split, launches per step,
- * int8; shape_us[s] = average launch duration in microseconds. */
-int llmt_profile_gemm_shapes(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
-                             const llmt_hparams* hp, int step, int reps, int max_shapes,
-                             int* nshapes, int* shape_info, float* shape_us);
+ * epilogues, 5 cross-entropy, 6 LoRA gradients, 7 AdamW), launches[k] per
+ * step, us[k] = average launch duration in microseconds, flops[k] and
+ * bytes[k] = algorithmic work of one launch for the GEMMs (2 M N K, streamed
+ * weight bytes), 0 for the other kernels. */
+int llmt_profile_kernels(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
+                         const llmt_hparams* hp, int step, int reps, int max_kinds, int* nkinds,
+                         const char** names, int* cats, int* launches, float* us, double* flops,
+                         double* bytes);
 
 /* ---- standalone operators (stream may be NULL) ---- */
 

@@ -147,7 +147,7 @@ int llmt_head_ce(llmt_ctx* ctx, const void* hidden16, const int* targets, int ba
   TRY_ARG(c->embed_ready, "embedding not set");
   TRY_ARG(batch >= 1 && batch <= c->maxB && (batch * c->S) % 16 == 0, "batch");
   const int T = batch * c->S;
-  int rc = head_ce_packed(c->st, (const _Float16*)hidden16, c->E, c->ET, targets, T, c->S, c->H,
+  int rc = head_ce_packed(c->st, (const _Float16*)hidden16, c->Eh, c->EhT, targets, T, c->S, c->H,
                           c->V, c->logits, c->grad16, c->ce_stats, c->loss_rows, c->loss_dev,
                           dlogits, dhidden, c->part, c->part_elems);
   if (rc) return rc;

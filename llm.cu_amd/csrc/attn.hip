@@ -708,9 +708,7 @@ void launch_bwd(const AttnArgs& a, int B, int nkvb, int nqb, hipStream_t st) {
 void launch_attn_bwd(const AttnArgs& a, int B, int nwk, int nwq, int rw, hipStream_t st) {
   const int nkvb = (a.S + nwk * 16 - 1) / (nwk * 16);
   const int nqb = (a.S + nwq * rw * 16 - 1) / (nwq * rw * 16);
-  const char* ce = getenv("LLMT_ATTN_COMBINE_MAX");
-  const long long cmax = ce && *ce ? atoll(ce) : 2048;
-  const bool small = (long long)nkvb * a.nq * B < cmax;
+  const bool small = (long long)nkvb * a.nq * B < 2048;
   if (nwk == nwq && small) {
     switch (nwq * 10 + rw) {
       case 42: launch_bwd<4, 2, 0>(a, B, nkvb, nqb, st); break;

@@ -226,8 +226,24 @@ void ensure_weights(const MW* m) {
                                 w.q_norm, w.k_norm),
              "set layer");
   }
-  const void* e = f16(m->embed_table ? m->embed_table : m->lm_head, m->_pad[0], big, 0);
+  // The token gather reads embed_table (src/kernels/embed.cu:6-20) and the
+  // logits read lm_head (src/kernels/lora_forward.cu:304), each loaded from
+  // its own file by the reference (src/train.cu:56-88).  The fp16 lm_head pad
+  // (src/main.cu:63) stands for lm_head, and for the embedding when
+  // embed_table is NULL (tied).  Distinct sources make an untied head.
+  const void* emb_src = m->embed_table ? (const void*)m->embed_table
+                                       : (m->_pad[0] ? m->_pad[0] : (const void*)m->lm_head);
+  const void* head_src = m->_pad[0] ? m->_pad[0] : (m->lm_head ? (const void*)m->lm_head : emb_src);
+  const void* e = m->embed_table ? f16(m->embed_table, nullptr, big, 0)
+                                 : f16(m->lm_head, m->_pad[0], big, 0);
   check_rc(llmt_set_embed_f16(g.ctx, e, m->final_norm), "set embedding");
+  if (head_src != emb_src) {
+    const void* h = f16(m->lm_head, m->_pad[0], big, 0);
+    check_rc(llmt_set_lm_head_f16(g.ctx, h), "set lm_head");
+  } else {  // tied (again): the head reads the embedding's packed copies
+    c->Eh = c->E;
+    c->EhT = c->ET;
+  }
   g.model = m;
   g.model_key = key;
 }

@@ -137,6 +137,8 @@ int Ctx::init() {
   }
   TRY_PTR(E = alloc_n<_Float16>((size_t)V * H));
   TRY_PTR(ET = alloc_n<_Float16>((size_t)V * H));
+  Eh = E;
+  EhT = ET;
   TRY_PTR(final_norm = alloc_n<float>(H));
 
   // per-layer stashes
@@ -335,6 +337,28 @@ int llmt_set_embed_f16(llmt_ctx* ctx, const void* embed_lm_head, const float* fi
   return LLMT_OK;
 }
 
+int llmt_set_lm_head_f16(llmt_ctx* ctx, const void* lm_head) {
+  set_error("");
+  Ctx* c = C_(ctx);
+  TRY_ARG(c && lm_head, "llmt_set_lm_head_f16: NULL argument");
+  if (c->Eh == c->E) {
+    _Float16* eh = c->alloc_n<_Float16>((size_t)c->V * c->H);
+    _Float16* eht = eh ? c->alloc_n<_Float16>((size_t)c->V * c->H) : nullptr;
+    if (!eh || !eht) return LLMT_ERR_HIP;
+    c->Eh = eh;
+    c->EhT = eht;
+  }
+  const _Float16* w = (const _Float16*)lm_head;
+  TRY_HIP(pack_f16(w, c->H, 0, c->V, c->H, c->Eh, c->H, 0, 0, c->st));
+  TRY_HIP(pack_f16(w, c->H, 1, c->H, c->V, c->EhT, c->V, 0, 0, c->st));
+  TRY_HIP(hipStreamSynchronize(c->st));
+  if (c->graph_exec) {  // a captured step would keep the old operands
+    (void)hipGraphExecDestroy(c->graph_exec);
+    c->graph_exec = nullptr;
+  }
+  return LLMT_OK;
+}
+
 // ---------------------------------------------------------------- file formats
 
 // Raw little-endian fp32, no header (python/export_weights.py:19-26); the
@@ -459,8 +483,6 @@ int llmt_load_weights_dir(llmt_ctx* ctx, const char* dir) {
     }
     if (rc) return fail(rc);
   }
-  // Tied embedding / lm_head: the reference's scripts write lm_head.weight.bin
-  // as a copy of the embedding (scripts/run.sh:19); the embedding file is used.
   std::vector<float> fn;
   snprintf(path, sizeof(path), "%s/model.norm.weight.bin", dir);
   if ((rc = read_f32(path, H, fn))) return fail(rc);
@@ -468,7 +490,24 @@ int llmt_load_weights_dir(llmt_ctx* ctx, const char* dir) {
   if (f32_to_f16(f32, f16, (size_t)V * H, c->st) != hipSuccess || hipStreamSynchronize(c->st) != hipSuccess ||
       hipMemcpy(f32, fn.data(), H * 4, hipMemcpyHostToDevice) != hipSuccess)
     return fail(LLMT_ERR_HIP);
-  rc = llmt_set_embed_f16(ctx, f16, f32);
+  if ((rc = llmt_set_embed_f16(ctx, f16, f32))) return fail(rc);
+  // The reference loads lm_head.weight.bin on its own (src/train.cu:87-88);
+  // its scripts write it as a copy of the embedding (scripts/run.sh:19).  A
+  // head file equal to the embedding keeps the tied buffers; a different one
+  // becomes an untied head; no file means tied.
+  snprintf(path, sizeof(path), "%s/lm_head.weight.bin", dir);
+  if (FILE* hf = fopen(path, "rb")) {
+    fclose(hf);
+    std::vector<float> head;
+    if ((rc = read_f32(path, (size_t)V * H, head))) return fail(rc);
+    if (memcmp(head.data(), host.data(), head.size() * sizeof(float)) != 0) {
+      if (hipMemcpy(f32, head.data(), head.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+          f32_to_f16(f32, f16, (size_t)V * H, c->st) != hipSuccess ||
+          hipStreamSynchronize(c->st) != hipSuccess)
+        return fail(LLMT_ERR_HIP);
+      rc = llmt_set_lm_head_f16(ctx, f16);
+    }
+  }
   return fail(rc);
 }
 

@@ -1,6 +1,8 @@
 // ctx.h — the training-step context behind the llmt_ctx handle.
 #pragma once
 
+#include <functional>
+#include <string>
 #include <vector>
 
 #include "../../include/llmt.h"
@@ -11,7 +13,7 @@ namespace llmt {
 constexpr int kHeadDim = 128;
 constexpr int kRank = 16;
 
-// Categories of the per-kernel profile (llmt_profile_step).
+// Categories of the per-kernel profile (llmt_profile_kernels).
 enum {
   CAT_GEMM_FWD = 0,
   CAT_GEMM_BWD = 1,
@@ -20,10 +22,17 @@ enum {
   CAT_ROWS = 4,
   CAT_CE = 5,
   CAT_LORA = 6,
-  CAT_ADAM = 7,
-  CAT_REDUCE = 8,
-  CAT_END = 9,
-  CAT_COUNT = 9
+  CAT_ADAM = 7
+};
+
+// One recorded kernel launch: its kind (kernel name, plus the shape for
+// GEMMs), category, a closure that launches it again on a given stream, and
+// its algorithmic work (GEMMs: 2 M N K flops and the streamed weight bytes).
+struct Launch {
+  int cat;
+  std::string kind;
+  std::function<hipError_t(hipStream_t)> fn;
+  double flops, bytes;
 };
 
 // One frozen weight matrix as a GEMM B operand: fragment-packed fp16 or int8
@@ -84,6 +93,10 @@ struct Ctx {
   std::vector<Layer> layers;
   _Float16* E = nullptr;   // [V, H] tied embedding / lm_head (packed, K = H)
   _Float16* ET = nullptr;  // [H, V] (packed, K = V)
+  // The lm_head GEMM operands: E / ET while the head is tied to the
+  // embedding; their own buffers after llmt_set_lm_head_f16.
+  _Float16* Eh = nullptr;
+  _Float16* EhT = nullptr;
   float* final_norm = nullptr;
   bool embed_ready = false;
 
@@ -145,13 +158,12 @@ struct Ctx {
   const int* graph_tok = nullptr;  // input pointers the graph copies from (NULL: none)
   const int* graph_tgt = nullptr;
   bool inputs_move = false;  // input pointers changed between steps: copies stay outside the graph
-  bool profiling = false;
-  std::vector<hipEvent_t> prof_ev;
-  std::vector<int> prof_cat;
-  int prof_n = 0;
-  double gemm_flops = 0, gemm_wbytes = 0;
-  bool record_gemms = false;       // keep the GemmArgs of every GEMM launched
-  std::vector<GemmArgs> recorded;
+  // Profiling: with `recording` set, every kernel launch of the step is also
+  // kept as a closure (kind, category, work) so that it can be replayed on
+  // its own (llmt_profile_kernels).
+  bool recording = false;
+  std::vector<Launch> launches;
+  std::vector<std::string> prof_names;  // kind names handed out by the last profile call
 
   ~Ctx();
   int init();
@@ -167,7 +179,12 @@ struct Ctx {
     return true;
   }
 
-  hipError_t mark(int cat);
+  // Launch one kernel (f(stream)), recording it when profiling.
+  template <class F>
+  hipError_t run(int cat, const char* kind, F&& f) {
+    if (recording) launches.push_back({cat, kind, std::function<hipError_t(hipStream_t)>(f), 0, 0});
+    return f(st);
+  }
   // C = A B^T over the segments.  direct: split 1 into `direct` (ld ldc).
   // Otherwise the fp32 split-K partials land in `part` and *out describes
   // them; the consuming row epilogue sums them in split order.  glu16 (with

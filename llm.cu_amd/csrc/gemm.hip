@@ -251,317 +251,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
   }
 }
 
-// Large-M kernel (the T = 4096 configurations, where the GEMMs are
-// MFMA-bound): a 256 x BN output tile per workgroup of WN x 2 waves (each
-// 128 x 64: 32 accumulator fragments), both operands staged through LDS in
-// MFMA fragment order in 64-wide K chunks (double-buffered; the next chunk's
-// global loads are issued before the current chunk is multiplied).  int8 B
-// pieces are dequantised (times the per-k scale, if any) on their way into
-// LDS; per-row scales are applied in the epilogue.  Split-K over blockIdx.y
-// (partials summed by the consumer).  Wider tiles raise the flops per byte
-// fetched from L2 / MALL, which bounds this kernel before the MFMA rate does.
-constexpr int BM = 256, BCH = 2;  // BCH k-steps per chunk
-template <int WN>
-__global__ __launch_bounds__(WN * 128) void gemm_big_kernel(const GemmArgs g, int g_order) {
-  constexpr int BN = WN * 64, NT = WN * 128;
-  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * BCH * KSTEP];
-  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * BCH * KSTEP];
-  constexpr int AP = BM * BCH * KSTEP / 8 / NT;  // 16-byte A pieces per thread
-  constexpr int BP = BN * BCH * KSTEP / 8 / NT;  // B pieces per thread
-  constexpr int NFB = BN / 16;                    // column fragments per k-step
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
-  // Tile order: workgroup i runs on XCD i % 8, so tiles are renumbered to
-  // give each XCD a contiguous run of them (operand reuse in its L2).
-  const int ntn = (g.N + BN - 1) / BN, ntm = g.M / BM, nwg = ntn * ntm;
-  int t = blockIdx.x;
-  if (g_order >= 1 && nwg % 8 == 0) t = (t % 8) * (nwg / 8) + t / 8;
-  int tn = t % ntn, tm = t / ntn;
-  const int gmx = g_order >= 2 ? g_order : 1;  // groups of gmx row tiles
-  if (gmx > 1 && ntm % gmx == 0) {
-    const int grp = t / (gmx * ntn), r = t % (gmx * ntn);
-    tm = grp * gmx + r % gmx;
-    tn = r / gmx;
-  }
-  const int n0 = tn * BN, m0 = tm * BM;
-  const int ksteps = g.K / KSTEP;
-  const int c0 = (int)((long long)blockIdx.y * (ksteps / BCH) / g.split);
-  const int c1 = (int)((long long)(blockIdx.y + 1) * (ksteps / BCH) / g.split);
-
-  // B pieces of this thread: piece idx = tid + NT p -> fragment fr = idx >> 6
-  // (wave-uniform: k-step q = fr / NFB, row block ni = fr % NFB), lane idx & 63.
-  const char* bptr[BP];
-  int bi8[BP];
-  const _Float16* bks[BP];
-#pragma unroll
-  for (int p = 0; p < BP; ++p) {
-    const int fr = (tid + NT * p) >> 6, ni = fr % NFB;
-    const int nn = min(n0 + ni * 16, g.N - 16);
-    int sgi = 0;
-#pragma unroll
-    for (int i = 1; i < 4; ++i)
-      if (i < g.nseg && nn >= g.seg_start[i]) sgi = i;
-    const BSeg& sg = g.seg[sgi];
-    const long long rb16 = (nn - g.seg_start[sgi]) >> 4;
-    bi8[p] = sg.is_i8;
-    bptr[p] = (const char*)sg.ptr + ((rb16 * ksteps) * 512 + lane * 8) * (sg.is_i8 ? 1 : 2);
-    bks[p] = sg.is_i8 && sg.kscale ? sg.kscale + (lane >> 4) * 8 : nullptr;
-  }
-  u32x4 ra[AP], rbv[BP];
-  half8 rks[BP];
-  auto load = [&](int c) LLMT_INLINE {
-    const int kb = c * BCH;
-#pragma unroll
-    for (int p = 0; p < AP; ++p) {
-      const int idx = tid + NT * p, fr = idx >> 6, l = idx & 63;
-      const int q = fr / 16, mi = fr % 16;
-      const int r = mi * 16 + (l & 15);
-      const int k = (kb + q) * KSTEP + (l >> 4) * 8;
-      ra[p] = *reinterpret_cast<const u32x4*>(g.A + (long long)(m0 + r) * g.lda + k);
-    }
-#pragma unroll
-    for (int p = 0; p < BP; ++p) {
-      const int q = ((tid + NT * p) >> 6) / NFB;
-      const long long ks = kb + q;
-      if (bi8[p]) {
-        const u32x2 v = *reinterpret_cast<const u32x2*>(bptr[p] + ks * 512);
-        rbv[p] = u32x4{v[0], v[1], 0u, 0u};
-        if (bks[p]) rks[p] = *reinterpret_cast<const half8*>(bks[p] + ks * KSTEP);
-      } else {
-        rbv[p] = *reinterpret_cast<const u32x4*>(bptr[p] + ks * 1024);
-      }
-    }
-  };
-  auto store = [&](int buf) LLMT_INLINE {
-#pragma unroll
-    for (int p = 0; p < AP; ++p)
-      *reinterpret_cast<u32x4*>(&As[buf][(tid + NT * p) * 8]) = ra[p];
-#pragma unroll
-    for (int p = 0; p < BP; ++p) {
-      half8 h;
-      if (bi8[p]) {
-        const int8x8 q8 = __builtin_bit_cast(int8x8, u32x2{rbv[p][0], rbv[p][1]});
-#pragma unroll
-        for (int i = 0; i < 8; ++i) h[i] = (_Float16)(float)q8[i];
-        if (bks[p]) h = h * rks[p];
-      } else {
-        h = __builtin_bit_cast(half8, rbv[p]);
-      }
-      *reinterpret_cast<half8*>(&Bs[buf][(tid + NT * p) * 8]) = h;
-    }
-  };
-
-  floatx4 acc[8][4];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-  if (c1 > c0) {
-    load(c0);
-    store(0);
-    __syncthreads();
-  }
-  for (int c = c0; c < c1; ++c) {
-    const int buf = (c - c0) & 1;
-    if (c + 1 < c1) load(c + 1);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int q = 0; q < BCH; ++q) {
-      half8 b[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        b[j] = *reinterpret_cast<const half8*>(&Bs[buf][((q * NFB + wn * 4 + j) * 64 + lane) * 8]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const half8 a =
-            *reinterpret_cast<const half8*>(&As[buf][((q * 16 + wm * 8 + i) * 64 + lane) * 8]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16(a, b[j], acc[i][j]);
-      }
-    }
-    if (c + 1 < c1) store(buf ^ 1);
-    __syncthreads();
-  }
-
-  // epilogue: D[4 g + v][c] of fragment (i, j)
-  float* C = g.C + (long long)blockIdx.y * g.split_stride;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int col = n0 + wn * 64 + j * 16 + (lane & 15);
-    if (col >= g.N) continue;
-    int sgi = 0;
-#pragma unroll
-    for (int i = 1; i < 4; ++i)
-      if (i < g.nseg && col >= g.seg_start[i]) sgi = i;
-    const _Float16* cs = g.seg[sgi].colscale;
-    const float sc = cs ? (float)cs[col - g.seg_start[sgi]] : 1.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = m0 + wm * 128 + i * 16 + (lane >> 4) * 4 + v;
-        C[(long long)row * g.ldc + col] = acc[i][j][v] * sc;
-      }
-  }
-}
-
-// Four-wave variant of the same 256 x 256 tile: each wave owns 128 x 128
-// (64 accumulator fragments, held in the accumulation registers), which halves
-// the LDS fragment reads per MFMA, and frees enough registers for two chunks
-// of global loads in flight (prefetch distance 2), so a chunk's L2 / MALL
-// latency is covered by two chunks of MFMA work.
-template <bool I8, bool KS, int PD>
-__global__ __launch_bounds__(256) void gemm_big4_kernel(const GemmArgs g, int g_order) {
-  constexpr int BN = 256, NT = 256;
-  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * BCH * KSTEP];
-  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * BCH * KSTEP];
-  constexpr int AP = BM * BCH * KSTEP / 8 / NT;  // 8
-  constexpr int BP = BN * BCH * KSTEP / 8 / NT;  // 8
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
-  const int ntn = (g.N + BN - 1) / BN, ntm = g.M / BM, nwg = ntn * ntm;
-  int t = blockIdx.x;
-  if (g_order >= 1 && nwg % 8 == 0) t = (t % 8) * (nwg / 8) + t / 8;
-  const int tn = t % ntn, tm = t / ntn;
-  const int n0 = tn * BN, m0 = tm * BM;
-  const int ksteps = g.K / KSTEP;
-  const int c0 = (int)((long long)blockIdx.y * (ksteps / BCH) / g.split);
-  const int c1 = (int)((long long)(blockIdx.y + 1) * (ksteps / BCH) / g.split);
-
-  // Thread pieces (one segment, uniform element type): piece p of the chunk
-  // is fragment wave + 4 p, i.e. k-step p / 4 and 16-row block
-  // wave + 4 (p % 4) of the tile; lane l carries row (l & 15), k (l >> 4) * 8.
-  const _Float16* abase = g.A + (long long)(m0 + wave * 16 + (lane & 15)) * g.lda + (lane >> 4) * 8;
-  const long long astep = 64LL * g.lda;  // 4 row blocks
-  const BSeg& sg = g.seg[0];
-  constexpr int ES = I8 ? 1 : 2;
-  const char* bbase = (const char*)sg.ptr + (long long)lane * 8 * ES;
-  long long boff[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int rb = min((n0 >> 4) + wave + 4 * j, (g.N >> 4) - 1);
-    boff[j] = (long long)rb * ksteps * 512 * ES;
-  }
-  const _Float16* kscale = KS ? sg.kscale + (lane >> 4) * 8 : nullptr;
-  using BRaw = std::conditional_t<I8, u32x2, u32x4>;
-  u32x4 ra[PD][AP];
-  BRaw rbv[PD][BP];
-  half8 rks[PD][BCH];
-  auto load = [&](int c, auto R) LLMT_INLINE {
-    constexpr int r = decltype(R)::value;
-    const int kb = min(c, c1 - 1) * BCH;
-#pragma unroll
-    for (int p = 0; p < AP; ++p)
-      ra[r][p] = *reinterpret_cast<const u32x4*>(abase + (p % 4) * astep + (kb + p / 4) * KSTEP);
-#pragma unroll
-    for (int p = 0; p < BP; ++p)
-      rbv[r][p] = *reinterpret_cast<const BRaw*>(bbase + boff[p % 4] + (long long)(kb + p / 4) * 512 * ES);
-    if constexpr (KS) {
-#pragma unroll
-      for (int q = 0; q < BCH; ++q)
-        rks[r][q] = *reinterpret_cast<const half8*>(kscale + (long long)(kb + q) * KSTEP);
-    }
-  };
-  auto store = [&](int buf, auto R) LLMT_INLINE {
-    constexpr int r = decltype(R)::value;
-#pragma unroll
-    for (int p = 0; p < AP; ++p)
-      *reinterpret_cast<u32x4*>(&As[buf][(tid + NT * p) * 8]) = ra[r][p];
-#pragma unroll
-    for (int p = 0; p < BP; ++p) {
-      half8 h;
-      if constexpr (I8) {
-        const int8x8 q8 = __builtin_bit_cast(int8x8, rbv[r][p]);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) h[i] = (_Float16)(float)q8[i];
-        if constexpr (KS) h = h * rks[r][p / 4];
-      } else {
-        h = __builtin_bit_cast(half8, rbv[r][p]);
-      }
-      *reinterpret_cast<half8*>(&Bs[buf][(tid + NT * p) * 8]) = h;
-    }
-  };
-
-  floatx4 acc[8][8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-  auto compute = [&](int buf) LLMT_INLINE {
-#pragma unroll
-    for (int q = 0; q < BCH; ++q) {
-      half8 b[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        b[j] = *reinterpret_cast<const half8*>(&Bs[buf][((q * 16 + wn * 8 + j) * 64 + lane) * 8]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const half8 a =
-            *reinterpret_cast<const half8*>(&As[buf][((q * 16 + wm * 8 + i) * 64 + lane) * 8]);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = mfma16(a, b[j], acc[i][j]);
-      }
-    }
-  };
-  // Chunk x of this split lives in register set (x - c0) % PD while in
-  // flight and in LDS buffer (x - c0) % 2 while multiplied; with PD = 2 a
-  // loop trip covers two chunks so every set index is static; loads past the
-  // end are clamped re-reads that are never multiplied.
-  const int nck = c1 - c0;
-  if constexpr (PD == 1) {
-    if (nck > 0) {
-      load(c0, IC<0>{});
-      store(0, IC<0>{});
-      __syncthreads();
-    }
-    for (int c = c0; c < c1; ++c) {
-      const int buf = (c - c0) & 1;
-      load(c + 1, IC<0>{});
-      __builtin_amdgcn_sched_barrier(0);
-      compute(buf);
-      store(buf ^ 1, IC<0>{});
-      __syncthreads();
-    }
-  } else if (nck > 0) {
-    load(c0, IC<0>{});
-    load(c0 + 1, IC<1>{});
-    store(0, IC<0>{});
-    __syncthreads();
-    for (int pr = 0; pr < nck / 2; ++pr) {
-      const int c = c0 + 2 * pr;
-      load(c + 2, IC<0>{});
-      __builtin_amdgcn_sched_barrier(0);
-      compute(0);
-      store(1, IC<1>{});
-      __syncthreads();
-      load(c + 3, IC<1>{});
-      __builtin_amdgcn_sched_barrier(0);
-      compute(1);
-      store(0, IC<0>{});
-      __syncthreads();
-    }
-    if (nck & 1) compute(0);
-  }
-
-  float* C = g.C + (long long)blockIdx.y * g.split_stride;
-  const _Float16* cs = sg.colscale;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int col = n0 + wn * 128 + j * 16 + (lane & 15);
-    if (col >= g.N) continue;
-    const float sc = cs ? (float)cs[col] : 1.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = m0 + wm * 128 + i * 16 + (lane >> 4) * 4 + v;
-        C[(long long)row * g.ldc + col] = acc[i][j][v] * sc;
-      }
-  }
-}
+constexpr int BM = 256, BCH = 2;  // large-tile rows; k-steps per big_tiles() K quantum
 
 // LDS-DMA kernel for the large-M GEMMs: the operands go from global memory
 // straight into LDS (global_load_lds: lane l's 16 bytes land at offset 16 l
@@ -955,43 +645,14 @@ hipError_t launch_cfg(const GemmArgs& g, hipStream_t st) {
   return hipGetLastError();
 }
 
-// Pipeline variants (waves per workgroup, LDS chunk k-steps, B ring slots,
-// A prefetch distance); LLMT_GEMM_CFG selects one for tuning.
-struct GemmCfg {
-  int nw, chs, ring, adist;
-};
-constexpr GemmCfg kCfgs[] = {
-    {8, 2, 4, 1}, {8, 2, 4, 2}, {8, 2, 8, 2}, {8, 2, 6, 1}, {4, 2, 6, 2},
-    {4, 2, 4, 1}, {4, 2, 4, 2}, {4, 2, 8, 2}, {4, 2, 8, 1}, {4, 2, 6, 1},
-};
-constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
-constexpr int kNF = 2;
-
-int gemm_cfg() {
-  const int c = env_int("LLMT_GEMM_CFG", 5);
-  return c >= 0 && c < kNumCfgs ? c : 0;
-}
-
-template <int MF, int C>
-hipError_t launch_c(const GemmArgs& g, hipStream_t st) {
-  constexpr GemmCfg k = kCfgs[C];
-  return launch_cfg<MF, kNF, k.nw, k.chs, k.ring, k.adist>(g, st);
-}
+// The register-staged kernel's pipeline: 4 waves a workgroup, 2 k-steps an
+// LDS chunk, a 4-slot B ring, A prefetched one chunk ahead (measured the
+// fastest of the variants tried on the logits GEMM and the int8 GEMMs).
+constexpr int kNF = 2, kNW = 4;
 
 template <int MF>
 hipError_t launch_mf(const GemmArgs& g, hipStream_t st) {
-  switch (gemm_cfg()) {
-    case 1: return launch_c<MF, 1>(g, st);
-    case 2: return launch_c<MF, 2>(g, st);
-    case 3: return launch_c<MF, 3>(g, st);
-    case 4: return launch_c<MF, 4>(g, st);
-    case 5: return launch_c<MF, 5>(g, st);
-    case 6: return launch_c<MF, 6>(g, st);
-    case 7: return launch_c<MF, 7>(g, st);
-    case 8: return launch_c<MF, 8>(g, st);
-    case 9: return launch_c<MF, 9>(g, st);
-    default: return launch_c<MF, 0>(g, st);
-  }
+  return launch_cfg<MF, kNF, kNW, 2, 4, 1>(g, st);
 }
 
 // Fixed-order split-K reduction fused with the LoRA up-projections:
@@ -1231,9 +892,8 @@ void gemm_finalize_segments(GemmArgs& g) {
 }
 
 // Split-K factor: enough (column tiles x splits) workgroups for about one
-// per CU (tunable with LLMT_GEMM_TARGET_WG), without splits shorter than
-// LLMT_GEMM_MIN_STEPS k-steps of 32.  Fewer splits means fewer fp32
-// partials to reduce.
+// per CU, without splits shorter than 4 k-steps of 32.  Fewer splits means
+// fewer fp32 partials to reduce.
 // DMA skinny kernel (fp16 weights, M % 128 == 0; LLMT_GEMM_SKINNY_STAGES = 0
 // selects the register-staged kernel).  Plan: 64-column tiles (48 when that
 // fills more of the GPU) and the most splits that keep the grid within one
@@ -1249,7 +909,7 @@ struct SkinnyPlan {
 static SkinnyPlan skinny_plan(int M, int N, int K) {
   const int frags = (N + 15) / 16, mt = M / 128;
   const int forced = env_int("LLMT_GEMM_SKINNY_NB", 0);
-  const int target = env_int("LLMT_GEMM_TARGET_WG", 256);
+  constexpr int target = 256;
   SkinnyPlan best{0, 0};
   int best_w = 0;
   // Very long reductions (the logits' dX, K = V): every column tile re-reads
@@ -1273,31 +933,22 @@ static SkinnyPlan skinny_plan(int M, int N, int K) {
   return best;
 }
 static bool skinny_ok(int M, int N, int K) {
-  return M % 128 == 0 && K % 64 == 0 && skinny_stages() != 0 &&
-         (N + 15) / 16 < env_int("LLMT_GEMM_SKINNY_MAX_FRAGS", 2048);
+  return M % 128 == 0 && K % 64 == 0 && skinny_stages() != 0 && (N + 15) / 16 < 2048;
 }
-int gemm_tile_n() { return kCfgs[gemm_cfg()].nw * kNF * 16; }
 
-// The 256 x 128 tile kernel takes GEMMs with many rows (no split-K); the
-// skinny kernel everything else.
+// The 256 x 256 tile kernel takes GEMMs with many rows; the skinny kernels
+// everything else.
 static bool big_tiles(int M, int K) { return M >= 1024 && M % BM == 0 && K % (BCH * KSTEP) == 0; }
 static bool use_big_tiles(const GemmArgs& g) {
   return big_tiles(g.M, g.K) && g.N >= 16 && g.split <= (g.K / (BCH * KSTEP));
 }
-// waves across the tile width: 256-wide tiles (4) unless LLMT_GEMM_BIG_WN=2
-static int big_wn(int N) {
-  (void)N;
-  return env_int("LLMT_GEMM_BIG_WN", 4) == 2 ? 2 : 4;
-}
-
 // Large-tile split-K: the smallest of 1, 2, 4 whose workgroup count fills
 // the 256 CUs in whole waves to >= 85% (partials cost traffic, so no more).
 // A trailing LoRA segment of <= 64 columns runs as its own skinny launch
 // (gemm_nt), so it is left out of the tile count.
 static int big_split(int M, int N, int K, int max_split) {
   const int nmain = (N % 256 != 0 && N % 64 != 0) ? N - N % 64 : N;
-  const int bn = big_wn(nmain) * 64;
-  const int tiles = (nmain + bn - 1) / bn * (M / BM);
+  const int tiles = (nmain + 255) / 256 * (M / BM);
   int best = 1;
   for (int split = 1; split <= 4 && split <= max_split && split <= K / (BCH * KSTEP) / 4;
        split *= 2) {
@@ -1308,14 +959,13 @@ static int big_split(int M, int N, int K, int max_split) {
   return best;
 }
 
-// The DMA large-tile kernel (the default for big tiles) carries the SwiGLU
-// epilogue: 256-wide tiles over 8 waves, gate/up fragment pairs per wave.
+// The DMA large-tile kernel carries the SwiGLU epilogue: 256-wide tiles over
+// 8 waves, gate/up fragment pairs per wave.
 bool gemm_glu_ok(int M, int I, int K, bool i8) {
   if (big_tiles(M, K))
-    return I % 128 == 0 && env_int("LLMT_GEMM_BIG_KIND", 2) == 2 && big_wn(2 * I) == 4 &&
-           env_int("LLMT_GEMM_DMA_WAVES", 8) == 8 && big_split(M, 2 * I, K, 64) == 1;
+    return I % 128 == 0 && big_split(M, 2 * I, K, 64) == 1;
   // the skinny kernel, 32 gate + 32 up columns a workgroup, split 1
-  return !i8 && skinny_ok(M, 2 * I, K) && I % 32 == 0 && env_int("LLMT_GEMM_SKINNY_GLU", 1) != 0;
+  return !i8 && skinny_ok(M, 2 * I, K) && I % 32 == 0;
 }
 
 int gemm_pick_split(int M, int N, int K, int max_split) {
@@ -1326,10 +976,10 @@ int gemm_pick_split(int M, int N, int K, int max_split) {
   }
   // Partials grow with the workgroup count: about 3/4 of the CUs for the
   // layer GEMMs, two waves of CUs for the very long lm_head dX reduction.
-  const int target = env_int("LLMT_GEMM_TARGET_WG", K > 16384 ? 512 : 192);
-  const int min_steps = env_int("LLMT_GEMM_MIN_STEPS", 4);
+  const int target = K > 16384 ? 512 : 192;
+  constexpr int min_steps = 4;
   const int mt = (M % 128 == 0) ? M / 128 : 1;
-  const int tn = gemm_tile_n();
+  constexpr int tn = kNW * kNF * 16;
   const int ntiles = (N + tn - 1) / tn * mt;
   int split = (target + ntiles / 2) / ntiles;
   const int kmax = (K / KSTEP) / min_steps;
@@ -1380,6 +1030,22 @@ static hipError_t launch_m128(const GemmArgs& g, hipStream_t st) {
   return hipGetLastError();
 }
 
+const char* gemm_kernel_name(const GemmArgs& g) {
+  if (use_big_tiles(g)) {
+    const int last = g.nseg - 1;
+    if (g.glu) return "gemm_dma_glu";
+    if (g.nseg > 1 && g.seg[last].rows <= 64 && g.seg_start[last] % 64 == 0)
+      return "gemm_dma+lora_skinny";
+    return "gemm_dma";
+  }
+  if (g.glu) return "gemm_skinny_glu";
+  bool i8 = false;
+  for (int i = 0; i < g.nseg; ++i) i8 = i8 || g.seg[i].is_i8;
+  if ((g.M / 16) % 8 == 0 && !i8 && skinny_ok(g.M, g.N, g.K) && g.split <= g.K / 64)
+    return "gemm_skinny";
+  return "gemm_nt";
+}
+
 hipError_t gemm_nt(const GemmArgs& g, hipStream_t st) {
   if (g.M <= 0 || g.N <= 0 || g.M % 16 || g.K % KSTEP || g.K < KSTEP || g.split < 1 ||
       g.split > g.K / KSTEP || g.nseg < 1 || g.nseg > 4) {
@@ -1413,49 +1079,32 @@ hipError_t gemm_nt(const GemmArgs& g, hipStream_t st) {
       gm.nseg = last;
       gemm_finalize_segments(gm);
     }
-    const int wn = big_wn(gm.N);
-    const int nwg = (gm.N + wn * 64 - 1) / (wn * 64) * (gm.M / BM);
+    const int nwg = (gm.N + 255) / 256 * (gm.M / BM);
     // XCD-contiguous tile runs: workgroup b goes to XCD b % 8, and the tiles
     // sharing an A row block then share that XCD's L2 (C4: +0.7% step rate)
-    const int order = env_int("LLMT_GEMM_BIG_ORDER", 1);
+    const int order = 1;
     const bool i8 = gm.seg[0].is_i8, ks = gm.seg[0].kscale != nullptr;
-    const int kind = env_int("LLMT_GEMM_BIG_KIND", 2);  // 0: 8-wave, 1: 4-wave, 2: DMA
-    if (kind == 2 && wn == 4 && gm.nseg == 1 && gm.N % 16 == 0) {
-      const dim3 gr(nwg, gm.split);
-      if (env_int("LLMT_GEMM_DMA_WAVES", 8) == 4) {
-        if (!i8)
-          hipLaunchKernelGGL((gemm_dma_kernel<false, false, 4, 2>), gr, dim3(256), 0, st, gm, order);
-        else if (ks)
-          hipLaunchKernelGGL((gemm_dma_kernel<true, true, 5, 2>), gr, dim3(256), 0, st, gm, order);
-        else
-          hipLaunchKernelGGL((gemm_dma_kernel<true, false, 5, 2>), gr, dim3(256), 0, st, gm, order);
-      } else if (gm.glu) {
-        if (!i8)
-          hipLaunchKernelGGL((gemm_dma_kernel<false, false, 4, 4, true>), gr, dim3(512), 0, st, gm, order);
-        else if (ks)
-          hipLaunchKernelGGL((gemm_dma_kernel<true, true, 5, 4, true>), gr, dim3(512), 0, st, gm, order);
-        else
-          hipLaunchKernelGGL((gemm_dma_kernel<true, false, 5, 4, true>), gr, dim3(512), 0, st, gm, order);
-      } else {
-        if (!i8)
-          hipLaunchKernelGGL((gemm_dma_kernel<false, false, 4, 4>), gr, dim3(512), 0, st, gm, order);
-        else if (ks)
-          hipLaunchKernelGGL((gemm_dma_kernel<true, true, 5, 4>), gr, dim3(512), 0, st, gm, order);
-        else
-          hipLaunchKernelGGL((gemm_dma_kernel<true, false, 5, 4>), gr, dim3(512), 0, st, gm, order);
-      }
-    } else if (kind == 1 && wn == 4 && gm.nseg == 1 && gm.N % 16 == 0) {
-      const dim3 gr(nwg, gm.split);
+    if (gm.nseg != 1 || gm.N % 16 != 0) {
+      set_error("gemm_nt: large tiles take one B segment with N %% 16 == 0 (N = %d, %d segments)",
+                gm.N, gm.nseg);
+      return hipErrorInvalidValue;
+    }
+    const dim3 gr(nwg, gm.split);
+    if (gm.glu) {
       if (!i8)
-        hipLaunchKernelGGL((gemm_big4_kernel<false, false, 1>), gr, dim3(256), 0, st, gm, order);
+        hipLaunchKernelGGL((gemm_dma_kernel<false, false, 4, 4, true>), gr, dim3(512), 0, st, gm, order);
       else if (ks)
-        hipLaunchKernelGGL((gemm_big4_kernel<true, true, 1>), gr, dim3(256), 0, st, gm, order);
+        hipLaunchKernelGGL((gemm_dma_kernel<true, true, 5, 4, true>), gr, dim3(512), 0, st, gm, order);
       else
-        hipLaunchKernelGGL((gemm_big4_kernel<true, false, 1>), gr, dim3(256), 0, st, gm, order);
-    } else if (wn == 4)
-      hipLaunchKernelGGL(gemm_big_kernel<4>, dim3(nwg, gm.split), dim3(512), 0, st, gm, order);
-    else
-      hipLaunchKernelGGL(gemm_big_kernel<2>, dim3(nwg, gm.split), dim3(256), 0, st, gm, order);
+        hipLaunchKernelGGL((gemm_dma_kernel<true, false, 5, 4, true>), gr, dim3(512), 0, st, gm, order);
+    } else {
+      if (!i8)
+        hipLaunchKernelGGL((gemm_dma_kernel<false, false, 4, 4>), gr, dim3(512), 0, st, gm, order);
+      else if (ks)
+        hipLaunchKernelGGL((gemm_dma_kernel<true, true, 5, 4>), gr, dim3(512), 0, st, gm, order);
+      else
+        hipLaunchKernelGGL((gemm_dma_kernel<true, false, 5, 4>), gr, dim3(512), 0, st, gm, order);
+    }
     e = hipGetLastError();
     if (e == hipSuccess && lora_tail) {
       GemmArgs gl = g;

@@ -305,16 +305,6 @@ __global__ __launch_bounds__(NTH) void lora_init_kernel(float* __restrict__ p,
   }
 }
 
-// Spin on the constant-rate device wall clock; the loop count is capped so
-// the kernel always exits.
-__global__ void delay_kernel(unsigned long long ticks, long long max_iter) {
-  const unsigned long long t0 = wall_clock64();
-  for (long long i = 0; i < max_iter; ++i) {
-    if (wall_clock64() - t0 >= ticks) break;
-    __builtin_amdgcn_s_sleep(32);
-  }
-}
-
 inline unsigned grid_for(long long n) {
   long long g = (n + NTH - 1) / NTH;
   return (unsigned)(g > 8192 ? 8192 : (g < 1 ? 1 : g));
@@ -366,19 +356,6 @@ hipError_t adamw(float* p, const float* g, float* m, float* v, long long n, cons
   const unsigned bx = (unsigned)std::min<long long>((seg + 4 * NTH - 1) / (4 * NTH), 64);
   hipLaunchKernelGGL(adamw_shadow_kernel, dim3(bx, (unsigned)(n / sh.per_layer * 8)), dim3(NTH), 0,
                      st, p, g, m, v, hp, update, sh);
-  LLMT_LAUNCH_CHECK();
-  return hipSuccess;
-}
-
-hipError_t gpu_delay(int us, hipStream_t st) {
-  int dev = 0, khz = 0;
-  LLMT_HIP_TRY(hipGetDevice(&dev));
-  LLMT_HIP_TRY(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
-  if (khz <= 0) khz = 100000;
-  const unsigned long long ticks = (unsigned long long)us * (unsigned long long)khz / 1000ull;
-  // s_sleep 32 is ~2k cycles; bound the loop at ~4x the requested time at 2.4 GHz.
-  const long long max_iter = 4ll * us * 2400 / 2048 + 16;
-  hipLaunchKernelGGL(delay_kernel, dim3(1), dim3(1), 0, st, ticks, max_iter);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }

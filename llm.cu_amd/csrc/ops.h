@@ -49,6 +49,8 @@ void gemm_finalize_segments(GemmArgs& g);
 // Split factor for a GEMM of this shape on this device (>=1, bounded by K).
 int gemm_pick_split(int M, int N, int K, int max_split);
 hipError_t gemm_nt(const GemmArgs& g, hipStream_t st);
+// Name of the kernel gemm_nt launches for g ("gemm_skinny", "gemm_dma", ...).
+const char* gemm_kernel_name(const GemmArgs& g);
 // out[m][n] = sum_s part[s][m][n] in split order, plus for output columns
 // [c0, c0 + n) of each LoRA adapter lscale * sum_r part-sum[m][hcol + r] *
 // M(r, n') (M = B [n, 16] if is_B, else A [16, n]).  out != part; M % 16 == 0.
@@ -243,10 +245,6 @@ hipError_t attn_bwd(const AttnArgs& a, int B, hipStream_t st);
 hipError_t attn_delta(const float* dO, long long ldd, const _Float16* o, long long ldo, int nq,
                       int S, int T, float* delta, _Float16* dO16, long long ld16, float* dsc,
                       hipStream_t st);
-
-// A one-thread kernel that returns after about `us` microseconds of device
-// wall clock (never more than a few times that: the wait loop is bounded).
-hipError_t gpu_delay(int us, hipStream_t st);
 
 // ---------------------------------------------------------------- LoRA / AdamW
 struct LoraGradJob {

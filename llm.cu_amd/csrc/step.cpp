@@ -40,7 +40,6 @@ void* Ctx::alloc(size_t bytes) {
 
 Ctx::~Ctx() {
   if (graph_exec) hipGraphExecDestroy(graph_exec);
-  for (auto& e : prof_ev) hipEventDestroy(e);
   for (void* p : blocks) hipFree(p);
   if (host_loss) hipHostFree(host_loss);
   if (host_hp) hipHostFree(host_hp);
@@ -48,20 +47,6 @@ Ctx::~Ctx() {
 }
 
 // ------------------------------------------------------------------ launches
-
-hipError_t Ctx::mark(int cat) {
-  if (!profiling) return hipSuccess;
-  if (prof_n >= (int)prof_ev.size()) {
-    hipEvent_t e;
-    LLMT_HIP_TRY(hipEventCreate(&e));
-    prof_ev.push_back(e);
-  }
-  prof_cat.resize(prof_n + 1);
-  prof_cat[prof_n] = cat;
-  LLMT_HIP_TRY(hipEventRecord(prof_ev[prof_n], st));
-  ++prof_n;
-  return hipSuccess;
-}
 
 hipError_t Ctx::gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int nseg, int M, int K,
                      float* direct, int ldc, GemmOut* out, _Float16* glu16) {
@@ -93,13 +78,16 @@ hipError_t Ctx::gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int 
       return hipErrorInvalidValue;
     }
   }
-  LLMT_HIP_TRY(mark(cat));
+  if (recording) {
+    double wbytes = 0;
+    for (int i = 0; i < nseg; ++i) wbytes += (double)segs[i].rows * K * (segs[i].is_i8 ? 1 : 2);
+    char kind[128];
+    snprintf(kind, sizeof kind, "%s M%d N%d K%d split%d%s", gemm_kernel_name(g), M, g.N, K,
+             g.split, segs[0].is_i8 ? " int8" : "");
+    launches.push_back({cat, kind, [g](hipStream_t s) { return gemm_nt(g, s); },
+                        2.0 * M * g.N * K, wbytes});
+  }
   LLMT_HIP_TRY(gemm_nt(g, st));
-  if (record_gemms) recorded.push_back(g);
-  gemm_flops += 2.0 * M * g.N * K;
-  double wbytes = 0;
-  for (int i = 0; i < nseg; ++i) wbytes += (double)segs[i].rows * K * (segs[i].is_i8 ? 1 : 2);
-  gemm_wbytes += wbytes;
   if (!out) return hipSuccess;
   out->part = g.C;
   out->split = g.split;
@@ -200,56 +188,82 @@ hipError_t Ctx::layer_fwd(int l, int B, const float* next_w, float* x_out, _Floa
   qa.cosT = cosT; qa.sinT = sinT;
   qa.S = S; qa.nq = nq; qa.nkv = nkv; qa.eps = eps;
   qa.qkraw = s.qkraw; qa.qkv16 = s.qkv16; qa.hbuf = s.h;
-  LLMT_HIP_TRY(mark(CAT_ROWS));
-  LLMT_HIP_TRY(qkv_post(qa, T, st));
-  AttnArgs aa = attn_args(s);
-  LLMT_HIP_TRY(mark(CAT_ATTN));
-  LLMT_HIP_TRY(attn_fwd(aa, B, st));
+  LLMT_HIP_TRY(run(CAT_ROWS, "qkv_post", [=](hipStream_t q) { return qkv_post(qa, T, q); }));
+  const AttnArgs aa = attn_args(s);
+  LLMT_HIP_TRY(run(CAT_ATTN, "attn_fwd", [=](hipStream_t q) { return attn_fwd(aa, B, q); }));
   // O (+ LoRA A) projection, residual, FFN norm
   BSeg so[2] = {wseg(w.wo), hseg(shadow_ptr(l, sh_a_o), kRank, Q)};
   const LoraTerm to[1] = {{shadow_rm + (size_t)l * shadow_per_layer + sh_bt_o, 0, H, 0, H, 0}};
   LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.o16, Q, so, 2, T, Q, nullptr, 0, &go));
-  LLMT_HIP_TRY(mark(CAT_ROWS));
-  LLMT_HIP_TRY(o_post(row_in(go, H, kRank, 1, to), s.x_in, w.ffn_norm, eps, H, T, s.h, s.x_mid,
-                      s.xn2, st));
+  {
+    const RowIn ri = row_in(go, H, kRank, 1, to);
+    const float *x_in = s.x_in, *fw = w.ffn_norm;
+    float *hb = s.h, *x_mid = s.x_mid;
+    _Float16* xn2 = s.xn2;
+    const int Hh = H;
+    LLMT_HIP_TRY(run(CAT_ROWS, "o_post", [=](hipStream_t q) {
+      return o_post(ri, x_in, fw, eps, Hh, T, hb, x_mid, xn2, q);
+    }));
+  }
   // gate/up, SwiGLU (in the GEMM epilogue where the large-tile kernel runs)
   BSeg sg[1] = {wseg(w.wgu)};
   if (gemm_glu_ok(T, I, H, sg[0].is_i8)) {
     LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn2, H, sg, 1, T, H, s.gu, 2 * I, nullptr, a16));
   } else {
     LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn2, H, sg, 1, T, H, nullptr, 0, &go));
-    LLMT_HIP_TRY(mark(CAT_ROWS));
-    LLMT_HIP_TRY(gu_post(row_in(go), I, T, s.gu, a16, st));
+    const RowIn ri = row_in(go);
+    float* gu = s.gu;
+    _Float16* a = a16;
+    const int Ii = I;
+    LLMT_HIP_TRY(run(CAT_ROWS, "gu_post", [=](hipStream_t q) { return gu_post(ri, Ii, T, gu, a, q); }));
   }
   // down, residual, next norm
   BSeg sd[1] = {wseg(w.wd)};
   LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, a16, I, sd, 1, T, I, nullptr, 0, &go));
-  LLMT_HIP_TRY(mark(CAT_ROWS));
-  LLMT_HIP_TRY(resid_norm(row_in(go), s.x_mid, next_w, eps, H, T, x_out, xn_out, st));
+  {
+    const RowIn ri = row_in(go);
+    const float* x_mid = s.x_mid;
+    const int Hh = H;
+    LLMT_HIP_TRY(run(CAT_ROWS, "resid_norm", [=](hipStream_t q) {
+      return resid_norm(ri, x_mid, next_w, eps, Hh, T, x_out, xn_out, q);
+    }));
+  }
   return hipSuccess;
 }
 
 hipError_t Ctx::forward(const int* tok, int B, float* logits_out) {
   const int T = B * S;
-  LLMT_HIP_TRY(mark(CAT_ROWS));
-  LLMT_HIP_TRY(embed_norm(tok, E, V, H, layers[0].attn_norm, dims.eps, T, stash[0].x_in,
-                          stash[0].xn, st));
+  {
+    const _Float16* e = E;
+    const int Vv = V, Hh = H;
+    const float *w0 = layers[0].attn_norm, eps = dims.eps;
+    float* x0 = stash[0].x_in;
+    _Float16* xn0 = stash[0].xn;
+    LLMT_HIP_TRY(run(CAT_ROWS, "embed_norm", [=](hipStream_t q) {
+      return embed_norm(tok, e, Vv, Hh, w0, eps, T, x0, xn0, q);
+    }));
+  }
   for (int l = 0; l < L; ++l) {
     const bool last = l + 1 == L;
     LLMT_HIP_TRY(layer_fwd(l, B, last ? final_norm : layers[l + 1].attn_norm,
                            last ? x_final : stash[l + 1].x_in, last ? xf16 : stash[l + 1].xn));
   }
   // lm_head logits (tied embedding)
-  BSeg se[1] = {hseg(E, V, H)};
+  BSeg se[1] = {hseg(Eh, V, H)};
   LLMT_HIP_TRY(gemm(CAT_GEMM_HEAD, xf16, H, se, 1, T, H, logits_out ? logits_out : logits, V,
                     nullptr));
   return hipSuccess;
 }
 
 hipError_t Ctx::ce(const float* lg, const int* tgt, int B, float* dlogits_out) {
-  LLMT_HIP_TRY(mark(CAT_CE));
-  LLMT_HIP_TRY(cross_entropy(lg ? lg : logits, tgt, B * S, V, S, ce_stats, dlogits_out, grad16,
-                             loss_rows, loss_dev, st));
+  const float* x = lg ? lg : logits;
+  const int rows = B * S, Vv = V, Ss = S;
+  float2* stats = ce_stats;
+  _Float16* g16c = grad16;
+  float *lr = loss_rows, *lm = loss_dev;
+  LLMT_HIP_TRY(run(CAT_CE, "cross_entropy", [=](hipStream_t q) {
+    return cross_entropy(x, tgt, rows, Vv, Ss, stats, dlogits_out, g16c, lr, lm, q);
+  }));
   return hipSuccess;
 }
 
@@ -292,7 +306,7 @@ hipError_t Ctx::head_bwd(int B) {
   const int n_valid = B * (S - 1);
   GemmOut go;
   // lm_head dX over the vocabulary, then the final RMSNorm backward.
-  BSeg sh_[1] = {hseg(ET, H, V)};
+  BSeg sh_[1] = {hseg(EhT, H, V)};
   LLMT_HIP_TRY(gemm(CAT_GEMM_HEAD, grad16, V, sh_, 1, T, V, nullptr, 0, &go));
   NormBwdArgs nb{};
   nb.in = row_in(go);
@@ -308,8 +322,7 @@ hipError_t Ctx::head_bwd(int B) {
   nb.dmid_out = nullptr;
   nb.g16 = g16;
   nb.rinv_out = rinv;
-  LLMT_HIP_TRY(mark(CAT_ROWS));
-  LLMT_HIP_TRY(norm_bwd(nb, T, st));
+  LLMT_HIP_TRY(run(CAT_ROWS, "norm_bwd", [=](hipStream_t q) { return norm_bwd(nb, T, q); }));
   return hipSuccess;
 }
 
@@ -332,8 +345,16 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   // MLP: down dX -> SwiGLU bwd -> gate/up dX -> FFN norm bwd (+ residual)
   BSeg sd[1] = {wseg(w.wdT)};
   LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, sd, 1, T, H, nullptr, 0, &go_));
-  LLMT_HIP_TRY(mark(CAT_ROWS));
-  LLMT_HIP_TRY(swiglu_bwd(row_in(go_), rinv, s.gu, I, T, dgu16, rinv2, st));
+  {
+    const RowIn ri = row_in(go_);
+    const float *ri_in = rinv, *gu = s.gu;
+    _Float16* d16 = dgu16;
+    float* r2 = rinv2;
+    const int Ii = I;
+    LLMT_HIP_TRY(run(CAT_ROWS, "swiglu_bwd", [=](hipStream_t q) {
+      return swiglu_bwd(ri, ri_in, gu, Ii, T, d16, r2, q);
+    }));
+  }
   BSeg sg[1] = {wseg(w.wguT)};
   LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, dgu16, 2 * I, sg, 1, T, 2 * I, nullptr, 0, &go_));
   nb = NormBwdArgs{};
@@ -350,19 +371,25 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   nb.dmid_out = nullptr;
   nb.g16 = og16;
   nb.rinv_out = ro(l);
-  LLMT_HIP_TRY(mark(CAT_ROWS));
-  LLMT_HIP_TRY(norm_bwd(nb, T, st));
+  LLMT_HIP_TRY(run(CAT_ROWS, "norm_bwd", [=](hipStream_t q) { return norm_bwd(nb, T, q); }));
   // O projection dX (+ dh_o through the B_o^T rows)
   BSeg so[2] = {wseg(w.woT), hseg(shadow_ptr(l, sh_bt_o), kRank, H)};
   const LoraTerm tbo[1] = {{shadow_rm + (size_t)l * shadow_per_layer + sh_a_o, 0, Q, 0, Q, 0}};
   LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, og16, H, so, 2, T, H, nullptr, 0, &go_));
-  LLMT_HIP_TRY(mark(CAT_ROWS));
-  LLMT_HIP_TRY(o_dx_post(row_in(go_, Q, kRank, 1, tbo), ro(l), s.o16, nq, S, T, dh, dO16, delta,
-                         dsc, st));
+  {
+    const RowIn ri = row_in(go_, Q, kRank, 1, tbo);
+    const float* r = ro(l);
+    const _Float16* o16 = s.o16;
+    _Float16* d16 = dO16;
+    float *de = delta, *ds = dsc;
+    const int nqh = nq, Ss = S;
+    LLMT_HIP_TRY(run(CAT_ROWS, "o_dx_post", [=](hipStream_t q) {
+      return o_dx_post(ri, r, o16, nqh, Ss, T, dh, d16, de, ds, q);
+    }));
+  }
   // attention backward
-  AttnArgs aa = attn_args(s);
-  LLMT_HIP_TRY(mark(CAT_ATTN));
-  LLMT_HIP_TRY(attn_bwd(aa, B, st));
+  const AttnArgs aa = attn_args(s);
+  LLMT_HIP_TRY(run(CAT_ATTN, "attn_bwd", [=](hipStream_t q) { return attn_bwd(aa, B, q); }));
   // RoPE + QK-norm backward
   QkBwdArgs qb{};
   qb.dqkv = dqkv32; qb.ld_dqkv = NT;
@@ -372,8 +399,7 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   qb.cosT = cosT; qb.sinT = sinT;
   qb.S = S; qb.nq = nq; qb.nkv = nkv; qb.eps = eps;
   qb.dy32 = nullptr; qb.g16 = qg16; qb.rinv_out = rq(l);
-  LLMT_HIP_TRY(mark(CAT_ROWS));
-  LLMT_HIP_TRY(qk_bwd(qb, T, st));
+  LLMT_HIP_TRY(run(CAT_ROWS, "qk_bwd", [=](hipStream_t q) { return qk_bwd(qb, T, q); }));
   // Q/K/V dX (+ dh_q, dh_k, dh_v through the B^T rows), attention norm bwd
   BSeg sq[2] = {wseg(w.wqkvT), hseg(shadow_ptr(l, sh_bt_qkv), 3 * kRank, NT)};
   const _Float16* a_qkv = shadow_rm + (size_t)l * shadow_per_layer + sh_a_qkv;
@@ -396,14 +422,18 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   nb.dmid_out = nullptr;
   nb.g16 = g16;
   nb.rinv_out = rinv;
-  LLMT_HIP_TRY(mark(CAT_ROWS));
-  LLMT_HIP_TRY(norm_bwd(nb, T, st));
+  LLMT_HIP_TRY(run(CAT_ROWS, "norm_bwd_lora", [=](hipStream_t q) { return norm_bwd(nb, T, q); }));
   return hipSuccess;
 }
 
 hipError_t Ctx::lora_grads(int l0, int nl, int B, int accumulate) {
-  LLMT_HIP_TRY(mark(CAT_LORA));
-  return lora_grad(lora_jobs + (size_t)l0 * kLoraJobs, lora_plan, nl, B * S, lscale, accumulate, st);
+  const LoraGradJob* jobs = lora_jobs + (size_t)l0 * kLoraJobs;
+  const LoraGradPlan plan = lora_plan;
+  const float ls = lscale;
+  const int T = B * S;
+  return run(CAT_LORA, "lora_grad", [=](hipStream_t q) {
+    return lora_grad(jobs, plan, nl, T, ls, accumulate, q);
+  });
 }
 
 hipError_t Ctx::backward(int B, int accumulate) {
@@ -415,9 +445,11 @@ hipError_t Ctx::backward(int B, int accumulate) {
 }
 
 hipError_t Ctx::optimizer() {
-  LLMT_HIP_TRY(mark(CAT_ADAM));
-  LLMT_HIP_TRY(adamw(lora_p, lora_g, lora_m, lora_v, (long long)lora_numel, hp_dev, 1,
-                     shadow_desc(), st));
+  float *p = lora_p, *g = lora_g, *m = lora_m, *v = lora_v;
+  const long long n = (long long)lora_numel;
+  const AdamHp* hp = hp_dev;
+  const AdamShadow sh = shadow_desc();
+  LLMT_HIP_TRY(run(CAT_ADAM, "adamw", [=](hipStream_t q) { return adamw(p, g, m, v, n, hp, 1, sh, q); }));
   return hipSuccess;
 }
 
@@ -432,7 +464,6 @@ hipError_t Ctx::device_step(int B, int with_adam) {
   LLMT_HIP_TRY(ce(nullptr, tgt_buf, B, nullptr));
   LLMT_HIP_TRY(backward(B, 0));
   if (with_adam) LLMT_HIP_TRY(optimizer());
-  LLMT_HIP_TRY(mark(CAT_END));
   return hipSuccess;
 }
 
@@ -595,11 +626,7 @@ static int set_hp(Ctx* c, const llmt_hparams* hp, int step) {
 // the first change switches the context to copies outside the graph (one
 // rebuild, then the graph is reused whatever the pointers).
 static bool graph_inputs(Ctx* c, const int* tokens, const int* targets) {
-  static const int on = [] {
-    const char* e = getenv("LLMT_GRAPH_INPUTS");
-    return e ? atoi(e) : 1;
-  }();
-  if (!c->use_graph || c->profiling || on == 0 || c->inputs_move) return false;
+  if (!c->use_graph || c->recording || c->inputs_move) return false;
   if (c->graph_exec && c->graph_tok && (c->graph_tok != tokens || c->graph_tgt != targets)) {
     c->inputs_move = true;
     return false;
@@ -611,7 +638,7 @@ static bool graph_inputs(Ctx* c, const int* tokens, const int* targets) {
 // hyper-parameters) are copied inside the graph instead of before it.
 static int run_step(Ctx* c, int batch, int with_adam, float* loss_host,
                     const int* tokens = nullptr, const int* targets = nullptr) {
-  if (c->use_graph && !c->profiling) {
+  if (c->use_graph && !c->recording) {
     if (!c->graph_exec || c->graph_batch != batch || c->graph_adam != with_adam ||
         c->graph_tok != tokens || c->graph_tgt != targets) {
       if (c->graph_exec) {
@@ -642,8 +669,6 @@ static int run_step(Ctx* c, int batch, int with_adam, float* loss_host,
     }
     TRY_HIP(hipGraphLaunch(c->graph_exec, c->st));
   } else {
-    c->prof_n = 0;
-    c->gemm_flops = c->gemm_wbytes = 0;
     TRY_HIP(c->device_step(batch, with_adam));
   }
   TRY_HIP(hipMemcpyAsync(c->host_loss, c->loss_dev, sizeof(float), hipMemcpyDeviceToHost, c->st));
@@ -702,197 +727,104 @@ int llmt_set_graph(llmt_ctx* ctx, int enable) {
 
 const float* llmt_logits(const llmt_ctx* ctx) { return ctx ? C_(ctx)->logits : nullptr; }
 
-// Replays exactly the GEMM launches of one step (same shapes, operands and
-// workspaces; the other kernels left out) `reps` times as one captured graph
-// and returns the average duration of one GEMM launch.
-int llmt_profile_gemms(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
-                       const llmt_hparams* hp, int step, int reps, float* avg_us,
-                       int* launches, double* weight_bytes, double* flops) {
-  set_error("");
-  Ctx* c = C_(ctx);
-  int rc = check_tokens(c, tokens, targets, batch);
-  if (rc) return rc;
-  TRY_ARG(avg_us && reps >= 1, "llmt_profile_gemms: avg_us, reps");
-  if ((rc = set_hp(c, hp, step))) return rc;
-  if ((rc = stage_inputs(c, tokens, targets, batch))) return rc;
-  const bool was_graph = c->use_graph;
-  c->use_graph = false;
-  c->record_gemms = true;
-  c->recorded.clear();
-  rc = run_step(c, batch, 1, nullptr);
-  c->record_gemms = false;
-  c->use_graph = was_graph;
-  if (rc) return rc;
-  const double fl = c->gemm_flops, wb = c->gemm_wbytes;
-  std::vector<GemmArgs> gs = c->recorded;
+const float* llmt_layer_in(const llmt_ctx* ctx, int layer) {
+  const Ctx* c = C_(ctx);
+  return c && layer >= 0 && layer < c->L ? c->stash[layer].x_in : nullptr;
+}
+
+// Times `fns` replayed back to back `reps` times as one captured graph
+// (after one warm-up launch): the average duration of one of them in us.
+static int replay_us(Ctx* c, const std::vector<const Launch*>& fns, int reps, float* us) {
   hipGraph_t gph = nullptr;
   hipGraphExec_t ex = nullptr;
   TRY_HIP(hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
   hipError_t e = hipSuccess;
-  for (const GemmArgs& g : gs)
-    if (e == hipSuccess) e = gemm_nt(g, c->st);
+  for (const Launch* l : fns)
+    if (e == hipSuccess) e = l->fn(c->st);
   hipError_t e2 = hipStreamEndCapture(c->st, &gph);
   TRY_HIP(e);
   TRY_HIP(e2);
   e = hipGraphInstantiate(&ex, gph, nullptr, nullptr, 0);
   hipGraphDestroy(gph);
   TRY_HIP(e);
-  hipEvent_t e0, e1;
-  TRY_HIP(hipEventCreate(&e0));
-  TRY_HIP(hipEventCreate(&e1));
-  TRY_HIP(hipGraphLaunch(ex, c->st));  // warm
-  TRY_HIP(hipEventRecord(e0, c->st));
-  for (int r = 0; r < reps; ++r) TRY_HIP(hipGraphLaunch(ex, c->st));
-  TRY_HIP(hipEventRecord(e1, c->st));
-  TRY_HIP(hipEventSynchronize(e1));
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  e = hipEventCreate(&e0);
+  if (e == hipSuccess) e = hipEventCreate(&e1);
+  if (e == hipSuccess) e = hipGraphLaunch(ex, c->st);  // warm
+  if (e == hipSuccess) e = hipEventRecord(e0, c->st);
+  for (int r = 0; r < reps && e == hipSuccess; ++r) e = hipGraphLaunch(ex, c->st);
+  if (e == hipSuccess) e = hipEventRecord(e1, c->st);
+  if (e == hipSuccess) e = hipEventSynchronize(e1);
   float ms = 0.f;
-  TRY_HIP(hipEventElapsedTime(&ms, e0, e1));
-  hipEventDestroy(e0);
-  hipEventDestroy(e1);
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+  if (e0) hipEventDestroy(e0);
+  if (e1) hipEventDestroy(e1);
   hipGraphExecDestroy(ex);
-  *avg_us = gs.empty() ? 0.f : ms * 1e3f / (float)(reps * gs.size());
-  if (launches) *launches = (int)gs.size();
-  if (weight_bytes) *weight_bytes = wb;
-  if (flops) *flops = fl;
+  TRY_HIP(e);
+  *us = ms * 1e3f / (float)(reps * fns.size());
   return LLMT_OK;
 }
 
-int llmt_profile_gemm_shapes(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
-                             const llmt_hparams* hp, int step, int reps, int max_shapes,
-                             int* nshapes, int* shape_info, float* shape_us) {
+int llmt_profile_kernels(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
+                         const llmt_hparams* hp, int step, int reps, int max_kinds, int* nkinds,
+                         const char** names, int* cats, int* launches, float* us, double* flops,
+                         double* bytes) {
   set_error("");
   Ctx* c = C_(ctx);
   int rc = check_tokens(c, tokens, targets, batch);
   if (rc) return rc;
-  TRY_ARG(nshapes && shape_info && shape_us && reps >= 1 && max_shapes >= 1,
-          "llmt_profile_gemm_shapes: outputs, reps");
+  TRY_ARG(nkinds && names && cats && launches && us && flops && bytes && reps >= 1 &&
+              max_kinds >= 1,
+          "llmt_profile_kernels: outputs, reps, max_kinds");
   if ((rc = set_hp(c, hp, step))) return rc;
   if ((rc = stage_inputs(c, tokens, targets, batch))) return rc;
-  const bool was_graph = c->use_graph;
-  c->use_graph = false;
-  c->record_gemms = true;
-  c->recorded.clear();
+  // 1. one eager step, every launch recorded
+  c->recording = true;
+  c->launches.clear();
   rc = run_step(c, batch, 1, nullptr);
-  c->record_gemms = false;
-  c->use_graph = was_graph;
+  c->recording = false;
   if (rc) return rc;
-  // group launches by (N, K, split), in first-seen order
-  std::vector<std::vector<int>> groups;
-  std::vector<std::array<int, 4>> keys;
-  for (size_t i = 0; i < c->recorded.size(); ++i) {
-    const GemmArgs& g = c->recorded[i];
-    const std::array<int, 4> k{g.N, g.K, g.split, g.seg[0].is_i8};
+  // 2. group by kind, in first-seen order
+  std::vector<std::vector<const Launch*>> groups;
+  std::vector<std::string> keys;
+  for (const Launch& l : c->launches) {
     size_t j = 0;
-    while (j < keys.size() && keys[j] != k) ++j;
+    while (j < keys.size() && keys[j] != l.kind) ++j;
     if (j == keys.size()) {
-      keys.push_back(k);
+      keys.push_back(l.kind);
       groups.emplace_back();
     }
-    groups[j].push_back((int)i);
+    groups[j].push_back(&l);
   }
-  const int ns = (int)std::min<size_t>(groups.size(), (size_t)max_shapes);
-  hipEvent_t e0, e1;
-  TRY_HIP(hipEventCreate(&e0));
-  TRY_HIP(hipEventCreate(&e1));
-  for (int s = 0; s < ns; ++s) {
-    {
-      hipGraph_t gph = nullptr;
-      hipGraphExec_t ex = nullptr;
-      TRY_HIP(hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
-      hipError_t e = hipSuccess;
-      for (int i : groups[s])
-        if (e == hipSuccess) e = gemm_nt(c->recorded[i], c->st);
-      hipError_t e2 = hipStreamEndCapture(c->st, &gph);
-      TRY_HIP(e);
-      TRY_HIP(e2);
-      e = hipGraphInstantiate(&ex, gph, nullptr, nullptr, 0);
-      hipGraphDestroy(gph);
-      TRY_HIP(e);
-      TRY_HIP(hipGraphLaunch(ex, c->st));
-      TRY_HIP(hipEventRecord(e0, c->st));
-      for (int r = 0; r < reps; ++r) TRY_HIP(hipGraphLaunch(ex, c->st));
-      TRY_HIP(hipEventRecord(e1, c->st));
-      TRY_HIP(hipEventSynchronize(e1));
-      float ms = 0.f;
-      TRY_HIP(hipEventElapsedTime(&ms, e0, e1));
-      hipGraphExecDestroy(ex);
-      shape_us[s] = ms * 1e3f / (float)(reps * groups[s].size());
-    }
-    const GemmArgs& g = c->recorded[groups[s][0]];
-    int* inf = shape_info + 5 * s;
-    inf[0] = g.N;
-    inf[1] = g.K;
-    inf[2] = g.split;
-    inf[3] = (int)groups[s].size();
-    inf[4] = g.seg[0].is_i8;
+  // 3. replay each kind on its own.  AdamW replays would step the adapters
+  // again: the arenas are saved first and restored after.
+  const size_t nb = c->lora_numel * sizeof(float);
+  float* saved = nullptr;
+  TRY_HIP(hipMalloc(&saved, 3 * nb));
+  float* arena[3] = {c->lora_p, c->lora_m, c->lora_v};
+  hipError_t e = hipSuccess;
+  for (int i = 0; i < 3 && e == hipSuccess; ++i)
+    e = hipMemcpyAsync((char*)saved + i * nb, arena[i], nb, hipMemcpyDeviceToDevice, c->st);
+  const int nk = (int)std::min<size_t>(groups.size(), (size_t)max_kinds);
+  c->prof_names = keys;
+  for (int k = 0; k < nk && rc == LLMT_OK && e == hipSuccess; ++k) {
+    rc = replay_us(c, groups[k], reps, &us[k]);
+    const Launch& l0 = *groups[k][0];
+    names[k] = c->prof_names[k].c_str();
+    cats[k] = l0.cat;
+    launches[k] = (int)groups[k].size();
+    flops[k] = l0.flops;
+    bytes[k] = l0.bytes;
   }
-  hipEventDestroy(e0);
-  hipEventDestroy(e1);
-  *nshapes = ns;
-  return LLMT_OK;
-}
-
-int llmt_profile_step(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
-                      const llmt_hparams* hp, int step, float* cat_ms, int ncat,
-                      double* gemm_flops, double* gemm_weight_bytes, int* profile_graph) {
-  set_error("");
-  Ctx* c = C_(ctx);
-  int rc = check_tokens(c, tokens, targets, batch);
+  for (int i = 0; i < 3 && e == hipSuccess; ++i)
+    e = hipMemcpyAsync(arena[i], (char*)saved + i * nb, nb, hipMemcpyDeviceToDevice, c->st);
+  if (e == hipSuccess) e = c->refresh_shadows();
+  if (e == hipSuccess) e = hipStreamSynchronize(c->st);
+  hipFree(saved);
+  c->launches.clear();
   if (rc) return rc;
-  TRY_ARG(cat_ms && ncat >= 1, "llmt_profile_step: cat_ms");
-  if ((rc = set_hp(c, hp, step))) return rc;
-  if ((rc = stage_inputs(c, tokens, targets, batch))) return rc;
-  // Events between consecutive kernels.  The profiled step is captured into
-  // a graph (event-record nodes) and replayed, so the kernels run back to
-  // back as in the timed loop; an eager run is the fallback.
-  c->profiling = true;
-  c->prof_n = 0;
-  c->gemm_flops = c->gemm_wbytes = 0;
-  bool captured = false;
-  {
-    hipGraph_t gph = nullptr;
-    hipGraphExec_t ex = nullptr;
-    if (hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal) == hipSuccess) {
-      hipError_t e = c->device_step(batch, 1);
-      hipError_t e2 = hipStreamEndCapture(c->st, &gph);
-      if (e == hipSuccess && e2 == hipSuccess &&
-          hipGraphInstantiate(&ex, gph, nullptr, nullptr, 0) == hipSuccess &&
-          hipGraphLaunch(ex, c->st) == hipSuccess && hipGraphLaunch(ex, c->st) == hipSuccess &&
-          hipStreamSynchronize(c->st) == hipSuccess) {
-        // Event-record nodes only help if their timestamps can be read back.
-        float ms = 0.f;
-        captured = c->prof_n > 1 &&
-                   hipEventElapsedTime(&ms, c->prof_ev[0], c->prof_ev[1]) == hipSuccess;
-      }
-      if (ex) hipGraphExecDestroy(ex);
-      if (gph) hipGraphDestroy(gph);
-    }
-    (void)hipGetLastError();
-  }
-  if (!captured) {
-    // Eager fallback: a bounded delay kernel first keeps the GPU busy while
-    // the host enqueues the whole step, so the kernels (and the events
-    // between them) then run back to back without host launch gaps.
-    TRY_HIP(gpu_delay(20000, c->st));
-    c->prof_n = 0;
-    c->gemm_flops = c->gemm_wbytes = 0;
-    rc = run_step(c, batch, 1, nullptr);
-    if (rc) {
-      c->profiling = false;
-      return rc;
-    }
-  }
-  c->profiling = false;
-  if (profile_graph) *profile_graph = captured ? 1 : 0;
-  for (int i = 0; i < ncat; ++i) cat_ms[i] = 0.f;
-  for (int i = 0; i + 1 < c->prof_n; ++i) {
-    float ms = 0.f;
-    TRY_HIP(hipEventElapsedTime(&ms, c->prof_ev[i], c->prof_ev[i + 1]));
-    const int cat = c->prof_cat[i];
-    if (cat >= 0 && cat < ncat) cat_ms[cat] += ms;
-  }
-  if (gemm_flops) *gemm_flops = c->gemm_flops;
-  if (gemm_weight_bytes) *gemm_weight_bytes = c->gemm_wbytes;
+  TRY_HIP(e);
+  *nkinds = nk;
   return LLMT_OK;
 }
 

@@ -58,6 +58,7 @@ _PROTOS = {
     "llmt_set_layer_f16": (i32, [vp, i32] + [vp] * 11),
     "llmt_set_layer_i8": (i32, [vp, i32, C.POINTER(vp), C.POINTER(vp), vp, vp, vp, vp]),
     "llmt_set_embed_f16": (i32, [vp, vp, vp]),
+    "llmt_set_lm_head_f16": (i32, [vp, vp]),
     "llmt_load_weights_dir": (i32, [vp, C.c_char_p]),
     "llmt_lora_numel": (sz, [vp]),
     "llmt_lora_offset": (sz, [vp, i32, i32, i32]),
@@ -71,18 +72,15 @@ _PROTOS = {
     "llmt_forward_backward": (i32, [vp, vp, vp, i32, fp]),
     "llmt_set_graph": (i32, [vp, i32]),
     "llmt_logits": (vp, [vp]),
+    "llmt_layer_in": (vp, [vp, i32]),
     "llmt_layer_forward": (i32, [vp, i32, vp, vp, i32]),
     "llmt_layer_backward": (i32, [vp, i32, vp, vp, i32]),
     "llmt_adamw": (i32, [vp, C.POINTER(HParams), i32]),
     "llmt_head_ce": (i32, [vp, vp, vp, i32, fp, vp, vp]),
-    "llmt_profile_gemm_shapes": (i32, [vp, vp, vp, i32, C.POINTER(HParams), i32, i32, i32,
-                                       C.POINTER(C.c_int), C.POINTER(C.c_int), fp]),
-    "llmt_profile_gemms": (i32, [vp, vp, vp, i32, C.POINTER(HParams), i32, i32, fp,
-                                 C.POINTER(C.c_int), C.POINTER(C.c_double),
-                                 C.POINTER(C.c_double)]),
-    "llmt_profile_step": (i32, [vp, vp, vp, i32, C.POINTER(HParams), i32, fp, i32,
-                                C.POINTER(C.c_double), C.POINTER(C.c_double),
-                                C.POINTER(C.c_int)]),
+    "llmt_profile_kernels": (i32, [vp, vp, vp, i32, C.POINTER(HParams), i32, i32, i32,
+                                   C.POINTER(C.c_int), C.POINTER(C.c_char_p),
+                                   C.POINTER(C.c_int), C.POINTER(C.c_int), fp,
+                                   C.POINTER(C.c_double), C.POINTER(C.c_double)]),
 }
 
 _lib = None
@@ -190,7 +188,7 @@ def cross_entropy(logits, targets, seq_len, want_dlogits=True, stream=None):
 # ------------------------------------------------------------------ training context
 
 PROFILE_CATEGORIES = ("gemm_fwd", "gemm_bwd", "gemm_lm_head", "attention", "row_epilogues",
-                      "cross_entropy", "lora_grad", "adamw", "split_reduce")
+                      "cross_entropy", "lora_grad", "adamw")
 
 
 def hparams(lr=3e-4, beta1=0.9, beta2=0.999, eps=1e-8, wd=0.01) -> HParams:
@@ -242,6 +240,10 @@ class Context:
     def set_embed_f16(self, embed, final_norm):
         check(lib().llmt_set_embed_f16(self.h, ptr(embed), ptr(final_norm)))
 
+    def set_lm_head_f16(self, lm_head):
+        """An untied lm_head [V, H] fp16 (llmt_set_lm_head_f16)."""
+        check(lib().llmt_set_lm_head_f16(self.h, ptr(lm_head)))
+
     def load_weights_dir(self, path):
         check(lib().llmt_load_weights_dir(self.h, str(path).encode()))
 
@@ -283,20 +285,56 @@ class Context:
         check(lib().llmt_lora_load_state(self.h, str(path).encode(), step))
 
     # -- the step
+    def _check_tokens(self, tokens, targets):
+        """tokens/targets must be int32 device tensors [B, seq_len] with
+        1 <= B <= max_batch, contiguous (the library copies B * seq_len ids
+        from each pointer; the step graph repeats that copy on every replay)."""
+        import torch
+        for name, t in (("tokens", tokens), ("targets", targets)):
+            if not isinstance(t, torch.Tensor):
+                raise LlmtError(f"{name} must be a torch tensor")
+            if t.dtype != torch.int32:
+                raise LlmtError(f"{name} must be int32 (got {t.dtype})")
+            if not t.is_cuda:
+                raise LlmtError(f"{name} must be a device tensor")
+            if not t.is_contiguous():
+                raise LlmtError(f"{name} must be contiguous")
+            if t.dim() != 2 or t.shape[1] != self.seq_len or not 1 <= t.shape[0] <= self.max_batch:
+                raise LlmtError(f"{name} must be [B, {self.seq_len}] with 1 <= B <= "
+                                f"{self.max_batch} (got {tuple(t.shape)})")
+        if tokens.shape != targets.shape:
+            raise LlmtError(f"tokens {tuple(tokens.shape)} and targets {tuple(targets.shape)} differ")
+        return tokens.shape[0]
+
     def set_graph(self, enable: bool):
         check(lib().llmt_set_graph(self.h, int(enable)))
 
     def step(self, tokens, targets, hp: HParams, step: int) -> float:
+        B = self._check_tokens(tokens, targets)
         loss = C.c_float()
-        check(lib().llmt_step(self.h, ptr(tokens), ptr(targets), tokens.shape[0], C.byref(hp),
-                              step, C.byref(loss)))
+        check(lib().llmt_step(self.h, ptr(tokens), ptr(targets), B, C.byref(hp), step,
+                              C.byref(loss)))
         return loss.value
 
     def forward_backward(self, tokens, targets) -> float:
+        B = self._check_tokens(tokens, targets)
         loss = C.c_float()
-        check(lib().llmt_forward_backward(self.h, ptr(tokens), ptr(targets), tokens.shape[0],
-                                          C.byref(loss)))
+        check(lib().llmt_forward_backward(self.h, ptr(tokens), ptr(targets), B, C.byref(loss)))
         return loss.value
+
+    def layer_in(self, layer, rows):
+        """A copy of the fp32 residual stream [rows, H] at the input of
+        `layer` from the last forward (llmt_layer_in)."""
+        import torch
+        addr = lib().llmt_layer_in(self.h, layer)
+        if not addr:
+            raise LlmtError(f"llmt_layer_in: no layer {layer}")
+        H = self.dims.hidden
+
+        class _View:
+            __cuda_array_interface__ = {"shape": (rows, H), "typestr": "<f4",
+                                        "data": (addr, False), "version": 3, "strides": None}
+        return torch.as_tensor(_View(), device="cuda").clone()
 
     def head_ce(self, hidden16, targets, want_dlogits=False):
         """C1 on the context's tied embedding: (loss, dlogits or None, dhidden)."""
@@ -322,37 +360,23 @@ class Context:
         check(lib().llmt_layer_backward(self.h, layer, ptr(dy), ptr(dx), batch))
         return dx
 
-    def profile_gemms(self, tokens, targets, hp: HParams, step: int, reps: int = 5):
-        """(average GEMM launch us, launches per step, weight bytes, flops per step)."""
-        us, n, wb, fl = C.c_float(), C.c_int(), C.c_double(), C.c_double()
-        check(lib().llmt_profile_gemms(self.h, ptr(tokens), ptr(targets), tokens.shape[0],
-                                       C.byref(hp), step, reps, C.byref(us), C.byref(n),
-                                       C.byref(wb), C.byref(fl)))
-        return us.value, n.value, wb.value, fl.value
-
-    def profile_gemm_shapes(self, tokens, targets, hp: HParams, step: int, reps: int = 5):
-        """Per GEMM shape of the step: dicts with N, K, split, launches, int8
-        and us (average launch duration)."""
-        mx = 32
+    def profile_kernels(self, tokens, targets, hp: HParams, step: int, reps: int = 5):
+        """Per kernel kind of one step (llmt_profile_kernels): a list of dicts
+        with name, category, launches (per step), us (average launch
+        duration), flops and bytes (per launch; GEMMs only).  The adapters
+        advance by one AdamW step."""
+        mx = 256
         ns = C.c_int()
-        info = (C.c_int * (5 * mx))()
+        names = (C.c_char_p * mx)()
+        cats, nl = (C.c_int * mx)(), (C.c_int * mx)()
         us = (C.c_float * mx)()
-        check(lib().llmt_profile_gemm_shapes(self.h, ptr(tokens), ptr(targets), tokens.shape[0],
-                                             C.byref(hp), step, reps, mx, C.byref(ns), info, us))
-        keys = ("N", "K", "split", "launches", "int8")
-        return [dict(zip(keys, info[5 * s:5 * s + 5]), us=us[s]) for s in range(ns.value)]
-
-    def profile_step(self, tokens, targets, hp: HParams, step: int):
-        """Per-category kernel milliseconds of one eager step, plus the step's
-        GEMM FLOPs and weight bytes."""
-        n = len(PROFILE_CATEGORIES)
-        ms = (C.c_float * n)()
-        fl, wb, gr = C.c_double(), C.c_double(), C.c_int()
-        check(lib().llmt_profile_step(self.h, ptr(tokens), ptr(targets), tokens.shape[0],
-                                      C.byref(hp), step, ms, n, C.byref(fl), C.byref(wb),
-                                      C.byref(gr)))
-        self.last_profile_graph = bool(gr.value)
-        return dict(zip(PROFILE_CATEGORIES, list(ms))), fl.value, wb.value
+        fl, by = (C.c_double * mx)(), (C.c_double * mx)()
+        check(lib().llmt_profile_kernels(self.h, ptr(tokens), ptr(targets),
+                                         self._check_tokens(tokens, targets), C.byref(hp), step,
+                                         reps, mx, C.byref(ns), names, cats, nl, us, fl, by))
+        return [dict(name=names[k].decode(), category=PROFILE_CATEGORIES[cats[k]],
+                     launches=nl[k], us=us[k], flops=fl[k], bytes=by[k])
+                for k in range(ns.value)]
 
 
 def flatten_adapters(adapters, attr=("A", "B")):

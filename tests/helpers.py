@@ -61,3 +61,29 @@ def grad_errors(flat_gpu, grads_ref, dims):
             errs[(l, p, "A")] = rel_l2(got[l][p][0], grads_ref[l][p][0])
             errs[(l, p, "B")] = rel_l2(got[l][p][1], grads_ref[l][p][1])
     return errs
+
+
+def write_weights_dir(W, d, lm_head=None):
+    """A model in the reference's weight-file layout (src/train.cu:56-89,
+    python/export_weights.py:19-26): <d>/<hf_param_name>.bin raw fp32.  The
+    lm_head file is a copy of the embedding (scripts/run.sh:19) unless
+    lm_head is given."""
+    from pathlib import Path
+    d = Path(d)
+    d.mkdir(parents=True, exist_ok=True)
+
+    def put(name, t):
+        t.detach().to(torch.float32).contiguous().numpy().astype("<f4").tofile(d / f"{name}.bin")
+
+    put("model.embed_tokens.weight", W.embed)
+    put("lm_head.weight", W.embed if lm_head is None else lm_head)
+    put("model.norm.weight", W.final_norm)
+    for l, lw in enumerate(W.layers):
+        p = f"model.layers.{l}."
+        for name, t in (("self_attn.q_proj", lw.wq), ("self_attn.k_proj", lw.wk),
+                        ("self_attn.v_proj", lw.wv), ("self_attn.o_proj", lw.wo),
+                        ("mlp.gate_proj", lw.w_gate), ("mlp.up_proj", lw.w_up),
+                        ("mlp.down_proj", lw.w_down), ("input_layernorm", lw.attn_norm),
+                        ("post_attention_layernorm", lw.ffn_norm),
+                        ("self_attn.q_norm", lw.q_norm), ("self_attn.k_norm", lw.k_norm)):
+            put(p + name + ".weight", t)

@@ -17,7 +17,7 @@ import pytest
 import torch
 
 import llmt
-from helpers import SMALL, small_problem
+from helpers import SMALL, small_problem, write_weights_dir
 from oracle import lora_step as ref
 
 pytestmark = pytest.mark.gpu
@@ -31,23 +31,7 @@ DIMS = (f"{SMALL.hidden},{SMALL.n_layers},{SMALL.n_heads},{SMALL.n_kv_heads},"
 
 
 def _write_weights(W, d: Path):
-    d.mkdir(parents=True, exist_ok=True)
-
-    def put(name, t):
-        t.detach().to(torch.float32).contiguous().numpy().astype("<f4").tofile(d / f"{name}.bin")
-
-    put("model.embed_tokens.weight", W.embed)
-    put("lm_head.weight", W.embed)
-    put("model.norm.weight", W.final_norm)
-    for l, lw in enumerate(W.layers):
-        p = f"model.layers.{l}."
-        for name, t in (("self_attn.q_proj", lw.wq), ("self_attn.k_proj", lw.wk),
-                        ("self_attn.v_proj", lw.wv), ("self_attn.o_proj", lw.wo),
-                        ("mlp.gate_proj", lw.w_gate), ("mlp.up_proj", lw.w_up),
-                        ("mlp.down_proj", lw.w_down), ("input_layernorm", lw.attn_norm),
-                        ("post_attention_layernorm", lw.ffn_norm),
-                        ("self_attn.q_norm", lw.q_norm), ("self_attn.k_norm", lw.k_norm)):
-            put(p + name + ".weight", t)
+    write_weights_dir(W, d)
 
 
 def _run(args):

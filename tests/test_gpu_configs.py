@@ -260,8 +260,6 @@ def _attn_block_ref(q_raw, k_raw, v, do, eps=1e-6, theta=1e6):
     qr, kr, vv, dd = (t.float() for t in (q_raw, k_raw, v, do))
     qn = ref.rope_fwd(ref.rmsnorm(qr, w, eps), cos, sin)
     kn = ref.rope_fwd(ref.rmsnorm(kr, w, eps), cos, sin)
-    # the GPU rounds the normed q, k to fp16 before the attention
-    qn, kn = qn.half().float(), kn.half().float()
     o, lse = ref.attention_fwd(qn, kn, vv)
     dq, dk, dv = ref.attention_bwd(dd, qn, kn, vv, o, lse)
     dq = ref.rmsnorm_bwd(ref.rope_bwd(dq, cos, sin), qr, w, eps)
@@ -396,6 +394,49 @@ def test_c4_int8_reduced_matches_oracle(dev):
         ctx.close()
 
 
+def test_c4_int8_large_tile_full_width_matches_oracle(dev):
+    """C4's token count (B8 x S512 = 4096 rows) on the large-tile path
+    (gemm_dma_kernel with per-row and per-k int8 scales, the fused SwiGLU
+    epilogue at N = 2 x 6144, LoRA tail columns, the fp16 logits GEMM) at full
+    width with 2 layers; vocabulary 8192 keeps the CPU oracle to seconds."""
+    print("case: C4 T=4096 full width, 2 layers, V 8192, int8", flush=True)
+    torch.set_num_threads(16)
+    d = ref.Dims(n_layers=2, vocab=8192)
+    W, ad, tok, tgt, qs = config_model(d, batch=8, seq_len=512, seed=1014, int8=True)
+    loss_ref, grads_ref, _ = oracle_grads(W, ad, tok, tgt, d)
+    ctx = llmt.Context(llmt.make_dims(d), 8, 512, int8=True)
+    try:
+        _upload_i8(ctx, W, qs, dev)
+        ctx.lora_set("param", llmt.flatten_adapters(ad).to(dev))
+        loss = ctx.forward_backward(tok.to(dev), tgt.to(dev))
+        print(f"C4 T=4096: loss {loss:.6f} oracle {float(loss_ref):.6f}", flush=True)
+        assert abs(loss - float(loss_ref)) < LOSS_TOL
+        errs = grad_errors(ctx.lora_get("grad"), grads_ref, d)
+        print("C4 T=4096 worst", max(errs.items(), key=lambda kv: kv[1]), flush=True)
+        assert max(errs.values()) < GRAD_TOL
+    finally:
+        ctx.close()
+
+
+def test_logits_gemm_full_size(dev):
+    """The C4 logits GEMM shape, M = 4096 x N = 151936 x K = 2048 (fp16, fp32
+    accumulation), against fp32 torch on column slices at both ends and a
+    random sample of columns."""
+    print("case: GEMM 4096 x 151936 x 2048", flush=True)
+    M, N, K = 4096, 151936, 2048
+    g = torch.Generator(device=dev).manual_seed(1024)
+    A = torch.randn(M, K, generator=g, device=dev).half()
+    B = (torch.randn(N, K, generator=g, device=dev) * 0.02).half()
+    C = llmt.gemm_f16(A, B)
+    torch.cuda.synchronize()
+    cols = torch.cat([torch.arange(0, 256), torch.arange(N - 256, N),
+                      torch.randperm(N, generator=torch.Generator().manual_seed(3))[:512]])
+    want = A.float().cpu() @ B[cols.to(dev)].float().cpu().t()
+    got = C[:, cols.to(dev)].cpu()
+    assert rel_l2(got, want) < 1e-5
+    del C
+
+
 def test_device_quantizer_matches_oracle_on_c4_weights(dev):
     g = torch.Generator().manual_seed(1004)
     w = torch.randn(2048, 2048, generator=g) * 0.02
@@ -420,6 +461,16 @@ def test_c4_full_size_properties(dev):
         tok, tgt = win[:, :-1].contiguous(), win[:, 1:].contiguous()
         l1 = ctx.forward_backward(tok, tgt)
         g1 = ctx.lora_get("grad").clone()
+        # the loss is the mean over the 8 x 511 rows with a target of
+        # logsumexp(row) - row[target], from the library's own fp32 logits
+        logits = _ptr_tensor(llmt.lib().llmt_logits(ctx.h), 4096 * Q3.vocab, dev).view(4096, -1)
+        t = tgt.reshape(-1).long()
+        lse = torch.logsumexp(logits.double(), 1)
+        rows = lse - logits.gather(1, t[:, None]).squeeze(1).double()
+        valid = ref.valid_rows(8, 512).to(dev)
+        want = float(rows[valid].mean())
+        print(f"C4 full: loss {l1:.6f} from logits {want:.6f}", flush=True)
+        assert abs(l1 - want) < 1e-4
         l2 = ctx.forward_backward(tok, tgt)
         g2 = ctx.lora_get("grad")
         assert math.isfinite(l1) and abs(l1 - math.log(Q3.vocab)) < 2.0
