@@ -317,6 +317,15 @@ int llmt_quantize_rows_i8(const float* w, int rows, int cols, int8_t* q, float* 
  * (may be NULL). */
 int llmt_cross_entropy(const float* logits, const int* targets, int rows, int V, int seq_len,
                        float* dlogits, float* loss_rows, float* loss_mean, void* stream);
+/* llmt_cross_entropy without any allocation: no counterpart in the reference;
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops).  Same arguments, results and errors, plus
+ * LLMT_ERR_ARG when rows * ceil(V / 8192) exceeds 262144 (the library's
+ * built-in 2 MiB statistics scratch: 13,797 rows at V = 151936).  Calls that
+ * overlap on one GPU share that scratch and race. */
+int llmt_cross_entropy_noalloc(const float* logits, const int* targets, int rows, int V,
+                               int seq_len, float* dlogits, float* loss_rows, float* loss_mean,
+                               void* stream);
 /* Config C1: logits = hidden W^T, fused CE, dlogits, dhidden = dlogits W.
  * hidden [T, H] fp16, W [V, H] fp16 row-major (packed into temporaries on
  * every call); outputs fp32; *loss_mean is a device float; dlogits may be

@@ -15,6 +15,9 @@
 // Rows i with (i % seq_len) == seq_len - 1 have no target inside their
 // window (loss.cu:18-21); their loss is 0 and their dlogits row is written
 // as zeros (the reference leaves it uninitialised).
+#include <mutex>
+
+#include "../../include/llmt.h"
 #include "ops.h"
 
 namespace llmt {
@@ -158,4 +161,67 @@ hipError_t cross_entropy(const float* logits, const int* targets, int rows, int 
   return hipSuccess;
 }
 
+// ------------------------------------------------------------------ no-alloc variant
+// llmt_cross_entropy_noalloc keeps the per-(row, chunk) softmax statistics
+// in a file-scope device array instead of a workspace allocated per call:
+// kNoAllocStats float2 entries (2 MiB), enough for rows * ce_chunks(V) of
+// 13,797 rows at V = 151936.  Each GPU holds its own copy for the life of the
+// process; its address is looked up once per device with
+// hipGetSymbolAddress (the array's name is a host-side stand-in and is never
+// passed to a kernel).  Phase 1 writes every entry phase 2 reads, so nothing
+// needs clearing between calls.  Calls that overlap on one GPU share the
+// array and race.
+constexpr long long kNoAllocStats = 262144;
+static __device__ __align__(256) float2 scratch[kNoAllocStats];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float2* g_scratch[kMaxDevices] = {};
+
+// The current device's address of `scratch` (looked up on first use).
+hipError_t scratch_address(float2** out) {
+  int dev = 0;
+  LLMT_HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error("llmt_cross_entropy_noalloc: device %d outside the %d supported", dev, kMaxDevices);
+    return hipErrorInvalidDevice;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    LLMT_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    g_scratch[dev] = static_cast<float2*>(p);
+  }
+  *out = g_scratch[dev];
+  return hipSuccess;
+}
+}  // namespace
+
 }  // namespace llmt
+
+extern "C" int llmt_cross_entropy_noalloc(const float* logits, const int* targets, int rows, int V,
+                                          int seq_len, float* dlogits, float* loss_rows,
+                                          float* loss_mean, void* stream) {
+  using namespace llmt;
+  set_error("");
+  if (!logits || !targets || !loss_rows || rows <= 0 || V <= 0 || V % 4 || seq_len < 2 ||
+      rows % seq_len) {
+    set_error("llmt_cross_entropy_noalloc: bad arguments (V%%4 == 0, rows %% seq_len == 0, "
+              "seq_len >= 2)");
+    return LLMT_ERR_ARG;
+  }
+  const long long need = (long long)rows * ce_chunks(V);
+  if (need > kNoAllocStats) {
+    set_error("llmt_cross_entropy_noalloc: rows x chunks = %d x %d = %lld statistics exceed the "
+              "%lld of the built-in scratch (at most %lld rows at V = %d)",
+              rows, ce_chunks(V), need, kNoAllocStats, kNoAllocStats / ce_chunks(V), V);
+    return LLMT_ERR_ARG;
+  }
+  float2* stats = nullptr;
+  hipError_t e = scratch_address(&stats);
+  if (e == hipSuccess)
+    e = cross_entropy(logits, targets, rows, V, seq_len, stats, dlogits, nullptr, loss_rows,
+                      loss_mean, (hipStream_t)stream);
+  return e == hipSuccess ? LLMT_OK : (e == hipErrorInvalidValue ? LLMT_ERR_ARG : LLMT_ERR_HIP);
+}
