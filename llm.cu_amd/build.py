@@ -39,8 +39,10 @@ def _sources():
     return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
 
 
-# Per-file additions.  attn.hip: MFMA results and accumulators in ordinary
-# VGPRs (its softmax works on every score, so AGPR copies cost VALU slots).
+# Per-file additions.  attn.hip (the attention forward): MFMA results and
+# accumulators in ordinary VGPRs (its softmax works on every score, so AGPR
+# copies cost VALU slots).  The backward (attn_bwd.hip) keeps its dK/dV
+# accumulators in AGPRs.
 EXTRA = {"attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 

@@ -221,11 +221,10 @@ int llmt_attention_bwd(const void* q, const void* k, const void* v, const void* 
   Temps tmp(st);
   float* delta = tmp.get<float>((size_t)B * nq * S);
   float* dsc = tmp.get<float>((size_t)T * nq);
-  float* dkvp = tmp.get<float>((size_t)T * 2 * nq * kHeadDim);
   _Float16* dO16 = tmp.get<_Float16>((size_t)T * nq * kHeadDim);
-  TRY_ARG(delta && dsc && dkvp && dO16, "llmt_attention_bwd: out of memory");
+  TRY_ARG(delta && dsc && dO16, "llmt_attention_bwd: out of memory");
   const long long ldq = (long long)nq * kHeadDim, ldkv = (long long)nkv * kHeadDim;
-  TRY_HIP(attn_delta(dout, ldq, (const _Float16*)o, ldq, nq, S, T, delta, dO16, ldq, dsc, st));
+  TRY_HIP(attn_delta(dout, 0, ldq, (const _Float16*)o, ldq, nq, S, T, delta, dO16, ldq, dsc, st));
   AttnArgs a{};
   a.q = (const _Float16*)q;
   a.ldq = ldq;
@@ -244,7 +243,6 @@ int llmt_attention_bwd(const void* q, const void* k, const void* v, const void* 
   a.delta = delta;
   a.dq = dq;
   a.ldgq = ldq;
-  a.dkvp = dkvp;
   a.dk = dk;
   a.dv = dv;
   a.ldgkv = ldkv;
@@ -252,6 +250,10 @@ int llmt_attention_bwd(const void* q, const void* k, const void* v, const void* 
   return LLMT_OK;
 }
 
+// Config C3 on the caller's layouts, no copies: per-head QK-norm + RoPE of
+// q_raw / k_raw, flash forward (v read in place), dO operand from the fp16
+// dout, flash backward (dv written in place), QK-norm + RoPE backward into
+// dq_raw / dk_raw.
 int llmt_attention_block_bwd(const void* q_raw, const void* k_raw, const void* v,
                              const float* q_norm, const float* k_norm, const void* dout,
                              float* dq_raw, float* dk_raw, float* dv, int B, int S, int nq,
@@ -261,42 +263,31 @@ int llmt_attention_block_bwd(const void* q_raw, const void* k_raw, const void* v
               attn_shape_ok(B, S, nq, nkv),
           "llmt_attention_block_bwd: bad arguments");
   hipStream_t st = (hipStream_t)stream;
-  const int T = B * S, Q = nq * kHeadDim, KV = nkv * kHeadDim, NT = Q + 2 * KV;
+  const int T = B * S, Q = nq * kHeadDim, KV = nkv * kHeadDim;
   Temps tmp(st);
-  _Float16* raw16 = tmp.get<_Float16>((size_t)T * NT);
-  _Float16* qkv16 = tmp.get<_Float16>((size_t)T * NT);
-  float* qkraw = tmp.get<float>((size_t)T * (Q + KV));
+  _Float16* q16 = tmp.get<_Float16>((size_t)T * Q);
+  _Float16* k16 = tmp.get<_Float16>((size_t)T * KV);
   _Float16* o16 = tmp.get<_Float16>((size_t)T * Q);
   float* lse = tmp.get<float>((size_t)B * nq * S);
-  float* dO = tmp.get<float>((size_t)T * Q);
   float* delta = tmp.get<float>((size_t)B * nq * S);
   float* dsc = tmp.get<float>((size_t)T * nq);
-  float* dqkv = tmp.get<float>((size_t)T * NT);
-  float* dkvp = tmp.get<float>((size_t)T * 2 * Q);
   _Float16* dO16 = tmp.get<_Float16>((size_t)T * Q);
-  float* dy = tmp.get<float>((size_t)T * NT);
-  _Float16* g16 = tmp.get<_Float16>((size_t)T * NT);
-  float* rinv = tmp.get<float>(T);
+  float* dq = tmp.get<float>((size_t)T * Q);
+  float* dk = tmp.get<float>((size_t)T * KV);
   float* cosT = tmp.get<float>((size_t)S * 64);
   float* sinT = tmp.get<float>((size_t)S * 64);
-  TRY_ARG(raw16 && qkv16 && qkraw && o16 && lse && dO && delta && dsc && dqkv && dkvp && dO16 &&
-              dy && g16 && rinv && cosT && sinT,
+  TRY_ARG(q16 && k16 && o16 && lse && delta && dsc && dO16 && dq && dk && cosT && sinT,
           "llmt_attention_block_bwd: out of memory");
   TRY_HIP(rope_tables(S, (double)theta, cosT, sinT, st));
-  // [q_raw | k_raw | v] rows
-  TRY_HIP(hipMemcpy2DAsync(raw16, NT * 2, q_raw, Q * 2, Q * 2, T, hipMemcpyDeviceToDevice, st));
-  TRY_HIP(hipMemcpy2DAsync(raw16 + Q, NT * 2, k_raw, KV * 2, KV * 2, T, hipMemcpyDeviceToDevice, st));
-  TRY_HIP(hipMemcpy2DAsync(raw16 + Q + KV, NT * 2, v, KV * 2, KV * 2, T, hipMemcpyDeviceToDevice,
-                           st));
-  TRY_HIP(f16_to_f32_rows(raw16, NT, T, Q + KV, qkraw, Q + KV, st));
-  TRY_HIP(qk_norm_rope(raw16, q_norm, k_norm, cosT, sinT, S, nq, nkv, eps, T, qkv16, st));
+  TRY_HIP(head_norm_rope((const _Float16*)q_raw, q_norm, cosT, sinT, S, nq, T, eps, q16, st));
+  TRY_HIP(head_norm_rope((const _Float16*)k_raw, k_norm, cosT, sinT, S, nkv, T, eps, k16, st));
   AttnArgs a{};
-  a.q = qkv16;
-  a.ldq = NT;
-  a.k = qkv16 + Q;
-  a.ldk = NT;
-  a.v = qkv16 + Q + KV;
-  a.ldv = NT;
+  a.q = q16;
+  a.ldq = Q;
+  a.k = k16;
+  a.ldk = KV;
+  a.v = (const _Float16*)v;
+  a.ldv = KV;
   a.nq = nq;
   a.nkv = nkv;
   a.S = S;
@@ -305,38 +296,21 @@ int llmt_attention_block_bwd(const void* q_raw, const void* k_raw, const void* v
   a.ldo = Q;
   a.lse = lse;
   TRY_HIP(attn_fwd(a, B, st));
-  TRY_HIP(f16_to_f32_rows((const _Float16*)dout, Q, T, Q, dO, Q, st));
-  TRY_HIP(attn_delta(dO, Q, o16, Q, nq, S, T, delta, dO16, Q, dsc, st));
+  TRY_HIP(attn_delta(dout, 1, Q, o16, Q, nq, S, T, delta, dO16, Q, dsc, st));
   a.dO16 = dO16;
   a.ld16 = Q;
   a.dsc = dsc;
   a.delta = delta;
-  a.dq = dqkv;
-  a.ldgq = NT;
-  a.dkvp = dkvp;
-  a.dk = nullptr;  // qk_bwd sums the per-query-head shares
-  a.dv = nullptr;
+  a.dq = dq;
+  a.ldgq = Q;
+  a.dk = dk;
+  a.dv = dv;
+  a.ldgkv = KV;
   TRY_HIP(attn_bwd(a, B, st));
-  QkBwdArgs qb{};
-  qb.dqkv = dqkv;
-  qb.ld_dqkv = NT;
-  qb.dkvp = dkvp;
-  qb.qkraw = qkraw;
-  qb.qn = q_norm;
-  qb.kn = k_norm;
-  qb.cosT = cosT;
-  qb.sinT = sinT;
-  qb.S = S;
-  qb.nq = nq;
-  qb.nkv = nkv;
-  qb.eps = eps;
-  qb.dy32 = dy;
-  qb.g16 = g16;
-  qb.rinv_out = rinv;
-  TRY_HIP(qk_bwd(qb, T, st));
-  TRY_HIP(hipMemcpy2DAsync(dq_raw, Q * 4, dy, NT * 4, Q * 4, T, hipMemcpyDeviceToDevice, st));
-  TRY_HIP(hipMemcpy2DAsync(dk_raw, KV * 4, dy + Q, NT * 4, KV * 4, T, hipMemcpyDeviceToDevice, st));
-  TRY_HIP(hipMemcpy2DAsync(dv, KV * 4, dy + Q + KV, NT * 4, KV * 4, T, hipMemcpyDeviceToDevice, st));
+  TRY_HIP(head_norm_rope_bwd(dq, (const _Float16*)q_raw, q_norm, cosT, sinT, S, nq, T, eps, dq_raw,
+                             st));
+  TRY_HIP(head_norm_rope_bwd(dk, (const _Float16*)k_raw, k_norm, cosT, sinT, S, nkv, T, eps,
+                             dk_raw, st));
   return LLMT_OK;
 }
 

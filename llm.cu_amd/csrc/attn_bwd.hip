@@ -1,0 +1,447 @@
+// attn_bwd.hip — the deterministic causal GQA flash-attention backward
+// (head_dim 128) on fp16 MFMA for gfx950, recomputing P from Q, K and the
+// forward's log-sum-exp.  Two kinds of workgroups that share no outputs:
+//   dQ blocks   (query block, query head): dQ = dS K / sqrt(128), each query
+//               row in its own dO scale;
+//   dK/dV blocks (key block, KV head): dK = dS^T Q / sqrt(128), dV = P^T dO
+//               summed over the query heads of the KV head's GQA group inside
+//               the workgroup (heads, then query tiles, in a fixed order; no
+//               atomics, no per-head partial results in memory).
+// Small grids run both kinds side by side in one launch; large ones as one
+// launch each.  dO arrives as fp16 rows each scaled by its own power of two
+// (the producer writes the inverse scales): dK/dV, which mix rows, bring each
+// row to the group's common scale on the fly.
+//
+// Replaces the reference's attn_backward_kernel (src/kernels/lora_backward.cu:
+// 104-186, float atomics) and its GQA contraction (:189-208).  Math:
+// dP = dO V^T; dS = P (dP - delta), delta = rowsum(dO * O); dQ = dS K / sqrt(d);
+// dK = dS^T Q / sqrt(d); dV = P^T dO.  Query head h reads KV head
+// h / (nq / nkv) (include/config.h:15).  Tile layout, DMA and fragment
+// conventions: attn_common.h.
+#include <algorithm>
+
+#include "attn_common.h"
+
+namespace llmt {
+
+namespace {
+
+// ---------------------------------------------------------------- dQ
+// dS^T for one 64-key tile: dp (rows key, column query) = dP^T in, dS^T out.
+template <int RW, bool MASK>
+__device__ __forceinline__ void ds_tile_q(const floatx4 (&pt)[RW][4], floatx4 (&dp)[RW][4],
+                                          const float (&lse2)[RW], const float (&del)[RW],
+                                          float sl2, int key0, int q0, int S, int lane) {
+  const int c = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int q = q0 + 16 * r + c;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float pv = __builtin_amdgcn_exp2f(fmaf(pt[r][mt][v], sl2, -lse2[r]));
+        if (MASK) {
+          const int key = key0 + mt * 16 + 4 * g + v;
+          pv = (key <= q && key < S && q < S) ? pv : 0.f;
+        }
+        dp[r][mt][v] = pv * (dp[r][mt][v] - del[r]);
+      }
+  }
+}
+
+// Query block qb of head h, batch b: the forward's tiling (LDS: two
+// buffers of K and V tiles, 4 TILE halves).  dQ row q depends on dO row q
+// only, so each row stays in its own dO scale 1 / dsc[q] throughout.
+template <int NW, int RW>
+__device__ __forceinline__ void dq_block(const AttnArgs& a, _Float16* smem, int qb, int h, int b) {
+  constexpr int QB = NW * RW * 16;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, g = lane >> 4;
+  const int S = a.S;
+  const int kvh = h / (a.nq / a.nkv);
+  const long long rowb = (long long)b * S;
+  const int q0 = qb * QB + w * RW * 16;
+  const int qlast = min(q0 + RW * 16, S) - 1;
+  const float sl2 = a.sm_scale * LOG2E;
+  const _Float16* kbase = a.k + rowb * a.ldk + kvh * HD;
+  const _Float16* vbase = a.v + rowb * a.ldv + kvh * HD;
+  const int nkb = min((qb * QB + QB - 1) / BLK, (S - 1) / BLK) + 1;
+  TileDma<NW> dk, dv;
+  dk.init(a.ldk, w);
+  dv.init(a.ldv, w);
+  dk.issue(kbase, a.ldk, 0, S, smem, w);
+  dv.issue(vbase, a.ldv, 0, S, smem + TILE, w);
+  half8 qf[RW][4], df[RW][4];
+  float lse2[RW], del[RW], fq[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int q = q0 + 16 * r + c;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      qf[r][ks] = frag_global(a.q + rowb * a.ldq + h * HD, a.ldq, q, S, ks, lane);
+      df[r][ks] = frag_global(a.dO16 + rowb * a.ld16 + h * HD, a.ld16, q, S, ks, lane);
+    }
+    const bool ok = q < S;
+    lse2[r] = ok ? a.lse[((long long)b * a.nq + h) * S + q] * LOG2E : 0.f;
+    const float dsc = ok ? a.dsc[((long long)b * a.nq + h) * S + q] : 0.f;
+    del[r] = dsc > 0.f ? a.delta[((long long)b * a.nq + h) * S + q] / dsc : 0.f;
+    fq[r] = a.sm_scale * dsc;
+  }
+  floatx4 dqT[RW][8];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dqT[r][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  for (int kb = 0; kb < nkb; ++kb) {
+    wait_vm<0>();
+    tile_barrier();
+    if (kb + 1 < nkb) {
+      _Float16* nb = smem + ((kb + 1) & 1) * 2 * TILE;
+      dk.issue(kbase, a.ldk, (kb + 1) * BLK, S, nb, w);
+      dv.issue(vbase, a.ldv, (kb + 1) * BLK, S, nb + TILE, w);
+    }
+    if (kb * BLK > qlast) continue;
+    const _Float16* Ks = smem + (kb & 1) * 2 * TILE;
+    const _Float16* Vs = Ks + TILE;
+    floatx4 pt[RW][4], dp[RW][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        pt[r][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+        dp[r][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const half8 kf = frag_rm(Ks, mt * 16, ks, lane);
+        const half8 vf = frag_rm(Vs, mt * 16, ks, lane);
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+          pt[r][mt] = mfma16(kf, qf[r][ks], pt[r][mt]);
+          dp[r][mt] = mfma16(vf, df[r][ks], dp[r][mt]);
+        }
+      }
+    }
+    if (kb * BLK + BLK - 1 <= q0 && kb * BLK + BLK <= S && qlast == q0 + RW * 16 - 1)
+      ds_tile_q<RW, false>(pt, dp, lse2, del, sl2, kb * BLK, q0, S, lane);
+    else
+      ds_tile_q<RW, true>(pt, dp, lse2, del, sl2, kb * BLK, q0, S, lane);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      half8 db[RW];
+#pragma unroll
+      for (int r = 0; r < RW; ++r) db[r] = pair_frag(dp[r][2 * j], dp[r][2 * j + 1]);
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        const half8 kt = frag_tr(Ks, d * 16, j, lane);
+#pragma unroll
+        for (int r = 0; r < RW; ++r) dqT[r][d] = mfma16(kt, db[r], dqT[r][d]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int q = q0 + 16 * r + c;
+    const float f = fq[r];
+    if (q < S) {
+      float* dq = a.dq + (rowb + q) * a.ldgq + h * HD;
+#pragma unroll
+      for (int d = 0; d < 8; ++d)
+        *reinterpret_cast<float4*>(dq + d * 16 + 4 * g) =
+            make_float4(dqT[r][d][0] * f, dqT[r][d][1] * f, dqT[r][d][2] * f, dqT[r][d][3] * f);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- dK, dV
+// P and dS for 32 queries (half j2 of a 64-query tile; rows query, column
+// key), both in the group's dO scale gs: ds arrives in each query row's own
+// dO scale, so row q's factor r = gs * dsc[q] (<= 1) brings dP there, and P
+// times r is the operand against the row-scaled dO16 of dV.
+template <bool MASK>
+__device__ __forceinline__ void ds_half_kv(floatx4 (&p)[2], floatx4 (&ds)[2], const float* lse_s,
+                                           const float* del_s, const float* dsc_s, float sl2,
+                                           float gs, int qq0, int j2, int key, int S, int lane) {
+  const int g = lane >> 4;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int r0 = (2 * j2 + u) * 16 + 4 * g;
+    const float4 ls = *reinterpret_cast<const float4*>(lse_s + r0);
+    const float4 dl = *reinterpret_cast<const float4*>(del_s + r0);
+    const float4 sc = *reinterpret_cast<const float4*>(dsc_s + r0);
+    const float lv[4] = {ls.x, ls.y, ls.z, ls.w};
+    const float dv[4] = {dl.x, dl.y, dl.z, dl.w};
+    const float rv[4] = {sc.x * gs, sc.y * gs, sc.z * gs, sc.w * gs};
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float pv = __builtin_amdgcn_exp2f(fmaf(p[u][v], sl2, -lv[v] * LOG2E));
+      if (MASK) {
+        const int qq = qq0 + r0 + v;
+        pv = (key <= qq && qq < S) ? pv : 0.f;
+      }
+      p[u][v] = pv * rv[v];
+      ds[u][v] = pv * fmaf(ds[u][v], rv[v], -dv[v] * gs);
+    }
+  }
+}
+
+// Common power-of-two scale of the fp16 dO rows of the query heads of KV
+// head j in batch b: the reciprocal of their largest inverse row scale
+// (all-zero rows store 0), 1 when every row is zero.  Identical in every
+// workgroup of (b, j).  Row t enters the products times r_t = gs * dsc[t]
+// <= 1, which brings it to this common scale.
+template <int NT>
+__device__ float group_do_scale(const float* __restrict__ dsc, int b, int nq, int j, int group,
+                                int S, float* red) {
+  const float* base = dsc + ((long long)b * nq + (long long)j * group) * S;
+  float m = 0.f;
+  for (int s = threadIdx.x; s < group * S; s += NT) m = fmaxf(m, base[s]);
+  m = block_max<NT / 64>(m, red);
+  return m > 0.f ? 1.0f / m : 1.0f;
+}
+
+constexpr int KV_BUF = 2 * TILE + 3 * BLK * 2;  // halves per dK/dV LDS buffer
+
+// Workgroup (key block kb of 16 KW NW keys, KV head j, batch b).  Wave w
+// owns the keys k0 = kb 16 KW NW + 16 KW w .. as KW 16-key tiles (every Q
+// and dO fragment read from LDS feeds KW MFMAs) and runs over the query
+// heads of the group and, for each, the 64-query tiles at or after the
+// block, in two 32-query halves (P and dS of one half live at a time).
+// The kernels use KW = 1: measured at B4 x S2048, one tile a wave at two
+// waves per SIMD (184 VGPRs) takes 292 us, two tiles at one wave per SIMD
+// (460 registers) 424 us.
+// LDS: two buffers of (Q tile, dO16 tile, lse[64], delta[64], dsc[64]); the
+// next (head, tile) lands while the current one is computed.
+template <int NW, int KW>
+__device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* smem, float* red, int kb,
+                                           int j, int b) {
+  constexpr int NT = NW * 64, KB = NW * 16 * KW;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  const int S = a.S, group = a.nq / a.nkv;
+  const long long rowb = (long long)b * S;
+  const int k0 = kb * KB + w * 16 * KW;
+  const float sl2 = a.sm_scale * LOG2E;
+  const int qb0 = (kb * KB) / BLK;
+  const int nqt = (S + BLK - 1) / BLK - qb0;  // query tiles per head
+  const int niter = group * nqt;
+  TileDma<NW> dq_, dd_;
+  dq_.init(a.ldq, w);
+  dd_.init(a.ld16, w);
+  auto issue = [&](int it, _Float16* buf) {
+    const int h = j * group + it / nqt, qb = qb0 + it % nqt;
+    dq_.issue(a.q + rowb * a.ldq + h * HD, a.ldq, qb * BLK, S, buf, w);
+    dd_.issue(a.dO16 + rowb * a.ld16 + h * HD, a.ld16, qb * BLK, S, buf + TILE, w);
+    float* vec = reinterpret_cast<float*>(buf + 2 * TILE);
+    const long long bh = ((long long)b * a.nq + h) * S;
+    if (w == 0) dma_vec64(a.lse + bh, qb * BLK, S, vec);
+    if (w == NW - 1) dma_vec64(a.delta + bh, qb * BLK, S, vec + BLK);
+    if (w == NW / 2) dma_vec64(a.dsc + bh, qb * BLK, S, vec + 2 * BLK);
+  };
+  issue(0, smem);
+  const float gs = group_do_scale<NT>(a.dsc, b, a.nq, j, group, S, red);
+  half8 kf[KW][4], vf[KW][4];
+#pragma unroll
+  for (int t = 0; t < KW; ++t)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      kf[t][ks] = frag_global(a.k + rowb * a.ldk + j * HD, a.ldk, k0 + 16 * t + c, S, ks, lane);
+      vf[t][ks] = frag_global(a.v + rowb * a.ldv + j * HD, a.ldv, k0 + 16 * t + c, S, ks, lane);
+    }
+  floatx4 dkT[KW][8], dvT[KW][8];
+#pragma unroll
+  for (int t = 0; t < KW; ++t)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      dkT[t][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+      dvT[t][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+  for (int it = 0; it < niter; ++it) {
+    wait_vm<0>();
+    tile_barrier();
+    if (it + 1 < niter) issue(it + 1, smem + ((it + 1) & 1) * KV_BUF);
+    const _Float16* buf = smem + (it & 1) * KV_BUF;
+    const int qb = qb0 + it % nqt;
+    if (qb * BLK + BLK - 1 < k0) continue;  // every query before every key of the wave
+    const _Float16* Qs = buf;
+    const _Float16* Ds = buf + TILE;
+    const float* lse_s = reinterpret_cast<const float*>(buf + 2 * TILE);
+    const float* del_s = lse_s + BLK;
+    const float* dsc_s = lse_s + 2 * BLK;
+    // every query of the tile >= every key of the wave and < S: no mask
+    const bool full = qb * BLK >= k0 + 16 * KW - 1 && qb * BLK + BLK <= S;
+#pragma unroll
+    for (int j2 = 0; j2 < 2; ++j2) {  // queries 32 j2 .. 32 j2 + 31 of the tile
+      floatx4 p[KW][2], ds[KW][2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int mt = 2 * j2 + u;
+#pragma unroll
+        for (int t = 0; t < KW; ++t) {
+          p[t][u] = floatx4{0.f, 0.f, 0.f, 0.f};
+          ds[t][u] = floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const half8 qf = frag_rm(Qs, mt * 16, ks, lane);
+          const half8 df = frag_rm(Ds, mt * 16, ks, lane);
+#pragma unroll
+          for (int t = 0; t < KW; ++t) {
+            p[t][u] = mfma16(qf, kf[t][ks], p[t][u]);
+            ds[t][u] = mfma16(df, vf[t][ks], ds[t][u]);
+          }
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < KW; ++t) {
+        if (full)
+          ds_half_kv<false>(p[t], ds[t], lse_s, del_s, dsc_s, sl2, gs, qb * BLK, j2,
+                            k0 + 16 * t + c, S, lane);
+        else
+          ds_half_kv<true>(p[t], ds[t], lse_s, del_s, dsc_s, sl2, gs, qb * BLK, j2,
+                           k0 + 16 * t + c, S, lane);
+      }
+      half8 pb[KW], db[KW];
+#pragma unroll
+      for (int t = 0; t < KW; ++t) {
+        pb[t] = pair_frag(p[t][0], p[t][1]);
+        db[t] = pair_frag(ds[t][0], ds[t][1]);
+      }
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const half8 dtr = frag_tr(Ds, dt * 16, j2, lane);
+        const half8 qtr = frag_tr(Qs, dt * 16, j2, lane);
+#pragma unroll
+        for (int t = 0; t < KW; ++t) {
+          dvT[t][dt] = mfma16(dtr, pb[t], dvT[t][dt]);
+          dkT[t][dt] = mfma16(qtr, db[t], dkT[t][dt]);
+        }
+      }
+    }
+  }
+  const float inv = 1.0f / gs;
+  const float fk = a.sm_scale * inv;
+#pragma unroll
+  for (int t = 0; t < KW; ++t) {
+    const int key = k0 + 16 * t + c;
+    if (key < S) {
+      float* dk = a.dk + (rowb + key) * a.ldgkv + j * HD;
+      float* dv = a.dv + (rowb + key) * a.ldgkv + j * HD;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        *reinterpret_cast<float4*>(dk + dt * 16 + 4 * g) =
+            make_float4(dkT[t][dt][0] * fk, dkT[t][dt][1] * fk, dkT[t][dt][2] * fk,
+                        dkT[t][dt][3] * fk);
+        *reinterpret_cast<float4*>(dv + dt * 16 + 4 * g) =
+            make_float4(dvT[t][dt][0] * inv, dvT[t][dt][1] * inv, dvT[t][dt][2] * inv,
+                        dvT[t][dt][3] * inv);
+      }
+    }
+  }
+}
+
+// The attention backward of a launch over a flat grid (x, B): x < nkv nkvb
+// are dK/dV blocks (key block x / nkv, KV head x % nkv: the longest key
+// blocks first), the next nq nqb dQ blocks (the last, i.e. longest, query
+// blocks first).  PART 0: both kinds; 1: dK/dV only; 2: dQ only -- the
+// one-kind forms keep their own (smaller) register and LDS budgets.
+constexpr int BWD_SMEM = 2 * KV_BUF > 4 * TILE ? 2 * KV_BUF : 4 * TILE;
+
+template <int NW, int RW, int PART>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void attn_bwd_kernel(const AttnArgs a, int nkvb, int nqb) {
+  constexpr int SMEM = PART == 1 ? 2 * KV_BUF : PART == 2 ? 4 * TILE : BWD_SMEM;
+  __shared__ __attribute__((aligned(1024))) _Float16 smem[SMEM];
+  __shared__ float red[NW];
+  const int x = blockIdx.x, b = blockIdx.y;
+  const int nkvx = PART == 2 ? 0 : nkvb * a.nkv;
+  if constexpr (PART != 2) {
+    if (x < nkvx) {
+      dkdv_block<NW, 1>(a, smem, red, x / a.nkv, x % a.nkv, b);
+      return;
+    }
+  }
+  if constexpr (PART != 1) {
+    const int y = x - nkvx;
+    dq_block<NW, RW>(a, smem, nqb - 1 - y / a.nq, y % a.nq, b);
+  }
+}
+
+int dkdv_waves(int B, int S, int nkv) {
+  const char* e = getenv("LLMT_ATTN_DKDV_WAVES");
+  if (e && (e[0] == '2' || e[0] == '4') && !e[1]) return e[0] - '0';
+  return (long long)B * nkv * ((S + 63) / 64) >= 256 ? 4 : 2;
+}
+
+template <int NW, int RW, int PART>
+void launch_bwd(const AttnArgs& a, int B, int nkvb, int nqb, hipStream_t st) {
+  const int nx = (PART == 2 ? 0 : nkvb * a.nkv) + (PART == 1 ? 0 : nqb * a.nq);
+  hipLaunchKernelGGL((attn_bwd_kernel<NW, RW, PART>), dim3(nx, B), dim3(NW * 64), 0, st, a, nkvb,
+                     nqb);
+}
+
+// dK/dV key blocks of nwk waves and dQ query blocks of nwq waves x rw tiles:
+// one launch when the wave counts agree and the grid is small (under 2048
+// workgroups: a second launch would mostly wait on the first one's tail),
+// else one launch each.
+void launch_attn_bwd(const AttnArgs& a, int B, int nwk, int nwq, int rw, hipStream_t st) {
+  const int nkvb = (a.S + nwk * 16 - 1) / (nwk * 16);
+  const int nqb = (a.S + nwq * rw * 16 - 1) / (nwq * rw * 16);
+  const bool small = ((long long)nkvb * a.nkv + (long long)nqb * a.nq) * B < 2048;
+  if (nwk == nwq && small) {
+    switch (nwq * 10 + rw) {
+      case 42: launch_bwd<4, 2, 0>(a, B, nkvb, nqb, st); break;
+      case 41: launch_bwd<4, 1, 0>(a, B, nkvb, nqb, st); break;
+      case 22: launch_bwd<2, 2, 0>(a, B, nkvb, nqb, st); break;
+      case 11: launch_bwd<1, 1, 0>(a, B, nkvb, nqb, st); break;
+      default: launch_bwd<2, 1, 0>(a, B, nkvb, nqb, st); break;
+    }
+    return;
+  }
+  // dQ first: its sweep leaves Q, K, V and dO warm for the dK/dV launch
+  switch (nwq * 10 + rw) {
+    case 42: launch_bwd<4, 2, 2>(a, B, 0, nqb, st); break;
+    case 41: launch_bwd<4, 1, 2>(a, B, 0, nqb, st); break;
+    case 22: launch_bwd<2, 2, 2>(a, B, 0, nqb, st); break;
+    case 11: launch_bwd<1, 1, 2>(a, B, 0, nqb, st); break;
+    default: launch_bwd<2, 1, 2>(a, B, 0, nqb, st); break;
+  }
+  if (nwk == 4)
+    launch_bwd<4, 1, 1>(a, B, nkvb, 0, st);
+  else if (nwk == 1)
+    launch_bwd<1, 1, 1>(a, B, nkvb, 0, st);
+  else
+    launch_bwd<2, 1, 1>(a, B, nkvb, 0, st);
+}
+
+}  // namespace
+
+hipError_t attn_bwd(const AttnArgs& a, int B, hipStream_t st) {
+  if (a.nq % a.nkv || a.S <= 0 || !a.dO16 || !a.dsc || !a.dk || !a.dv) {
+    set_error("attn_bwd: nq=%d nkv=%d S=%d (fp16 dO, its scales and dK/dV outputs required)",
+              a.nq, a.nkv, a.S);
+    return hipErrorInvalidValue;
+  }
+  // dQ holds twice the accumulators of the forward: one 16-row tile a wave
+  // keeps two waves per SIMD, measured faster at every S; LLMT_ATTN_CFG
+  // still selects any shape for tuning.
+  AttnShape s = attn_shape(B, a.S, a.nq);
+  int nwk = dkdv_waves(B, a.S, a.nkv);
+  if (!getenv("LLMT_ATTN_CFG")) {
+    s.rw = 1;
+    // tiny grids (the B1 x S128 step: 8 KV heads x 2 key blocks): one-wave
+    // workgroups, so the few key blocks of each GQA group spread wider
+    if (!getenv("LLMT_ATTN_DKDV_WAVES") && (long long)B * a.nq * ((a.S + 63) / 64) < 64)
+      s.nw = nwk = 1;
+  }
+  launch_attn_bwd(a, B, nwk, s.nw, s.rw, st);
+  LLMT_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+}  // namespace llmt

@@ -195,7 +195,6 @@ int Ctx::init() {
   TRY_PTR(delta = alloc_n<float>((size_t)maxB * nq * S));
   TRY_PTR(dsc = alloc_n<float>((size_t)maxB * nq * S));
   TRY_PTR(dqkv32 = alloc_n<float>(T * NT));
-  TRY_PTR(dkvp = alloc_n<float>((size_t)T * 2 * Q));
   TRY_PTR(dO16 = alloc_n<_Float16>((size_t)T * Q));
   TRY_PTR(gq16_all = alloc_n<_Float16>((size_t)L * T * NT));
   TRY_PTR(rq_all = alloc_n<float>((size_t)L * T));

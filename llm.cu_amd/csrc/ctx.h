@@ -148,7 +148,6 @@ struct Ctx {
   LoraGradJob* lora_jobs = nullptr;  // device [L][kLoraJobs]
   LoraGradPlan lora_plan{};
   hipError_t lora_grads(int l0, int nl, int B, int accumulate);
-  float* dkvp = nullptr;  // [T, 2 Q]: per-query-head dK | dV shares
   _Float16* dO16 = nullptr;  // [T, Q]: row-scaled fp16 dO of the attention backward
 
   // graph + profiling

@@ -161,8 +161,6 @@ struct NormBwdArgs {
 struct QkBwdArgs {
   const float* dqkv;  // attention grads [T, ld] (dq | dk | dv)
   int ld_dqkv;
-  const float* dkvp;  // if set: dk, dv are the group sums of these per-query-head shares
-                      // [T, 2 nq 128] (attn_bwd's dkvp) instead of dqkv's columns
   const float* qkraw;
   const float* qn;
   const float* kn;
@@ -185,9 +183,13 @@ hipError_t resid_norm(const RowIn& in, const float* x_res, const float* w, float
                       float* x_out, _Float16* xn, hipStream_t st);
 // cos / sin tables of the half-split RoPE, [S, 64] fp32 each, on the device.
 hipError_t rope_tables(int S, double theta, float* cosT, float* sinT, hipStream_t st);
-hipError_t qk_norm_rope(const _Float16* raw, const float* qn, const float* kn, const float* cosT,
-                        const float* sinT, int S, int nq, int nkv, float eps, int T, _Float16* out,
-                        hipStream_t st);
+// Per-head QK-RMSNorm + RoPE of [T, nh, 128] fp16 rows (weights w [128]),
+// and its backward from dy fp32 [T, nh, 128] to dx fp32 (x: the raw rows).
+hipError_t head_norm_rope(const _Float16* x, const float* w, const float* cosT, const float* sinT,
+                          int S, int nh, int T, float eps, _Float16* out, hipStream_t st);
+hipError_t head_norm_rope_bwd(const float* dy, const _Float16* x, const float* w,
+                              const float* cosT, const float* sinT, int S, int nh, int T,
+                              float eps, float* dx, hipStream_t st);
 hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st);
 hipError_t swiglu_bwd(const RowIn& in, const float* rinv_in, const float* gu, int I, int T,
                       _Float16* dgu16, float* rinv_out, hipStream_t st);
@@ -232,19 +234,18 @@ struct AttnArgs {
   const float* delta;   // [B, nq, S] rowsum(dO * O)
   float* dq;            // fp32 [T, ldgq]
   long long ldgq;
-  float* dkvp;          // [T, 2 nq 128]: each query head's share of dK | dV
-  float* dk;            // optional: dK, dV summed over each GQA group,
-  float* dv;            //   fp32 [T, ldgkv] (NULL: the consumer sums dkvp)
+  float* dk;            // dK, dV (summed over each GQA group) fp32 [T, ldgkv]
+  float* dv;
   long long ldgkv;
 };
 hipError_t attn_fwd(const AttnArgs& a, int B, hipStream_t st);
 hipError_t attn_bwd(const AttnArgs& a, int B, hipStream_t st);
-// Operands of a standalone attention backward from dO fp32 [T, ldd] and O
-// fp16 [T, ldo]: delta[b, h, s] = sum_d dO * O, dO16 [T, ld16] and dsc as
-// o_dx_post writes them.
-hipError_t attn_delta(const float* dO, long long ldd, const _Float16* o, long long ldo, int nq,
-                      int S, int T, float* delta, _Float16* dO16, long long ld16, float* dsc,
-                      hipStream_t st);
+// Operands of a standalone attention backward from dO [T, ldd] (fp32, or
+// fp16 with dO_is_f16) and O fp16 [T, ldo]: delta[b, h, s] = sum_d dO * O,
+// dO16 [T, ld16] and dsc as o_dx_post writes them.
+hipError_t attn_delta(const void* dO, int dO_is_f16, long long ldd, const _Float16* o,
+                      long long ldo, int nq, int S, int T, float* delta, _Float16* dO16,
+                      long long ld16, float* dsc, hipStream_t st);
 
 // ---------------------------------------------------------------- LoRA / AdamW
 struct LoraGradJob {

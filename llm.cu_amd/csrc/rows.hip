@@ -446,36 +446,48 @@ __global__ __launch_bounds__(RT) void resid_norm_kernel(const RowIn in,
   }
 }
 
-// QK-RMSNorm + RoPE forward from fp16 raw q/k (the standalone attention
-// block of config C3): raw [T, NT] fp16 -> qkv16 [T, NT] fp16, v copied.
-__global__ __launch_bounds__(RT) void qk_norm_rope_kernel(const _Float16* __restrict__ raw,
-                                                          const float* __restrict__ qn,
-                                                          const float* __restrict__ kn,
-                                                          const float* __restrict__ cosT,
-                                                          const float* __restrict__ sinT, int S,
-                                                          int nq, int nkv, float eps,
-                                                          _Float16* __restrict__ out) {
-  const int t = blockIdx.x;
-  const int NT = (nq + 2 * nkv) * HD;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int pos = t % S;
+// Per-head QK-RMSNorm + RoPE on [T, nh, 128] rows (the attention block API's
+// separate q / k inputs; the training step fuses this into qkv_post): one
+// wave per (token, head), lane = RoPE pair (d, d + 64).
+//   forward:  y = rope(x * r * w), r = rsqrt(mean x^2 + eps)
+//   backward: n = rope^T(dy); dx = r (n w - (r^2 / 128) sum(n w x) x)
+// (src/kernels/rmsnorm.cu:6-41, 53-95; src/kernels/rope.cu:7-46, 57-89).
+__global__ __launch_bounds__(RT) void head_norm_rope_kernel(const _Float16* __restrict__ x,
+                                                            const float* __restrict__ w,
+                                                            const float* __restrict__ cosT,
+                                                            const float* __restrict__ sinT, int S,
+                                                            int nh, int T, float eps,
+                                                            _Float16* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const long long row = (long long)blockIdx.x * RW + (threadIdx.x >> 6);  // (token, head)
+  if (row >= (long long)T * nh) return;
+  const int pos = (int)(row / nh) % S;
   const float cs = cosT[pos * (HD / 2) + lane], sn = sinT[pos * (HD / 2) + lane];
-  const _Float16* x = raw + (long long)t * NT;
-  _Float16* o = out + (long long)t * NT;
-  for (int hh = wave; hh < nq + 2 * nkv; hh += RW) {
-    const int base = hh * HD;
-    const float x0 = (float)x[base + lane], x1 = (float)x[base + 64 + lane];
-    if (hh >= nq + nkv) {
-      o[base + lane] = (_Float16)x0;
-      o[base + 64 + lane] = (_Float16)x1;
-      continue;
-    }
-    const float* w = hh < nq ? qn : kn;
-    const float r = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / HD + eps);
-    const float y0 = x0 * r * w[lane], y1 = x1 * r * w[lane + 64];
-    o[base + lane] = (_Float16)(y0 * cs - y1 * sn);
-    o[base + 64 + lane] = (_Float16)(y1 * cs + y0 * sn);
-  }
+  const _Float16* xr = x + row * HD;
+  const float x0 = (float)xr[lane], x1 = (float)xr[lane + 64];
+  const float r = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / HD + eps);
+  const float y0 = x0 * r * w[lane], y1 = x1 * r * w[lane + 64];
+  out[row * HD + lane] = (_Float16)(y0 * cs - y1 * sn);
+  out[row * HD + lane + 64] = (_Float16)(y1 * cs + y0 * sn);
+}
+
+__global__ __launch_bounds__(RT) void head_norm_rope_bwd_kernel(
+    const float* __restrict__ dy, const _Float16* __restrict__ x, const float* __restrict__ w,
+    const float* __restrict__ cosT, const float* __restrict__ sinT, int S, int nh, int T, float eps,
+    float* __restrict__ dx) {
+  const int lane = threadIdx.x & 63;
+  const long long row = (long long)blockIdx.x * RW + (threadIdx.x >> 6);
+  if (row >= (long long)T * nh) return;
+  const int pos = (int)(row / nh) % S;
+  const float cs = cosT[pos * (HD / 2) + lane], sn = sinT[pos * (HD / 2) + lane];
+  const float d0 = dy[row * HD + lane], d1 = dy[row * HD + lane + 64];
+  const float x0 = (float)x[row * HD + lane], x1 = (float)x[row * HD + lane + 64];
+  const float w0 = w[lane], w1 = w[lane + 64];
+  const float n0 = d0 * cs + d1 * sn, n1 = d1 * cs - d0 * sn;
+  const float r = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / HD + eps);
+  const float coef = r * r / HD * wave_sum(n0 * w0 * x0 + n1 * w1 * x1);
+  dx[row * HD + lane] = r * (n0 * w0 - coef * x0);
+  dx[row * HD + lane + 64] = r * (n1 * w1 - coef * x1);
 }
 
 // ---------------------------------------------------------------- backward
@@ -817,32 +829,18 @@ __global__ __launch_bounds__(RT) void o_dx_post_row_kernel(const RowIn in,
 // backward with x = q_raw/k_raw (src/kernels/rmsnorm.cu:53-95) ->
 // dy = [dq_raw | dk_raw | dv] fp32 (the LoRA dB operand) and fp16 (scaled).
 // HPW > 0: every load of a row (a wave's nq + nkv <= HPW RW heads, then
-// KV <= 2 RT v columns; G = the query heads per KV head when K/V come as
-// shares, 0 when not) is issued before any of the math, the shares summed
-// afterwards in the same order (the rows are latency-bound at small T).
-// HPW = 0: one head at a time, any shape.
-template <int HPW, int G>
+// KV <= 2 RT v columns) is issued before any of the math (the rows are
+// latency-bound at small T).  HPW = 0: one head at a time, any shape.
+template <int HPW>
 __global__ __launch_bounds__(RT) void qk_bwd_kernel(const QkBwdArgs a) {
   extern __shared__ float ds[];  // [NT]
   __shared__ float red[2 * RW];
   const int t = blockIdx.x;
   const int Q = a.nq * HD, KV = a.nkv * HD, NT = Q + 2 * KV;
-  const int group = a.nq / a.nkv;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int pos = t % a.S;
   const float cs = a.cosT[pos * (HD / 2) + lane], sn = a.sinT[pos * (HD / 2) + lane];
   const float* g = a.dqkv + (long long)t * a.ld_dqkv;
-  const float* sh = a.dkvp ? a.dkvp + (long long)t * 2 * Q : nullptr;
-  // gradient at column c of [dq | dk | dv] (the K/V ones summed over the
-  // query heads of their group, in order, when given as shares)
-  auto grad = [&](int c) -> float {
-    if (!sh || c < Q) return g[c];
-    const int kv = c < Q + KV ? 0 : 1;
-    const int cc = c - Q - kv * KV, j = cc / HD, d = cc - j * HD;
-    float s = 0.f;
-    for (int gi = 0; gi < group; ++gi) s += sh[(kv * a.nq + j * group + gi) * HD + d];
-    return s;
-  };
   auto head = [&](int hh, float d0, float d1, float x0, float x1, float w0,
                   float w1) __attribute__((always_inline)) {
     const int base = hh * HD;
@@ -855,41 +853,20 @@ __global__ __launch_bounds__(RT) void qk_bwd_kernel(const QkBwdArgs a) {
   };
   const float* xrow = a.qkraw + (long long)t * (Q + KV);
   if constexpr (HPW > 0) {
-    constexpr int NV = G > 0 ? G : 1;  // loads per gradient value
-    // isq: column c is a q column (its NV loads all read g[c]; the address is
-    // a select, not a branch, so no load waits on another)
-    auto load = [&](int c, bool isq, float* v) __attribute__((always_inline)) {
-      if constexpr (G == 0) {
-        v[0] = g[c];
-      } else {
-        const int kv = c < Q + KV ? 0 : 1;
-        const int cc = c - Q - kv * KV, j = cc / HD, d = cc - j * HD;
-#pragma unroll
-        for (int k = 0; k < NV; ++k)
-          v[k] = *(isq ? g + c : sh + (kv * a.nq + j * NV + k) * HD + d);
-      }
-    };
-    auto sum = [&](const float* v, bool isq) __attribute__((always_inline)) {
-      float x = v[0];
-#pragma unroll
-      for (int k = 1; k < NV; ++k)
-        if (!isq) x += v[k];
-      return x;
-    };
     const float wq0 = a.qn[lane], wq1 = a.qn[lane + 64], wk0 = a.kn[lane], wk1 = a.kn[lane + 64];
-    float vv[2][NV];
+    float vv[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int c = Q + KV + threadIdx.x + u * RT;
-      load(c < NT ? c : Q + KV, false, vv[u]);
+      vv[u] = g[c < NT ? c : Q + KV];
     }
-    float d0[HPW][NV], d1[HPW][NV], x0[HPW], x1[HPW];
+    float d0[HPW], d1[HPW], x0[HPW], x1[HPW];
 #pragma unroll
     for (int k = 0; k < HPW; ++k) {
       const int hh = __builtin_amdgcn_readfirstlane(wave + k * RW);
       const int base = (hh < a.nq + a.nkv ? hh : 0) * HD;
-      load(base + lane, base < Q, d0[k]);
-      load(base + 64 + lane, base < Q, d1[k]);
+      d0[k] = g[base + lane];
+      d1[k] = g[base + 64 + lane];
       x0[k] = xrow[base + lane];
       x1[k] = xrow[base + 64 + lane];
     }
@@ -897,24 +874,22 @@ __global__ __launch_bounds__(RT) void qk_bwd_kernel(const QkBwdArgs a) {
     for (int k = 0; k < HPW; ++k)
       if (wave + k * RW < a.nq + a.nkv) {
         const bool isq = wave + k * RW < a.nq;
-        head(wave + k * RW, sum(d0[k], isq), sum(d1[k], isq), x0[k], x1[k], isq ? wq0 : wk0,
-             isq ? wq1 : wk1);
+        head(wave + k * RW, d0[k], d1[k], x0[k], x1[k], isq ? wq0 : wk0, isq ? wq1 : wk1);
       }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int c = Q + KV + threadIdx.x + u * RT;
-      if (c < NT) ds[c] = sum(vv[u], false);
+      if (c < NT) ds[c] = vv[u];
     }
   } else {
     for (int hh = wave; hh < a.nq + a.nkv; hh += RW) {
       const int base = hh * HD;
       const float* w = hh < a.nq ? a.qn : a.kn;
-      head(hh, grad(base + lane), grad(base + 64 + lane), xrow[base + lane], xrow[base + 64 + lane],
+      head(hh, g[base + lane], g[base + 64 + lane], xrow[base + lane], xrow[base + 64 + lane],
            w[lane], w[lane + 64]);
     }
+    for (int c = Q + KV + threadIdx.x; c < NT; c += RT) ds[c] = g[c];
   }
-  if constexpr (HPW == 0)
-    for (int c = Q + KV + threadIdx.x; c < NT; c += RT) ds[c] = grad(c);
   __syncthreads();
   float amax = 0.f;
   for (int c = threadIdx.x; c < NT; c += RT) {
@@ -1142,11 +1117,21 @@ hipError_t rope_tables(int S, double theta, float* cosT, float* sinT, hipStream_
   return hipSuccess;
 }
 
-hipError_t qk_norm_rope(const _Float16* raw, const float* qn, const float* kn, const float* cosT,
-                        const float* sinT, int S, int nq, int nkv, float eps, int T, _Float16* out,
-                        hipStream_t st) {
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(T), dim3(RT), 0, st, raw, qn, kn, cosT, sinT, S, nq,
-                     nkv, eps, out);
+hipError_t head_norm_rope(const _Float16* x, const float* w, const float* cosT, const float* sinT,
+                          int S, int nh, int T, float eps, _Float16* out, hipStream_t st) {
+  const long long rows = (long long)T * nh;
+  hipLaunchKernelGGL(head_norm_rope_kernel, dim3((unsigned)((rows + RW - 1) / RW)), dim3(RT), 0, st,
+                     x, w, cosT, sinT, S, nh, T, eps, out);
+  LLMT_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+hipError_t head_norm_rope_bwd(const float* dy, const _Float16* x, const float* w,
+                              const float* cosT, const float* sinT, int S, int nh, int T,
+                              float eps, float* dx, hipStream_t st) {
+  const long long rows = (long long)T * nh;
+  hipLaunchKernelGGL(head_norm_rope_bwd_kernel, dim3((unsigned)((rows + RW - 1) / RW)), dim3(RT),
+                     0, st, dy, x, w, cosT, sinT, S, nh, T, eps, dx);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
@@ -1231,21 +1216,16 @@ hipError_t o_dx_post(const RowIn& in, const float* rinv_in, const _Float16* o16,
 hipError_t qk_bwd(const QkBwdArgs& a, int T, hipStream_t st) {
   const int NT = (a.nq + 2 * a.nkv) * HD;
   const int hpw = (a.nq + a.nkv + RW - 1) / RW;
-  const int G = a.dkvp ? a.nq / a.nkv : 0;
   const size_t lds = NT * sizeof(float);
   const char* e = getenv("LLMT_QK_BWD_HOIST");
-  const bool hoist = (!e || atoi(e) != 0) && hpw <= 4 && a.nkv * HD <= 2 * RT &&
-                     (G == 0 || G == 1 || G == 2 || G == 4);
-  const int key = hoist ? hpw * 8 + G : 0;
+  const bool hoist = (!e || atoi(e) != 0) && hpw <= 4 && a.nkv * HD <= 2 * RT;
   auto go = [&](auto kern) { hipLaunchKernelGGL(kern, dim3(T), dim3(RT), lds, st, a); };
-  switch (key) {
-#define LLMT_QK_CASE(H, GG) \
-  case H * 8 + GG: go(qk_bwd_kernel<H, GG>); break;
-#define LLMT_QK_CASES(H) LLMT_QK_CASE(H, 0) LLMT_QK_CASE(H, 1) LLMT_QK_CASE(H, 2) LLMT_QK_CASE(H, 4)
-    LLMT_QK_CASES(1) LLMT_QK_CASES(2) LLMT_QK_CASES(3) LLMT_QK_CASES(4)
-#undef LLMT_QK_CASES
-#undef LLMT_QK_CASE
-    default: go(qk_bwd_kernel<0, 0>); break;
+  switch (hoist ? hpw : 0) {
+    case 1: go(qk_bwd_kernel<1>); break;
+    case 2: go(qk_bwd_kernel<2>); break;
+    case 3: go(qk_bwd_kernel<3>); break;
+    case 4: go(qk_bwd_kernel<4>); break;
+    default: go(qk_bwd_kernel<0>); break;
   }
   LLMT_LAUNCH_CHECK();
   return hipSuccess;

@@ -288,9 +288,8 @@ AttnArgs Ctx::attn_args(const Stash& s) const {
   a.delta = delta;
   a.dq = dqkv32;
   a.ldgq = NT;
-  a.dkvp = dkvp;
-  a.dk = nullptr;  // qk_bwd sums the per-query-head shares
-  a.dv = nullptr;
+  a.dk = dqkv32 + Q;
+  a.dv = dqkv32 + Q + KV;
   a.ldgkv = NT;
   return a;
 }
@@ -393,7 +392,6 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   // RoPE + QK-norm backward
   QkBwdArgs qb{};
   qb.dqkv = dqkv32; qb.ld_dqkv = NT;
-  qb.dkvp = dkvp;
   qb.qkraw = s.qkraw;
   qb.qn = w.q_norm; qb.kn = w.k_norm;
   qb.cosT = cosT; qb.sinT = sinT;
