@@ -345,6 +345,130 @@ __device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* smem, fl
   }
 }
 
+// Small grids (the B1 x S128 step: 8 KV heads x 8 key blocks): the NW waves
+// of the workgroup all own the same 16 keys and split the group's
+// (query head, query tile) iterations between them (wave w takes it = w,
+// w + NW, ..), each through two LDS buffers of its own (no barriers in the
+// loop); their dK/dV sums meet in LDS at the end, in wave order.
+template <int NW>
+__device__ __forceinline__ void dkdv_block_split(const AttnArgs& a, _Float16* smem, float* red,
+                                                 int kb, int j, int b) {
+  constexpr int NT = NW * 64;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  const int S = a.S, group = a.nq / a.nkv;
+  const long long rowb = (long long)b * S;
+  const int k0 = kb * 16;
+  const float sl2 = a.sm_scale * LOG2E;
+  const int qb0 = k0 / BLK;
+  const int nqt = (S + BLK - 1) / BLK - qb0;
+  const int niter = group * nqt;
+  _Float16* mine = smem + w * 2 * KV_BUF;
+  TileDma<1> dq_, dd_;
+  dq_.init(a.ldq, 0);
+  dd_.init(a.ld16, 0);
+  auto issue = [&](int it, _Float16* buf) {
+    const int h = j * group + it / nqt, qb = qb0 + it % nqt;
+    dq_.issue(a.q + rowb * a.ldq + h * HD, a.ldq, qb * BLK, S, buf, 0);
+    dd_.issue(a.dO16 + rowb * a.ld16 + h * HD, a.ld16, qb * BLK, S, buf + TILE, 0);
+    float* vec = reinterpret_cast<float*>(buf + 2 * TILE);
+    const long long bh = ((long long)b * a.nq + h) * S;
+    dma_vec64(a.lse + bh, qb * BLK, S, vec);
+    dma_vec64(a.delta + bh, qb * BLK, S, vec + BLK);
+    dma_vec64(a.dsc + bh, qb * BLK, S, vec + 2 * BLK);
+  };
+  if (w < niter) issue(w, mine);
+  const float gs = group_do_scale<NT>(a.dsc, b, a.nq, j, group, S, red);
+  half8 kf[4], vf[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    kf[ks] = frag_global(a.k + rowb * a.ldk + j * HD, a.ldk, k0 + c, S, ks, lane);
+    vf[ks] = frag_global(a.v + rowb * a.ldv + j * HD, a.ldv, k0 + c, S, ks, lane);
+  }
+  floatx4 dkT[8], dvT[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    dkT[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    dvT[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+  int n = 0;
+  for (int it = w; it < niter; it += NW, ++n) {
+    wait_vm<0>();  // this wave's own tile (its buffers are private)
+    asm volatile("" ::: "memory");
+    if (it + NW < niter) issue(it + NW, mine + ((n + 1) & 1) * KV_BUF);
+    const _Float16* buf = mine + (n & 1) * KV_BUF;
+    const int qb = qb0 + it % nqt;
+    if (qb * BLK + BLK - 1 < k0) continue;
+    const _Float16* Qs = buf;
+    const _Float16* Ds = buf + TILE;
+    const float* lse_s = reinterpret_cast<const float*>(buf + 2 * TILE);
+    const float* del_s = lse_s + BLK;
+    const float* dsc_s = lse_s + 2 * BLK;
+    const bool full = qb * BLK >= k0 + 15 && qb * BLK + BLK <= S;
+#pragma unroll
+    for (int j2 = 0; j2 < 2; ++j2) {
+      floatx4 p[2], ds[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int mt = 2 * j2 + u;
+        p[u] = floatx4{0.f, 0.f, 0.f, 0.f};
+        ds[u] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          p[u] = mfma16(frag_rm(Qs, mt * 16, ks, lane), kf[ks], p[u]);
+          ds[u] = mfma16(frag_rm(Ds, mt * 16, ks, lane), vf[ks], ds[u]);
+        }
+      }
+      if (full)
+        ds_half_kv<false>(p, ds, lse_s, del_s, dsc_s, sl2, gs, qb * BLK, j2, k0 + c, S, lane);
+      else
+        ds_half_kv<true>(p, ds, lse_s, del_s, dsc_s, sl2, gs, qb * BLK, j2, k0 + c, S, lane);
+      const half8 pb = pair_frag(p[0], p[1]);
+      const half8 db = pair_frag(ds[0], ds[1]);
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        dvT[dt] = mfma16(frag_tr(Ds, dt * 16, j2, lane), pb, dvT[dt]);
+        dkT[dt] = mfma16(frag_tr(Qs, dt * 16, j2, lane), db, dkT[dt]);
+      }
+    }
+  }
+  // waves 1 .. NW-1 hand their sums to wave 0, which adds them in order
+  wait_vm<0>();
+  __syncthreads();
+  floatx4* xch = reinterpret_cast<floatx4*>(smem);
+  if (w > 0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      xch[((w - 1) * 16 + i) * 64 + lane] = dkT[i];
+      xch[((w - 1) * 16 + 8 + i) * 64 + lane] = dvT[i];
+    }
+  }
+  __syncthreads();
+  if (w > 0) return;
+  for (int ww = 1; ww < NW; ++ww)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      dkT[i] += xch[((ww - 1) * 16 + i) * 64 + lane];
+      dvT[i] += xch[((ww - 1) * 16 + 8 + i) * 64 + lane];
+    }
+  const int key = k0 + c;
+  if (key < S) {
+    const float inv = 1.0f / gs;
+    const float fk = a.sm_scale * inv;
+    float* dk = a.dk + (rowb + key) * a.ldgkv + j * HD;
+    float* dv = a.dv + (rowb + key) * a.ldgkv + j * HD;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      *reinterpret_cast<float4*>(dk + dt * 16 + 4 * g) =
+          make_float4(dkT[dt][0] * fk, dkT[dt][1] * fk, dkT[dt][2] * fk, dkT[dt][3] * fk);
+      *reinterpret_cast<float4*>(dv + dt * 16 + 4 * g) =
+          make_float4(dvT[dt][0] * inv, dvT[dt][1] * inv, dvT[dt][2] * inv, dvT[dt][3] * inv);
+    }
+  }
+}
+
 // The attention backward of a launch over a flat grid (x, B): x < nkv nkvb
 // are dK/dV blocks (key block x / nkv, KV head x % nkv: the longest key
 // blocks first), the next nq nqb dQ blocks (the last, i.e. longest, query
@@ -355,14 +479,20 @@ constexpr int BWD_SMEM = 2 * KV_BUF > 4 * TILE ? 2 * KV_BUF : 4 * TILE;
 template <int NW, int RW, int PART>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_bwd_kernel(const AttnArgs a, int nkvb, int nqb) {
-  constexpr int SMEM = PART == 1 ? 2 * KV_BUF : PART == 2 ? 4 * TILE : BWD_SMEM;
+  constexpr int SMEM = PART == 1   ? 2 * KV_BUF
+                       : PART == 2 ? 4 * TILE
+                       : PART == 3 ? (NW * 2 * KV_BUF > 4 * TILE ? NW * 2 * KV_BUF : 4 * TILE)
+                                   : BWD_SMEM;
   __shared__ __attribute__((aligned(1024))) _Float16 smem[SMEM];
   __shared__ float red[NW];
   const int x = blockIdx.x, b = blockIdx.y;
   const int nkvx = PART == 2 ? 0 : nkvb * a.nkv;
   if constexpr (PART != 2) {
     if (x < nkvx) {
-      dkdv_block<NW, 1>(a, smem, red, x / a.nkv, x % a.nkv, b);
+      if constexpr (PART == 3)
+        dkdv_block_split<NW>(a, smem, red, x / a.nkv, x % a.nkv, b);
+      else
+        dkdv_block<NW, 1>(a, smem, red, x / a.nkv, x % a.nkv, b);
       return;
     }
   }
@@ -398,7 +528,6 @@ void launch_attn_bwd(const AttnArgs& a, int B, int nwk, int nwq, int rw, hipStre
       case 42: launch_bwd<4, 2, 0>(a, B, nkvb, nqb, st); break;
       case 41: launch_bwd<4, 1, 0>(a, B, nkvb, nqb, st); break;
       case 22: launch_bwd<2, 2, 0>(a, B, nkvb, nqb, st); break;
-      case 11: launch_bwd<1, 1, 0>(a, B, nkvb, nqb, st); break;
       default: launch_bwd<2, 1, 0>(a, B, nkvb, nqb, st); break;
     }
     return;
@@ -408,13 +537,10 @@ void launch_attn_bwd(const AttnArgs& a, int B, int nwk, int nwq, int rw, hipStre
     case 42: launch_bwd<4, 2, 2>(a, B, 0, nqb, st); break;
     case 41: launch_bwd<4, 1, 2>(a, B, 0, nqb, st); break;
     case 22: launch_bwd<2, 2, 2>(a, B, 0, nqb, st); break;
-    case 11: launch_bwd<1, 1, 2>(a, B, 0, nqb, st); break;
     default: launch_bwd<2, 1, 2>(a, B, 0, nqb, st); break;
   }
   if (nwk == 4)
     launch_bwd<4, 1, 1>(a, B, nkvb, 0, st);
-  else if (nwk == 1)
-    launch_bwd<1, 1, 1>(a, B, nkvb, 0, st);
   else
     launch_bwd<2, 1, 1>(a, B, nkvb, 0, st);
 }
@@ -431,15 +557,17 @@ hipError_t attn_bwd(const AttnArgs& a, int B, hipStream_t st) {
   // keeps two waves per SIMD, measured faster at every S; LLMT_ATTN_CFG
   // still selects any shape for tuning.
   AttnShape s = attn_shape(B, a.S, a.nq);
-  int nwk = dkdv_waves(B, a.S, a.nkv);
   if (!getenv("LLMT_ATTN_CFG")) {
     s.rw = 1;
-    // tiny grids (the B1 x S128 step: 8 KV heads x 2 key blocks): one-wave
-    // workgroups, so the few key blocks of each GQA group spread wider
-    if (!getenv("LLMT_ATTN_DKDV_WAVES") && (long long)B * a.nq * ((a.S + 63) / 64) < 64)
-      s.nw = nwk = 1;
+    // tiny grids (the B1 x S128 step): dK/dV blocks of 16 keys whose two
+    // waves split the group's query tiles, beside 32-query dQ blocks
+    if (!getenv("LLMT_ATTN_DKDV_WAVES") && (long long)B * a.nq * ((a.S + 63) / 64) < 64) {
+      launch_bwd<2, 1, 3>(a, B, (a.S + 15) / 16, (a.S + 31) / 32, st);
+      LLMT_LAUNCH_CHECK();
+      return hipSuccess;
+    }
   }
-  launch_attn_bwd(a, B, nwk, s.nw, s.rw, st);
+  launch_attn_bwd(a, B, dkdv_waves(B, a.S, a.nkv), s.nw, s.rw, st);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
