@@ -26,8 +26,9 @@ Prints ONE JSON line.  Besides the contract fields it carries
                 CE in GB/s of their compulsory bytes;
   cpu_baseline: the CPU oracle (PyTorch fp32, oracle/lora_step.py) on a
                 bounded sample of the same step;
-  c4, c3:       (default run) the C4 step (B8 x S512, int8 weights) and the
-                C3 attention block measured in the same run.
+  c4, c3, c1:   (default run) the C4 step (B8 x S512, int8 weights), the
+                C3 attention block and the C1 head (lm_head + CE + dX)
+                measured in the same run.
 --config c3 / c4 --only times one of those alone.
 """
 from __future__ import annotations
@@ -262,6 +263,48 @@ def bench_c3(steps, warmup):
     }
 
 
+def bench_c1(steps, warmup):
+    """C1: the fused cross-entropy + lm_head backward alone (llmt_head_ce on a
+    context whose tied embedding is packed once): logits = hidden W^T,
+    softmax + NLL + fp32 dlogits over V = 151936, dhidden = dlogits W, one
+    host sync a call for the loss.  hidden fp16 N(0,1) [128, 2048], W fp16
+    N(0,0.02), targets uniform.  Algorithmic bytes: W read twice (2 x 622.3
+    MB fp16) + logits read and fp32 dlogits written (155.6 MB)."""
+    import torch
+    import llmt
+    T, H, V = 128, 2048, 151936
+    d = llmt.qwen3_dims()
+    d.n_layers = 1
+    ctx = llmt.Context(d, 1, T)
+    g = torch.Generator(device="cuda").manual_seed(1001)
+    W = (torch.randn(V, H, generator=g, device="cuda") * 0.02).half()
+    ctx.set_embed_f16(W, torch.ones(H, device="cuda"))
+    del W
+    x = torch.randn(T, H, generator=g, device="cuda").half()
+    tgt = torch.randint(0, V, (T,), generator=g, device="cuda", dtype=torch.int32)
+    for _ in range(warmup):
+        ctx.head_ce(x, tgt, want_dlogits=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss, _, _ = ctx.head_ce(x, tgt, want_dlogits=True)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    ctx.close()
+    nbytes = 2 * V * H * 2 + 2 * T * V * 4
+    gbs = nbytes / dt / 1e9
+    return {
+        "workload": "C1: fused CE + lm_head backward, hidden 128 x 2048 fp16, tied W 151936 x "
+                    "2048 fp16, fp32 dlogits and dhidden (one host sync a call)",
+        "value": round(T / dt, 2), "unit": "tokens/s", "steps": steps, "warmup": warmup,
+        "ms_per_step": round(dt * 1e3, 4), "loss": round(loss, 5),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": nbytes,
+                     "kernel": "logits GEMM + fused CE + dX GEMM (whole call)"},
+    }
+
+
 def kernel_summary(kinds):
     """Per-category milliseconds per step from llmt_profile_kernels' per-kind
     replays (kernels only: no events between kernels, no launch gaps)."""
@@ -442,6 +485,7 @@ def main():
                                         "loss_first_last")}
         out["c4"]["unit"] = "tokens/s"
         out["c3"] = bench_c3(min(a.steps, 20), 3)
+        out["c1"] = bench_c1(min(a.steps, 20), 3)
     out["achievable"] = achievable_peaks()
     if not a.no_cpu:
         if a.config == "c2":
