@@ -19,6 +19,7 @@
 // h / (nq / nkv) (include/config.h:15).  Tile layout, DMA and fragment
 // conventions: attn_common.h.
 #include <algorithm>
+#include <type_traits>
 
 #include "attn_common.h"
 
@@ -95,7 +96,11 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, _Float16* smem, int 
 #pragma unroll
     for (int i = 0; i < 8; ++i) dqT[r][i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  for (int kb = 0; kb < nkb; ++kb) {
+  // key tiles wholly at or before every query of the wave (no mask) first,
+  // then the diagonal / sequence-end tiles as a loop of their own (every wave
+  // runs nkb iterations, so the per-tile barriers stay matched)
+  const int nfull = qlast == q0 + RW * 16 - 1 ? min((q0 + 1) / BLK, nkb) : 0;
+  auto tile_step = [&](int kb, auto mask_tag) __attribute__((always_inline)) {
     wait_vm<0>();
     tile_barrier();
     if (kb + 1 < nkb) {
@@ -103,7 +108,8 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, _Float16* smem, int 
       dk.issue(kbase, a.ldk, (kb + 1) * BLK, S, nb, w);
       dv.issue(vbase, a.ldv, (kb + 1) * BLK, S, nb + TILE, w);
     }
-    if (kb * BLK > qlast) continue;
+    constexpr bool MASK = decltype(mask_tag)::value;
+    if (MASK && kb * BLK > qlast) return;  // every key after every query of the wave
     const _Float16* Ks = smem + (kb & 1) * 2 * TILE;
     const _Float16* Vs = Ks + TILE;
     floatx4 pt[RW][4], dp[RW][4];
@@ -125,10 +131,10 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, _Float16* smem, int 
         }
       }
     }
-    if (kb * BLK + BLK - 1 <= q0 && kb * BLK + BLK <= S && qlast == q0 + RW * 16 - 1)
-      ds_tile_q<RW, false>(pt, dp, lse2, del, sl2, kb * BLK, q0, S, lane);
-    else
-      ds_tile_q<RW, true>(pt, dp, lse2, del, sl2, kb * BLK, q0, S, lane);
+    sched_reads_ahead<32, 32 * RW, 8, 2 * RW, 2, 0>();
+    __builtin_amdgcn_sched_barrier(0);
+    ds_tile_q<RW, MASK>(pt, dp, lse2, del, sl2, kb * BLK, q0, S, lane);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       half8 db[RW];
@@ -141,7 +147,11 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, _Float16* smem, int 
         for (int r = 0; r < RW; ++r) dqT[r][d] = mfma16(kt, db[r], dqT[r][d]);
       }
     }
-  }
+    sched_reads_ahead<32, 16 * RW, 8, RW, 2, 1>();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  for (int kb = 0; kb < nfull; ++kb) tile_step(kb, std::false_type{});
+  for (int kb = nfull; kb < nkb; ++kb) tile_step(kb, std::true_type{});
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
     const int q = q0 + 16 * r + c;
@@ -203,6 +213,60 @@ __device__ float group_do_scale(const float* __restrict__ dsc, int b, int nq, in
   return m > 0.f ? 1.0f / m : 1.0f;
 }
 
+// Scores of half j2 (queries 32 j2 .. 32 j2 + 31 of the tile) against the
+// wave's 16 keys: p = Q K^T and ds = dO V^T, rows query, column key.
+__device__ __forceinline__ void kv_scores(const _Float16* Qs, const _Float16* Ds,
+                                          const half8 (&kf)[4], const half8 (&vf)[4], int j2,
+                                          floatx4 (&p)[2], floatx4 (&ds)[2], int lane) {
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int mt = 2 * j2 + u;
+    p[u] = floatx4{0.f, 0.f, 0.f, 0.f};
+    ds[u] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      p[u] = mfma16(frag_rm(Qs, mt * 16, ks, lane), kf[ks], p[u]);
+      ds[u] = mfma16(frag_rm(Ds, mt * 16, ks, lane), vf[ks], ds[u]);
+    }
+  }
+}
+
+// dV^T += dO^T P and dK^T += Q^T dS over half j2 (P, dS paired into B operands).
+__device__ __forceinline__ void kv_accum(const _Float16* Qs, const _Float16* Ds, int j2,
+                                         const half8& pb, const half8& db, floatx4 (&dkT)[8],
+                                         floatx4 (&dvT)[8], int lane) {
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) {
+    dvT[dt] = mfma16(frag_tr(Ds, dt * 16, j2, lane), pb, dvT[dt]);
+    dkT[dt] = mfma16(frag_tr(Qs, dt * 16, j2, lane), db, dkT[dt]);
+  }
+}
+
+// One 64-query tile for a wave's 16 keys, the halves one after the other,
+// each phase its own scheduling region with the LDS reads issued ahead of the
+// MFMAs.  (Interleaving one half's dS VALU with the other half's MFMAs was
+// measured slower at B4 x S2048: 277 against 255 us.)
+template <bool MASK>
+__device__ __forceinline__ void kv_tile(const _Float16* Qs, const _Float16* Ds,
+                                        const float* lse_s, const float* del_s,
+                                        const float* dsc_s, const half8 (&kf)[4],
+                                        const half8 (&vf)[4], floatx4 (&dkT)[8],
+                                        floatx4 (&dvT)[8], float sl2, float gs, int qq0, int key,
+                                        int S, int lane) {
+#pragma unroll
+  for (int j2 = 0; j2 < 2; ++j2) {
+    floatx4 p[2], ds[2];
+    kv_scores(Qs, Ds, kf, vf, j2, p, ds, lane);
+    sched_reads_ahead<16, 16, 6, 2, 2, 0>();
+    __builtin_amdgcn_sched_barrier(0);
+    ds_half_kv<MASK>(p, ds, lse_s, del_s, dsc_s, sl2, gs, qq0, j2, key, S, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    kv_accum(Qs, Ds, j2, pair_frag(p[0], p[1]), pair_frag(ds[0], ds[1]), dkT, dvT, lane);
+    sched_reads_ahead<32, 16, 8, 2, 4, 1>();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 constexpr int KV_BUF = 2 * TILE + 3 * BLK * 2;  // halves per dK/dV LDS buffer
 
 // Workgroup (key block kb of 16 KW NW keys, KV head j, batch b).  Wave w
@@ -218,6 +282,7 @@ constexpr int KV_BUF = 2 * TILE + 3 * BLK * 2;  // halves per dK/dV LDS buffer
 template <int NW, int KW>
 __device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* smem, float* red, int kb,
                                            int j, int b) {
+  static_assert(KW == 1, "kv_tile handles one 16-key tile a wave");
   constexpr int NT = NW * 64, KB = NW * 16 * KW;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -228,13 +293,32 @@ __device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* smem, fl
   const int k0 = kb * KB + w * 16 * KW;
   const float sl2 = a.sm_scale * LOG2E;
   const int qb0 = (kb * KB) / BLK;
-  const int nqt = (S + BLK - 1) / BLK - qb0;  // query tiles per head
+  const int qlast = (S - 1) / BLK;
+  const int nqt = qlast - qb0 + 1;  // query tiles per head
   const int niter = group * nqt;
+  // Iteration order: the tiles that need the causal / sequence-end mask (the
+  // diagonal tile of each head, then a partial last tile of each head) come
+  // first, as their own loop, then the full tiles of each head.
+  const int nlast = (S % BLK && nqt > 1) ? 1 : 0;
+  const int nmask = group * (1 + nlast), nfull = nqt - 1 - nlast;
+  auto tile_of = [&](int it, int& h, int& qb) {
+    if (it < group) {
+      h = j * group + it;
+      qb = qb0;
+    } else if (it < nmask) {
+      h = j * group + it - group;
+      qb = qlast;
+    } else {
+      h = j * group + (it - nmask) / nfull;
+      qb = qb0 + 1 + (it - nmask) % nfull;
+    }
+  };
   TileDma<NW> dq_, dd_;
   dq_.init(a.ldq, w);
   dd_.init(a.ld16, w);
   auto issue = [&](int it, _Float16* buf) {
-    const int h = j * group + it / nqt, qb = qb0 + it % nqt;
+    int h, qb;
+    tile_of(it, h, qb);
     dq_.issue(a.q + rowb * a.ldq + h * HD, a.ldq, qb * BLK, S, buf, w);
     dd_.issue(a.dO16 + rowb * a.ld16 + h * HD, a.ld16, qb * BLK, S, buf + TILE, w);
     float* vec = reinterpret_cast<float*>(buf + 2 * TILE);
@@ -261,69 +345,24 @@ __device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* smem, fl
       dkT[t][i] = floatx4{0.f, 0.f, 0.f, 0.f};
       dvT[t][i] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
-  for (int it = 0; it < niter; ++it) {
+  // one iteration: wait for tile it, start tile it + 1, run tile it
+  auto tile_step = [&](int it, auto mask_tag) __attribute__((always_inline)) {
     wait_vm<0>();
     tile_barrier();
     if (it + 1 < niter) issue(it + 1, smem + ((it + 1) & 1) * KV_BUF);
     const _Float16* buf = smem + (it & 1) * KV_BUF;
-    const int qb = qb0 + it % nqt;
-    if (qb * BLK + BLK - 1 < k0) continue;  // every query before every key of the wave
+    int h, qb;
+    tile_of(it, h, qb);
     const _Float16* Qs = buf;
     const _Float16* Ds = buf + TILE;
     const float* lse_s = reinterpret_cast<const float*>(buf + 2 * TILE);
     const float* del_s = lse_s + BLK;
     const float* dsc_s = lse_s + 2 * BLK;
-    // every query of the tile >= every key of the wave and < S: no mask
-    const bool full = qb * BLK >= k0 + 16 * KW - 1 && qb * BLK + BLK <= S;
-#pragma unroll
-    for (int j2 = 0; j2 < 2; ++j2) {  // queries 32 j2 .. 32 j2 + 31 of the tile
-      floatx4 p[KW][2], ds[KW][2];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int mt = 2 * j2 + u;
-#pragma unroll
-        for (int t = 0; t < KW; ++t) {
-          p[t][u] = floatx4{0.f, 0.f, 0.f, 0.f};
-          ds[t][u] = floatx4{0.f, 0.f, 0.f, 0.f};
-        }
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const half8 qf = frag_rm(Qs, mt * 16, ks, lane);
-          const half8 df = frag_rm(Ds, mt * 16, ks, lane);
-#pragma unroll
-          for (int t = 0; t < KW; ++t) {
-            p[t][u] = mfma16(qf, kf[t][ks], p[t][u]);
-            ds[t][u] = mfma16(df, vf[t][ks], ds[t][u]);
-          }
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < KW; ++t) {
-        if (full)
-          ds_half_kv<false>(p[t], ds[t], lse_s, del_s, dsc_s, sl2, gs, qb * BLK, j2,
-                            k0 + 16 * t + c, S, lane);
-        else
-          ds_half_kv<true>(p[t], ds[t], lse_s, del_s, dsc_s, sl2, gs, qb * BLK, j2,
-                           k0 + 16 * t + c, S, lane);
-      }
-      half8 pb[KW], db[KW];
-#pragma unroll
-      for (int t = 0; t < KW; ++t) {
-        pb[t] = pair_frag(p[t][0], p[t][1]);
-        db[t] = pair_frag(ds[t][0], ds[t][1]);
-      }
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const half8 dtr = frag_tr(Ds, dt * 16, j2, lane);
-        const half8 qtr = frag_tr(Qs, dt * 16, j2, lane);
-#pragma unroll
-        for (int t = 0; t < KW; ++t) {
-          dvT[t][dt] = mfma16(dtr, pb[t], dvT[t][dt]);
-          dkT[t][dt] = mfma16(qtr, db[t], dkT[t][dt]);
-        }
-      }
-    }
-  }
+    kv_tile<decltype(mask_tag)::value>(Qs, Ds, lse_s, del_s, dsc_s, kf[0], vf[0], dkT[0], dvT[0],
+                                       sl2, gs, qb * BLK, k0 + c, S, lane);
+  };
+  for (int it = 0; it < nmask; ++it) tile_step(it, std::true_type{});
+  for (int it = nmask; it < niter; ++it) tile_step(it, std::false_type{});
   const float inv = 1.0f / gs;
   const float fk = a.sm_scale * inv;
 #pragma unroll

@@ -146,6 +146,24 @@ __device__ __forceinline__ half8 frag_global(const _Float16* base, long long ld,
   return row < n ? x : half8{};
 }
 
+// Scheduling of a straight-line block of NR LDS reads feeding NM MFMAs (the
+// gfx950 backend's sched_group_barrier): RA reads issued ahead, then groups
+// of MP MFMAs each followed by the next DP reads, then the remaining MFMAs.
+// The default schedule waits on each read right before its MFMA; running the
+// reads ahead hides the LDS latency behind the MFMAs already issued.
+constexpr int SG_MFMA = 0x008, SG_DSR = 0x100;
+template <int NR, int NM, int RA, int MP, int DP, int ID>
+__device__ __forceinline__ void sched_reads_ahead() {
+  static_assert(RA <= NR && (NR - RA) % DP == 0 && (NR - RA) / DP * MP <= NM, "schedule shape");
+  __builtin_amdgcn_sched_group_barrier(SG_DSR, RA, ID);
+#pragma unroll
+  for (int i = 0; i < (NR - RA) / DP; ++i) {
+    __builtin_amdgcn_sched_group_barrier(SG_MFMA, MP, ID);
+    __builtin_amdgcn_sched_group_barrier(SG_DSR, DP, ID);
+  }
+  __builtin_amdgcn_sched_group_barrier(SG_MFMA, NM - (NR - RA) / DP * MP, ID);
+}
+
 // Launch shape: NW waves of RW 16-row tiles.  Two tiles a wave halve the LDS
 // operand reads per MFMA; fewer, smaller workgroups keep short sequences
 // spread over the CUs.  LLMT_ATTN_CFG = "NW,RW" (NW 2 or 4, RW 1 or 2)

@@ -8,13 +8,15 @@ no fallback path.
 from __future__ import annotations
 
 import ctypes as C
+import os
 import re
 from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 PKG = HERE.parent
 ROOT = PKG.parent
-LIB_PATH = PKG / "libllmt.so"
+# LLMT_LIB names another build of the library (default: the in-tree one)
+LIB_PATH = Path(os.environ.get("LLMT_LIB") or PKG / "libllmt.so")
 HEADER = ROOT / "include" / "llmt.h"
 
 vp, i32, f32, sz, u64 = C.c_void_p, C.c_int, C.c_float, C.c_size_t, C.c_uint64
