@@ -387,6 +387,11 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
 #pragma unroll
       for (int j = 0; j < NFR; ++j) acc[i][j] = mfma16(a, b[j], acc[i][j]);
     }
+    // every LDS read of the chunk first, then its MFMAs (the default
+    // schedule waits on each A fragment right before its four MFMAs;
+    // 4-5% faster at the C4 shapes)
+    __builtin_amdgcn_sched_group_barrier(0x100, NFR + 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 8 * NFR, 0);
   }
   wait_vm<0>();
 
