@@ -446,32 +446,12 @@ __device__ __forceinline__ void dkdv_block_split(const AttnArgs& a, _Float16* sm
     const float* del_s = lse_s + BLK;
     const float* dsc_s = lse_s + 2 * BLK;
     const bool full = qb * BLK >= k0 + 15 && qb * BLK + BLK <= S;
-#pragma unroll
-    for (int j2 = 0; j2 < 2; ++j2) {
-      floatx4 p[2], ds[2];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int mt = 2 * j2 + u;
-        p[u] = floatx4{0.f, 0.f, 0.f, 0.f};
-        ds[u] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          p[u] = mfma16(frag_rm(Qs, mt * 16, ks, lane), kf[ks], p[u]);
-          ds[u] = mfma16(frag_rm(Ds, mt * 16, ks, lane), vf[ks], ds[u]);
-        }
-      }
-      if (full)
-        ds_half_kv<false>(p, ds, lse_s, del_s, dsc_s, sl2, gs, qb * BLK, j2, k0 + c, S, lane);
-      else
-        ds_half_kv<true>(p, ds, lse_s, del_s, dsc_s, sl2, gs, qb * BLK, j2, k0 + c, S, lane);
-      const half8 pb = pair_frag(p[0], p[1]);
-      const half8 db = pair_frag(ds[0], ds[1]);
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        dvT[dt] = mfma16(frag_tr(Ds, dt * 16, j2, lane), pb, dvT[dt]);
-        dkT[dt] = mfma16(frag_tr(Qs, dt * 16, j2, lane), db, dkT[dt]);
-      }
-    }
+    if (full)
+      kv_tile<false>(Qs, Ds, lse_s, del_s, dsc_s, kf, vf, dkT, dvT, sl2, gs, qb * BLK, k0 + c, S,
+                     lane);
+    else
+      kv_tile<true>(Qs, Ds, lse_s, del_s, dsc_s, kf, vf, dkT, dvT, sl2, gs, qb * BLK, k0 + c, S,
+                    lane);
   }
   // waves 1 .. NW-1 hand their sums to wave 0, which adds them in order
   wait_vm<0>();
