@@ -212,7 +212,8 @@ struct Ctx {
   hipError_t backward(int B, int accumulate);
   hipError_t optimizer();
   hipError_t refresh_shadows();
-  hipError_t device_step(int B, int with_adam);
+  // tok / tgt: device token and target ids read in place (default: tok_buf, tgt_buf)
+  hipError_t device_step(int B, int with_adam, const int* tok = nullptr, const int* tgt = nullptr);
 };
 
 }  // namespace llmt

@@ -457,9 +457,9 @@ hipError_t Ctx::refresh_shadows() {
   return hipSuccess;
 }
 
-hipError_t Ctx::device_step(int B, int with_adam) {
-  LLMT_HIP_TRY(forward(tok_buf, B, nullptr));
-  LLMT_HIP_TRY(ce(nullptr, tgt_buf, B, nullptr));
+hipError_t Ctx::device_step(int B, int with_adam, const int* tok, const int* tgt) {
+  LLMT_HIP_TRY(forward(tok ? tok : tok_buf, B, nullptr));
+  LLMT_HIP_TRY(ce(nullptr, tgt ? tgt : tgt_buf, B, nullptr));
   LLMT_HIP_TRY(backward(B, 0));
   if (with_adam) LLMT_HIP_TRY(optimizer());
   return hipSuccess;
@@ -632,8 +632,10 @@ static bool graph_inputs(Ctx* c, const int* tokens, const int* targets) {
   return true;
 }
 
-// tokens/targets non-NULL: the inputs (and, with AdamW, the staged
-// hyper-parameters) are copied inside the graph instead of before it.
+// tokens/targets non-NULL: the graph's kernels read the caller's token and
+// target buffers in place (the graph is keyed by those pointers), the staged
+// hyper-parameters (with AdamW) are copied inside the graph, and so is the
+// loss read-back, so a step is one graph launch and one wait.
 static int run_step(Ctx* c, int batch, int with_adam, float* loss_host,
                     const int* tokens = nullptr, const int* targets = nullptr) {
   if (c->use_graph && !c->recording) {
@@ -646,14 +648,11 @@ static int run_step(Ctx* c, int batch, int with_adam, float* loss_host,
       hipGraph_t g;
       TRY_HIP(hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
       hipError_t e = hipSuccess;
-      if (tokens) {
-        const size_t n = (size_t)batch * c->S * sizeof(int);
-        e = hipMemcpyAsync(c->tok_buf, tokens, n, hipMemcpyDefault, c->st);
-        if (e == hipSuccess) e = hipMemcpyAsync(c->tgt_buf, targets, n, hipMemcpyDefault, c->st);
-        if (e == hipSuccess && with_adam)
-          e = hipMemcpyAsync(c->hp_dev, c->host_hp, sizeof(AdamHp), hipMemcpyHostToDevice, c->st);
-      }
-      if (e == hipSuccess) e = c->device_step(batch, with_adam);
+      if (tokens && with_adam)
+        e = hipMemcpyAsync(c->hp_dev, c->host_hp, sizeof(AdamHp), hipMemcpyHostToDevice, c->st);
+      if (e == hipSuccess) e = c->device_step(batch, with_adam, tokens, targets);
+      if (e == hipSuccess)
+        e = hipMemcpyAsync(c->host_loss, c->loss_dev, sizeof(float), hipMemcpyDeviceToHost, c->st);
       hipError_t e2 = hipStreamEndCapture(c->st, &g);
       TRY_HIP(e);
       TRY_HIP(e2);
@@ -668,8 +667,8 @@ static int run_step(Ctx* c, int batch, int with_adam, float* loss_host,
     TRY_HIP(hipGraphLaunch(c->graph_exec, c->st));
   } else {
     TRY_HIP(c->device_step(batch, with_adam));
+    TRY_HIP(hipMemcpyAsync(c->host_loss, c->loss_dev, sizeof(float), hipMemcpyDeviceToHost, c->st));
   }
-  TRY_HIP(hipMemcpyAsync(c->host_loss, c->loss_dev, sizeof(float), hipMemcpyDeviceToHost, c->st));
   TRY_HIP(hipStreamSynchronize(c->st));
   if (loss_host) *loss_host = *c->host_loss;
   return LLMT_OK;
