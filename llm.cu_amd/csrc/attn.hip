@@ -171,9 +171,10 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnArgs a) {
   }
 }
 
-// Per token row, one wave per head: delta[b, h, s] = sum_d dO * O, and
-// dO16 = fp16(dO * sc) with sc the power-of-two scale of the head's max |dO|,
-// dsc[b, h, s] = 1 / sc (0 for an all-zero head row).
+// Per token row, 16 lanes per head (lane j: dims 8 j .. 8 j + 7, 16-byte
+// accesses): delta[b, h, s] = sum_d dO * O, and dO16 = fp16(dO * sc) with sc
+// the power-of-two scale of the head's max |dO|, dsc[b, h, s] = 1 / sc (0 for
+// an all-zero head row).
 template <typename TD>
 __global__ __launch_bounds__(256) void attn_delta_kernel(const TD* __restrict__ dO, long long ldd,
                                                          const _Float16* __restrict__ o,
@@ -182,23 +183,43 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(const TD* __restrict__ 
                                                          _Float16* __restrict__ dO16,
                                                          long long ld16, float* __restrict__ dsc) {
   const int t = blockIdx.x;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int j = threadIdx.x & 15;
   const int b = t / S, s = t - b * S;
-  for (int h = w; h < nq; h += 4) {
-    const TD* d = dO + (long long)t * ldd + h * HD;
-    const _Float16* oo = o + (long long)t * ldo + h * HD;
-    const float d0 = (float)d[lane], d1 = (float)d[lane + 64];
-    const float v = wave_sum(d0 * (float)oo[lane] + d1 * (float)oo[lane + 64]);
-    const float amax = wave_max(fmaxf(fabsf(d0), fabsf(d1)));
+  for (int h = threadIdx.x >> 4; h < nq; h += 16) {  // whole 16-lane groups
+    const TD* d = dO + (long long)t * ldd + h * HD + 8 * j;
+    float dv[8];
+    if constexpr (sizeof(TD) == 2) {
+      const half8 x = *reinterpret_cast<const half8*>(d);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dv[i] = (float)x[i];
+    } else {
+      const float4 x0 = *reinterpret_cast<const float4*>(d);
+      const float4 x1 = *reinterpret_cast<const float4*>(d + 4);
+      dv[0] = x0.x; dv[1] = x0.y; dv[2] = x0.z; dv[3] = x0.w;
+      dv[4] = x1.x; dv[5] = x1.y; dv[6] = x1.z; dv[7] = x1.w;
+    }
+    const half8 ov = *reinterpret_cast<const half8*>(o + (long long)t * ldo + h * HD + 8 * j);
+    float v = 0.f, amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      v += dv[i] * (float)ov[i];
+      amax = fmaxf(amax, fabsf(dv[i]));
+    }
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1) {
+      v += __shfl_xor(v, m, 64);
+      amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+    }
     const float sc = pow2_scale_for(amax, kDoScaleExp);
     const long long bhs = ((long long)b * nq + h) * S + s;
-    if (lane == 0) {
+    if (j == 0) {
       delta[bhs] = v;
       dsc[bhs] = pow2_inv_scale_for(amax, kDoScaleExp);
     }
-    _Float16* d16 = dO16 + (long long)t * ld16 + h * HD;
-    d16[lane] = (_Float16)(d0 * sc);
-    d16[lane + 64] = (_Float16)(d1 * sc);
+    half8 o16;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o16[i] = (_Float16)(dv[i] * sc);
+    *reinterpret_cast<half8*>(dO16 + (long long)t * ld16 + h * HD + 8 * j) = o16;
   }
 }
 
@@ -214,6 +235,13 @@ void launch_fwd(const AttnArgs& a, int B, hipStream_t st) {
 hipError_t attn_delta(const void* dO, int dO_is_f16, long long ldd, const _Float16* o,
                       long long ldo, int nq, int S, int T, float* delta, _Float16* dO16,
                       long long ld16, float* dsc, hipStream_t st) {
+  // 16-byte accesses: row pitches and bases aligned to them
+  const size_t es = dO_is_f16 ? 2 : 4;
+  if (((uintptr_t)dO | (uintptr_t)o | (uintptr_t)dO16) % 16 || (ldd * es) % 16 || (ldo * 2) % 16 ||
+      (ld16 * 2) % 16) {
+    set_error("attn_delta: dO, O and dO16 rows need 16-byte alignment");
+    return hipErrorInvalidValue;
+  }
   if (dO_is_f16)
     hipLaunchKernelGGL(attn_delta_kernel<_Float16>, dim3(T), dim3(256), 0, st,
                        (const _Float16*)dO, ldd, o, ldo, nq, S, delta, dO16, ld16, dsc);

@@ -447,47 +447,88 @@ __global__ __launch_bounds__(RT) void resid_norm_kernel(const RowIn in,
 }
 
 // Per-head QK-RMSNorm + RoPE on [T, nh, 128] rows (the attention block API's
-// separate q / k inputs; the training step fuses this into qkv_post): one
-// wave per (token, head), lane = RoPE pair (d, d + 64).
+// separate q / k inputs; the training step fuses this into qkv_post): 16
+// lanes per (token, head) row, lane j holding the RoPE pairs (d, d + 64) for
+// d = 4 j .. 4 j + 3, so every access is 8 (fp16) or 16 (fp32) bytes a lane.
 //   forward:  y = rope(x * r * w), r = rsqrt(mean x^2 + eps)
 //   backward: n = rope^T(dy); dx = r (n w - (r^2 / 128) sum(n w x) x)
 // (src/kernels/rmsnorm.cu:6-41, 53-95; src/kernels/rope.cu:7-46, 57-89).
+constexpr int HN_ROWS = RT / 16;  // rows a workgroup
+
+// Sum over the 16 lanes of a row group.
+__device__ __forceinline__ float sum16(float v) {
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float4 ldh4(const _Float16* p) {
+  const half4 h = *reinterpret_cast<const half4*>(p);
+  return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+}
+
 __global__ __launch_bounds__(RT) void head_norm_rope_kernel(const _Float16* __restrict__ x,
                                                             const float* __restrict__ w,
                                                             const float* __restrict__ cosT,
                                                             const float* __restrict__ sinT, int S,
                                                             int nh, int T, float eps,
                                                             _Float16* __restrict__ out) {
-  const int lane = threadIdx.x & 63;
-  const long long row = (long long)blockIdx.x * RW + (threadIdx.x >> 6);  // (token, head)
-  if (row >= (long long)T * nh) return;
+  const int j = threadIdx.x & 15;
+  const long long row = (long long)blockIdx.x * HN_ROWS + (threadIdx.x >> 4);  // (token, head)
+  if (row >= (long long)T * nh) return;  // whole 16-lane groups
   const int pos = (int)(row / nh) % S;
-  const float cs = cosT[pos * (HD / 2) + lane], sn = sinT[pos * (HD / 2) + lane];
-  const _Float16* xr = x + row * HD;
-  const float x0 = (float)xr[lane], x1 = (float)xr[lane + 64];
-  const float r = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / HD + eps);
-  const float y0 = x0 * r * w[lane], y1 = x1 * r * w[lane + 64];
-  out[row * HD + lane] = (_Float16)(y0 * cs - y1 * sn);
-  out[row * HD + lane + 64] = (_Float16)(y1 * cs + y0 * sn);
+  const float4 cs = ld4(cosT + pos * (HD / 2) + 4 * j), sn = ld4(sinT + pos * (HD / 2) + 4 * j);
+  const float4 x0 = ldh4(x + row * HD + 4 * j), x1 = ldh4(x + row * HD + 64 + 4 * j);
+  const float4 w0 = ld4(w + 4 * j), w1 = ld4(w + 64 + 4 * j);
+  const float ss = x0.x * x0.x + x0.y * x0.y + x0.z * x0.z + x0.w * x0.w + x1.x * x1.x +
+                   x1.y * x1.y + x1.z * x1.z + x1.w * x1.w;
+  const float r = rsqrtf(sum16(ss) / HD + eps);
+  const float a0[4] = {x0.x * r * w0.x, x0.y * r * w0.y, x0.z * r * w0.z, x0.w * r * w0.w};
+  const float a1[4] = {x1.x * r * w1.x, x1.y * r * w1.y, x1.z * r * w1.z, x1.w * r * w1.w};
+  const float c[4] = {cs.x, cs.y, cs.z, cs.w}, sg[4] = {sn.x, sn.y, sn.z, sn.w};
+  half4 o0, o1;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o0[i] = (_Float16)(a0[i] * c[i] - a1[i] * sg[i]);
+    o1[i] = (_Float16)(a1[i] * c[i] + a0[i] * sg[i]);
+  }
+  *reinterpret_cast<half4*>(out + row * HD + 4 * j) = o0;
+  *reinterpret_cast<half4*>(out + row * HD + 64 + 4 * j) = o1;
 }
 
 __global__ __launch_bounds__(RT) void head_norm_rope_bwd_kernel(
     const float* __restrict__ dy, const _Float16* __restrict__ x, const float* __restrict__ w,
     const float* __restrict__ cosT, const float* __restrict__ sinT, int S, int nh, int T, float eps,
     float* __restrict__ dx) {
-  const int lane = threadIdx.x & 63;
-  const long long row = (long long)blockIdx.x * RW + (threadIdx.x >> 6);
-  if (row >= (long long)T * nh) return;
+  const int j = threadIdx.x & 15;
+  const long long row = (long long)blockIdx.x * HN_ROWS + (threadIdx.x >> 4);
+  if (row >= (long long)T * nh) return;  // whole 16-lane groups
   const int pos = (int)(row / nh) % S;
-  const float cs = cosT[pos * (HD / 2) + lane], sn = sinT[pos * (HD / 2) + lane];
-  const float d0 = dy[row * HD + lane], d1 = dy[row * HD + lane + 64];
-  const float x0 = (float)x[row * HD + lane], x1 = (float)x[row * HD + lane + 64];
-  const float w0 = w[lane], w1 = w[lane + 64];
-  const float n0 = d0 * cs + d1 * sn, n1 = d1 * cs - d0 * sn;
-  const float r = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / HD + eps);
-  const float coef = r * r / HD * wave_sum(n0 * w0 * x0 + n1 * w1 * x1);
-  dx[row * HD + lane] = r * (n0 * w0 - coef * x0);
-  dx[row * HD + lane + 64] = r * (n1 * w1 - coef * x1);
+  const float4 cs = ld4(cosT + pos * (HD / 2) + 4 * j), sn = ld4(sinT + pos * (HD / 2) + 4 * j);
+  const float4 d0 = ld4(dy + row * HD + 4 * j), d1 = ld4(dy + row * HD + 64 + 4 * j);
+  const float4 x0 = ldh4(x + row * HD + 4 * j), x1 = ldh4(x + row * HD + 64 + 4 * j);
+  const float4 w0 = ld4(w + 4 * j), w1 = ld4(w + 64 + 4 * j);
+  const float c[4] = {cs.x, cs.y, cs.z, cs.w}, sg[4] = {sn.x, sn.y, sn.z, sn.w};
+  const float dd0[4] = {d0.x, d0.y, d0.z, d0.w}, dd1[4] = {d1.x, d1.y, d1.z, d1.w};
+  const float xx0[4] = {x0.x, x0.y, x0.z, x0.w}, xx1[4] = {x1.x, x1.y, x1.z, x1.w};
+  const float ww0[4] = {w0.x, w0.y, w0.z, w0.w}, ww1[4] = {w1.x, w1.y, w1.z, w1.w};
+  float n0[4], n1[4], ss = 0.f, dot = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    n0[i] = dd0[i] * c[i] + dd1[i] * sg[i];
+    n1[i] = dd1[i] * c[i] - dd0[i] * sg[i];
+    ss += xx0[i] * xx0[i] + xx1[i] * xx1[i];
+    dot += n0[i] * ww0[i] * xx0[i] + n1[i] * ww1[i] * xx1[i];
+  }
+  const float r = rsqrtf(sum16(ss) / HD + eps);
+  const float coef = r * r / HD * sum16(dot);
+  float o0[4], o1[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o0[i] = r * (n0[i] * ww0[i] - coef * xx0[i]);
+    o1[i] = r * (n1[i] * ww1[i] - coef * xx1[i]);
+  }
+  *reinterpret_cast<float4*>(dx + row * HD + 4 * j) = make_float4(o0[0], o0[1], o0[2], o0[3]);
+  *reinterpret_cast<float4*>(dx + row * HD + 64 + 4 * j) = make_float4(o1[0], o1[1], o1[2], o1[3]);
 }
 
 // ---------------------------------------------------------------- backward
@@ -1120,8 +1161,12 @@ hipError_t rope_tables(int S, double theta, float* cosT, float* sinT, hipStream_
 hipError_t head_norm_rope(const _Float16* x, const float* w, const float* cosT, const float* sinT,
                           int S, int nh, int T, float eps, _Float16* out, hipStream_t st) {
   const long long rows = (long long)T * nh;
-  hipLaunchKernelGGL(head_norm_rope_kernel, dim3((unsigned)((rows + RW - 1) / RW)), dim3(RT), 0, st,
-                     x, w, cosT, sinT, S, nh, T, eps, out);
+  if ((uintptr_t)w % 16 || ((uintptr_t)x | (uintptr_t)out) % 8) {
+    set_error("head_norm_rope: w needs 16-byte and x, out 8-byte alignment");
+    return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL(head_norm_rope_kernel, dim3((unsigned)((rows + HN_ROWS - 1) / HN_ROWS)),
+                     dim3(RT), 0, st, x, w, cosT, sinT, S, nh, T, eps, out);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
@@ -1130,8 +1175,12 @@ hipError_t head_norm_rope_bwd(const float* dy, const _Float16* x, const float* w
                               const float* cosT, const float* sinT, int S, int nh, int T,
                               float eps, float* dx, hipStream_t st) {
   const long long rows = (long long)T * nh;
-  hipLaunchKernelGGL(head_norm_rope_bwd_kernel, dim3((unsigned)((rows + RW - 1) / RW)), dim3(RT),
-                     0, st, dy, x, w, cosT, sinT, S, nh, T, eps, dx);
+  if (((uintptr_t)dy | (uintptr_t)dx | (uintptr_t)w) % 16 || (uintptr_t)x % 8) {
+    set_error("head_norm_rope_bwd: dy, dx, w need 16-byte and x 8-byte alignment");
+    return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL(head_norm_rope_bwd_kernel, dim3((unsigned)((rows + HN_ROWS - 1) / HN_ROWS)),
+                     dim3(RT), 0, st, dy, x, w, cosT, sinT, S, nh, T, eps, dx);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
