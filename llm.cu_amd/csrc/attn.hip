@@ -19,6 +19,8 @@ namespace llmt {
 
 namespace {
 
+#define LLMT_INLINE __attribute__((always_inline))
+
 // ---------------------------------------------------------------- forward
 // One 64-key tile of the online softmax for RW 16-query tiles of a wave:
 // st holds the raw scores (rows key, column query); on return the fp32
@@ -45,22 +47,20 @@ __device__ __forceinline__ void softmax_tile(floatx4 (&st)[RW][4], float (&m)[RW
         }
         bm = fmaxf(bm, s);
       }
-    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
-    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    bm = xg_max(bm);
     const float mn = fmaxf(m[r], bm * sl2);  // sl2 > 0: max commutes with the scale
     const float mu = mn == -INFINITY ? 0.f : mn;
     const float alpha = __builtin_amdgcn_exp2f(m[r] - mu);
     m[r] = mn;
-    float ps = 0.f;
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(st[r][mt][v], sl2, -mu));
-        st[r][mt][v] = p;
-        ps += p;
-      }
-    l[r] = l[r] * alpha + ps;
+      for (int v = 0; v < 4; ++v) st[r][mt][v] = __builtin_amdgcn_exp2f(fmaf(st[r][mt][v], sl2, -mu));
+    // row sum as a tree (independent adds) rather than one serial chain
+    float ps4[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) ps4[mt] = (st[r][mt][0] + st[r][mt][1]) + (st[r][mt][2] + st[r][mt][3]);
+    l[r] = l[r] * alpha + ((ps4[0] + ps4[1]) + (ps4[2] + ps4[3]));
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) ot[r][dt] *= alpha;
   }
@@ -72,7 +72,11 @@ __device__ __forceinline__ void softmax_tile(floatx4 (&st)[RW][4], float (&m)[RW
 template <int NW, int RW>
 __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnArgs a) {
   constexpr int QB = NW * RW * 16;
-  __shared__ __attribute__((aligned(1024))) _Float16 smem[4 * TILE];
+  // two LDS buffers of (K tile, V tile) as separate arrays, the tile loop
+  // unrolled by two: which buffer a read or a DMA targets is then static, so
+  // the reads of tile kb are not made to wait for the DMA of tile kb + 1
+  __shared__ __attribute__((aligned(1024))) _Float16 buf0[2 * TILE];
+  __shared__ __attribute__((aligned(1024))) _Float16 buf1[2 * TILE];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, g = lane >> 4;
@@ -90,8 +94,8 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnArgs a) {
   TileDma<NW> dk, dv;
   dk.init(a.ldk, w);
   dv.init(a.ldv, w);
-  dk.issue(kbase, a.ldk, 0, S, smem, w);
-  dv.issue(vbase, a.ldv, 0, S, smem + TILE, w);
+  dk.issue(kbase, a.ldk, 0, S, buf0, w);
+  dv.issue(vbase, a.ldv, 0, S, buf0 + TILE, w);
   half8 qf[RW][4];
 #pragma unroll
   for (int r = 0; r < RW; ++r)
@@ -109,16 +113,14 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnArgs a) {
     for (int i = 0; i < 8; ++i) ot[r][i] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
 
-  for (int kb = 0; kb < nkb; ++kb) {
+  auto tile = [&](int kb, const _Float16* Ks, _Float16* nb) LLMT_INLINE {
     wait_vm<0>();
     tile_barrier();
     if (kb + 1 < nkb) {
-      _Float16* nb = smem + ((kb + 1) & 1) * 2 * TILE;
       dk.issue(kbase, a.ldk, (kb + 1) * BLK, S, nb, w);
       dv.issue(vbase, a.ldv, (kb + 1) * BLK, S, nb + TILE, w);
     }
-    if (kb * BLK > qlast) continue;  // every key after every query of the wave
-    const _Float16* Ks = smem + (kb & 1) * 2 * TILE;
+    if (kb * BLK > qlast) return;  // every key after every query of the wave
     const _Float16* Vs = Ks + TILE;
     floatx4 st[RW][4];
 #pragma unroll
@@ -149,12 +151,15 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnArgs a) {
         for (int r = 0; r < RW; ++r) ot[r][dt] = mfma16(vf, pb[r], ot[r][dt]);
       }
     }
+  };
+  for (int kb = 0; kb < nkb; kb += 2) {
+    tile(kb, buf0, buf1);
+    if (kb + 1 < nkb) tile(kb + 1, buf1, buf0);
   }
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
     float lr = l[r];
-    lr += __shfl_xor(lr, 16, 64);
-    lr += __shfl_xor(lr, 32, 64);
+    lr = xg_sum(lr);
     const int q = q0 + 16 * r + c;
     if (q < S) {
       const float inv = 1.0f / lr;

@@ -55,7 +55,8 @@ __device__ __forceinline__ void ds_tile_q(const floatx4 (&pt)[RW][4], floatx4 (&
 // buffers of K and V tiles, 4 TILE halves).  dQ row q depends on dO row q
 // only, so each row stays in its own dO scale 1 / dsc[q] throughout.
 template <int NW, int RW>
-__device__ __forceinline__ void dq_block(const AttnArgs& a, _Float16* smem, int qb, int h, int b) {
+__device__ __forceinline__ void dq_block(const AttnArgs& a, _Float16* buf0, _Float16* buf1, int qb,
+                                         int h, int b) {
   constexpr int QB = NW * RW * 16;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -72,8 +73,8 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, _Float16* smem, int 
   TileDma<NW> dk, dv;
   dk.init(a.ldk, w);
   dv.init(a.ldv, w);
-  dk.issue(kbase, a.ldk, 0, S, smem, w);
-  dv.issue(vbase, a.ldv, 0, S, smem + TILE, w);
+  dk.issue(kbase, a.ldk, 0, S, buf0, w);
+  dv.issue(vbase, a.ldv, 0, S, buf0 + TILE, w);
   half8 qf[RW][4], df[RW][4];
   float lse2[RW], del[RW], fq[RW];
 #pragma unroll
@@ -100,17 +101,17 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, _Float16* smem, int 
   // then the diagonal / sequence-end tiles as a loop of their own (every wave
   // runs nkb iterations, so the per-tile barriers stay matched)
   const int nfull = qlast == q0 + RW * 16 - 1 ? min((q0 + 1) / BLK, nkb) : 0;
-  auto tile_step = [&](int kb, auto mask_tag) __attribute__((always_inline)) {
+  // tile kb lives in buffer kb & 1 (Ks), tile kb + 1 lands in the other (nb)
+  auto tile_step = [&](int kb, auto mask_tag, const _Float16* Ks, _Float16* nb)
+                       __attribute__((always_inline)) {
     wait_vm<0>();
     tile_barrier();
     if (kb + 1 < nkb) {
-      _Float16* nb = smem + ((kb + 1) & 1) * 2 * TILE;
       dk.issue(kbase, a.ldk, (kb + 1) * BLK, S, nb, w);
       dv.issue(vbase, a.ldv, (kb + 1) * BLK, S, nb + TILE, w);
     }
     constexpr bool MASK = decltype(mask_tag)::value;
     if (MASK && kb * BLK > qlast) return;  // every key after every query of the wave
-    const _Float16* Ks = smem + (kb & 1) * 2 * TILE;
     const _Float16* Vs = Ks + TILE;
     floatx4 pt[RW][4], dp[RW][4];
 #pragma unroll
@@ -150,8 +151,16 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, _Float16* smem, int 
     sched_reads_ahead<32, 16 * RW, 8, RW, 2, 1>();
     __builtin_amdgcn_sched_barrier(0);
   };
-  for (int kb = 0; kb < nfull; ++kb) tile_step(kb, std::false_type{});
-  for (int kb = nfull; kb < nkb; ++kb) tile_step(kb, std::true_type{});
+  // The unmasked tiles in pairs with the buffers named statically: the
+  // compiler then sees that a tile's LDS reads and the DMA of the next tile
+  // touch different arrays and does not make the reads wait for that DMA
+  // (with buffers chosen at run time it waits for every DMA in flight).
+  for (int kb = 0; kb < nfull; kb += 2) {
+    tile_step(kb, std::false_type{}, buf0, buf1);
+    if (kb + 1 < nfull) tile_step(kb + 1, std::false_type{}, buf1, buf0);
+  }
+  for (int kb = nfull; kb < nkb; ++kb)
+    tile_step(kb, std::true_type{}, (kb & 1) ? buf1 : buf0, (kb & 1) ? buf0 : buf1);
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
     const int q = q0 + 16 * r + c;
@@ -280,8 +289,8 @@ constexpr int KV_BUF = 2 * TILE + 3 * BLK * 2;  // halves per dK/dV LDS buffer
 // LDS: two buffers of (Q tile, dO16 tile, lse[64], delta[64], dsc[64]); the
 // next (head, tile) lands while the current one is computed.
 template <int NW, int KW>
-__device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* smem, float* red, int kb,
-                                           int j, int b) {
+__device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* buf0, _Float16* buf1,
+                                           float* red, int kb, int j, int b) {
   static_assert(KW == 1, "kv_tile handles one 16-key tile a wave");
   constexpr int NT = NW * 64, KB = NW * 16 * KW;
   const int lane = threadIdx.x & 63;
@@ -327,7 +336,7 @@ __device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* smem, fl
     if (w == NW - 1) dma_vec64(a.delta + bh, qb * BLK, S, vec + BLK);
     if (w == NW / 2) dma_vec64(a.dsc + bh, qb * BLK, S, vec + 2 * BLK);
   };
-  issue(0, smem);
+  issue(0, buf0);
   const float gs = group_do_scale<NT>(a.dsc, b, a.nq, j, group, S, red);
   half8 kf[KW][4], vf[KW][4];
 #pragma unroll
@@ -345,12 +354,13 @@ __device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* smem, fl
       dkT[t][i] = floatx4{0.f, 0.f, 0.f, 0.f};
       dvT[t][i] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
-  // one iteration: wait for tile it, start tile it + 1, run tile it
-  auto tile_step = [&](int it, auto mask_tag) __attribute__((always_inline)) {
+  // one iteration: wait for tile it (in buf, buffer it & 1), start tile
+  // it + 1 (into nb), run tile it
+  auto tile_step = [&](int it, auto mask_tag, const _Float16* buf, _Float16* nb)
+                       __attribute__((always_inline)) {
     wait_vm<0>();
     tile_barrier();
-    if (it + 1 < niter) issue(it + 1, smem + ((it + 1) & 1) * KV_BUF);
-    const _Float16* buf = smem + (it & 1) * KV_BUF;
+    if (it + 1 < niter) issue(it + 1, nb);
     int h, qb;
     tile_of(it, h, qb);
     const _Float16* Qs = buf;
@@ -361,8 +371,17 @@ __device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* smem, fl
     kv_tile<decltype(mask_tag)::value>(Qs, Ds, lse_s, del_s, dsc_s, kf[0], vf[0], dkT[0], dvT[0],
                                        sl2, gs, qb * BLK, k0 + c, S, lane);
   };
-  for (int it = 0; it < nmask; ++it) tile_step(it, std::true_type{});
-  for (int it = nmask; it < niter; ++it) tile_step(it, std::false_type{});
+  auto step_rt = [&](int it, auto mask_tag) __attribute__((always_inline)) {
+    tile_step(it, mask_tag, (it & 1) ? buf1 : buf0, (it & 1) ? buf0 : buf1);
+  };
+  for (int it = 0; it < nmask; ++it) step_rt(it, std::true_type{});
+  // the full tiles in pairs with statically named buffers (see dq_block)
+  int it = nmask;
+  if (it < niter && (it & 1)) step_rt(it++, std::false_type{});
+  for (; it < niter; it += 2) {
+    tile_step(it, std::false_type{}, buf0, buf1);
+    if (it + 1 < niter) tile_step(it + 1, std::false_type{}, buf1, buf0);
+  }
   const float inv = 1.0f / gs;
   const float fk = a.sm_scale * inv;
 #pragma unroll
@@ -493,31 +512,35 @@ __device__ __forceinline__ void dkdv_block_split(const AttnArgs& a, _Float16* sm
 // blocks first), the next nq nqb dQ blocks (the last, i.e. longest, query
 // blocks first).  PART 0: both kinds; 1: dK/dV only; 2: dQ only -- the
 // one-kind forms keep their own (smaller) register and LDS budgets.
-constexpr int BWD_SMEM = 2 * KV_BUF > 4 * TILE ? 2 * KV_BUF : 4 * TILE;
+constexpr int BWD_BUF = KV_BUF > 2 * TILE ? KV_BUF : 2 * TILE;  // halves per buffer
 
 template <int NW, int RW, int PART>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_bwd_kernel(const AttnArgs a, int nkvb, int nqb) {
-  constexpr int SMEM = PART == 1   ? 2 * KV_BUF
-                       : PART == 2 ? 4 * TILE
-                       : PART == 3 ? (NW * 2 * KV_BUF > 4 * TILE ? NW * 2 * KV_BUF : 4 * TILE)
-                                   : BWD_SMEM;
-  __shared__ __attribute__((aligned(1024))) _Float16 smem[SMEM];
+  // PART 0-2: the two tile buffers as separate arrays (statically named
+  // buffers, see dq_block); PART 3: one array split per wave.
+  constexpr int BUF = PART == 1 ? KV_BUF : PART == 2 ? 2 * TILE : BWD_BUF;
+  constexpr int SMEM3 = NW * 2 * KV_BUF > 4 * TILE ? NW * 2 * KV_BUF : 4 * TILE;
+  __shared__ __attribute__((aligned(1024))) _Float16 buf0[PART == 3 ? SMEM3 : BUF];
+  __shared__ __attribute__((aligned(1024))) _Float16 buf1[PART == 3 ? 8 : BUF];
   __shared__ float red[NW];
   const int x = blockIdx.x, b = blockIdx.y;
   const int nkvx = PART == 2 ? 0 : nkvb * a.nkv;
   if constexpr (PART != 2) {
     if (x < nkvx) {
       if constexpr (PART == 3)
-        dkdv_block_split<NW>(a, smem, red, x / a.nkv, x % a.nkv, b);
+        dkdv_block_split<NW>(a, buf0, red, x / a.nkv, x % a.nkv, b);
       else
-        dkdv_block<NW, 1>(a, smem, red, x / a.nkv, x % a.nkv, b);
+        dkdv_block<NW, 1>(a, buf0, buf1, red, x / a.nkv, x % a.nkv, b);
       return;
     }
   }
   if constexpr (PART != 1) {
     const int y = x - nkvx;
-    dq_block<NW, RW>(a, smem, nqb - 1 - y / a.nq, y % a.nq, b);
+    if constexpr (PART == 3)
+      dq_block<NW, RW>(a, buf0, buf0 + 2 * TILE, nqb - 1 - y / a.nq, y % a.nq, b);
+    else
+      dq_block<NW, RW>(a, buf0, buf1, nqb - 1 - y / a.nq, y % a.nq, b);
   }
 }
 

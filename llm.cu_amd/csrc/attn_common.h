@@ -129,6 +129,25 @@ __device__ __forceinline__ half8 frag_tr(const _Float16* t, int d0, int j, int l
   return x;
 }
 
+// Max / sum over the four lanes c, c + 16, c + 32, c + 48 (the key groups
+// g of one query column c) with gfx950's lane-swap VALU instructions
+// instead of LDS permutes: after v_permlane32_swap / v_permlane16_swap of a
+// value with itself, lane i holds x[i] and x[i ^ 32] (x[i ^ 16]) in its two
+// results, so one max or add finishes each step; every lane gets the same
+// bits (min/max and a + b are symmetric).
+__device__ __forceinline__ float xg_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xg_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // B fragment built from two accumulator tiles (see the file comment).
 __device__ __forceinline__ half8 pair_frag(const floatx4& a, const floatx4& b) {
   half8 r;
