@@ -12,6 +12,7 @@
 #include <math.h>
 #include <string.h>
 
+#include <mutex>
 #include <vector>
 
 #include "ctx.h"
@@ -54,6 +55,65 @@ struct Temps {
     for (void* p : ptrs) (void)hipFreeAsync(p, st);
   }
 };
+
+// Device workspace of llmt_attention_block_bwd, one per (device, stream),
+// kept for the life of the process and grown on demand: a new size waits for
+// the stream to finish with the old buffer, frees it and allocates the new
+// one (hipMalloc), so a steady caller allocates nothing per call and leaves
+// the GPU no idle gap between calls.  Calls on one stream are ordered by the
+// stream; calls on different streams use different workspaces.  The RoPE
+// tables of the last (S, theta) stay at its start and are rebuilt only when
+// either changes.  Host threads must not issue calls on one stream at once.
+struct BlockWs {
+  int dev = -1;
+  hipStream_t st = nullptr;
+  char* base = nullptr;
+  size_t cap = 0, used = 0;
+  int rope_S = 0;
+  double rope_theta = 0.0;
+  // sub-buffer of n elements, 256-byte aligned (nullptr past the capacity)
+  template <class T>
+  T* get(size_t n) {
+    const size_t off = (used + 255) & ~(size_t)255;
+    if (off + n * sizeof(T) > cap) return nullptr;
+    used = off + n * sizeof(T);
+    return reinterpret_cast<T*>(base + off);
+  }
+};
+static std::mutex g_ws_mu;
+static std::vector<BlockWs*> g_ws;
+
+static hipError_t block_ws(hipStream_t st, size_t bytes, BlockWs** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  BlockWs* w = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    for (BlockWs* x : g_ws)
+      if (x->dev == dev && x->st == st) w = x;
+    if (!w) {
+      w = new BlockWs;
+      w->dev = dev;
+      w->st = st;
+      g_ws.push_back(w);
+    }
+  }
+  if (bytes > w->cap) {
+    if (w->base) {
+      if ((e = hipStreamSynchronize(st)) != hipSuccess) return e;
+      if ((e = hipFree(w->base)) != hipSuccess) return e;
+      w->base = nullptr;
+      w->cap = 0;
+    }
+    if ((e = hipMalloc((void**)&w->base, bytes)) != hipSuccess) return e;
+    w->cap = bytes;
+    w->rope_S = 0;
+  }
+  w->used = 0;
+  *out = w;
+  return hipSuccess;
+}
 
 extern "C" {
 
@@ -264,21 +324,30 @@ int llmt_attention_block_bwd(const void* q_raw, const void* k_raw, const void* v
           "llmt_attention_block_bwd: bad arguments");
   hipStream_t st = (hipStream_t)stream;
   const int T = B * S, Q = nq * kHeadDim, KV = nkv * kHeadDim;
-  Temps tmp(st);
-  _Float16* q16 = tmp.get<_Float16>((size_t)T * Q);
-  _Float16* k16 = tmp.get<_Float16>((size_t)T * KV);
-  _Float16* o16 = tmp.get<_Float16>((size_t)T * Q);
-  float* lse = tmp.get<float>((size_t)B * nq * S);
-  float* delta = tmp.get<float>((size_t)B * nq * S);
-  float* dsc = tmp.get<float>((size_t)T * nq);
-  _Float16* dO16 = tmp.get<_Float16>((size_t)T * Q);
-  float* dq = tmp.get<float>((size_t)T * Q);
-  float* dk = tmp.get<float>((size_t)T * KV);
-  float* cosT = tmp.get<float>((size_t)S * 64);
-  float* sinT = tmp.get<float>((size_t)S * 64);
+  const size_t f16 = sizeof(_Float16), f32 = sizeof(float);
+  const size_t need = 11 * 256 + (size_t)S * 64 * f32 * 2 + (size_t)T * Q * f16 * 3 +
+                      (size_t)T * KV * f16 + (size_t)B * nq * S * f32 * 2 + (size_t)T * nq * f32 +
+                      (size_t)T * Q * f32 + (size_t)T * KV * f32;
+  BlockWs* ws = nullptr;
+  TRY_HIP(block_ws(st, need, &ws));
+  float* cosT = ws->get<float>((size_t)S * 64);
+  float* sinT = ws->get<float>((size_t)S * 64);
+  _Float16* q16 = ws->get<_Float16>((size_t)T * Q);
+  _Float16* k16 = ws->get<_Float16>((size_t)T * KV);
+  _Float16* o16 = ws->get<_Float16>((size_t)T * Q);
+  float* lse = ws->get<float>((size_t)B * nq * S);
+  float* delta = ws->get<float>((size_t)B * nq * S);
+  float* dsc = ws->get<float>((size_t)T * nq);
+  _Float16* dO16 = ws->get<_Float16>((size_t)T * Q);
+  float* dq = ws->get<float>((size_t)T * Q);
+  float* dk = ws->get<float>((size_t)T * KV);
   TRY_ARG(q16 && k16 && o16 && lse && delta && dsc && dO16 && dq && dk && cosT && sinT,
-          "llmt_attention_block_bwd: out of memory");
-  TRY_HIP(rope_tables(S, (double)theta, cosT, sinT, st));
+          "llmt_attention_block_bwd: workspace layout");
+  if (ws->rope_S != S || ws->rope_theta != (double)theta) {
+    TRY_HIP(rope_tables(S, (double)theta, cosT, sinT, st));
+    ws->rope_S = S;
+    ws->rope_theta = (double)theta;
+  }
   TRY_HIP(head_norm_rope((const _Float16*)q_raw, q_norm, cosT, sinT, S, nq, T, eps, q16, st));
   TRY_HIP(head_norm_rope((const _Float16*)k_raw, k_norm, cosT, sinT, S, nkv, T, eps, k16, st));
   AttnArgs a{};
