@@ -348,8 +348,9 @@ int llmt_attention_block_bwd(const void* q_raw, const void* k_raw, const void* v
     ws->rope_S = S;
     ws->rope_theta = (double)theta;
   }
-  TRY_HIP(head_norm_rope((const _Float16*)q_raw, q_norm, cosT, sinT, S, nq, T, eps, q16, st));
-  TRY_HIP(head_norm_rope((const _Float16*)k_raw, k_norm, cosT, sinT, S, nkv, T, eps, k16, st));
+  const HeadRows fw[2] = {{(const _Float16*)q_raw, q_norm, nullptr, q16, nq},
+                          {(const _Float16*)k_raw, k_norm, nullptr, k16, nkv}};
+  TRY_HIP(head_norm_rope(fw, 2, cosT, sinT, S, T, eps, st));
   AttnArgs a{};
   a.q = q16;
   a.ldq = Q;
@@ -376,10 +377,9 @@ int llmt_attention_block_bwd(const void* q_raw, const void* k_raw, const void* v
   a.dv = dv;
   a.ldgkv = KV;
   TRY_HIP(attn_bwd(a, B, st));
-  TRY_HIP(head_norm_rope_bwd(dq, (const _Float16*)q_raw, q_norm, cosT, sinT, S, nq, T, eps, dq_raw,
-                             st));
-  TRY_HIP(head_norm_rope_bwd(dk, (const _Float16*)k_raw, k_norm, cosT, sinT, S, nkv, T, eps,
-                             dk_raw, st));
+  const HeadRows bw[2] = {{(const _Float16*)q_raw, q_norm, dq, dq_raw, nq},
+                          {(const _Float16*)k_raw, k_norm, dk, dk_raw, nkv}};
+  TRY_HIP(head_norm_rope_bwd(bw, 2, cosT, sinT, S, T, eps, st));
   return LLMT_OK;
 }
 

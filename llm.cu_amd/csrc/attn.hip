@@ -179,52 +179,63 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnArgs a) {
 // Per token row, 16 lanes per head (lane j: dims 8 j .. 8 j + 7, 16-byte
 // accesses): delta[b, h, s] = sum_d dO * O, and dO16 = fp16(dO * sc) with sc
 // the power-of-two scale of the head's max |dO|, dsc[b, h, s] = 1 / sc (0 for
-// an all-zero head row).
+// an all-zero head row).  A workgroup of 256 threads covers DR token rows x
+// 16 heads a pass, every load of a pass issued before its math.
+constexpr int DR = 4;
 template <typename TD>
 __global__ __launch_bounds__(256) void attn_delta_kernel(const TD* __restrict__ dO, long long ldd,
                                                          const _Float16* __restrict__ o,
-                                                         long long ldo, int nq, int S,
+                                                         long long ldo, int nq, int S, int T,
                                                          float* __restrict__ delta,
                                                          _Float16* __restrict__ dO16,
                                                          long long ld16, float* __restrict__ dsc) {
-  const int t = blockIdx.x;
   const int j = threadIdx.x & 15;
-  const int b = t / S, s = t - b * S;
   for (int h = threadIdx.x >> 4; h < nq; h += 16) {  // whole 16-lane groups
-    const TD* d = dO + (long long)t * ldd + h * HD + 8 * j;
-    float dv[8];
-    if constexpr (sizeof(TD) == 2) {
-      const half8 x = *reinterpret_cast<const half8*>(d);
+    float dv[DR][8];
+    half8 ov[DR];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) dv[i] = (float)x[i];
-    } else {
-      const float4 x0 = *reinterpret_cast<const float4*>(d);
-      const float4 x1 = *reinterpret_cast<const float4*>(d + 4);
-      dv[0] = x0.x; dv[1] = x0.y; dv[2] = x0.z; dv[3] = x0.w;
-      dv[4] = x1.x; dv[5] = x1.y; dv[6] = x1.z; dv[7] = x1.w;
-    }
-    const half8 ov = *reinterpret_cast<const half8*>(o + (long long)t * ldo + h * HD + 8 * j);
-    float v = 0.f, amax = 0.f;
+    for (int i = 0; i < DR; ++i) {
+      const long long t = min((long long)blockIdx.x * DR + i, (long long)T - 1);
+      const TD* d = dO + t * ldd + h * HD + 8 * j;
+      if constexpr (sizeof(TD) == 2) {
+        const half8 x = *reinterpret_cast<const half8*>(d);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      v += dv[i] * (float)ov[i];
-      amax = fmaxf(amax, fabsf(dv[i]));
+        for (int e = 0; e < 8; ++e) dv[i][e] = (float)x[e];
+      } else {
+        const float4 x0 = *reinterpret_cast<const float4*>(d);
+        const float4 x1 = *reinterpret_cast<const float4*>(d + 4);
+        dv[i][0] = x0.x; dv[i][1] = x0.y; dv[i][2] = x0.z; dv[i][3] = x0.w;
+        dv[i][4] = x1.x; dv[i][5] = x1.y; dv[i][6] = x1.z; dv[i][7] = x1.w;
+      }
+      ov[i] = *reinterpret_cast<const half8*>(o + t * ldo + h * HD + 8 * j);
     }
 #pragma unroll
-    for (int m = 8; m >= 1; m >>= 1) {
-      v += __shfl_xor(v, m, 64);
-      amax = fmaxf(amax, __shfl_xor(amax, m, 64));
-    }
-    const float sc = pow2_scale_for(amax, kDoScaleExp);
-    const long long bhs = ((long long)b * nq + h) * S + s;
-    if (j == 0) {
-      delta[bhs] = v;
-      dsc[bhs] = pow2_inv_scale_for(amax, kDoScaleExp);
-    }
-    half8 o16;
+    for (int i = 0; i < DR; ++i) {
+      const long long t = (long long)blockIdx.x * DR + i;
+      float v = 0.f, amax = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o16[i] = (_Float16)(dv[i] * sc);
-    *reinterpret_cast<half8*>(dO16 + (long long)t * ld16 + h * HD + 8 * j) = o16;
+      for (int e = 0; e < 8; ++e) {
+        v += dv[i][e] * (float)ov[i][e];
+        amax = fmaxf(amax, fabsf(dv[i][e]));
+      }
+#pragma unroll
+      for (int m = 8; m >= 1; m >>= 1) {
+        v += __shfl_xor(v, m, 64);
+        amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+      }
+      if (t >= T) continue;  // whole 16-lane groups (after the group reductions)
+      const int b = (int)((unsigned)t / (unsigned)S), s = (int)t - b * S;  // T < 2^31
+      const float sc = pow2_scale_for(amax, kDoScaleExp);
+      const long long bhs = ((long long)b * nq + h) * S + s;
+      if (j == 0) {
+        delta[bhs] = v;
+        dsc[bhs] = pow2_inv_scale_for(amax, kDoScaleExp);
+      }
+      half8 o16;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o16[e] = (_Float16)(dv[i][e] * sc);
+      *reinterpret_cast<half8*>(dO16 + t * ld16 + h * HD + 8 * j) = o16;
+    }
   }
 }
 
@@ -247,12 +258,13 @@ hipError_t attn_delta(const void* dO, int dO_is_f16, long long ldd, const _Float
     set_error("attn_delta: dO, O and dO16 rows need 16-byte alignment");
     return hipErrorInvalidValue;
   }
+  const dim3 grid((T + DR - 1) / DR);
   if (dO_is_f16)
-    hipLaunchKernelGGL(attn_delta_kernel<_Float16>, dim3(T), dim3(256), 0, st,
-                       (const _Float16*)dO, ldd, o, ldo, nq, S, delta, dO16, ld16, dsc);
+    hipLaunchKernelGGL(attn_delta_kernel<_Float16>, grid, dim3(256), 0, st, (const _Float16*)dO,
+                       ldd, o, ldo, nq, S, T, delta, dO16, ld16, dsc);
   else
-    hipLaunchKernelGGL(attn_delta_kernel<float>, dim3(T), dim3(256), 0, st, (const float*)dO, ldd,
-                       o, ldo, nq, S, delta, dO16, ld16, dsc);
+    hipLaunchKernelGGL(attn_delta_kernel<float>, grid, dim3(256), 0, st, (const float*)dO, ldd, o,
+                       ldo, nq, S, T, delta, dO16, ld16, dsc);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }

@@ -185,11 +185,18 @@ hipError_t resid_norm(const RowIn& in, const float* x_res, const float* w, float
 hipError_t rope_tables(int S, double theta, float* cosT, float* sinT, hipStream_t st);
 // Per-head QK-RMSNorm + RoPE of [T, nh, 128] fp16 rows (weights w [128]),
 // and its backward from dy fp32 [T, nh, 128] to dx fp32 (x: the raw rows).
-hipError_t head_norm_rope(const _Float16* x, const float* w, const float* cosT, const float* sinT,
-                          int S, int nh, int T, float eps, _Float16* out, hipStream_t st);
-hipError_t head_norm_rope_bwd(const float* dy, const _Float16* x, const float* w,
-                              const float* cosT, const float* sinT, int S, int nh, int T,
-                              float eps, float* dx, hipStream_t st);
+// Up to two tensors (q and k) in one launch.
+struct HeadRows {
+  const _Float16* x;  // raw rows
+  const float* w;     // norm weights [128]
+  const float* dy;    // backward: upstream gradient (unused in the forward)
+  void* out;          // forward: fp16 normed, rotated rows; backward: fp32 dx
+  int nh;
+};
+hipError_t head_norm_rope(const HeadRows* segs, int nseg, const float* cosT, const float* sinT,
+                          int S, int T, float eps, hipStream_t st);
+hipError_t head_norm_rope_bwd(const HeadRows* segs, int nseg, const float* cosT,
+                              const float* sinT, int S, int T, float eps, hipStream_t st);
 hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st);
 hipError_t swiglu_bwd(const RowIn& in, const float* rinv_in, const float* gu, int I, int T,
                       _Float16* dgu16, float* rinv_out, hipStream_t st);

@@ -20,6 +20,7 @@
 // next to the operand and the consuming epilogue multiplies the GEMM result
 // row by it.  The scale is a power of two, so applying and removing it is
 // exact in fp32.
+#include <algorithm>
 #include <stdlib.h>
 
 #include "ops.h"
@@ -466,69 +467,116 @@ __device__ __forceinline__ float4 ldh4(const _Float16* p) {
   return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
 }
 
-__global__ __launch_bounds__(RT) void head_norm_rope_kernel(const _Float16* __restrict__ x,
-                                                            const float* __restrict__ w,
-                                                            const float* __restrict__ cosT,
-                                                            const float* __restrict__ sinT, int S,
-                                                            int nh, int T, float eps,
-                                                            _Float16* __restrict__ out) {
+// Launch arguments: tensor blockIdx.y of segs; every 16-lane group owns HN_R
+// rows spaced a grid stride apart, all of whose loads are issued before the
+// math (one memory round trip per group of rows).
+constexpr int HN_R = 4;
+struct HeadNormArgs {
+  HeadRows seg[2];
+  const float* cosT;
+  const float* sinT;
+  int S, T;
+  float eps;
+};
+
+__global__ __launch_bounds__(RT) void head_norm_rope_kernel(const HeadNormArgs a) {
+  const HeadRows& sg = a.seg[blockIdx.y];
   const int j = threadIdx.x & 15;
-  const long long row = (long long)blockIdx.x * HN_ROWS + (threadIdx.x >> 4);  // (token, head)
-  if (row >= (long long)T * nh) return;  // whole 16-lane groups
-  const int pos = (int)(row / nh) % S;
-  const float4 cs = ld4(cosT + pos * (HD / 2) + 4 * j), sn = ld4(sinT + pos * (HD / 2) + 4 * j);
-  const float4 x0 = ldh4(x + row * HD + 4 * j), x1 = ldh4(x + row * HD + 64 + 4 * j);
-  const float4 w0 = ld4(w + 4 * j), w1 = ld4(w + 64 + 4 * j);
-  const float ss = x0.x * x0.x + x0.y * x0.y + x0.z * x0.z + x0.w * x0.w + x1.x * x1.x +
-                   x1.y * x1.y + x1.z * x1.z + x1.w * x1.w;
-  const float r = rsqrtf(sum16(ss) / HD + eps);
-  const float a0[4] = {x0.x * r * w0.x, x0.y * r * w0.y, x0.z * r * w0.z, x0.w * r * w0.w};
-  const float a1[4] = {x1.x * r * w1.x, x1.y * r * w1.y, x1.z * r * w1.z, x1.w * r * w1.w};
-  const float c[4] = {cs.x, cs.y, cs.z, cs.w}, sg[4] = {sn.x, sn.y, sn.z, sn.w};
-  half4 o0, o1;
+  const long long nrows = (long long)a.T * sg.nh;
+  const long long r0 = (long long)blockIdx.x * HN_ROWS + (threadIdx.x >> 4);
+  const long long stride = (long long)gridDim.x * HN_ROWS;
+  const float4 w0 = ld4(sg.w + 4 * j), w1 = ld4(sg.w + 64 + 4 * j);
+  float4 x0[HN_R], x1[HN_R], cs[HN_R], sn[HN_R];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    o0[i] = (_Float16)(a0[i] * c[i] - a1[i] * sg[i]);
-    o1[i] = (_Float16)(a1[i] * c[i] + a0[i] * sg[i]);
+  for (int i = 0; i < HN_R; ++i) {
+    const long long row = min(r0 + i * stride, nrows - 1);
+    // 32-bit division (rows < 2^31, checked on the host): the 64-bit form
+    // expands to about a hundred instructions a row
+    const int pos = (int)(((unsigned)row / (unsigned)sg.nh) % (unsigned)a.S);
+    cs[i] = ld4(a.cosT + pos * (HD / 2) + 4 * j);
+    sn[i] = ld4(a.sinT + pos * (HD / 2) + 4 * j);
+    x0[i] = ldh4(sg.x + row * HD + 4 * j);
+    x1[i] = ldh4(sg.x + row * HD + 64 + 4 * j);
   }
-  *reinterpret_cast<half4*>(out + row * HD + 4 * j) = o0;
-  *reinterpret_cast<half4*>(out + row * HD + 64 + 4 * j) = o1;
+  _Float16* out = static_cast<_Float16*>(sg.out);
+#pragma unroll
+  for (int i = 0; i < HN_R; ++i) {
+    const long long row = r0 + i * stride;
+    const float ss = x0[i].x * x0[i].x + x0[i].y * x0[i].y + x0[i].z * x0[i].z +
+                     x0[i].w * x0[i].w + x1[i].x * x1[i].x + x1[i].y * x1[i].y +
+                     x1[i].z * x1[i].z + x1[i].w * x1[i].w;
+    const float r = rsqrtf(sum16(ss) / HD + a.eps);
+    if (row >= nrows) continue;  // whole 16-lane groups (after the group sum)
+    const float a0[4] = {x0[i].x * r * w0.x, x0[i].y * r * w0.y, x0[i].z * r * w0.z,
+                         x0[i].w * r * w0.w};
+    const float a1[4] = {x1[i].x * r * w1.x, x1[i].y * r * w1.y, x1[i].z * r * w1.z,
+                         x1[i].w * r * w1.w};
+    const float c[4] = {cs[i].x, cs[i].y, cs[i].z, cs[i].w};
+    const float s4[4] = {sn[i].x, sn[i].y, sn[i].z, sn[i].w};
+    half4 o0, o1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o0[e] = (_Float16)(a0[e] * c[e] - a1[e] * s4[e]);
+      o1[e] = (_Float16)(a1[e] * c[e] + a0[e] * s4[e]);
+    }
+    *reinterpret_cast<half4*>(out + row * HD + 4 * j) = o0;
+    *reinterpret_cast<half4*>(out + row * HD + 64 + 4 * j) = o1;
+  }
 }
 
-__global__ __launch_bounds__(RT) void head_norm_rope_bwd_kernel(
-    const float* __restrict__ dy, const _Float16* __restrict__ x, const float* __restrict__ w,
-    const float* __restrict__ cosT, const float* __restrict__ sinT, int S, int nh, int T, float eps,
-    float* __restrict__ dx) {
+__global__ __launch_bounds__(RT) void head_norm_rope_bwd_kernel(const HeadNormArgs a) {
+  const HeadRows& sg = a.seg[blockIdx.y];
   const int j = threadIdx.x & 15;
-  const long long row = (long long)blockIdx.x * HN_ROWS + (threadIdx.x >> 4);
-  if (row >= (long long)T * nh) return;  // whole 16-lane groups
-  const int pos = (int)(row / nh) % S;
-  const float4 cs = ld4(cosT + pos * (HD / 2) + 4 * j), sn = ld4(sinT + pos * (HD / 2) + 4 * j);
-  const float4 d0 = ld4(dy + row * HD + 4 * j), d1 = ld4(dy + row * HD + 64 + 4 * j);
-  const float4 x0 = ldh4(x + row * HD + 4 * j), x1 = ldh4(x + row * HD + 64 + 4 * j);
-  const float4 w0 = ld4(w + 4 * j), w1 = ld4(w + 64 + 4 * j);
-  const float c[4] = {cs.x, cs.y, cs.z, cs.w}, sg[4] = {sn.x, sn.y, sn.z, sn.w};
-  const float dd0[4] = {d0.x, d0.y, d0.z, d0.w}, dd1[4] = {d1.x, d1.y, d1.z, d1.w};
-  const float xx0[4] = {x0.x, x0.y, x0.z, x0.w}, xx1[4] = {x1.x, x1.y, x1.z, x1.w};
+  const long long nrows = (long long)a.T * sg.nh;
+  const long long r0 = (long long)blockIdx.x * HN_ROWS + (threadIdx.x >> 4);
+  const long long stride = (long long)gridDim.x * HN_ROWS;
+  const float4 w0 = ld4(sg.w + 4 * j), w1 = ld4(sg.w + 64 + 4 * j);
   const float ww0[4] = {w0.x, w0.y, w0.z, w0.w}, ww1[4] = {w1.x, w1.y, w1.z, w1.w};
-  float n0[4], n1[4], ss = 0.f, dot = 0.f;
+  float4 d0[HN_R], d1[HN_R], x0[HN_R], x1[HN_R], cs[HN_R], sn[HN_R];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    n0[i] = dd0[i] * c[i] + dd1[i] * sg[i];
-    n1[i] = dd1[i] * c[i] - dd0[i] * sg[i];
-    ss += xx0[i] * xx0[i] + xx1[i] * xx1[i];
-    dot += n0[i] * ww0[i] * xx0[i] + n1[i] * ww1[i] * xx1[i];
+  for (int i = 0; i < HN_R; ++i) {
+    const long long row = min(r0 + i * stride, nrows - 1);
+    // 32-bit division (rows < 2^31, checked on the host): the 64-bit form
+    // expands to about a hundred instructions a row
+    const int pos = (int)(((unsigned)row / (unsigned)sg.nh) % (unsigned)a.S);
+    cs[i] = ld4(a.cosT + pos * (HD / 2) + 4 * j);
+    sn[i] = ld4(a.sinT + pos * (HD / 2) + 4 * j);
+    d0[i] = ld4(sg.dy + row * HD + 4 * j);
+    d1[i] = ld4(sg.dy + row * HD + 64 + 4 * j);
+    x0[i] = ldh4(sg.x + row * HD + 4 * j);
+    x1[i] = ldh4(sg.x + row * HD + 64 + 4 * j);
   }
-  const float r = rsqrtf(sum16(ss) / HD + eps);
-  const float coef = r * r / HD * sum16(dot);
-  float o0[4], o1[4];
+  float* dx = static_cast<float*>(sg.out);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    o0[i] = r * (n0[i] * ww0[i] - coef * xx0[i]);
-    o1[i] = r * (n1[i] * ww1[i] - coef * xx1[i]);
+  for (int i = 0; i < HN_R; ++i) {
+    const long long row = r0 + i * stride;
+    const float c[4] = {cs[i].x, cs[i].y, cs[i].z, cs[i].w};
+    const float s4[4] = {sn[i].x, sn[i].y, sn[i].z, sn[i].w};
+    const float dd0[4] = {d0[i].x, d0[i].y, d0[i].z, d0[i].w};
+    const float dd1[4] = {d1[i].x, d1[i].y, d1[i].z, d1[i].w};
+    const float xx0[4] = {x0[i].x, x0[i].y, x0[i].z, x0[i].w};
+    const float xx1[4] = {x1[i].x, x1[i].y, x1[i].z, x1[i].w};
+    float n0[4], n1[4], ss = 0.f, dot = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      n0[e] = dd0[e] * c[e] + dd1[e] * s4[e];
+      n1[e] = dd1[e] * c[e] - dd0[e] * s4[e];
+      ss += xx0[e] * xx0[e] + xx1[e] * xx1[e];
+      dot += n0[e] * ww0[e] * xx0[e] + n1[e] * ww1[e] * xx1[e];
+    }
+    const float r = rsqrtf(sum16(ss) / HD + a.eps);
+    const float coef = r * r / HD * sum16(dot);
+    if (row >= nrows) continue;  // whole 16-lane groups (after the group sums)
+    float o0[4], o1[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o0[e] = r * (n0[e] * ww0[e] - coef * xx0[e]);
+      o1[e] = r * (n1[e] * ww1[e] - coef * xx1[e]);
+    }
+    *reinterpret_cast<float4*>(dx + row * HD + 4 * j) = make_float4(o0[0], o0[1], o0[2], o0[3]);
+    *reinterpret_cast<float4*>(dx + row * HD + 64 + 4 * j) =
+        make_float4(o1[0], o1[1], o1[2], o1[3]);
   }
-  *reinterpret_cast<float4*>(dx + row * HD + 4 * j) = make_float4(o0[0], o0[1], o0[2], o0[3]);
-  *reinterpret_cast<float4*>(dx + row * HD + 64 + 4 * j) = make_float4(o1[0], o1[1], o1[2], o1[3]);
 }
 
 // ---------------------------------------------------------------- backward
@@ -1158,31 +1206,54 @@ hipError_t rope_tables(int S, double theta, float* cosT, float* sinT, hipStream_
   return hipSuccess;
 }
 
-hipError_t head_norm_rope(const _Float16* x, const float* w, const float* cosT, const float* sinT,
-                          int S, int nh, int T, float eps, _Float16* out, hipStream_t st) {
-  const long long rows = (long long)T * nh;
-  if ((uintptr_t)w % 16 || ((uintptr_t)x | (uintptr_t)out) % 8) {
-    set_error("head_norm_rope: w needs 16-byte and x, out 8-byte alignment");
+static hipError_t head_norm_launch(const HeadRows* segs, int nseg, const float* cosT,
+                                   const float* sinT, int S, int T, float eps, bool bwd,
+                                   hipStream_t st) {
+  const char* who = bwd ? "head_norm_rope_bwd" : "head_norm_rope";
+  if (nseg < 1 || nseg > 2 || T <= 0 || S <= 0) {
+    set_error("%s: %d tensors, T=%d, S=%d", who, nseg, T, S);
     return hipErrorInvalidValue;
   }
-  hipLaunchKernelGGL(head_norm_rope_kernel, dim3((unsigned)((rows + HN_ROWS - 1) / HN_ROWS)),
-                     dim3(RT), 0, st, x, w, cosT, sinT, S, nh, T, eps, out);
+  HeadNormArgs a{};
+  long long maxrows = 0;
+  for (int i = 0; i < nseg; ++i) {
+    const HeadRows& r = segs[i];
+    const bool al = (uintptr_t)r.w % 16 == 0 && (uintptr_t)r.x % 8 == 0 &&
+                    (uintptr_t)r.out % (bwd ? 16 : 8) == 0 && (!bwd || (uintptr_t)r.dy % 16 == 0);
+    if (!r.x || !r.w || !r.out || (bwd && !r.dy) || r.nh <= 0 || !al) {
+      set_error("%s: tensor %d: bad pointers, alignment (w, dy, fp32 out 16 B; x, fp16 out 8 B) "
+                "or nh=%d", who, i, r.nh);
+      return hipErrorInvalidValue;
+    }
+    if ((long long)T * r.nh >= (1LL << 31)) {
+      set_error("%s: %lld rows (at most 2^31 - 1)", who, (long long)T * r.nh);
+      return hipErrorInvalidValue;
+    }
+    a.seg[i] = r;
+    maxrows = std::max(maxrows, (long long)T * r.nh);
+  }
+  a.cosT = cosT;
+  a.sinT = sinT;
+  a.S = S;
+  a.T = T;
+  a.eps = eps;
+  const dim3 grid((unsigned)((maxrows + HN_ROWS * HN_R - 1) / (HN_ROWS * HN_R)), nseg);
+  if (bwd)
+    hipLaunchKernelGGL(head_norm_rope_bwd_kernel, grid, dim3(RT), 0, st, a);
+  else
+    hipLaunchKernelGGL(head_norm_rope_kernel, grid, dim3(RT), 0, st, a);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
 
-hipError_t head_norm_rope_bwd(const float* dy, const _Float16* x, const float* w,
-                              const float* cosT, const float* sinT, int S, int nh, int T,
-                              float eps, float* dx, hipStream_t st) {
-  const long long rows = (long long)T * nh;
-  if (((uintptr_t)dy | (uintptr_t)dx | (uintptr_t)w) % 16 || (uintptr_t)x % 8) {
-    set_error("head_norm_rope_bwd: dy, dx, w need 16-byte and x 8-byte alignment");
-    return hipErrorInvalidValue;
-  }
-  hipLaunchKernelGGL(head_norm_rope_bwd_kernel, dim3((unsigned)((rows + HN_ROWS - 1) / HN_ROWS)),
-                     dim3(RT), 0, st, dy, x, w, cosT, sinT, S, nh, T, eps, dx);
-  LLMT_LAUNCH_CHECK();
-  return hipSuccess;
+hipError_t head_norm_rope(const HeadRows* segs, int nseg, const float* cosT, const float* sinT,
+                          int S, int T, float eps, hipStream_t st) {
+  return head_norm_launch(segs, nseg, cosT, sinT, S, T, eps, false, st);
+}
+
+hipError_t head_norm_rope_bwd(const HeadRows* segs, int nseg, const float* cosT,
+                              const float* sinT, int S, int T, float eps, hipStream_t st) {
+  return head_norm_launch(segs, nseg, cosT, sinT, S, T, eps, true, st);
 }
 
 hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st) {
