@@ -334,7 +334,7 @@ def bandwidth_kernels(kinds, dims, T):
                      (7 x 4 B; the fp16 operand shadows it also writes are
                      not counted);
       swiglu_bwd     dY [T, I] fp32 (summed GEMM output), gate and up
-                     [T, 2I] fp32 read, dgate | dup [T, 2I] fp16 written;
+                     [T, 2I] fp16 read, dgate | dup [T, 2I] fp16 written;
       norm_bwd       dY, x, residual-gradient in [T, H] fp32 read, residual
                      gradient out fp32 and the fp16 GEMM operand written;
       cross_entropy  logits [T, V] fp32 read once, the fp16 dlogits operand
@@ -343,7 +343,7 @@ def bandwidth_kernels(kinds, dims, T):
     nparam = dims.n_layers * 16 * (3 * H + 2 * dims.n_heads * dims.head_dim +
                                    2 * dims.n_kv_heads * dims.head_dim + H)
     want = {"adamw": 7 * 4 * nparam,
-            "swiglu_bwd": T * I * 4 + T * 2 * I * 4 + T * 2 * I * 2,
+            "swiglu_bwd": T * I * 4 + T * 2 * I * 2 + T * 2 * I * 2,
             "norm_bwd": T * H * (4 + 4 + 4 + 4 + 2),
             "cross_entropy": T * V * (4 + 2)}
     out = {}

@@ -148,14 +148,14 @@ int Ctx::init() {
     Stash& s = stash[l];
     TRY_PTR(s.x_in = alloc_n<float>(T * H));
     TRY_PTR(s.xn = alloc_n<_Float16>(T * H));
-    TRY_PTR(s.qkraw = alloc_n<float>(T * (Q + KV)));
+    TRY_PTR(s.qkraw = alloc_n<_Float16>(T * (Q + KV)));
     TRY_PTR(s.qkv16 = alloc_n<_Float16>(T * NT));
     TRY_PTR(s.h = alloc_n<float>(T * 64));
     TRY_PTR(s.o16 = alloc_n<_Float16>(T * Q));
     TRY_PTR(s.lse = alloc_n<float>((size_t)maxB * nq * S));
     TRY_PTR(s.x_mid = alloc_n<float>(T * H));
     TRY_PTR(s.xn2 = alloc_n<_Float16>(T * H));
-    TRY_PTR(s.gu = alloc_n<float>(T * 2 * I));
+    TRY_PTR(s.gu = alloc_n<_Float16>(T * 2 * I));
   }
   TRY_PTR(x_final = alloc_n<float>(T * H));
   TRY_PTR(xf16 = alloc_n<_Float16>(T * H));

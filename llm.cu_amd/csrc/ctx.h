@@ -62,14 +62,14 @@ struct Layer {
 struct Stash {
   float* x_in;       // [T, H] residual stream at the layer input
   _Float16* xn;      // [T, H] attention-norm output (GEMM / LoRA-A input)
-  float* qkraw;      // [T, Q + KV] q, k before the QK-norm
+  _Float16* qkraw;   // [T, Q + KV] q, k before the QK-norm (fp16)
   _Float16* qkv16;   // [T, Q + 2 KV] normed + rotated q, k and v
   float* h;          // [T, 64] LoRA h = x A^T for q, k, v, o
   _Float16* o16;     // [T, Q] attention output
   float* lse;        // [B, nq, S]
   float* x_mid;      // [T, H] residual after attention
   _Float16* xn2;     // [T, H] FFN-norm output
-  float* gu;         // [T, 2 I] gate, up pre-activations
+  _Float16* gu;      // [T, 2 I] gate, up pre-activations (fp16)
 };
 
 struct GemmOut {
@@ -186,11 +186,13 @@ struct Ctx {
   }
   // C = A B^T over the segments.  direct: split 1 into `direct` (ld ldc).
   // Otherwise the fp32 split-K partials land in `part` and *out describes
-  // them; the consuming row epilogue sums them in split order.  glu16 (with
-  // direct): the fused SwiGLU epilogue also writes fp16(silu(gate) * up)
-  // [M, N / 2] there (gemm_glu_ok shapes only).
+  // them; the consuming row epilogue sums them in split order.  glu16: the
+  // fused SwiGLU epilogue (split 1, gemm_glu_ok shapes only) writes [gate |
+  // up] fp16 [M, N] to gu16 and fp16(silu(gate) * up) [M, N / 2] to glu16
+  // (direct and ldc unused).
   hipError_t gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int nseg, int M, int K,
-                  float* direct, int ldc, GemmOut* out, _Float16* glu16 = nullptr);
+                  float* direct, int ldc, GemmOut* out, _Float16* glu16 = nullptr,
+                  _Float16* gu16 = nullptr);
   // A GEMM's partials as a row-epilogue input with raw h columns
   // [hcol, hcol + nh) and LoRA up-projection terms.
   RowIn row_in(const GemmOut& go, int hcol = 0, int nh = 0, int nterm = 0,

@@ -412,13 +412,13 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const long long row = m0 + wm * 128 + i * 16 + (lane >> 4) * 4 + v;
-        float* crow = C + row * g.ldc + col0;
+        _Float16* grow = g.gu16 + row * (2LL * g.glu) + col0;
         _Float16* arow = g.glu16 + row * g.ldglu + col0;
 #pragma unroll
         for (int jj = 0; jj < NFR / 2; ++jj) {
           const float gt = acc[i][2 * jj][v] * sgu[2 * jj], up = acc[i][2 * jj + 1][v] * sgu[2 * jj + 1];
-          crow[16 * jj] = gt;
-          crow[g.glu + 16 * jj] = up;
+          grow[16 * jj] = (_Float16)gt;
+          grow[g.glu + 16 * jj] = (_Float16)up;
           arow[16 * jj] = (_Float16)(gt / (1.0f + __expf(-gt)) * up);
         }
       }
@@ -608,8 +608,8 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(const GemmArgs g) {
         for (int v = 0; v < 4; ++v) {
           const long long row = m0 + (2 * wr + i) * 16 + (lane >> 4) * 4 + v;
           const float gt = acc[i][2 * jj][v] * sg, up = acc[i][2 * jj + 1][v] * su;
-          C[row * g.ldc + col] = gt;
-          C[row * g.ldc + g.glu + col] = up;
+          g.gu16[row * (2LL * g.glu) + col] = (_Float16)gt;
+          g.gu16[row * (2LL * g.glu) + g.glu + col] = (_Float16)up;
           g.glu16[row * g.ldglu + col] = (_Float16)(gt / (1.0f + __expf(-gt)) * up);
         }
     }
@@ -1063,7 +1063,7 @@ hipError_t gemm_nt(const GemmArgs& g, hipStream_t st) {
       set_error("gemm_nt: segment rows must be a multiple of 16 (%d)", g.seg[i].rows);
       return hipErrorInvalidValue;
     }
-  if (g.glu && !(g.N == 2 * g.glu && g.nseg == 1 && g.split == 1 && g.glu16 &&
+  if (g.glu && !(g.N == 2 * g.glu && g.nseg == 1 && g.split == 1 && g.glu16 && g.gu16 &&
                  gemm_glu_ok(g.M, g.glu, g.K, g.seg[0].is_i8))) {
     set_error("gemm_nt: SwiGLU epilogue needs split 1, one segment, N = 2 x %d", g.glu);
     return hipErrorInvalidValue;

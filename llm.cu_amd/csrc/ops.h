@@ -33,11 +33,13 @@ struct GemmArgs {
   long long split_stride;  // elements between split partials
   int M, N, K, split;
   // glu > 0: fused SwiGLU epilogue (split 1, N = 2 glu, one segment whose
-  // rows [0, glu) are the gate and [glu, 2 glu) the up projection): C gets
-  // [gate | up] as without it, and glu16[m][n] = fp16(silu(gate) * up).
+  // rows [0, glu) are the gate and [glu, 2 glu) the up projection): gu16
+  // gets [gate | up] in fp16 ([M, 2 glu], the backward's stash; C unused)
+  // and glu16[m][n] = fp16(silu(gate) * up), both from the fp32 sums.
   int glu;
   _Float16* glu16;
   int ldglu;
+  _Float16* gu16;
 };
 // The fused SwiGLU epilogue exists for this GEMM shape and weight type.
 bool gemm_glu_ok(int M, int I, int K, bool i8);
@@ -136,7 +138,7 @@ struct QkvPostArgs {
   const float* sinT;  // [S, 64]
   int S, nq, nkv;
   float eps;
-  float* qkraw;      // [T, Q + KV] fp32
+  _Float16* qkraw;   // [T, Q + KV] fp16
   _Float16* qkv16;   // [T, Q + 2 KV]
   float* hbuf;       // [T, 64]: h columns 0..47
 };
@@ -161,7 +163,7 @@ struct NormBwdArgs {
 struct QkBwdArgs {
   const float* dqkv;  // attention grads [T, ld] (dq | dk | dv)
   int ld_dqkv;
-  const float* qkraw;
+  const _Float16* qkraw;  // [T, Q + KV] q, k before the QK-norm (fp16)
   const float* qn;
   const float* kn;
   const float* cosT;
@@ -178,7 +180,7 @@ hipError_t embed_norm(const int* tok, const _Float16* E, int V, int H, const flo
 hipError_t qkv_post(const QkvPostArgs& a, int T, hipStream_t st);
 hipError_t o_post(const RowIn& in, const float* x_in, const float* w, float eps, int H, int T,
                   float* hbuf, float* x_mid, _Float16* xn2, hipStream_t st);
-hipError_t gu_post(const RowIn& in, int I, int T, float* gu, _Float16* a16, hipStream_t st);
+hipError_t gu_post(const RowIn& in, int I, int T, _Float16* gu, _Float16* a16, hipStream_t st);
 hipError_t resid_norm(const RowIn& in, const float* x_res, const float* w, float eps, int H, int T,
                       float* x_out, _Float16* xn, hipStream_t st);
 // cos / sin tables of the half-split RoPE, [S, 64] fp32 each, on the device.
@@ -198,7 +200,7 @@ hipError_t head_norm_rope(const HeadRows* segs, int nseg, const float* cosT, con
 hipError_t head_norm_rope_bwd(const HeadRows* segs, int nseg, const float* cosT,
                               const float* sinT, int S, int T, float eps, hipStream_t st);
 hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st);
-hipError_t swiglu_bwd(const RowIn& in, const float* rinv_in, const float* gu, int I, int T,
+hipError_t swiglu_bwd(const RowIn& in, const float* rinv_in, const _Float16* gu, int I, int T,
                       _Float16* dgu16, float* rinv_out, hipStream_t st);
 // dX of the O projection -> the attention's dO operand: dO16 (row t, head h)
 // = fp16(dO * 2^k) with 2^k the power-of-two scale of that head row,

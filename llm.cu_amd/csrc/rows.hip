@@ -318,9 +318,9 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(const QkvPostArgs a, int 
       out[64 + lane] = (_Float16)v1;
       continue;
     }
-    float* raw = a.qkraw + (long long)t * (Q + KV) + base;
-    raw[lane] = v0;
-    raw[64 + lane] = v1;
+    _Float16* raw = a.qkraw + (long long)t * (Q + KV) + base;
+    raw[lane] = (_Float16)v0;
+    raw[64 + lane] = (_Float16)v1;
     const float r = rsqrtf(wave_sum(v0 * v0 + v1 * v1) / HD + a.eps);
     const int pos = t % a.S;
     const float cs = a.cosT[pos * (HD / 2) + lane], sn = a.sinT[pos * (HD / 2) + lane];
@@ -385,10 +385,11 @@ __global__ __launch_bounds__(RT) void o_post_kernel(const RowIn in,
   }
 }
 
-// After the fused gate/up GEMM: stash g, u (fp32) and a = silu(g) * u
-// (src/kernels/activation.cu:5-18) as the fp16 operand of the down GEMM.
+// After the fused gate/up GEMM: stash g, u (fp16, for the backward) and
+// a = silu(g) * u (src/kernels/activation.cu:5-18) from the fp32 sums as the
+// fp16 operand of the down GEMM.
 __global__ __launch_bounds__(RT) void gu_post_kernel(const RowIn in, int I, long long n4,
-                                                     float* __restrict__ gu,
+                                                     _Float16* __restrict__ gu,
                                                      _Float16* __restrict__ a16) {
   for (long long i = (long long)blockIdx.x * RT + threadIdx.x; i < n4;
        i += (long long)gridDim.x * RT) {
@@ -397,8 +398,8 @@ __global__ __launch_bounds__(RT) void gu_post_kernel(const RowIn in, int I, long
     const float* p = in.part + t * in.ldp + c;
     const float4 g = sum_splits4(p, in.split, in.ss);
     const float4 u = sum_splits4(p + I, in.split, in.ss);
-    *reinterpret_cast<float4*>(gu + t * 2 * I + c) = g;
-    *reinterpret_cast<float4*>(gu + t * 2 * I + I + c) = u;
+    st_h4(gu + t * 2 * I + c, g);
+    st_h4(gu + t * 2 * I + I + c, u);
     half4 o;
     o[0] = (_Float16)(silu(g.x) * u.x);
     o[1] = (_Float16)(silu(g.y) * u.y);
@@ -708,18 +709,18 @@ __global__ __launch_bounds__(RT) void norm_bwd_lora_kernel(const NormBwdArgs a, 
 template <int P>
 __global__ __launch_bounds__(RT) void swiglu_bwd_kernel(const RowIn in,
                                                         const float* __restrict__ rinv_in,
-                                                        const float* __restrict__ gu, int I,
+                                                        const _Float16* __restrict__ gu, int I,
                                                         _Float16* __restrict__ dgu16,
                                                         float* __restrict__ rinv_out) {
   __shared__ float red[2 * RW];
   const int t = blockIdx.x;
-  const float* gr = gu + (long long)t * 2 * I;
+  const _Float16* gr = gu + (long long)t * 2 * I;
   float4 g4[P], u4[P];
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int c = min(4 * ((int)threadIdx.x + p * RT), I - 4);
-    g4[p] = ld4(gr + c);
-    u4[p] = ld4(gr + I + c);
+    g4[p] = ldh4(gr + c);
+    u4[p] = ldh4(gr + I + c);
   }
   const float rs = rinv_in[t];
   float4 v[P];
@@ -940,7 +941,7 @@ __global__ __launch_bounds__(RT) void qk_bwd_kernel(const QkBwdArgs a) {
     ds[base + lane] = r * (n0 * w0 - coef * x0);
     ds[base + 64 + lane] = r * (n1 * w1 - coef * x1);
   };
-  const float* xrow = a.qkraw + (long long)t * (Q + KV);
+  const _Float16* xrow = a.qkraw + (long long)t * (Q + KV);
   if constexpr (HPW > 0) {
     const float wq0 = a.qn[lane], wq1 = a.qn[lane + 64], wk0 = a.kn[lane], wk1 = a.kn[lane + 64];
     float vv[2];
@@ -956,8 +957,8 @@ __global__ __launch_bounds__(RT) void qk_bwd_kernel(const QkBwdArgs a) {
       const int base = (hh < a.nq + a.nkv ? hh : 0) * HD;
       d0[k] = g[base + lane];
       d1[k] = g[base + 64 + lane];
-      x0[k] = xrow[base + lane];
-      x1[k] = xrow[base + 64 + lane];
+      x0[k] = (float)xrow[base + lane];
+      x1[k] = (float)xrow[base + 64 + lane];
     }
 #pragma unroll
     for (int k = 0; k < HPW; ++k)
@@ -1162,7 +1163,7 @@ hipError_t o_post(const RowIn& in, const float* x_in, const float* w, float eps,
   return hipSuccess;
 }
 
-hipError_t gu_post(const RowIn& in, int I, int T, float* gu, _Float16* a16, hipStream_t st) {
+hipError_t gu_post(const RowIn& in, int I, int T, _Float16* gu, _Float16* a16, hipStream_t st) {
   if (!row_in_ok(in, I, "gu_post") || in.nterm) return hipErrorInvalidValue;
   const long long n4 = (long long)T * (I / 4);
   hipLaunchKernelGGL(gu_post_kernel, dim3(grid_elems(n4)), dim3(RT), 0, st, in, I, n4, gu, a16);
@@ -1286,7 +1287,7 @@ hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st) {
   return hipSuccess;
 }
 
-hipError_t swiglu_bwd(const RowIn& in, const float* rinv_in, const float* gu, int I, int T,
+hipError_t swiglu_bwd(const RowIn& in, const float* rinv_in, const _Float16* gu, int I, int T,
                       _Float16* dgu16, float* rinv_out, hipStream_t st) {
   if (!row_in_ok(in, I, "swiglu_bwd")) return hipErrorInvalidValue;
   const int P = (I + 4 * RT - 1) / (4 * RT);

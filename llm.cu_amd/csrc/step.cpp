@@ -49,7 +49,7 @@ Ctx::~Ctx() {
 // ------------------------------------------------------------------ launches
 
 hipError_t Ctx::gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int nseg, int M, int K,
-                     float* direct, int ldc, GemmOut* out, _Float16* glu16) {
+                     float* direct, int ldc, GemmOut* out, _Float16* glu16, _Float16* gu16) {
   GemmArgs g{};
   g.A = A;
   g.lda = lda;
@@ -58,16 +58,20 @@ hipError_t Ctx::gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int 
   gemm_finalize_segments(g);
   g.M = M;
   g.K = K;
-  if (direct) {
+  if (glu16) {
+    g.split = 1;
+    g.C = nullptr;
+    g.ldc = 0;
+    g.split_stride = 0;
+    g.glu = g.N / 2;
+    g.glu16 = glu16;
+    g.ldglu = g.N / 2;
+    g.gu16 = gu16;
+  } else if (direct) {
     g.split = 1;
     g.C = direct;
     g.ldc = ldc;
     g.split_stride = 0;
-    if (glu16) {
-      g.glu = g.N / 2;
-      g.glu16 = glu16;
-      g.ldglu = g.N / 2;
-    }
   } else {
     g.split = gemm_pick_split(M, g.N, K, 64);
     g.C = part;
@@ -208,11 +212,11 @@ hipError_t Ctx::layer_fwd(int l, int B, const float* next_w, float* x_out, _Floa
   // gate/up, SwiGLU (in the GEMM epilogue where the large-tile kernel runs)
   BSeg sg[1] = {wseg(w.wgu)};
   if (gemm_glu_ok(T, I, H, sg[0].is_i8)) {
-    LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn2, H, sg, 1, T, H, s.gu, 2 * I, nullptr, a16));
+    LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn2, H, sg, 1, T, H, nullptr, 0, nullptr, a16, s.gu));
   } else {
     LLMT_HIP_TRY(gemm(CAT_GEMM_FWD, s.xn2, H, sg, 1, T, H, nullptr, 0, &go));
     const RowIn ri = row_in(go);
-    float* gu = s.gu;
+    _Float16* gu = s.gu;
     _Float16* a = a16;
     const int Ii = I;
     LLMT_HIP_TRY(run(CAT_ROWS, "gu_post", [=](hipStream_t q) { return gu_post(ri, Ii, T, gu, a, q); }));
@@ -346,7 +350,8 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, sd, 1, T, H, nullptr, 0, &go_));
   {
     const RowIn ri = row_in(go_);
-    const float *ri_in = rinv, *gu = s.gu;
+    const float* ri_in = rinv;
+    const _Float16* gu = s.gu;
     _Float16* d16 = dgu16;
     float* r2 = rinv2;
     const int Ii = I;
