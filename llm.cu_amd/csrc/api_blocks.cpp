@@ -310,10 +310,12 @@ int llmt_attention_bwd(const void* q, const void* k, const void* v, const void* 
   return LLMT_OK;
 }
 
-// Config C3 on the caller's layouts, no copies: per-head QK-norm + RoPE of
-// q_raw / k_raw, flash forward (v read in place), dO operand from the fp16
-// dout, flash backward (dv written in place), QK-norm + RoPE backward into
-// dq_raw / dk_raw.
+// Config C3 on the caller's layouts, no copies, three launches after the
+// RoPE tables: per-head QK-norm + RoPE of k_raw; the flash forward, which
+// also normalises and rotates its q rows (keeping them for the backward) and
+// prepares the dO operand from the fp16 dout (v read in place); the flash
+// backward, whose dQ / dK epilogues run the QK-norm + RoPE backward into
+// dq_raw / dk_raw (dv written in place).
 int llmt_attention_block_bwd(const void* q_raw, const void* k_raw, const void* v,
                              const float* q_norm, const float* k_norm, const void* dout,
                              float* dq_raw, float* dk_raw, float* dv, int B, int S, int nq,
@@ -322,12 +324,16 @@ int llmt_attention_block_bwd(const void* q_raw, const void* k_raw, const void* v
   TRY_ARG(q_raw && k_raw && v && q_norm && k_norm && dout && dq_raw && dk_raw && dv &&
               attn_shape_ok(B, S, nq, nkv),
           "llmt_attention_block_bwd: bad arguments");
+  TRY_ARG(((uintptr_t)q_raw | (uintptr_t)dout | (uintptr_t)q_norm | (uintptr_t)k_norm |
+           (uintptr_t)dq_raw | (uintptr_t)dk_raw | (uintptr_t)dv) % 16 == 0 &&
+              (uintptr_t)k_raw % 8 == 0 && (uintptr_t)v % 16 == 0,
+          "llmt_attention_block_bwd: q_raw, v, dout, the norm weights and the fp32 outputs need "
+          "16-byte alignment, k_raw 8");
   hipStream_t st = (hipStream_t)stream;
   const int T = B * S, Q = nq * kHeadDim, KV = nkv * kHeadDim;
   const size_t f16 = sizeof(_Float16), f32 = sizeof(float);
-  const size_t need = 11 * 256 + (size_t)S * 64 * f32 * 2 + (size_t)T * Q * f16 * 3 +
-                      (size_t)T * KV * f16 + (size_t)B * nq * S * f32 * 2 + (size_t)T * nq * f32 +
-                      (size_t)T * Q * f32 + (size_t)T * KV * f32;
+  const size_t need = 9 * 256 + (size_t)S * 64 * f32 * 2 + (size_t)T * Q * f16 * 3 +
+                      (size_t)T * KV * f16 + (size_t)B * nq * S * f32 * 2 + (size_t)T * nq * f32;
   BlockWs* ws = nullptr;
   TRY_HIP(block_ws(st, need, &ws));
   float* cosT = ws->get<float>((size_t)S * 64);
@@ -339,18 +345,18 @@ int llmt_attention_block_bwd(const void* q_raw, const void* k_raw, const void* v
   float* delta = ws->get<float>((size_t)B * nq * S);
   float* dsc = ws->get<float>((size_t)T * nq);
   _Float16* dO16 = ws->get<_Float16>((size_t)T * Q);
-  float* dq = ws->get<float>((size_t)T * Q);
-  float* dk = ws->get<float>((size_t)T * KV);
-  TRY_ARG(q16 && k16 && o16 && lse && delta && dsc && dO16 && dq && dk && cosT && sinT,
+  TRY_ARG(q16 && k16 && o16 && lse && delta && dsc && dO16 && cosT && sinT,
           "llmt_attention_block_bwd: workspace layout");
   if (ws->rope_S != S || ws->rope_theta != (double)theta) {
     TRY_HIP(rope_tables(S, (double)theta, cosT, sinT, st));
     ws->rope_S = S;
     ws->rope_theta = (double)theta;
   }
-  const HeadRows fw[2] = {{(const _Float16*)q_raw, q_norm, nullptr, q16, nq},
-                          {(const _Float16*)k_raw, k_norm, nullptr, k16, nkv}};
-  TRY_HIP(head_norm_rope(fw, 2, cosT, sinT, S, T, eps, st));
+  // k's QK-norm + RoPE on its own (every dK/dV and forward workgroup reads
+  // all of it); q's runs inside the forward, which writes q16 for the
+  // backward, and dO's operand preparation in the forward's epilogue
+  const HeadRows fk[1] = {{(const _Float16*)k_raw, k_norm, k16, nkv}};
+  TRY_HIP(head_norm_rope(fk, 1, cosT, sinT, S, T, eps, st));
   AttnArgs a{};
   a.q = q16;
   a.ldq = Q;
@@ -365,21 +371,34 @@ int llmt_attention_block_bwd(const void* q_raw, const void* k_raw, const void* v
   a.o = o16;
   a.ldo = Q;
   a.lse = lse;
-  TRY_HIP(attn_fwd(a, B, st));
-  TRY_HIP(attn_delta(dout, 1, Q, o16, Q, nq, S, T, delta, dO16, Q, dsc, st));
-  a.dO16 = dO16;
+  a.qraw = (const _Float16*)q_raw;
+  a.ldqr = Q;
+  a.kraw = (const _Float16*)k_raw;
+  a.ldkr = KV;
+  a.qn = q_norm;
+  a.cosT = cosT;
+  a.sinT = sinT;
+  a.eps = eps;
+  a.q16w = q16;
+  a.dout = (const _Float16*)dout;
+  a.lddo = Q;
+  a.dO16w = dO16;
+  a.deltaw = delta;
+  a.dscw = dsc;
   a.ld16 = Q;
+  TRY_HIP(attn_fwd(a, B, st));
+  a.dout = nullptr;
+  a.dO16 = dO16;
   a.dsc = dsc;
   a.delta = delta;
-  a.dq = dq;
+  // dQ / dK go through the QK-norm + RoPE backward in the kernels' epilogues
+  a.kn = k_norm;
+  a.dq = dq_raw;
   a.ldgq = Q;
-  a.dk = dk;
+  a.dk = dk_raw;
   a.dv = dv;
   a.ldgkv = KV;
   TRY_HIP(attn_bwd(a, B, st));
-  const HeadRows bw[2] = {{(const _Float16*)q_raw, q_norm, dq, dq_raw, nq},
-                          {(const _Float16*)k_raw, k_norm, dk, dk_raw, nkv}};
-  TRY_HIP(head_norm_rope_bwd(bw, 2, cosT, sinT, S, T, eps, st));
   return LLMT_OK;
 }
 

@@ -97,11 +97,28 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnArgs a) {
   dk.issue(kbase, a.ldk, 0, S, buf0, w);
   dv.issue(vbase, a.ldv, 0, S, buf0 + TILE, w);
   half8 qf[RW][4];
+  if (a.qn) {  // the block API: QK-norm + RoPE of the raw q here, q16w for the backward
 #pragma unroll
-  for (int r = 0; r < RW; ++r)
+    for (int r = 0; r < RW; ++r) {
+      const int q = q0 + 16 * r + c, qc = min(q, S - 1);
+      norm_rope_frag(qf[r], a.qraw + (rowb + qc) * a.ldqr + h * HD, a.qn, a.cosT, a.sinT, qc,
+                     a.eps, g);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      qf[r][ks] = frag_global(a.q + rowb * a.ldq + h * HD, a.ldq, q0 + 16 * r + c, S, ks, lane);
+      for (int ks = 0; ks < 4; ++ks) {
+        if (q < S)
+          *reinterpret_cast<half8*>(a.q16w + (rowb + q) * a.ldq + h * HD + 32 * ks + 8 * g) =
+              qf[r][ks];
+        else
+          qf[r][ks] = half8{};
+      }
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        qf[r][ks] = frag_global(a.q + rowb * a.ldq + h * HD, a.ldq, q0 + 16 * r + c, S, ks, lane);
+  }
 
   floatx4 ot[RW][8];
   float m[RW], l[RW];
@@ -161,17 +178,52 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnArgs a) {
     float lr = l[r];
     lr = xg_sum(lr);
     const int q = q0 + 16 * r + c;
+    const float inv = 1.0f / lr;
+    half4v ov[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) ov[dt][v] = (_Float16)(ot[r][dt][v] * inv);
+    const long long bhq = ((long long)b * a.nq + h) * S + q;
     if (q < S) {
-      const float inv = 1.0f / lr;
       _Float16* o = a.o + (rowb + q) * a.ldo + h * HD;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        half4v x;
+      for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<half4v*>(o + dt * 16 + 4 * g) = ov[dt];
+      if (g == 0) a.lse[bhq] = (m[r] + __log2f(lr)) * LN2;
+    }
+    if (a.dout) {
+      // the block API: the backward's dO operand for this row and head
+      // (delta = sum dO * fp16(O), the row's power-of-two dO scale), every
+      // lane taking part in the cross-lane sums
+      const _Float16* dr = a.dout + (rowb + min(q, S - 1)) * a.lddo + h * HD;
+      half4v dv[8];
+      float dl = 0.f, am = 0.f;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) x[v] = (_Float16)(ot[r][dt][v] * inv);
-        *reinterpret_cast<half4v*>(o + dt * 16 + 4 * g) = x;
+      for (int dt = 0; dt < 8; ++dt) {
+        dv[dt] = *reinterpret_cast<const half4v*>(dr + dt * 16 + 4 * g);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          dl += (float)dv[dt][v] * (float)ov[dt][v];
+          am = fmaxf(am, fabsf((float)dv[dt][v]));
+        }
       }
-      if (g == 0) a.lse[((long long)b * a.nq + h) * S + q] = (m[r] + __log2f(lr)) * LN2;
+      dl = xg_sum(dl);
+      am = xg_max(am);
+      if (q < S) {
+        const float sc = pow2_scale_for(am, kDoScaleExp);
+        _Float16* d16 = a.dO16w + (rowb + q) * a.ld16 + h * HD;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          half4v x;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) x[v] = (_Float16)((float)dv[dt][v] * sc);
+          *reinterpret_cast<half4v*>(d16 + dt * 16 + 4 * g) = x;
+        }
+        if (g == 0) {
+          a.deltaw[bhq] = dl;
+          a.dscw[bhq] = pow2_inv_scale_for(am, kDoScaleExp);
+        }
+      }
     }
   }
 }
@@ -272,6 +324,12 @@ hipError_t attn_delta(const void* dO, int dO_is_f16, long long ldd, const _Float
 hipError_t attn_fwd(const AttnArgs& a, int B, hipStream_t st) {
   if (a.nq % a.nkv || a.S <= 0) {
     set_error("attn_fwd: nq=%d nkv=%d S=%d", a.nq, a.nkv, a.S);
+    return hipErrorInvalidValue;
+  }
+  if ((a.qn && !(a.qraw && a.cosT && a.sinT && a.q16w)) ||
+      (a.dout && !(a.dO16w && a.deltaw && a.dscw))) {
+    set_error("attn_fwd: the fused q norm needs qraw, the RoPE tables and q16w; the dO "
+              "operand needs dO16w, deltaw and dscw");
     return hipErrorInvalidValue;
   }
   const AttnShape s = attn_shape(B, a.S, a.nq);

@@ -165,12 +165,52 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, _Float16* buf0, _Flo
   for (int r = 0; r < RW; ++r) {
     const int q = q0 + 16 * r + c;
     const float f = fq[r];
+    float dy[8][4];
+#pragma unroll
+    for (int d = 0; d < 8; ++d)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) dy[d][v] = dqT[r][d][v] * f;
+    if (a.qn) {  // the block API: through q's RoPE and norm to d qraw
+      const int qc = min(q, S - 1);
+      norm_rope_bwd_row(dy, a.qraw + (rowb + qc) * a.ldqr + h * HD, a.qn, a.cosT, a.sinT, qc,
+                        a.eps, g);
+    }
     if (q < S) {
       float* dq = a.dq + (rowb + q) * a.ldgq + h * HD;
 #pragma unroll
       for (int d = 0; d < 8; ++d)
         *reinterpret_cast<float4*>(dq + d * 16 + 4 * g) =
-            make_float4(dqT[r][d][0] * f, dqT[r][d][1] * f, dqT[r][d][2] * f, dqT[r][d][3] * f);
+            make_float4(dy[d][0], dy[d][1], dy[d][2], dy[d][3]);
+    }
+  }
+}
+
+// dK and dV rows of one key (dkT / dvT in the group's dO scale gs): dK
+// through k's RoPE and norm when the block API asks for it (kn).
+__device__ __forceinline__ void store_dkdv(const AttnArgs& a, const floatx4 (&dkT)[8],
+                                           const floatx4 (&dvT)[8], float gs, long long rowb,
+                                           int key, int j, int g) {
+  const float inv = 1.0f / gs;
+  const float fk = a.sm_scale * inv;
+  float dy[8][4];
+#pragma unroll
+  for (int d = 0; d < 8; ++d)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) dy[d][v] = dkT[d][v] * fk;
+  if (a.kn) {
+    const int kc = min(key, a.S - 1);
+    norm_rope_bwd_row(dy, a.kraw + (rowb + kc) * a.ldkr + j * HD, a.kn, a.cosT, a.sinT, kc,
+                      a.eps, g);
+  }
+  if (key < a.S) {
+    float* dk = a.dk + (rowb + key) * a.ldgkv + j * HD;
+    float* dv = a.dv + (rowb + key) * a.ldgkv + j * HD;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      *reinterpret_cast<float4*>(dk + dt * 16 + 4 * g) =
+          make_float4(dy[dt][0], dy[dt][1], dy[dt][2], dy[dt][3]);
+      *reinterpret_cast<float4*>(dv + dt * 16 + 4 * g) =
+          make_float4(dvT[dt][0] * inv, dvT[dt][1] * inv, dvT[dt][2] * inv, dvT[dt][3] * inv);
     }
   }
 }
@@ -382,25 +422,8 @@ __device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* buf0, _F
     tile_step(it, std::false_type{}, buf0, buf1);
     if (it + 1 < niter) tile_step(it + 1, std::false_type{}, buf1, buf0);
   }
-  const float inv = 1.0f / gs;
-  const float fk = a.sm_scale * inv;
 #pragma unroll
-  for (int t = 0; t < KW; ++t) {
-    const int key = k0 + 16 * t + c;
-    if (key < S) {
-      float* dk = a.dk + (rowb + key) * a.ldgkv + j * HD;
-      float* dv = a.dv + (rowb + key) * a.ldgkv + j * HD;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        *reinterpret_cast<float4*>(dk + dt * 16 + 4 * g) =
-            make_float4(dkT[t][dt][0] * fk, dkT[t][dt][1] * fk, dkT[t][dt][2] * fk,
-                        dkT[t][dt][3] * fk);
-        *reinterpret_cast<float4*>(dv + dt * 16 + 4 * g) =
-            make_float4(dvT[t][dt][0] * inv, dvT[t][dt][1] * inv, dvT[t][dt][2] * inv,
-                        dvT[t][dt][3] * inv);
-      }
-    }
-  }
+  for (int t = 0; t < KW; ++t) store_dkdv(a, dkT[t], dvT[t], gs, rowb, k0 + 16 * t + c, j, g);
 }
 
 // Small grids (the B1 x S128 step: 8 KV heads x 8 key blocks): the NW waves
@@ -491,20 +514,7 @@ __device__ __forceinline__ void dkdv_block_split(const AttnArgs& a, _Float16* sm
       dkT[i] += xch[((ww - 1) * 16 + i) * 64 + lane];
       dvT[i] += xch[((ww - 1) * 16 + 8 + i) * 64 + lane];
     }
-  const int key = k0 + c;
-  if (key < S) {
-    const float inv = 1.0f / gs;
-    const float fk = a.sm_scale * inv;
-    float* dk = a.dk + (rowb + key) * a.ldgkv + j * HD;
-    float* dv = a.dv + (rowb + key) * a.ldgkv + j * HD;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      *reinterpret_cast<float4*>(dk + dt * 16 + 4 * g) =
-          make_float4(dkT[dt][0] * fk, dkT[dt][1] * fk, dkT[dt][2] * fk, dkT[dt][3] * fk);
-      *reinterpret_cast<float4*>(dv + dt * 16 + 4 * g) =
-          make_float4(dvT[dt][0] * inv, dvT[dt][1] * inv, dvT[dt][2] * inv, dvT[dt][3] * inv);
-    }
-  }
+  store_dkdv(a, dkT, dvT, gs, rowb, k0 + c, j, g);
 }
 
 // The attention backward of a launch over a flat grid (x, B): x < nkv nkvb
@@ -593,6 +603,10 @@ hipError_t attn_bwd(const AttnArgs& a, int B, hipStream_t st) {
   if (a.nq % a.nkv || a.S <= 0 || !a.dO16 || !a.dsc || !a.dk || !a.dv) {
     set_error("attn_bwd: nq=%d nkv=%d S=%d (fp16 dO, its scales and dK/dV outputs required)",
               a.nq, a.nkv, a.S);
+    return hipErrorInvalidValue;
+  }
+  if ((a.qn && !a.qraw) || (a.kn && !a.kraw) || ((a.qn || a.kn) && !(a.cosT && a.sinT))) {
+    set_error("attn_bwd: the fused QK-norm backward needs the raw q / k and the RoPE tables");
     return hipErrorInvalidValue;
   }
   // dQ holds twice the accumulators of the forward: one 16-row tile a wave

@@ -148,6 +148,87 @@ __device__ __forceinline__ float xg_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Per-head RMSNorm + half-split RoPE of one 128-wide row (the block API's
+// QK-norm, src/kernels/rmsnorm.cu:36-41 and src/kernels/rope.cu:7-27) as an
+// MFMA operand: lane (c, g) of the four lanes c + 16 g holding the row gets
+// y = fp16(rope(x * r * w)) at halves 32 ks + 8 g .. + 7 in y[ks], r =
+// rsqrt(mean x^2 + eps), position pos.  Every lane of the wave must call it
+// (the row sum crosses lanes).
+__device__ __forceinline__ void norm_rope_frag(half8 (&y)[4], const _Float16* x, const float* w,
+                                               const float* cosT, const float* sinT, int pos,
+                                               float eps, int g) {
+  float a[4][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const half8 h = *reinterpret_cast<const half8*>(x + 32 * ks + 8 * g);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      a[ks][i] = (float)h[i];
+      ss += a[ks][i] * a[ks][i];
+    }
+  }
+  const float r = rsqrtf(xg_sum(ss) / HD + eps);
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[ks][i] = a[ks][i] * r * w[32 * ks + 8 * g + i];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int d = 32 * ks + 8 * g + i;
+      const float cs = cosT[pos * (HD / 2) + d], sn = sinT[pos * (HD / 2) + d];
+      y[ks][i] = (_Float16)(a[ks][i] * cs - a[ks + 2][i] * sn);
+      y[ks + 2][i] = (_Float16)(a[ks + 2][i] * cs + a[ks][i] * sn);
+    }
+}
+
+// Backward of the same map for one row held as accumulator columns: lane
+// (c, g) has dy at dims 16 d + 4 g + v in dy[d][v] (d < 8); on return dx of
+// the raw input x there (src/kernels/rope.cu:57-89, then
+// src/kernels/rmsnorm.cu:53-95 over 128-wide rows):
+//   n = rope^T(dy); dx = r (n w - (r^2 / 128) sum(n w x) x).
+// Every lane of the wave must call it.
+__device__ __forceinline__ void norm_rope_bwd_row(float (&dy)[8][4], const _Float16* x,
+                                                  const float* w, const float* cosT,
+                                                  const float* sinT, int pos, float eps, int g) {
+  float xv[8][4], wv[8][4], n[8][4];
+  float ss = 0.f, dot = 0.f;
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+    const half4v h = *reinterpret_cast<const half4v*>(x + 16 * d + 4 * g);
+    const float4 ww = *reinterpret_cast<const float4*>(w + 16 * d + 4 * g);
+    wv[d][0] = ww.x; wv[d][1] = ww.y; wv[d][2] = ww.z; wv[d][3] = ww.w;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) xv[d][v] = (float)h[v];
+  }
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const float4 c4 = *reinterpret_cast<const float4*>(cosT + pos * (HD / 2) + 16 * d + 4 * g);
+    const float4 s4 = *reinterpret_cast<const float4*>(sinT + pos * (HD / 2) + 16 * d + 4 * g);
+    const float cs[4] = {c4.x, c4.y, c4.z, c4.w}, sn[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      n[d][v] = dy[d][v] * cs[v] + dy[d + 4][v] * sn[v];
+      n[d + 4][v] = dy[d + 4][v] * cs[v] - dy[d][v] * sn[v];
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < 8; ++d)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      ss += xv[d][v] * xv[d][v];
+      dot += n[d][v] * wv[d][v] * xv[d][v];
+    }
+  const float r = rsqrtf(xg_sum(ss) / HD + eps);
+  const float coef = r * r / HD * xg_sum(dot);
+#pragma unroll
+  for (int d = 0; d < 8; ++d)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) dy[d][v] = r * (n[d][v] * wv[d][v] - coef * xv[d][v]);
+}
+
 // B fragment built from two accumulator tiles (see the file comment).
 __device__ __forceinline__ half8 pair_frag(const floatx4& a, const floatx4& b) {
   half8 r;

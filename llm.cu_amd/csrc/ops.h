@@ -185,20 +185,17 @@ hipError_t resid_norm(const RowIn& in, const float* x_res, const float* w, float
                       float* x_out, _Float16* xn, hipStream_t st);
 // cos / sin tables of the half-split RoPE, [S, 64] fp32 each, on the device.
 hipError_t rope_tables(int S, double theta, float* cosT, float* sinT, hipStream_t st);
-// Per-head QK-RMSNorm + RoPE of [T, nh, 128] fp16 rows (weights w [128]),
-// and its backward from dy fp32 [T, nh, 128] to dx fp32 (x: the raw rows).
-// Up to two tensors (q and k) in one launch.
+// Per-head QK-RMSNorm + RoPE of [T, nh, 128] fp16 rows (weights w [128]).
+// Up to two tensors in one launch.  (The backward runs inside the attention
+// backward's epilogues, AttnArgs::qn / kn.)
 struct HeadRows {
   const _Float16* x;  // raw rows
   const float* w;     // norm weights [128]
-  const float* dy;    // backward: upstream gradient (unused in the forward)
-  void* out;          // forward: fp16 normed, rotated rows; backward: fp32 dx
+  _Float16* out;      // normed, rotated rows
   int nh;
 };
 hipError_t head_norm_rope(const HeadRows* segs, int nseg, const float* cosT, const float* sinT,
                           int S, int T, float eps, hipStream_t st);
-hipError_t head_norm_rope_bwd(const HeadRows* segs, int nseg, const float* cosT,
-                              const float* sinT, int S, int T, float eps, hipStream_t st);
 hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st);
 hipError_t swiglu_bwd(const RowIn& in, const float* rinv_in, const _Float16* gu, int I, int T,
                       _Float16* dgu16, float* rinv_out, hipStream_t st);
@@ -246,6 +243,30 @@ struct AttnArgs {
   float* dk;            // dK, dV (summed over each GQA group) fp32 [T, ldgkv]
   float* dv;
   long long ldgkv;
+  // The attention block API's fusions (all null in the training step, whose
+  // row epilogues do this work).  qn: q is per-head RMSNorm (weights qn,
+  // eps) + RoPE (cosT / sinT [S, 64]) of qraw [T, ldqr]: the forward applies
+  // both to its Q fragments and writes the fp16 result to q16w (the
+  // backward's q); the dQ blocks apply their backward to dQ (dq then holds
+  // d qraw).  kn: the same backward for k on the dK blocks (kraw [T, ldkr];
+  // dk then holds d kraw).  dout: the forward also writes the backward's dO
+  // operand from dout fp16 [T, lddo] into dO16w, deltaw and dscw (as
+  // attn_delta does).
+  const _Float16* qraw;
+  long long ldqr;
+  const _Float16* kraw;
+  long long ldkr;
+  const float* qn;
+  const float* kn;
+  const float* cosT;
+  const float* sinT;
+  float eps;
+  _Float16* q16w;
+  const _Float16* dout;
+  long long lddo;
+  _Float16* dO16w;
+  float* deltaw;
+  float* dscw;
 };
 hipError_t attn_fwd(const AttnArgs& a, int B, hipStream_t st);
 hipError_t attn_bwd(const AttnArgs& a, int B, hipStream_t st);

@@ -449,12 +449,12 @@ __global__ __launch_bounds__(RT) void resid_norm_kernel(const RowIn in,
 }
 
 // Per-head QK-RMSNorm + RoPE on [T, nh, 128] rows (the attention block API's
-// separate q / k inputs; the training step fuses this into qkv_post): 16
-// lanes per (token, head) row, lane j holding the RoPE pairs (d, d + 64) for
-// d = 4 j .. 4 j + 3, so every access is 8 (fp16) or 16 (fp32) bytes a lane.
-//   forward:  y = rope(x * r * w), r = rsqrt(mean x^2 + eps)
-//   backward: n = rope^T(dy); dx = r (n w - (r^2 / 128) sum(n w x) x)
-// (src/kernels/rmsnorm.cu:6-41, 53-95; src/kernels/rope.cu:7-46, 57-89).
+// k input; its q goes through the same map inside the attention forward, and
+// the training step fuses this into qkv_post): 16 lanes per (token, head)
+// row, lane j holding the RoPE pairs (d, d + 64) for d = 4 j .. 4 j + 3, so
+// every access is 8 (fp16) or 16 (fp32) bytes a lane.
+//   y = rope(x * r * w), r = rsqrt(mean x^2 + eps)
+// (src/kernels/rmsnorm.cu:6-41; src/kernels/rope.cu:7-46).
 constexpr int HN_ROWS = RT / 16;  // rows a workgroup
 
 // Sum over the 16 lanes of a row group.
@@ -499,7 +499,7 @@ __global__ __launch_bounds__(RT) void head_norm_rope_kernel(const HeadNormArgs a
     x0[i] = ldh4(sg.x + row * HD + 4 * j);
     x1[i] = ldh4(sg.x + row * HD + 64 + 4 * j);
   }
-  _Float16* out = static_cast<_Float16*>(sg.out);
+  _Float16* out = sg.out;
 #pragma unroll
   for (int i = 0; i < HN_R; ++i) {
     const long long row = r0 + i * stride;
@@ -522,61 +522,6 @@ __global__ __launch_bounds__(RT) void head_norm_rope_kernel(const HeadNormArgs a
     }
     *reinterpret_cast<half4*>(out + row * HD + 4 * j) = o0;
     *reinterpret_cast<half4*>(out + row * HD + 64 + 4 * j) = o1;
-  }
-}
-
-__global__ __launch_bounds__(RT) void head_norm_rope_bwd_kernel(const HeadNormArgs a) {
-  const HeadRows& sg = a.seg[blockIdx.y];
-  const int j = threadIdx.x & 15;
-  const long long nrows = (long long)a.T * sg.nh;
-  const long long r0 = (long long)blockIdx.x * HN_ROWS + (threadIdx.x >> 4);
-  const long long stride = (long long)gridDim.x * HN_ROWS;
-  const float4 w0 = ld4(sg.w + 4 * j), w1 = ld4(sg.w + 64 + 4 * j);
-  const float ww0[4] = {w0.x, w0.y, w0.z, w0.w}, ww1[4] = {w1.x, w1.y, w1.z, w1.w};
-  float4 d0[HN_R], d1[HN_R], x0[HN_R], x1[HN_R], cs[HN_R], sn[HN_R];
-#pragma unroll
-  for (int i = 0; i < HN_R; ++i) {
-    const long long row = min(r0 + i * stride, nrows - 1);
-    // 32-bit division (rows < 2^31, checked on the host): the 64-bit form
-    // expands to about a hundred instructions a row
-    const int pos = (int)(((unsigned)row / (unsigned)sg.nh) % (unsigned)a.S);
-    cs[i] = ld4(a.cosT + pos * (HD / 2) + 4 * j);
-    sn[i] = ld4(a.sinT + pos * (HD / 2) + 4 * j);
-    d0[i] = ld4(sg.dy + row * HD + 4 * j);
-    d1[i] = ld4(sg.dy + row * HD + 64 + 4 * j);
-    x0[i] = ldh4(sg.x + row * HD + 4 * j);
-    x1[i] = ldh4(sg.x + row * HD + 64 + 4 * j);
-  }
-  float* dx = static_cast<float*>(sg.out);
-#pragma unroll
-  for (int i = 0; i < HN_R; ++i) {
-    const long long row = r0 + i * stride;
-    const float c[4] = {cs[i].x, cs[i].y, cs[i].z, cs[i].w};
-    const float s4[4] = {sn[i].x, sn[i].y, sn[i].z, sn[i].w};
-    const float dd0[4] = {d0[i].x, d0[i].y, d0[i].z, d0[i].w};
-    const float dd1[4] = {d1[i].x, d1[i].y, d1[i].z, d1[i].w};
-    const float xx0[4] = {x0[i].x, x0[i].y, x0[i].z, x0[i].w};
-    const float xx1[4] = {x1[i].x, x1[i].y, x1[i].z, x1[i].w};
-    float n0[4], n1[4], ss = 0.f, dot = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      n0[e] = dd0[e] * c[e] + dd1[e] * s4[e];
-      n1[e] = dd1[e] * c[e] - dd0[e] * s4[e];
-      ss += xx0[e] * xx0[e] + xx1[e] * xx1[e];
-      dot += n0[e] * ww0[e] * xx0[e] + n1[e] * ww1[e] * xx1[e];
-    }
-    const float r = rsqrtf(sum16(ss) / HD + a.eps);
-    const float coef = r * r / HD * sum16(dot);
-    if (row >= nrows) continue;  // whole 16-lane groups (after the group sums)
-    float o0[4], o1[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      o0[e] = r * (n0[e] * ww0[e] - coef * xx0[e]);
-      o1[e] = r * (n1[e] * ww1[e] - coef * xx1[e]);
-    }
-    *reinterpret_cast<float4*>(dx + row * HD + 4 * j) = make_float4(o0[0], o0[1], o0[2], o0[3]);
-    *reinterpret_cast<float4*>(dx + row * HD + 64 + 4 * j) =
-        make_float4(o1[0], o1[1], o1[2], o1[3]);
   }
 }
 
@@ -1207,27 +1152,24 @@ hipError_t rope_tables(int S, double theta, float* cosT, float* sinT, hipStream_
   return hipSuccess;
 }
 
-static hipError_t head_norm_launch(const HeadRows* segs, int nseg, const float* cosT,
-                                   const float* sinT, int S, int T, float eps, bool bwd,
-                                   hipStream_t st) {
-  const char* who = bwd ? "head_norm_rope_bwd" : "head_norm_rope";
+hipError_t head_norm_rope(const HeadRows* segs, int nseg, const float* cosT, const float* sinT,
+                          int S, int T, float eps, hipStream_t st) {
   if (nseg < 1 || nseg > 2 || T <= 0 || S <= 0) {
-    set_error("%s: %d tensors, T=%d, S=%d", who, nseg, T, S);
+    set_error("head_norm_rope: %d tensors, T=%d, S=%d", nseg, T, S);
     return hipErrorInvalidValue;
   }
   HeadNormArgs a{};
   long long maxrows = 0;
   for (int i = 0; i < nseg; ++i) {
     const HeadRows& r = segs[i];
-    const bool al = (uintptr_t)r.w % 16 == 0 && (uintptr_t)r.x % 8 == 0 &&
-                    (uintptr_t)r.out % (bwd ? 16 : 8) == 0 && (!bwd || (uintptr_t)r.dy % 16 == 0);
-    if (!r.x || !r.w || !r.out || (bwd && !r.dy) || r.nh <= 0 || !al) {
-      set_error("%s: tensor %d: bad pointers, alignment (w, dy, fp32 out 16 B; x, fp16 out 8 B) "
-                "or nh=%d", who, i, r.nh);
+    const bool al = (uintptr_t)r.w % 16 == 0 && (uintptr_t)r.x % 8 == 0 && (uintptr_t)r.out % 8 == 0;
+    if (!r.x || !r.w || !r.out || r.nh <= 0 || !al) {
+      set_error("head_norm_rope: tensor %d: bad pointers, alignment (w 16 B; x, out 8 B) or nh=%d",
+                i, r.nh);
       return hipErrorInvalidValue;
     }
     if ((long long)T * r.nh >= (1LL << 31)) {
-      set_error("%s: %lld rows (at most 2^31 - 1)", who, (long long)T * r.nh);
+      set_error("head_norm_rope: %lld rows (at most 2^31 - 1)", (long long)T * r.nh);
       return hipErrorInvalidValue;
     }
     a.seg[i] = r;
@@ -1239,22 +1181,9 @@ static hipError_t head_norm_launch(const HeadRows* segs, int nseg, const float* 
   a.T = T;
   a.eps = eps;
   const dim3 grid((unsigned)((maxrows + HN_ROWS * HN_R - 1) / (HN_ROWS * HN_R)), nseg);
-  if (bwd)
-    hipLaunchKernelGGL(head_norm_rope_bwd_kernel, grid, dim3(RT), 0, st, a);
-  else
-    hipLaunchKernelGGL(head_norm_rope_kernel, grid, dim3(RT), 0, st, a);
+  hipLaunchKernelGGL(head_norm_rope_kernel, grid, dim3(RT), 0, st, a);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
-}
-
-hipError_t head_norm_rope(const HeadRows* segs, int nseg, const float* cosT, const float* sinT,
-                          int S, int T, float eps, hipStream_t st) {
-  return head_norm_launch(segs, nseg, cosT, sinT, S, T, eps, false, st);
-}
-
-hipError_t head_norm_rope_bwd(const HeadRows* segs, int nseg, const float* cosT,
-                              const float* sinT, int S, int T, float eps, hipStream_t st) {
-  return head_norm_launch(segs, nseg, cosT, sinT, S, T, eps, true, st);
 }
 
 hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st) {
