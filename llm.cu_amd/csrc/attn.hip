@@ -66,8 +66,12 @@ __device__ __forceinline__ void softmax_tile(floatx4 (&st)[RW][4], float (&m)[RW
   }
 }
 
-// grid (ceil(S / QB), nq, B), QB = 16 NW RW queries; blockIdx.x runs the
-// longest (last) query blocks first.  Wave w owns queries q0 + 16 r + c
+// grid (nq, B, ceil(S / QB)), QB = 16 NW RW queries: blockIdx.z runs the
+// longest (last) query blocks first over all heads and batches (workgroups
+// are dispatched x fastest), and a workgroup's XCD (its linear index mod 8)
+// follows its head, so every XCD gets the same mix of causal block lengths.
+// (With the query block on x, XCD k got only blocks k, k + 8, ..: at B4 x
+// S2048 the XCDs' work differed by 2.4x.)  Wave w owns queries q0 + 16 r + c
 // (r < RW).  LDS: two buffers of (K tile, V tile).
 template <int NW, int RW>
 __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnArgs a) {
@@ -80,7 +84,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnArgs a) {
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, g = lane >> 4;
-  const int qb = gridDim.x - 1 - blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int qb = gridDim.z - 1 - blockIdx.z, h = blockIdx.x, b = blockIdx.y;
   const int S = a.S;
   const int kvh = h / (a.nq / a.nkv);
   const long long rowb = (long long)b * S;
@@ -294,7 +298,7 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(const TD* __restrict__ 
 template <int NW, int RW>
 void launch_fwd(const AttnArgs& a, int B, hipStream_t st) {
   constexpr int QB = NW * RW * 16;
-  hipLaunchKernelGGL((attn_fwd_kernel<NW, RW>), dim3((a.S + QB - 1) / QB, a.nq, B), dim3(NW * 64),
+  hipLaunchKernelGGL((attn_fwd_kernel<NW, RW>), dim3(a.nq, B, (a.S + QB - 1) / QB), dim3(NW * 64),
                      0, st, a);
 }
 
