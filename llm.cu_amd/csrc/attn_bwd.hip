@@ -517,11 +517,15 @@ __device__ __forceinline__ void dkdv_block_split(const AttnArgs& a, _Float16* sm
   store_dkdv(a, dkT, dvT, gs, rowb, k0 + c, j, g);
 }
 
-// The attention backward of a launch over a flat grid (x, B): x < nkv nkvb
-// are dK/dV blocks (key block x / nkv, KV head x % nkv: the longest key
-// blocks first), the next nq nqb dQ blocks (the last, i.e. longest, query
-// blocks first).  PART 0: both kinds; 1: dK/dV only; 2: dQ only -- the
-// one-kind forms keep their own (smaller) register and LDS budgets.
+// The attention backward of a launch over a grid (B, x): x < nkv nkvb are
+// dK/dV blocks (key block x / nkv, KV head x % nkv: the longest key blocks
+// first), the next nq nqb dQ blocks (the last, i.e. longest, query blocks
+// first).  The batch is the fastest grid index, so the longest blocks of
+// every batch are dispatched first (with the batch outermost, at B4 x S2048
+// the last batches' 178 us key blocks started only once earlier ones had
+// drained, leaving a tail at half occupancy for 45% of the dK/dV launch).
+// PART 0: both kinds; 1: dK/dV only; 2: dQ only -- the one-kind forms keep
+// their own (smaller) register and LDS budgets.
 constexpr int BWD_BUF = KV_BUF > 2 * TILE ? KV_BUF : 2 * TILE;  // halves per buffer
 
 template <int NW, int RW, int PART>
@@ -534,7 +538,7 @@ void attn_bwd_kernel(const AttnArgs a, int nkvb, int nqb) {
   __shared__ __attribute__((aligned(1024))) _Float16 buf0[PART == 3 ? SMEM3 : BUF];
   __shared__ __attribute__((aligned(1024))) _Float16 buf1[PART == 3 ? 8 : BUF];
   __shared__ float red[NW];
-  const int x = blockIdx.x, b = blockIdx.y;
+  const int x = blockIdx.y, b = blockIdx.x;
   const int nkvx = PART == 2 ? 0 : nkvb * a.nkv;
   if constexpr (PART != 2) {
     if (x < nkvx) {
@@ -563,7 +567,7 @@ int dkdv_waves(int B, int S, int nkv) {
 template <int NW, int RW, int PART>
 void launch_bwd(const AttnArgs& a, int B, int nkvb, int nqb, hipStream_t st) {
   const int nx = (PART == 2 ? 0 : nkvb * a.nkv) + (PART == 1 ? 0 : nqb * a.nq);
-  hipLaunchKernelGGL((attn_bwd_kernel<NW, RW, PART>), dim3(nx, B), dim3(NW * 64), 0, st, a, nkvb,
+  hipLaunchKernelGGL((attn_bwd_kernel<NW, RW, PART>), dim3(B, nx), dim3(NW * 64), 0, st, a, nkvb,
                      nqb);
 }
 
@@ -603,6 +607,10 @@ hipError_t attn_bwd(const AttnArgs& a, int B, hipStream_t st) {
   if (a.nq % a.nkv || a.S <= 0 || !a.dO16 || !a.dsc || !a.dk || !a.dv) {
     set_error("attn_bwd: nq=%d nkv=%d S=%d (fp16 dO, its scales and dK/dV outputs required)",
               a.nq, a.nkv, a.S);
+    return hipErrorInvalidValue;
+  }
+  if ((long long)(a.S + 15) / 16 * (a.nq + a.nkv) > 65535) {
+    set_error("attn_bwd: S=%d with %d + %d heads exceeds the grid's y range", a.S, a.nq, a.nkv);
     return hipErrorInvalidValue;
   }
   if ((a.qn && !a.qraw) || (a.kn && !a.kraw) || ((a.qn || a.kn) && !(a.cosT && a.sinT))) {
