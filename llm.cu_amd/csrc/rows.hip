@@ -385,6 +385,113 @@ __global__ __launch_bounds__(RT) void o_post_kernel(const RowIn in,
   }
 }
 
+// Split-K sums of NR rows' pieces (columns 4 tid .. + 3, live when < n) and,
+// with HH, of this thread's four raw h columns (tid < nh / 4), rows t0 ..
+// t0 + NR - 1 clamped to T - 1: every row's loads of a split are issued
+// before that split's in-order adds, so NR rows cost one memory round trip
+// per split.
+template <int NR, bool HH>
+__device__ __forceinline__ void load_rows(const RowIn& in, int t0, int T, int n, float4 (&v)[NR],
+                                          float4 (&h)[NR]) {
+  const int c = 4 * (int)threadIdx.x;
+  const int off = c < n ? c : 0;
+  const int hoff = in.hcol + 4 * ((int)threadIdx.x < in.nh / 4 ? (int)threadIdx.x : 0);
+  const float* prow[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    prow[i] = in.part + (long long)min(t0 + i, T - 1) * in.ldp;
+    v[i] = ld4(prow[i] + off);
+    if (HH) h[i] = ld4(prow[i] + hoff);
+  }
+  for (int k = 1; k < in.split; ++k) {
+    float4 x[NR], y[NR];
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      x[i] = ld4(prow[i] + (long long)k * in.ss + off);
+      if (HH) y[i] = ld4(prow[i] + (long long)k * in.ss + hoff);
+    }
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      v[i] = add4(v[i], x[i]);
+      if (HH) h[i] = add4(h[i], y[i]);
+    }
+  }
+}
+
+// NR block sums at once (one barrier pair).
+template <int NR>
+__device__ __forceinline__ void block_sums(float (&a)[NR], float* red) {
+  const int w = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    a[i] = wave_sum(a[i]);
+    if ((threadIdx.x & 63) == 0) red[i * RW + w] = a[i];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    float x = 0.f;
+#pragma unroll
+    for (int q = 0; q < RW; ++q) x += red[i * RW + q];
+    a[i] = x;
+  }
+  __syncthreads();
+}
+
+// o_post for rows of one piece per thread at large T: NR rows a workgroup
+// side by side (each thread's four columns of every row), so their loads
+// share one memory round trip, their row sums one barrier pair and the
+// adapter values (loaded once) every row.  (The one-row kernel spends a
+// round trip and two barrier phases a row; rows handled one after another
+// in a workgroup measured no faster.)
+template <int NR>
+__global__ __launch_bounds__(RT) void o_post_rows_kernel(const RowIn in,
+                                                         const float* __restrict__ x_in,
+                                                         const float* __restrict__ w, float eps,
+                                                         int H, float* __restrict__ hbuf,
+                                                         float* __restrict__ x_mid,
+                                                         _Float16* __restrict__ xn2, int T) {
+  __shared__ float red[NR * RW];
+  __shared__ float hs[NR][64];
+  const int t0 = blockIdx.x * NR;
+  const int c = 4 * (int)threadIdx.x;
+  const int cc = min(c, H - 4);
+  const bool live = c < H;
+  float4 xi[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) xi[i] = ld4(x_in + (long long)min(t0 + i, T - 1) * H + cc);
+  float4 v[NR], hv[NR];
+  load_rows<NR, true>(in, t0, T, H, v, hv);
+  const float4 wv = ld4(w + cc);
+  LoraRegs<1, 1> L;
+  lora_load<1, 1>(in, H, L);
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    store_h(in, hv[i], hs[i]);
+    if ((int)threadIdx.x < in.nh / 4 && t0 + i < T)
+      *reinterpret_cast<float4*>(hbuf + (long long)(t0 + i) * 64 + 3 * R + 4 * threadIdx.x) = hv[i];
+  }
+  __syncthreads();
+  float ssq[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    float4 vi[1] = {v[i]};
+    lora_apply<1, 1>(in, hs[i], L, vi);
+    v[i] = add4(xi[i], vi[0]);
+    if (live && t0 + i < T) *reinterpret_cast<float4*>(x_mid + (long long)(t0 + i) * H + c) = v[i];
+    ssq[i] = live ? v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w : 0.f;
+  }
+  block_sums<NR>(ssq, red);
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const float r = rsqrtf(ssq[i] / H + eps);
+    if (live && t0 + i < T)
+      st_h4(xn2 + (long long)(t0 + i) * H + c,
+            make_float4(v[i].x * r * wv.x, v[i].y * r * wv.y, v[i].z * r * wv.z,
+                        v[i].w * r * wv.w));
+  }
+}
+
 // After the fused gate/up GEMM: stash g, u (fp16, for the backward) and
 // a = silu(g) * u (src/kernels/activation.cu:5-18) from the fp32 sums as the
 // fp16 operand of the down GEMM.
@@ -1087,6 +1194,17 @@ hipError_t o_post(const RowIn& in, const float* x_in, const float* w, float eps,
                   float* hbuf, float* x_mid, _Float16* xn2, hipStream_t st) {
   if (!row_in_ok(in, H, "o_post")) return hipErrorInvalidValue;
   const int P = (H + 4 * RT - 1) / (4 * RT);
+  const char* e = getenv("LLMT_O_POST_ROWS");
+  const int nr = e && *e ? atoi(e) : (T >= 2048 ? 4 : 1);
+  if (P == 1 && nr > 1) {
+    switch (nr) {
+      case 2: hipLaunchKernelGGL(o_post_rows_kernel<2>, dim3((T + 1) / 2), dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T); break;
+      case 8: hipLaunchKernelGGL(o_post_rows_kernel<8>, dim3((T + 7) / 8), dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T); break;
+      default: hipLaunchKernelGGL(o_post_rows_kernel<4>, dim3((T + 3) / 4), dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T); break;
+    }
+    LLMT_LAUNCH_CHECK();
+    return hipSuccess;
+  }
   const int rpw = rows_per_wg(T, P);
   const dim3 g((T + rpw - 1) / rpw);
   switch (P) {
