@@ -175,6 +175,36 @@ __device__ __forceinline__ void lora_apply(const RowIn& in, const float* hs,
   }
 }
 
+// lora_apply for NR rows of one piece per thread (hs[i]: row i's h values),
+// each adapter value converted once and used for every row, in the one-row
+// form's order of adds.
+template <int NR, int NTM>
+__device__ __forceinline__ void lora_apply_rows(const RowIn& in, const float (*hs)[64],
+                                                const LoraRegs<1, NTM>& L, float4 (&v)[NR]) {
+  float4 acc[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int s = 0; s < NTM; ++s) {
+    if (L.hidx[0][s] < 0) continue;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float w0 = (float)L.w[0][s][r][0], w1 = (float)L.w[0][s][r][1];
+      const float w2 = (float)L.w[0][s][r][2], w3 = (float)L.w[0][s][r][3];
+#pragma unroll
+      for (int i = 0; i < NR; ++i) {
+        const float h = hs[i][L.hidx[0][s] + r];
+        acc[i].x += h * w0;
+        acc[i].y += h * w1;
+        acc[i].z += h * w2;
+        acc[i].w += h * w3;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NR; ++i) v[i] = add4(v[i], mul4(acc[i], in.lscale));
+}
+
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
 // Two block sums at once (one barrier pair).
@@ -333,32 +363,27 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(const QkvPostArgs a, int 
 // After the O(+LoRA-A) GEMM (LoRA term added by its reduction):
 // x_mid = x_in + oW^T + s (o A^T) B^T (residual, src/kernels/elementwise.cu:
 // 4-15), stash h_o, then the FFN RMSNorm -> fp16.
-template <int P, bool MULTI>
+template <int P>
 __global__ __launch_bounds__(RT) void o_post_kernel(const RowIn in,
                                                     const float* __restrict__ x_in,
                                                     const float* __restrict__ w, float eps, int H,
                                                     float* __restrict__ hbuf,
                                                     float* __restrict__ x_mid,
-                                                    _Float16* __restrict__ xn2, int T, int rpw) {
+                                                    _Float16* __restrict__ xn2) {
   __shared__ float red[2 * RW];
   __shared__ float hs[64];
-  float4 wv[P];
+  const int t = blockIdx.x;
+  float4 wv[P], xi[P];
 #pragma unroll
-  for (int p = 0; p < P; ++p) wv[p] = ld4(w + min(4 * ((int)threadIdx.x + p * RT), H - 4));
-  LoraRegs<P, 1> L;
-  if constexpr (MULTI) lora_load<P, 1>(in, H, L);
-  const int nrows = MULTI ? rpw : 1;
-  for (int it = 0; it < nrows; ++it) {
-  const int t = blockIdx.x * nrows + it;
-  if (t >= T) break;
-  if (it) __syncthreads();
-  float4 xi[P];
-#pragma unroll
-  for (int p = 0; p < P; ++p)
-    xi[p] = ld4(x_in + (long long)t * H + min(4 * ((int)threadIdx.x + p * RT), H - 4));
+  for (int p = 0; p < P; ++p) {
+    const int c = min(4 * ((int)threadIdx.x + p * RT), H - 4);
+    wv[p] = ld4(w + c);
+    xi[p] = ld4(x_in + (long long)t * H + c);
+  }
   float4 v[P], hv;
   load_row<P, true>(in, t, H, v, hv);
-  if constexpr (!MULTI) lora_load<P, 1>(in, H, L);
+  LoraRegs<P, 1> L;
+  lora_load<P, 1>(in, H, L);
   store_h(in, hv, hs);
   if ((int)threadIdx.x < in.nh / 4)
     *reinterpret_cast<float4*>(hbuf + (long long)t * 64 + 3 * R + 4 * threadIdx.x) = hv;
@@ -381,7 +406,6 @@ __global__ __launch_bounds__(RT) void o_post_kernel(const RowIn in,
     st_h4(xn2 + (long long)t * H + c,
           make_float4(v[p].x * r * wv[p].x, v[p].y * r * wv[p].y, v[p].z * r * wv[p].z,
                       v[p].w * r * wv[p].w));
-  }
   }
 }
 
@@ -442,8 +466,8 @@ __device__ __forceinline__ void block_sums(float (&a)[NR], float* red) {
 // side by side (each thread's four columns of every row), so their loads
 // share one memory round trip, their row sums one barrier pair and the
 // adapter values (loaded once) every row.  (The one-row kernel spends a
-// round trip and two barrier phases a row; rows handled one after another
-// in a workgroup measured no faster.)
+// round trip and three barrier phases a row; rows handled one after another
+// in a workgroup, adapter values loaded once, measured no faster than it.)
 template <int NR>
 __global__ __launch_bounds__(RT) void o_post_rows_kernel(const RowIn in,
                                                          const float* __restrict__ x_in,
@@ -472,12 +496,11 @@ __global__ __launch_bounds__(RT) void o_post_rows_kernel(const RowIn in,
       *reinterpret_cast<float4*>(hbuf + (long long)(t0 + i) * 64 + 3 * R + 4 * threadIdx.x) = hv[i];
   }
   __syncthreads();
+  lora_apply_rows<NR, 1>(in, hs, L, v);
   float ssq[NR];
 #pragma unroll
   for (int i = 0; i < NR; ++i) {
-    float4 vi[1] = {v[i]};
-    lora_apply<1, 1>(in, hs[i], L, vi);
-    v[i] = add4(xi[i], vi[0]);
+    v[i] = add4(xi[i], v[i]);
     if (live && t0 + i < T) *reinterpret_cast<float4*>(x_mid + (long long)(t0 + i) * H + c) = v[i];
     ssq[i] = live ? v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w : 0.f;
   }
@@ -487,6 +510,64 @@ __global__ __launch_bounds__(RT) void o_post_rows_kernel(const RowIn in,
     const float r = rsqrtf(ssq[i] / H + eps);
     if (live && t0 + i < T)
       st_h4(xn2 + (long long)(t0 + i) * H + c,
+            make_float4(v[i].x * r * wv.x, v[i].y * r * wv.y, v[i].z * r * wv.z,
+                        v[i].w * r * wv.w));
+  }
+}
+
+// NR block maxima at once (one barrier pair).
+template <int NR>
+__device__ __forceinline__ void block_maxes(float (&a)[NR], float* red) {
+  const int w = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    a[i] = wave_max(a[i]);
+    if ((threadIdx.x & 63) == 0) red[i * RW + w] = a[i];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    float x = red[i * RW];
+#pragma unroll
+    for (int q = 1; q < RW; ++q) x = fmaxf(x, red[i * RW + q]);
+    a[i] = x;
+  }
+  __syncthreads();
+}
+
+// resid_norm for rows of one piece per thread at large T, NR rows a
+// workgroup side by side (as o_post_rows_kernel).
+template <int NR>
+__global__ __launch_bounds__(RT) void resid_norm_rows_kernel(const RowIn in,
+                                                             const float* __restrict__ x_res,
+                                                             const float* __restrict__ w,
+                                                             float eps, int H,
+                                                             float* __restrict__ x_out,
+                                                             _Float16* __restrict__ xn, int T) {
+  __shared__ float red[NR * RW];
+  const int t0 = blockIdx.x * NR;
+  const int c = 4 * (int)threadIdx.x;
+  const int cc = min(c, H - 4);
+  const bool live = c < H;
+  float4 xr[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) xr[i] = ld4(x_res + (long long)min(t0 + i, T - 1) * H + cc);
+  float4 v[NR], hv[NR];
+  load_rows<NR, false>(in, t0, T, H, v, hv);
+  const float4 wv = ld4(w + cc);
+  float ssq[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    v[i] = add4(xr[i], v[i]);
+    if (live && t0 + i < T) *reinterpret_cast<float4*>(x_out + (long long)(t0 + i) * H + c) = v[i];
+    ssq[i] = live ? v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w : 0.f;
+  }
+  block_sums<NR>(ssq, red);
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const float r = rsqrtf(ssq[i] / H + eps);
+    if (live && t0 + i < T)
+      st_h4(xn + (long long)(t0 + i) * H + c,
             make_float4(v[i].x * r * wv.x, v[i].y * r * wv.y, v[i].z * r * wv.z,
                         v[i].w * r * wv.w));
   }
@@ -705,53 +786,74 @@ __global__ __launch_bounds__(RT) void norm_bwd_kernel(const NormBwdArgs a) {
   }
 }
 
-// The same for rows of one piece per thread (P = 1) with three adapter terms
-// at large T: the adapter values are loaded once per workgroup and kept in
-// registers for NR rows (their 196 KB at H = 2048 would otherwise be read
-// again for every row).
-template <int NR>
-__global__ __launch_bounds__(RT) void norm_bwd_lora_kernel(const NormBwdArgs a, int T) {
-  __shared__ float red[2 * RW];
-  __shared__ float hs[64];
+// norm_bwd for rows of one piece per thread at large T, NR rows a workgroup
+// side by side (as o_post_rows_kernel), with no adapter terms or with three
+// (LORA: the attention norm's q, k, v terms, each over all H columns, whose
+// 48 x 4 values a thread loads once for all its rows).
+template <int NR, bool LORA>
+__global__ __launch_bounds__(RT) void norm_bwd_rows_kernel(const NormBwdArgs a, int T) {
+  __shared__ float red[2 * NR * RW];
+  __shared__ float hs[NR][64];
   const int H = a.H;
+  const int t0 = blockIdx.x * NR;
   const int c = 4 * (int)threadIdx.x;
   const int cc = min(c, H - 4);
-  LoraRegs<1, 3> L;
-  lora_load<1, 3>(a.in, H, L);
+  const bool live = c < H;
+  float4 xv[NR], dr[NR];
+  float rs[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const int t = min(t0 + i, T - 1);
+    xv[i] = ld4(a.x + (long long)t * H + cc);
+    dr[i] = a.dres_in ? ld4(a.dres_in + (long long)t * H + cc) : make_float4(0.f, 0.f, 0.f, 0.f);
+    rs[i] = (a.rinv_in ? a.rinv_in[t] : 1.0f) * a.gscale;
+  }
+  float4 v[NR], hv[NR];
+  load_rows<NR, true>(a.in, t0, T, H, v, hv);
   const float4 ww = ld4(a.w + cc);
-#pragma unroll 1
-  for (int it = 0; it < NR; ++it) {
-    const int t = blockIdx.x * NR + it;
-    if (t >= T) break;
-    if (it) __syncthreads();
-    const float4 x = ld4(a.x + (long long)t * H + cc);
-    const float4 dr = a.dres_in ? ld4(a.dres_in + (long long)t * H + cc) : make_float4(0.f, 0.f, 0.f, 0.f);
-    const float rs = (a.rinv_in ? a.rinv_in[t] : 1.0f) * a.gscale;
-    float4 v[1], hv;
-    load_row<1, true, 4>(a.in, t, H, v, hv);  // 4 loads in flight: the adapter values hold 96 VGPRs
-    store_h(a.in, hv, hs);
-    if ((int)threadIdx.x < a.in.nh / 4)
-      *reinterpret_cast<float4*>(a.dh_out + (long long)t * 64 + a.dh_col + 4 * threadIdx.x) =
-          mul4(hv, rs);
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    if (LORA) store_h(a.in, hv[i], hs[i]);
+    if ((int)threadIdx.x < a.in.nh / 4 && t0 + i < T)
+      *reinterpret_cast<float4*>(a.dh_out + (long long)(t0 + i) * 64 + a.dh_col + 4 * threadIdx.x) =
+          mul4(hv[i], rs[i]);
+  }
+  if constexpr (LORA) {
+    LoraRegs<1, 3> L;
+    lora_load<1, 3>(a.in, H, L);
     __syncthreads();
-    lora_apply<1, 3>(a.in, hs, L, v);
-    const bool live = c < H;
-    const float4 d = mul4(v[0], rs);
-    const float dot = live ? d.x * ww.x * x.x + d.y * ww.y * x.y + d.z * ww.z * x.z + d.w * ww.w * x.w : 0.f;
-    const float ssx = live ? x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w : 0.f;
-    const float2 s2 = block_sum2(dot, ssx, red);
-    const float r = rsqrtf(s2.y / H + a.eps);
-    const float coef = r * r / H * s2.x;
-    const float4 o = make_float4(dr.x + r * (d.x * ww.x - coef * x.x), dr.y + r * (d.y * ww.y - coef * x.y),
-                                 dr.z + r * (d.z * ww.z - coef * x.z), dr.w + r * (d.w * ww.w - coef * x.w));
-    if (live) {
-      *reinterpret_cast<float4*>(a.dres_out + (long long)t * H + c) = o;
-      if (a.dmid_out) *reinterpret_cast<float4*>(a.dmid_out + (long long)t * H + c) = o;
+    lora_apply_rows<NR, 3>(a.in, hs, L, v);
+  }
+  float s2[2 * NR];  // dot(d w, x), then sum x^2, of each row
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const float4 d = mul4(v[i], rs[i]), x = xv[i];
+    v[i] = d;
+    s2[i] = live ? d.x * ww.x * x.x + d.y * ww.y * x.y + d.z * ww.z * x.z + d.w * ww.w * x.w : 0.f;
+    s2[NR + i] = live ? x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w : 0.f;
+  }
+  block_sums<2 * NR>(s2, red);
+  float amax[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const float r = rsqrtf(s2[NR + i] / H + a.eps);
+    const float coef = r * r / H * s2[i];
+    const float4 d = v[i], x = xv[i];
+    v[i] = make_float4(dr[i].x + r * (d.x * ww.x - coef * x.x), dr[i].y + r * (d.y * ww.y - coef * x.y),
+                       dr[i].z + r * (d.z * ww.z - coef * x.z), dr[i].w + r * (d.w * ww.w - coef * x.w));
+    if (live && t0 + i < T) {
+      *reinterpret_cast<float4*>(a.dres_out + (long long)(t0 + i) * H + c) = v[i];
+      if (a.dmid_out) *reinterpret_cast<float4*>(a.dmid_out + (long long)(t0 + i) * H + c) = v[i];
     }
-    const float amax = block_max<RW>(live ? amax4(o) : 0.f, red);
-    const float sc = pow2_scale_for(amax);
-    if (threadIdx.x == 0) a.rinv_out[t] = 1.0f / sc;
-    if (live) st_h4(a.g16 + (long long)t * H + c, mul4(o, sc));
+    amax[i] = live ? amax4(v[i]) : 0.f;
+  }
+  block_maxes<NR>(amax, red);
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    if (t0 + i >= T) continue;
+    const float sc = pow2_scale_for(amax[i]);
+    if (threadIdx.x == 0) a.rinv_out[t0 + i] = 1.0f / sc;
+    if (live) st_h4(a.g16 + (long long)(t0 + i) * H + c, mul4(v[i], sc));
   }
 }
 
@@ -1107,21 +1209,24 @@ inline unsigned grid_elems(long long n) {
 
 }  // namespace
 
-// Token rows per workgroup of the one-term LoRA epilogues.  One: the adapter
-// loads (row-major shadows, coalesced) cost less than serialising rows in a
-// workgroup (C4, 4096 rows: 51-53 us at one row against 57 us at eight).
-// LLMT_ROWS_PER_WG > 1 selects the loop variant (adapter values loaded once
-// per workgroup) for rows of at most 2 pieces per thread (P); wider rows kept
-// beside the adapter values across the loop spill.
-static int rows_per_wg(int T, int P) {
-  (void)T;
-  if (P > 2) return 1;
+// Token rows a workgroup of the parallel-rows epilogues (o_post, resid_norm,
+// norm_bwd with rows of one piece per thread): NR rows side by side share a
+// memory round trip, a barrier pair per reduction and (o_post, the attention
+// norm's backward) the adapter values.  At T >= 2048 each kernel takes the
+// count measured best for it (C4, 4096 rows, us at NR = 1 / 2 / 4 / 8):
+// resid_norm 37.1 / 24.2 / 24.5 / 25.6, norm_bwd 41.5 / 32.1 / 34.5 / 41.7,
+// o_post 52.8 / 32.1 / 30.5 / 35.3, norm_bwd with the three adapter terms
+// 82.3 / 76.7 / 68.0 / 58.7 (its 196 KB of adapter values per workgroup).
+// At short T (the B1 x S128 step) one row a workgroup keeps every CU busy.
+// LLMT_ROWS_PER_WG (1, 2, 3, 4 or 8) overrides all of them.
+static int rows_per_wg(int T, int P, int large_t) {
+  if (P != 1) return 1;
   const char* e = getenv("LLMT_ROWS_PER_WG");
   if (e && *e) {
     const int v = atoi(e);
-    if (v >= 1 && v <= 64) return v;
+    if (v == 1 || v == 2 || v == 3 || v == 4 || v == 8) return v;
   }
-  return 1;
+  return T >= 2048 ? large_t : 1;
 }
 
 static bool row_in_ok(const RowIn& in, int n, const char* who) {
@@ -1194,30 +1299,17 @@ hipError_t o_post(const RowIn& in, const float* x_in, const float* w, float eps,
                   float* hbuf, float* x_mid, _Float16* xn2, hipStream_t st) {
   if (!row_in_ok(in, H, "o_post")) return hipErrorInvalidValue;
   const int P = (H + 4 * RT - 1) / (4 * RT);
-  const char* e = getenv("LLMT_O_POST_ROWS");
-  const int nr = e && *e ? atoi(e) : (T >= 2048 ? 4 : 1);
-  if (P == 1 && nr > 1) {
-    switch (nr) {
-      case 2: hipLaunchKernelGGL(o_post_rows_kernel<2>, dim3((T + 1) / 2), dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T); break;
-      case 8: hipLaunchKernelGGL(o_post_rows_kernel<8>, dim3((T + 7) / 8), dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T); break;
-      default: hipLaunchKernelGGL(o_post_rows_kernel<4>, dim3((T + 3) / 4), dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T); break;
-    }
-    LLMT_LAUNCH_CHECK();
-    return hipSuccess;
-  }
-  const int rpw = rows_per_wg(T, P);
-  const dim3 g((T + rpw - 1) / rpw);
-  switch (P) {
-    case 1:
-      if (rpw > 1) hipLaunchKernelGGL((o_post_kernel<1, true>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T, rpw);
-      else hipLaunchKernelGGL((o_post_kernel<1, false>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T, rpw);
-      break;
-    case 2:
-      if (rpw > 1) hipLaunchKernelGGL((o_post_kernel<2, true>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T, rpw);
-      else hipLaunchKernelGGL((o_post_kernel<2, false>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T, rpw);
-      break;
-    case 3: hipLaunchKernelGGL((o_post_kernel<3, false>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T, rpw); break;
-    case 4: hipLaunchKernelGGL((o_post_kernel<4, false>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T, rpw); break;
+  const int nr = rows_per_wg(T, P, 4);
+  const dim3 g((T + nr - 1) / nr);
+  switch (P * 10 + nr) {
+    case 11: hipLaunchKernelGGL((o_post_kernel<1>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2); break;
+    case 12: hipLaunchKernelGGL((o_post_rows_kernel<2>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T); break;
+    case 13: hipLaunchKernelGGL((o_post_rows_kernel<3>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T); break;
+    case 14: hipLaunchKernelGGL((o_post_rows_kernel<4>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T); break;
+    case 18: hipLaunchKernelGGL((o_post_rows_kernel<8>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T); break;
+    case 21: hipLaunchKernelGGL((o_post_kernel<2>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2); break;
+    case 31: hipLaunchKernelGGL((o_post_kernel<3>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2); break;
+    case 41: hipLaunchKernelGGL((o_post_kernel<4>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2); break;
     default:
       set_error("o_post: row width %d above %d", H, 16 * RT);
       return hipErrorInvalidValue;
@@ -1238,11 +1330,17 @@ hipError_t resid_norm(const RowIn& in, const float* x_res, const float* w, float
                       float* x_out, _Float16* xn, hipStream_t st) {
   if (!row_in_ok(in, H, "resid_norm")) return hipErrorInvalidValue;
   const int P = (H + 4 * RT - 1) / (4 * RT);
-  switch (P) {
-    case 1: hipLaunchKernelGGL(resid_norm_kernel<1>, dim3(T), dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn); break;
-    case 2: hipLaunchKernelGGL(resid_norm_kernel<2>, dim3(T), dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn); break;
-    case 3: hipLaunchKernelGGL(resid_norm_kernel<3>, dim3(T), dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn); break;
-    case 4: hipLaunchKernelGGL(resid_norm_kernel<4>, dim3(T), dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn); break;
+  const int nr = rows_per_wg(T, P, 2);
+  const dim3 g((T + nr - 1) / nr);
+  switch (P * 10 + nr) {
+    case 11: hipLaunchKernelGGL(resid_norm_kernel<1>, g, dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn); break;
+    case 12: hipLaunchKernelGGL(resid_norm_rows_kernel<2>, g, dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn, T); break;
+    case 13: hipLaunchKernelGGL(resid_norm_rows_kernel<3>, g, dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn, T); break;
+    case 14: hipLaunchKernelGGL(resid_norm_rows_kernel<4>, g, dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn, T); break;
+    case 18: hipLaunchKernelGGL(resid_norm_rows_kernel<8>, g, dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn, T); break;
+    case 21: hipLaunchKernelGGL(resid_norm_kernel<2>, g, dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn); break;
+    case 31: hipLaunchKernelGGL(resid_norm_kernel<3>, g, dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn); break;
+    case 41: hipLaunchKernelGGL(resid_norm_kernel<4>, g, dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn); break;
     default:
       set_error("resid_norm: row width %d above %d", H, 16 * RT);
       return hipErrorInvalidValue;
@@ -1307,25 +1405,22 @@ hipError_t head_norm_rope(const HeadRows* segs, int nseg, const float* cosT, con
 hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st) {
   if (!row_in_ok(a.in, a.H, "norm_bwd") || a.dh_col % 4) return hipErrorInvalidValue;
   const int P = (a.H + 4 * RT - 1) / (4 * RT);
-  // three adapter terms over one-piece rows at large T: NR rows a workgroup
-  // (C4, 4096 rows: 89 us at one row, 69 us at four; eight measured best;
-  // LLMT_NORM_LORA_ROWS overrides, 1 = the one-row kernel)
-  const char* e = getenv("LLMT_NORM_LORA_ROWS");
-  const int nr = e && *e ? atoi(e) : (T >= 2048 ? 8 : 1);
-  if (P == 1 && a.in.nterm == 3 && nr > 1) {
-    switch (nr) {
-      case 2: hipLaunchKernelGGL(norm_bwd_lora_kernel<2>, dim3((T + 1) / 2), dim3(RT), 0, st, a, T); break;
-      case 8: hipLaunchKernelGGL(norm_bwd_lora_kernel<8>, dim3((T + 7) / 8), dim3(RT), 0, st, a, T); break;
-      default: hipLaunchKernelGGL(norm_bwd_lora_kernel<4>, dim3((T + 3) / 4), dim3(RT), 0, st, a, T); break;
-    }
-    LLMT_LAUNCH_CHECK();
-    return hipSuccess;
-  }
-  switch (P) {
-    case 1: hipLaunchKernelGGL(norm_bwd_kernel<1>, dim3(T), dim3(RT), 0, st, a); break;
-    case 2: hipLaunchKernelGGL(norm_bwd_kernel<2>, dim3(T), dim3(RT), 0, st, a); break;
-    case 3: hipLaunchKernelGGL(norm_bwd_kernel<3>, dim3(T), dim3(RT), 0, st, a); break;
-    case 4: hipLaunchKernelGGL(norm_bwd_kernel<4>, dim3(T), dim3(RT), 0, st, a); break;
+  const bool lora = a.in.nterm > 0;
+  const int nr = rows_per_wg(T, P, lora ? 8 : 2);
+  const dim3 g((T + nr - 1) / nr);
+  switch (P * 100 + nr * 10 + (lora ? 1 : 0)) {
+    case 110: case 111: hipLaunchKernelGGL(norm_bwd_kernel<1>, g, dim3(RT), 0, st, a); break;
+    case 120: hipLaunchKernelGGL((norm_bwd_rows_kernel<2, false>), g, dim3(RT), 0, st, a, T); break;
+    case 121: hipLaunchKernelGGL((norm_bwd_rows_kernel<2, true>), g, dim3(RT), 0, st, a, T); break;
+    case 130: hipLaunchKernelGGL((norm_bwd_rows_kernel<3, false>), g, dim3(RT), 0, st, a, T); break;
+    case 131: hipLaunchKernelGGL((norm_bwd_rows_kernel<3, true>), g, dim3(RT), 0, st, a, T); break;
+    case 140: hipLaunchKernelGGL((norm_bwd_rows_kernel<4, false>), g, dim3(RT), 0, st, a, T); break;
+    case 141: hipLaunchKernelGGL((norm_bwd_rows_kernel<4, true>), g, dim3(RT), 0, st, a, T); break;
+    case 180: hipLaunchKernelGGL((norm_bwd_rows_kernel<8, false>), g, dim3(RT), 0, st, a, T); break;
+    case 181: hipLaunchKernelGGL((norm_bwd_rows_kernel<8, true>), g, dim3(RT), 0, st, a, T); break;
+    case 210: case 211: hipLaunchKernelGGL(norm_bwd_kernel<2>, g, dim3(RT), 0, st, a); break;
+    case 310: case 311: hipLaunchKernelGGL(norm_bwd_kernel<3>, g, dim3(RT), 0, st, a); break;
+    case 410: case 411: hipLaunchKernelGGL(norm_bwd_kernel<4>, g, dim3(RT), 0, st, a); break;
     default:
       set_error("norm_bwd: row width %d above %d", a.H, 16 * RT);
       return hipErrorInvalidValue;
