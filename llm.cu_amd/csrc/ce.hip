@@ -36,21 +36,42 @@ __device__ __forceinline__ void merge(float& m, float& s, float m2, float s2) {
   m = mn;
 }
 
+// A thread's share of a chunk: CE_U float4 pieces, piece k at column
+// j0 + 4 tid + 4 CE_THREADS k, all loaded before any use (pieces past the
+// row end read as -inf).  exp2 is the hardware v_exp_f32 on fma-scaled
+// arguments: the probabilities it cannot represent as fp32 normals
+// (< 2^-126) vanish in the fp16 GEMM operand and leave the row sums unchanged.
+constexpr int CE_U = CE_CHUNK / (4 * CE_THREADS);
+static_assert(CE_U * 4 * CE_THREADS == CE_CHUNK, "chunk = whole float4 pieces a thread");
+__device__ __forceinline__ void ce_load(const float* x, int j0, int j1, float4 (&v)[CE_U]) {
+#pragma unroll
+  for (int k = 0; k < CE_U; ++k) {
+    const int j = j0 + 4 * (int)threadIdx.x + 4 * CE_THREADS * k;
+    v[k] = j < j1 ? *reinterpret_cast<const float4*>(x + j)
+                  : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+  }
+}
+
 __global__ __launch_bounds__(CE_THREADS) void ce_phase1(const float* __restrict__ logits, int V,
                                                         int chunks, float2* __restrict__ stats) {
   const int row = blockIdx.y, ch = blockIdx.x;
-  const float* x = logits + (long long)row * V;
   const int j0 = ch * CE_CHUNK;
   const int j1 = min(V, j0 + CE_CHUNK);
-  float m = -INFINITY, s = 0.f;
   // 16-byte loads; V is a multiple of 4 for every supported vocabulary.
-  for (int j = j0 + threadIdx.x * 4; j < j1; j += CE_THREADS * 4) {
-    const float4 v = *reinterpret_cast<const float4*>(x + j);
-    const float mx = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
-    const float mn = fmaxf(m, mx);
-    s = s * exp2f((m - mn) * LOG2E) + exp2f((v.x - mn) * LOG2E) + exp2f((v.y - mn) * LOG2E) +
-        exp2f((v.z - mn) * LOG2E) + exp2f((v.w - mn) * LOG2E);
-    m = mn;
+  float4 v[CE_U];
+  ce_load(logits + (long long)row * V, j0, j1, v);
+  float m = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < CE_U; ++k) m = fmaxf(m, fmaxf(fmaxf(v[k].x, v[k].y), fmaxf(v[k].z, v[k].w)));
+  float s = 0.f;
+  if (m != -INFINITY) {  // else every piece is past the row end
+    const float m2 = m * LOG2E;
+#pragma unroll
+    for (int k = 0; k < CE_U; ++k)
+      s += (__builtin_amdgcn_exp2f(fmaf(v[k].x, LOG2E, -m2)) +
+            __builtin_amdgcn_exp2f(fmaf(v[k].y, LOG2E, -m2))) +
+           (__builtin_amdgcn_exp2f(fmaf(v[k].z, LOG2E, -m2)) +
+            __builtin_amdgcn_exp2f(fmaf(v[k].w, LOG2E, -m2)));
   }
   // wave then block merge of (m, s)
 #pragma unroll
@@ -71,6 +92,18 @@ __global__ __launch_bounds__(CE_THREADS) void ce_phase1(const float* __restrict_
   }
 }
 
+__device__ __forceinline__ void ce_store(float* dlogits, _Float16* grad16, long long at, float4 g,
+                                         float inv_valid) {
+  if (dlogits)
+    *reinterpret_cast<float4*>(dlogits + at) =
+        make_float4(g.x * inv_valid, g.y * inv_valid, g.z * inv_valid, g.w * inv_valid);
+  if (grad16) {
+    half4 h = {(_Float16)(g.x * kGradLogitScale), (_Float16)(g.y * kGradLogitScale),
+               (_Float16)(g.z * kGradLogitScale), (_Float16)(g.w * kGradLogitScale)};
+    *reinterpret_cast<half4*>(grad16 + at) = h;
+  }
+}
+
 __global__ __launch_bounds__(CE_THREADS) void ce_phase2(const float* __restrict__ logits,
                                                         const int* __restrict__ targets, int V,
                                                         int seq_len, int chunks, float inv_valid,
@@ -84,42 +117,44 @@ __global__ __launch_bounds__(CE_THREADS) void ce_phase2(const float* __restrict_
   const int j1 = min(V, j0 + CE_CHUNK);
   const long long base = (long long)row * V;
   if (!valid) {
-    for (int j = j0 + threadIdx.x * 4; j < j1; j += CE_THREADS * 4) {
-      if (dlogits) *reinterpret_cast<float4*>(dlogits + base + j) = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (grad16) {
-        half4 z = {(_Float16)0.f, (_Float16)0.f, (_Float16)0.f, (_Float16)0.f};
-        *reinterpret_cast<half4*>(grad16 + base + j) = z;
-      }
+#pragma unroll
+    for (int k = 0; k < CE_U; ++k) {
+      const int j = j0 + 4 * (int)threadIdx.x + 4 * CE_THREADS * k;
+      if (j < j1) ce_store(dlogits, grad16, base + j, make_float4(0.f, 0.f, 0.f, 0.f), 0.f);
     }
     if (ch == 0 && threadIdx.x == 0) loss_rows[row] = 0.f;
     return;
   }
+  float4 v[CE_U];
+  ce_load(logits + base, j0, j1, v);
   float M = -INFINITY, S = 0.f;
   for (int c = 0; c < chunks; ++c) {
     const float2 p = stats[(long long)row * chunks + c];
     merge(M, S, p.x, p.y);
   }
   const float lse = M + __logf(S);
+  const float l2 = lse * LOG2E;
   // Out-of-range ids are clamped (never read out of bounds); the reference
   // does not check them.
   const int t = min(max(targets[row], 0), V - 1);
   if (ch == 0 && threadIdx.x == 0) loss_rows[row] = lse - logits[base + t];
-  const float* x = logits + base;
-  for (int j = j0 + threadIdx.x * 4; j < j1; j += CE_THREADS * 4) {
-    const float4 v = *reinterpret_cast<const float4*>(x + j);
-    float g[4] = {exp2f((v.x - lse) * LOG2E), exp2f((v.y - lse) * LOG2E),
-                  exp2f((v.z - lse) * LOG2E), exp2f((v.w - lse) * LOG2E)};
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (j + i == t) g[i] -= 1.0f;
-    if (dlogits)
-      *reinterpret_cast<float4*>(dlogits + base + j) =
-          make_float4(g[0] * inv_valid, g[1] * inv_valid, g[2] * inv_valid, g[3] * inv_valid);
-    if (grad16) {
-      half4 h = {(_Float16)(g[0] * kGradLogitScale), (_Float16)(g[1] * kGradLogitScale),
-                 (_Float16)(g[2] * kGradLogitScale), (_Float16)(g[3] * kGradLogitScale)};
-      *reinterpret_cast<half4*>(grad16 + base + j) = h;
-    }
+  for (int k = 0; k < CE_U; ++k) {
+    const int j = j0 + 4 * (int)threadIdx.x + 4 * CE_THREADS * k;
+    if (j < j1)
+      ce_store(dlogits, grad16, base + j,
+               make_float4(__builtin_amdgcn_exp2f(fmaf(v[k].x, LOG2E, -l2)),
+                           __builtin_amdgcn_exp2f(fmaf(v[k].y, LOG2E, -l2)),
+                           __builtin_amdgcn_exp2f(fmaf(v[k].z, LOG2E, -l2)),
+                           __builtin_amdgcn_exp2f(fmaf(v[k].w, LOG2E, -l2))),
+               inv_valid);
+  }
+  // p - 1 at the target, stored again by the thread whose piece holds it
+  // (program order puts it after that thread's first store)
+  if (t >= j0 && t < j1 && (((t - j0) >> 2) & (CE_THREADS - 1)) == (int)threadIdx.x) {
+    const float gt = __builtin_amdgcn_exp2f(fmaf(logits[base + t], LOG2E, -l2)) - 1.0f;
+    if (dlogits) dlogits[base + t] = gt * inv_valid;
+    if (grad16) grad16[base + t] = (_Float16)(gt * kGradLogitScale);
   }
 }
 
