@@ -150,10 +150,13 @@ int llmt_layer_backward(llmt_ctx* ctx, int layer, const float* dy, float* dx, in
 
 // ------------------------------------------------------------------ C1
 
-// lm_head GEMMs on packed operands E (K = H) and ET (K = V), fused CE between.
+// lm_head GEMMs on packed operands E (K = H) and ET (K = V), fused CE between:
+// the logits GEMM also writes the softmax pairs of its column tiles (stats:
+// T * ce_stats_per_row(V) pairs; lse: T floats), so the CE reads the logits
+// once.
 static int head_ce_packed(hipStream_t st, const _Float16* hidden, const _Float16* E,
                           const _Float16* ET, const int* targets, int T, int seq_len, int H,
-                          int V, float* logits, _Float16* grad16, float2* stats,
+                          int V, float* logits, _Float16* grad16, float2* stats, float* lse,
                           float* loss_rows, float* loss_mean, float* dlogits, float* dhidden,
                           float* part, size_t part_elems) {
   GemmArgs g{};
@@ -167,9 +170,12 @@ static int head_ce_packed(hipStream_t st, const _Float16* hidden, const _Float16
   g.split = 1;
   g.C = logits;
   g.ldc = V;
+  const int nt = gemm_rowstats_tiles(g);
+  TRY_ARG(nt > 0 && nt <= ce_stats_per_row(V), "head_ce: logits tile statistics");
+  g.rowstats = stats;
   TRY_HIP(gemm_nt(g, st));
-  TRY_HIP(cross_entropy(logits, targets, T, V, seq_len, stats, dlogits, grad16, loss_rows,
-                        loss_mean, st));
+  TRY_HIP(cross_entropy_from_stats(logits, stats, nt, targets, T, V, seq_len, lse, dlogits, grad16,
+                                   loss_rows, loss_mean, st));
   GemmArgs d{};
   d.A = grad16;
   d.lda = V;
@@ -208,8 +214,8 @@ int llmt_head_ce(llmt_ctx* ctx, const void* hidden16, const int* targets, int ba
   TRY_ARG(batch >= 1 && batch <= c->maxB && (batch * c->S) % 16 == 0, "batch");
   const int T = batch * c->S;
   int rc = head_ce_packed(c->st, (const _Float16*)hidden16, c->Eh, c->EhT, targets, T, c->S, c->H,
-                          c->V, c->logits, c->grad16, c->ce_stats, c->loss_rows, c->loss_dev,
-                          dlogits, dhidden, c->part, c->part_elems);
+                          c->V, c->logits, c->grad16, c->ce_stats, c->lse_rows, c->loss_rows,
+                          c->loss_dev, dlogits, dhidden, c->part, c->part_elems);
   if (rc) return rc;
   TRY_HIP(hipMemcpyAsync(c->host_loss, c->loss_dev, 4, hipMemcpyDeviceToHost, c->st));
   TRY_HIP(hipStreamSynchronize(c->st));
@@ -230,15 +236,17 @@ int llmt_lm_head_ce(const void* hidden, const void* W, const int* targets, int T
   _Float16* ET = tmp.get<_Float16>((size_t)V * H);
   float* logits = tmp.get<float>((size_t)T * V);
   _Float16* g16 = tmp.get<_Float16>((size_t)T * V);
-  float2* stats = tmp.get<float2>((size_t)T * ce_chunks(V));
+  float2* stats = tmp.get<float2>((size_t)T * ce_stats_per_row(V));
   float* rows = tmp.get<float>(T);
+  float* lse = tmp.get<float>(T);
   const size_t pe = (size_t)gemm_pick_split(T, H, V, 64) * T * H;
   float* part = tmp.get<float>(pe);
-  TRY_ARG(E && ET && logits && g16 && stats && rows && part, "llmt_lm_head_ce: out of memory");
+  TRY_ARG(E && ET && logits && g16 && stats && rows && lse && part,
+          "llmt_lm_head_ce: out of memory");
   TRY_HIP(pack_f16((const _Float16*)W, H, 0, V, H, E, H, 0, 0, st));
   TRY_HIP(pack_f16((const _Float16*)W, H, 1, H, V, ET, V, 0, 0, st));
   return head_ce_packed(st, (const _Float16*)hidden, E, ET, targets, T, seq_len, H, V, logits, g16,
-                        stats, rows, loss_mean, dlogits, dhidden, part, pe);
+                        stats, lse, rows, loss_mean, dlogits, dhidden, part, pe);
 }
 
 // ------------------------------------------------------------------ C3

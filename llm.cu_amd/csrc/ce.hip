@@ -12,9 +12,14 @@
 //            epilogue divides it out exactly).  The chunk's second read hits
 //            L2 / MALL (the 77.8 MB of logits fit in the 256 MB MALL).
 //   phase 3: one workgroup sums the per-row losses in a fixed order.
+// In the training step and the lm_head entry point the logits GEMM writes
+// the (max, sum exp) pairs of its column tiles itself (GemmArgs::rowstats):
+// phase 1 is then a merge of those pairs per row (ce_lse_kernel) and the
+// logits are read once.
 // Rows i with (i % seq_len) == seq_len - 1 have no target inside their
 // window (loss.cu:18-21); their loss is 0 and their dlogits row is written
 // as zeros (the reference leaves it uninitialised).
+#include <algorithm>
 #include <mutex>
 
 #include "../../include/llmt.h"
@@ -30,10 +35,7 @@ constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 
 __device__ __forceinline__ void merge(float& m, float& s, float m2, float s2) {
-  const float mn = fmaxf(m, m2);
-  if (mn == -INFINITY) return;
-  s = s * exp2f((m - mn) * LOG2E) + s2 * exp2f((m2 - mn) * LOG2E);
-  m = mn;
+  softmax_merge(m, s, m2, s2);
 }
 
 // A thread's share of a chunk: CE_U float4 pieces, piece k at column
@@ -104,10 +106,14 @@ __device__ __forceinline__ void ce_store(float* dlogits, _Float16* grad16, long 
   }
 }
 
+// FROM_LSE: the row's lse comes from lse_rows (ce_lse_kernel, which also
+// wrote the row loss), else from merging the row's chunk pairs in stats.
+template <bool FROM_LSE>
 __global__ __launch_bounds__(CE_THREADS) void ce_phase2(const float* __restrict__ logits,
                                                         const int* __restrict__ targets, int V,
                                                         int seq_len, int chunks, float inv_valid,
                                                         const float2* __restrict__ stats,
+                                                        const float* __restrict__ lse_rows,
                                                         float* __restrict__ dlogits,
                                                         _Float16* __restrict__ grad16,
                                                         float* __restrict__ loss_rows) {
@@ -122,22 +128,27 @@ __global__ __launch_bounds__(CE_THREADS) void ce_phase2(const float* __restrict_
       const int j = j0 + 4 * (int)threadIdx.x + 4 * CE_THREADS * k;
       if (j < j1) ce_store(dlogits, grad16, base + j, make_float4(0.f, 0.f, 0.f, 0.f), 0.f);
     }
-    if (ch == 0 && threadIdx.x == 0) loss_rows[row] = 0.f;
+    if (!FROM_LSE && ch == 0 && threadIdx.x == 0) loss_rows[row] = 0.f;
     return;
   }
   float4 v[CE_U];
   ce_load(logits + base, j0, j1, v);
-  float M = -INFINITY, S = 0.f;
-  for (int c = 0; c < chunks; ++c) {
-    const float2 p = stats[(long long)row * chunks + c];
-    merge(M, S, p.x, p.y);
+  float lse;
+  if constexpr (FROM_LSE) {
+    lse = lse_rows[row];
+  } else {
+    float M = -INFINITY, S = 0.f;
+    for (int c = 0; c < chunks; ++c) {
+      const float2 p = stats[(long long)row * chunks + c];
+      merge(M, S, p.x, p.y);
+    }
+    lse = M + __logf(S);
   }
-  const float lse = M + __logf(S);
   const float l2 = lse * LOG2E;
   // Out-of-range ids are clamped (never read out of bounds); the reference
   // does not check them.
   const int t = min(max(targets[row], 0), V - 1);
-  if (ch == 0 && threadIdx.x == 0) loss_rows[row] = lse - logits[base + t];
+  if (!FROM_LSE && ch == 0 && threadIdx.x == 0) loss_rows[row] = lse - logits[base + t];
 #pragma unroll
   for (int k = 0; k < CE_U; ++k) {
     const int j = j0 + 4 * (int)threadIdx.x + 4 * CE_THREADS * k;
@@ -158,6 +169,45 @@ __global__ __launch_bounds__(CE_THREADS) void ce_phase2(const float* __restrict_
   }
 }
 
+// A row's lse from the ntiles (max, sum exp) pairs the logits GEMM wrote:
+// thread i merges tiles i, i + CE_THREADS, .. in order, then the threads'
+// pairs meet in a fixed butterfly and the waves' in wave order; also the
+// row's loss lse - x_t (0 for rows without a target).
+__global__ __launch_bounds__(CE_THREADS) void ce_lse_kernel(const float2* __restrict__ stats,
+                                                            int ntiles,
+                                                            const float* __restrict__ logits,
+                                                            const int* __restrict__ targets, int V,
+                                                            int seq_len,
+                                                            float* __restrict__ lse_rows,
+                                                            float* __restrict__ loss_rows) {
+  const int row = blockIdx.x;
+  float m = -INFINITY, s = 0.f;
+  for (int i = threadIdx.x; i < ntiles; i += CE_THREADS) {
+    const float2 p = stats[(long long)row * ntiles + i];
+    merge(m, s, p.x, p.y);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float m2 = __shfl_xor(m, o, 64), s2 = __shfl_xor(s, o, 64);
+    merge(m, s, m2, s2);
+  }
+  __shared__ float rm[CE_THREADS / 64], rs[CE_THREADS / 64];
+  if ((threadIdx.x & 63) == 0) {
+    rm[threadIdx.x >> 6] = m;
+    rs[threadIdx.x >> 6] = s;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float M = rm[0], S = rs[0];
+    for (int i = 1; i < CE_THREADS / 64; ++i) merge(M, S, rm[i], rs[i]);
+    const float lse = M + __logf(S);
+    lse_rows[row] = lse;
+    const bool valid = (row % seq_len) != seq_len - 1;
+    const int t = min(max(targets[row], 0), V - 1);
+    loss_rows[row] = valid ? lse - logits[(long long)row * V + t] : 0.f;
+  }
+}
+
 // Deterministic mean over valid rows (fixed summation order).
 __global__ __launch_bounds__(CE_THREADS) void ce_mean(const float* __restrict__ loss_rows, int rows,
                                                       float inv_valid, float* __restrict__ out) {
@@ -171,6 +221,7 @@ __global__ __launch_bounds__(CE_THREADS) void ce_mean(const float* __restrict__ 
 }  // namespace
 
 int ce_chunks(int V) { return (V + CE_CHUNK - 1) / CE_CHUNK; }
+int ce_stats_per_row(int V) { return std::max(ce_chunks(V), (V + 127) / 128); }
 
 hipError_t cross_entropy(const float* logits, const int* targets, int rows, int V, int seq_len,
                          float2* stats, float* dlogits, _Float16* grad16, float* loss_rows,
@@ -185,8 +236,36 @@ hipError_t cross_entropy(const float* logits, const int* targets, int rows, int 
   hipLaunchKernelGGL(ce_phase1, dim3(chunks, rows), dim3(CE_THREADS), 0, st, logits, V, chunks,
                      stats);
   LLMT_LAUNCH_CHECK();
-  hipLaunchKernelGGL(ce_phase2, dim3(chunks, rows), dim3(CE_THREADS), 0, st, logits, targets, V,
-                     seq_len, chunks, inv_valid, stats, dlogits, grad16, loss_rows);
+  hipLaunchKernelGGL(ce_phase2<false>, dim3(chunks, rows), dim3(CE_THREADS), 0, st, logits,
+                     targets, V, seq_len, chunks, inv_valid, stats, nullptr, dlogits, grad16,
+                     loss_rows);
+  LLMT_LAUNCH_CHECK();
+  if (loss_mean) {
+    hipLaunchKernelGGL(ce_mean, dim3(1), dim3(CE_THREADS), 0, st, loss_rows, rows, inv_valid,
+                       loss_mean);
+    LLMT_LAUNCH_CHECK();
+  }
+  return hipSuccess;
+}
+
+hipError_t cross_entropy_from_stats(const float* logits, const float2* stats, int ntiles,
+                                    const int* targets, int rows, int V, int seq_len, float* lse,
+                                    float* dlogits, _Float16* grad16, float* loss_rows,
+                                    float* loss_mean, hipStream_t st) {
+  if (V % 4 || seq_len < 2 || rows % seq_len || ntiles < 1 || !stats || !lse) {
+    set_error("cross_entropy_from_stats: unsupported V=%d seq_len=%d rows=%d ntiles=%d", V,
+              seq_len, rows, ntiles);
+    return hipErrorInvalidValue;
+  }
+  const int chunks = ce_chunks(V);
+  const int n_valid = rows / seq_len * (seq_len - 1);
+  const float inv_valid = 1.0f / (float)n_valid;
+  hipLaunchKernelGGL(ce_lse_kernel, dim3(rows), dim3(CE_THREADS), 0, st, stats, ntiles, logits,
+                     targets, V, seq_len, lse, loss_rows);
+  LLMT_LAUNCH_CHECK();
+  hipLaunchKernelGGL(ce_phase2<true>, dim3(chunks, rows), dim3(CE_THREADS), 0, st, logits,
+                     targets, V, seq_len, chunks, inv_valid, nullptr, lse, dlogits, grad16,
+                     loss_rows);
   LLMT_LAUNCH_CHECK();
   if (loss_mean) {
     hipLaunchKernelGGL(ce_mean, dim3(1), dim3(CE_THREADS), 0, st, loss_rows, rows, inv_valid,

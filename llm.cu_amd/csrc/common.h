@@ -52,6 +52,57 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Online-softmax pairs (m, s = sum exp(x - m)): (m, s) <- the pair of the
+// union with (m2, s2).  Empty pairs are (-inf, 0).
+__device__ __forceinline__ void softmax_merge(float& m, float& s, float m2, float s2) {
+  constexpr float kLog2e = 1.4426950408889634f;
+  const float mn = fmaxf(m, m2);
+  if (mn == -INFINITY) return;
+  s = s * __builtin_amdgcn_exp2f((m - mn) * kLog2e) + s2 * __builtin_amdgcn_exp2f((m2 - mn) * kLog2e);
+  m = mn;
+}
+
+// Value of another lane of the same 16-lane row through a DPP modifier (a
+// VALU operand, no LDS): quad_perm [1,0,3,2] (0xB1) and [2,3,0,1] (0x4E),
+// row_half_mirror (0x141, lane i <- 7 - i within 8) and row_mirror (0x140,
+// lane i <- 15 - i within 16).  After the two quad steps every lane of a
+// quad holds the quad's result, so the two mirrors finish a reduction over
+// the 16 lanes.
+template <int CTRL>
+__device__ __forceinline__ float dpp16(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float max16(float v) {
+  v = fmaxf(v, dpp16<0xB1>(v));
+  v = fmaxf(v, dpp16<0x4E>(v));
+  v = fmaxf(v, dpp16<0x141>(v));
+  return fmaxf(v, dpp16<0x140>(v));
+}
+__device__ __forceinline__ float sum16_dpp(float v) {
+  v += dpp16<0xB1>(v);
+  v += dpp16<0x4E>(v);
+  v += dpp16<0x141>(v);
+  return v + dpp16<0x140>(v);
+}
+
+// The pair of NF values x[f] of one row held by each of the 16 lanes of a
+// lane group (lanes 16 q .. 16 q + 15): every lane gets it.
+template <int NF>
+__device__ __forceinline__ float2 softmax_pair16(const float (&x)[NF]) {
+  constexpr float kLog2e = 1.4426950408889634f;
+  float m = -INFINITY;
+#pragma unroll
+  for (int f = 0; f < NF; ++f) m = fmaxf(m, x[f]);
+  m = max16(m);
+  float s = 0.f;
+  if (m != -INFINITY) {
+    const float m2 = m * kLog2e;
+#pragma unroll
+    for (int f = 0; f < NF; ++f) s += __builtin_amdgcn_exp2f(fmaf(x[f], kLog2e, -m2));
+  }
+  return make_float2(m, sum16_dpp(s));
+}
+
 // Block-wide reductions for blocks of NW waves; `red` is LDS of >= NW floats.
 // Every thread gets the result.  Contains __syncthreads().
 template <int NW>

@@ -161,7 +161,8 @@ int Ctx::init() {
   TRY_PTR(xf16 = alloc_n<_Float16>(T * H));
   TRY_PTR(logits = alloc_n<float>(T * V));
   TRY_PTR(grad16 = alloc_n<_Float16>(T * V));
-  TRY_PTR(ce_stats = alloc_n<float2>(T * ce_chunks(V)));
+  TRY_PTR(ce_stats = alloc_n<float2>((size_t)T * ce_stats_per_row(V)));
+  TRY_PTR(lse_rows = alloc_n<float>(T));
   TRY_PTR(loss_rows = alloc_n<float>(T));
   TRY_PTR(loss_dev = alloc_n<float>(1));
   TRY_PTR(tok_buf = alloc_n<int>(T));

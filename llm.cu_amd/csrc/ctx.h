@@ -116,7 +116,9 @@ struct Ctx {
   _Float16* xf16 = nullptr;
   float* logits = nullptr;
   _Float16* grad16 = nullptr;
-  float2* ce_stats = nullptr;
+  float2* ce_stats = nullptr;  // [Tmax, ce_stats_per_row(V)]: CE chunk or logits-tile pairs
+  float* lse_rows = nullptr;   // [Tmax]
+  int head_tiles = 0;          // > 0: the last forward's logits GEMM wrote its tile pairs
   float* loss_rows = nullptr;
   float* loss_dev = nullptr;
   float* host_loss = nullptr;
@@ -190,9 +192,11 @@ struct Ctx {
   // fused SwiGLU epilogue (split 1, gemm_glu_ok shapes only) writes [gate |
   // up] fp16 [M, N] to gu16 and fp16(silu(gate) * up) [M, N / 2] to glu16
   // (direct and ldc unused).
+  // rowstats (direct only): also the per-(row, column tile) softmax pairs
+  // (GemmArgs::rowstats); *tiles gets their row width.
   hipError_t gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int nseg, int M, int K,
                   float* direct, int ldc, GemmOut* out, _Float16* glu16 = nullptr,
-                  _Float16* gu16 = nullptr);
+                  _Float16* gu16 = nullptr, float2* rowstats = nullptr, int* tiles = nullptr);
   // A GEMM's partials as a row-epilogue input with raw h columns
   // [hcol, hcol + nh) and LoRA up-projection terms.
   RowIn row_in(const GemmOut& go, int hcol = 0, int nh = 0, int nterm = 0,

@@ -235,18 +235,44 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
   }
 
   float* C = g.C + (long long)blockIdx.y * g.split_stride;
+  float cs[NF];
+#pragma unroll
+  for (int f = 0; f < NF; ++f) cs[f] = cscale[f] ? (float)cscale[f][lane & 15] : 1.0f;
 #pragma unroll
   for (int f = 0; f < NF; ++f) {
     if (!valid[f]) continue;
     const int col = ncol[f] + (lane & 15);
-    const float cs = cscale[f] ? (float)cscale[f][lane & 15] : 1.0f;
 #pragma unroll
     for (int mi = 0; mi < MF; ++mi) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int row = m0 + mi * 16 + (lane >> 4) * 4 + v;
-        C[(long long)row * g.ldc + col] = acc[mi][f][v] * cs;
+        C[(long long)row * g.ldc + col] = acc[mi][f][v] * cs[f];
       }
+    }
+  }
+  if (g.rowstats) {
+    // each row's (max, sum exp) over the workgroup's NW NF 16 columns: a
+    // wave's pair from its 16-lane groups, the NW waves merged in wave order
+    float2* sh = reinterpret_cast<float2*>(&As[0][0]);  // [MT][NW]
+    static_assert(MT * NW * 8 <= 2 * MT * CH * 2, "pairs fit in the A buffers");
+    __syncthreads();  // every wave is past its last A fragment read
+#pragma unroll
+    for (int mi = 0; mi < MF; ++mi)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float x[NF];
+#pragma unroll
+        for (int f = 0; f < NF; ++f) x[f] = valid[f] ? acc[mi][f][v] * cs[f] : -INFINITY;
+        const float2 p = softmax_pair16<NF>(x);
+        if ((lane & 15) == 0) sh[(mi * 16 + (lane >> 4) * 4 + v) * NW + wave] = p;
+      }
+    __syncthreads();
+    for (int r = tid; r < MT; r += NT) {
+      float m = -INFINITY, s = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) softmax_merge(m, s, sh[r * NW + w].x, sh[r * NW + w].y);
+      g.rowstats[(long long)(m0 + r) * gridDim.x + blockIdx.x] = make_float2(m, s);
     }
   }
 }
@@ -424,18 +450,50 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
       }
     return;
   }
+  float scj[NFR];
+#pragma unroll
+  for (int j = 0; j < NFR; ++j) {
+    const int col = n0 + wn * WC + j * 16 + (lane & 15);
+    scj[j] = cs && col < g.N ? (float)cs[col] : 1.0f;
+  }
 #pragma unroll
   for (int j = 0; j < NFR; ++j) {
     const int col = n0 + wn * WC + j * 16 + (lane & 15);
     if (col >= g.N) continue;
-    const float sc = cs ? (float)cs[col] : 1.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int row = m0 + wm * 128 + i * 16 + (lane >> 4) * 4 + v;
-        C[(long long)row * g.ldc + col] = acc[i][j][v] * sc;
+        C[(long long)row * g.ldc + col] = acc[i][j][v] * scj[j];
       }
+  }
+  if (g.rowstats) {
+    // each row's (max, sum exp) over the tile's 256 columns: a wave's pair
+    // over its WC columns from its 16-lane groups, the WNN waves of a row
+    // block merged in order (the ring is free: every DMA has landed)
+    float2* sh = reinterpret_cast<float2*>(smem);  // [256 rows][WNN]
+    __syncthreads();  // every wave is past its last fragment read
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float x[NFR];
+#pragma unroll
+        for (int j = 0; j < NFR; ++j) {
+          const int col = n0 + wn * WC + j * 16 + (lane & 15);
+          x[j] = col < g.N ? acc[i][j][v] * scj[j] : -INFINITY;
+        }
+        const float2 p = softmax_pair16<NFR>(x);
+        if ((lane & 15) == 0) sh[(wm * 128 + i * 16 + (lane >> 4) * 4 + v) * WNN + wn] = p;
+      }
+    __syncthreads();
+    for (int r = tid; r < 256; r += WNN * 128) {
+      float m = -INFINITY, s = 0.f;
+#pragma unroll
+      for (int w = 0; w < WNN; ++w) softmax_merge(m, s, sh[r * WNN + w].x, sh[r * WNN + w].y);
+      g.rowstats[(long long)(m0 + r) * ntn + tn] = make_float2(m, s);
+    }
   }
 }
 
@@ -967,6 +1025,12 @@ static int big_split(int M, int N, int K, int max_split) {
 
 // The DMA large-tile kernel carries the SwiGLU epilogue: 256-wide tiles over
 // 8 waves, gate/up fragment pairs per wave.
+int gemm_rowstats_tiles(const GemmArgs& g) {
+  if (g.split != 1 || g.nseg != 1 || g.glu || g.N < 16) return 0;
+  if (use_big_tiles(g)) return (g.N + 255) / 256;  // gemm_dma_kernel tiles
+  return (g.N + kNW * kNF * 16 - 1) / (kNW * kNF * 16);  // gemm_nt_kernel workgroups
+}
+
 bool gemm_glu_ok(int M, int I, int K, bool i8) {
   if (big_tiles(M, K))
     return I % 128 == 0 && big_split(M, 2 * I, K, 64) == 1;
@@ -1020,7 +1084,8 @@ static void launch_skinny(const GemmArgs& g, int nb, hipStream_t st) {
 static hipError_t launch_m128(const GemmArgs& g, hipStream_t st) {
   bool i8 = false;
   for (int i = 0; i < g.nseg; ++i) i8 = i8 || g.seg[i].is_i8;
-  if (i8 || !skinny_ok(g.M, g.N, g.K) || g.split > g.K / 64) return launch_mf<8>(g, st);
+  if (i8 || g.rowstats || !skinny_ok(g.M, g.N, g.K) || g.split > g.K / 64)
+    return launch_mf<8>(g, st);
   const int nb = skinny_plan(g.M, g.N, g.K).nb;
   const int stages = skinny_stages();
   if (stages == 6 && nb > 4) {
@@ -1047,7 +1112,8 @@ const char* gemm_kernel_name(const GemmArgs& g) {
   if (g.glu) return "gemm_skinny_glu";
   bool i8 = false;
   for (int i = 0; i < g.nseg; ++i) i8 = i8 || g.seg[i].is_i8;
-  if ((g.M / 16) % 8 == 0 && !i8 && skinny_ok(g.M, g.N, g.K) && g.split <= g.K / 64)
+  if ((g.M / 16) % 8 == 0 && !i8 && !g.rowstats && skinny_ok(g.M, g.N, g.K) &&
+      g.split <= g.K / 64)
     return "gemm_skinny";
   return "gemm_nt";
 }
@@ -1066,6 +1132,10 @@ hipError_t gemm_nt(const GemmArgs& g, hipStream_t st) {
   if (g.glu && !(g.N == 2 * g.glu && g.nseg == 1 && g.split == 1 && g.glu16 && g.gu16 &&
                  gemm_glu_ok(g.M, g.glu, g.K, g.seg[0].is_i8))) {
     set_error("gemm_nt: SwiGLU epilogue needs split 1, one segment, N = 2 x %d", g.glu);
+    return hipErrorInvalidValue;
+  }
+  if (g.rowstats && gemm_rowstats_tiles(g) == 0) {
+    set_error("gemm_nt: row statistics need split 1, one segment and no SwiGLU epilogue");
     return hipErrorInvalidValue;
   }
   if (g.glu && !use_big_tiles(g)) {

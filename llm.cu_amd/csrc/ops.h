@@ -40,9 +40,18 @@ struct GemmArgs {
   _Float16* glu16;
   int ldglu;
   _Float16* gu16;
+  // rowstats (split 1, one segment, no SwiGLU): the epilogue also writes,
+  // for every row m and column tile t of the launch, the online-softmax pair
+  // (max, sum exp(C - max)) of the row's stored values in the tile:
+  // rowstats[m * gemm_rowstats_tiles(g) + t] (the fused cross entropy's
+  // statistics of the lm_head logits, so the logits are read only once).
+  float2* rowstats;
 };
 // The fused SwiGLU epilogue exists for this GEMM shape and weight type.
 bool gemm_glu_ok(int M, int I, int K, bool i8);
+// Column tiles per row whose statistics gemm_nt writes for g.rowstats (the
+// row width of the rowstats array), 0 if this GEMM cannot write them.
+int gemm_rowstats_tiles(const GemmArgs& g);
 
 // Every B segment is fragment-packed (packed_index, common.h) with row
 // length K; rows a multiple of 16.  A is row-major fp16 [M, lda], K % 32 == 0.
@@ -100,9 +109,18 @@ hipError_t f32_scale_to_f16(const float* s, _Float16* d, int n, hipStream_t st);
 // fp16 (p - 1[j=t]) * 2^14; dlogits (may be NULL) receives fp32
 // (p - 1[j=t]) / n_valid.  loss_rows[r] = lse - x_t (0 for invalid rows).
 int ce_chunks(int V);
+// float2 pairs a row that hold either the CE's chunk pairs or a logits
+// GEMM's tile pairs (every tile width gemm_nt uses is >= 128 columns).
+int ce_stats_per_row(int V);
 hipError_t cross_entropy(const float* logits, const int* targets, int rows, int V, int seq_len,
                          float2* stats, float* dlogits, _Float16* grad16, float* loss_rows,
                          float* loss_mean, hipStream_t st);
+// The same from statistics the logits GEMM wrote (GemmArgs::rowstats, ntiles
+// pairs a row): one pass over the logits.  lse: float [rows] workspace.
+hipError_t cross_entropy_from_stats(const float* logits, const float2* stats, int ntiles,
+                                    const int* targets, int rows, int V, int seq_len, float* lse,
+                                    float* dlogits, _Float16* grad16, float* loss_rows,
+                                    float* loss_mean, hipStream_t st);
 constexpr float kGradLogitScale = 16384.0f;  // 2^14
 
 // ---------------------------------------------------------------- row kernels

@@ -1217,16 +1217,17 @@ inline unsigned grid_elems(long long n) {
 // resid_norm 37.1 / 24.2 / 24.5 / 25.6, norm_bwd 41.5 / 32.1 / 34.5 / 41.7,
 // o_post 52.8 / 32.1 / 30.5 / 35.3, norm_bwd with the three adapter terms
 // 82.3 / 76.7 / 68.0 / 58.7 (its 196 KB of adapter values per workgroup).
-// At short T (the B1 x S128 step) one row a workgroup keeps every CU busy.
+// At short T (the B1 x S128 step) one row a workgroup keeps more CUs busy,
+// except for resid_norm (4.84 against 4.39 us at two rows, 128 rows).
 // LLMT_ROWS_PER_WG (1, 2, 3, 4 or 8) overrides all of them.
-static int rows_per_wg(int T, int P, int large_t) {
+static int rows_per_wg(int T, int P, int large_t, int small_t = 1) {
   if (P != 1) return 1;
   const char* e = getenv("LLMT_ROWS_PER_WG");
   if (e && *e) {
     const int v = atoi(e);
     if (v == 1 || v == 2 || v == 3 || v == 4 || v == 8) return v;
   }
-  return T >= 2048 ? large_t : 1;
+  return T >= 2048 ? large_t : small_t;
 }
 
 static bool row_in_ok(const RowIn& in, int n, const char* who) {
@@ -1330,7 +1331,7 @@ hipError_t resid_norm(const RowIn& in, const float* x_res, const float* w, float
                       float* x_out, _Float16* xn, hipStream_t st) {
   if (!row_in_ok(in, H, "resid_norm")) return hipErrorInvalidValue;
   const int P = (H + 4 * RT - 1) / (4 * RT);
-  const int nr = rows_per_wg(T, P, 2);
+  const int nr = rows_per_wg(T, P, 2, 2);
   const dim3 g((T + nr - 1) / nr);
   switch (P * 10 + nr) {
     case 11: hipLaunchKernelGGL(resid_norm_kernel<1>, g, dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn); break;

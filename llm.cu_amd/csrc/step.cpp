@@ -49,7 +49,8 @@ Ctx::~Ctx() {
 // ------------------------------------------------------------------ launches
 
 hipError_t Ctx::gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int nseg, int M, int K,
-                     float* direct, int ldc, GemmOut* out, _Float16* glu16, _Float16* gu16) {
+                     float* direct, int ldc, GemmOut* out, _Float16* glu16, _Float16* gu16,
+                     float2* rowstats, int* tiles) {
   GemmArgs g{};
   g.A = A;
   g.lda = lda;
@@ -72,6 +73,15 @@ hipError_t Ctx::gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int 
     g.C = direct;
     g.ldc = ldc;
     g.split_stride = 0;
+    if (rowstats) {
+      const int nt = gemm_rowstats_tiles(g);
+      if (nt <= 0 || (size_t)M * nt > (size_t)Tmax * ce_stats_per_row(V)) {
+        set_error("gemm: row statistics unavailable for this shape (%d tiles)", nt);
+        return hipErrorInvalidValue;
+      }
+      g.rowstats = rowstats;
+      if (tiles) *tiles = nt;
+    }
   } else {
     g.split = gemm_pick_split(M, g.N, K, 64);
     g.C = part;
@@ -252,10 +262,16 @@ hipError_t Ctx::forward(const int* tok, int B, float* logits_out) {
     LLMT_HIP_TRY(layer_fwd(l, B, last ? final_norm : layers[l + 1].attn_norm,
                            last ? x_final : stash[l + 1].x_in, last ? xf16 : stash[l + 1].xn));
   }
-  // lm_head logits (tied embedding)
+  // lm_head logits (tied embedding); into the context's logits with the
+  // softmax pairs of the GEMM's column tiles for the fused cross entropy
   BSeg se[1] = {hseg(Eh, V, H)};
-  LLMT_HIP_TRY(gemm(CAT_GEMM_HEAD, xf16, H, se, 1, T, H, logits_out ? logits_out : logits, V,
-                    nullptr));
+  if (logits_out) {
+    head_tiles = 0;
+    LLMT_HIP_TRY(gemm(CAT_GEMM_HEAD, xf16, H, se, 1, T, H, logits_out, V, nullptr));
+  } else {
+    LLMT_HIP_TRY(gemm(CAT_GEMM_HEAD, xf16, H, se, 1, T, H, logits, V, nullptr, nullptr, nullptr,
+                      ce_stats, &head_tiles));
+  }
   return hipSuccess;
 }
 
@@ -264,7 +280,15 @@ hipError_t Ctx::ce(const float* lg, const int* tgt, int B, float* dlogits_out) {
   const int rows = B * S, Vv = V, Ss = S;
   float2* stats = ce_stats;
   _Float16* g16c = grad16;
-  float *lr = loss_rows, *lm = loss_dev;
+  float *lr = loss_rows, *lm = loss_dev, *lse = lse_rows;
+  if (!lg && head_tiles > 0) {  // the forward's logits with their tile pairs
+    const int nt = head_tiles;
+    LLMT_HIP_TRY(run(CAT_CE, "cross_entropy", [=](hipStream_t q) {
+      return cross_entropy_from_stats(x, stats, nt, tgt, rows, Vv, Ss, lse, dlogits_out, g16c, lr,
+                                      lm, q);
+    }));
+    return hipSuccess;
+  }
   LLMT_HIP_TRY(run(CAT_CE, "cross_entropy", [=](hipStream_t q) {
     return cross_entropy(x, tgt, rows, Vv, Ss, stats, dlogits_out, g16c, lr, lm, q);
   }));
