@@ -23,7 +23,9 @@ Prints ONE JSON line.  Besides the contract fields it carries
                 replays (kernels only: their sum, kernels_sum_ms, is below
                 ms_per_step by the launch gaps);
   bandwidth_kernels: AdamW, SwiGLU backward, RMSNorm backward and the fused
-                CE in GB/s of their compulsory bytes;
+                CE in GB/s of their compulsory bytes, with frac of the
+                datasheet 8 TB/s and copy_frac of the device copy rate
+                (copy_gbs) measured in the same run;
   cpu_baseline: the CPU oracle (PyTorch fp32, oracle/lora_step.py) on a
                 bounded sample of the same step;
   c4, c3, c1:   (default run) the C4 step (B8 x S512, int8 weights), the
@@ -330,9 +332,9 @@ def bandwidth_kernels(kinds, dims, T):
     """The bandwidth-bound kernels of the step (north star: >= 70% of HBM):
     each kernel's compulsory bytes per launch in the dtypes it reads and
     writes, divided by its average replayed launch duration.
-      adamw          p, g, m, v read and p, m, v written, fp32, per parameter
-                     (7 x 4 B; the fp16 operand shadows it also writes are
-                     not counted);
+      adamw          p, g, m, v read and p, m, v written, fp32, per parameter,
+                     and the two fp16 operand copies of the new value the
+                     next step's GEMMs read (7 x 4 B + 2 x 2 B);
       swiglu_bwd     dY [T, I] fp32 (summed GEMM output), gate and up
                      [T, 2I] fp16 read, dgate | dup [T, 2I] fp16 written;
       norm_bwd       dY, x, residual-gradient in [T, H] fp32 read, residual
@@ -342,7 +344,7 @@ def bandwidth_kernels(kinds, dims, T):
     H, I, V = dims.hidden, dims.intermediate, dims.vocab
     nparam = dims.n_layers * 16 * (3 * H + 2 * dims.n_heads * dims.head_dim +
                                    2 * dims.n_kv_heads * dims.head_dim + H)
-    want = {"adamw": 7 * 4 * nparam,
+    want = {"adamw": (7 * 4 + 2 * 2) * nparam,
             "swiglu_bwd": T * I * 4 + T * 2 * I * 2 + T * 2 * I * 2,
             "norm_bwd": T * H * (4 + 4 + 4 + 4 + 2),
             "cross_entropy": T * V * (4 + 2)}
@@ -487,6 +489,12 @@ def main():
         out["c3"] = bench_c3(min(a.steps, 20), 3)
         out["c1"] = bench_c1(min(a.steps, 20), 3)
     out["achievable"] = achievable_peaks()
+    # each bandwidth kernel beside the device copy rate measured in this run
+    copy_gbs = out["achievable"]["hbm_copy_gbs"]
+    for obj in (out, out.get("c4", {})):
+        for k in obj.get("bandwidth_kernels", {}).values():
+            k["copy_gbs"] = copy_gbs
+            k["copy_frac"] = round(k["gbs"] / copy_gbs, 4)
     if not a.no_cpu:
         if a.config == "c2":
             out["cpu_baseline"] = cpu_baseline(r["batch"], r["seq_len"])

@@ -1006,19 +1006,27 @@ static bool big_tiles(int M, int K) { return M >= 1024 && M % BM == 0 && K % (BC
 static bool use_big_tiles(const GemmArgs& g) {
   return big_tiles(g.M, g.K) && g.N >= 16 && g.split <= (g.K / (BCH * KSTEP));
 }
-// Large-tile split-K: the smallest of 1, 2, 4 whose workgroup count fills
-// the 256 CUs in whole waves to >= 85% (partials cost traffic, so no more).
+// Large-tile split-K: the one of 1, 2, 4 with the least modelled time.  A
+// wave of tiles costs (0.54 + K / split / 1024) units, one unit being a
+// 256 x 256 tile's 1024-deep K slice; each split past the first adds an fp32
+// [M, N] partial that the GEMM writes and its consumer reads back, M N / 3.15e7
+// units.  (Fitted on MI355X at M = 4096: int8 tiles of K = 1024 and 2048 took
+// 49 and 81 us, and the SwiGLU backward read 100 MB of extra partial in
+// 25 us; so N = 6144, K = 2048 runs unsplit in 1.5 waves, 384 tiles, while the
+// 128-tile GEMMs split in two.)
 // A trailing LoRA segment of <= 64 columns runs as its own skinny launch
 // (gemm_nt), so it is left out of the tile count.
 static int big_split(int M, int N, int K, int max_split) {
   const int nmain = (N % 256 != 0 && N % 64 != 0) ? N - N % 64 : N;
   const int tiles = (nmain + 255) / 256 * (M / BM);
+  const double partial = (double)M * N / 3.15e7;
   int best = 1;
+  double best_t = 1e300;
   for (int split = 1; split <= 4 && split <= max_split && split <= K / (BCH * KSTEP) / 4;
        split *= 2) {
-    best = split;
-    const double waves = tiles * split / 256.0;
-    if (waves / ceil(waves) >= 0.85) break;
+    const double t = ceil(tiles * split / 256.0) * (0.54 + K / (1024.0 * split)) +
+                     (split - 1) * partial;
+    if (t < best_t) best_t = t, best = split;
   }
   return best;
 }
