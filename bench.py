@@ -30,7 +30,9 @@ Prints ONE JSON line.  Besides the contract fields it carries
                 bounded sample of the same step;
   c4, c3, c1:   (default run) the C4 step (B8 x S512, int8 weights), the
                 C3 attention block and the C1 head (lm_head + CE + dX)
-                measured in the same run.
+                measured in the same run; the C4 GEMM roofline also as
+                frac_of_hipblaslt, against the 8192^3 fp16 hipBLASLt GEMM
+                of the same run (achievable.mfma_f16_tflops_hipblaslt).
 --config c3 / c4 --only times one of those alone.
 """
 from __future__ import annotations
@@ -489,6 +491,12 @@ def main():
         out["c3"] = bench_c3(min(a.steps, 20), 3)
         out["c1"] = bench_c1(min(a.steps, 20), 3)
     out["achievable"] = achievable_peaks()
+    # the C4 GEMM family beside hipBLASLt's fp16 GEMM rate measured in this run
+    if "c4" in out:
+        blas = out["achievable"]["mfma_f16_tflops_hipblaslt"]
+        out["c4"]["roofline"]["hipblaslt_tflops"] = blas
+        out["c4"]["roofline"]["frac_of_hipblaslt"] = round(
+            out["c4"]["roofline"]["achieved"] / blas, 4)
     # each bandwidth kernel beside the device copy rate measured in this run
     copy_gbs = out["achievable"]["hbm_copy_gbs"]
     for obj in (out, out.get("c4", {})):
