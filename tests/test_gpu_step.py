@@ -107,6 +107,29 @@ def test_lora_save_load_roundtrip(small, tmp_path, dev):
     assert torch.equal(ctx.lora_get("param"), before)
 
 
+def test_lora_peft_round_trip(small, tmp_path, dev):
+    """Adapters saved by the library -> PEFT safetensors -> adapter files ->
+    llmt_lora_load: the same parameters bit for bit, and each PEFT tensor is
+    the context's slice for that layer and projection."""
+    import numpy as np
+    from llmt import peft
+    ctx = small["ctx"]
+    dims = peft.AdapterDims(SMALL.n_layers, SMALL.hidden, SMALL.n_heads, SMALL.n_kv_heads,
+                            SMALL.head_dim, SMALL.rank, SMALL.alpha)
+    before = ctx.lora_get("param").clone()
+    (tmp_path / "a").mkdir()
+    ctx.lora_save(tmp_path / "a", 4)
+    peft.to_peft(tmp_path / "a", 4, tmp_path / "hf", dims)
+    state = peft.load_peft(tmp_path / "hf")
+    q_a = state["base_model.model.model.layers.1.self_attn.q_proj.lora_A.weight"]
+    off = ctx.lora_offset(1, "wq", 0)
+    assert np.array_equal(q_a.ravel(), before[off:off + q_a.size].cpu().numpy())
+    peft.from_peft(tmp_path / "hf", tmp_path / "b", 9, dims)
+    ctx.lora_set("param", torch.zeros_like(before))
+    ctx.lora_load(tmp_path / "b", 9)
+    assert torch.equal(ctx.lora_get("param"), before)
+
+
 def test_small_model_matches_golden_fixture(small, dev):
     """Same step against the committed fixture (tests/golden/small_step.npz)."""
     import numpy as np
