@@ -171,6 +171,45 @@ def test_weights_dir_tied_head_file(dev, tmp_path):
         ctx.close()
 
 
+def test_hf_checkpoint_export_matches_transformers(dev, tmp_path):
+    """A random-init transformers Qwen3ForCausalLM (the SMALL shape, weights
+    rounded to fp16 values, norm weights randomised, tied head) saved as a
+    safetensors checkpoint, exported by llmt.export, loaded by
+    llmt_load_weights_dir: with zero adapters the step's loss equals
+    transformers' own fp32 loss on the same tokens (labels = inputs, i.e.
+    the mean over the S - 1 next-token rows of each sequence)."""
+    transformers = pytest.importorskip("transformers")
+    from llmt import export
+    print("case: HF checkpoint -> llmt.export -> load_weights_dir", flush=True)
+    torch.manual_seed(21)
+    cfg = transformers.Qwen3Config(
+        vocab_size=SMALL.vocab, hidden_size=SMALL.hidden, intermediate_size=SMALL.intermediate,
+        num_hidden_layers=SMALL.n_layers, num_attention_heads=SMALL.n_heads,
+        num_key_value_heads=SMALL.n_kv_heads, head_dim=SMALL.head_dim, rms_norm_eps=SMALL.eps,
+        rope_theta=SMALL.theta, tie_word_embeddings=True)
+    model = transformers.Qwen3ForCausalLM(cfg).float().eval()
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if name.endswith("norm.weight"):
+                p.copy_(1.0 + 0.2 * torch.randn_like(p))
+            p.copy_(p.half().float())
+    model.save_pretrained(tmp_path / "ckpt", safe_serialization=True)
+    export.export_checkpoint(tmp_path / "ckpt", tmp_path / "w")
+    g = torch.Generator().manual_seed(22)
+    win = torch.randint(0, SMALL.vocab, (2, 65), generator=g, dtype=torch.int32)
+    tok, tgt = win[:, :-1].contiguous(), win[:, 1:].contiguous()
+    with torch.no_grad():
+        want = float(model(input_ids=tok.long(), labels=tok.long()).loss)
+    ctx = llmt.Context(llmt.make_dims(SMALL), tok.shape[0], tok.shape[1])
+    try:
+        ctx.load_weights_dir(tmp_path / "w")
+        ctx.lora_set("param", torch.zeros(ctx.lora_numel, device=dev))
+        loss = ctx.forward_backward(tok.to(dev), tgt.to(dev))
+        assert abs(loss - want) < LOSS_TOL, (loss, want)
+    finally:
+        ctx.close()
+
+
 class _AdapterC(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in ("A", "B", "mA", "vA", "mB", "vB")] + \
                [("d_in", C.c_int), ("d_out", C.c_int)]
