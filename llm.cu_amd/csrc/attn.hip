@@ -274,11 +274,8 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(const TD* __restrict__ 
         v += dv[i][e] * (float)ov[i][e];
         amax = fmaxf(amax, fabsf(dv[i][e]));
       }
-#pragma unroll
-      for (int m = 8; m >= 1; m >>= 1) {
-        v += __shfl_xor(v, m, 64);
-        amax = fmaxf(amax, __shfl_xor(amax, m, 64));
-      }
+      v = sum16_dpp(v);
+      amax = max16(amax);
       if (t >= T) continue;  // whole 16-lane groups (after the group reductions)
       const int b = (int)((unsigned)t / (unsigned)S), s = (int)t - b * S;  // T < 2^31
       const float sc = pow2_scale_for(amax, kDoScaleExp);

@@ -129,25 +129,6 @@ __device__ __forceinline__ half8 frag_tr(const _Float16* t, int d0, int j, int l
   return x;
 }
 
-// Max / sum over the four lanes c, c + 16, c + 32, c + 48 (the key groups
-// g of one query column c) with gfx950's lane-swap VALU instructions
-// instead of LDS permutes: after v_permlane32_swap / v_permlane16_swap of a
-// value with itself, lane i holds x[i] and x[i ^ 32] (x[i ^ 16]) in its two
-// results, so one max or add finishes each step; every lane gets the same
-// bits (min/max and a + b are symmetric).
-__device__ __forceinline__ float xg_max(float x) {
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-  r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float xg_sum(float x) {
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
 // Per-head RMSNorm + half-split RoPE of one 128-wide row (the block API's
 // QK-norm, src/kernels/rmsnorm.cu:36-41 and src/kernels/rope.cu:7-27) as an
 // MFMA operand: lane (c, g) of the four lanes c + 16 g holding the row gets

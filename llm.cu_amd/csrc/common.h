@@ -40,28 +40,6 @@ __device__ __forceinline__ floatx4 mfma16(half8 a, half8 b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-
-// Online-softmax pairs (m, s = sum exp(x - m)): (m, s) <- the pair of the
-// union with (m2, s2).  Empty pairs are (-inf, 0).
-__device__ __forceinline__ void softmax_merge(float& m, float& s, float m2, float s2) {
-  constexpr float kLog2e = 1.4426950408889634f;
-  const float mn = fmaxf(m, m2);
-  if (mn == -INFINITY) return;
-  s = s * __builtin_amdgcn_exp2f((m - mn) * kLog2e) + s2 * __builtin_amdgcn_exp2f((m2 - mn) * kLog2e);
-  m = mn;
-}
-
 // Value of another lane of the same 16-lane row through a DPP modifier (a
 // VALU operand, no LDS): quad_perm [1,0,3,2] (0xB1) and [2,3,0,1] (0x4E),
 // row_half_mirror (0x141, lane i <- 7 - i within 8) and row_mirror (0x140,
@@ -83,6 +61,50 @@ __device__ __forceinline__ float sum16_dpp(float v) {
   v += dpp16<0x4E>(v);
   v += dpp16<0x141>(v);
   return v + dpp16<0x140>(v);
+}
+
+// Max / sum over the four lanes c, c + 16, c + 32, c + 48 (the 16-lane rows
+// of a wave) with gfx950's lane-swap VALU instructions instead of LDS
+// permutes: after v_permlane32_swap / v_permlane16_swap of a value with
+// itself, lane i holds x[i] and x[i ^ 32] (x[i ^ 16]) in its two results, so
+// one max or add finishes each step; every lane gets the same bits (min/max
+// and a + b are symmetric).
+__device__ __forceinline__ float xg_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xg_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// Over the 32 lanes of a half wave (lanes 32 q .. 32 q + 31).
+__device__ __forceinline__ float sum32(float x) {
+  x = sum16_dpp(x);
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max32(float x) {
+  x = max16(x);
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// Over the whole wave; every lane gets the same bits.  All 64 lanes must be
+// active (the reductions read their neighbours' registers).
+__device__ __forceinline__ float wave_sum(float v) { return xg_sum(sum16_dpp(v)); }
+__device__ __forceinline__ float wave_max(float v) { return xg_max(max16(v)); }
+
+// Online-softmax pairs (m, s = sum exp(x - m)): (m, s) <- the pair of the
+// union with (m2, s2).  Empty pairs are (-inf, 0).
+__device__ __forceinline__ void softmax_merge(float& m, float& s, float m2, float s2) {
+  constexpr float kLog2e = 1.4426950408889634f;
+  const float mn = fmaxf(m, m2);
+  if (mn == -INFINITY) return;
+  s = s * __builtin_amdgcn_exp2f((m - mn) * kLog2e) + s2 * __builtin_amdgcn_exp2f((m2 - mn) * kLog2e);
+  m = mn;
 }
 
 // The pair of NF values x[f] of one row held by each of the 16 lanes of a

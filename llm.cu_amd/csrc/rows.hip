@@ -332,7 +332,7 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(const QkvPostArgs a, int 
       float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const float h = __shfl(hv[i], r, 64);
+        const float h = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hv[i]), r));
         acc0 += h * b0[r];
         acc1 += h * b1[r];
       }
@@ -645,12 +645,6 @@ __global__ __launch_bounds__(RT) void resid_norm_kernel(const RowIn in,
 // (src/kernels/rmsnorm.cu:6-41; src/kernels/rope.cu:7-46).
 constexpr int HN_ROWS = RT / 16;  // rows a workgroup
 
-// Sum over the 16 lanes of a row group.
-__device__ __forceinline__ float sum16(float v) {
-#pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
 __device__ __forceinline__ float4 ldh4(const _Float16* p) {
   const half4 h = *reinterpret_cast<const half4*>(p);
   return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
@@ -694,7 +688,7 @@ __global__ __launch_bounds__(RT) void head_norm_rope_kernel(const HeadNormArgs a
     const float ss = x0[i].x * x0[i].x + x0[i].y * x0[i].y + x0[i].z * x0[i].z +
                      x0[i].w * x0[i].w + x1[i].x * x1[i].x + x1[i].y * x1[i].y +
                      x1[i].z * x1[i].z + x1[i].w * x1[i].w;
-    const float r = rsqrtf(sum16(ss) / HD + a.eps);
+    const float r = rsqrtf(sum16_dpp(ss) / HD + a.eps);
     if (row >= nrows) continue;  // whole 16-lane groups (after the group sum)
     const float a0[4] = {x0[i].x * r * w0.x, x0[i].y * r * w0.y, x0[i].z * r * w0.z,
                          x0[i].w * r * w0.w};
@@ -986,7 +980,7 @@ __global__ __launch_bounds__(256) void o_dx_post_kernel(const RowIn in,
       float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const float hr = __shfl(hv[i], r, 64);
+        const float hr = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hv[i]), r));
         acc0 += hr * b0[r];
         acc1 += hr * b1[r];
       }
@@ -1053,11 +1047,8 @@ __global__ __launch_bounds__(RT) void o_dx_post_row_kernel(const RowIn in,
                             d.w * (float)ov[p][3]
                       : 0.f;
     float amax = live ? amax4(d) : 0.f;
-#pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) {
-      part += __shfl_xor(part, o, 64);
-      amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-    }
+    part = sum32(part);
+    amax = max32(amax);
     if (!live) continue;
     st_h4(dO16 + (long long)t * Q + c, mul4(d, pow2_scale_for(amax, kDoScaleExp)));
     if ((threadIdx.x & 31) == 0) {
