@@ -97,6 +97,13 @@ __device__ __forceinline__ float max32(float x) {
 __device__ __forceinline__ float wave_sum(float v) { return xg_sum(sum16_dpp(v)); }
 __device__ __forceinline__ float wave_max(float v) { return xg_max(max16(v)); }
 
+// Logistic sigmoid through the hardware reciprocal (v_rcp_f32, 1 ulp)
+// rather than an IEEE division (about ten instructions); every use rounds the
+// result into an fp16 operand.  x -> -inf gives rcp(inf) = 0, x -> +inf 1.
+__device__ __forceinline__ float sigmoid_rcp(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+}
+
 // Online-softmax pairs (m, s = sum exp(x - m)): (m, s) <- the pair of the
 // union with (m2, s2).  Empty pairs are (-inf, 0).
 __device__ __forceinline__ void softmax_merge(float& m, float& s, float m2, float s2) {

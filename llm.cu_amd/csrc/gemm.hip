@@ -450,7 +450,7 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
           const float gt = acc[i][2 * jj][v] * sgu[2 * jj], up = acc[i][2 * jj + 1][v] * sgu[2 * jj + 1];
           grow[16 * jj] = (_Float16)gt;
           grow[g.glu + 16 * jj] = (_Float16)up;
-          arow[16 * jj] = (_Float16)(gt / (1.0f + __expf(-gt)) * up);
+          arow[16 * jj] = (_Float16)(gt * sigmoid_rcp(gt) * up);
         }
       }
     return;
@@ -673,7 +673,7 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(const GemmArgs g) {
           const float gt = acc[i][2 * jj][v] * sg, up = acc[i][2 * jj + 1][v] * su;
           g.gu16[row * (2LL * g.glu) + col] = (_Float16)gt;
           g.gu16[row * (2LL * g.glu) + g.glu + col] = (_Float16)up;
-          g.glu16[row * g.ldglu + col] = (_Float16)(gt / (1.0f + __expf(-gt)) * up);
+          g.glu16[row * g.ldglu + col] = (_Float16)(gt * sigmoid_rcp(gt) * up);
         }
     }
     return;

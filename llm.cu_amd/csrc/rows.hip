@@ -205,7 +205,7 @@ __device__ __forceinline__ void lora_apply_rows(const RowIn& in, const float (*h
   for (int i = 0; i < NR; ++i) v[i] = add4(v[i], mul4(acc[i], in.lscale));
 }
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+__device__ __forceinline__ float silu(float g) { return g * sigmoid_rcp(g); }
 
 // Two block sums at once (one barrier pair).
 __device__ __forceinline__ float2 block_sum2(float a, float b, float* red) {
@@ -883,7 +883,7 @@ __global__ __launch_bounds__(RT) void swiglu_bwd_kernel(const RowIn in,
     float o1[4], o2[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float sg = 1.0f / (1.0f + __expf(-g[e]));
+      const float sg = sigmoid_rcp(g[e]);
       o1[e] = da[e] * u[e] * (sg * (1.0f + g[e] * (1.0f - sg)));
       o2[e] = da[e] * (g[e] * sg);
     }
