@@ -575,11 +575,16 @@ void launch_bwd(const AttnArgs& a, int B, int nkvb, int nqb, hipStream_t st) {
 // one launch when the wave counts agree and the grid is small (under 2048
 // workgroups: a second launch would mostly wait on the first one's tail),
 // else one launch each.
+bool bwd_one_launch(const AttnArgs& a, int B, int nwk, int nwq, int rw) {
+  const int nkvb = (a.S + nwk * 16 - 1) / (nwk * 16);
+  const int nqb = (a.S + nwq * rw * 16 - 1) / (nwq * rw * 16);
+  return nwk == nwq && ((long long)nkvb * a.nkv + (long long)nqb * a.nq) * B < 2048;
+}
+
 void launch_attn_bwd(const AttnArgs& a, int B, int nwk, int nwq, int rw, hipStream_t st) {
   const int nkvb = (a.S + nwk * 16 - 1) / (nwk * 16);
   const int nqb = (a.S + nwq * rw * 16 - 1) / (nwq * rw * 16);
-  const bool small = ((long long)nkvb * a.nkv + (long long)nqb * a.nq) * B < 2048;
-  if (nwk == nwq && small) {
+  if (bwd_one_launch(a, B, nwk, nwq, rw)) {
     switch (nwq * 10 + rw) {
       case 42: launch_bwd<4, 2, 0>(a, B, nkvb, nqb, st); break;
       case 41: launch_bwd<4, 1, 0>(a, B, nkvb, nqb, st); break;
@@ -617,12 +622,14 @@ hipError_t attn_bwd(const AttnArgs& a, int B, hipStream_t st) {
     set_error("attn_bwd: the fused QK-norm backward needs the raw q / k and the RoPE tables");
     return hipErrorInvalidValue;
   }
-  // dQ holds twice the accumulators of the forward: one 16-row tile a wave
-  // keeps two waves per SIMD, measured faster at every S; LLMT_ATTN_CFG
-  // still selects any shape for tuning.
+  // dQ holds twice the accumulators of the forward: in a launch of its own
+  // one 16-row tile a wave (two waves per SIMD) was faster at every S; where
+  // dQ and dK/dV blocks share one launch (B8 x S512) the forward's two tiles
+  // a wave are (attention backward 54.4 against 58.4 us), the dQ blocks then
+  // being as long as the dK/dV ones.  LLMT_ATTN_CFG still selects any shape.
   AttnShape s = attn_shape(B, a.S, a.nq);
   if (!getenv("LLMT_ATTN_CFG")) {
-    s.rw = 1;
+    if (!bwd_one_launch(a, B, dkdv_waves(B, a.S, a.nkv), s.nw, s.rw)) s.rw = 1;
     // tiny grids (the B1 x S128 step): dK/dV blocks of 16 keys whose two
     // waves split the group's query tiles, beside 32-query dQ blocks
     if (!getenv("LLMT_ATTN_DKDV_WAVES") && (long long)B * a.nq * ((a.S + 63) / 64) < 64) {
