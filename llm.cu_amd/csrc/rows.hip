@@ -240,19 +240,37 @@ __global__ __launch_bounds__(RT) void embed_norm_kernel(const int* __restrict__ 
   const int t = blockIdx.x;
   const int id = min(max(tok[t], 0), V - 1);
   // E is fragment-packed (K = H): the row's 8-element pieces are contiguous.
+  // A thread keeps its pieces (EP of them, H <= 8 EP RT) in registers for
+  // both passes, so the normed operand is written without reading x back.
+  constexpr int EP = 2;
+  half8 v[EP];
   float ss = 0.f;
-  for (int c = threadIdx.x * 8; c < H; c += RT * 8) {
-    const half8 v = *reinterpret_cast<const half8*>(E + packed_index(id, c, H));
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float f = (float)v[i];
-      x[(long long)t * H + c + i] = f;
-      ss += f * f;
-    }
+  for (int p = 0; p < EP; ++p) {
+    const int c = (threadIdx.x + p * RT) * 8;
+    v[p] = c < H ? *reinterpret_cast<const half8*>(E + packed_index(id, c, H)) : half8{};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += (float)v[p][i] * (float)v[p][i];
   }
   const float r = rsqrtf(block_sum2(ss, 0.f, red).x / H + eps);
-  for (int c = threadIdx.x; c < H; c += RT)
-    xn[(long long)t * H + c] = (_Float16)(x[(long long)t * H + c] * r * w[c]);
+#pragma unroll
+  for (int p = 0; p < EP; ++p) {
+    const int c = (threadIdx.x + p * RT) * 8;
+    if (c >= H) continue;
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = (float)v[p][i];
+    float4* xo = reinterpret_cast<float4*>(x + (long long)t * H + c);
+    xo[0] = make_float4(f[0], f[1], f[2], f[3]);
+    xo[1] = make_float4(f[4], f[5], f[6], f[7]);
+    const float4 w0 = *reinterpret_cast<const float4*>(w + c);
+    const float4 w1 = *reinterpret_cast<const float4*>(w + c + 4);
+    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    half8 o;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (_Float16)(f[i] * r * wv[i]);
+    *reinterpret_cast<half8*>(xn + (long long)t * H + c) = o;
+  }
 }
 
 // After the fused Q/K/V(+LoRA-A) GEMM: y = sum of the split partials plus
@@ -1263,6 +1281,11 @@ hipError_t f32_to_f16_scaled(const float* src, _Float16* dst, size_t n, float sc
 
 hipError_t embed_norm(const int* tok, const _Float16* E, int V, int H, const float* w, float eps,
                       int T, float* x, _Float16* xn, hipStream_t st) {
+  if (H % 8 || H > 2 * 8 * RT || ((uintptr_t)x | (uintptr_t)xn | (uintptr_t)w) % 16) {
+    set_error("embed_norm: H=%d (a multiple of 8, at most %d) and 16-byte aligned rows required",
+              H, 2 * 8 * RT);
+    return hipErrorInvalidValue;
+  }
   hipLaunchKernelGGL(embed_norm_kernel, dim3(T), dim3(RT), 0, st, tok, E, V, H, w, eps, x, xn);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
