@@ -102,10 +102,14 @@ typedef struct {
 
 /* src/train.cu:10-17 (= src/kernels/lora_forward.cu:18-32).  The 21 pad slots
  * mirror src/main.cu:40-55: _pad[0..6] = fp16 (uint16 bits) copies of
- * wq, wk, wv, wo, w_gate, w_up, w_down; _pad[7..20] = (int8 q, scale) pairs
- * in the same order.  The library reads fp16 pads when set, else converts
- * the fp32 fields once and caches the result.  The fp32 weight fields may be
- * NULL when the fp16 (or int8) pads are supplied.  An int8 scale is fp16. */
+ * wq, wk, wv, wo, w_gate, w_up, w_down; _pad[7..20] = (int8_t* q, float*
+ * scale) pairs in the same order (q [out, in], scale fp32 [out], the
+ * src/kernels/quantize.cu recipe).  Weight source, decided by layer 0: its
+ * fp16 pads when set (fp16 weights; layers whose pads are NULL convert their
+ * fp32 fields once); else its int8 pads when set (int8 weights, the scales
+ * rounded to fp16 as the int8 GEMMs take them; layers whose int8 pads are
+ * NULL quantise their fp32 fields); else the fp32 fields converted to fp16.
+ * The fp32 weight fields may be NULL when the pads are supplied. */
 typedef struct {
     float* attn_norm;
     float* ffn_norm;
@@ -115,10 +119,12 @@ typedef struct {
     void* _pad[21];
 } LW;
 
-/* src/train.cu:18-24.  _pad[0] = fp16 lm_head, _pad[1..2] = int8 lm_head and
- * its scale (src/main.cu:63-64).  embed_table may be NULL when the lm_head is
- * tied and given in fp16 (the reference scripts copy embed -> lm_head,
- * scripts/run.sh:19); the gather then reads the fp16 lm_head rows. */
+/* src/train.cu:18-24.  _pad[0] = fp16 lm_head, _pad[1..2] = int8_t* lm_head
+ * and its float* row scales (src/main.cu:63-64).  The head is read from the
+ * fp16 pad, else the fp32 lm_head, else the int8 pair (as fp16 q * scale).
+ * embed_table may be NULL when the lm_head is tied (the reference scripts
+ * copy embed -> lm_head, scripts/run.sh:19); the gather then reads the
+ * lm_head rows. */
 typedef struct {
     float* embed_table;
     LW layers[LLMT_NUM_LAYERS];
@@ -147,8 +153,8 @@ void gpu_zero(float* buf, int n);
 /* src/kernels/lora_forward.cu:169-186.  The workspaces and acts are accepted
  * for ABI compatibility and not touched (the stashes live in the library's
  * context); logits receives the fp32 logits [seq, V].  Frozen weights are
- * uploaded (fp16 pads when set, else the fp32 fields converted) on the first
- * call for a given MW, adapters on every call.  seq_len % 16 == 0. */
+ * uploaded (by the MW pad map above) on the first call for a given MW,
+ * adapters on every call.  Any seq_len >= 2. */
 void transformer_forward_lora(const int* token_ids, const MW* model, const LoraWeights* lora,
                               float* hidden, float* residual, float* norm_out,
                               float* q, float* k, float* v, float* k_exp, float* v_exp,
@@ -218,7 +224,8 @@ int llmt_set_layer_f16(llmt_ctx* ctx, int layer, const void* wq, const void* wk,
 int llmt_set_layer_i8(llmt_ctx* ctx, int layer, const int8_t* const q[7], const void* const scale[7],
                       const float* attn_norm, const float* ffn_norm, const float* q_norm,
                       const float* k_norm);
-/* Tied embedding / lm_head [V, H] fp16 and the final norm [H] fp32. */
+/* Tied embedding / lm_head [V, H] fp16 and the final norm [H] fp32.  Ties
+ * the head to this embedding (again, after an llmt_set_lm_head_f16). */
 int llmt_set_embed_f16(llmt_ctx* ctx, const void* embed_lm_head, const float* final_norm);
 /* An untied lm_head [V, H] fp16 (the reference loads lm_head.weight.bin on its
  * own, src/train.cu:87-88): the logits and the head's dX use it, the token
@@ -252,10 +259,12 @@ int llmt_lora_init(llmt_ctx* ctx, uint64_t seed, float a_std, float b_std);
 
 /* One training step (src/train.cu:251-288): forward, fused CE, backward,
  * AdamW with bias-correction step `step` (1-based).  tokens/targets: int32
- * device [batch, seq_len].  The loss is the mean over batch*(seq_len-1) rows
- * (src/kernels/loss.cu:86-90).  *loss_host is written after the one host
- * sync.  llmt_forward_backward runs everything but AdamW (grads are left in
- * the GRAD arena, overwritten, not accumulated). */
+ * device [batch, seq_len], any seq_len >= 2 and batch <= max_batch (the
+ * kernels run on batch*seq_len rows rounded up to a multiple of 16; the pad
+ * rows are zero and add nothing).  The loss is the mean over
+ * batch*(seq_len-1) rows (src/kernels/loss.cu:86-90).  *loss_host is written
+ * after the one host sync.  llmt_forward_backward runs everything but AdamW
+ * (grads are left in the GRAD arena, overwritten, not accumulated). */
 int llmt_step(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
               const llmt_hparams* hp, int step, float* loss_host);
 int llmt_forward_backward(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
@@ -263,7 +272,8 @@ int llmt_forward_backward(llmt_ctx* ctx, const int* tokens, const int* targets, 
 /* Capture llmt_step's device work into a HIP graph and replay it
  * (enable = 1); the graph is rebuilt when batch changes. */
 int llmt_set_graph(llmt_ctx* ctx, int enable);
-/* fp32 logits [batch*seq_len, V] of the last forward (NULL if not kept). */
+/* fp32 logits of the last forward: rows 0 .. batch*seq_len-1 in token order
+ * (then the zero pad rows up to a multiple of 16), V wide. */
 const float* llmt_logits(const llmt_ctx* ctx);
 /* fp32 residual stream [batch*seq_len, H] at the input of `layer` (0..L-1)
  * from the last forward, the reference's LoraActs.layer_in[layer]
@@ -273,8 +283,8 @@ const float* llmt_logits(const llmt_ctx* ctx);
 const float* llmt_layer_in(const llmt_ctx* ctx, int layer);
 
 /* Single-layer forward/backward through layer `layer` (config C0): x, y, dy,
- * dx are fp32 [batch*seq_len, H]. The backward writes the layer's adapter
- * gradients into the GRAD arena and dx. */
+ * dx are fp32 [batch*seq_len, H], batch*seq_len a multiple of 16. The
+ * backward writes the layer's adapter gradients into the GRAD arena and dx. */
 int llmt_layer_forward(llmt_ctx* ctx, int layer, const float* x, float* y, int batch);
 int llmt_layer_backward(llmt_ctx* ctx, int layer, const float* dy, float* dx, int batch);
 /* AdamW over the whole arena (one multi-tensor launch). */
@@ -332,9 +342,10 @@ int llmt_cross_entropy_noalloc(const float* logits, const int* targets, int rows
  * NULL.  T % 16 == 0, T % seq_len == 0. */
 int llmt_lm_head_ce(const void* hidden, const void* W, const int* targets, int T, int seq_len,
                     int H, int V, float* loss_mean, float* dlogits, float* dhidden, void* stream);
-/* Config C1 on a context's tied embedding (already packed by
- * llmt_set_embed_f16): hidden fp16 [batch*seq_len, H], dlogits (may be
- * NULL) and dhidden fp32 device buffers; *loss_host after one host sync. */
+/* Config C1 on a context's lm_head (already packed by llmt_set_embed_f16 /
+ * llmt_set_lm_head_f16): hidden fp16 [batch*seq_len, H] (batch*seq_len a
+ * multiple of 16), dlogits (may be NULL) and dhidden fp32 device buffers;
+ * *loss_host after one host sync. */
 int llmt_head_ce(llmt_ctx* ctx, const void* hidden16, const int* targets, int batch,
                  float* loss_host, float* dlogits, float* dhidden);
 /* Causal GQA flash attention (config C3).  q [B,S,nq,128], k/v [B,S,nkv,128]

@@ -57,18 +57,23 @@ struct Temps {
 };
 
 // Device workspace of llmt_attention_block_bwd, one per (device, stream),
-// kept for the life of the process and grown on demand: a new size waits for
-// the stream to finish with the old buffer, frees it and allocates the new
-// one (hipMalloc), so a steady caller allocates nothing per call and leaves
-// the GPU no idle gap between calls.  Calls on one stream are ordered by the
-// stream; calls on different streams use different workspaces.  The RoPE
+// kept across calls and grown on demand: a new size waits for the stream to
+// finish with the old buffer, frees it and allocates the new one (hipMalloc),
+// so a steady caller allocates nothing per call and leaves the GPU no idle
+// gap between calls.  Calls on one stream are ordered by the stream; calls
+// on different streams use different workspaces.  At most kMaxBlockWs
+// workspaces live per device: a stream beyond that takes over the least
+// recently used one after a device synchronisation (its stream may be gone,
+// so the whole device is drained before the buffer is reused).  The RoPE
 // tables of the last (S, theta) stay at its start and are rebuilt only when
 // either changes.  Host threads must not issue calls on one stream at once.
+constexpr int kMaxBlockWs = 4;
 struct BlockWs {
   int dev = -1;
   hipStream_t st = nullptr;
   char* base = nullptr;
   size_t cap = 0, used = 0;
+  unsigned long long last_use = 0;
   int rope_S = 0;
   double rope_theta = 0.0;
   // sub-buffer of n elements, 256-byte aligned (nullptr past the capacity)
@@ -82,6 +87,7 @@ struct BlockWs {
 };
 static std::mutex g_ws_mu;
 static std::vector<BlockWs*> g_ws;
+static unsigned long long g_ws_clock = 0;
 
 static hipError_t block_ws(hipStream_t st, size_t bytes, BlockWs** out) {
   int dev = 0;
@@ -90,14 +96,26 @@ static hipError_t block_ws(hipStream_t st, size_t bytes, BlockWs** out) {
   BlockWs* w = nullptr;
   {
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    for (BlockWs* x : g_ws)
-      if (x->dev == dev && x->st == st) w = x;
+    int on_dev = 0;
+    BlockWs* lru = nullptr;
+    for (BlockWs* x : g_ws) {
+      if (x->dev != dev) continue;
+      ++on_dev;
+      if (x->st == st) w = x;
+      if (!lru || x->last_use < lru->last_use) lru = x;
+    }
+    if (!w && on_dev >= kMaxBlockWs) {  // reuse the least recently used one
+      if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+      w = lru;
+      w->st = st;
+    }
     if (!w) {
       w = new BlockWs;
       w->dev = dev;
       w->st = st;
       g_ws.push_back(w);
     }
+    w->last_use = ++g_ws_clock;
   }
   if (bytes > w->cap) {
     if (w->base) {
@@ -128,6 +146,7 @@ int llmt_layer_forward(llmt_ctx* ctx, int layer, const float* x, float* y, int b
   const int T = batch * c->S;
   Stash& s = c->stash[layer];
   Layer& w = c->layers[layer];
+  c->pad_batch = 0;  // rows a later step may pad are written here
   TRY_HIP(copy_norm(x, w.attn_norm, c->dims.eps, c->H, T, s.x_in, s.xn, c->st));
   TRY_HIP(c->layer_fwd(layer, batch, w.attn_norm, y, c->xf16));
   TRY_HIP(hipStreamSynchronize(c->st));
@@ -140,6 +159,7 @@ int llmt_layer_backward(llmt_ctx* ctx, int layer, const float* dy, float* dx, in
   TRY_ARG(c && dy && dx && layer >= 0 && layer < c->L, "llmt_layer_backward: bad arguments");
   TRY_ARG(batch >= 1 && batch <= c->maxB && (batch * c->S) % 16 == 0, "batch");
   const int T = batch * c->S;
+  c->pad_batch = 0;
   TRY_HIP(grad_rows(dy, c->H, T, c->d_res, c->g16, c->rinv, c->st));
   TRY_HIP(c->layer_bwd(layer, batch));
   TRY_HIP(c->lora_grads(layer, 1, batch, 0));
@@ -213,6 +233,7 @@ int llmt_head_ce(llmt_ctx* ctx, const void* hidden16, const int* targets, int ba
   TRY_ARG(c->embed_ready, "embedding not set");
   TRY_ARG(batch >= 1 && batch <= c->maxB && (batch * c->S) % 16 == 0, "batch");
   const int T = batch * c->S;
+  c->pad_batch = 0;
   int rc = head_ce_packed(c->st, (const _Float16*)hidden16, c->Eh, c->EhT, targets, T, c->S, c->H,
                           c->V, c->logits, c->grad16, c->ce_stats, c->lse_rows, c->loss_rows,
                           c->loss_dev, dlogits, dhidden, c->part, c->part_elems);

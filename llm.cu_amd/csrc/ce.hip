@@ -303,8 +303,15 @@ hipError_t scratch_address(float2** out) {
   }
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   if (!g_scratch[dev]) {
+    // The first call may come under a caller's stream capture: the lookup
+    // (no stream work) runs in relaxed capture mode for this thread, so a
+    // global-mode capture does not reject it, and the mode is restored.
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    LLMT_HIP_TRY(hipThreadExchangeStreamCaptureMode(&mode));
     void* p = nullptr;
-    LLMT_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    LLMT_HIP_TRY(hipThreadExchangeStreamCaptureMode(&mode));
+    LLMT_HIP_TRY(e);
     g_scratch[dev] = static_cast<float2*>(p);
   }
   *out = g_scratch[dev];

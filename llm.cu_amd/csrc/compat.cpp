@@ -54,9 +54,13 @@ void check_hip(hipError_t e, const char* what) {
 struct Compat {
   llmt_ctx* ctx = nullptr;
   int seq_len = 0;
+  int wfmt = LLMT_WEIGHTS_F16;
   const MW* model = nullptr;
   const void* model_key = nullptr;  // first frozen weight pointer seen for `model`
   _Float16* conv = nullptr;         // fp32 -> fp16 staging for fp32-only weights
+  int8_t* q8 = nullptr;             // int8 staging (fp32 weights quantised for an int8 context)
+  float* s32 = nullptr;             // its fp32 scales
+  _Float16* s16 = nullptr;          // fp16 scales of one layer's seven matrices
   AdamHp* hp_dev = nullptr;
   AdamHp* hp_host = nullptr;
 };
@@ -180,9 +184,26 @@ __global__ __launch_bounds__(256) void lora_add_kernel(const float* __restrict__
   }
 }
 
-// Create (or re-create for a new seq_len) the compat context.
-void ensure_ctx(int seq_len) {
-  if (g.ctx && g.seq_len == seq_len) return;
+// int8 row q [rows, cols] times its fp32 row scale, as fp16 (an int8-only
+// lm_head, src/main.cu:64, as the fp16 operand of the logits GEMM).
+__global__ void dequant_rows_kernel(const int8_t* __restrict__ q, const float* __restrict__ s,
+                                    long long cols, long long n, _Float16* __restrict__ out) {
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (long long)gridDim.x * blockDim.x)
+    out[i] = (_Float16)((float)q[i] * s[i / cols]);
+}
+
+// Frozen-weight format of `m`: layer 0's fp16 pads decide fp16; without
+// them, int8 pads (src/main.cu:49-55) make an int8 context; else fp16 from
+// the fp32 fields.
+int weight_format(const MW* m) {
+  const LW& w = m->layers[0];
+  return !w._pad[0] && w._pad[7] && w._pad[8] ? LLMT_WEIGHTS_I8 : LLMT_WEIGHTS_F16;
+}
+
+// Create (or re-create for a new seq_len or weight format) the compat context.
+void ensure_ctx(int seq_len, int wfmt) {
+  if (g.ctx && g.seq_len == seq_len && g.wfmt == wfmt) return;
   if (g.ctx) {
     llmt_ctx_destroy(g.ctx);
     g.ctx = nullptr;
@@ -190,17 +211,24 @@ void ensure_ctx(int seq_len) {
   }
   llmt_dims d;
   llmt_dims_qwen3_1_7b(&d);
-  check_rc(llmt_ctx_create(&d, 1, seq_len, LLMT_WEIGHTS_F16, nullptr, &g.ctx), "context");
+  check_rc(llmt_ctx_create(&d, 1, seq_len, wfmt, nullptr, &g.ctx), "context");
   g.seq_len = seq_len;
+  g.wfmt = wfmt;
 }
 
-// Upload the frozen weights of `m` (once per model): fp16 pads when given
-// (src/main.cu:40-55 slot map), else the fp32 fields converted on the device.
+// Upload the frozen weights of `m` (once per model), by the src/main.cu:40-55
+// slot map: in an fp16 context the fp16 pads _pad[0..6] when given, else the
+// fp32 fields converted on the device; in an int8 context the (int8, fp32
+// scale) pairs _pad[7..20], the scales rounded to fp16 (the int8 GEMMs'
+// scale type), else the fp32 fields quantised on the device
+// (src/kernels/quantize.cu:8-44).
 void ensure_weights(const MW* m) {
-  const void* key = m->layers[0]._pad[0] ? m->layers[0]._pad[0] : (const void*)m->layers[0].wq;
+  const LW& w0 = m->layers[0];
+  const void* key = w0._pad[0] ? w0._pad[0] : w0._pad[7] ? w0._pad[7] : (const void*)w0.wq;
   if (g.model == m && g.model_key == key) return;
   Ctx* c = native();
   const size_t big = (size_t)c->V * c->H;
+  const size_t H = c->H, Q = c->Q, KV = c->KV, I = c->I;
   if (!g.conv) check_hip(hipMalloc((void**)&g.conv, big * 2), "staging");
   auto f16 = [&](const float* f32, void* pad, size_t n, size_t off) -> const void* {
     if (pad) return pad;
@@ -211,39 +239,90 @@ void ensure_weights(const MW* m) {
     check_hip(f32_to_f16(f32, g.conv + off, n, c->st), "fp32->fp16");
     return g.conv + off;
   };
-  const size_t H = c->H, Q = c->Q, KV = c->KV, I = c->I;
-  for (int l = 0; l < c->L; ++l) {
-    const LW& w = m->layers[l];
-    size_t o = 0;
-    const void* wq = f16(w.wq, w._pad[0], Q * H, o); o += Q * H;
-    const void* wk = f16(w.wk, w._pad[1], KV * H, o); o += KV * H;
-    const void* wv = f16(w.wv, w._pad[2], KV * H, o); o += KV * H;
-    const void* wo = f16(w.wo, w._pad[3], H * Q, o); o += H * Q;
-    const void* wg = f16(w.w_gate, w._pad[4], I * H, o); o += I * H;
-    const void* wu = f16(w.w_up, w._pad[5], I * H, o); o += I * H;
-    const void* wd = f16(w.w_down, w._pad[6], H * I, o);
-    check_rc(llmt_set_layer_f16(g.ctx, l, wq, wk, wv, wo, wg, wu, wd, w.attn_norm, w.ffn_norm,
-                                w.q_norm, w.k_norm),
-             "set layer");
+  const size_t rows[7] = {Q, KV, KV, H, I, I, H}, cols[7] = {H, H, H, Q, H, H, I};
+  if (g.wfmt == LLMT_WEIGHTS_I8) {
+    const size_t layer_elems = H * (2 * Q + 2 * KV + 3 * I), nsc = 2 * I + Q + 2 * KV + 2 * H;
+    if (!g.q8) {
+      check_hip(hipMalloc((void**)&g.q8, layer_elems), "staging");
+      check_hip(hipMalloc((void**)&g.s32, nsc * 4), "staging");
+      check_hip(hipMalloc((void**)&g.s16, nsc * 2), "staging");
+    }
+    for (int l = 0; l < c->L; ++l) {
+      const LW& w = m->layers[l];
+      const float* f32[7] = {w.wq, w.wk, w.wv, w.wo, w.w_gate, w.w_up, w.w_down};
+      const int8_t* qp[7];
+      const void* sp[7];
+      size_t o = 0, so = 0;
+      for (int k = 0; k < 7; ++k) {
+        const int8_t* q = (const int8_t*)w._pad[7 + 2 * k];
+        const float* sc = (const float*)w._pad[8 + 2 * k];
+        if (!q || !sc) {  // quantise the fp32 field
+          if (!f32[k]) {
+            fprintf(stderr, "llmt: layer %d weight %d is NULL in its fp32 and int8 slots\n", l, k);
+            exit(EXIT_FAILURE);
+          }
+          check_hip(quantize_rows_i8(f32[k], (int)rows[k], (int)cols[k], g.q8 + o, g.s32 + so,
+                                     c->st),
+                    "quantize");
+          q = g.q8 + o;
+          sc = g.s32 + so;
+        }
+        check_hip(f32_scale_to_f16(sc, g.s16 + so, (int)rows[k], c->st), "scale");
+        qp[k] = q;
+        sp[k] = g.s16 + so;
+        o += rows[k] * cols[k];
+        so += rows[k];
+      }
+      check_rc(llmt_set_layer_i8(g.ctx, l, qp, sp, w.attn_norm, w.ffn_norm, w.q_norm, w.k_norm),
+               "set layer");
+    }
+  } else {
+    for (int l = 0; l < c->L; ++l) {
+      const LW& w = m->layers[l];
+      const float* f32[7] = {w.wq, w.wk, w.wv, w.wo, w.w_gate, w.w_up, w.w_down};
+      const void* wp[7];
+      size_t o = 0;
+      for (int k = 0; k < 7; ++k) {
+        wp[k] = f16(f32[k], w._pad[k], rows[k] * cols[k], o);
+        o += rows[k] * cols[k];
+      }
+      check_rc(llmt_set_layer_f16(g.ctx, l, wp[0], wp[1], wp[2], wp[3], wp[4], wp[5], wp[6],
+                                  w.attn_norm, w.ffn_norm, w.q_norm, w.k_norm),
+               "set layer");
+    }
   }
   // The token gather reads embed_table (src/kernels/embed.cu:6-20) and the
   // logits read lm_head (src/kernels/lora_forward.cu:304), each loaded from
-  // its own file by the reference (src/train.cu:56-88).  The fp16 lm_head pad
-  // (src/main.cu:63) stands for lm_head, and for the embedding when
-  // embed_table is NULL (tied).  Distinct sources make an untied head.
-  const void* emb_src = m->embed_table ? (const void*)m->embed_table
-                                       : (m->_pad[0] ? m->_pad[0] : (const void*)m->lm_head);
-  const void* head_src = m->_pad[0] ? m->_pad[0] : (m->lm_head ? (const void*)m->lm_head : emb_src);
-  const void* e = m->embed_table ? f16(m->embed_table, nullptr, big, 0)
-                                 : f16(m->lm_head, m->_pad[0], big, 0);
-  check_rc(llmt_set_embed_f16(g.ctx, e, m->final_norm), "set embedding");
-  if (head_src != emb_src) {
-    const void* h = f16(m->lm_head, m->_pad[0], big, 0);
-    check_rc(llmt_set_lm_head_f16(g.ctx, h), "set lm_head");
-  } else {  // tied (again): the head reads the embedding's packed copies
-    c->Eh = c->E;
-    c->EhT = c->ET;
+  // its own file by the reference (src/train.cu:56-88).  The head comes from
+  // the fp16 pad (src/main.cu:63), else the fp32 field, else the int8 pair
+  // (src/main.cu:64, values _pad[1], fp32 row scales _pad[2]) as fp16
+  // q * scale; it stands for the embedding too when embed_table is NULL
+  // (tied).  Distinct sources make an untied head.
+  const bool head_i8 = !m->_pad[0] && !m->lm_head && m->_pad[1] && m->_pad[2];
+  const void* head_src = m->_pad[0] ? m->_pad[0]
+                         : m->lm_head ? (const void*)m->lm_head
+                         : head_i8    ? m->_pad[1]
+                                      : nullptr;
+  const void* emb_src = m->embed_table ? (const void*)m->embed_table : head_src;
+  if (!emb_src) {
+    fprintf(stderr, "llmt: neither an embedding nor an lm_head is given\n");
+    exit(EXIT_FAILURE);
   }
+  // The head as an fp16 buffer in the staging area (which it then occupies).
+  auto head16 = [&]() -> const void* {
+    if (m->_pad[0]) return m->_pad[0];
+    if (m->lm_head) return f16(m->lm_head, nullptr, big, 0);
+    hipLaunchKernelGGL(dequant_rows_kernel, dim3(grid_for((long long)big)), dim3(256), 0, c->st,
+                       (const int8_t*)m->_pad[1], (const float*)m->_pad[2], (long long)H,
+                       (long long)big, g.conv);
+    check_hip(hipGetLastError(), "lm_head dequant");
+    return g.conv;
+  };
+  const void* e = m->embed_table ? f16(m->embed_table, nullptr, big, 0) : head16();
+  // (synchronous: the staging area is free again afterwards.)  It also ties
+  // the head to the embedding.
+  check_rc(llmt_set_embed_f16(g.ctx, e, m->final_norm), "set embedding");
+  if (head_src && head_src != emb_src) check_rc(llmt_set_lm_head_f16(g.ctx, head16()), "set lm_head");
   g.model = m;
   g.model_key = key;
 }
@@ -427,15 +506,23 @@ void transformer_forward_lora(const int* token_ids, const MW* model, const LoraW
                               int seq_len) {
   (void)hidden; (void)residual; (void)norm_out; (void)q; (void)k; (void)v; (void)k_exp;
   (void)v_exp; (void)attn_out; (void)gate_buf; (void)up_buf; (void)acts;
-  if (seq_len < 2 || seq_len % 16) {
-    fprintf(stderr, "llmt: seq_len must be a multiple of 16 (got %d)\n", seq_len);
+  if (seq_len < 2) {
+    fprintf(stderr, "llmt: seq_len must be at least 2 (got %d)\n", seq_len);
     exit(EXIT_FAILURE);
   }
-  ensure_ctx(seq_len);
+  ensure_ctx(seq_len, weight_format(model));
   ensure_weights(model);
   gather_params(lora);
   Ctx* c = native();
-  check_hip(c->forward(token_ids, 1, logits), "forward");
+  check_hip(c->clear_pad_rows(1), "pad rows");
+  if (c->rows(1) == seq_len) {
+    check_hip(c->forward(token_ids, 1, logits), "forward");
+  } else {  // the logits GEMM writes rows(1) rows: the caller's buffer holds seq_len
+    check_hip(c->forward(token_ids, 1, c->logits), "forward");
+    check_hip(hipMemcpyAsync(logits, c->logits, (size_t)seq_len * c->V * sizeof(float),
+                             hipMemcpyDeviceToDevice, c->st),
+              "logits");
+  }
 }
 
 float cross_entropy_forward(const float* logits, const int* targets, float* dlogits,

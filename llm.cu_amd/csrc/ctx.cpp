@@ -48,7 +48,7 @@ int Ctx::init() {
   I = dims.intermediate;
   V = dims.vocab;
   L = dims.n_layers;
-  Tmax = maxB * S;
+  Tmax = rows(maxB);
   lscale = dims.alpha / (float)dims.rank;
   const long long R = kRank;
 
@@ -176,8 +176,7 @@ int Ctx::init() {
                             {H + 3 * kRank, NT}};
   part_elems = 0;
   for (int b = 1; b <= maxB; ++b) {
-    const int M = b * S;
-    if (M % 16) continue;
+    const int M = rows(b);
     for (auto& sh : shapes) {
       const size_t e = (size_t)gemm_pick_split(M, sh[0], sh[1], 64) * M * sh[0];
       if (e > part_elems) part_elems = e;
@@ -193,8 +192,12 @@ int Ctx::init() {
   TRY_PTR(rinv = alloc_n<float>(T));
   TRY_PTR(rinv2 = alloc_n<float>(T));
   TRY_PTR(dgu16 = alloc_n<_Float16>(T * 2 * I));
-  TRY_PTR(delta = alloc_n<float>((size_t)maxB * nq * S));
-  TRY_PTR(dsc = alloc_n<float>((size_t)maxB * nq * S));
+  // [B, nq, S] per sequence; the O-projection epilogue also writes the pad
+  // rows (row t at sequence t / S, position t % S), so whole sequences up to
+  // row Tmax - 1 are allocated.
+  const size_t nseq_pad = ((size_t)Tmax + S - 1) / S;
+  TRY_PTR(delta = alloc_n<float>(nseq_pad * nq * S));
+  TRY_PTR(dsc = alloc_n<float>(nseq_pad * nq * S));
   TRY_PTR(dqkv32 = alloc_n<float>(T * NT));
   TRY_PTR(dO16 = alloc_n<_Float16>((size_t)T * Q));
   TRY_PTR(gq16_all = alloc_n<_Float16>((size_t)L * T * NT));
@@ -333,6 +336,15 @@ int llmt_set_embed_f16(llmt_ctx* ctx, const void* embed_lm_head, const float* fi
   TRY_HIP(pack_f16(e, c->H, 1, c->H, c->V, c->ET, c->V, 0, 0, c->st));
   TRY_HIP(hipMemcpyAsync(c->final_norm, final_norm, c->H * 4, hipMemcpyDefault, c->st));
   TRY_HIP(hipStreamSynchronize(c->st));
+  // The tied embedding is the lm_head again (an earlier untied head keeps
+  // its buffers for a later llmt_set_lm_head_f16); a captured step that
+  // read the untied head is rebuilt.
+  if (c->Eh != c->E && c->graph_exec) {
+    (void)hipGraphExecDestroy(c->graph_exec);
+    c->graph_exec = nullptr;
+  }
+  c->Eh = c->E;
+  c->EhT = c->ET;
   c->embed_ready = true;
   return LLMT_OK;
 }
@@ -341,13 +353,15 @@ int llmt_set_lm_head_f16(llmt_ctx* ctx, const void* lm_head) {
   set_error("");
   Ctx* c = C_(ctx);
   TRY_ARG(c && lm_head, "llmt_set_lm_head_f16: NULL argument");
-  if (c->Eh == c->E) {
+  if (!c->head_own) {
     _Float16* eh = c->alloc_n<_Float16>((size_t)c->V * c->H);
     _Float16* eht = eh ? c->alloc_n<_Float16>((size_t)c->V * c->H) : nullptr;
     if (!eh || !eht) return LLMT_ERR_HIP;
-    c->Eh = eh;
-    c->EhT = eht;
+    c->head_own = eh;
+    c->headT_own = eht;
   }
+  c->Eh = c->head_own;
+  c->EhT = c->headT_own;
   const _Float16* w = (const _Float16*)lm_head;
   TRY_HIP(pack_f16(w, c->H, 0, c->V, c->H, c->Eh, c->H, 0, 0, c->st));
   TRY_HIP(pack_f16(w, c->H, 1, c->H, c->V, c->EhT, c->V, 0, 0, c->st));

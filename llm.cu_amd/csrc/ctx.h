@@ -82,6 +82,18 @@ struct GemmOut {
 struct Ctx {
   llmt_dims dims{};
   int maxB = 1, S = 0, wfmt = 0;
+  // Token rows of a batch of B sequences as the kernels see them: B * S
+  // rounded up to the GEMMs' 16-row granule.  Rows B * S .. rows(B) - 1 are
+  // pad rows: their forward values and gradients are exactly zero (the
+  // token gather leaves them zero, they have no target, and the attention
+  // never reads or writes them), so they add nothing to the loss or to the
+  // adapter gradients.
+  int rows(int B) const { return (B * S + 15) & ~15; }
+  // The batch whose pad rows are known to be zero in the buffers the step
+  // writes only at real rows (0: none).  Entry points that write those
+  // buffers at other rows reset it.
+  int pad_batch = 0;
+  hipError_t clear_pad_rows(int B);
   hipStream_t st = nullptr;
   bool own_stream = false;
   int H = 0, Q = 0, KV = 0, NT = 0, I = 0, V = 0, L = 0, nq = 0, nkv = 0, Tmax = 0;
@@ -97,6 +109,10 @@ struct Ctx {
   // embedding; their own buffers after llmt_set_lm_head_f16.
   _Float16* Eh = nullptr;
   _Float16* EhT = nullptr;
+  // An untied head's packed copies, kept for reuse after the head is tied
+  // again (llmt_set_embed_f16).
+  _Float16* head_own = nullptr;
+  _Float16* headT_own = nullptr;
   float* final_norm = nullptr;
   bool embed_ready = false;
 

@@ -33,9 +33,36 @@ void* Ctx::alloc(size_t bytes) {
     set_error("hipMalloc(%zu) failed", bytes);
     return nullptr;
   }
+  // Every buffer starts zeroed: rows the step never writes (the pad rows of
+  // a batch, see Ctx::rows) then hold finite values from the start.
+  if (hipMemset(p, 0, bytes) != hipSuccess) {
+    hipFree(p);
+    set_error("hipMemset(%zu) failed", bytes);
+    return nullptr;
+  }
   blocks.push_back(p);
   device_bytes += bytes;
   return p;
+}
+
+// Rows B * S .. rows(B) - 1 of the buffers the step writes only at real
+// token rows (the layer-0 input rows the token gather fills, the attention
+// output and gradients, the CE's fp16 dlogits) are zeroed once per batch
+// size, outside any captured graph; with them zero, every other kernel of
+// the step keeps the pad rows at exactly zero.
+hipError_t Ctx::clear_pad_rows(int B) {
+  if (B == pad_batch) return hipSuccess;
+  const size_t r0 = (size_t)B * S, n = (size_t)rows(B) - r0;
+  if (n) {
+    LLMT_HIP_TRY(hipMemsetAsync(stash[0].x_in + r0 * H, 0, n * H * sizeof(float), st));
+    LLMT_HIP_TRY(hipMemsetAsync(stash[0].xn + r0 * H, 0, n * H * sizeof(_Float16), st));
+    for (int l = 0; l < L; ++l)
+      LLMT_HIP_TRY(hipMemsetAsync(stash[l].o16 + r0 * Q, 0, n * Q * sizeof(_Float16), st));
+    LLMT_HIP_TRY(hipMemsetAsync(dqkv32 + r0 * NT, 0, n * NT * sizeof(float), st));
+    LLMT_HIP_TRY(hipMemsetAsync(grad16 + r0 * V, 0, n * V * sizeof(_Float16), st));
+  }
+  pad_batch = B;
+  return hipSuccess;
 }
 
 Ctx::~Ctx() {
@@ -183,7 +210,7 @@ AdamShadow Ctx::shadow_desc() const {
 // RMSNorm with next_w (the next layer's attention norm, or the final norm)
 // to xn_out.
 hipError_t Ctx::layer_fwd(int l, int B, const float* next_w, float* x_out, _Float16* xn_out) {
-  const int T = B * S;
+  const int T = rows(B);
   const float eps = dims.eps;
   Layer& w = layers[l];
   Stash& s = stash[l];
@@ -246,15 +273,17 @@ hipError_t Ctx::layer_fwd(int l, int B, const float* next_w, float* x_out, _Floa
 }
 
 hipError_t Ctx::forward(const int* tok, int B, float* logits_out) {
-  const int T = B * S;
+  const int T = rows(B);
   {
+    // the token gather fills the B * S real rows (the pad rows stay zero)
+    const int nt = B * S;
     const _Float16* e = E;
     const int Vv = V, Hh = H;
     const float *w0 = layers[0].attn_norm, eps = dims.eps;
     float* x0 = stash[0].x_in;
     _Float16* xn0 = stash[0].xn;
     LLMT_HIP_TRY(run(CAT_ROWS, "embed_norm", [=](hipStream_t q) {
-      return embed_norm(tok, e, Vv, Hh, w0, eps, T, x0, xn0, q);
+      return embed_norm(tok, e, Vv, Hh, w0, eps, nt, x0, xn0, q);
     }));
   }
   for (int l = 0; l < L; ++l) {
@@ -263,7 +292,8 @@ hipError_t Ctx::forward(const int* tok, int B, float* logits_out) {
                            last ? x_final : stash[l + 1].x_in, last ? xf16 : stash[l + 1].xn));
   }
   // lm_head logits (tied embedding); into the context's logits with the
-  // softmax pairs of the GEMM's column tiles for the fused cross entropy
+  // softmax pairs of the GEMM's column tiles for the fused cross entropy.
+  // logits_out receives rows(B) rows.
   BSeg se[1] = {hseg(Eh, V, H)};
   if (logits_out) {
     head_tiles = 0;
@@ -328,7 +358,7 @@ AttnArgs Ctx::attn_args(const Stash& s) const {
 // and the final RMSNorm backward: leaves the residual-stream gradient in
 // d_res and its fp16 operand in g16 / rinv.
 hipError_t Ctx::head_bwd(int B) {
-  const int T = B * S;
+  const int T = rows(B);
   const float eps = dims.eps;
   const int n_valid = B * (S - 1);
   GemmOut go;
@@ -359,7 +389,7 @@ hipError_t Ctx::head_bwd(int B) {
 // the projections' upstream gradients as the fp16 GEMM operands with their
 // row factors) in its per-layer slots for lora_grads.
 hipError_t Ctx::layer_bwd(int l, int B) {
-  const int T = B * S;
+  const int T = rows(B);
   const float eps = dims.eps;
   GemmOut go_;
   NormBwdArgs nb{};
@@ -457,7 +487,7 @@ hipError_t Ctx::lora_grads(int l0, int nl, int B, int accumulate) {
   const LoraGradJob* jobs = lora_jobs + (size_t)l0 * kLoraJobs;
   const LoraGradPlan plan = lora_plan;
   const float ls = lscale;
-  const int T = B * S;
+  const int T = rows(B);
   return run(CAT_LORA, "lora_grad", [=](hipStream_t q) {
     return lora_grad(jobs, plan, nl, T, ls, accumulate, q);
   });
@@ -609,7 +639,6 @@ static int check_tokens(Ctx* c, const int* tokens, const int* targets, int batch
   TRY_ARG(c && tokens && targets, "NULL argument");
   TRY_ARG(batch >= 1 && batch <= c->maxB, "batch %d outside [1, %d]", batch, c->maxB);
   TRY_ARG(c->weights_ready(), "frozen weights not set (llmt_set_layer_* / llmt_set_embed_f16)");
-  TRY_ARG((batch * c->S) % 16 == 0, "batch*seq_len must be a multiple of 16");
   return LLMT_OK;
 }
 
@@ -667,6 +696,7 @@ static bool graph_inputs(Ctx* c, const int* tokens, const int* targets) {
 // loss read-back, so a step is one graph launch and one wait.
 static int run_step(Ctx* c, int batch, int with_adam, float* loss_host,
                     const int* tokens = nullptr, const int* targets = nullptr) {
+  TRY_HIP(c->clear_pad_rows(batch));
   if (c->use_graph && !c->recording) {
     if (!c->graph_exec || c->graph_batch != batch || c->graph_adam != with_adam ||
         c->graph_tok != tokens || c->graph_tgt != targets) {
@@ -674,7 +704,7 @@ static int run_step(Ctx* c, int batch, int with_adam, float* loss_host,
         hipGraphExecDestroy(c->graph_exec);
         c->graph_exec = nullptr;
       }
-      hipGraph_t g;
+      hipGraph_t g = nullptr;
       TRY_HIP(hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
       hipError_t e = hipSuccess;
       if (tokens && with_adam)
@@ -683,6 +713,7 @@ static int run_step(Ctx* c, int batch, int with_adam, float* loss_host,
       if (e == hipSuccess)
         e = hipMemcpyAsync(c->host_loss, c->loss_dev, sizeof(float), hipMemcpyDeviceToHost, c->st);
       hipError_t e2 = hipStreamEndCapture(c->st, &g);
+      if ((e != hipSuccess || e2 != hipSuccess) && g) hipGraphDestroy(g);
       TRY_HIP(e);
       TRY_HIP(e2);
       e = hipGraphInstantiate(&c->graph_exec, g, nullptr, nullptr, 0);
@@ -768,6 +799,7 @@ static int replay_us(Ctx* c, const std::vector<const Launch*>& fns, int reps, fl
   for (const Launch* l : fns)
     if (e == hipSuccess) e = l->fn(c->st);
   hipError_t e2 = hipStreamEndCapture(c->st, &gph);
+  if ((e != hipSuccess || e2 != hipSuccess) && gph) hipGraphDestroy(gph);
   TRY_HIP(e);
   TRY_HIP(e2);
   e = hipGraphInstantiate(&ex, gph, nullptr, nullptr, 0);

@@ -15,8 +15,12 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 PKG = HERE.parent
 ROOT = PKG.parent
-# LLMT_LIB names another build of the library (default: the in-tree one)
-LIB_PATH = Path(os.environ.get("LLMT_LIB") or PKG / "libllmt.so")
+# Always the in-tree build: tests and the bench must measure the library
+# built from this tree, so an override of the path is refused outright.
+if os.environ.get("LLMT_LIB"):
+    raise ImportError("LLMT_LIB is set; llmt loads only the in-tree llm.cu_amd/libllmt.so "
+                      "(unset LLMT_LIB)")
+LIB_PATH = PKG / "libllmt.so"
 HEADER = ROOT / "include" / "llmt.h"
 
 vp, i32, f32, sz, u64 = C.c_void_p, C.c_int, C.c_float, C.c_size_t, C.c_uint64
@@ -335,6 +339,18 @@ class Context:
 
         class _View:
             __cuda_array_interface__ = {"shape": (rows, H), "typestr": "<f4",
+                                        "data": (addr, False), "version": 3, "strides": None}
+        return torch.as_tensor(_View(), device="cuda").clone()
+
+    def logits(self, rows):
+        """A copy of the first `rows` rows of the fp32 logits of the last
+        forward (llmt_logits)."""
+        import torch
+        addr = lib().llmt_logits(self.h)
+        V = self.dims.vocab
+
+        class _View:
+            __cuda_array_interface__ = {"shape": (rows, V), "typestr": "<f4",
                                         "data": (addr, False), "version": 3, "strides": None}
         return torch.as_tensor(_View(), device="cuda").clone()
 

@@ -123,3 +123,35 @@ def test_matches_library_and_resume(files, dev):
                           for l in range(SMALL.n_layers) for p in ("wq", "wk", "wv", "wo")
                           for m in ("A", "B")])
     assert np.array_equal(got, want.numpy())
+
+
+def test_int8_ragged_seq_first_loss_matches_oracle(files, dev):
+    """llm_train --int8 at --seq-len 60 (not a multiple of 16): the fp32
+    weight files quantised on the device (src/kernels/quantize.cu recipe,
+    fp16 scales); the first logged loss against the oracle on the
+    dequantised weights."""
+    import copy
+    from oracle.configs import quantize_model_int8
+    S60 = 60
+    d = files["root"] / "i8"
+    _write_weights(files["W"], d)
+    print("case: llm_train --int8 --seq-len 60", flush=True)
+    r = subprocess.run([str(EXE), "--dims", DIMS, "--seq-len", str(S60), "--seed", str(SEED),
+                        "--int8", "--data", str(files["tok"]), "--weights", str(d), "--steps", "1",
+                        "--log-every", "1", "--save-every", "1"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "(int8)" in r.stdout
+    loss = _losses(r.stdout)[1]
+    ctx = llmt.Context(llmt.make_dims(SMALL), max_batch=1, seq_len=S60)
+    try:
+        ctx.lora_init(SEED, 0.02, 0.0)
+        ad = [{p: ref.Adapter(A.clone(), B.clone()) for p, (A, B) in dd.items()}
+              for dd in llmt.unflatten_adapters(ctx.lora_get("param").cpu(), SMALL)]
+    finally:
+        ctx.close()
+    Wq, _ = quantize_model_int8(copy.deepcopy(files["W"]))
+    win = files["ids"][: S60 + 1]
+    logits, _ = ref.model_forward(Wq, ad, win[None, :-1], SMALL)
+    loss_ref, _, _ = ref.cross_entropy(logits, win[1:].long(), ref.valid_rows(1, S60))
+    assert abs(loss - float(loss_ref)) < 1e-3 + 5e-5

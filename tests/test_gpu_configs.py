@@ -97,9 +97,7 @@ def test_compat_struct_sizes():
     assert C.sizeof(MWC) == 8 * (1 + 32 * 28 + 5)
 
 
-def test_compat_reference_api_matches_oracle(c2, dev):
-    """The reference's own step API (src/train.cu:261-287 call sequence) with
-    fp16 weights in the MW pad slots (src/main.cu:40-55 map)."""
+def _compat_bind():
     L = llmt.lib()
     L.lora_weights_init.argtypes = [C.POINTER(LoraWeightsC)]
     L.lora_grads_alloc.argtypes = [C.POINTER(LoraGradsC), C.POINTER(LoraWeightsC)]
@@ -116,7 +114,58 @@ def test_compat_reference_api_matches_oracle(c2, dev):
         [C.c_float] * 5 + [C.c_int]
     L.lora_weights_free.argtypes = [C.POINTER(LoraWeightsC)]
     L.lora_grads_free.argtypes = [C.POINTER(LoraGradsC)]
+    return L
 
+
+def _compat_step(L, mw, ad, tok, tgt, S, dev):
+    """One forward / CE / backward through the reference's call sequence
+    (src/train.cu:261-287) with library-allocated adapters holding `ad`.
+    Returns (loss, dlogits, grads[l][proj] = (dA, dB) on the CPU, lora, grads)."""
+    lora = LoraWeightsC()
+    L.lora_weights_init(C.byref(lora))
+    for l in range(len(ad)):
+        for p in ref.PROJS:
+            a = getattr(lora, p)[l]
+            for addr, t in ((a.A, ad[l][p].A), (a.B, ad[l][p].B)):
+                _ptr_tensor(addr, t.numel(), dev).copy_(t.reshape(-1).float().to(dev))
+    grads = LoraGradsC()
+    L.lora_grads_alloc(C.byref(grads), C.byref(lora))
+    acts = LoraActsC()
+    L.lora_acts_alloc(C.byref(acts), S)
+    tokd = tok.reshape(-1).to(dev)
+    tgtd = tgt.reshape(-1).to(dev)
+    logits = torch.full((S, Q3.vocab), float("nan"), device=dev)
+    dlogits = torch.full((S, Q3.vocab), float("nan"), device=dev)
+    ws = [torch.empty(1, device=dev) for _ in range(15)]
+    torch.cuda.synchronize()
+    L.transformer_forward_lora(tokd.data_ptr(), C.byref(mw), C.byref(lora),
+                               *[w.data_ptr() for w in ws[:11]], logits.data_ptr(), C.byref(acts), S)
+    loss = L.cross_entropy_forward(logits.data_ptr(), tgtd.data_ptr(), dlogits.data_ptr(), S)
+    L.lora_grads_zero(C.byref(grads))
+    L.transformer_backward_lora(dlogits.data_ptr(), C.byref(mw), C.byref(lora), C.byref(acts),
+                                C.byref(grads), *[w.data_ptr() for w in ws[:14]], S)
+    torch.cuda.synchronize()
+    out = []
+    for l in range(len(ad)):
+        d = {}
+        for p in ref.PROJS:
+            gg = getattr(grads, p)[l]
+            nA, nB = ad[l][p].A.numel(), ad[l][p].B.numel()
+            d[p] = (_ptr_tensor(gg.dA, nA, dev).cpu().view_as(ad[l][p].A),
+                    _ptr_tensor(gg.dB, nB, dev).cpu().view_as(ad[l][p].B))
+        out.append(d)
+    return loss, dlogits, out, lora, grads
+
+
+def _worst(got, want):
+    return max(max(rel_l2(got[l][p][0], want[l][p][0]), rel_l2(got[l][p][1], want[l][p][1]))
+               for l in range(len(want)) for p in ref.PROJS)
+
+
+def test_compat_reference_api_matches_oracle(c2, dev):
+    """The reference's own step API (src/train.cu:261-287 call sequence) with
+    fp16 weights in the MW pad slots (src/main.cu:40-55 map)."""
+    L = _compat_bind()
     W, S = c2["W"], 128
     keep = []
 
@@ -139,41 +188,10 @@ def test_compat_reference_api_matches_oracle(c2, dev):
             d._pad[i] = dev16(getattr(lw, name))
     mw._pad[0] = dev16(W.embed)
     mw.final_norm = dev32(W.final_norm)
-    lora = LoraWeightsC()
-    L.lora_weights_init(C.byref(lora))
-    # the oracle's adapters into the library-allocated buffers
-    for l in range(28):
-        for p in ref.PROJS:
-            a = getattr(lora, p)[l]
-            for addr, t in ((a.A, c2["ad"][l][p].A), (a.B, c2["ad"][l][p].B)):
-                _ptr_tensor(addr, t.numel(), dev).copy_(t.reshape(-1).float().to(dev))
-    grads = LoraGradsC()
-    L.lora_grads_alloc(C.byref(grads), C.byref(lora))
-    acts = LoraActsC()
-    L.lora_acts_alloc(C.byref(acts), S)
-    tok = c2["tok"].reshape(-1).to(dev)
-    tgt = c2["tgt"].reshape(-1).to(dev)
-    logits = torch.empty(S, Q3.vocab, device=dev)
-    dlogits = torch.empty(S, Q3.vocab, device=dev)
-    ws = [torch.empty(1, device=dev) for _ in range(15)]
-    torch.cuda.synchronize()
-    L.transformer_forward_lora(tok.data_ptr(), C.byref(mw), C.byref(lora),
-                               *[w.data_ptr() for w in ws[:11]], logits.data_ptr(), C.byref(acts), S)
-    loss = L.cross_entropy_forward(logits.data_ptr(), tgt.data_ptr(), dlogits.data_ptr(), S)
+    loss, dlogits, got, lora, grads = _compat_step(L, mw, c2["ad"], c2["tok"], c2["tgt"], S, dev)
     assert abs(loss - c2["loss_ref"]) < LOSS_TOL
     assert float(dlogits[-1].abs().max()) == 0.0       # Q4: last row written as zeros
-    L.lora_grads_zero(C.byref(grads))
-    L.transformer_backward_lora(dlogits.data_ptr(), C.byref(mw), C.byref(lora), C.byref(acts),
-                                C.byref(grads), *[w.data_ptr() for w in ws[:14]], S)
-    torch.cuda.synchronize()
-    worst = 0.0
-    for l in range(28):
-        for p in ref.PROJS:
-            gg = getattr(grads, p)[l]
-            dA = _ptr_tensor(gg.dA, c2["grads_ref"][l][p][0].numel(), dev)
-            dB = _ptr_tensor(gg.dB, c2["grads_ref"][l][p][1].numel(), dev)
-            worst = max(worst, rel_l2(dA.cpu().view_as(c2["grads_ref"][l][p][0]), c2["grads_ref"][l][p][0]),
-                        rel_l2(dB.cpu().view_as(c2["grads_ref"][l][p][1]), c2["grads_ref"][l][p][1]))
+    worst = _worst(got, c2["grads_ref"])
     print("compat worst grad rel-L2", worst, flush=True)
     assert worst < GRAD_TOL
     L.adamw_step_lora(C.byref(lora), C.byref(grads), 3e-4, 0.9, 0.999, 1e-8, 0.01, 1)
@@ -183,6 +201,61 @@ def test_compat_reference_api_matches_oracle(c2, dev):
     want, _, _ = ref.adamw(c2["ad"][0]["wq"].A, c2["grads_ref"][0]["wq"][0], torch.zeros(16, 2048),
                            torch.zeros(16, 2048), 3e-4, 0.9, 0.999, 1e-8, 0.01, 1)
     assert rel_l2(got, want) < GRAD_TOL
+    L.lora_grads_free(C.byref(grads))
+    L.lora_weights_free(C.byref(lora))
+
+
+def test_compat_int8_pads_ragged_seq_matches_oracle(dev):
+    """The reference API with int8 frozen weights in the LW pad slots
+    _pad[7..20] (int8 values, float* row scales: src/main.cu:49-55), the
+    embedding as the fp32 embed_table and the lm_head as the MW int8 pair
+    _pad[1..2] (src/main.cu:64), at a sequence length that is not a multiple
+    of 16 (seq 100, src/train.cu:176,187).  Against the oracle on the
+    dequantised weights (fp16 scales of the C4 recipe; the head as fp16
+    q * scale)."""
+    import numpy as np
+    from oracle.quant import dequant, quantize_rows
+    torch.set_num_threads(16)
+    S = 100
+    print("case: compat API, int8 pads, full model, B1 x S100", flush=True)
+    W, ad, tok, tgt, qs = config_model(Q3, 1, S, 1005, int8=True)
+    hq, hs = quantize_rows(W.embed.numpy())
+    W.lm_head = torch.from_numpy(dequant(hq, hs)).half().float()
+    loss_ref, grads_ref, _ = oracle_grads(W, ad, tok, tgt, Q3)
+    L = _compat_bind()
+    keep = []
+
+    def put(a):
+        x = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+        keep.append(x)
+        return x.data_ptr()
+
+    def dev32(t):
+        x = t.to(torch.float32).to(dev).contiguous()
+        keep.append(x)
+        return x.data_ptr()
+
+    mw = MWC()
+    for l, lw in enumerate(W.layers):
+        d = mw.layers[l]
+        d.attn_norm, d.ffn_norm = dev32(lw.attn_norm), dev32(lw.ffn_norm)
+        d.q_norm, d.k_norm = dev32(lw.q_norm), dev32(lw.k_norm)
+        for i, name in enumerate(("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")):
+            q, s16 = qs[(l, name)]
+            d._pad[7 + 2 * i] = put(q)
+            d._pad[8 + 2 * i] = put(s16.astype(np.float32))
+    mw.embed_table = dev32(W.embed)
+    mw._pad[1] = put(hq)
+    mw._pad[2] = put(hs.astype(np.float32))
+    mw.final_norm = dev32(W.final_norm)
+    loss, dlogits, got, lora, grads = _compat_step(L, mw, ad, tok, tgt, S, dev)
+    print(f"compat int8 S{S}: loss {loss:.6f} oracle {float(loss_ref):.6f}", flush=True)
+    assert abs(loss - float(loss_ref)) < LOSS_TOL
+    assert float(dlogits[-1].abs().max()) == 0.0
+    assert torch.isfinite(dlogits).all()
+    worst = _worst(got, grads_ref)
+    print("compat int8 worst grad rel-L2", worst, flush=True)
+    assert worst < GRAD_TOL
     L.lora_grads_free(C.byref(grads))
     L.lora_weights_free(C.byref(lora))
 

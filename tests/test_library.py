@@ -86,3 +86,20 @@ def test_llm_train_cli_rejects_bad_input(tmp_path):
     r = run("--data", str(tok), "--seq-len", "8")
     assert r.returncode == 1 and "need at least 9 tokens, got 3" in r.stderr
     assert "Training config: lr=3.00e-04 steps=1000 seq_len=8" in r.stdout
+
+
+def test_noalloc_cross_entropy_rejects_inputs_beyond_the_scratch():
+    """llmt_cross_entropy_noalloc refuses, before any device work, inputs whose
+    statistics exceed its built-in 2 MiB scratch (the pointers are never
+    dereferenced: the host-side size check answers first)."""
+    f = llmt.lib().llmt_cross_entropy_noalloc
+    f.restype = C.c_int
+    f.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
+                  C.c_void_p, C.c_void_p]
+    V = 151936
+    rows = 14000   # 14000 x 19 chunks > the 262144 statistics of the scratch
+    rc = f(C.c_void_p(256), C.c_void_p(256), rows, V, 2, None, C.c_void_p(256), None, None)
+    assert rc == llmt.LLMT_ERR_ARG
+    assert "exceed" in llmt.lib().llmt_last_error().decode()
+    # the largest input that fits is not refused by the size check
+    assert 13797 * 19 <= 262144 < 13798 * 19
