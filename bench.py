@@ -330,32 +330,32 @@ def gemm_family(kinds):
     return n, t_us / n, by / n, fl / n
 
 
-def bandwidth_kernels(kinds, dims, T):
+BANDWIDTH_KINDS = ("adamw", "swiglu_bwd", "norm_bwd", "cross_entropy")
+
+
+def bandwidth_kernels(kinds):
     """The bandwidth-bound kernels of the step (north star: >= 70% of HBM):
-    each kernel's compulsory bytes per launch in the dtypes it reads and
-    writes, divided by its average replayed launch duration.
+    each kernel's bytes per launch as the library records them
+    (llmt_profile_kernels: what the kernel's interface reads and writes in
+    the dtypes it uses, split-K partials included), divided by its average
+    replayed launch duration.
       adamw          p, g, m, v read and p, m, v written, fp32, per parameter,
                      and the two fp16 operand copies of the new value the
                      next step's GEMMs read (7 x 4 B + 2 x 2 B);
-      swiglu_bwd     dY [T, I] fp32 (summed GEMM output), gate and up
-                     [T, 2I] fp16 read, dgate | dup [T, 2I] fp16 written;
-      norm_bwd       dY, x, residual-gradient in [T, H] fp32 read, residual
-                     gradient out fp32 and the fp16 GEMM operand written;
-      cross_entropy  logits [T, V] fp32 read once, the fp16 dlogits operand
-                     [T, V] written."""
-    H, I, V = dims.hidden, dims.intermediate, dims.vocab
-    nparam = dims.n_layers * 16 * (3 * H + 2 * dims.n_heads * dims.head_dim +
-                                   2 * dims.n_kv_heads * dims.head_dim + H)
-    want = {"adamw": (7 * 4 + 2 * 2) * nparam,
-            "swiglu_bwd": T * I * 4 + T * 2 * I * 2 + T * 2 * I * 2,
-            "norm_bwd": T * H * (4 + 4 + 4 + 4 + 2),
-            "cross_entropy": T * V * (4 + 2)}
+      swiglu_bwd     the down dX GEMM's fp32 split partials [split, T, I],
+                     gate and up [T, 2I] fp16 read, dgate | dup [T, 2I] fp16
+                     written;
+      norm_bwd       the gate/up dX GEMM's split partials, x and the residual
+                     gradient [T, H] fp32 read, the residual gradient fp32 and
+                     the fp16 GEMM operand written;
+      cross_entropy  the per-tile softmax pairs and the logits [T, V] fp32
+                     read once, the fp16 dlogits operand [T, V] written."""
     out = {}
     for k in kinds:
-        if k["name"] in want:
-            b = want[k["name"]]
+        if k["name"] in BANDWIDTH_KINDS:
+            b = k["bytes"]
             gbs = b / (k["us"] * 1e-6) / 1e9
-            out[k["name"]] = {"us": round(k["us"], 2), "bytes": b, "gbs": round(gbs, 1),
+            out[k["name"]] = {"us": round(k["us"], 2), "bytes": round(b), "gbs": round(gbs, 1),
                               "frac": round(gbs / HBM_PEAK_GBS, 4)}
     return out
 
@@ -429,7 +429,7 @@ def bench_step(cfg, steps, warmup, graph=True):
         "roofline": roofline, "kernels": kernel_summary(kinds),
         "kernels_sum_ms": round(sum(k["us"] * k["launches"] for k in kinds) / 1e3, 4),
         "launches_per_step": sum(k["launches"] for k in kinds),
-        "bandwidth_kernels": bandwidth_kernels(kinds, dims, T),
+        "bandwidth_kernels": bandwidth_kernels(kinds),
         "loss_first_last": [round(losses[0], 5), round(losses[-1], 5)],
     }
 

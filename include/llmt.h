@@ -303,8 +303,10 @@ int llmt_adamw(llmt_ctx* ctx, const llmt_hparams* hp, int step);
  * (0 forward GEMMs, 1 backward GEMMs, 2 lm_head GEMMs, 3 attention, 4 row
  * epilogues, 5 cross-entropy, 6 LoRA gradients, 7 AdamW), launches[k] per
  * step, us[k] = average launch duration in microseconds, flops[k] and
- * bytes[k] = algorithmic work of one launch for the GEMMs (2 M N K, streamed
- * weight bytes), 0 for the other kernels. */
+ * bytes[k] = algorithmic work of one launch: GEMMs 2 M N K and the streamed
+ * weight bytes; attention the flops of its causal S x S x 128 products (two
+ * forward, five backward) and no bytes; every other kernel no flops and the
+ * bytes its interface reads and writes (split-K partials included). */
 int llmt_profile_kernels(llmt_ctx* ctx, const int* tokens, const int* targets, int batch,
                          const llmt_hparams* hp, int step, int reps, int max_kinds, int* nkinds,
                          const char** names, int* cats, int* launches, float* us, double* flops,

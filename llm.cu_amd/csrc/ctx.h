@@ -27,7 +27,9 @@ enum {
 
 // One recorded kernel launch: its kind (kernel name, plus the shape for
 // GEMMs), category, a closure that launches it again on a given stream, and
-// its algorithmic work (GEMMs: 2 M N K flops and the streamed weight bytes).
+// its algorithmic work: GEMMs 2 M N K flops and the streamed weight bytes;
+// attention the flops of its causal products; the other kernels the bytes
+// they read and write (split-K partials included).
 struct Launch {
   int cat;
   std::string kind;
@@ -196,10 +198,13 @@ struct Ctx {
     return true;
   }
 
-  // Launch one kernel (f(stream)), recording it when profiling.
+  // Launch one kernel (f(stream)), recording it when profiling with its
+  // algorithmic work: flops (attention) and the bytes its interface moves
+  // (the row kernels, CE, adapter gradients, AdamW).
   template <class F>
-  hipError_t run(int cat, const char* kind, F&& f) {
-    if (recording) launches.push_back({cat, kind, std::function<hipError_t(hipStream_t)>(f), 0, 0});
+  hipError_t run(int cat, const char* kind, F&& f, double flops = 0, double bytes = 0) {
+    if (recording)
+      launches.push_back({cat, kind, std::function<hipError_t(hipStream_t)>(f), flops, bytes});
     return f(st);
   }
   // C = A B^T over the segments.  direct: split 1 into `direct` (ld ldc).

@@ -200,19 +200,38 @@ __device__ __forceinline__ void shadow_store(const AdamShadow& sh, long long i, 
   sh.rm[q.base + q.row * q.len + q.col] = h;
 }
 
-// One AdamW element update (src/kernels/lora.cu:206-220); returns the new
-// parameter.
+// The AdamW update of one element (src/kernels/lora.cu:206-220):
+//   m = b1 m + (1 - b1) g;  v = b2 v + (1 - b2) g^2;
+//   p = p (1 - lr wd) - lr (m / bc1) / (sqrt(v / bc2) + eps).
+// The bias corrections enter as reciprocals taken once (ib1 = 1 / bc1,
+// ib2 = 1 / bc2), and the square root and the last reciprocal are the
+// hardware v_sqrt_f32 / v_rcp_f32 (1 ulp each): the IEEE division and
+// square-root sequences had made the kernel VALU-bound (about 200 VALU
+// instructions a thread for four elements).  The update differs from the
+// correctly rounded formula by a few ulp of itself.
+struct AdamCoef {
+  float b1, b2, c1, c2, ib1, ib2, decay, lr, eps;
+};
+__device__ __forceinline__ AdamCoef adam_coef(const AdamHp& hp) {
+  return {hp.beta1, hp.beta2, 1.0f - hp.beta1, 1.0f - hp.beta2, 1.0f / hp.bc1, 1.0f / hp.bc2,
+          1.0f - hp.lr * hp.wd, hp.lr, hp.eps};
+}
+__device__ __forceinline__ float adam_update(const AdamCoef& k, float p, float g, float& m,
+                                             float& v) {
+  m = k.b1 * m + k.c1 * g;
+  v = k.b2 * v + k.c2 * g * g;
+  const float denom = __builtin_amdgcn_sqrtf(v * k.ib2) + k.eps;
+  return p * k.decay - k.lr * (m * k.ib1) * __builtin_amdgcn_rcpf(denom);
+}
+
+// One AdamW element update in place; returns the new parameter.
 __device__ __forceinline__ float adamw_elem(float* __restrict__ p, const float* __restrict__ g,
                                             float* __restrict__ m, float* __restrict__ v,
-                                            long long i, const AdamHp& hp) {
-  const float gi = g[i];
-  const float mi = hp.beta1 * m[i] + (1.0f - hp.beta1) * gi;
-  const float vi = hp.beta2 * v[i] + (1.0f - hp.beta2) * gi * gi;
+                                            long long i, const AdamCoef& k) {
+  float mi = m[i], vi = v[i];
+  const float pi = adam_update(k, p[i], g[i], mi, vi);
   m[i] = mi;
   v[i] = vi;
-  const float m_hat = mi / hp.bc1;
-  const float v_hat = vi / hp.bc2;
-  const float pi = p[i] * (1.0f - hp.lr * hp.wd) - hp.lr * m_hat / (sqrtf(v_hat) + hp.eps);
   p[i] = pi;
   return pi;
 }
@@ -223,52 +242,97 @@ __global__ __launch_bounds__(NTH) void adamw_kernel(float* __restrict__ p,
                                                     float* __restrict__ m, float* __restrict__ v,
                                                     long long n,
                                                     const AdamHp* __restrict__ hpp) {
-  const AdamHp hp = *hpp;
+  const AdamCoef k = adam_coef(*hpp);
   for (long long i = (long long)blockIdx.x * NTH + threadIdx.x; i < n;
        i += (long long)gridDim.x * NTH)
-    adamw_elem(p, g, m, v, i, hp);
+    adamw_elem(p, g, m, v, i, k);
 }
 
 // The whole arena with its fp16 shadows, one launch: blockIdx.y = layer x 8
-// + segment (q, k, v, o x A, B), so every block knows where its elements'
-// shadow rows and columns are (32-bit index math only).  update = 0 only
-// refreshes the shadows from the parameters.
+// + segment (q, k, v, o x A, B), blockIdx.x = a tile of kTile elements of
+// that segment, so every block knows where its elements' shadow rows and
+// columns are (32-bit index math only).  A thread moves four elements as
+// 16-byte loads and stores of p, g, m, v (one 16-byte piece a thread over
+// many blocks keeps the DRAM streams dense: a copy in this form measured
+// 6.3 TB/s on MI355X against 4.6-5.6 TB/s grid-stride; here nontemporal
+// loads and stores measured slower, 43 against 37 us).  Each tile covers
+// the 16 shadow rows x 64 columns of two whole fragment-packed 16 x 32
+// blocks, so a block writes complete 1 KB packed blocks and 128-byte pieces
+// of the row-major twin (the same kernel over linear half-row tiles, whose
+// packed stores leave partial lines, took 41 us):
+// an A tile is rows r = 0..15 x columns c0 .. c0 + 63 of A (16 pieces of
+// 256 bytes of the arena; thread = row t / 16, four columns); a B tile is
+// the 64 rows o0 .. o0 + 63 of B [d_out, 16] (contiguous in the arena),
+// transposed through LDS so that each thread stores four consecutive
+// columns o of one row r of B^T.  update = 0 only refreshes the shadows
+// from the parameters.
+constexpr int kTile = 4 * NTH;
+
+__device__ __forceinline__ floatx4 ld4v(const float* p) {
+  return *reinterpret_cast<const floatx4*>(p);
+}
+__device__ __forceinline__ void st4v(float* p, floatx4 v) {
+  *reinterpret_cast<floatx4*>(p) = v;
+}
+
 __global__ __launch_bounds__(NTH) void adamw_shadow_kernel(float* __restrict__ p,
                                                            const float* __restrict__ g,
                                                            float* __restrict__ m,
                                                            float* __restrict__ v,
                                                            const AdamHp* __restrict__ hpp,
                                                            int update, const AdamShadow sh) {
-  const AdamHp hp = *hpp;
+  __shared__ _Float16 bt[R][64 + 4];
   const int l = blockIdx.y >> 3, s = blockIdx.y & 7, q = s >> 1;
-  const long long i0 = (long long)l * sh.per_layer + sh.seg_off[s];
   const int n = (int)((s < 7 ? sh.seg_off[s + 1] : sh.per_layer) - sh.seg_off[s]);
-  const long long lb = (long long)l * sh.shadow_per_layer;
-  // A [16, d_in]: element j = (r, c) -> row row0 + r, column c of a block of
-  // row length d_in; B [d_out, 16]: element j = (o, r) -> row row0 + r,
-  // column col0 + o of B^T (row length len)
+  if (blockIdx.x * kTile >= n) return;
   const bool is_b = s & 1;
-  const int row0 = q < 3 ? q * R : 0;
-  const int len = is_b ? (q < 3 ? sh.nt : sh.d_out[3]) : sh.d_in[q];
-  const int col0 = is_b && q < 3 ? sh.col_off[q] : 0;
-  const long long base = lb + (is_b ? (q < 3 ? sh.bt_qkv : sh.bt_o) : (q < 3 ? sh.a_qkv : sh.a_o));
-  const unsigned ulen = (unsigned)len;
-  for (int j = blockIdx.x * NTH + threadIdx.x; j < n; j += gridDim.x * NTH) {
-    const long long i = i0 + j;
-    const float pi = update ? adamw_elem(p, g, m, v, i, hp) : p[i];
-    int row, col;
-    if (is_b) {
-      row = row0 + (j & (R - 1));
-      col = col0 + (j >> 4);
-    } else {
-      const unsigned r = (unsigned)j / ulen;
-      row = row0 + (int)r;
-      col = j - (int)(r * ulen);
+  // A: element (r, c0 + 4 (t % 16)) with r = t / 16; B: elements 4 t .. of the tile
+  const int a_len = sh.d_in[q];
+  const int ar = threadIdx.x >> 4, ac = blockIdx.x * 64 + 4 * (threadIdx.x & 15);
+  const int jt = is_b ? blockIdx.x * kTile + 4 * threadIdx.x : ar * a_len + ac;
+  const long long i = (long long)l * sh.per_layer + sh.seg_off[s] + jt;
+  floatx4 pv = ld4v(p + i);
+  if (update) {
+    const AdamCoef k = adam_coef(*hpp);
+    const floatx4 gv = ld4v(g + i);
+    floatx4 mv = ld4v(m + i), vv = ld4v(v + i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float me = mv[e], ve = vv[e];
+      pv[e] = adam_update(k, pv[e], gv[e], me, ve);
+      mv[e] = me;
+      vv[e] = ve;
     }
-    const _Float16 h = (_Float16)pi;
-    sh.shadow[base + packed_index(row, col, len)] = h;
-    sh.rm[base + (long long)row * len + col] = h;
+    st4v(p + i, pv);
+    st4v(m + i, mv);
+    st4v(v + i, vv);
   }
+  const half4 h = {(_Float16)pv[0], (_Float16)pv[1], (_Float16)pv[2], (_Float16)pv[3]};
+  const long long lb = (long long)l * sh.shadow_per_layer;
+  if (!is_b) {
+    // A [16, d_in]: element (r, c) -> row row0 + r, column c (row length d_in)
+    const int row = (q < 3 ? q * R : 0) + ar;
+    const long long base = lb + (q < 3 ? sh.a_qkv : sh.a_o);
+    *reinterpret_cast<half4*>(sh.shadow + base + packed_index(row, ac, a_len)) = h;
+    *reinterpret_cast<half4*>(sh.rm + base + (long long)row * a_len + ac) = h;
+    return;
+  }
+  // B [d_out, 16]: element j = (o, r) -> row row0 + r, column col0 + o of
+  // B^T (row length len); this tile holds o in [64 blockIdx.x, 64 blockIdx.x + 64)
+  {
+    const int o = threadIdx.x >> 2, r = 4 * (threadIdx.x & 3);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) bt[r + e][o] = h[e];
+  }
+  __syncthreads();
+  const int len = q < 3 ? sh.nt : sh.d_out[3];
+  const int r = threadIdx.x >> 4, c4 = 4 * (threadIdx.x & 15);
+  const int row = (q < 3 ? q * R : 0) + r;
+  const int col = (q < 3 ? sh.col_off[q] : 0) + 64 * blockIdx.x + c4;
+  const half4 t = *reinterpret_cast<const half4*>(&bt[r][c4]);
+  const long long base = lb + (q < 3 ? sh.bt_qkv : sh.bt_o);
+  *reinterpret_cast<half4*>(sh.shadow + base + packed_index(row, col, len)) = t;
+  *reinterpret_cast<half4*>(sh.rm + base + (long long)row * len + col) = t;
 }
 
 // Counter-based normal draws: SplitMix64 of (seed, index) -> two 24-bit
@@ -350,12 +414,24 @@ hipError_t adamw(float* p, const float* g, float* m, float* v, long long n, cons
     set_error("adamw: %lld parameters are not whole layers of %lld", n, sh.per_layer);
     return hipErrorInvalidValue;
   }
+  // every segment is whole tiles (its A rows and B^T rows a multiple of 64
+  // columns, 16-byte aligned), so the tiles never straddle segments
   long long seg = 0;
-  for (int s = 0; s < 8; ++s)
-    seg = std::max(seg, (s < 7 ? sh.seg_off[s + 1] : sh.per_layer) - sh.seg_off[s]);
-  const unsigned bx = (unsigned)std::min<long long>((seg + 4 * NTH - 1) / (4 * NTH), 64);
-  hipLaunchKernelGGL(adamw_shadow_kernel, dim3(bx, (unsigned)(n / sh.per_layer * 8)), dim3(NTH), 0,
-                     st, p, g, m, v, hp, update, sh);
+  for (int s = 0; s < 8; ++s) {
+    const long long ns = (s < 7 ? sh.seg_off[s + 1] : sh.per_layer) - sh.seg_off[s];
+    if (ns % kTile || sh.seg_off[s] % 4) {
+      set_error("adamw: segment %d of %lld elements is not whole %d-element tiles", s, ns, kTile);
+      return hipErrorInvalidValue;
+    }
+    seg = std::max(seg, ns);
+  }
+  for (int q = 0; q < 4; ++q)
+    if (sh.d_in[q] % 64 || sh.d_out[q] % 64) {
+      set_error("adamw: adapter %d dims %d x %d not multiples of 64", q, sh.d_out[q], sh.d_in[q]);
+      return hipErrorInvalidValue;
+    }
+  hipLaunchKernelGGL(adamw_shadow_kernel, dim3((unsigned)(seg / kTile), (unsigned)(n / sh.per_layer * 8)),
+                     dim3(NTH), 0, st, p, g, m, v, hp, update, sh);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }

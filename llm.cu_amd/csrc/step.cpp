@@ -151,6 +151,12 @@ RowIn Ctx::row_in(const GemmOut& go, int hcol, int nh, int nterm, const LoraTerm
   return r;
 }
 
+// Bytes a row epilogue reads from a GEMM's split partials: split x T rows of
+// n columns plus the raw h columns.
+static double part_bytes(const RowIn& r, int T, int n) {
+  return 4.0 * r.split * (double)T * (n + r.nh);
+}
+
 // ------------------------------------------------------------------ layout helpers
 
 BSeg Ctx::wseg(const WMat& w) const {
@@ -229,9 +235,14 @@ hipError_t Ctx::layer_fwd(int l, int B, const float* next_w, float* x_out, _Floa
   qa.cosT = cosT; qa.sinT = sinT;
   qa.S = S; qa.nq = nq; qa.nkv = nkv; qa.eps = eps;
   qa.qkraw = s.qkraw; qa.qkv16 = s.qkv16; qa.hbuf = s.h;
-  LLMT_HIP_TRY(run(CAT_ROWS, "qkv_post", [=](hipStream_t q) { return qkv_post(qa, T, q); }));
+  // partials in; q/k raw (fp16), q/k/v (fp16) and the 48 h columns out
+  LLMT_HIP_TRY(run(CAT_ROWS, "qkv_post", [=](hipStream_t q) { return qkv_post(qa, T, q); }, 0,
+                   part_bytes(qa.in, T, NT) + (double)T * ((Q + KV) * 2 + NT * 2 + 48 * 4)));
   const AttnArgs aa = attn_args(s);
-  LLMT_HIP_TRY(run(CAT_ATTN, "attn_fwd", [=](hipStream_t q) { return attn_fwd(aa, B, q); }));
+  // QK^T and PV: two causal S x S x 128 products per (sequence, query head)
+  const double attn_prod = 2.0 * B * nq * (S * (S + 1.0) / 2.0) * kHeadDim;
+  LLMT_HIP_TRY(run(CAT_ATTN, "attn_fwd", [=](hipStream_t q) { return attn_fwd(aa, B, q); },
+                   2 * attn_prod));
   // O (+ LoRA A) projection, residual, FFN norm
   BSeg so[2] = {wseg(w.wo), hseg(shadow_ptr(l, sh_a_o), kRank, Q)};
   const LoraTerm to[1] = {{shadow_rm + (size_t)l * shadow_per_layer + sh_bt_o, 0, H, 0, H, 0}};
@@ -242,9 +253,10 @@ hipError_t Ctx::layer_fwd(int l, int B, const float* next_w, float* x_out, _Floa
     float *hb = s.h, *x_mid = s.x_mid;
     _Float16* xn2 = s.xn2;
     const int Hh = H;
+    // partials and x_in in; x_mid (fp32), its norm (fp16) and h_o out
     LLMT_HIP_TRY(run(CAT_ROWS, "o_post", [=](hipStream_t q) {
       return o_post(ri, x_in, fw, eps, Hh, T, hb, x_mid, xn2, q);
-    }));
+    }, 0, part_bytes(ri, T, H) + (double)T * (H * 4 + H * 4 + H * 2 + 16 * 4)));
   }
   // gate/up, SwiGLU (in the GEMM epilogue where the large-tile kernel runs)
   BSeg sg[1] = {wseg(w.wgu)};
@@ -256,7 +268,8 @@ hipError_t Ctx::layer_fwd(int l, int B, const float* next_w, float* x_out, _Floa
     _Float16* gu = s.gu;
     _Float16* a = a16;
     const int Ii = I;
-    LLMT_HIP_TRY(run(CAT_ROWS, "gu_post", [=](hipStream_t q) { return gu_post(ri, Ii, T, gu, a, q); }));
+    LLMT_HIP_TRY(run(CAT_ROWS, "gu_post", [=](hipStream_t q) { return gu_post(ri, Ii, T, gu, a, q); },
+                     0, part_bytes(ri, T, 2 * I) + (double)T * (2 * I * 2 + I * 2)));
   }
   // down, residual, next norm
   BSeg sd[1] = {wseg(w.wd)};
@@ -267,7 +280,7 @@ hipError_t Ctx::layer_fwd(int l, int B, const float* next_w, float* x_out, _Floa
     const int Hh = H;
     LLMT_HIP_TRY(run(CAT_ROWS, "resid_norm", [=](hipStream_t q) {
       return resid_norm(ri, x_mid, next_w, eps, Hh, T, x_out, xn_out, q);
-    }));
+    }, 0, part_bytes(ri, T, H) + (double)T * (H * 4 + H * 4 + H * 2)));
   }
   return hipSuccess;
 }
@@ -284,7 +297,7 @@ hipError_t Ctx::forward(const int* tok, int B, float* logits_out) {
     _Float16* xn0 = stash[0].xn;
     LLMT_HIP_TRY(run(CAT_ROWS, "embed_norm", [=](hipStream_t q) {
       return embed_norm(tok, e, Vv, Hh, w0, eps, nt, x0, xn0, q);
-    }));
+    }, 0, (double)nt * (4 + H * 2 + H * 4 + H * 2)));
   }
   for (int l = 0; l < L; ++l) {
     const bool last = l + 1 == L;
@@ -311,17 +324,20 @@ hipError_t Ctx::ce(const float* lg, const int* tgt, int B, float* dlogits_out) {
   float2* stats = ce_stats;
   _Float16* g16c = grad16;
   float *lr = loss_rows, *lm = loss_dev, *lse = lse_rows;
+  // the logits (fp32) in, the fp16 operand and optionally fp32 dlogits out
+  const double out_bytes = (double)rows * V * (2 + (dlogits_out ? 4 : 0));
   if (!lg && head_tiles > 0) {  // the forward's logits with their tile pairs
     const int nt = head_tiles;
     LLMT_HIP_TRY(run(CAT_CE, "cross_entropy", [=](hipStream_t q) {
       return cross_entropy_from_stats(x, stats, nt, tgt, rows, Vv, Ss, lse, dlogits_out, g16c, lr,
                                       lm, q);
-    }));
+    }, 0, (double)rows * (V * 4.0 + nt * 8.0) + out_bytes));
     return hipSuccess;
   }
+  // two reads of the logits (statistics, then the gradient)
   LLMT_HIP_TRY(run(CAT_CE, "cross_entropy", [=](hipStream_t q) {
     return cross_entropy(x, tgt, rows, Vv, Ss, stats, dlogits_out, g16c, lr, lm, q);
-  }));
+  }, 0, (double)rows * V * 8.0 + out_bytes));
   return hipSuccess;
 }
 
@@ -379,7 +395,9 @@ hipError_t Ctx::head_bwd(int B) {
   nb.dmid_out = nullptr;
   nb.g16 = g16;
   nb.rinv_out = rinv;
-  LLMT_HIP_TRY(run(CAT_ROWS, "norm_bwd", [=](hipStream_t q) { return norm_bwd(nb, T, q); }));
+  // partials and x in; the residual gradient (fp32) and its fp16 operand out
+  LLMT_HIP_TRY(run(CAT_ROWS, "norm_bwd_final", [=](hipStream_t q) { return norm_bwd(nb, T, q); },
+                   0, part_bytes(nb.in, T, H) + (double)T * H * (4 + 4 + 2)));
   return hipSuccess;
 }
 
@@ -409,9 +427,10 @@ hipError_t Ctx::layer_bwd(int l, int B) {
     _Float16* d16 = dgu16;
     float* r2 = rinv2;
     const int Ii = I;
+    // partials and gate|up (fp16) in, dgate|dup (fp16) out
     LLMT_HIP_TRY(run(CAT_ROWS, "swiglu_bwd", [=](hipStream_t q) {
       return swiglu_bwd(ri, ri_in, gu, Ii, T, d16, r2, q);
-    }));
+    }, 0, part_bytes(ri, T, I) + (double)T * (2 * I * 2 + 2 * I * 2)));
   }
   BSeg sg[1] = {wseg(w.wguT)};
   LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, dgu16, 2 * I, sg, 1, T, 2 * I, nullptr, 0, &go_));
@@ -429,7 +448,10 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   nb.dmid_out = nullptr;
   nb.g16 = og16;
   nb.rinv_out = ro(l);
-  LLMT_HIP_TRY(run(CAT_ROWS, "norm_bwd", [=](hipStream_t q) { return norm_bwd(nb, T, q); }));
+  // partials, x and the residual gradient in; the residual gradient and its
+  // fp16 operand out
+  LLMT_HIP_TRY(run(CAT_ROWS, "norm_bwd", [=](hipStream_t q) { return norm_bwd(nb, T, q); }, 0,
+                   part_bytes(nb.in, T, H) + (double)T * H * (4 + 4 + 4 + 2)));
   // O projection dX (+ dh_o through the B_o^T rows)
   BSeg so[2] = {wseg(w.woT), hseg(shadow_ptr(l, sh_bt_o), kRank, H)};
   const LoraTerm tbo[1] = {{shadow_rm + (size_t)l * shadow_per_layer + sh_a_o, 0, Q, 0, Q, 0}};
@@ -441,13 +463,17 @@ hipError_t Ctx::layer_bwd(int l, int B) {
     _Float16* d16 = dO16;
     float *de = delta, *ds = dsc;
     const int nqh = nq, Ss = S;
+    // partials and O (fp16) in; dO (fp16), dh_o and delta / dsc out
     LLMT_HIP_TRY(run(CAT_ROWS, "o_dx_post", [=](hipStream_t q) {
       return o_dx_post(ri, r, o16, nqh, Ss, T, dh, d16, de, ds, q);
-    }));
+    }, 0, part_bytes(ri, T, Q) + (double)T * (Q * 2 + Q * 2 + 16 * 4 + nq * 8)));
   }
   // attention backward
   const AttnArgs aa = attn_args(s);
-  LLMT_HIP_TRY(run(CAT_ATTN, "attn_bwd", [=](hipStream_t q) { return attn_bwd(aa, B, q); }));
+  // recomputed QK^T, dO V^T, P^T dO, dS^T Q, dS K: five causal products
+  const double attn_prod = 2.0 * B * nq * (S * (S + 1.0) / 2.0) * kHeadDim;
+  LLMT_HIP_TRY(run(CAT_ATTN, "attn_bwd", [=](hipStream_t q) { return attn_bwd(aa, B, q); },
+                   5 * attn_prod));
   // RoPE + QK-norm backward
   QkBwdArgs qb{};
   qb.dqkv = dqkv32; qb.ld_dqkv = NT;
@@ -456,7 +482,9 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   qb.cosT = cosT; qb.sinT = sinT;
   qb.S = S; qb.nq = nq; qb.nkv = nkv; qb.eps = eps;
   qb.dy32 = nullptr; qb.g16 = qg16; qb.rinv_out = rq(l);
-  LLMT_HIP_TRY(run(CAT_ROWS, "qk_bwd", [=](hipStream_t q) { return qk_bwd(qb, T, q); }));
+  // dq/dk/dv (fp32) and q/k raw (fp16) in, the fp16 operand out
+  LLMT_HIP_TRY(run(CAT_ROWS, "qk_bwd", [=](hipStream_t q) { return qk_bwd(qb, T, q); }, 0,
+                   (double)T * (NT * 4 + (Q + KV) * 2 + NT * 2)));
   // Q/K/V dX (+ dh_q, dh_k, dh_v through the B^T rows), attention norm bwd
   BSeg sq[2] = {wseg(w.wqkvT), hseg(shadow_ptr(l, sh_bt_qkv), 3 * kRank, NT)};
   const _Float16* a_qkv = shadow_rm + (size_t)l * shadow_per_layer + sh_a_qkv;
@@ -479,7 +507,8 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   nb.dmid_out = nullptr;
   nb.g16 = g16;
   nb.rinv_out = rinv;
-  LLMT_HIP_TRY(run(CAT_ROWS, "norm_bwd_lora", [=](hipStream_t q) { return norm_bwd(nb, T, q); }));
+  LLMT_HIP_TRY(run(CAT_ROWS, "norm_bwd_lora", [=](hipStream_t q) { return norm_bwd(nb, T, q); },
+                   0, part_bytes(nb.in, T, H) + (double)T * (H * (4 + 4 + 4 + 2) + 48 * 4)));
   return hipSuccess;
 }
 
@@ -488,9 +517,14 @@ hipError_t Ctx::lora_grads(int l0, int nl, int B, int accumulate) {
   const LoraGradPlan plan = lora_plan;
   const float ls = lscale;
   const int T = rows(B);
+  // per layer: the dA inputs (xn three times, o; fp16) and the dB inputs
+  // (the two fp16 gradient operands) with the h / dh columns (fp32), the
+  // gradients out (fp32)
+  const double per_layer = (double)T * ((3.0 * H + Q) * 2 + (NT + H) * 2 + 2 * 64 * 4) +
+                           (double)lora_per_layer * 4 * (accumulate ? 2 : 1);
   return run(CAT_LORA, "lora_grad", [=](hipStream_t q) {
     return lora_grad(jobs, plan, nl, T, ls, accumulate, q);
-  });
+  }, 0, per_layer * nl);
 }
 
 hipError_t Ctx::backward(int B, int accumulate) {
@@ -506,7 +540,9 @@ hipError_t Ctx::optimizer() {
   const long long n = (long long)lora_numel;
   const AdamHp* hp = hp_dev;
   const AdamShadow sh = shadow_desc();
-  LLMT_HIP_TRY(run(CAT_ADAM, "adamw", [=](hipStream_t q) { return adamw(p, g, m, v, n, hp, 1, sh, q); }));
+  // p, g, m, v in; p, m, v and the two fp16 copies of p out
+  LLMT_HIP_TRY(run(CAT_ADAM, "adamw", [=](hipStream_t q) { return adamw(p, g, m, v, n, hp, 1, sh, q); },
+                   0, (double)n * (7 * 4 + 2 * 2)));
   return hipSuccess;
 }
 

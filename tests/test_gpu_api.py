@@ -146,7 +146,9 @@ def test_profile_kernels_contract(prob, dev):
     assert count["cross_entropy"] == 1
     assert count["attn_fwd"] == L and count["attn_bwd"] == L
     assert count["qkv_post"] == L and count["qk_bwd"] == L
-    gemms = sum(k["launches"] for k in kinds if k["flops"] > 0)
+    gemms = sum(k["launches"] for k in kinds if k["category"].startswith("gemm"))
+    for k in kinds:   # every kind carries its algorithmic work
+        assert k["flops"] > 0 or k["bytes"] > 0, k["name"]
     assert gemms == 8 * L + 2       # 4 forward + 4 backward GEMMs a layer, logits, head dX
 
 
