@@ -15,10 +15,14 @@ Prints ONE JSON line.  Besides the contract fields it carries
                 graph of its own (llmt_profile_kernels), timed with HIP
                 events on the context's stream; achieved = streamed weight
                 bytes per launch / average launch time, against 8 TB/s HBM
-                (C4: TFLOP/s against 2.5 PFLOP/s); traffic = measured HBM
-                bytes per launch (rocprofv3 FETCH_SIZE and WRITE_SIZE passes
-                scaled by the copy calibration, read from
-                profiles/gemm_c2_traffic.md);
+                (C4: TFLOP/s against 2.5 PFLOP/s); attainable_frac = the
+                launches' roofline times (max of MFMA time at peak and
+                compulsory HBM time) over their measured times; traffic =
+                measured HBM bytes per launch (rocprofv3 FETCH_SIZE and
+                WRITE_SIZE passes scaled by the copy calibration, read from
+                profiles/gemm_<config>_traffic.md);
+  roofline_bwd: the same for the backward's dX GEMMs alone (the metric's
+                "bwd % MFMA / HBM peak"): hbm_frac and mfma_frac both given;
   kernels:      per-category kernel milliseconds of a step from the same
                 replays (kernels only: their sum, kernels_sum_ms, is below
                 ms_per_step by the launch gaps);
@@ -27,13 +31,14 @@ Prints ONE JSON line.  Besides the contract fields it carries
                 datasheet 8 TB/s and copy_frac of the device copy rate
                 (copy_gbs) measured in the same run;
   cpu_baseline: the CPU oracle (PyTorch fp32, oracle/lora_step.py) on a
-                bounded sample of the same step;
+                bounded sample of the same step (c4, c3 and c1 carry their own);
   c4, c3, c1:   (default run) the C4 step (B8 x S512, int8 weights), the
                 C3 attention block and the C1 head (lm_head + CE + dX)
                 measured in the same run; the C4 GEMM roofline also as
                 frac_of_hipblaslt, against the 8192^3 fp16 hipBLASLt GEMM
                 of the same run (achievable.mfma_f16_tflops_hipblaslt).
---config c3 / c4 --only times one of those alone.
+--config c3 / c4 --only times one of those alone; --kinds-md also prints the
+per-kind markdown table of the step (the profiles/ kind tables).
 """
 from __future__ import annotations
 
@@ -155,13 +160,80 @@ def cpu_baseline(batch, seq_len, min_s=10.0):
     }
 
 
-def measured_traffic():
-    """HBM bytes per GEMM launch of the C2 step from the committed rocprofv3
-    counter summary (None if absent)."""
-    f = ROOT / "profiles" / "gemm_c2_traffic.md"
+def cpu_baseline_c3(B=1, S=2048, nq=16, nkv=8, min_s=10.0):
+    """C3 on the CPU oracle (PyTorch fp32): QK-RMSNorm + RoPE, causal GQA
+    attention forward and backward, the norm / RoPE backward, on a bounded
+    sample (B1 x S2048: a quarter of the B4 workload), timed like
+    cpu_baseline."""
+    import torch
+    from oracle import lora_step as ref
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    g = torch.Generator().manual_seed(1003)
+    q, k, v, do = (torch.randn(B, S, h, 128, generator=g) for h in (nq, nkv, nkv, nq))
+    w = torch.ones(128)
+    cos, sin = ref.rope_tables(S, 128, 1e6)
+
+    def run():
+        qn = ref.rope_fwd(ref.rmsnorm(q, w, 1e-6), cos, sin)
+        kn = ref.rope_fwd(ref.rmsnorm(k, w, 1e-6), cos, sin)
+        o, lse = ref.attention_fwd(qn, kn, v)
+        dq, dk, dv = ref.attention_bwd(do, qn, kn, v, o, lse)
+        ref.rmsnorm_bwd(ref.rope_bwd(dq, cos, sin), q, w, 1e-6)
+        ref.rmsnorm_bwd(ref.rope_bwd(dk, cos, sin), k, w, 1e-6)
+    med, n = _timed_median(run, min_s)
+    return {"value": round(B * S / med, 2), "unit": "tokens/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"CPU oracle (PyTorch fp32) attention block fwd+bwd (QK-norm, RoPE, causal "
+                       f"GQA {nq}/{nkv} heads) at B{B}xS{S} (a quarter of the B4 workload): "
+                       f"median of {n} calls after 1 warm-up, {med:.3f} s/call; "
+                       f"{torch.get_num_threads()} threads on {cpu_description()}")}
+
+
+def cpu_baseline_c1(T=128, H=2048, V=151936, min_s=10.0):
+    """C1 on the CPU oracle (PyTorch fp32): logits = hidden W^T, the fused
+    cross entropy with dlogits, dhidden = dlogits W, on the whole workload."""
+    import torch
+    from oracle import lora_step as ref
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    g = torch.Generator().manual_seed(1001)
+    W = torch.randn(V, H, generator=g) * 0.02
+    x = torch.randn(T, H, generator=g)
+    tgt = torch.randint(0, V, (T,), generator=g, dtype=torch.int32)
+    valid = ref.valid_rows(1, T)
+
+    def run():
+        logits = x @ W.t()
+        _, dlogits, _ = ref.cross_entropy(logits, tgt, valid)
+        dlogits @ W
+    med, n = _timed_median(run, min_s)
+    return {"value": round(T / med, 2), "unit": "tokens/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"CPU oracle (PyTorch fp32) lm_head GEMM + fused CE + dX GEMM at T{T}, "
+                       f"V {V}, H {H} (the whole workload): median of {n} calls after 1 "
+                       f"warm-up, {med:.3f} s/call; {torch.get_num_threads()} threads on "
+                       f"{cpu_description()}")}
+
+
+def _timed_median(fn, min_s):
+    """One warm-up call, then calls until about min_s seconds (at least 3, at
+    most 50): the median call time and the number of timed calls."""
+    fn()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < min_s and len(times) < 50):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2], len(times)
+
+
+def measured_traffic(name, key="traffic_bytes_per_launch"):
+    """HBM bytes per launch from a committed rocprofv3 counter summary
+    (profiles/<name>.md, the line `<key>: N`; None if absent)."""
+    f = ROOT / "profiles" / f"{name}.md"
     if not f.exists():
         return None
-    m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", f.read_text())
+    m = re.search(re.escape(key) + r":\s*(\d+)", f.read_text())
     return int(m.group(1)) if m else None
 
 
@@ -262,7 +334,8 @@ def bench_c3(steps, warmup):
                     "head_dim 128, QK-norm, RoPE 1e6",
         "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_F16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
-                     "traffic": None,
+                     "traffic": measured_traffic("attention_c3_traffic",
+                                                 "traffic_bytes_per_call"),
                      "kernel": "attention block (norm/RoPE + flash fwd + flash bwd)"},
     }
 
@@ -303,7 +376,8 @@ def bench_c1(steps, warmup):
         "value": round(T / dt, 2), "unit": "tokens/s", "steps": steps, "warmup": warmup,
         "ms_per_step": round(dt * 1e3, 4), "loss": round(loss, 5),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("head_c1_traffic", "traffic_bytes_per_call"),
                      "algorithmic_bytes": nbytes,
                      "kernel": "logits GEMM + fused CE + dX GEMM (whole call)"},
     }
@@ -319,15 +393,98 @@ def kernel_summary(kinds):
     return {c: round(v, 4) for c, v in cats.items()}
 
 
-def gemm_family(kinds):
-    """The frozen-weight GEMMs of the step as one family: launches, average
-    launch duration, algorithmic weight bytes and FLOPs per launch."""
-    g = [k for k in kinds if k["category"] in ("gemm_fwd", "gemm_bwd", "gemm_lm_head")]
+GEMM_SHAPE = re.compile(r"M(\d+) N(\d+) K(\d+)")
+
+
+def gemm_attainable_us(k):
+    """The roofline time of one GEMM launch: the larger of its MFMA time at
+    the dense fp16 peak and its compulsory HBM time at 8 TB/s (the weights it
+    streams, its fp16 A operand and its fp32 output, M x N x 4)."""
+    M, N, K = (int(x) for x in GEMM_SHAPE.search(k["name"]).groups())
+    hbm = k["bytes"] + M * K * 2 + M * N * 4
+    return max(k["flops"] / (MFMA_F16_PEAK_TFLOPS * 1e12), hbm / (HBM_PEAK_GBS * 1e9)) * 1e6
+
+
+def is_backward_gemm(k):
+    """The dX GEMMs of the backward: the layers' and the lm_head's (K = V)."""
+    if k["category"] == "gemm_bwd":
+        return True
+    m = GEMM_SHAPE.search(k["name"])
+    return k["category"] == "gemm_lm_head" and m and int(m.group(3)) > int(m.group(2))
+
+
+def gemm_family(kinds, pred=None):
+    """A set of the step's frozen-weight GEMMs as one family: launches,
+    average launch duration, algorithmic weight bytes and FLOPs per launch,
+    and the fraction of the attainable roofline (sum of the launches'
+    roofline times over their measured times)."""
+    g = [k for k in kinds if k["category"] in ("gemm_fwd", "gemm_bwd", "gemm_lm_head")
+         and (pred is None or pred(k))]
     n = sum(k["launches"] for k in g)
     t_us = sum(k["us"] * k["launches"] for k in g)
     by = sum(k["bytes"] * k["launches"] for k in g)
     fl = sum(k["flops"] * k["launches"] for k in g)
-    return n, t_us / n, by / n, fl / n
+    att = sum(gemm_attainable_us(k) * k["launches"] for k in g)
+    return n, t_us / n, by / n, fl / n, att / t_us
+
+
+def roofline_obj(cfg, kinds, pred, label):
+    """The roofline object of a GEMM family (see gemm_family)."""
+    n, avg_us, bytes_per_launch, flops_per_launch, att = gemm_family(kinds, pred)
+    gbs = bytes_per_launch / (avg_us * 1e-6) / 1e9
+    tflops = flops_per_launch / (avg_us * 1e-6) / 1e12
+    if cfg == "c2":  # intensity ~T = 128 flop/byte < ridge ~312: HBM-bound
+        bound, ach, peak, unit = "hbm", round(gbs, 1), HBM_PEAK_GBS, "GB/s"
+    else:            # T = 4096: MFMA-bound
+        bound, ach, peak, unit = "mfma", round(tflops, 2), MFMA_F16_PEAK_TFLOPS, "TFLOP/s"
+    sel = [k for k in kinds if k["category"].startswith("gemm") and (pred is None or pred(k))]
+    return {
+        "bound": bound,
+        "kernel": label + " (" + ", ".join(sorted({k["name"].split()[0] for k in sel})) + ")",
+        "achieved": ach, "peak": peak, "unit": unit, "frac": round(ach / peak, 4),
+        "algorithmic_bytes_per_launch": round(bytes_per_launch),
+        "launches_per_step": n,
+        "avg_launch_us": round(avg_us, 3),
+        "weight_gbs": round(gbs, 1),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "gemm_tflops": round(tflops, 2),
+        "mfma_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+        "attainable_frac": round(att, 4),
+    }
+
+
+def kinds_markdown(cfg, kinds):
+    """Every kernel kind of one step as a markdown table: launches, average
+    replayed launch duration, algorithmic work and rate, the bound and the
+    fraction of it (GEMMs also against their attainable roofline time)."""
+    lines = ["| Kind | Category | Launches | Avg us | Step ms | Work / launch | Rate | Bound | "
+             "Frac of peak |", "|---|---|---:|---:|---:|---:|---:|---|---:|"]
+    for k in sorted(kinds, key=lambda k: -k["us"] * k["launches"]):
+        us, step_ms = k["us"], k["us"] * k["launches"] / 1e3
+        if k["category"].startswith("gemm"):
+            gbs = k["bytes"] / (us * 1e-6) / 1e9
+            tf = k["flops"] / (us * 1e-6) / 1e12
+            if cfg == "c2":
+                work, rate = f"{k['bytes'] / 1e6:.2f} MB weights", f"{gbs:.0f} GB/s ({tf:.0f} TFLOP/s)"
+                bound, frac = "HBM", gbs / HBM_PEAK_GBS
+            else:
+                work, rate = f"{k['flops'] / 1e9:.1f} GFLOP", f"{tf:.0f} TFLOP/s"
+                bound, frac = "MFMA", tf / MFMA_F16_PEAK_TFLOPS
+            bound += f"; attainable {gemm_attainable_us(k) / us:.0%}"
+        elif k["flops"] > 0:
+            tf = k["flops"] / (us * 1e-6) / 1e12
+            work, rate, bound, frac = f"{k['flops'] / 1e9:.2f} GFLOP", f"{tf:.0f} TFLOP/s", \
+                "MFMA", tf / MFMA_F16_PEAK_TFLOPS
+        else:
+            gbs = k["bytes"] / (us * 1e-6) / 1e9
+            work, rate, bound, frac = f"{k['bytes'] / 1e6:.2f} MB", f"{gbs:.0f} GB/s", "HBM", \
+                gbs / HBM_PEAK_GBS
+        lines.append(f"| `{k['name']}` | {k['category']} | {k['launches']} | {us:.2f} | "
+                     f"{step_ms:.3f} | {work} | {rate} | {bound} | {frac:.1%} |")
+    total = sum(k["us"] * k["launches"] for k in kinds) / 1e3
+    lines.append(f"\nSum of the kinds: {total:.3f} ms a step, "
+                 f"{sum(k['launches'] for k in kinds)} launches.")
+    return "\n".join(lines)
 
 
 BANDWIDTH_KINDS = ("adamw", "swiglu_bwd", "norm_bwd", "cross_entropy")
@@ -360,7 +517,7 @@ def bandwidth_kernels(kinds):
     return out
 
 
-def bench_step(cfg, steps, warmup, graph=True):
+def bench_step(cfg, steps, warmup, graph=True, kinds_md=False):
     """The LoRA training step of config c2 or c4 through llmt_step (one HIP
     graph launch a step), then llmt_profile_kernels for the per-kernel
     breakdown and the GEMM roofline."""
@@ -402,34 +559,25 @@ def bench_step(cfg, steps, warmup, graph=True):
           flush=True)
     kinds = ctx.profile_kernels(tok, tgt, hp, step, reps=5 if cfg == "c2" else 2)
     ctx.close()
-    n_gemm, avg_us, bytes_per_launch, flops_per_launch = gemm_family(kinds)
-    achieved = bytes_per_launch / (avg_us * 1e-6) / 1e9
-    tflops = flops_per_launch / (avg_us * 1e-6) / 1e12
-    if cfg == "c2":  # intensity ~T = 128 flop/byte < ridge ~312: HBM-bound
-        bound, ach, peak, unit = "hbm", round(achieved, 1), HBM_PEAK_GBS, "GB/s"
-    else:            # T = 4096: MFMA-bound
-        bound, ach, peak, unit = "mfma", round(tflops, 2), MFMA_F16_PEAK_TFLOPS, "TFLOP/s"
-    roofline = {
-        "bound": bound,
-        "kernel": "frozen-weight GEMMs of the step (" + ", ".join(sorted(
-            {k["name"].split()[0] for k in kinds if k["category"].startswith("gemm")})) + ")",
-        "achieved": ach, "peak": peak, "unit": unit, "frac": round(ach / peak, 4),
-        "traffic": measured_traffic() if cfg == "c2" else None,
-        "algorithmic_bytes_per_launch": round(bytes_per_launch),
-        "launches_per_step": n_gemm,
-        "avg_launch_us": round(avg_us, 3),
-        "weight_gbs": round(achieved, 1),
-        "gemm_tflops": round(tflops, 2),
-        "mfma_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
-    }
+    if kinds_md:
+        print(kinds_markdown(cfg, kinds), flush=True)
+    roofline = roofline_obj(cfg, kinds, None, "frozen-weight GEMMs of the step")
+    roofline["traffic"] = measured_traffic(f"gemm_{cfg}_traffic")
+    # the metric's "bwd % MFMA / HBM peak": the backward's dX GEMMs alone
+    roofline_bwd = roofline_obj(cfg, kinds, is_backward_gemm,
+                                "backward dX GEMMs (layers and lm_head)")
+    roofline_bwd["traffic"] = measured_traffic(f"gemm_{cfg}_traffic", "bwd_traffic_bytes_per_launch")
+    bw = bandwidth_kernels(kinds)
+    for name, obj in bw.items():
+        obj["traffic"] = measured_traffic(f"bandwidth_{cfg}_traffic", f"{name}_traffic_bytes")
     ms = dt / steps * 1e3
     return {
         "value": round(T * steps / dt, 2), "ms_per_step": round(ms, 4), "steps": steps,
         "warmup": warmup, "T": T, "batch": batch, "seq_len": seq_len, "workload": workload,
-        "roofline": roofline, "kernels": kernel_summary(kinds),
+        "roofline": roofline, "roofline_bwd": roofline_bwd, "kernels": kernel_summary(kinds),
         "kernels_sum_ms": round(sum(k["us"] * k["launches"] for k in kinds) / 1e3, 4),
         "launches_per_step": sum(k["launches"] for k in kinds),
-        "bandwidth_kernels": bandwidth_kernels(kinds),
+        "bandwidth_kernels": bw,
         "loss_first_last": [round(losses[0], 5), round(losses[-1], 5)],
     }
 
@@ -445,6 +593,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--copy-cal", action="store_true", help="PMC byte-counter calibration")
+    ap.add_argument("--kinds-md", action="store_true",
+                    help="also print the per-kind markdown table of the step (before the line)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {a.gpus}); the multi-GPU "
@@ -457,7 +607,7 @@ def main():
         print(json.dumps(bench_c3(a.steps, a.warmup)), flush=True)
         return
 
-    r = bench_step(a.config, a.steps, a.warmup, graph=not a.no_graph)
+    r = bench_step(a.config, a.steps, a.warmup, graph=not a.no_graph, kinds_md=a.kinds_md)
     out = {
         "metric": METRIC,
         "value": r["value"],
@@ -474,6 +624,7 @@ def main():
         "config": {"workload": r["workload"], "global_batch": r["batch"], "seq_len": r["seq_len"],
                    "tokens_per_step": r["T"], "graph": not a.no_graph},
         "roofline": r["roofline"],
+        "roofline_bwd": r["roofline_bwd"],
         "kernels": r["kernels"],
         "kernels_sum_ms": r["kernels_sum_ms"],
         "launches_per_step": r["launches_per_step"],
@@ -484,7 +635,7 @@ def main():
         # the other headline configurations, measured in the same run
         c4 = bench_step("c4", min(a.steps, 10), 2, graph=not a.no_graph)
         out["c4"] = {k: c4[k] for k in ("workload", "value", "ms_per_step", "steps", "warmup",
-                                        "roofline", "kernels", "kernels_sum_ms",
+                                        "roofline", "roofline_bwd", "kernels", "kernels_sum_ms",
                                         "launches_per_step", "bandwidth_kernels",
                                         "loss_first_last")}
         out["c4"]["unit"] = "tokens/s"
@@ -494,9 +645,9 @@ def main():
     # the C4 GEMM family beside hipBLASLt's fp16 GEMM rate measured in this run
     if "c4" in out:
         blas = out["achievable"]["mfma_f16_tflops_hipblaslt"]
-        out["c4"]["roofline"]["hipblaslt_tflops"] = blas
-        out["c4"]["roofline"]["frac_of_hipblaslt"] = round(
-            out["c4"]["roofline"]["achieved"] / blas, 4)
+        for key in ("roofline", "roofline_bwd"):
+            out["c4"][key]["hipblaslt_tflops"] = blas
+            out["c4"][key]["frac_of_hipblaslt"] = round(out["c4"][key]["achieved"] / blas, 4)
     # each bandwidth kernel beside the device copy rate measured in this run
     copy_gbs = out["achievable"]["hbm_copy_gbs"]
     for obj in (out, out.get("c4", {})):
@@ -508,6 +659,10 @@ def main():
             out["cpu_baseline"] = cpu_baseline(r["batch"], r["seq_len"])
             if "c4" in out:
                 out["c4"]["cpu_baseline"] = cpu_baseline_sampled(8, 512)
+            if "c3" in out:
+                out["c3"]["cpu_baseline"] = cpu_baseline_c3()
+            if "c1" in out:
+                out["c1"]["cpu_baseline"] = cpu_baseline_c1()
         else:
             out["cpu_baseline"] = cpu_baseline_sampled(r["batch"], r["seq_len"])
     print(json.dumps(out), flush=True)
