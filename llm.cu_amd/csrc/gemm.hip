@@ -316,15 +316,26 @@ __device__ __forceinline__ half8 i8x8_to_h8(u32x2 raw) {
   return h - (_Float16)1152.0f;
 }
 
-template <bool I8, bool KS, int S, int WNN, bool GLU = false>
-__global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, int g_order) {
+// TL: a trailing fp16 segment `tail` of at most 64 rows (the LoRA A or B^T
+// rows of a projection, output columns tail_c0 ..) rides along: its 16-row
+// fragment f is computed by the workgroups of column tile f, over their row
+// block and K range (two extra MFMAs a wave per chunk, the fragment's 1 KB
+// a chunk moved by eight lanes of every wave), instead of a separate launch
+// that streamed the whole activation matrix again.
+template <bool I8, bool KS, int S, int WNN, bool GLU = false, bool TL = false>
+__global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, int g_order,
+                                                             const BSeg tail, int tail_c0) {
   // WNN waves across N (2: four waves of 128 x 128; 4: eight waves of 128 x 64)
   constexpr int NW = 2 * WNN, WC = 256 / WNN, NFR = WC / 16;  // wave columns, fragments
   constexpr int FPW = 16 / NW;                                 // A (and B) fragments each wave moves
   constexpr int ABYTES = 256 * KSTEP * 2;
   constexpr int BBYTES = 256 * KSTEP * (I8 ? 1 : 2);
-  constexpr int SBYTES = ABYTES + BBYTES + (KS ? 256 : 0);
-  constexpr int OPS = 2 * FPW + (KS ? 1 : 0);                  // DMA issues per chunk per thread
+  constexpr int KSBYTES = KS ? 256 : 0;
+  constexpr int TOFF = ABYTES + BBYTES + KSBYTES;              // tail fragment slot
+  constexpr int SBYTES = TOFF + (TL ? 1024 : 0);
+  constexpr int OPS = 2 * FPW + (KS ? 1 : 0) + (TL ? 1 : 0);   // DMA issues per chunk per thread
+  static_assert(!(TL && GLU), "no tail with the SwiGLU epilogue");
+  static_assert(!TL || WNN == 4, "the tail fragment is split over four column waves");
   __shared__ __attribute__((aligned(1024))) char smem[S * SBYTES];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -362,6 +373,13 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
     boff[j] = (long long)rb * ksteps * 512 * ES;
   }
   const _Float16* ksrc = KS ? sg.kscale + (wave & 3) * 8 : nullptr;
+  // tail fragment of this column tile (tiles past the last fragment load the
+  // last one, unused, so every wave issues the same number of DMAs)
+  const int ntf = TL ? tail.rows / 16 : 0;
+  const bool has_tail = TL && tn < ntf;
+  const _Float16* tsrc =
+      TL ? (const _Float16*)tail.ptr + (long long)min(tn, ntf - 1) * ksteps * 512 + (wave * 8 + lane) * 8
+         : nullptr;
   auto issue = [&](int c) LLMT_INLINE {
     const int cc = min(c, c1 - 1);
     char* st = smem + (c % S) * SBYTES;
@@ -384,6 +402,9 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
       else if (lane == 0)  // keep the per-thread DMA count uniform (a harmless re-read)
         dma16(ksrc + (long long)cc * KSTEP, reinterpret_cast<_Float16*>(st + ABYTES + BBYTES + 64 + (wave & 3) * 16));
     }
+    if constexpr (TL) {  // wave w moves bytes 128 w .. 128 w + 127 of the fragment
+      if (lane < 8) dma16(tsrc + (long long)cc * 512, reinterpret_cast<_Float16*>(st + TOFF + wave * 128));
+    }
   };
 
   floatx4 acc[8][NFR];
@@ -391,6 +412,8 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
   for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < NFR; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  // tail: this wave's rows 16 (2 wn + j) .. of its 128-row half
+  floatx4 acc_t[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
 
 #pragma unroll
   for (int c = 0; c < S - 1; ++c) issue(c0 + c);
@@ -424,6 +447,16 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
     // 4-5% faster at the C4 shapes)
     __builtin_amdgcn_sched_group_barrier(0x100, NFR + 8, 0);
     __builtin_amdgcn_sched_group_barrier(0x008, 8 * NFR, 0);
+    if constexpr (TL) {
+      if (has_tail) {
+        const half8 bt = *reinterpret_cast<const half8*>(st + TOFF + lane * 16);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const half8 a = *reinterpret_cast<const half8*>(st + (wm * 8 + 2 * wn + j) * 1024 + lane * 16);
+          acc_t[j] = mfma16(a, bt, acc_t[j]);
+        }
+      }
+    }
   }
   wait_vm<0>();
 
@@ -454,6 +487,18 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
         }
       }
     return;
+  }
+  if constexpr (TL) {
+    if (has_tail) {
+      const int col = tail_c0 + tn * 16 + (lane & 15);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int row = m0 + wm * 128 + (2 * wn + j) * 16 + (lane >> 4) * 4 + v;
+          C[(long long)row * g.ldc + col] = acc_t[j][v];
+        }
+    }
   }
   float scj[NFR];
 #pragma unroll
@@ -1025,8 +1070,8 @@ static bool use_big_tiles(const GemmArgs& g) {
 // 49 and 81 us, and the SwiGLU backward read 100 MB of extra partial in
 // 25 us; so N = 6144, K = 2048 runs unsplit in 1.5 waves, 384 tiles, while the
 // 128-tile GEMMs split in two.)
-// A trailing LoRA segment of <= 64 columns runs as its own skinny launch
-// (gemm_nt), so it is left out of the tile count.
+// A trailing LoRA segment of <= 64 columns rides in the main launch (its
+// fragments on the first column tiles' workgroups), so it adds no tiles.
 static int big_split(int M, int N, int K, int max_split) {
   const int nmain = (N % 256 != 0 && N % 64 != 0) ? N - N % 64 : N;
   const int tiles = (nmain + 255) / 256 * (M / BM);
@@ -1125,7 +1170,8 @@ const char* gemm_kernel_name(const GemmArgs& g) {
     const int last = g.nseg - 1;
     if (g.glu) return "gemm_dma_glu";
     if (g.nseg > 1 && g.seg[last].rows <= 64 && g.seg_start[last] % 64 == 0)
-      return "gemm_dma+lora_skinny";
+      return g.seg[last].is_i8 || getenv("LLMT_TAIL_SEPARATE") ? "gemm_dma+lora_skinny"
+                                                                : "gemm_dma+lora";
     return "gemm_dma";
   }
   if (g.glu) return "gemm_skinny_glu";
@@ -1185,23 +1231,36 @@ hipError_t gemm_nt(const GemmArgs& g, hipStream_t st) {
       return hipErrorInvalidValue;
     }
     const dim3 gr(nwg, gm.split);
+    // the LoRA rows fold into the main launch (fragment f with column tile f)
+    // when they are fp16 and no more fragments than column tiles
+    const BSeg tl = lora_tail ? g.seg[last] : BSeg{};
+    const bool fold = lora_tail && !tl.is_i8 && tl.rows / 16 <= (gm.N + 255) / 256 &&
+                      !getenv("LLMT_TAIL_SEPARATE");
+    const int tc0 = lora_tail ? g.seg_start[last] : 0;
     if (gm.glu) {
       if (!i8)
-        hipLaunchKernelGGL((gemm_dma_kernel<false, false, 4, 4, true>), gr, dim3(512), 0, st, gm, order);
+        hipLaunchKernelGGL((gemm_dma_kernel<false, false, 4, 4, true>), gr, dim3(512), 0, st, gm, order, tl, tc0);
       else if (ks)
-        hipLaunchKernelGGL((gemm_dma_kernel<true, true, 5, 4, true>), gr, dim3(512), 0, st, gm, order);
+        hipLaunchKernelGGL((gemm_dma_kernel<true, true, 5, 4, true>), gr, dim3(512), 0, st, gm, order, tl, tc0);
       else
-        hipLaunchKernelGGL((gemm_dma_kernel<true, false, 5, 4, true>), gr, dim3(512), 0, st, gm, order);
+        hipLaunchKernelGGL((gemm_dma_kernel<true, false, 5, 4, true>), gr, dim3(512), 0, st, gm, order, tl, tc0);
+    } else if (fold) {
+      if (!i8)
+        hipLaunchKernelGGL((gemm_dma_kernel<false, false, 4, 4, false, true>), gr, dim3(512), 0, st, gm, order, tl, tc0);
+      else if (ks)
+        hipLaunchKernelGGL((gemm_dma_kernel<true, true, 5, 4, false, true>), gr, dim3(512), 0, st, gm, order, tl, tc0);
+      else
+        hipLaunchKernelGGL((gemm_dma_kernel<true, false, 5, 4, false, true>), gr, dim3(512), 0, st, gm, order, tl, tc0);
     } else {
       if (!i8)
-        hipLaunchKernelGGL((gemm_dma_kernel<false, false, 4, 4>), gr, dim3(512), 0, st, gm, order);
+        hipLaunchKernelGGL((gemm_dma_kernel<false, false, 4, 4>), gr, dim3(512), 0, st, gm, order, tl, tc0);
       else if (ks)
-        hipLaunchKernelGGL((gemm_dma_kernel<true, true, 5, 4>), gr, dim3(512), 0, st, gm, order);
+        hipLaunchKernelGGL((gemm_dma_kernel<true, true, 5, 4>), gr, dim3(512), 0, st, gm, order, tl, tc0);
       else
-        hipLaunchKernelGGL((gemm_dma_kernel<true, false, 5, 4>), gr, dim3(512), 0, st, gm, order);
+        hipLaunchKernelGGL((gemm_dma_kernel<true, false, 5, 4>), gr, dim3(512), 0, st, gm, order, tl, tc0);
     }
     e = hipGetLastError();
-    if (e == hipSuccess && lora_tail) {
+    if (e == hipSuccess && lora_tail && !fold) {
       GemmArgs gl = g;
       gl.nseg = 1;
       gl.seg[0] = g.seg[last];
