@@ -178,7 +178,8 @@ int Ctx::init() {
   for (int b = 1; b <= maxB; ++b) {
     const int M = rows(b);
     for (auto& sh : shapes) {
-      const size_t e = (size_t)gemm_pick_split(M, sh[0], sh[1], 64) * M * sh[0];
+      const int split = gemm_split_col(M, sh[0], sh[1]) ? 2 : gemm_pick_split(M, sh[0], sh[1], 64);
+      const size_t e = (size_t)split * M * sh[0];
       if (e > part_elems) part_elems = e;
     }
   }

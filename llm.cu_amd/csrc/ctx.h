@@ -79,6 +79,7 @@ struct GemmOut {
   int split;
   long long ss;
   int ldp;
+  int split_col;  // GemmArgs::split_col
 };
 
 struct Ctx {
@@ -214,10 +215,13 @@ struct Ctx {
   // up] fp16 [M, N] to gu16 and fp16(silu(gate) * up) [M, N / 2] to glu16
   // (direct and ldc unused).
   // rowstats (direct only): also the per-(row, column tile) softmax pairs
-  // (GemmArgs::rowstats); *tiles gets their row width.
+  // (GemmArgs::rowstats); *tiles gets their row width.  last_wave_split:
+  // the consumer reads the partials through load_row, so an unsplit
+  // large-tile GEMM may split only its last wave (gemm_split_col).
   hipError_t gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int nseg, int M, int K,
                   float* direct, int ldc, GemmOut* out, _Float16* glu16 = nullptr,
-                  _Float16* gu16 = nullptr, float2* rowstats = nullptr, int* tiles = nullptr);
+                  _Float16* gu16 = nullptr, float2* rowstats = nullptr, int* tiles = nullptr,
+                  bool last_wave_split = false);
   // A GEMM's partials as a row-epilogue input with raw h columns
   // [hcol, hcol + nh) and LoRA up-projection terms.
   RowIn row_in(const GemmOut& go, int hcol = 0, int nh = 0, int nterm = 0,

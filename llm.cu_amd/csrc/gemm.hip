@@ -340,19 +340,37 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WNN, wn = wave % WNN;
-  const int ntn = (g.N + 255) / 256, ntm = g.M / 256, nwg = ntn * ntm;
-  int t = blockIdx.x;
+  const int ntn = (g.N + 255) / 256, ntm = g.M / 256;
+  int t = blockIdx.x, sidx = blockIdx.y, nsp = g.split, tn0 = 0, ntn_r = ntn;
+  if (g.split_col > 0) {
+    // column tiles [0, ntc) unsplit (workgroups 0 .. ntc ntm - 1), then the
+    // rest split in two over K (split 0 of every such tile, then split 1)
+    const int ntc = g.split_col / 256, nfull = ntc * ntm;
+    if (t < nfull) {
+      nsp = 1;
+      sidx = 0;
+      ntn_r = ntc;
+    } else {
+      t -= nfull;
+      nsp = 2;
+      tn0 = ntc;
+      ntn_r = ntn - ntc;
+      sidx = t / (ntn_r * ntm);
+      t -= sidx * (ntn_r * ntm);
+    }
+  }
+  const int nwg = ntn_r * ntm;
   if (g_order >= 1 && nwg % 8 == 0) t = (t % 8) * (nwg / 8) + t / 8;
   // Consecutive t of one XCD walk GM row blocks per column step, so the 32
   // tiles an XCD runs at once share 4 A row blocks and 8 B column blocks in
   // its L2 (not 1 and 32): the logits GEMM 3.05 -> 2.88 ms at C4.
   const int GM = ntm % 4 == 0 ? 4 : ntm % 2 == 0 ? 2 : 1;
-  const int grp = t / (GM * ntn), tr = t % (GM * ntn);
-  const int tm = grp * GM + tr % GM, tn = tr / GM;
+  const int grp = t / (GM * ntn_r), tr = t % (GM * ntn_r);
+  const int tm = grp * GM + tr % GM, tn = tn0 + tr / GM;
   const int n0 = tn * 256, m0 = tm * 256;
   const int ksteps = g.K / KSTEP;
-  const int c0 = (int)((long long)blockIdx.y * ksteps / g.split);
-  const int c1 = (int)((long long)(blockIdx.y + 1) * ksteps / g.split);
+  const int c0 = (int)((long long)sidx * ksteps / nsp);
+  const int c1 = (int)((long long)(sidx + 1) * ksteps / nsp);
 
   // issue pointers: wave w moves A fragments FPW w .. and B fragments FPW w ..
   // of every chunk (plus, with KS, k-scales through lane 0 of waves 0-3)
@@ -460,7 +478,7 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
   }
   wait_vm<0>();
 
-  float* C = g.C + (long long)blockIdx.y * g.split_stride;
+  float* C = g.C + (long long)sidx * g.split_stride;
   const _Float16* cs = sg.colscale;
   if constexpr (GLU) {
     float sgu[NFR];
@@ -1102,6 +1120,21 @@ bool gemm_glu_ok(int M, int I, int K, bool i8) {
   return !i8 && skinny_ok(M, 2 * I, K) && I % 32 == 0;
 }
 
+// The last wave of an unsplit large-tile GEMM: with tiles = full waves of
+// the 256 CUs plus r more (r <= 128, whole column tiles), the last r tiles
+// run as 2 r half-K workgroups, so the launch takes 1 + 1/2 wave-times of a
+// tile instead of 2 (C4's down-projection dX: 384 tiles).  Their partial
+// is an extra fp32 [M, r/ntm x 256] the consumer reads back.
+int gemm_split_col(int M, int N, int K) {
+  if (!big_tiles(M, K) || N % 256 || big_split(M, N, K, 64) != 1 ||
+      K / (BCH * KSTEP) < 8 || getenv("LLMT_NO_SPLIT_COL"))
+    return 0;
+  const int ntm = M / BM, ntn = N / 256, tiles = ntm * ntn;
+  const int rest = tiles % 256;
+  if (tiles < 256 || rest == 0 || rest > 128 || rest % ntm) return 0;
+  return (ntn - rest / ntm) * 256;
+}
+
 int gemm_pick_split(int M, int N, int K, int max_split) {
   if (big_tiles(M, K)) return big_split(M, N, K, max_split);
   if (skinny_ok(M, N, K)) {
@@ -1199,6 +1232,10 @@ hipError_t gemm_nt(const GemmArgs& g, hipStream_t st) {
     set_error("gemm_nt: SwiGLU epilogue needs split 1, one segment, N = 2 x %d", g.glu);
     return hipErrorInvalidValue;
   }
+  if (g.split_col && !use_big_tiles(g)) {
+    set_error("gemm_nt: split_col needs the large-tile kernel");
+    return hipErrorInvalidValue;
+  }
   if (g.rowstats && gemm_rowstats_tiles(g) == 0) {
     set_error("gemm_nt: row statistics need split 1, one segment and no SwiGLU epilogue");
     return hipErrorInvalidValue;
@@ -1230,7 +1267,16 @@ hipError_t gemm_nt(const GemmArgs& g, hipStream_t st) {
                 gm.N, gm.nseg);
       return hipErrorInvalidValue;
     }
-    const dim3 gr(nwg, gm.split);
+    if (gm.split_col > 0 &&
+        (gm.split != 2 || gm.split_col % 256 || gm.split_col >= gm.N || gm.N % 256 || gm.glu ||
+         gm.rowstats || lora_tail)) {
+      set_error("gemm_nt: split_col %d needs split 2 and whole 256-column tiles (N = %d)",
+                gm.split_col, gm.N);
+      return hipErrorInvalidValue;
+    }
+    const dim3 gr = gm.split_col > 0
+                        ? dim3(gm.split_col / 256 * (gm.M / BM) + 2 * (gm.N - gm.split_col) / 256 * (gm.M / BM), 1)
+                        : dim3(nwg, gm.split);
     // the LoRA rows fold into the main launch (fragment f with column tile f)
     // when they are fp16 and no more fragments than column tiles
     const BSeg tl = lora_tail ? g.seg[last] : BSeg{};

@@ -32,6 +32,10 @@ struct GemmArgs {
   int ldc;
   long long split_stride;  // elements between split partials
   int M, N, K, split;
+  // split_col > 0 (large tiles, split 2): only the column tiles at or past
+  // split_col are split over K; the others write their whole sum to partial
+  // 0 and leave partial 1 untouched (gemm_split_col).
+  int split_col;
   // glu > 0: fused SwiGLU epilogue (split 1, N = 2 glu, one segment whose
   // rows [0, glu) are the gate and [glu, 2 glu) the up projection): gu16
   // gets [gate | up] in fp16 ([M, 2 glu], the backward's stash; C unused)
@@ -59,6 +63,11 @@ int gemm_rowstats_tiles(const GemmArgs& g);
 void gemm_finalize_segments(GemmArgs& g);
 // Split factor for a GEMM of this shape on this device (>=1, bounded by K).
 int gemm_pick_split(int M, int N, int K, int max_split);
+// For a large-tile GEMM planned unsplit whose 256 x 256 tiles end in a
+// partial wave of the CUs: the column where tiles start to be split in two
+// so that the last wave is full (GemmArgs::split_col, with split 2); 0 when
+// the tiles fill whole waves or the shape does not allow it.
+int gemm_split_col(int M, int N, int K);
 hipError_t gemm_nt(const GemmArgs& g, hipStream_t st);
 // Name of the kernel gemm_nt launches for g ("gemm_skinny", "gemm_dma", ...).
 const char* gemm_kernel_name(const GemmArgs& g);
@@ -142,6 +151,7 @@ struct RowIn {
   int split;
   long long ss;
   int ldp;
+  int split_col;  // > 0: columns below it have only partial 0 (GemmArgs::split_col)
   int hcol, nh;  // nh % 4 == 0, nh <= 64 (0: none)
   int nterm;     // <= 3
   LoraTerm term[3];

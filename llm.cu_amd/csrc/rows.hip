@@ -76,7 +76,9 @@ __device__ __forceinline__ float4 sum_splits4(const float* p, int split, long lo
 // group 0's).  One loop for both, with up to 24 loads in flight per batch
 // and branch-free in-order adds, so a row costs one memory round trip per
 // batch of splits.
-template <int P, bool HH, int LOADS = 24>
+// SC: the input may carry RowIn::split_col (only kernels instantiated with
+// it accept such inputs; row_in_ok).
+template <int P, bool HH, int LOADS = 24, bool SC = false>
 __device__ __forceinline__ void load_row(const RowIn& in, int t, int n, float4 (&v)[P], float4& h) {
   const float* prow = in.part + (long long)t * in.ldp;
   int off[P];
@@ -88,6 +90,19 @@ __device__ __forceinline__ void load_row(const RowIn& in, int t, int n, float4 (
   }
   const int hoff = in.hcol + 4 * ((int)threadIdx.x < in.nh / 4 ? (int)threadIdx.x : 0);
   if (HH) h = ld4(prow + hoff);
+  if constexpr (SC) {
+    // two partials, the second one only for columns at or past split_col
+    // (GemmArgs::split_col; a piece's 64 lanes cover 256 columns and
+    // split_col is a multiple of 256, so the condition is uniform over a
+    // wave).  Kept apart from the general loop below, whose register use it
+    // would otherwise raise.
+    const float* q = prow + in.ss;
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+      if (off[p] >= in.split_col) v[p] = add4(v[p], ld4(q + off[p]));
+    if (HH) h = add4(h, ld4(q + hoff));
+    return;
+  }
   constexpr int SB = LOADS / (P + (HH ? 1 : 0));
   for (int k = 1; k < in.split; k += SB) {
     float4 x[SB][P], y[SB];
@@ -108,10 +123,10 @@ __device__ __forceinline__ void load_row(const RowIn& in, int t, int n, float4 (
   }
 }
 
-template <int P>
+template <int P, bool SC = false>
 __device__ __forceinline__ void load_partials(const RowIn& in, int t, int n, float4 (&v)[P]) {
   float4 h;
-  load_row<P, false>(in, t, n, v, h);
+  load_row<P, false, 24, SC>(in, t, n, v, h);
 }
 
 __device__ __forceinline__ void store_h(const RowIn& in, float4 h, float* hs) {
@@ -872,7 +887,7 @@ __global__ __launch_bounds__(RT) void norm_bwd_rows_kernel(const NormBwdArgs a, 
 // dX of the down projection -> SwiGLU backward (src/kernels/activation.cu:
 // 26-43 with d_up = dy * silu(g), i.e. without the reference's aliasing of
 // d_gate and d_swiglu at src/kernels/lora_backward.cu:287) -> [dg | du] fp16.
-template <int P>
+template <int P, bool SC = false>
 __global__ __launch_bounds__(RT) void swiglu_bwd_kernel(const RowIn in,
                                                         const float* __restrict__ rinv_in,
                                                         const _Float16* __restrict__ gu, int I,
@@ -890,7 +905,7 @@ __global__ __launch_bounds__(RT) void swiglu_bwd_kernel(const RowIn in,
   }
   const float rs = rinv_in[t];
   float4 v[P];
-  load_partials<P>(in, t, I, v);
+  load_partials<P, SC>(in, t, I, v);
   float4 dg[P], du[P];
   float amax = 0.f;
 #pragma unroll
@@ -1239,10 +1254,13 @@ static int rows_per_wg(int T, int P, int large_t, int small_t = 1) {
   return T >= 2048 ? large_t : small_t;
 }
 
-static bool row_in_ok(const RowIn& in, int n, const char* who) {
+// split_col_ok: the kernel reads its partials through load_row, which alone
+// honours RowIn::split_col.
+static bool row_in_ok(const RowIn& in, int n, const char* who, bool split_col_ok = false) {
   bool ok = in.nh % 4 == 0 && in.nh >= 0 && in.nh <= 64 && in.nterm >= 0 && in.nterm <= 3 &&
             n % 4 == 0 && in.ldp % 4 == 0 && in.split >= 1 && (in.split == 1 || in.ss % 4 == 0) &&
-            in.hcol % 4 == 0;
+            in.hcol % 4 == 0 && in.split_col >= 0 && in.split_col % 4 == 0 &&
+            (in.split_col == 0 || split_col_ok);
   for (int q = 0; q < in.nterm && ok; ++q)
     ok = in.term[q].c0 % 4 == 0 && in.term[q].n % 4 == 0 && in.term[q].hidx + R <= in.nh;
   if (!ok) set_error("%s: unsupported row-input layout (n=%d nh=%d nterm=%d)", who, n, in.nh, in.nterm);
@@ -1446,13 +1464,25 @@ hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st) {
 
 hipError_t swiglu_bwd(const RowIn& in, const float* rinv_in, const _Float16* gu, int I, int T,
                       _Float16* dgu16, float* rinv_out, hipStream_t st) {
-  if (!row_in_ok(in, I, "swiglu_bwd")) return hipErrorInvalidValue;
+  if (!row_in_ok(in, I, "swiglu_bwd", true)) return hipErrorInvalidValue;
   const int P = (I + 4 * RT - 1) / (4 * RT);
-  switch (P) {
-    case 1: hipLaunchKernelGGL(swiglu_bwd_kernel<1>, dim3(T), dim3(RT), 0, st, in, rinv_in, gu, I, dgu16, rinv_out); break;
-    case 2: hipLaunchKernelGGL(swiglu_bwd_kernel<2>, dim3(T), dim3(RT), 0, st, in, rinv_in, gu, I, dgu16, rinv_out); break;
-    case 3: hipLaunchKernelGGL(swiglu_bwd_kernel<3>, dim3(T), dim3(RT), 0, st, in, rinv_in, gu, I, dgu16, rinv_out); break;
-    case 4: hipLaunchKernelGGL(swiglu_bwd_kernel<4>, dim3(T), dim3(RT), 0, st, in, rinv_in, gu, I, dgu16, rinv_out); break;
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(T), dim3(RT), 0, st, in, rinv_in, gu, I, dgu16, rinv_out);
+  };
+  const bool sc = in.split_col > 0;
+  if (sc && in.split != 2) {
+    set_error("swiglu_bwd: a split_col input has two partials (got %d)", in.split);
+    return hipErrorInvalidValue;
+  }
+  switch (P * 2 + (sc ? 1 : 0)) {
+    case 2: go(swiglu_bwd_kernel<1>); break;
+    case 3: go(swiglu_bwd_kernel<1, true>); break;
+    case 4: go(swiglu_bwd_kernel<2>); break;
+    case 5: go(swiglu_bwd_kernel<2, true>); break;
+    case 6: go(swiglu_bwd_kernel<3>); break;
+    case 7: go(swiglu_bwd_kernel<3, true>); break;
+    case 8: go(swiglu_bwd_kernel<4>); break;
+    case 9: go(swiglu_bwd_kernel<4, true>); break;
     default:
       set_error("swiglu_bwd: row width %d above %d", I, 16 * RT);
       return hipErrorInvalidValue;

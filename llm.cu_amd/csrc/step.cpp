@@ -77,7 +77,7 @@ Ctx::~Ctx() {
 
 hipError_t Ctx::gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int nseg, int M, int K,
                      float* direct, int ldc, GemmOut* out, _Float16* glu16, _Float16* gu16,
-                     float2* rowstats, int* tiles) {
+                     float2* rowstats, int* tiles, bool last_wave_split) {
   GemmArgs g{};
   g.A = A;
   g.lda = lda;
@@ -111,6 +111,10 @@ hipError_t Ctx::gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int 
     }
   } else {
     g.split = gemm_pick_split(M, g.N, K, 64);
+    if (last_wave_split && nseg == 1 && g.split == 1) {
+      g.split_col = gemm_split_col(M, g.N, K);
+      if (g.split_col) g.split = 2;
+    }
     g.C = part;
     g.ldc = g.N;
     g.split_stride = (long long)M * g.N;
@@ -134,6 +138,7 @@ hipError_t Ctx::gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int 
   out->split = g.split;
   out->ss = g.split_stride;
   out->ldp = g.ldc;
+  out->split_col = g.split_col;
   return hipSuccess;
 }
 
@@ -143,6 +148,7 @@ RowIn Ctx::row_in(const GemmOut& go, int hcol, int nh, int nterm, const LoraTerm
   r.split = go.split;
   r.ss = go.ss;
   r.ldp = go.ldp;
+  r.split_col = go.split_col;
   r.hcol = hcol;
   r.nh = nh;
   r.nterm = nterm;
@@ -154,6 +160,7 @@ RowIn Ctx::row_in(const GemmOut& go, int hcol, int nh, int nterm, const LoraTerm
 // Bytes a row epilogue reads from a GEMM's split partials: split x T rows of
 // n columns plus the raw h columns.
 static double part_bytes(const RowIn& r, int T, int n) {
+  if (r.split_col > 0) return 4.0 * (double)T * (n + (n - r.split_col) + r.nh);
   return 4.0 * r.split * (double)T * (n + r.nh);
 }
 
@@ -419,7 +426,8 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   _Float16* const qg16 = gq16(l);  // q/k/v projections upstream gradient (row factor rq)
   // MLP: down dX -> SwiGLU bwd -> gate/up dX -> FFN norm bwd (+ residual)
   BSeg sd[1] = {wseg(w.wdT)};
-  LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, sd, 1, T, H, nullptr, 0, &go_));
+  LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, sd, 1, T, H, nullptr, 0, &go_, nullptr, nullptr, nullptr,
+                    nullptr, true));
   {
     const RowIn ri = row_in(go_);
     const float* ri_in = rinv;
