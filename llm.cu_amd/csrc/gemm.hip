@@ -567,7 +567,7 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
 
 // Skinny fp16 kernel fed by DMA (the T = 128 training step): a 128 x BN
 // output tile (BN = 16 NB) per workgroup of eight waves, K split over
-// blockIdx.y in 64-wide stages.  Wave w = 4 kg + wr computes rows
+// blockIdx.x (the fastest grid index) in 64-wide stages.  Wave w = 4 kg + wr computes rows
 // 32 wr .. 32 wr + 31 x all BN columns over k half kg (32 of the 64) of
 // every stage, so each SIMD runs two waves whose LDS reads and MFMAs
 // interleave; the two halves' sums meet in LDS at the end (kg 1 hands its
@@ -612,11 +612,17 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(const GemmArgs g) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wr = wave & 3, kg = wave >> 2;
-  const int n0 = blockIdx.x * (NB * 16), m0 = blockIdx.z * 128;
+  // grid = (split, column tile, row tile): the split is the fastest index,
+  // so workgroup b (on XCD b % 8) of split s reads A's K slice s, and that
+  // slice reaches only the XCDs running split s (one of eight at split 8 or
+  // 16) instead of every XCD's L2 -- the lm_head dX at C2 had fetched its
+  // 39 MB A operand eight times over
+  const int ct = blockIdx.y, sp = blockIdx.x;
+  const int n0 = ct * (NB * 16), m0 = blockIdx.z * 128;
   const int ksteps = g.K / KSTEP;
   const int nst = g.K / 64;
-  const int c0 = (int)((long long)blockIdx.y * nst / g.split);
-  const int c1 = (int)((long long)(blockIdx.y + 1) * nst / g.split);
+  const int c0 = (int)((long long)sp * nst / g.split);
+  const int c1 = (int)((long long)(sp + 1) * nst / g.split);
 
   // A: wave w moves rows 16 w .. 16 w + 15 (two 1 KB pieces of 8 rows)
   const __amdgpu_buffer_rsrc_t ars =
@@ -633,7 +639,7 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(const GemmArgs g) {
   for (int i = 0; i < BPW; ++i) {
     if constexpr (GLU) {
       const int f = min(wr + 4 * i, NB - 1);
-      const long long rb = (f & 1) * (g.glu >> 4) + (long long)blockIdx.x * (NB / 2) + (f >> 1);
+      const long long rb = (f & 1) * (g.glu >> 4) + (long long)ct * (NB / 2) + (f >> 1);
       brs[i] = make_rsrc((const _Float16*)g.seg[0].ptr + rb * ksteps * 512, (unsigned)(ksteps * 1024u));
       continue;
     }
@@ -721,12 +727,12 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(const GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) acc[i][j] += xch[(i * NB + j) * 64 + lane];
 
-  float* C = g.C + (long long)blockIdx.y * g.split_stride;
+  float* C = g.C + (long long)sp * g.split_stride;
   if constexpr (GLU) {
     const _Float16* cs = g.seg[0].colscale;
 #pragma unroll
     for (int jj = 0; jj < NB / 2; ++jj) {
-      const int col = (blockIdx.x * (NB / 2) + jj) * 16 + (lane & 15);
+      const int col = (ct * (NB / 2) + jj) * 16 + (lane & 15);
       const float sg = cs ? (float)cs[col] : 1.0f, su = cs ? (float)cs[g.glu + col] : 1.0f;
 #pragma unroll
       for (int i = 0; i < 2; ++i)
@@ -1163,7 +1169,7 @@ constexpr bool skinny_fits = S * (16384 + NB * 2048) <= 160 * 1024;
 
 template <int S>
 static void launch_skinny(const GemmArgs& g, int nb, hipStream_t st) {
-  const dim3 grid((g.N + nb * 16 - 1) / (nb * 16), g.split, g.M / 128);
+  const dim3 grid(g.split, (g.N + nb * 16 - 1) / (nb * 16), g.M / 128);
   switch (nb) {
     case 2: hipLaunchKernelGGL((gemm_skinny_kernel<S, 2>), grid, dim3(512), 0, st, g); break;
     case 3: hipLaunchKernelGGL((gemm_skinny_kernel<S, 3>), grid, dim3(512), 0, st, g); break;
@@ -1241,7 +1247,7 @@ hipError_t gemm_nt(const GemmArgs& g, hipStream_t st) {
     return hipErrorInvalidValue;
   }
   if (g.glu && !use_big_tiles(g)) {
-    hipLaunchKernelGGL((gemm_skinny_kernel<4, 4, true>), dim3(g.glu / 32, 1, g.M / 128), dim3(512),
+    hipLaunchKernelGGL((gemm_skinny_kernel<4, 4, true>), dim3(1, g.glu / 32, g.M / 128), dim3(512),
                        0, st, g);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) set_error("gemm_nt launch: %s", hipGetErrorString(e));
