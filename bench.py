@@ -6,7 +6,7 @@ seq 128, token ids uniform over the vocabulary, next-token targets.  The step
 runs as one captured HIP graph of libllmt.so kernels (llmt_step); inputs are
 resident in HBM before the timed region.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c3|c4] [--only] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c1|c2|c3|c4] [--only] [--no-cpu]
     python bench.py --copy-cal      # plain 512 MiB copies (PMC byte-counter scale)
 
 Prints ONE JSON line.  Besides the contract fields it carries
@@ -37,7 +37,7 @@ Prints ONE JSON line.  Besides the contract fields it carries
                 measured in the same run; the C4 GEMM roofline also as
                 frac_of_hipblaslt, against the 8192^3 fp16 hipBLASLt GEMM
                 of the same run (achievable.mfma_f16_tflops_hipblaslt).
---config c3 / c4 --only times one of those alone; --kinds-md also prints the
+--config c1 / c3 / c4 --only times one of those alone; --kinds-md also prints the
 per-kind markdown table of the step (the profiles/ kind tables).
 """
 from __future__ import annotations
@@ -587,7 +587,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", choices=["c2", "c3", "c4"], default="c2")
+    ap.add_argument("--config", choices=["c1", "c2", "c3", "c4"], default="c2")
     ap.add_argument("--only", action="store_true",
                     help="the selected config alone (no c3 / c4 sub-objects in the c2 line)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
@@ -603,8 +603,11 @@ def main():
     if a.copy_cal:
         copy_calibration()
         return
-    if a.config == "c3":
-        print(json.dumps(bench_c3(a.steps, a.warmup)), flush=True)
+    if a.config in ("c3", "c1"):
+        r = (bench_c3 if a.config == "c3" else bench_c1)(a.steps, a.warmup)
+        if not a.no_cpu:
+            r["cpu_baseline"] = (cpu_baseline_c3 if a.config == "c3" else cpu_baseline_c1)()
+        print(json.dumps(r), flush=True)
         return
 
     r = bench_step(a.config, a.steps, a.warmup, graph=not a.no_graph, kinds_md=a.kinds_md)
