@@ -636,7 +636,8 @@ def main():
     }
     if a.config == "c2" and not a.only:
         # the other headline configurations, measured in the same run
-        c4 = bench_step("c4", min(a.steps, 10), 2, graph=not a.no_graph)
+        c4 = bench_step("c4", min(a.steps, 10), 2, graph=not a.no_graph,
+                        kinds_md=a.kinds_md)
         out["c4"] = {k: c4[k] for k in ("workload", "value", "ms_per_step", "steps", "warmup",
                                         "roofline", "roofline_bwd", "kernels", "kernels_sum_ms",
                                         "launches_per_step", "bandwidth_kernels",

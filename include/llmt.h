@@ -292,7 +292,8 @@ int llmt_adamw(llmt_ctx* ctx, const llmt_hparams* hp, int step);
 /* Per-kernel timing of one llmt_step (no counterpart in the reference).  The
  * step (forward, CE, backward, AdamW: the adapters advance by this one step)
  * runs once eagerly with every kernel launch recorded; then the launches of
- * each kind (one kernel at one shape) are replayed back to back, `reps`
+ * each kind (one kernel at one shape; a backward dX GEMM's name ends in
+ * " dX") are replayed back to back, `reps`
  * times, as a HIP graph of their own and timed with HIP events on the
  * context's stream, so no events sit between kernels and no dependent-launch
  * gaps are counted (the kinds' totals sum to less than a step).  The

@@ -126,9 +126,12 @@ hipError_t Ctx::gemm(int cat, const _Float16* A, int lda, const BSeg* segs, int 
   if (recording) {
     double wbytes = 0;
     for (int i = 0; i < nseg; ++i) wbytes += (double)segs[i].rows * K * (segs[i].is_i8 ? 1 : 2);
+    // the backward's dX GEMMs are kinds of their own (the O projection's dX
+    // has the forward's shape)
+    const bool dx = cat == CAT_GEMM_BWD || (cat == CAT_GEMM_HEAD && !direct);
     char kind[128];
-    snprintf(kind, sizeof kind, "%s M%d N%d K%d split%d%s", gemm_kernel_name(g), M, g.N, K,
-             g.split, segs[0].is_i8 ? " int8" : "");
+    snprintf(kind, sizeof kind, "%s M%d N%d K%d split%d%s%s", gemm_kernel_name(g), M, g.N, K,
+             g.split, segs[0].is_i8 ? " int8" : "", dx ? " dX" : "");
     launches.push_back({cat, kind, [g](hipStream_t s) { return gemm_nt(g, s); },
                         2.0 * M * g.N * K, wbytes});
   }

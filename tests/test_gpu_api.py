@@ -150,6 +150,11 @@ def test_profile_kernels_contract(prob, dev):
     for k in kinds:   # every kind carries its algorithmic work
         assert k["flops"] > 0 or k["bytes"] > 0, k["name"]
     assert gemms == 8 * L + 2       # 4 forward + 4 backward GEMMs a layer, logits, head dX
+    per_cat = {}
+    for k in kinds:
+        per_cat[k["category"]] = per_cat.get(k["category"], 0) + k["launches"]
+    assert per_cat["gemm_fwd"] == 4 * L and per_cat["gemm_bwd"] == 4 * L
+    assert sum(k["launches"] for k in kinds if k["name"].endswith(" dX")) == 4 * L + 1
 
 
 def test_lm_head_retied_by_set_embed(prob, dev, tmp_path):
