@@ -1133,7 +1133,7 @@ bool gemm_glu_ok(int M, int I, int K, bool i8) {
 // is an extra fp32 [M, r/ntm x 256] the consumer reads back.
 int gemm_split_col(int M, int N, int K) {
   if (!big_tiles(M, K) || N % 256 || big_split(M, N, K, 64) != 1 ||
-      K / (BCH * KSTEP) < 8 || getenv("LLMT_NO_SPLIT_COL"))
+      K / (BCH * KSTEP) < 8)
     return 0;
   const int ntm = M / BM, ntn = N / 256, tiles = ntm * ntn;
   const int rest = tiles % 256;
@@ -1209,8 +1209,9 @@ const char* gemm_kernel_name(const GemmArgs& g) {
     const int last = g.nseg - 1;
     if (g.glu) return "gemm_dma_glu";
     if (g.nseg > 1 && g.seg[last].rows <= 64 && g.seg_start[last] % 64 == 0)
-      return g.seg[last].is_i8 || getenv("LLMT_TAIL_SEPARATE") ? "gemm_dma+lora_skinny"
-                                                                : "gemm_dma+lora";
+      return g.seg[last].is_i8 || g.seg[last].rows / 16 > (g.N - g.seg[last].rows + 255) / 256
+                 ? "gemm_dma+lora_skinny"
+                 : "gemm_dma+lora";
     return "gemm_dma";
   }
   if (g.glu) return "gemm_skinny_glu";
@@ -1286,8 +1287,7 @@ hipError_t gemm_nt(const GemmArgs& g, hipStream_t st) {
     // the LoRA rows fold into the main launch (fragment f with column tile f)
     // when they are fp16 and no more fragments than column tiles
     const BSeg tl = lora_tail ? g.seg[last] : BSeg{};
-    const bool fold = lora_tail && !tl.is_i8 && tl.rows / 16 <= (gm.N + 255) / 256 &&
-                      !getenv("LLMT_TAIL_SEPARATE");
+    const bool fold = lora_tail && !tl.is_i8 && tl.rows / 16 <= (gm.N + 255) / 256;
     const int tc0 = lora_tail ? g.seg_start[last] : 0;
     if (gm.glu) {
       if (!i8)
