@@ -322,7 +322,7 @@ __device__ __forceinline__ half8 i8x8_to_h8(u32x2 raw) {
 // block and K range (two extra MFMAs a wave per chunk, the fragment's 1 KB
 // a chunk moved by eight lanes of every wave), instead of a separate launch
 // that streamed the whole activation matrix again.
-template <bool I8, bool KS, int S, int WNN, bool GLU = false, bool TL = false>
+template <bool I8, bool KS, int S, int WNN, bool GLU = false, bool TL = false, bool PF = false>
 __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, int g_order,
                                                              const BSeg tail, int tail_c0) {
   // WNN waves across N (2: four waves of 128 x 128; 4: eight waves of 128 x 64)
@@ -433,6 +433,75 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
   // tail: this wave's rows 16 (2 wn + j) .. of its 128-row half
   floatx4 acc_t[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
 
+  if constexpr (PF) {
+    // Fragments one chunk ahead: after the barrier that publishes chunk
+    // c + 1, each A fragment register of chunk c is refilled from chunk c + 1
+    // right after its last MFMA, and chunk c + 1's B bytes (and k-scales,
+    // tail fragment) are read at the top, dequantised after the last MFMA;
+    // so LDS latency sits under the MFMAs and the registers stay one set.
+    half8 a[8], b[NFR], bt, btn, ksn;
+    u32x2 bn8[NFR];
+    half8 bn16[NFR];
+    auto read_b = [&](const char* st) LLMT_INLINE {
+      if constexpr (KS) ksn = *reinterpret_cast<const half8*>(st + ABYTES + BBYTES + (lane >> 4) * 16);
+#pragma unroll
+      for (int j = 0; j < NFR; ++j) {
+        const int fr = wn * NFR + j;
+        if constexpr (I8)
+          bn8[j] = *reinterpret_cast<const u32x2*>(st + ABYTES + fr * 512 + lane * 8);
+        else
+          bn16[j] = *reinterpret_cast<const half8*>(st + ABYTES + fr * 1024 + lane * 16);
+      }
+      if constexpr (TL) btn = *reinterpret_cast<const half8*>(st + TOFF + lane * 16);
+    };
+    auto take_b = [&]() LLMT_INLINE {
+#pragma unroll
+      for (int j = 0; j < NFR; ++j) {
+        if constexpr (I8) {
+          b[j] = i8x8_to_h8(bn8[j]);
+          if constexpr (KS) b[j] = b[j] * ksn;
+        } else {
+          b[j] = bn16[j];
+        }
+      }
+      if constexpr (TL) bt = btn;
+    };
+    auto read_a = [&](const char* st, int i) LLMT_INLINE {
+      a[i] = *reinterpret_cast<const half8*>(st + (wm * 8 + i) * 1024 + lane * 16);
+    };
+#pragma unroll
+    for (int c = 0; c < S; ++c) issue(c0 + c);
+    static_assert((S - 1) * OPS < 64, "vmcnt range");
+    wait_vm<(S - 1) * OPS>();
+    __builtin_amdgcn_s_barrier();
+    {
+      const char* st = smem + (c0 % S) * SBYTES;
+      read_b(st);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) read_a(st, i);
+      take_b();
+    }
+    for (int c = c0; c < c1; ++c) {
+      // vmcnt: chunk c + 1 landed; lgkmcnt 0: this wave's reads of chunk c
+      // returned, so after the barrier chunk c's slot takes chunk c + S
+      constexpr int N = (S - 2) * OPS;
+      __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+      __builtin_amdgcn_s_barrier();
+      issue(c + S);
+      const char* st = smem + ((c + 1) % S) * SBYTES;
+      read_b(st);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int j = 0; j < NFR; ++j) acc[i][j] = mfma16(a[i], b[j], acc[i][j]);
+        if constexpr (TL) {
+          if (has_tail && (i >> 1) == wn) acc_t[i & 1] = mfma16(a[i], bt, acc_t[i & 1]);
+        }
+        read_a(st, i);
+      }
+      take_b();
+    }
+  } else {
 #pragma unroll
   for (int c = 0; c < S - 1; ++c) issue(c0 + c);
   for (int c = c0; c < c1; ++c) {
@@ -475,6 +544,7 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
         }
       }
     }
+  }
   }
   wait_vm<0>();
 
@@ -1289,27 +1359,31 @@ hipError_t gemm_nt(const GemmArgs& g, hipStream_t st) {
     const BSeg tl = lora_tail ? g.seg[last] : BSeg{};
     const bool fold = lora_tail && !tl.is_i8 && tl.rows / 16 <= (gm.N + 255) / 256;
     const int tc0 = lora_tail ? g.seg_start[last] : 0;
+    // ring depth 5 (int8) / 4 (fp16): 4 measured the same, 6 slower.  The
+    // register-prefetch form (PF) for the launches without a LoRA tail: the
+    // C4 dX GEMMs 187.5 -> 183.5 us, the lm_head GEMMs 1% faster, the rest
+    // unchanged; with the tail it measured 2-7% slower.
+    auto go = [&](auto i8c, auto ksc, auto gluc, auto tlc) {
+      constexpr bool I8 = decltype(i8c)::value, KS = decltype(ksc)::value;
+      constexpr bool GL = decltype(gluc)::value, TLc = decltype(tlc)::value;
+      constexpr int SD = I8 ? 5 : 4;
+      hipLaunchKernelGGL((gemm_dma_kernel<I8, KS, SD, 4, GL, TLc, !TLc>), gr, dim3(512), 0, st, gm,
+                         order, tl, tc0);
+    };
+    using BT = std::integral_constant<bool, true>;
+    using BF = std::integral_constant<bool, false>;
     if (gm.glu) {
-      if (!i8)
-        hipLaunchKernelGGL((gemm_dma_kernel<false, false, 4, 4, true>), gr, dim3(512), 0, st, gm, order, tl, tc0);
-      else if (ks)
-        hipLaunchKernelGGL((gemm_dma_kernel<true, true, 5, 4, true>), gr, dim3(512), 0, st, gm, order, tl, tc0);
-      else
-        hipLaunchKernelGGL((gemm_dma_kernel<true, false, 5, 4, true>), gr, dim3(512), 0, st, gm, order, tl, tc0);
+      if (!i8) go(BF(), BF(), BT(), BF());
+      else if (ks) go(BT(), BT(), BT(), BF());
+      else go(BT(), BF(), BT(), BF());
     } else if (fold) {
-      if (!i8)
-        hipLaunchKernelGGL((gemm_dma_kernel<false, false, 4, 4, false, true>), gr, dim3(512), 0, st, gm, order, tl, tc0);
-      else if (ks)
-        hipLaunchKernelGGL((gemm_dma_kernel<true, true, 5, 4, false, true>), gr, dim3(512), 0, st, gm, order, tl, tc0);
-      else
-        hipLaunchKernelGGL((gemm_dma_kernel<true, false, 5, 4, false, true>), gr, dim3(512), 0, st, gm, order, tl, tc0);
+      if (!i8) go(BF(), BF(), BF(), BT());
+      else if (ks) go(BT(), BT(), BF(), BT());
+      else go(BT(), BF(), BF(), BT());
     } else {
-      if (!i8)
-        hipLaunchKernelGGL((gemm_dma_kernel<false, false, 4, 4>), gr, dim3(512), 0, st, gm, order, tl, tc0);
-      else if (ks)
-        hipLaunchKernelGGL((gemm_dma_kernel<true, true, 5, 4>), gr, dim3(512), 0, st, gm, order, tl, tc0);
-      else
-        hipLaunchKernelGGL((gemm_dma_kernel<true, false, 5, 4>), gr, dim3(512), 0, st, gm, order, tl, tc0);
+      if (!i8) go(BF(), BF(), BF(), BF());
+      else if (ks) go(BT(), BT(), BF(), BF());
+      else go(BT(), BF(), BF(), BF());
     }
     e = hipGetLastError();
     if (e == hipSuccess && lora_tail && !fold) {
