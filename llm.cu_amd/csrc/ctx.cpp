@@ -74,6 +74,7 @@ int Ctx::init() {
   TRY_PTR(lora_v = alloc_n<float>(lora_numel));
   TRY_PTR(shadow = alloc_n<_Float16>(shadow_per_layer * L));
   TRY_PTR(shadow_rm = alloc_n<_Float16>(shadow_per_layer * L));
+  TRY_PTR(shadow_at = alloc_n<_Float16>((size_t)L * H * 3 * R));
   TRY_PTR(hp_dev = alloc_n<AdamHp>(1));
   TRY_HIP(hipMemset(lora_p, 0, lora_numel * sizeof(float)));
   TRY_HIP(hipMemset(lora_g, 0, lora_numel * sizeof(float)));
@@ -81,6 +82,7 @@ int Ctx::init() {
   TRY_HIP(hipMemset(lora_v, 0, lora_numel * sizeof(float)));
   TRY_HIP(hipMemset(shadow, 0, shadow_per_layer * L * sizeof(_Float16)));
   TRY_HIP(hipMemset(shadow_rm, 0, shadow_per_layer * L * sizeof(_Float16)));
+  TRY_HIP(hipMemset(shadow_at, 0, (size_t)L * H * 3 * R * sizeof(_Float16)));
 
   // RoPE tables: angles in double, rounded once to fp32 (src/kernels/rope.cu:15-18).
   {

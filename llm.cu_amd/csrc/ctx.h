@@ -126,6 +126,9 @@ struct Ctx {
   _Float16* shadow = nullptr;
   long long shadow_per_layer = 0, sh_a_qkv = 0, sh_a_o = 0, sh_bt_qkv = 0, sh_bt_o = 0;
   _Float16* shadow_rm = nullptr;  // row-major twin of `shadow` (row epilogues)
+  // A_q | A_k | A_v transposed, [L][H][3 R] (the LoRA dx term's MFMA operand
+  // in the attention norm's backward)
+  _Float16* shadow_at = nullptr;
   AdamHp* hp_dev = nullptr;
   AdamHp* host_hp = nullptr;
 

@@ -264,6 +264,12 @@ __device__ __forceinline__ void shadow_store(const AdamShadow& sh, long long i, 
   const _Float16 h = (_Float16)v;
   sh.shadow[q.base + packed_index(q.row, q.col, q.len)] = h;
   sh.rm[q.base + q.row * q.len + q.col] = h;
+  if (sh.at) {  // A of q, k, v: also at (layer, column, row) of the transposed copy
+    const long long l = i / sh.per_layer, j = i - l * sh.per_layer;
+    if (j < sh.seg_off[5] && (j < sh.seg_off[1] || (j >= sh.seg_off[2] && j < sh.seg_off[3]) ||
+                              j >= sh.seg_off[4]))
+      sh.at[(l * sh.d_in[0] + q.col) * (3 * R) + q.row] = h;
+  }
 }
 
 // The AdamW update of one element (src/kernels/lora.cu:206-220):
@@ -404,6 +410,23 @@ __global__ __launch_bounds__(NTH) void adamw_shadow_kernel(float* __restrict__ p
                        (_Float16)pv[u][3]};
       *reinterpret_cast<half4*>(sh.shadow + base + packed_index(row, ac, a_len)) = h;
       *reinterpret_cast<half4*>(sh.rm + base + (long long)row * a_len + ac) = h;
+    }
+    if (q == 3 || !sh.at) return;  // block-uniform
+    // q, k, v: the transposed copy [column][3 R], through LDS: thread t then
+    // stores ranks 4 (t % 4) .. of column t / 4 of the tile (8 bytes)
+    __shared__ _Float16 at_t[TPB][64][R + 4];
+#pragma unroll
+    for (int u = 0; u < TPB; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) at_t[u][4 * (threadIdx.x & 15) + e][ar] = (_Float16)pv[u][e];
+    __syncthreads();
+    const int oc = threadIdx.x >> 2, orq = 4 * (threadIdx.x & 3);
+#pragma unroll
+    for (int u = 0; u < TPB; ++u) {
+      const int col = (blockIdx.x * TPB + u) * 64 + oc;
+      const half4 t = {at_t[u][oc][orq], at_t[u][oc][orq + 1], at_t[u][oc][orq + 2],
+                       at_t[u][oc][orq + 3]};
+      *reinterpret_cast<half4*>(sh.at + ((long long)l * a_len + col) * (3 * R) + q * R + orq) = t;
     }
     return;
   }

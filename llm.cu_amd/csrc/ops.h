@@ -186,6 +186,9 @@ struct NormBwdArgs {
   float* dmid_out;       // may be NULL
   _Float16* g16;
   float* rinv_out;
+  // NULL, or the layer's A_q | A_k | A_v transposed [H][3 R] fp16: with the
+  // three full-width q/k/v terms, the LoRA dx term then runs on MFMA
+  const _Float16* lora_at;
 };
 
 struct QkBwdArgs {
@@ -338,6 +341,7 @@ struct AdamHp {
 struct AdamShadow {
   _Float16* shadow;  // NULL: no shadow writes
   _Float16* rm;      // row-major twin (same block offsets), written with shadow
+  _Float16* at;      // NULL, or A_q | A_k | A_v transposed: [layer][d_in[0]][3 R]
   long long per_layer;
   long long seg_off[8];
   int d_in[4];

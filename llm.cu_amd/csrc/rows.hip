@@ -830,10 +830,70 @@ __global__ __launch_bounds__(RT) void norm_bwd_kernel(const NormBwdArgs a) {
 // side by side (as o_post_rows_kernel), with no adapter terms or with three
 // (LORA: the attention norm's q, k, v terms, each over all H columns, whose
 // 48 x 4 values a thread loads once for all its rows).
-template <int NR, bool LORA, bool NT = false>
+// The attention norm's LoRA dx term s (dh_q A_q + dh_k A_k + dh_v A_v) of
+// NR rows on MFMA (16 x 16 x 16 fp16: rows x ranks of one adapter times
+// ranks x 16 columns): wave w takes columns 256 w .. of the row, A operand
+// = the rows' dh values (rows past NR zero), scaled by 2^-10 into fp16 range
+// (dh is in the GEMM's scaled units), B operand = 4 consecutive ranks of one
+// column from the transposed copy at [H][48].  The 16 x 16 results go
+// through LDS (out[NR][H], H <= 4 RT) to the thread that owns the column.
+constexpr float kLoraMfmaScale = 1.0f / 1024.0f;
+
+template <int NR>
+__device__ __forceinline__ void lora_rows_mfma(const NormBwdArgs& a, const float (*hs)[64],
+                                               float* out) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kq = lane >> 4, n = lane & 15;
+  half4 aop[3];
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    const float4 h4 = n < NR ? *reinterpret_cast<const float4*>(&hs[n][a.in.term[q].hidx + 4 * kq])
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+    aop[q] = half4{(_Float16)(h4.x * kLoraMfmaScale), (_Float16)(h4.y * kLoraMfmaScale),
+                   (_Float16)(h4.z * kLoraMfmaScale), (_Float16)(h4.w * kLoraMfmaScale)};
+  }
+  const int H = a.H;
+#pragma unroll
+  for (int cg = 0; cg < 4; ++cg) {
+    const int cb = 256 * wave + 64 * cg;
+    if (cb >= H) break;  // wave-uniform
+    half4 b[3][4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const int col = min(cb + 16 * nb + n, H - 1);
+#pragma unroll
+      for (int q = 0; q < 3; ++q)
+        b[q][nb] = *reinterpret_cast<const half4*>(a.lora_at + (long long)col * (3 * R) + q * R + 4 * kq);
+    }
+    floatx4 acc[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      acc[nb] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < 3; ++q)
+        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16f16(aop[q], b[q][nb], acc[nb], 0, 0, 0);
+    }
+    // lane: rows 4 kq + i of column cb + 16 nb + n
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 4 * kq + i;
+      if (row >= NR) continue;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        const int col = cb + 16 * nb + n;
+        if (col < H) out[row * H + col] = acc[nb][i];
+      }
+    }
+  }
+}
+
+// LM: 0 no adapter terms, 1 the q/k/v terms on VALU, 2 on MFMA
+// (lora_rows_mfma: 255 -> 229 VGPRs, C4 52.6 -> 45.9 us a layer).
+template <int NR, int LM, bool NT = false>
 __global__ __launch_bounds__(RT) void norm_bwd_rows_kernel(const NormBwdArgs a, int T) {
+  constexpr bool LORA = LM > 0;
   __shared__ float red[2 * NR * RW];
-  __shared__ float hs[NR][64];
+  __shared__ __attribute__((aligned(16))) float hs[NR][64];
   const int H = a.H;
   const int t0 = blockIdx.x * NR;
   const int c = 4 * (int)threadIdx.x;
@@ -858,7 +918,16 @@ __global__ __launch_bounds__(RT) void norm_bwd_rows_kernel(const NormBwdArgs a, 
       *reinterpret_cast<float4*>(a.dh_out + (long long)(t0 + i) * 64 + a.dh_col + 4 * threadIdx.x) =
           mul4(hv[i], rs[i]);
   }
-  if constexpr (LORA) {
+  if constexpr (LM == 2) {
+    __shared__ __attribute__((aligned(16))) float lora_out[NR * 4 * RT];  // [NR][H]
+    __syncthreads();
+    lora_rows_mfma<NR>(a, hs, lora_out);
+    __syncthreads();
+    const float ls = a.in.lscale / kLoraMfmaScale;
+#pragma unroll
+    for (int i = 0; i < NR; ++i)
+      v[i] = add4(v[i], mul4(*reinterpret_cast<const float4*>(&lora_out[i * H + cc]), ls));
+  } else if constexpr (LM == 1) {
     LoraRegs<1, 3> L;
     lora_load<1, 3>(a.in, H, L);
     __syncthreads();
@@ -1465,13 +1534,28 @@ hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st) {
   // 32 MB a launch (C4: 33.5 MB each) nontemporal (C4 LoRA form 58.4 ->
   // 56.9 us, the plain form unchanged)
   const bool nt = (long long)T * a.H * 4 >= (32ll << 20);
+  // the MFMA form of the LoRA term: three full-width q/k/v terms, hidx and
+  // adapter rows 16 q, one piece a thread (H <= 4 RT), [NR][H] fp32 of LDS
+  NormBwdArgs am = a;
+  if (am.lora_at) {
+    bool ok = lora && am.in.nterm == 3 && a.H <= 4 * RT && a.H % 16 == 0;
+    for (int q = 0; q < am.in.nterm && ok; ++q)
+      ok = am.in.term[q].c0 == 0 && am.in.term[q].n == a.H && am.in.term[q].hidx == q * R;
+    if (!ok) am.lora_at = nullptr;
+  }
   auto rows = [&](auto nr_, auto lora_) {
     constexpr int NR = decltype(nr_)::value;
     constexpr bool LO = decltype(lora_)::value;
-    if (nt)
-      hipLaunchKernelGGL((norm_bwd_rows_kernel<NR, LO, true>), g, dim3(RT), 0, st, a, T);
-    else
-      hipLaunchKernelGGL((norm_bwd_rows_kernel<NR, LO, false>), g, dim3(RT), 0, st, a, T);
+    if (LO && am.lora_at) {
+      if (nt)
+        hipLaunchKernelGGL((norm_bwd_rows_kernel<NR, 2, true>), g, dim3(RT), 0, st, am, T);
+      else
+        hipLaunchKernelGGL((norm_bwd_rows_kernel<NR, 2, false>), g, dim3(RT), 0, st, am, T);
+    } else if (nt) {
+      hipLaunchKernelGGL((norm_bwd_rows_kernel<NR, LO ? 1 : 0, true>), g, dim3(RT), 0, st, am, T);
+    } else {
+      hipLaunchKernelGGL((norm_bwd_rows_kernel<NR, LO ? 1 : 0, false>), g, dim3(RT), 0, st, am, T);
+    }
   };
   using std::integral_constant;
   using T1 = integral_constant<bool, true>;

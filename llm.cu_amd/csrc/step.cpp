@@ -200,6 +200,7 @@ AdamShadow Ctx::shadow_desc() const {
   AdamShadow sh{};
   sh.shadow = shadow;
   sh.rm = shadow_rm;
+  sh.at = shadow_at;
   sh.per_layer = lora_per_layer;
   for (int i = 0; i < 8; ++i) sh.seg_off[i] = seg_off[i];
   sh.d_in[0] = sh.d_in[1] = sh.d_in[2] = H;
@@ -518,6 +519,7 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   nb.dmid_out = nullptr;
   nb.g16 = g16;
   nb.rinv_out = rinv;
+  nb.lora_at = shadow_at + (size_t)l * H * 3 * kRank;
   LLMT_HIP_TRY(run(CAT_ROWS, "norm_bwd_lora", [=](hipStream_t q) { return norm_bwd(nb, T, q); },
                    0, part_bytes(nb.in, T, H) + (double)T * (H * (4 + 4 + 4 + 2) + 48 * 4)));
   return hipSuccess;
