@@ -284,13 +284,16 @@ constexpr int BM = 256, BCH = 2;  // large-tile rows; k-steps per big_tiles() K 
 // of the wave's block; a fragment-packed fp16 fragment is 1 KB in lane order
 // and an int8 one 512 B, moved by the first 32 lanes, so both arrive in MFMA
 // fragment order with no register staging and no LDS store phase), through
-// an S-stage ring of 32-wide K chunks: chunk c + S - 1 is in flight while
-// chunk c is multiplied, so S - 1 chunks of MFMA work cover the memory
-// latency.  Each workgroup of eight waves owns a 256 x 256 tile (2 x 4
-// waves of 128 x 64, 32 accumulator fragments a wave; the four-wave form with
-// 128 x 128 a wave measured 12-20% slower at the C4 shapes).
-// int8 B fragments are dequantised at read time (exact int8 -> fp16 through
-// the 1024 + x bias trick, times the per-k scale if any).  The waits are
+// an S-stage ring of 32-wide K chunks: chunks up to c + S - 1 are in flight
+// while chunk c is multiplied.  Each workgroup of eight waves owns a 256 x 256
+// tile (2 x 4 waves of 128 x 64, 32 accumulator fragments a wave; the
+// four-wave form with 128 x 128 a wave measured 12-20% slower at the C4
+// shapes).  The fragments run one chunk ahead in registers: while the MFMAs
+// of chunk c issue, chunk c + 1's fragments are read from LDS (each A
+// fragment register refilled right after its last MFMA), so LDS latency and
+// the int8 dequantisation (exact int8 -> fp16 through the 1024 + x bias
+// trick, times the per-k scale if any) leave the critical path (C4 dX
+// GEMMs 187.5 -> 183.5 us, the tail-folded ones 2-3% faster).  The waits are
 // explicit: vmcnt counts this thread's DMA issues, which complete in order,
 // and a plain s_barrier (no fence, which would drain every load) publishes
 // the chunk to the other waves.
@@ -322,7 +325,7 @@ __device__ __forceinline__ half8 i8x8_to_h8(u32x2 raw) {
 // block and K range (two extra MFMAs a wave per chunk, the fragment's 1 KB
 // a chunk moved by eight lanes of every wave), instead of a separate launch
 // that streamed the whole activation matrix again.
-template <bool I8, bool KS, int S, int WNN, bool GLU = false, bool TL = false, bool PF = false>
+template <bool I8, bool KS, int S, int WNN, bool GLU = false, bool TL = false>
 __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, int g_order,
                                                              const BSeg tail, int tail_c0) {
   // WNN waves across N (2: four waves of 128 x 128; 4: eight waves of 128 x 64)
@@ -433,118 +436,87 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
   // tail: this wave's rows 16 (2 wn + j) .. of its 128-row half
   floatx4 acc_t[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
 
-  if constexpr (PF) {
-    // Fragments one chunk ahead: after the barrier that publishes chunk
-    // c + 1, each A fragment register of chunk c is refilled from chunk c + 1
-    // right after its last MFMA, and chunk c + 1's B bytes (and k-scales,
-    // tail fragment) are read at the top, dequantised after the last MFMA;
-    // so LDS latency sits under the MFMAs and the registers stay one set.
-    half8 a[8], b[NFR], bt, btn, ksn;
-    u32x2 bn8[NFR];
-    half8 bn16[NFR];
-    auto read_b = [&](const char* st) LLMT_INLINE {
-      if constexpr (KS) ksn = *reinterpret_cast<const half8*>(st + ABYTES + BBYTES + (lane >> 4) * 16);
-#pragma unroll
-      for (int j = 0; j < NFR; ++j) {
-        const int fr = wn * NFR + j;
-        if constexpr (I8)
-          bn8[j] = *reinterpret_cast<const u32x2*>(st + ABYTES + fr * 512 + lane * 8);
-        else
-          bn16[j] = *reinterpret_cast<const half8*>(st + ABYTES + fr * 1024 + lane * 16);
-      }
-      if constexpr (TL) btn = *reinterpret_cast<const half8*>(st + TOFF + lane * 16);
-    };
-    auto take_b = [&]() LLMT_INLINE {
-#pragma unroll
-      for (int j = 0; j < NFR; ++j) {
-        if constexpr (I8) {
-          b[j] = i8x8_to_h8(bn8[j]);
-          if constexpr (KS) b[j] = b[j] * ksn;
-        } else {
-          b[j] = bn16[j];
-        }
-      }
-      if constexpr (TL) bt = btn;
-    };
-    auto read_a = [&](const char* st, int i) LLMT_INLINE {
-      a[i] = *reinterpret_cast<const half8*>(st + (wm * 8 + i) * 1024 + lane * 16);
-    };
-#pragma unroll
-    for (int c = 0; c < S; ++c) issue(c0 + c);
-    static_assert((S - 1) * OPS < 64, "vmcnt range");
-    wait_vm<(S - 1) * OPS>();
-    __builtin_amdgcn_s_barrier();
-    {
-      const char* st = smem + (c0 % S) * SBYTES;
-      read_b(st);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) read_a(st, i);
-      take_b();
-    }
-    for (int c = c0; c < c1; ++c) {
-      // vmcnt: chunk c + 1 landed; lgkmcnt 0: this wave's reads of chunk c
-      // returned, so after the barrier chunk c's slot takes chunk c + S
-      constexpr int N = (S - 2) * OPS;
-      __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
-      __builtin_amdgcn_s_barrier();
-      issue(c + S);
-      const char* st = smem + ((c + 1) % S) * SBYTES;
-      read_b(st);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-#pragma unroll
-        for (int j = 0; j < NFR; ++j) acc[i][j] = mfma16(a[i], b[j], acc[i][j]);
-        if constexpr (TL) {
-          if (has_tail && (i >> 1) == wn) acc_t[i & 1] = mfma16(a[i], bt, acc_t[i & 1]);
-        }
-        read_a(st, i);
-      }
-      take_b();
-    }
-  } else {
-#pragma unroll
-  for (int c = 0; c < S - 1; ++c) issue(c0 + c);
-  for (int c = c0; c < c1; ++c) {
-    wait_vm<(S - 2) * OPS>();
-    __builtin_amdgcn_s_barrier();
-    issue(c + S - 1);
-    const char* st = smem + (c % S) * SBYTES;
-    half8 b[NFR];
-    half8 ksc;
-    if constexpr (KS) ksc = *reinterpret_cast<const half8*>(st + ABYTES + BBYTES + (lane >> 4) * 16);
+  // Fragments one chunk ahead: after the barrier that publishes chunk
+  // c + 1, each A fragment register of chunk c is refilled from chunk c + 1
+  // right after its last MFMA, and chunk c + 1's B bytes (and k-scales,
+  // tail fragment) are read at the top, dequantised after the last MFMA;
+  // so LDS latency sits under the MFMAs and the registers stay one set.
+  half8 a[8], b[NFR], bt, btn, ksn, at[2], atn[2];
+  u32x2 bn8[NFR];
+  half8 bn16[NFR];
+  auto read_b = [&](const char* st) LLMT_INLINE {
+    if constexpr (KS) ksn = *reinterpret_cast<const half8*>(st + ABYTES + BBYTES + (lane >> 4) * 16);
 #pragma unroll
     for (int j = 0; j < NFR; ++j) {
       const int fr = wn * NFR + j;
+      if constexpr (I8)
+        bn8[j] = *reinterpret_cast<const u32x2*>(st + ABYTES + fr * 512 + lane * 8);
+      else
+        bn16[j] = *reinterpret_cast<const half8*>(st + ABYTES + fr * 1024 + lane * 16);
+    }
+    if constexpr (TL) {
+      // the tail's fragment and the two A fragments it meets (rows
+      // 16 (2 wn + j) of the wave's half), read on their own so the tail
+      // MFMAs need no register selection
+      btn = *reinterpret_cast<const half8*>(st + TOFF + lane * 16);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        atn[j] = *reinterpret_cast<const half8*>(st + (wm * 8 + 2 * wn + j) * 1024 + lane * 16);
+    }
+  };
+  auto take_b = [&]() LLMT_INLINE {
+#pragma unroll
+    for (int j = 0; j < NFR; ++j) {
       if constexpr (I8) {
-        const u32x2 raw = *reinterpret_cast<const u32x2*>(st + ABYTES + fr * 512 + lane * 8);
-        b[j] = i8x8_to_h8(raw);
-        if constexpr (KS) b[j] = b[j] * ksc;
+        b[j] = i8x8_to_h8(bn8[j]);
+        if constexpr (KS) b[j] = b[j] * ksn;
       } else {
-        b[j] = *reinterpret_cast<const half8*>(st + ABYTES + fr * 1024 + lane * 16);
+        b[j] = bn16[j];
       }
     }
+    if constexpr (TL) {
+      bt = btn;
+      at[0] = atn[0];
+      at[1] = atn[1];
+    }
+  };
+  auto read_a = [&](const char* st, int i) LLMT_INLINE {
+    a[i] = *reinterpret_cast<const half8*>(st + (wm * 8 + i) * 1024 + lane * 16);
+  };
+#pragma unroll
+  for (int c = 0; c < S; ++c) issue(c0 + c);
+  static_assert((S - 1) * OPS < 64, "vmcnt range");
+  wait_vm<(S - 1) * OPS>();
+  __builtin_amdgcn_s_barrier();
+  {
+    const char* st = smem + (c0 % S) * SBYTES;
+    read_b(st);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) read_a(st, i);
+    take_b();
+  }
+  for (int c = c0; c < c1; ++c) {
+    // vmcnt: chunk c + 1 landed; lgkmcnt 0: this wave's reads of chunk c
+    // returned, so after the barrier chunk c's slot takes chunk c + S
+    constexpr int N = (S - 2) * OPS;
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+    __builtin_amdgcn_s_barrier();
+    issue(c + S);
+    const char* st = smem + ((c + 1) % S) * SBYTES;
+    read_b(st);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const half8 a = *reinterpret_cast<const half8*>(st + (wm * 8 + i) * 1024 + lane * 16);
 #pragma unroll
-      for (int j = 0; j < NFR; ++j) acc[i][j] = mfma16(a, b[j], acc[i][j]);
+      for (int j = 0; j < NFR; ++j) acc[i][j] = mfma16(a[i], b[j], acc[i][j]);
+      read_a(st, i);
     }
-    // every LDS read of the chunk first, then its MFMAs (the default
-    // schedule waits on each A fragment right before its four MFMAs;
-    // 4-5% faster at the C4 shapes)
-    __builtin_amdgcn_sched_group_barrier(0x100, NFR + 8, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 8 * NFR, 0);
     if constexpr (TL) {
       if (has_tail) {
-        const half8 bt = *reinterpret_cast<const half8*>(st + TOFF + lane * 16);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const half8 a = *reinterpret_cast<const half8*>(st + (wm * 8 + 2 * wn + j) * 1024 + lane * 16);
-          acc_t[j] = mfma16(a, bt, acc_t[j]);
-        }
+        acc_t[0] = mfma16(at[0], bt, acc_t[0]);
+        acc_t[1] = mfma16(at[1], bt, acc_t[1]);
       }
     }
-  }
+    take_b();
   }
   wait_vm<0>();
 
@@ -1359,16 +1331,13 @@ hipError_t gemm_nt(const GemmArgs& g, hipStream_t st) {
     const BSeg tl = lora_tail ? g.seg[last] : BSeg{};
     const bool fold = lora_tail && !tl.is_i8 && tl.rows / 16 <= (gm.N + 255) / 256;
     const int tc0 = lora_tail ? g.seg_start[last] : 0;
-    // ring depth 5 (int8) / 4 (fp16): 4 measured the same, 6 slower.  The
-    // register-prefetch form (PF) for the launches without a LoRA tail: the
-    // C4 dX GEMMs 187.5 -> 183.5 us, the lm_head GEMMs 1% faster, the rest
-    // unchanged; with the tail it measured 2-7% slower.
+    // ring depth 5 (int8) / 4 (fp16): 4 measured the same, 6 slower
     auto go = [&](auto i8c, auto ksc, auto gluc, auto tlc) {
       constexpr bool I8 = decltype(i8c)::value, KS = decltype(ksc)::value;
       constexpr bool GL = decltype(gluc)::value, TLc = decltype(tlc)::value;
       constexpr int SD = I8 ? 5 : 4;
-      hipLaunchKernelGGL((gemm_dma_kernel<I8, KS, SD, 4, GL, TLc, !TLc>), gr, dim3(512), 0, st, gm,
-                         order, tl, tc0);
+      hipLaunchKernelGGL((gemm_dma_kernel<I8, KS, SD, 4, GL, TLc>), gr, dim3(512), 0, st, gm, order,
+                         tl, tc0);
     };
     using BT = std::integral_constant<bool, true>;
     using BF = std::integral_constant<bool, false>;
