@@ -510,6 +510,16 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
       for (int j = 0; j < NFR; ++j) acc[i][j] = mfma16(a[i], b[j], acc[i][j]);
       read_a(st, i);
     }
+    // the order the loop states: chunk c + 1's B (and scale, tail) reads
+    // first, then per row its MFMAs followed by the read that refills its A
+    // register (left alone, the compiler sank all eight A reads below the
+    // last MFMA, exposing their latency at the barrier)
+    __builtin_amdgcn_sched_group_barrier(0x100, (I8 ? NFR / 2 : NFR) + (KS ? 1 : 0) + (TL ? 3 : 0), 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, NFR, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
     if constexpr (TL) {
       if (has_tail) {
         acc_t[0] = mfma16(at[0], bt, acc_t[0]);
