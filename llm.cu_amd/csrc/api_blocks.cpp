@@ -160,7 +160,8 @@ int llmt_layer_backward(llmt_ctx* ctx, int layer, const float* dy, float* dx, in
   TRY_ARG(batch >= 1 && batch <= c->maxB && (batch * c->S) % 16 == 0, "batch");
   const int T = batch * c->S;
   c->pad_batch = 0;
-  TRY_HIP(grad_rows(dy, c->H, T, c->d_res, c->g16, c->rinv, c->st));
+  // g16 feeds the layer's down dX, which takes int8 weights' scale from it
+  TRY_HIP(grad_rows(dy, c->H, T, c->d_res, c->g16, c->rinv, c->layers[layer].wdT.kscale, c->st));
   TRY_HIP(c->layer_bwd(layer, batch));
   TRY_HIP(c->lora_grads(layer, 1, batch, 0));
   TRY_HIP(hipMemcpyAsync(dx, c->d_res, (size_t)T * c->H * 4, hipMemcpyDeviceToDevice, c->st));

@@ -54,6 +54,21 @@ using IC = std::integral_constant<int, V>;
 constexpr int gcd_c(int a, int b) { return b == 0 ? a : gcd_c(b, a % b); }
 constexpr int lcm_c(int a, int b) { return a / gcd_c(a, b) * b; }
 
+// Packed int8 weights are stored biased, byte = x + 128 (x ^ 0x80; written by
+// pack_i8), so that fp16 bits 0x64 | byte read as 1024 + x + 128, exact.
+// v_perm_b32 picks bytes 0-3 from its second source and 4-7 from its
+// first: each output dword [b_i, 0x64, b_i+1, 0x64] is one instruction.
+__device__ __forceinline__ half8 i8x8_to_h8(u32x2 raw) {
+  constexpr unsigned k64 = 0x64646464u, s01 = 0x04010400u, s23 = 0x04030402u;
+  u32x4 bits;
+  bits[0] = __builtin_amdgcn_perm(k64, raw[0], s01);
+  bits[1] = __builtin_amdgcn_perm(k64, raw[0], s23);
+  bits[2] = __builtin_amdgcn_perm(k64, raw[1], s01);
+  bits[3] = __builtin_amdgcn_perm(k64, raw[1], s23);
+  const half8 h = __builtin_bit_cast(half8, bits);
+  return h - (_Float16)1152.0f;
+}
+
 // One workgroup: output tile (MF*16) x (NW*NF*16) over k-steps [s0, s1) of
 // its split.  The A tile goes through LDS in chunks of CHS k-steps (two LDS
 // buffers); chunk c + ADIST is loaded into registers while chunk c is
@@ -169,10 +184,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
     constexpr int st = decltype(S)::value;
     half8 h;
     if (I8 && bi8[f]) {
-      const u32x2 raw = {rb[st][f][0], rb[st][f][1]};
-      const int8x8 q = __builtin_bit_cast(int8x8, raw);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) h[i] = (_Float16)(float)q[i];
+      h = i8x8_to_h8(u32x2{rb[st][f][0], rb[st][f][1]});
       if (kscale[f]) {
         h = h * __builtin_bit_cast(half8, rk[st][f]);
       }
@@ -291,8 +303,9 @@ constexpr int BM = 256, BCH = 2;  // large-tile rows; k-steps per big_tiles() K 
 // shapes).  The fragments run one chunk ahead in registers: while the MFMAs
 // of chunk c issue, chunk c + 1's fragments are read from LDS (each A
 // fragment register refilled right after its last MFMA), so LDS latency and
-// the int8 dequantisation (exact int8 -> fp16 through the 1024 + x bias
-// trick, times the per-k scale if any) leave the critical path (C4 dX
+// the int8 dequantisation (exact int8 -> fp16 from the biased bytes, one
+// v_perm_b32 and one v_pk_add_f16 a dword, times the per-k scale if any)
+// leave the critical path (C4 dX
 // GEMMs 187.5 -> 183.5 us, the tail-folded ones 2-3% faster).  The waits are
 // explicit: vmcnt counts this thread's DMA issues, which complete in order,
 // and a plain s_barrier (no fence, which would drain every load) publishes
@@ -307,17 +320,6 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// fp16 from 8 int8 values: (1024 + (x + 128)) - 1152, exact.
-__device__ __forceinline__ half8 i8x8_to_h8(u32x2 raw) {
-  const unsigned lo = raw[0] ^ 0x80808080u, hi = raw[1] ^ 0x80808080u;
-  u32x4 bits;
-  bits[0] = 0x64006400u | (lo & 0xFFu) | ((lo & 0xFF00u) << 8);
-  bits[1] = 0x64006400u | ((lo >> 16) & 0xFFu) | ((lo >> 8) & 0xFF0000u);
-  bits[2] = 0x64006400u | (hi & 0xFFu) | ((hi & 0xFF00u) << 8);
-  bits[3] = 0x64006400u | ((hi >> 16) & 0xFFu) | ((hi >> 8) & 0xFF0000u);
-  const half8 h = __builtin_bit_cast(half8, bits);
-  return h - (_Float16)1152.0f;
-}
 
 // TL: a trailing fp16 segment `tail` of at most 64 rows (the LoRA A or B^T
 // rows of a projection, output columns tail_c0 ..) rides along: its 16-row
@@ -526,6 +528,11 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
         acc_t[1] = mfma16(at[1], bt, acc_t[1]);
       }
     }
+    // the dequantisation stays below the rows: hoisted up to the B reads
+    // (as the compiler otherwise does with part of it) it waits on them
+    // right at the top of the chunk.  VALU may not cross; MFMA, LDS, SALU
+    // and memory instructions may.
+    __builtin_amdgcn_sched_barrier(0);
     take_b();
   }
   wait_vm<0>();
@@ -982,7 +989,12 @@ __global__ void pack_kernel(const T* __restrict__ src, long long lds, int transp
       v[e] = transpose ? src[(long long)(jp * 8 + e) * lds + i] : src[(long long)i * lds + jp * 8 + e];
     T* d = dst + packed_index(row0 + i, k0 + jp * 8, K);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) d[e] = v[e];
+    for (int e = 0; e < 8; ++e) {
+      if constexpr (std::is_same_v<T, int8_t>)
+        d[e] = (int8_t)((uint8_t)v[e] ^ 0x80u);  // biased: byte = x + 128
+      else
+        d[e] = v[e];
+    }
   }
 }
 

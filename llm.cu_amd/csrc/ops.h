@@ -96,6 +96,8 @@ hipError_t reduce_lora(const ReduceArgs& a, hipStream_t st);
 // fragment-packed operand with row length K (transpose: the block is src^T).
 hipError_t pack_f16(const _Float16* src, long long lds, int transpose, int R, int C, _Float16* dst,
                     long long K, int row0, int k0, hipStream_t st);
+// pack_i8 stores each int8 x biased, as the byte x + 128 (x ^ 0x80), which
+// the GEMMs' int8 -> fp16 conversion expects.
 hipError_t pack_i8(const int8_t* src, long long lds, int transpose, int R, int C, int8_t* dst,
                    long long K, int row0, int k0, hipStream_t st);
 
@@ -186,6 +188,9 @@ struct NormBwdArgs {
   float* dmid_out;       // may be NULL
   _Float16* g16;
   float* rinv_out;
+  // NULL, or a per-column factor [H] folded into g16 (the consuming int8
+  // GEMM's per-k weight scale, which that GEMM then leaves out)
+  const _Float16* g16_ks;
   // NULL, or the layer's A_q | A_k | A_v transposed [H][3 R] fp16: with the
   // three full-width q/k/v terms, the LoRA dx term then runs on MFMA
   const _Float16* lora_at;
@@ -228,8 +233,9 @@ struct HeadRows {
 hipError_t head_norm_rope(const HeadRows* segs, int nseg, const float* cosT, const float* sinT,
                           int S, int T, float eps, hipStream_t st);
 hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st);
+// ks: NULL, or a per-column factor [2 I] folded into dgu16 (as g16_ks).
 hipError_t swiglu_bwd(const RowIn& in, const float* rinv_in, const _Float16* gu, int I, int T,
-                      _Float16* dgu16, float* rinv_out, hipStream_t st);
+                      _Float16* dgu16, float* rinv_out, const _Float16* ks, hipStream_t st);
 // dX of the O projection -> the attention's dO operand: dO16 (row t, head h)
 // = fp16(dO * 2^k) with 2^k the power-of-two scale of that head row,
 // dsc[b, h, s] = 2^-k (0 for an all-zero head row), delta[b, h, s] =
@@ -242,9 +248,10 @@ hipError_t qk_bwd(const QkBwdArgs& a, int T, hipStream_t st);
 hipError_t copy_norm(const float* x, const float* w, float eps, int H, int T, float* x_out,
                      _Float16* xn, hipStream_t st);
 // A gradient row as the fp16 GEMM operand: dres = dy (may alias), g16 =
-// fp16(dy * sc), rinv = 1 / sc with sc the row's power-of-two scale.
+// fp16(dy * ks * sc), rinv = 1 / sc with sc the row's power-of-two scale and
+// ks a per-column factor (1 when NULL).
 hipError_t grad_rows(const float* dy, int H, int T, float* dres, _Float16* g16, float* rinv,
-                     hipStream_t st);
+                     const _Float16* ks, hipStream_t st);
 // dst[r][c] = (float) src[r][c] for a [rows, cols] block (lds, ldd).
 hipError_t f16_to_f32_rows(const _Float16* src, long long lds, int rows, int cols, float* dst,
                            long long ldd, hipStream_t st);

@@ -56,6 +56,9 @@ __device__ __forceinline__ float4 add4(float4 a, float4 b) {
 __device__ __forceinline__ float4 mul4(float4 a, float s) {
   return make_float4(a.x * s, a.y * s, a.z * s, a.w * s);
 }
+__device__ __forceinline__ float4 mul4v(float4 a, float4 b) {
+  return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
+}
 __device__ __forceinline__ void st_h4(_Float16* p, float4 v) {
   half4 h;
   h[0] = (_Float16)v.x;
@@ -814,6 +817,7 @@ __global__ __launch_bounds__(RT) void norm_bwd_kernel(const NormBwdArgs a) {
                        dr[p].z + r * (d.z * ww.z - coef * x.z), dr[p].w + r * (d.w * ww.w - coef * x.w));
     *reinterpret_cast<float4*>(a.dres_out + (long long)t * H + c) = v[p];
     if (a.dmid_out) *reinterpret_cast<float4*>(a.dmid_out + (long long)t * H + c) = v[p];
+    if (a.g16_ks) v[p] = mul4v(v[p], ldh4(a.g16_ks + c));
     amax = fmaxf(amax, amax4(v[p]));
   }
   amax = block_max<RW>(amax, red);
@@ -942,6 +946,7 @@ __global__ __launch_bounds__(RT) void norm_bwd_rows_kernel(const NormBwdArgs a, 
     s2[NR + i] = live ? x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w : 0.f;
   }
   block_sums<2 * NR>(s2, red);
+  const float4 ks4 = a.g16_ks ? ldh4(a.g16_ks + cc) : make_float4(1.f, 1.f, 1.f, 1.f);
   float amax[NR];
 #pragma unroll
   for (int i = 0; i < NR; ++i) {
@@ -954,6 +959,7 @@ __global__ __launch_bounds__(RT) void norm_bwd_rows_kernel(const NormBwdArgs a, 
       *reinterpret_cast<float4*>(a.dres_out + (long long)(t0 + i) * H + c) = v[i];
       if (a.dmid_out) *reinterpret_cast<float4*>(a.dmid_out + (long long)(t0 + i) * H + c) = v[i];
     }
+    v[i] = mul4v(v[i], ks4);
     amax[i] = live ? amax4(v[i]) : 0.f;
   }
   block_maxes<NR>(amax, red);
@@ -974,7 +980,8 @@ __global__ __launch_bounds__(RT) void swiglu_bwd_kernel(const RowIn in,
                                                         const float* __restrict__ rinv_in,
                                                         const _Float16* __restrict__ gu, int I,
                                                         _Float16* __restrict__ dgu16,
-                                                        float* __restrict__ rinv_out) {
+                                                        float* __restrict__ rinv_out,
+                                                        const _Float16* __restrict__ ks) {
   __shared__ float red[2 * RW];
   const int t = blockIdx.x;
   const _Float16* gr = gu + (long long)t * 2 * I;
@@ -1011,6 +1018,11 @@ __global__ __launch_bounds__(RT) void swiglu_bwd_kernel(const RowIn in,
     }
     dg[p] = make_float4(o1[0], o1[1], o1[2], o1[3]);
     du[p] = make_float4(o2[0], o2[1], o2[2], o2[3]);
+    if (ks) {
+      const int c = min(4 * ((int)threadIdx.x + p * RT), I - 4);
+      dg[p] = mul4v(dg[p], ldh4(ks + c));
+      du[p] = mul4v(du[p], ldh4(ks + I + c));
+    }
     if (4 * ((int)threadIdx.x + p * RT) < I) amax = fmaxf(amax, fmaxf(amax4(dg[p]), amax4(du[p])));
   }
   amax = block_max<RW>(amax, red);
@@ -1280,21 +1292,24 @@ __global__ __launch_bounds__(RT) void copy_norm_kernel(const float* __restrict__
   }
 }
 
-// dres = dy; g16 = fp16(dy * sc); rinv = 1 / sc (sc: the row's power-of-two scale).
+// dres = dy; g16 = fp16(dy ks * sc); rinv = 1 / sc (sc: the row's power-of-two
+// scale; ks the operand's per-column factor, 1 when ks is NULL).
 __global__ __launch_bounds__(RT) void grad_rows_kernel(const float* dy, int H, float* dres,
                                                        _Float16* __restrict__ g16,
-                                                       float* __restrict__ rinv) {
+                                                       float* __restrict__ rinv,
+                                                       const _Float16* __restrict__ ks) {
   __shared__ float red[2 * RW];
   const int t = blockIdx.x;
   float amax = 0.f;
-  for (int c = threadIdx.x; c < H; c += RT) amax = fmaxf(amax, fabsf(dy[(long long)t * H + c]));
+  for (int c = threadIdx.x; c < H; c += RT)
+    amax = fmaxf(amax, fabsf(dy[(long long)t * H + c] * (ks ? (float)ks[c] : 1.0f)));
   amax = block_max<RW>(amax, red);
   const float sc = pow2_scale_for(amax);
   if (threadIdx.x == 0) rinv[t] = 1.0f / sc;
   for (int c = threadIdx.x; c < H; c += RT) {
     const float v = dy[(long long)t * H + c];
     dres[(long long)t * H + c] = v;
-    g16[(long long)t * H + c] = (_Float16)(v * sc);
+    g16[(long long)t * H + c] = (_Float16)(v * (ks ? (float)ks[c] : 1.0f) * sc);
   }
 }
 
@@ -1364,8 +1379,8 @@ hipError_t copy_norm(const float* x, const float* w, float eps, int H, int T, fl
 }
 
 hipError_t grad_rows(const float* dy, int H, int T, float* dres, _Float16* g16, float* rinv,
-                     hipStream_t st) {
-  hipLaunchKernelGGL(grad_rows_kernel, dim3(T), dim3(RT), 0, st, dy, H, dres, g16, rinv);
+                     const _Float16* ks, hipStream_t st) {
+  hipLaunchKernelGGL(grad_rows_kernel, dim3(T), dim3(RT), 0, st, dy, H, dres, g16, rinv, ks);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
@@ -1582,11 +1597,11 @@ hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st) {
 }
 
 hipError_t swiglu_bwd(const RowIn& in, const float* rinv_in, const _Float16* gu, int I, int T,
-                      _Float16* dgu16, float* rinv_out, hipStream_t st) {
+                      _Float16* dgu16, float* rinv_out, const _Float16* ks, hipStream_t st) {
   if (!row_in_ok(in, I, "swiglu_bwd", true)) return hipErrorInvalidValue;
   const int P = (I + 4 * RT - 1) / (4 * RT);
   auto go = [&](auto kern) {
-    hipLaunchKernelGGL(kern, dim3(T), dim3(RT), 0, st, in, rinv_in, gu, I, dgu16, rinv_out);
+    hipLaunchKernelGGL(kern, dim3(T), dim3(RT), 0, st, in, rinv_in, gu, I, dgu16, rinv_out, ks);
   };
   const bool sc = in.split_col > 0;
   if (sc && in.split != 2) {

@@ -406,6 +406,7 @@ hipError_t Ctx::head_bwd(int B) {
   nb.dmid_out = nullptr;
   nb.g16 = g16;
   nb.rinv_out = rinv;
+  nb.g16_ks = layers[L - 1].wdT.kscale;  // g16 feeds the last layer's down dX
   // partials and x in; the residual gradient (fp32) and its fp16 operand out
   LLMT_HIP_TRY(run(CAT_ROWS, "norm_bwd_final", [=](hipStream_t q) { return norm_bwd(nb, T, q); },
                    0, part_bytes(nb.in, T, H) + (double)T * H * (4 + 4 + 2)));
@@ -428,8 +429,12 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   float* const dh = this->dh(l);
   _Float16* const og16 = go16(l);  // o projection upstream gradient (fp16, row factor ro)
   _Float16* const qg16 = gq16(l);  // q/k/v projections upstream gradient (row factor rq)
-  // MLP: down dX -> SwiGLU bwd -> gate/up dX -> FFN norm bwd (+ residual)
+  // MLP: down dX -> SwiGLU bwd -> gate/up dX -> FFN norm bwd (+ residual).
+  // With int8 weights both dX GEMMs reduce over the weights' output channel,
+  // whose scale their fp16 operands (g16, dgu16) already carry: the writers
+  // fold it in per column, so these GEMMs dequantise without it.
   BSeg sd[1] = {wseg(w.wdT)};
+  sd[0].kscale = nullptr;
   LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, sd, 1, T, H, nullptr, 0, &go_, nullptr, nullptr, nullptr,
                     nullptr, true));
   {
@@ -439,12 +444,14 @@ hipError_t Ctx::layer_bwd(int l, int B) {
     _Float16* d16 = dgu16;
     float* r2 = rinv2;
     const int Ii = I;
+    const _Float16* ks = w.wguT.kscale;
     // partials and gate|up (fp16) in, dgate|dup (fp16) out
     LLMT_HIP_TRY(run(CAT_ROWS, "swiglu_bwd", [=](hipStream_t q) {
-      return swiglu_bwd(ri, ri_in, gu, Ii, T, d16, r2, q);
+      return swiglu_bwd(ri, ri_in, gu, Ii, T, d16, r2, ks, q);
     }, 0, part_bytes(ri, T, I) + (double)T * (2 * I * 2 + 2 * I * 2)));
   }
   BSeg sg[1] = {wseg(w.wguT)};
+  sg[0].kscale = nullptr;
   LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, dgu16, 2 * I, sg, 1, T, 2 * I, nullptr, 0, &go_));
   nb = NormBwdArgs{};
   nb.in = row_in(go_);
@@ -519,6 +526,7 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   nb.dmid_out = nullptr;
   nb.g16 = g16;
   nb.rinv_out = rinv;
+  nb.g16_ks = l > 0 ? layers[l - 1].wdT.kscale : nullptr;  // g16 feeds layer l - 1's down dX
   nb.lora_at = shadow_at + (size_t)l * H * 3 * kRank;
   LLMT_HIP_TRY(run(CAT_ROWS, "norm_bwd_lora", [=](hipStream_t q) { return norm_bwd(nb, T, q); },
                    0, part_bytes(nb.in, T, H) + (double)T * (H * (4 + 4 + 4 + 2) + 48 * 4)));
