@@ -1543,12 +1543,6 @@ hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st) {
   if (!row_in_ok(a.in, a.H, "norm_bwd") || a.dh_col % 4) return hipErrorInvalidValue;
   const int P = (a.H + 4 * RT - 1) / (4 * RT);
   const bool lora = a.in.nterm > 0;
-  const int nr = rows_per_wg(T, P, lora ? 8 : 2);
-  const dim3 g((T + nr - 1) / nr);
-  // the stashed x and the incoming residual gradient are read once: past
-  // 32 MB a launch (C4: 33.5 MB each) nontemporal (C4 LoRA form 58.4 ->
-  // 56.9 us, the plain form unchanged)
-  const bool nt = (long long)T * a.H * 4 >= (32ll << 20);
   // the MFMA form of the LoRA term: three full-width q/k/v terms, hidx and
   // adapter rows 16 q, one piece a thread (H <= 4 RT), [NR][H] fp32 of LDS
   NormBwdArgs am = a;
@@ -1558,6 +1552,15 @@ hipError_t norm_bwd(const NormBwdArgs& a, int T, hipStream_t st) {
       ok = am.in.term[q].c0 == 0 && am.in.term[q].n == a.H && am.in.term[q].hidx == q * R;
     if (!ok) am.lora_at = nullptr;
   }
+  // large T: the VALU LoRA form shares its adapter values over 8 rows; the
+  // MFMA form runs 4 (128 VGPRs, two workgroups a CU: C4 50.7 -> 49.0 us
+  // against 8 rows at 229 VGPRs; 2 rows 59 us)
+  const int nr = rows_per_wg(T, P, lora ? (am.lora_at ? 4 : 8) : 2);
+  const dim3 g((T + nr - 1) / nr);
+  // the stashed x and the incoming residual gradient are read once: past
+  // 32 MB a launch (C4: 33.5 MB each) nontemporal (C4 LoRA form 58.4 ->
+  // 56.9 us, the plain form unchanged)
+  const bool nt = (long long)T * a.H * 4 >= (32ll << 20);
   auto rows = [&](auto nr_, auto lora_) {
     constexpr int NR = decltype(nr_)::value;
     constexpr bool LO = decltype(lora_)::value;

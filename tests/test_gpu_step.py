@@ -76,19 +76,26 @@ def test_adamw_step_matches_oracle(small, dev):
     zeros = torch.zeros(ctx.lora_numel, device=dev)
     ctx.lora_set("m", zeros)
     ctx.lora_set("v", zeros)
-    loss = ctx.step(small["tok"], small["tgt"], hp, 1)
-    assert abs(loss - small["loss_ref"]) < LOSS_TOL
-    ref.adamw_all(ad, small["grads_ref"], hp.lr, hp.beta1, hp.beta2, hp.eps, hp.wd, 1)
-    want = llmt.flatten_adapters(ad)
-    got = ctx.lora_get("param").cpu()
-    assert rel_l2(got, want) < GRAD_TOL
-    want_m = llmt.flatten_adapters(ad, attr=("mA", "mB"))
-    assert rel_l2(ctx.lora_get("m").cpu(), want_m) < GRAD_TOL
-    # second step: the forward now reads the fp16 shadows AdamW refreshed
-    loss2 = ctx.step(small["tok"], small["tgt"], hp, 2)
-    ad2 = [{p: ref.Adapter(a.A, a.B) for p, a in d.items()} for d in ad]
-    loss2_ref, _, _ = oracle_grads(small["W"], ad2, small["tok"].cpu(), small["tgt"].cpu(), SMALL)
-    assert abs(loss2 - float(loss2_ref)) < LOSS_TOL
+    try:
+        loss = ctx.step(small["tok"], small["tgt"], hp, 1)
+        assert abs(loss - small["loss_ref"]) < LOSS_TOL
+        ref.adamw_all(ad, small["grads_ref"], hp.lr, hp.beta1, hp.beta2, hp.eps, hp.wd, 1)
+        want = llmt.flatten_adapters(ad)
+        got = ctx.lora_get("param").cpu()
+        assert rel_l2(got, want) < GRAD_TOL
+        want_m = llmt.flatten_adapters(ad, attr=("mA", "mB"))
+        assert rel_l2(ctx.lora_get("m").cpu(), want_m) < GRAD_TOL
+        # second step: the forward now reads the fp16 shadows AdamW refreshed
+        loss2 = ctx.step(small["tok"], small["tgt"], hp, 2)
+        ad2 = [{p: ref.Adapter(a.A, a.B) for p, a in d.items()} for d in ad]
+        loss2_ref, _, _ = oracle_grads(small["W"], ad2, small["tok"].cpu(), small["tgt"].cpu(),
+                                       SMALL)
+        assert abs(loss2 - float(loss2_ref)) < LOSS_TOL
+    finally:
+        # the module's later tests compare against the fixture's adapters
+        ctx.lora_set("param", llmt.flatten_adapters(small["ad"]).to(dev))
+        ctx.lora_set("m", zeros)
+        ctx.lora_set("v", zeros)
 
 
 def test_lora_save_load_roundtrip(small, tmp_path, dev):
