@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <utility>
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -49,6 +50,24 @@ __device__ __forceinline__ floatx4 mfma16(half8 a, half8 b, floatx4 c) {
 template <int CTRL>
 __device__ __forceinline__ float dpp16(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// Lane L of each 16-lane row, broadcast to the whole row (gfx950's DPP
+// row_newbcast:L, control 0x150 + L): a VALU operand, so a per-rank
+// broadcast needs no v_readlane into an SGPR (and none of the wait states a
+// VALU read of a VALU-written SGPR takes).
+template <int L>
+__device__ __forceinline__ float bcast16(float v) {
+  static_assert(L >= 0 && L < 16, "lane within a row");
+  // every lane has a source lane, so bound_ctrl changes nothing but lets
+  // the compiler fold the move into the consumer as its DPP operand
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + L, 0xF, 0xF, true));
+}
+// f(std::integral_constant<int, i>) for i = 0 .. N - 1, unrolled.
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  [&]<int... I>(std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+  }(std::make_integer_sequence<int, N>{});
 }
 __device__ __forceinline__ float max16(float v) {
   v = fmaxf(v, dpp16<0xB1>(v));

@@ -379,12 +379,12 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(const QkvPostArgs a, int 
     float v0 = x0[i], v1 = x1[i];
     if (lora) {
       float acc0 = 0.f, acc1 = 0.f;
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const float h = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hv[i]), r));
-        acc0 += h * b0[r];
-        acc1 += h * b1[r];
-      }
+      // lane r of every 16-lane row holds h[r]
+      static_for<R>([&](auto rc) {
+        const float h = bcast16<decltype(rc)::value>(hv[i]);
+        acc0 += h * b0[decltype(rc)::value];
+        acc1 += h * b1[decltype(rc)::value];
+      });
       v0 += acc0 * in.lscale;
       v1 += acc1 * in.lscale;
       // the first head of each projection stashes its 16 h columns
@@ -1112,12 +1112,12 @@ __global__ __launch_bounds__(256) void o_dx_post_kernel(const RowIn in,
     float v0 = x[i].x, v1 = x[i].y;
     if (lora) {
       float acc0 = 0.f, acc1 = 0.f;
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const float hr = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hv[i]), r));
-        acc0 += hr * b0[r];
-        acc1 += hr * b1[r];
-      }
+      // lane r of every 16-lane row holds h[r]
+      static_for<R>([&](auto rc) {
+        const float hr = bcast16<decltype(rc)::value>(hv[i]);
+        acc0 += hr * b0[decltype(rc)::value];
+        acc1 += hr * b1[decltype(rc)::value];
+      });
       v0 += acc0 * in.lscale;
       v1 += acc1 * in.lscale;
       if (h == 0 && lane < R) dh_out[(long long)t * 64 + 3 * R + lane] = hv[i] * rs;
