@@ -915,6 +915,7 @@ __global__ __launch_bounds__(RT) void norm_bwd_rows_kernel(const NormBwdArgs a, 
   float4 v[NR], hv[NR];
   load_rows<NR, true>(a.in, t0, T, H, v, hv);
   const float4 ww = ld4(a.w + cc);
+  const float4 ks4 = a.g16_ks ? ldh4(a.g16_ks + cc) : make_float4(1.f, 1.f, 1.f, 1.f);
 #pragma unroll
   for (int i = 0; i < NR; ++i) {
     if (LORA) store_h(a.in, hv[i], hs[i]);
@@ -946,7 +947,6 @@ __global__ __launch_bounds__(RT) void norm_bwd_rows_kernel(const NormBwdArgs a, 
     s2[NR + i] = live ? x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w : 0.f;
   }
   block_sums<2 * NR>(s2, red);
-  const float4 ks4 = a.g16_ks ? ldh4(a.g16_ks + cc) : make_float4(1.f, 1.f, 1.f, 1.f);
   float amax[NR];
 #pragma unroll
   for (int i = 0; i < NR; ++i) {
@@ -1210,6 +1210,14 @@ __global__ __launch_bounds__(RT) void qk_bwd_kernel(const QkBwdArgs a) {
   const int pos = t % a.S;
   const float cs = a.cosT[pos * (HD / 2) + lane], sn = a.sinT[pos * (HD / 2) + lane];
   const float* g = a.dqkv + (long long)t * a.ld_dqkv;
+  // the operand's per-column factors of this thread's eight columns (one
+  // 16-byte load with the row's first loads)
+  const int c8 = 8 * (int)threadIdx.x;
+  const bool own8 = NT <= 8 * RT && c8 < NT;
+  half8 ks8;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ks8[e] = (_Float16)1.0f;
+  if (a.g16_ks && own8) ks8 = *reinterpret_cast<const half8*>(a.g16_ks + c8);
   auto head = [&](int hh, float d0, float d1, float x0, float x1, float w0,
                   float w1) __attribute__((always_inline)) {
     const int base = hh * HD;
@@ -1260,6 +1268,41 @@ __global__ __launch_bounds__(RT) void qk_bwd_kernel(const QkBwdArgs a) {
     for (int c = Q + KV + threadIdx.x; c < NT; c += RT) ds[c] = g[c];
   }
   __syncthreads();
+  // the operand is times the per-column factor when one is given (dy32, the
+  // fp32 gradient, is not); a thread rescales only the columns it owns
+  // NT <= 8 RT (Qwen3-1.7B: 4096 = 8 x 512): thread i owns the eight
+  // columns 8 i .., so its fp32 reads of ds, its factors and its fp16
+  // operand store are 16 bytes each.  The operand is times the per-column
+  // factor when one is given (dy32, the fp32 gradient, is not).
+  if (NT <= 8 * RT) {
+    float v[8];
+    float amax = 0.f;
+    if (own8) {
+      const float4 lo = *reinterpret_cast<const float4*>(&ds[c8]);
+      const float4 hi = *reinterpret_cast<const float4*>(&ds[c8 + 4]);
+      if (a.dy32) {
+        *reinterpret_cast<float4*>(a.dy32 + (long long)t * NT + c8) = lo;
+        *reinterpret_cast<float4*>(a.dy32 + (long long)t * NT + c8 + 4) = hi;
+      }
+      v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
+      v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[e] *= (float)ks8[e];
+        amax = fmaxf(amax, fabsf(v[e]));
+      }
+    }
+    amax = block_max<RW>(amax, red);
+    const float sc = pow2_scale_for(amax);
+    if (threadIdx.x == 0) a.rinv_out[t] = 1.0f / sc;
+    if (own8) {
+      half8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (_Float16)(v[e] * sc);
+      *reinterpret_cast<half8*>(a.g16 + (long long)t * NT + c8) = o;
+    }
+    return;
+  }
   float amax = 0.f;
   for (int c = threadIdx.x; c < NT; c += RT) {
     const float v = ds[c];
@@ -1270,6 +1313,12 @@ __global__ __launch_bounds__(RT) void qk_bwd_kernel(const QkBwdArgs a) {
   const float sc = pow2_scale_for(amax);
   if (threadIdx.x == 0) a.rinv_out[t] = 1.0f / sc;
   for (int c = threadIdx.x; c < NT; c += RT) a.g16[(long long)t * NT + c] = (_Float16)(ds[c] * sc);
+}
+
+__global__ void nonzero_scales_kernel(const _Float16* __restrict__ s, int n,
+                                      _Float16* __restrict__ out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = s[i] == (_Float16)0.0f ? (_Float16)1.0f : s[i];
 }
 
 // x_out = x; xn = fp16(rmsnorm(x) * w).
@@ -1374,6 +1423,13 @@ static bool row_in_ok(const RowIn& in, int n, const char* who, bool split_col_ok
 hipError_t copy_norm(const float* x, const float* w, float eps, int H, int T, float* x_out,
                      _Float16* xn, hipStream_t st) {
   hipLaunchKernelGGL(copy_norm_kernel, dim3(T), dim3(RT), 0, st, x, w, eps, H, x_out, xn);
+  LLMT_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+hipError_t nonzero_scales(const _Float16* s, int n, _Float16* out, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(nonzero_scales_kernel, dim3((n + 255) / 256), dim3(256), 0, st, s, n, out);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
@@ -1675,6 +1731,10 @@ hipError_t o_dx_post(const RowIn& in, const float* rinv_in, const _Float16* o16,
 
 hipError_t qk_bwd(const QkBwdArgs& a, int T, hipStream_t st) {
   const int NT = (a.nq + 2 * a.nkv) * HD;
+  if (a.g16_ks && NT > 8 * RT) {
+    set_error("qk_bwd: operand factors need Q + 2 KV <= %d (got %d)", 8 * RT, NT);
+    return hipErrorInvalidValue;
+  }
   const int hpw = (a.nq + a.nkv + RW - 1) / RW;
   const size_t lds = NT * sizeof(float);
   const char* e = getenv("LLMT_QK_BWD_HOIST");

@@ -217,6 +217,7 @@ AdamShadow Ctx::shadow_desc() const {
   sh.a_o = sh_a_o;
   sh.bt_qkv = sh_bt_qkv;
   sh.bt_o = sh_bt_o;
+  sh.bt_ks = dx_ks;
   return sh;
 }
 
@@ -467,12 +468,14 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   nb.dmid_out = nullptr;
   nb.g16 = og16;
   nb.rinv_out = ro(l);
+  nb.g16_ks = dx_ks ? dx_ks + (size_t)l * (NT + H) + NT : nullptr;  // the O dX's per-k factors
   // partials, x and the residual gradient in; the residual gradient and its
   // fp16 operand out
   LLMT_HIP_TRY(run(CAT_ROWS, "norm_bwd", [=](hipStream_t q) { return norm_bwd(nb, T, q); }, 0,
                    part_bytes(nb.in, T, H) + (double)T * H * (4 + 4 + 4 + 2)));
   // O projection dX (+ dh_o through the B_o^T rows)
   BSeg so[2] = {wseg(w.woT), hseg(shadow_ptr(l, sh_bt_o), kRank, H)};
+  if (dx_ks) so[0].kscale = nullptr;  // og16 carries it (B^T rows stored / s')
   const LoraTerm tbo[1] = {{shadow_rm + (size_t)l * shadow_per_layer + sh_a_o, 0, Q, 0, Q, 0}};
   LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, og16, H, so, 2, T, H, nullptr, 0, &go_));
   {
@@ -501,11 +504,13 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   qb.cosT = cosT; qb.sinT = sinT;
   qb.S = S; qb.nq = nq; qb.nkv = nkv; qb.eps = eps;
   qb.dy32 = nullptr; qb.g16 = qg16; qb.rinv_out = rq(l);
+  qb.g16_ks = dx_ks ? dx_ks + (size_t)l * (NT + H) : nullptr;  // the Q/K/V dX's per-k factors
   // dq/dk/dv (fp32) and q/k raw (fp16) in, the fp16 operand out
   LLMT_HIP_TRY(run(CAT_ROWS, "qk_bwd", [=](hipStream_t q) { return qk_bwd(qb, T, q); }, 0,
                    (double)T * (NT * 4 + (Q + KV) * 2 + NT * 2)));
   // Q/K/V dX (+ dh_q, dh_k, dh_v through the B^T rows), attention norm bwd
   BSeg sq[2] = {wseg(w.wqkvT), hseg(shadow_ptr(l, sh_bt_qkv), 3 * kRank, NT)};
+  if (dx_ks) sq[0].kscale = nullptr;  // qg16 carries it (B^T rows stored / s')
   const _Float16* a_qkv = shadow_rm + (size_t)l * shadow_per_layer + sh_a_qkv;
   const LoraTerm tbq[3] = {{a_qkv, 0, H, 0, H, 0},
                            {a_qkv, kRank, H, 0, H, kRank},
