@@ -40,7 +40,8 @@ struct Launch {
 // One frozen weight matrix as a GEMM B operand: fragment-packed fp16 or int8
 // rows of length ld (the reduction dimension), with the int8 scale either per
 // row (colscale, forward layout [out, in]) or per reduction index (kscale,
-// transposed layout [in, out]).
+// transposed layout [in, out]; the dX GEMMs leave it to the writers of
+// their fp16 operands, which fold it in per column).
 struct WMat {
   const void* p = nullptr;
   const _Float16* colscale = nullptr;

@@ -15,8 +15,8 @@ namespace llmt {
 // optional fp16 colscale[rows] multiplies the result columns).
 struct BSeg {
   const void* ptr;
-  const _Float16* colscale;  // int8 [out, in] layout: per output row n
-  const _Float16* kscale;    // int8 [in, out] layout: per reduction index k
+  const _Float16* colscale;  // int8: per output row n (the transposed backward copies take
+                             // their per-k scale from the A operand's writer instead)
   int rows;
   int ld;
   int is_i8;
