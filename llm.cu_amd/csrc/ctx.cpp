@@ -267,12 +267,13 @@ static hipError_t put_f16(Ctx* c, const void* src, int rows, int cols, const WMa
   return pack_f16((const _Float16*)src, cols, 1, cols, rows, (_Float16*)b.p, b.ld, 0, r0, c->st);
 }
 
+// Rows whose fp16 scale is 0 are packed as zeros (both copies).
 static hipError_t put_i8(Ctx* c, const int8_t* src, const void* scale, int rows, int cols,
                          const WMat& f, int r0, const WMat& b) {
-  LLMT_HIP_TRY(pack_i8(src, cols, 0, rows, cols, (int8_t*)f.p, f.ld, r0, 0, c->st));
-  LLMT_HIP_TRY(hipMemcpyAsync((_Float16*)f.colscale + r0, scale, (size_t)rows * 2,
-                              hipMemcpyDefault, c->st));
-  return pack_i8(src, cols, 1, cols, rows, (int8_t*)b.p, b.ld, 0, r0, c->st);
+  const _Float16* sc = f.colscale + r0;
+  LLMT_HIP_TRY(hipMemcpyAsync((_Float16*)sc, scale, (size_t)rows * 2, hipMemcpyDefault, c->st));
+  LLMT_HIP_TRY(pack_i8(src, cols, 0, rows, cols, (int8_t*)f.p, f.ld, r0, 0, c->st, sc));
+  return pack_i8(src, cols, 1, cols, rows, (int8_t*)b.p, b.ld, 0, r0, c->st, sc);
 }
 
 static int put_norms(Ctx* c, Layer& w, const float* attn_norm, const float* ffn_norm,

@@ -952,9 +952,13 @@ __global__ __launch_bounds__(256) void reduce_lora_kernel(const ReduceArgs a) {
 // (row length K) from a row-major source (leading dimension lds): if
 // transpose, element (i, j) of the destination block is src[j][i], else
 // src[i][j].  One thread per 8-element piece; C % 8 == 0, k0 % 8 == 0.
+// int8: zs (may be NULL) is the fp16 scale of each source row; a row whose
+// scale is 0 is stored as zeros, so its weights are 0 in the backward GEMMs
+// too, which take no scale for it (their operands carry a factor of 1 there).
 template <typename T>
 __global__ void pack_kernel(const T* __restrict__ src, long long lds, int transpose, int R, int C,
-                            T* __restrict__ dst, long long K, int row0, int k0) {
+                            T* __restrict__ dst, long long K, int row0, int k0,
+                            const _Float16* __restrict__ zs) {
   const long long np = (long long)R * (C / 8);
   for (long long p = (long long)blockIdx.x * blockDim.x + threadIdx.x; p < np;
        p += (long long)gridDim.x * blockDim.x) {
@@ -968,8 +972,11 @@ __global__ void pack_kernel(const T* __restrict__ src, long long lds, int transp
     }
     T v[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      v[e] = transpose ? src[(long long)(jp * 8 + e) * lds + i] : src[(long long)i * lds + jp * 8 + e];
+    for (int e = 0; e < 8; ++e) {
+      const int sr = transpose ? jp * 8 + e : i;  // source row
+      v[e] = transpose ? src[(long long)sr * lds + i] : src[(long long)i * lds + jp * 8 + e];
+      if (zs && zs[sr] == (_Float16)0.0f) v[e] = T(0);
+    }
     T* d = dst + packed_index(row0 + i, k0 + jp * 8, K);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -1398,20 +1405,20 @@ hipError_t pack_f16(const _Float16* src, long long lds, int transpose, int R, in
   }
   const long long np = (long long)R * (C / 8);
   hipLaunchKernelGGL(pack_kernel<_Float16>, dim3(grid1d(np, 256)), dim3(256), 0, st, src, lds,
-                     transpose, R, C, dst, K, row0, k0);
+                     transpose, R, C, dst, K, row0, k0, nullptr);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }
 
 hipError_t pack_i8(const int8_t* src, long long lds, int transpose, int R, int C, int8_t* dst,
-                   long long K, int row0, int k0, hipStream_t st) {
+                   long long K, int row0, int k0, hipStream_t st, const _Float16* zs) {
   if (C % 8 || k0 % 8 || K % 32) {
     set_error("pack_i8: C, k0 must be multiples of 8 and K of 32");
     return hipErrorInvalidValue;
   }
   const long long np = (long long)R * (C / 8);
   hipLaunchKernelGGL(pack_kernel<int8_t>, dim3(grid1d(np, 256)), dim3(256), 0, st, src, lds,
-                     transpose, R, C, dst, K, row0, k0);
+                     transpose, R, C, dst, K, row0, k0, zs);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }

@@ -97,9 +97,11 @@ hipError_t reduce_lora(const ReduceArgs& a, hipStream_t st);
 hipError_t pack_f16(const _Float16* src, long long lds, int transpose, int R, int C, _Float16* dst,
                     long long K, int row0, int k0, hipStream_t st);
 // pack_i8 stores each int8 x biased, as the byte x + 128 (x ^ 0x80), which
-// the GEMMs' int8 -> fp16 conversion expects.
+// the GEMMs' int8 -> fp16 conversion expects; zs (NULL: none) is the fp16
+// scale of each source row (the block's rows, or its columns when
+// transposed), and rows whose scale is 0 are stored as zeros.
 hipError_t pack_i8(const int8_t* src, long long lds, int transpose, int R, int C, int8_t* dst,
-                   long long K, int row0, int k0, hipStream_t st);
+                   long long K, int row0, int k0, hipStream_t st, const _Float16* zs = nullptr);
 
 // ---------------------------------------------------------------- layout
 hipError_t transpose_f16(const _Float16* src, int rows, int cols, int lds, _Float16* dst, int ldd,

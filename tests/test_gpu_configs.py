@@ -554,13 +554,58 @@ def test_c4_full_size_properties(dev):
 
 
 # ------------------------------------------------------------------ large-T path
-# T = B x S >= 1024 runs every frozen-weight GEMM on the 256 x 128 tile kernel
-# (fp16 and int8 B operands, LoRA segments in the last column tile, per-row
-# and per-k int8 scales); checked against the oracle on the small model.
+# T = B x S >= 1024 runs every frozen-weight GEMM on the 256 x 256 tile kernel
+# (fp16 and int8 B operands, LoRA rows in the column tiles, per-row int8
+# scales, the dX GEMMs' per-k scales carried by their operands); checked
+# against the oracle on the small model.
 
 def _small_dims():
     from helpers import SMALL
     return SMALL
+
+
+@pytest.mark.parametrize("batch,seq", [(2, 64), (4, 256)])
+def test_int8_zero_scale_channels_match_oracle(dev, batch, seq):
+    """int8 weights with output channels whose fp16 scale is 0, in every
+    projection: an all-zero row, and (q, k, v, o) a row below 4e-6 whose scale
+    rounds to 0 in fp16 while its int8 values do not.  The dX GEMMs take the
+    per-k scale from their operands' writers, which use a factor of 1 for such
+    a channel (0 would divide the LoRA B^T rows of the Q/K/V and O dX by zero)
+    and whose packed int8 rows are stored as zeros; the step matches the
+    oracle on the dequantised weights at T = 128 (small-M GEMMs) and T = 1024
+    (large tiles)."""
+    from oracle.configs import quantize_model_int8
+    d = _small_dims()
+    print(f"case: int8 zero-scale channels, B{batch} S{seq}", flush=True)
+    W, ad, tok, tgt, _ = config_model(d, batch=batch, seq_len=seq, seed=1013)
+    chans = {"wq": (5, 130), "wk": (3, 70), "wv": (7, 100), "wo": (11, 200),
+             "w_gate": (2,), "w_up": (9,), "w_down": (4,)}
+    for lw in W.layers:
+        for name, rows in chans.items():
+            w = getattr(lw, name).float().clone()
+            w[rows[0]] = 0.0
+            if len(rows) > 1:
+                w[rows[1]] *= 1e-5  # |w| < 1e-6: the fp16 scale underflows to 0
+            setattr(lw, name, w)
+    W, qs = quantize_model_int8(W)
+    for l in range(d.n_layers):
+        for name, rows in chans.items():
+            q, sc16 = qs[(l, name)]
+            assert sc16[rows[0]] == 0 and not q[rows[0]].any()
+            if len(rows) > 1:  # the case is exercised: scale 0, int8 values not
+                assert sc16[rows[1]] == 0 and q[rows[1]].any()
+    loss_ref, grads_ref, _ = oracle_grads(W, ad, tok, tgt, d)
+    ctx = llmt.Context(llmt.make_dims(d), batch, seq, int8=True)
+    try:
+        _upload_i8(ctx, W, qs, dev)
+        ctx.lora_set("param", llmt.flatten_adapters(ad).to(dev))
+        loss = ctx.forward_backward(tok.to(dev), tgt.to(dev))
+        assert math.isfinite(loss) and abs(loss - float(loss_ref)) < LOSS_TOL
+        errs = grad_errors(ctx.lora_get("grad"), grads_ref, d)
+        print("zero-scale worst", max(errs.items(), key=lambda kv: kv[1]), flush=True)
+        assert max(errs.values()) < GRAD_TOL
+    finally:
+        ctx.close()
 
 
 @pytest.mark.parametrize("int8", [False, True])
