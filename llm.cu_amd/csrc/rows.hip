@@ -1303,10 +1303,16 @@ __global__ __launch_bounds__(RT) void qk_bwd_kernel(const QkBwdArgs a) {
     }
     return;
   }
+  // wider rows: a column a thread per pass (each thread rescales only the
+  // columns it owns)
   float amax = 0.f;
   for (int c = threadIdx.x; c < NT; c += RT) {
-    const float v = ds[c];
+    float v = ds[c];
     if (a.dy32) a.dy32[(long long)t * NT + c] = v;
+    if (a.g16_ks) {
+      v *= (float)a.g16_ks[c];
+      ds[c] = v;
+    }
     amax = fmaxf(amax, fabsf(v));
   }
   amax = block_max<RW>(amax, red);
@@ -1731,10 +1737,6 @@ hipError_t o_dx_post(const RowIn& in, const float* rinv_in, const _Float16* o16,
 
 hipError_t qk_bwd(const QkBwdArgs& a, int T, hipStream_t st) {
   const int NT = (a.nq + 2 * a.nkv) * HD;
-  if (a.g16_ks && NT > 8 * RT) {
-    set_error("qk_bwd: operand factors need Q + 2 KV <= %d (got %d)", 8 * RT, NT);
-    return hipErrorInvalidValue;
-  }
   const int hpw = (a.nq + a.nkv + RW - 1) / RW;
   const size_t lds = NT * sizeof(float);
   const char* e = getenv("LLMT_QK_BWD_HOIST");

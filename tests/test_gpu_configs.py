@@ -608,6 +608,28 @@ def test_int8_zero_scale_channels_match_oracle(dev, batch, seq):
         ctx.close()
 
 
+def test_int8_wide_qkv_rows_match_oracle(dev):
+    """int8 weights with 32 query / 8 KV heads: the Q/K/V operand rows are
+    6144 wide, past the 4096 the QK-norm backward writes eight columns a
+    thread, so its per-column int8 factors take the column-a-pass form."""
+    d = ref.Dims(hidden=256, n_layers=1, n_heads=32, n_kv_heads=8, head_dim=128,
+                 intermediate=512, vocab=2048)
+    print("case: int8, 32/8 heads (Q + 2 KV = 6144), B2 S64", flush=True)
+    W, ad, tok, tgt, qs = config_model(d, batch=2, seq_len=64, seed=1014, int8=True)
+    loss_ref, grads_ref, _ = oracle_grads(W, ad, tok, tgt, d)
+    ctx = llmt.Context(llmt.make_dims(d), 2, 64, int8=True)
+    try:
+        _upload_i8(ctx, W, qs, dev)
+        ctx.lora_set("param", llmt.flatten_adapters(ad).to(dev))
+        loss = ctx.forward_backward(tok.to(dev), tgt.to(dev))
+        assert abs(loss - float(loss_ref)) < LOSS_TOL
+        errs = grad_errors(ctx.lora_get("grad"), grads_ref, d)
+        print("wide-qkv worst", max(errs.items(), key=lambda kv: kv[1]), flush=True)
+        assert max(errs.values()) < GRAD_TOL
+    finally:
+        ctx.close()
+
+
 @pytest.mark.parametrize("int8", [False, True])
 def test_large_tile_step_matches_oracle(dev, int8):
     d = _small_dims()
