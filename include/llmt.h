@@ -221,8 +221,7 @@ int llmt_set_layer_f16(llmt_ctx* ctx, int layer, const void* wq, const void* wk,
                        const float* k_norm);
 /* int8 [out, in] weights with fp16 per-output-row scales (the quantize.cu
  * recipe, produced e.g. by llmt_quantize_rows_i8).  A row whose fp16 scale is
- * 0 is taken as all zeros.  Also rewrites the adapters' fp16 operand copies
- * (the backward's LoRA B^T rows are stored divided by these scales). */
+ * 0 is taken as all zeros. */
 int llmt_set_layer_i8(llmt_ctx* ctx, int layer, const int8_t* const q[7], const void* const scale[7],
                       const float* attn_norm, const float* ffn_norm, const float* q_norm,
                       const float* k_norm);

@@ -184,7 +184,7 @@ static int head_ce_packed(hipStream_t st, const _Float16* hidden, const _Float16
   g.A = hidden;
   g.lda = H;
   g.nseg = 1;
-  g.seg[0] = BSeg{E, nullptr, V, H, 0};
+  g.seg[0] = BSeg{E, nullptr, nullptr, V, H, 0};
   gemm_finalize_segments(g);
   g.M = T;
   g.K = H;
@@ -201,7 +201,7 @@ static int head_ce_packed(hipStream_t st, const _Float16* hidden, const _Float16
   d.A = grad16;
   d.lda = V;
   d.nseg = 1;
-  d.seg[0] = BSeg{ET, nullptr, H, V, 0};
+  d.seg[0] = BSeg{ET, nullptr, nullptr, H, V, 0};
   gemm_finalize_segments(d);
   d.M = T;
   d.K = V;

@@ -73,7 +73,7 @@ static int gemm_common(const void* A, int lda, const void* B, int ldb, int is_i8
   g.A = (const _Float16*)A;
   g.lda = lda;
   g.nseg = 1;
-  g.seg[0] = BSeg{packed, (const _Float16*)scale, N, K, is_i8};
+  g.seg[0] = BSeg{packed, (const _Float16*)scale, nullptr, N, K, is_i8};
   gemm_finalize_segments(g);
   g.M = M;
   g.K = K;

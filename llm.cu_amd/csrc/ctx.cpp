@@ -83,12 +83,6 @@ int Ctx::init() {
   TRY_HIP(hipMemset(shadow, 0, shadow_per_layer * L * sizeof(_Float16)));
   TRY_HIP(hipMemset(shadow_rm, 0, shadow_per_layer * L * sizeof(_Float16)));
   TRY_HIP(hipMemset(shadow_at, 0, (size_t)L * H * 3 * R * sizeof(_Float16)));
-  if (wfmt == LLMT_WEIGHTS_I8) {  // ones until a layer's weights are set
-    const size_t n = (size_t)L * (NT + H);
-    TRY_PTR(dx_ks = alloc_n<_Float16>(n));
-    TRY_HIP(hipMemset(dx_ks, 0, n * sizeof(_Float16)));
-    TRY_HIP(nonzero_scales(dx_ks, (int)n, dx_ks, nullptr));
-  }
 
   // RoPE tables: angles in double, rounded once to fp32 (src/kernels/rope.cu:15-18).
   {
@@ -220,7 +214,6 @@ int Ctx::init() {
       const Stash& s = stash[l];
       float* dhl = dh(l);
       const _Float16* gql = gq16(l);
-      const _Float16* ks = dx_ks ? dx_ks + (size_t)l * (NT + H) : nullptr;  // dB operand factors
       auto g = [&](int proj, int is_b) {
         return lora_g + (size_t)l * lora_per_layer + seg_off[2 * proj + is_b];
       };
@@ -229,10 +222,10 @@ int Ctx::init() {
           {s.xn, 1, H, nullptr, H, dhl + 16, 64, g(1, 0), 0},
           {s.xn, 1, H, nullptr, H, dhl + 32, 64, g(2, 0), 0},
           {s.o16, 1, Q, nullptr, Q, dhl + 48, 64, g(3, 0), 0},
-          {gql, 1, NT, rq(l), Q, s.h + 0, 64, g(0, 1), 1, ks},
-          {gql + Q, 1, NT, rq(l), KV, s.h + 16, 64, g(1, 1), 1, ks ? ks + Q : nullptr},
-          {gql + Q + KV, 1, NT, rq(l), KV, s.h + 32, 64, g(2, 1), 1, ks ? ks + Q + KV : nullptr},
-          {go16(l), 1, H, ro(l), H, s.h + 48, 64, g(3, 1), 1, ks ? ks + NT : nullptr},
+          {gql, 1, NT, rq(l), Q, s.h + 0, 64, g(0, 1), 1},
+          {gql + Q, 1, NT, rq(l), KV, s.h + 16, 64, g(1, 1), 1},
+          {gql + Q + KV, 1, NT, rq(l), KV, s.h + 32, 64, g(2, 1), 1},
+          {go16(l), 1, H, ro(l), H, s.h + 48, 64, g(3, 1), 1},
       };
       for (int j = 0; j < kLoraJobs; ++j) jobs[(size_t)l * kLoraJobs + j] = js[j];
       if (l == 0)
@@ -331,12 +324,6 @@ int llmt_set_layer_i8(llmt_ctx* ctx, int layer, const int8_t* const q[7],
   TRY_HIP(put_i8(c, q[4], scale[4], I, H, w.wgu, 0, w.wguT));
   TRY_HIP(put_i8(c, q[5], scale[5], I, H, w.wgu, I, w.wguT));
   TRY_HIP(put_i8(c, q[6], scale[6], H, I, w.wd, 0, w.wdT));
-  // the Q/K/V and O dX operands' factors, then the packed B^T shadows that
-  // are stored divided by them
-  _Float16* ks = c->dx_ks + (size_t)layer * (c->NT + H);
-  TRY_HIP(nonzero_scales(w.wqkvT.kscale, c->NT, ks, c->st));
-  TRY_HIP(nonzero_scales(w.woT.kscale, H, ks + c->NT, c->st));
-  TRY_HIP(c->refresh_shadows());
   int rc = put_norms(c, w, attn_norm, ffn_norm, q_norm, k_norm);
   if (rc) return rc;
   TRY_HIP(hipStreamSynchronize(c->st));

@@ -40,8 +40,7 @@ struct Launch {
 // One frozen weight matrix as a GEMM B operand: fragment-packed fp16 or int8
 // rows of length ld (the reduction dimension), with the int8 scale either per
 // row (colscale, forward layout [out, in]) or per reduction index (kscale,
-// transposed layout [in, out]; the dX GEMMs leave it to the writers of
-// their fp16 operands, which fold it in per column).
+// transposed layout [in, out]).
 struct WMat {
   const void* p = nullptr;
   const _Float16* colscale = nullptr;
@@ -130,11 +129,6 @@ struct Ctx {
   // A_q | A_k | A_v transposed, [L][H][3 R] (the LoRA dx term's MFMA operand
   // in the attention norm's backward)
   _Float16* shadow_at = nullptr;
-  // int8 weights: per layer [Q + 2 KV + H] factors s' (the Q/K/V and O dX
-  // GEMMs' per-k weight scales, 0 read as 1), carried by those GEMMs' fp16
-  // operands instead of being applied in the GEMM; the packed B^T shadows
-  // hold B^T / s' and the dB reductions divide by s'.  NULL for fp16.
-  _Float16* dx_ks = nullptr;
   AdamHp* hp_dev = nullptr;
   AdamHp* host_hp = nullptr;
 

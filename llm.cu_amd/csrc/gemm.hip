@@ -109,6 +109,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
   int bi8[NF];
   int ncol[NF];
   const _Float16* cscale[NF];
+  const _Float16* kscale[NF];
   bool valid[NF];
 #pragma unroll
   for (int f = 0; f < NF; ++f) {
@@ -127,6 +128,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
     bptr[f] = (const char*)sg.ptr + ((rb16 * ksteps) * 512 + lane * 8) * (i8 ? 1 : 2);
     bi8[f] = i8;
     cscale[f] = sg.colscale ? sg.colscale + (nn - g.seg_start[s]) : nullptr;
+    kscale[f] = (I8 && sg.kscale) ? sg.kscale + (lane >> 4) * 8 : nullptr;
   }
 
   floatx4 acc[MF][NF];
@@ -137,6 +139,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
 
   u32x4 ra[ADIST][APT];
   u32x4 rb[RING][NF];
+  u32x4 rk[RING][NF];
 
   auto load_a = [&](int c, auto R) LLMT_INLINE {
     constexpr int set = decltype(R)::value;
@@ -171,6 +174,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
       if (I8 && bi8[f]) {
         const u32x2 q = *reinterpret_cast<const u32x2*>(bptr[f] + ss * 512);
         rb[st][f] = u32x4{q[0], q[1], 0u, 0u};
+        if (kscale[f]) rk[st][f] = *reinterpret_cast<const u32x4*>(kscale[f] + ss * KSTEP);
       } else {
         rb[st][f] = *reinterpret_cast<const u32x4*>(bptr[f] + ss * 1024);
       }
@@ -181,6 +185,9 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(const GemmArgs g) {
     half8 h;
     if (I8 && bi8[f]) {
       h = i8x8_to_h8(u32x2{rb[st][f][0], rb[st][f][1]});
+      if (kscale[f]) {
+        h = h * __builtin_bit_cast(half8, rk[st][f]);
+      }
     } else {
       h = __builtin_bit_cast(half8, rb[st][f]);
     }
@@ -320,7 +327,7 @@ __device__ __forceinline__ void wait_vm() {
 // block and K range (two extra MFMAs a wave per chunk, the fragment's 1 KB
 // a chunk moved by eight lanes of every wave), instead of a separate launch
 // that streamed the whole activation matrix again.
-template <bool I8, int S, int WNN, bool GLU = false, bool TL = false>
+template <bool I8, bool KS, int S, int WNN, bool GLU = false, bool TL = false>
 __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, int g_order,
                                                              const BSeg tail, int tail_c0) {
   // WNN waves across N (2: four waves of 128 x 128; 4: eight waves of 128 x 64)
@@ -328,9 +335,10 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
   constexpr int FPW = 16 / NW;                                 // A (and B) fragments each wave moves
   constexpr int ABYTES = 256 * KSTEP * 2;
   constexpr int BBYTES = 256 * KSTEP * (I8 ? 1 : 2);
-  constexpr int TOFF = ABYTES + BBYTES;                        // tail fragment slot
+  constexpr int KSBYTES = KS ? 256 : 0;
+  constexpr int TOFF = ABYTES + BBYTES + KSBYTES;              // tail fragment slot
   constexpr int SBYTES = TOFF + (TL ? 1024 : 0);
-  constexpr int OPS = 2 * FPW + (TL ? 1 : 0);                  // DMA issues per chunk per thread
+  constexpr int OPS = 2 * FPW + (KS ? 1 : 0) + (TL ? 1 : 0);   // DMA issues per chunk per thread
   static_assert(!(TL && GLU), "no tail with the SwiGLU epilogue");
   static_assert(!TL || WNN == 4, "the tail fragment is split over four column waves");
   __shared__ __attribute__((aligned(1024))) char smem[S * SBYTES];
@@ -370,7 +378,7 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
   const int c1 = (int)((long long)(sidx + 1) * ksteps / nsp);
 
   // issue pointers: wave w moves A fragments FPW w .. and B fragments FPW w ..
-  // of every chunk
+  // of every chunk (plus, with KS, k-scales through lane 0 of waves 0-3)
   const _Float16* asrc =
       g.A + (long long)(m0 + wave * FPW * 16 + (lane & 15)) * g.lda + (lane >> 4) * 8;
   const long long astep = 16LL * g.lda;
@@ -387,6 +395,7 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
                        : min((n0 >> 4) + f, (g.N >> 4) - 1);
     boff[j] = (long long)rb * ksteps * 512 * ES;
   }
+  const _Float16* ksrc = KS ? sg.kscale + (wave & 3) * 8 : nullptr;
   // tail fragment of this column tile (tiles past the last fragment load the
   // last one, unused, so every wave issues the same number of DMAs)
   const int ntf = TL ? tail.rows / 16 : 0;
@@ -410,6 +419,12 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
         dma16(src, dst);
       }
     }
+    if constexpr (KS) {
+      if (lane == 0 && wave < 4)
+        dma16(ksrc + (long long)cc * KSTEP, reinterpret_cast<_Float16*>(st + ABYTES + BBYTES + wave * 16));
+      else if (lane == 0)  // keep the per-thread DMA count uniform (a harmless re-read)
+        dma16(ksrc + (long long)cc * KSTEP, reinterpret_cast<_Float16*>(st + ABYTES + BBYTES + 64 + (wave & 3) * 16));
+    }
     if constexpr (TL) {  // wave w moves bytes 128 w .. 128 w + 127 of the fragment
       if (lane < 8) dma16(tsrc + (long long)cc * 512, reinterpret_cast<_Float16*>(st + TOFF + wave * 128));
     }
@@ -428,10 +443,11 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
   // right after its last MFMA, and chunk c + 1's B bytes (and k-scales,
   // tail fragment) are read at the top, dequantised after the last MFMA;
   // so LDS latency sits under the MFMAs and the registers stay one set.
-  half8 a[8], b[NFR], bt, btn, at[2], atn[2];
+  half8 a[8], b[NFR], bt, btn, ksn, at[2], atn[2];
   u32x2 bn8[NFR];
   half8 bn16[NFR];
   auto read_b = [&](const char* st) LLMT_INLINE {
+    if constexpr (KS) ksn = *reinterpret_cast<const half8*>(st + ABYTES + BBYTES + (lane >> 4) * 16);
 #pragma unroll
     for (int j = 0; j < NFR; ++j) {
       const int fr = wn * NFR + j;
@@ -455,6 +471,7 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
     for (int j = 0; j < NFR; ++j) {
       if constexpr (I8) {
         b[j] = i8x8_to_h8(bn8[j]);
+        if constexpr (KS) b[j] = b[j] * ksn;
       } else {
         b[j] = bn16[j];
       }
@@ -499,7 +516,7 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
     // first, then per row its MFMAs followed by the read that refills its A
     // register (left alone, the compiler sank all eight A reads below the
     // last MFMA, exposing their latency at the barrier)
-    __builtin_amdgcn_sched_group_barrier(0x100, (I8 ? NFR / 2 : NFR) + (TL ? 3 : 0), 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, (I8 ? NFR / 2 : NFR) + (KS ? 1 : 0) + (TL ? 3 : 0), 0);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, NFR, 0);
@@ -953,8 +970,8 @@ __global__ __launch_bounds__(256) void reduce_lora_kernel(const ReduceArgs a) {
 // transpose, element (i, j) of the destination block is src[j][i], else
 // src[i][j].  One thread per 8-element piece; C % 8 == 0, k0 % 8 == 0.
 // int8: zs (may be NULL) is the fp16 scale of each source row; a row whose
-// scale is 0 is stored as zeros, so its weights are 0 in the backward GEMMs
-// too, which take no scale for it (their operands carry a factor of 1 there).
+// scale is 0 is stored as zeros, so the packed values agree with the
+// dequantised weights whichever side applies the scale.
 template <typename T>
 __global__ void pack_kernel(const T* __restrict__ src, long long lds, int transpose, int R, int C,
                             T* __restrict__ dst, long long K, int row0, int k0,
@@ -1322,7 +1339,7 @@ hipError_t gemm_nt(const GemmArgs& g, hipStream_t st) {
     // XCD-contiguous tile runs: workgroup b goes to XCD b % 8, and the tiles
     // sharing an A row block then share that XCD's L2 (C4: +0.7% step rate)
     const int order = 1;
-    const bool i8 = gm.seg[0].is_i8;
+    const bool i8 = gm.seg[0].is_i8, ks = gm.seg[0].kscale != nullptr;
     if (gm.nseg != 1 || gm.N % 16 != 0) {
       set_error("gemm_nt: large tiles take one B segment with N %% 16 == 0 (N = %d, %d segments)",
                 gm.N, gm.nseg);
@@ -1344,24 +1361,27 @@ hipError_t gemm_nt(const GemmArgs& g, hipStream_t st) {
     const bool fold = lora_tail && !tl.is_i8 && tl.rows / 16 <= (gm.N + 255) / 256;
     const int tc0 = lora_tail ? g.seg_start[last] : 0;
     // ring depth 5 (int8) / 4 (fp16): 4 measured the same, 6 slower
-    auto go = [&](auto i8c, auto gluc, auto tlc) {
-      constexpr bool I8 = decltype(i8c)::value;
+    auto go = [&](auto i8c, auto ksc, auto gluc, auto tlc) {
+      constexpr bool I8 = decltype(i8c)::value, KS = decltype(ksc)::value;
       constexpr bool GL = decltype(gluc)::value, TLc = decltype(tlc)::value;
       constexpr int SD = I8 ? 5 : 4;
-      hipLaunchKernelGGL((gemm_dma_kernel<I8, SD, 4, GL, TLc>), gr, dim3(512), 0, st, gm, order,
+      hipLaunchKernelGGL((gemm_dma_kernel<I8, KS, SD, 4, GL, TLc>), gr, dim3(512), 0, st, gm, order,
                          tl, tc0);
     };
     using BT = std::integral_constant<bool, true>;
     using BF = std::integral_constant<bool, false>;
     if (gm.glu) {
-      if (!i8) go(BF(), BT(), BF());
-      else go(BT(), BT(), BF());
+      if (!i8) go(BF(), BF(), BT(), BF());
+      else if (ks) go(BT(), BT(), BT(), BF());
+      else go(BT(), BF(), BT(), BF());
     } else if (fold) {
-      if (!i8) go(BF(), BF(), BT());
-      else go(BT(), BF(), BT());
+      if (!i8) go(BF(), BF(), BF(), BT());
+      else if (ks) go(BT(), BT(), BF(), BT());
+      else go(BT(), BF(), BF(), BT());
     } else {
-      if (!i8) go(BF(), BF(), BF());
-      else go(BT(), BF(), BF());
+      if (!i8) go(BF(), BF(), BF(), BF());
+      else if (ks) go(BT(), BT(), BF(), BF());
+      else go(BT(), BF(), BF(), BF());
     }
     e = hipGetLastError();
     if (e == hipSuccess && lora_tail && !fold) {

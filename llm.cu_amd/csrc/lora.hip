@@ -120,9 +120,8 @@ __global__ __launch_bounds__(NTH) void lora_grad_mfma_kernel(const LoraGradJob* 
     for (int nb = 0; nb < 4; ++nb) {
       float4* o = reinterpret_cast<float4*>(jb.out + (long long)(c + nb) * R + r0);
       const float4 prev = accumulate ? *o : make_float4(0.f, 0.f, 0.f, 0.f);
-      const float f = jb.xcs ? lscale / (float)jb.xcs[c + nb] : lscale;
-      *o = make_float4(prev.x + f * acc[nb][0], prev.y + f * acc[nb][1], prev.z + f * acc[nb][2],
-                       prev.w + f * acc[nb][3]);
+      *o = make_float4(prev.x + lscale * acc[nb][0], prev.y + lscale * acc[nb][1],
+                       prev.z + lscale * acc[nb][2], prev.w + lscale * acc[nb][3]);
     }
   } else {  // out[16][ncols]: four consecutive columns of each rank
 #pragma unroll
@@ -221,14 +220,13 @@ __global__ __launch_bounds__(NTH) void lora_grad_mfma2_kernel(const LoraGradJob*
   // thread i finishes column cb + i (all 16 ranks), the waves in order
   const int col = cb + (int)threadIdx.x;
   if (col >= jb.ncols) return;
-  const float f = jb.out_is_B && jb.xcs ? lscale / (float)jb.xcs[col] : lscale;
 #pragma unroll
   for (int rr = 0; rr < R; ++rr) {
     float v = red[0][rr][threadIdx.x];
 #pragma unroll
     for (int q = 1; q < 4; ++q) v += red[q][rr][threadIdx.x];
     float* o = jb.out_is_B ? jb.out + (long long)col * R + rr : jb.out + (long long)rr * jb.ncols + col;
-    *o = (accumulate ? *o : 0.f) + f * v;
+    *o = (accumulate ? *o : 0.f) + lscale * v;
   }
 }
 
@@ -264,14 +262,7 @@ __device__ __forceinline__ ShadowPos shadow_pos(const AdamShadow& sh, long long 
 __device__ __forceinline__ void shadow_store(const AdamShadow& sh, long long i, float v) {
   const ShadowPos q = shadow_pos(sh, i);
   const _Float16 h = (_Float16)v;
-  _Float16 hp = h;  // the packed copy: B^T / s' where factors are given
-  if (sh.bt_ks) {
-    const long long l = i / sh.per_layer, lb = l * sh.shadow_per_layer;
-    const _Float16* ks = sh.bt_ks + l * (sh.nt + sh.d_out[3]);
-    if (q.base == lb + sh.bt_qkv) hp = (_Float16)(v / (float)ks[q.col]);
-    if (q.base == lb + sh.bt_o) hp = (_Float16)(v / (float)ks[sh.nt + q.col]);
-  }
-  sh.shadow[q.base + packed_index(q.row, q.col, q.len)] = hp;
+  sh.shadow[q.base + packed_index(q.row, q.col, q.len)] = h;
   sh.rm[q.base + q.row * q.len + q.col] = h;
   if (sh.at) {  // A of q, k, v: also at (layer, column, row) of the transposed copy
     const long long l = i / sh.per_layer, j = i - l * sh.per_layer;
@@ -457,13 +448,7 @@ __global__ __launch_bounds__(NTH) void adamw_shadow_kernel(float* __restrict__ p
   for (int u = 0; u < TPB; ++u) {
     const int col = (q < 3 ? sh.col_off[q] : 0) + 64 * (blockIdx.x * TPB + u) + c4;
     const half4 t = *reinterpret_cast<const half4*>(&bt[u][r][c4]);
-    half4 tp = t;  // the packed copy: B^T / s' where factors are given
-    if (sh.bt_ks) {
-      const _Float16* ks = sh.bt_ks + (long long)l * (sh.nt + sh.d_out[3]) + (q < 3 ? 0 : sh.nt) + col;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) tp[e] = (_Float16)((float)t[e] / (float)ks[e]);
-    }
-    *reinterpret_cast<half4*>(sh.shadow + base + packed_index(row, col, len)) = tp;
+    *reinterpret_cast<half4*>(sh.shadow + base + packed_index(row, col, len)) = t;
     *reinterpret_cast<half4*>(sh.rm + base + (long long)row * len + col) = t;
   }
 }

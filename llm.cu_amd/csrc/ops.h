@@ -15,8 +15,8 @@ namespace llmt {
 // optional fp16 colscale[rows] multiplies the result columns).
 struct BSeg {
   const void* ptr;
-  const _Float16* colscale;  // int8: per output row n (the transposed backward copies take
-                             // their per-k scale from the A operand's writer instead)
+  const _Float16* colscale;  // int8 [out, in] layout: per output row n
+  const _Float16* kscale;    // int8 [in, out] layout: per reduction index k
   int rows;
   int ld;
   int is_i8;
@@ -211,7 +211,6 @@ struct QkBwdArgs {
   float* dy32;        // [T, NT], may be NULL
   _Float16* g16;      // [T, NT], row t scaled by 1 / rinv_out[t]
   float* rinv_out;
-  const _Float16* g16_ks;  // NULL, or a per-column factor [NT] folded into g16
 };
 
 hipError_t embed_norm(const int* tok, const _Float16* E, int V, int H, const float* w, float eps,
@@ -253,9 +252,6 @@ hipError_t copy_norm(const float* x, const float* w, float eps, int H, int T, fl
 // A gradient row as the fp16 GEMM operand: dres = dy (may alias), g16 =
 // fp16(dy * ks * sc), rinv = 1 / sc with sc the row's power-of-two scale and
 // ks a per-column factor (1 when NULL).
-// out[i] = s[i], or 1 where s[i] is 0 (an all-zero int8 weight channel):
-// the factor an int8 dX GEMM's operand carries in place of the k-scale.
-hipError_t nonzero_scales(const _Float16* s, int n, _Float16* out, hipStream_t st);
 hipError_t grad_rows(const float* dy, int H, int T, float* dres, _Float16* g16, float* rinv,
                      const _Float16* ks, hipStream_t st);
 // dst[r][c] = (float) src[r][c] for a [rows, cols] block (lds, ldd).
@@ -332,7 +328,6 @@ struct LoraGradJob {
   long long ldg;
   float* out;
   int out_is_B;      // 0: out[16][ncols] (dA), 1: out[ncols][16] (dB)
-  const _Float16* xcs;  // NULL, or column c of X stands for X[:, c] * xcs[c] (dB only)
 };
 // The adapter-gradient jobs of `layers` consecutive layers (kLoraJobs per
 // layer, same order and column counts in every layer) in one launch; `jobs`
@@ -364,10 +359,6 @@ struct AdamShadow {
   int nt;
   long long shadow_per_layer;
   long long a_qkv, a_o, bt_qkv, bt_o;
-  // NULL, or per layer [nt + d_out[3]] factors s' (q | k | v columns, then
-  // o's): the packed B^T copy (the dX GEMMs' LoRA rows) holds B^T / s', its
-  // row-major twin B^T itself
-  const _Float16* bt_ks;
 };
 // hp is a device pointer (so a captured graph picks up new step counts).
 hipError_t adamw(float* p, const float* g, float* m, float* v, long long n, const AdamHp* hp,

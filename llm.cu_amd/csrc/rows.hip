@@ -1210,14 +1210,6 @@ __global__ __launch_bounds__(RT) void qk_bwd_kernel(const QkBwdArgs a) {
   const int pos = t % a.S;
   const float cs = a.cosT[pos * (HD / 2) + lane], sn = a.sinT[pos * (HD / 2) + lane];
   const float* g = a.dqkv + (long long)t * a.ld_dqkv;
-  // the operand's per-column factors of this thread's eight columns (one
-  // 16-byte load with the row's first loads)
-  const int c8 = 8 * (int)threadIdx.x;
-  const bool own8 = NT <= 8 * RT && c8 < NT;
-  half8 ks8;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) ks8[e] = (_Float16)1.0f;
-  if (a.g16_ks && own8) ks8 = *reinterpret_cast<const half8*>(a.g16_ks + c8);
   auto head = [&](int hh, float d0, float d1, float x0, float x1, float w0,
                   float w1) __attribute__((always_inline)) {
     const int base = hh * HD;
@@ -1271,9 +1263,10 @@ __global__ __launch_bounds__(RT) void qk_bwd_kernel(const QkBwdArgs a) {
   // the operand is times the per-column factor when one is given (dy32, the
   // fp32 gradient, is not); a thread rescales only the columns it owns
   // NT <= 8 RT (Qwen3-1.7B: 4096 = 8 x 512): thread i owns the eight
-  // columns 8 i .., so its fp32 reads of ds, its factors and its fp16
-  // operand store are 16 bytes each.  The operand is times the per-column
-  // factor when one is given (dy32, the fp32 gradient, is not).
+  // columns 8 i .., so its fp32 reads of ds and its fp16 operand store are
+  // 16 bytes each (eight 2-byte stores a thread column by column)
+  const int c8 = 8 * (int)threadIdx.x;
+  const bool own8 = c8 < NT;
   if (NT <= 8 * RT) {
     float v[8];
     float amax = 0.f;
@@ -1287,10 +1280,7 @@ __global__ __launch_bounds__(RT) void qk_bwd_kernel(const QkBwdArgs a) {
       v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
       v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        v[e] *= (float)ks8[e];
-        amax = fmaxf(amax, fabsf(v[e]));
-      }
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
     }
     amax = block_max<RW>(amax, red);
     const float sc = pow2_scale_for(amax);
@@ -1303,16 +1293,11 @@ __global__ __launch_bounds__(RT) void qk_bwd_kernel(const QkBwdArgs a) {
     }
     return;
   }
-  // wider rows: a column a thread per pass (each thread rescales only the
-  // columns it owns)
+  // wider rows: a column a thread per pass
   float amax = 0.f;
   for (int c = threadIdx.x; c < NT; c += RT) {
-    float v = ds[c];
+    const float v = ds[c];
     if (a.dy32) a.dy32[(long long)t * NT + c] = v;
-    if (a.g16_ks) {
-      v *= (float)a.g16_ks[c];
-      ds[c] = v;
-    }
     amax = fmaxf(amax, fabsf(v));
   }
   amax = block_max<RW>(amax, red);
@@ -1321,11 +1306,6 @@ __global__ __launch_bounds__(RT) void qk_bwd_kernel(const QkBwdArgs a) {
   for (int c = threadIdx.x; c < NT; c += RT) a.g16[(long long)t * NT + c] = (_Float16)(ds[c] * sc);
 }
 
-__global__ void nonzero_scales_kernel(const _Float16* __restrict__ s, int n,
-                                      _Float16* __restrict__ out) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) out[i] = s[i] == (_Float16)0.0f ? (_Float16)1.0f : s[i];
-}
 
 // x_out = x; xn = fp16(rmsnorm(x) * w).
 __global__ __launch_bounds__(RT) void copy_norm_kernel(const float* __restrict__ x,
@@ -1429,13 +1409,6 @@ static bool row_in_ok(const RowIn& in, int n, const char* who, bool split_col_ok
 hipError_t copy_norm(const float* x, const float* w, float eps, int H, int T, float* x_out,
                      _Float16* xn, hipStream_t st) {
   hipLaunchKernelGGL(copy_norm_kernel, dim3(T), dim3(RT), 0, st, x, w, eps, H, x_out, xn);
-  LLMT_LAUNCH_CHECK();
-  return hipSuccess;
-}
-
-hipError_t nonzero_scales(const _Float16* s, int n, _Float16* out, hipStream_t st) {
-  if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(nonzero_scales_kernel, dim3((n + 255) / 256), dim3(256), 0, st, s, n, out);
   LLMT_LAUNCH_CHECK();
   return hipSuccess;
 }

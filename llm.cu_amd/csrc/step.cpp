@@ -173,6 +173,7 @@ BSeg Ctx::wseg(const WMat& w) const {
   BSeg s{};
   s.ptr = w.p;
   s.colscale = w.colscale;
+  s.kscale = w.kscale;
   s.rows = w.rows;
   s.ld = w.ld;
   s.is_i8 = w.i8;
@@ -216,7 +217,6 @@ AdamShadow Ctx::shadow_desc() const {
   sh.a_o = sh_a_o;
   sh.bt_qkv = sh_bt_qkv;
   sh.bt_o = sh_bt_o;
-  sh.bt_ks = dx_ks;
   return sh;
 }
 
@@ -434,6 +434,7 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   // whose scale their fp16 operands (g16, dgu16) already carry: the writers
   // fold it in per column, so these GEMMs dequantise without it.
   BSeg sd[1] = {wseg(w.wdT)};
+  sd[0].kscale = nullptr;
   LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, g16, H, sd, 1, T, H, nullptr, 0, &go_, nullptr, nullptr, nullptr,
                     nullptr, true));
   {
@@ -450,6 +451,7 @@ hipError_t Ctx::layer_bwd(int l, int B) {
     }, 0, part_bytes(ri, T, I) + (double)T * (2 * I * 2 + 2 * I * 2)));
   }
   BSeg sg[1] = {wseg(w.wguT)};
+  sg[0].kscale = nullptr;
   LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, dgu16, 2 * I, sg, 1, T, 2 * I, nullptr, 0, &go_));
   nb = NormBwdArgs{};
   nb.in = row_in(go_);
@@ -465,13 +467,15 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   nb.dmid_out = nullptr;
   nb.g16 = og16;
   nb.rinv_out = ro(l);
-  nb.g16_ks = dx_ks ? dx_ks + (size_t)l * (NT + H) + NT : nullptr;  // the O dX's per-k factors
   // partials, x and the residual gradient in; the residual gradient and its
   // fp16 operand out
   LLMT_HIP_TRY(run(CAT_ROWS, "norm_bwd", [=](hipStream_t q) { return norm_bwd(nb, T, q); }, 0,
                    part_bytes(nb.in, T, H) + (double)T * H * (4 + 4 + 4 + 2)));
   // O projection dX (+ dh_o through the B_o^T rows)
-  // (int8: og16 carries the per-k scale, the packed B^T rows are stored / s')
+  // (int8: this GEMM and the Q/K/V dX apply the per-k weight scale in the
+  // kernel; folded into their operands, the LoRA B^T rows riding in the same
+  // A stream would need B^T / s, and dh, in the operands' units, would grow
+  // by ~1 / s past the fp16 range of the LoRA norm backward's MFMA operand)
   BSeg so[2] = {wseg(w.woT), hseg(shadow_ptr(l, sh_bt_o), kRank, H)};
   const LoraTerm tbo[1] = {{shadow_rm + (size_t)l * shadow_per_layer + sh_a_o, 0, Q, 0, Q, 0}};
   LLMT_HIP_TRY(gemm(CAT_GEMM_BWD, og16, H, so, 2, T, H, nullptr, 0, &go_));
@@ -501,12 +505,10 @@ hipError_t Ctx::layer_bwd(int l, int B) {
   qb.cosT = cosT; qb.sinT = sinT;
   qb.S = S; qb.nq = nq; qb.nkv = nkv; qb.eps = eps;
   qb.dy32 = nullptr; qb.g16 = qg16; qb.rinv_out = rq(l);
-  qb.g16_ks = dx_ks ? dx_ks + (size_t)l * (NT + H) : nullptr;  // the Q/K/V dX's per-k factors
   // dq/dk/dv (fp32) and q/k raw (fp16) in, the fp16 operand out
   LLMT_HIP_TRY(run(CAT_ROWS, "qk_bwd", [=](hipStream_t q) { return qk_bwd(qb, T, q); }, 0,
                    (double)T * (NT * 4 + (Q + KV) * 2 + NT * 2)));
   // Q/K/V dX (+ dh_q, dh_k, dh_v through the B^T rows), attention norm bwd
-  // (int8: qg16 carries the per-k scale, the packed B^T rows are stored / s')
   BSeg sq[2] = {wseg(w.wqkvT), hseg(shadow_ptr(l, sh_bt_qkv), 3 * kRank, NT)};
   const _Float16* a_qkv = shadow_rm + (size_t)l * shadow_per_layer + sh_a_qkv;
   const LoraTerm tbq[3] = {{a_qkv, 0, H, 0, H, 0},

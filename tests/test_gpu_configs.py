@@ -568,12 +568,11 @@ def _small_dims():
 def test_int8_zero_scale_channels_match_oracle(dev, batch, seq):
     """int8 weights with output channels whose fp16 scale is 0, in every
     projection: an all-zero row, and (q, k, v, o) a row below 4e-6 whose scale
-    rounds to 0 in fp16 while its int8 values do not.  The dX GEMMs take the
-    per-k scale from their operands' writers, which use a factor of 1 for such
-    a channel (0 would divide the LoRA B^T rows of the Q/K/V and O dX by zero)
-    and whose packed int8 rows are stored as zeros; the step matches the
-    oracle on the dequantised weights at T = 128 (small-M GEMMs) and T = 1024
-    (large tiles)."""
+    rounds to 0 in fp16 while its int8 values do not.  The forward applies the
+    scale per output row, the Q/K/V and O dX GEMMs per k, and the down and
+    gate/up dX operands carry it per column; the step matches the oracle on
+    the dequantised weights at T = 128 (small-M GEMMs) and T = 1024 (large
+    tiles)."""
     from oracle.configs import quantize_model_int8
     d = _small_dims()
     print(f"case: int8 zero-scale channels, B{batch} S{seq}", flush=True)
@@ -611,7 +610,7 @@ def test_int8_zero_scale_channels_match_oracle(dev, batch, seq):
 def test_int8_wide_qkv_rows_match_oracle(dev):
     """int8 weights with 32 query / 8 KV heads: the Q/K/V operand rows are
     6144 wide, past the 4096 the QK-norm backward writes eight columns a
-    thread, so its per-column int8 factors take the column-a-pass form."""
+    thread, so it takes its column-a-pass form."""
     d = ref.Dims(hidden=256, n_layers=1, n_heads=32, n_kv_heads=8, head_dim=128,
                  intermediate=512, vocab=2048)
     print("case: int8, 32/8 heads (Q + 2 KV = 6144), B2 S64", flush=True)
