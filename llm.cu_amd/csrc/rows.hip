@@ -321,7 +321,9 @@ constexpr int QH_ROWS = 16;
 __global__ __launch_bounds__(256) void qkv_post_kernel(const QkvPostArgs a, int T) {
   constexpr int RPW = QH_ROWS / 4;
   const int hh = blockIdx.x;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  // the wave index as a scalar: row bases are then SGPR pairs, not per-lane
+  // 64-bit address math
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int Q = a.nq * HD, KV = a.nkv * HD, NT = Q + 2 * KV;
   const int base = hh * HD;
   const int term = hh < a.nq ? 0 : (hh < a.nq + a.nkv ? 1 : 2);
@@ -1057,7 +1059,9 @@ __global__ __launch_bounds__(256) void o_dx_post_kernel(const RowIn in,
                                                         float* __restrict__ dsc) {
   constexpr int RPW = OD_ROWS / 4;
   const int h = blockIdx.x;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  // the wave index as a scalar: row bases are then SGPR pairs, not per-lane
+  // 64-bit address math
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int Q = nq * HD, col = h * HD + 2 * lane;
   const bool lora = in.nterm > 0;
   float b0[R], b1[R];
