@@ -583,16 +583,22 @@ __global__ __launch_bounds__(WNN * 128) void gemm_dma_kernel(const GemmArgs g, i
     const int col = n0 + wn * WC + j * 16 + (lane & 15);
     scj[j] = cs && col < g.N ? (float)cs[col] : 1.0f;
   }
+  // store addresses: a wave-uniform row base plus one 32-bit lane offset
+  // for all stores (the compiler then steps one 64-bit address by ldc, one
+  // add a store instead of a 64-bit multiply-add and an add: the fp16
+  // logits GEMM at C4 2429 -> 2370 us; the same for the SwiGLU epilogue's
+  // fp16 stores measured 1% slower)
+  const int lo = (lane >> 4) * 4 * g.ldc + (lane & 15);
+  float* const Cw = C + (long long)(m0 + wm * 128) * g.ldc + n0 + wn * WC;
 #pragma unroll
   for (int j = 0; j < NFR; ++j) {
-    const int col = n0 + wn * WC + j * 16 + (lane & 15);
-    if (col >= g.N) continue;
+    if (n0 + wn * WC + j * 16 >= g.N) continue;  // N % 16 == 0: whole fragments
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int row = m0 + wm * 128 + i * 16 + (lane >> 4) * 4 + v;
-        C[(long long)row * g.ldc + col] = acc[i][j][v] * scj[j];
+        float* const Cr = Cw + (long long)(i * 16 + v) * g.ldc + j * 16;
+        Cr[lo] = acc[i][j][v] * scj[j];
       }
   }
   if (g.rowstats) {
