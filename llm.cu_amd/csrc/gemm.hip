@@ -812,6 +812,9 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(const GemmArgs g) {
     }
     return;
   }
+  // a wave-uniform row base plus one 32-bit lane offset for every store
+  const int lo = (lane >> 4) * 4 * g.ldc + (lane & 15);
+  float* const Cw = C + (long long)(m0 + 2 * wr * 16) * g.ldc + n0;
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
     const int nn = n0 + 16 * j;
@@ -827,8 +830,8 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(const GemmArgs g) {
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int row = m0 + (2 * wr + i) * 16 + (lane >> 4) * 4 + v;
-        C[(long long)row * g.ldc + col] = acc[i][j][v] * sc;
+        float* const Cr = Cw + (long long)(i * 16 + v) * g.ldc + 16 * j;
+        Cr[lo] = acc[i][j][v] * sc;
       }
   }
 }
