@@ -429,8 +429,15 @@ __device__ __forceinline__ void dkdv_block(const AttnArgs& a, _Float16* buf0, _F
 // Small grids (the B1 x S128 step: 8 KV heads x 8 key blocks): the NW waves
 // of the workgroup all own the same 16 keys and split the group's
 // (query head, query tile) iterations between them (wave w takes it = w,
-// w + NW, ..), each through two LDS buffers of its own (no barriers in the
-// loop); their dK/dV sums meet in LDS at the end, in wave order.
+// w + NW, ..), each through LDS buffers of its own (no barriers in the
+// loop); their dK/dV sums meet in LDS at the end, in wave order.  Two waves
+// keep two buffers each (the next tile lands during the current one); four
+// waves one each (4 x 33.5 KB of LDS), refilled once the wave's reads of it
+// have returned -- at B1 x S128 (2 query heads x 2 tiles) each wave then
+// has a single iteration.
+template <int NW>
+constexpr int split_bufs() { return NW >= 4 ? 1 : 2; }
+
 template <int NW>
 __device__ __forceinline__ void dkdv_block_split(const AttnArgs& a, _Float16* smem, float* red,
                                                  int kb, int j, int b) {
@@ -446,7 +453,8 @@ __device__ __forceinline__ void dkdv_block_split(const AttnArgs& a, _Float16* sm
   const int qb0 = k0 / BLK;
   const int nqt = (S + BLK - 1) / BLK - qb0;
   const int niter = group * nqt;
-  _Float16* mine = smem + w * 2 * KV_BUF;
+  constexpr int NB = split_bufs<NW>();
+  _Float16* mine = smem + w * NB * KV_BUF;
   TileDma<1> dq_, dd_;
   dq_.init(a.ldq, 0);
   dd_.init(a.ld16, 0);
@@ -478,10 +486,15 @@ __device__ __forceinline__ void dkdv_block_split(const AttnArgs& a, _Float16* sm
   for (int it = w; it < niter; it += NW, ++n) {
     wait_vm<0>();  // this wave's own tile (its buffers are private)
     asm volatile("" ::: "memory");
-    if (it + NW < niter) issue(it + NW, mine + ((n + 1) & 1) * KV_BUF);
-    const _Float16* buf = mine + (n & 1) * KV_BUF;
+    if constexpr (NB == 2)
+      if (it + NW < niter) issue(it + NW, mine + ((n + 1) & 1) * KV_BUF);
+    const _Float16* buf = mine + (NB == 2 ? (n & 1) * KV_BUF : 0);
     const int qb = qb0 + it % nqt;
-    if (qb * BLK + BLK - 1 < k0) continue;
+    if (qb * BLK + BLK - 1 < k0) {
+      if constexpr (NB == 1)
+        if (it + NW < niter) issue(it + NW, mine);
+      continue;
+    }
     const _Float16* Qs = buf;
     const _Float16* Ds = buf + TILE;
     const float* lse_s = reinterpret_cast<const float*>(buf + 2 * TILE);
@@ -494,6 +507,13 @@ __device__ __forceinline__ void dkdv_block_split(const AttnArgs& a, _Float16* sm
     else
       kv_tile<true>(Qs, Ds, lse_s, del_s, dsc_s, kf, vf, dkT, dvT, sl2, gs, qb * BLK, k0 + c, S,
                     lane);
+    if constexpr (NB == 1) {
+      if (it + NW < niter) {  // one buffer: refill it once this tile's reads returned
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        asm volatile("" ::: "memory");
+        issue(it + NW, mine);
+      }
+    }
   }
   // waves 1 .. NW-1 hand their sums to wave 0, which adds them in order
   wait_vm<0>();
@@ -534,7 +554,7 @@ void attn_bwd_kernel(const AttnArgs a, int nkvb, int nqb) {
   // PART 0-2: the two tile buffers as separate arrays (statically named
   // buffers, see dq_block); PART 3: one array split per wave.
   constexpr int BUF = PART == 1 ? KV_BUF : PART == 2 ? 2 * TILE : BWD_BUF;
-  constexpr int SMEM3 = NW * 2 * KV_BUF > 4 * TILE ? NW * 2 * KV_BUF : 4 * TILE;
+  constexpr int SMEM3 = NW * split_bufs<NW>() * KV_BUF > 4 * TILE ? NW * split_bufs<NW>() * KV_BUF : 4 * TILE;
   __shared__ __attribute__((aligned(1024))) _Float16 buf0[PART == 3 ? SMEM3 : BUF];
   __shared__ __attribute__((aligned(1024))) _Float16 buf1[PART == 3 ? 8 : BUF];
   __shared__ float red[NW];
@@ -630,10 +650,10 @@ hipError_t attn_bwd(const AttnArgs& a, int B, hipStream_t st) {
   AttnShape s = attn_shape(B, a.S, a.nq);
   if (!getenv("LLMT_ATTN_CFG")) {
     if (!bwd_one_launch(a, B, dkdv_waves(B, a.S, a.nkv), s.nw, s.rw)) s.rw = 1;
-    // tiny grids (the B1 x S128 step): dK/dV blocks of 16 keys whose two
-    // waves split the group's query tiles, beside 32-query dQ blocks
+    // tiny grids (the B1 x S128 step): dK/dV blocks of 16 keys whose four
+    // waves split the group's query tiles, beside 64-query dQ blocks
     if (!getenv("LLMT_ATTN_DKDV_WAVES") && (long long)B * a.nq * ((a.S + 63) / 64) < 64) {
-      launch_bwd<2, 1, 3>(a, B, (a.S + 15) / 16, (a.S + 31) / 32, st);
+      launch_bwd<4, 1, 3>(a, B, (a.S + 15) / 16, (a.S + 63) / 64, st);
       LLMT_LAUNCH_CHECK();
       return hipSuccess;
     }
