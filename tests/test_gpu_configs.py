@@ -294,6 +294,43 @@ def test_c0_single_layer(dev):
         ctx.close()
 
 
+def test_c0_single_layer_int8(dev):
+    """C0's layer on int8 weights through llmt_layer_forward /
+    llmt_layer_backward: the layer API's input-gradient rows (grad_rows) carry
+    the down projection's per-k weight scale into the down dX operand; output,
+    input gradient and adapter gradients against the oracle on the
+    dequantised weights."""
+    from oracle.quant import quantize_rows
+    print("case: C0 one layer int8 weights, B1 x S128 (layer API)", flush=True)
+    d1, lw, ad, x, dy = config0()
+    names = ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")
+    qs = {}
+    for n in names:
+        q, sc = quantize_rows(getattr(lw, n).float().numpy())
+        sc16 = sc.astype(np.float16)
+        qs[n] = (q, sc16)
+        setattr(lw, n, torch.from_numpy(q.astype(np.float32) * sc16.astype(np.float32)[:, None]))
+    cos, sin = ref.rope_tables(128, d1.head_dim, d1.theta)
+    y_ref, st = ref.layer_forward(x, lw, ad, d1, 1, 128, cos, sin)
+    dx_ref, grads_ref = ref.layer_backward(dy, st, lw, ad, d1, 1, 128, cos, sin)
+    ctx = llmt.Context(llmt.make_dims(d1), 1, 128, int8=True)
+    try:
+        f = lambda t: t.to(torch.float32).to(dev).contiguous()
+        ctx.set_layer_i8(0, [torch.from_numpy(qs[n][0]).to(dev) for n in names],
+                         [torch.from_numpy(qs[n][1]).to(dev) for n in names],
+                         f(lw.attn_norm), f(lw.ffn_norm), f(lw.q_norm), f(lw.k_norm))
+        ctx.lora_set("param", llmt.flatten_adapters([ad]).to(dev))
+        y = ctx.layer_forward(0, x.to(dev), 1)
+        assert rel_l2(y.cpu(), y_ref) < GRAD_TOL
+        dx = ctx.layer_backward(0, dy.to(dev), 1)
+        assert rel_l2(dx.cpu(), dx_ref) < GRAD_TOL
+        errs = grad_errors(ctx.lora_get("grad"), [grads_ref], d1)
+        print("C0 int8 worst", max(errs.items(), key=lambda kv: kv[1]), flush=True)
+        assert max(errs.values()) < GRAD_TOL
+    finally:
+        ctx.close()
+
+
 # ------------------------------------------------------------------ C1
 
 @pytest.mark.parametrize("via_ctx", [False, True])
