@@ -1385,7 +1385,9 @@ inline unsigned grid_elems(long long n) {
 // o_post 52.8 / 32.1 / 30.5 / 35.3, norm_bwd with the three adapter terms
 // 82.3 / 76.7 / 68.0 / 58.7 (its 196 KB of adapter values per workgroup).
 // At short T (the B1 x S128 step) one row a workgroup keeps more CUs busy,
-// except for resid_norm (4.84 against 4.39 us at two rows, 128 rows).
+// except for resid_norm (4.84 against 4.39 us at two rows, 128 rows) and
+// o_post (5.95 against 5.70 us; norm_bwd 5.0 / 5.9 / 9.0, with the adapter
+// terms 8.4 / 9.7 / 13.0 at 1 / 2 / 4 rows).
 // LLMT_ROWS_PER_WG (1, 2, 3, 4 or 8) overrides all of them.
 static int rows_per_wg(int T, int P, int large_t, int small_t = 1) {
   if (P != 1) return 1;
@@ -1475,7 +1477,7 @@ hipError_t o_post(const RowIn& in, const float* x_in, const float* w, float eps,
                   float* hbuf, float* x_mid, _Float16* xn2, hipStream_t st) {
   if (!row_in_ok(in, H, "o_post")) return hipErrorInvalidValue;
   const int P = (H + 4 * RT - 1) / (4 * RT);
-  const int nr = rows_per_wg(T, P, 4);
+  const int nr = rows_per_wg(T, P, 4, 2);
   const dim3 g((T + nr - 1) / nr);
   switch (P * 10 + nr) {
     case 11: hipLaunchKernelGGL((o_post_kernel<1>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2); break;
