@@ -139,19 +139,13 @@ __device__ __forceinline__ void load_row(const RowIn& in, int t, int n, float4 (
   }
 }
 
-template <int P, bool SC = false>
-__device__ __forceinline__ void load_partials(const RowIn& in, int t, int n, float4 (&v)[P]) {
-  float4 h;
-  load_row<P, false, 24, SC>(in, t, n, v, h);
-}
-
 // load_row with h, then mid() (more loads independent of the row), as one
 // memory round trip: for 2, 4 or 8 splits straight-line code issues every
 // split's loads, then mid(), then sums in split order (load_row's split
 // loop would wait for the loads issued before it); other counts take
 // load_row, then mid().  C2 (B1 x S128): the attention norm backward with
 // its adapter terms 8.5 -> 7.5 us, the FFN norm backward 5.1 -> 4.4 us.
-template <int P, int NS, typename F>
+template <int P, int NS, bool HH, typename F>
 __device__ __forceinline__ void load_row_ns(const RowIn& in, int t, int n, float4 (&v)[P],
                                             float4& h, F&& mid) {
   const float* prow = in.part + (long long)t * in.ldp;
@@ -168,29 +162,40 @@ __device__ __forceinline__ void load_row_ns(const RowIn& in, int t, int n, float
     const float* q = prow + (long long)i * in.ss;
 #pragma unroll
     for (int p = 0; p < P; ++p) x[i][p] = ld4(q + off[p]);
-    y[i] = ld4(q + hoff);
+    if (HH) y[i] = ld4(q + hoff);
   }
   mid();
 #pragma unroll
   for (int p = 0; p < P; ++p) v[p] = x[0][p];
-  h = y[0];
+  if (HH) h = y[0];
 #pragma unroll
   for (int i = 1; i < NS; ++i) {
 #pragma unroll
     for (int p = 0; p < P; ++p) v[p] = add4(v[p], x[i][p]);
-    h = add4(h, y[i]);
+    if (HH) h = add4(h, y[i]);
   }
 }
-template <int P, typename F>
+template <int P, bool HH = true, typename F>
 __device__ __forceinline__ void load_row_then(const RowIn& in, int t, int n, float4 (&v)[P],
                                               float4& h, F&& mid) {
   switch (in.split) {
-    case 2: load_row_ns<P, 2>(in, t, n, v, h, mid); break;
-    case 4: load_row_ns<P, 4>(in, t, n, v, h, mid); break;
-    case 8: load_row_ns<P, 8>(in, t, n, v, h, mid); break;
+    case 2: load_row_ns<P, 2, HH>(in, t, n, v, h, mid); break;
+    case 4: load_row_ns<P, 4, HH>(in, t, n, v, h, mid); break;
+    case 8: load_row_ns<P, 8, HH>(in, t, n, v, h, mid); break;
     default:
-      load_row<P, true>(in, t, n, v, h);
+      load_row<P, HH>(in, t, n, v, h);
       mid();
+  }
+}
+
+template <int P, bool SC = false>
+__device__ __forceinline__ void load_partials(const RowIn& in, int t, int n, float4 (&v)[P]) {
+  float4 h;
+  if constexpr (SC) {
+    load_row<P, false, 24, SC>(in, t, n, v, h);
+  } else {
+    auto none = []() {};
+    load_row_then<P, false>(in, t, n, v, h, none);
   }
 }
 
@@ -578,18 +583,17 @@ __device__ __forceinline__ void load_rows_ns(const RowIn& in, int t0, int T, int
       if (HH) h[i] = add4(h[i], y[k][i]);
     }
 }
-template <int NR, bool HH, typename F>
+// NS > 0: the NS-split straight-line form (the launch picks it for NR <= 2
+// and 4 or 8 splits); NS = 0: load_rows, then mid().
+template <int NR, bool HH, int NS, typename F>
 __device__ __forceinline__ void load_rows_then(const RowIn& in, int t0, int T, int n,
                                                float4 (&v)[NR], float4 (&h)[NR], F&& mid) {
-  if constexpr (NR <= 2) {
-    switch (in.split) {  // (at 2 splits, the large-T case, the loop measured faster)
-      case 4: load_rows_ns<NR, HH, 4>(in, t0, T, n, v, h, mid); return;
-      case 8: load_rows_ns<NR, HH, 8>(in, t0, T, n, v, h, mid); return;
-      default: break;
-    }
+  if constexpr (NS > 0) {
+    load_rows_ns<NR, HH, NS>(in, t0, T, n, v, h, mid);
+  } else {
+    load_rows<NR, HH>(in, t0, T, n, v, h);
+    mid();
   }
-  load_rows<NR, HH>(in, t0, T, n, v, h);
-  mid();
 }
 
 // NR block sums at once (one barrier pair).
@@ -618,7 +622,7 @@ __device__ __forceinline__ void block_sums(float (&a)[NR], float* red) {
 // adapter values (loaded once) every row.  (The one-row kernel spends a
 // round trip and three barrier phases a row; rows handled one after another
 // in a workgroup, adapter values loaded once, measured no faster than it.)
-template <int NR>
+template <int NR, int NS = 0>
 __global__ __launch_bounds__(RT) void o_post_rows_kernel(const RowIn in,
                                                          const float* __restrict__ x_in,
                                                          const float* __restrict__ w, float eps,
@@ -641,7 +645,7 @@ __global__ __launch_bounds__(RT) void o_post_rows_kernel(const RowIn in,
     wv = ld4(w + cc);
     lora_load<1, 1>(in, H, L);
   };
-  load_rows_then<NR, true>(in, t0, T, H, v, hv, mid);
+  load_rows_then<NR, true, NS>(in, t0, T, H, v, hv, mid);
 #pragma unroll
   for (int i = 0; i < NR; ++i) {
     store_h(in, hv[i], hs[i]);
@@ -690,7 +694,7 @@ __device__ __forceinline__ void block_maxes(float (&a)[NR], float* red) {
 
 // resid_norm for rows of one piece per thread at large T, NR rows a
 // workgroup side by side (as o_post_rows_kernel).
-template <int NR>
+template <int NR, int NS = 0>
 __global__ __launch_bounds__(RT) void resid_norm_rows_kernel(const RowIn in,
                                                              const float* __restrict__ x_res,
                                                              const float* __restrict__ w,
@@ -708,7 +712,7 @@ __global__ __launch_bounds__(RT) void resid_norm_rows_kernel(const RowIn in,
   float4 v[NR], hv[NR];
   float4 wv;
   auto mid = [&]() __attribute__((always_inline)) { wv = ld4(w + cc); };
-  load_rows_then<NR, false>(in, t0, T, H, v, hv, mid);
+  load_rows_then<NR, false, NS>(in, t0, T, H, v, hv, mid);
   float ssq[NR];
 #pragma unroll
   for (int i = 0; i < NR; ++i) {
@@ -1598,7 +1602,15 @@ hipError_t o_post(const RowIn& in, const float* x_in, const float* w, float eps,
   const dim3 g((T + nr - 1) / nr);
   switch (P * 10 + nr) {
     case 11: hipLaunchKernelGGL((o_post_kernel<1>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2); break;
-    case 12: hipLaunchKernelGGL((o_post_rows_kernel<2>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T); break;
+    case 12:
+      // (4 or 8 split partials: every load of the two rows in one round trip)
+      if (in.split == 4)
+        hipLaunchKernelGGL((o_post_rows_kernel<2, 4>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T);
+      else if (in.split == 8)
+        hipLaunchKernelGGL((o_post_rows_kernel<2, 8>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T);
+      else
+        hipLaunchKernelGGL((o_post_rows_kernel<2>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T);
+      break;
     case 13: hipLaunchKernelGGL((o_post_rows_kernel<3>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T); break;
     case 14: hipLaunchKernelGGL((o_post_rows_kernel<4>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T); break;
     case 18: hipLaunchKernelGGL((o_post_rows_kernel<8>), g, dim3(RT), 0, st, in, x_in, w, eps, H, hbuf, x_mid, xn2, T); break;
@@ -1629,7 +1641,14 @@ hipError_t resid_norm(const RowIn& in, const float* x_res, const float* w, float
   const dim3 g((T + nr - 1) / nr);
   switch (P * 10 + nr) {
     case 11: hipLaunchKernelGGL(resid_norm_kernel<1>, g, dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn); break;
-    case 12: hipLaunchKernelGGL(resid_norm_rows_kernel<2>, g, dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn, T); break;
+    case 12:
+      if (in.split == 4)
+        hipLaunchKernelGGL((resid_norm_rows_kernel<2, 4>), g, dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn, T);
+      else if (in.split == 8)
+        hipLaunchKernelGGL((resid_norm_rows_kernel<2, 8>), g, dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn, T);
+      else
+        hipLaunchKernelGGL(resid_norm_rows_kernel<2>, g, dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn, T);
+      break;
     case 13: hipLaunchKernelGGL(resid_norm_rows_kernel<3>, g, dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn, T); break;
     case 14: hipLaunchKernelGGL(resid_norm_rows_kernel<4>, g, dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn, T); break;
     case 18: hipLaunchKernelGGL(resid_norm_rows_kernel<8>, g, dim3(RT), 0, st, in, x_res, w, eps, H, x_out, xn, T); break;
