@@ -504,6 +504,28 @@ def test_c4_int8_reduced_matches_oracle(dev):
         ctx.close()
 
 
+def test_gqa_8_4_heads_t128_matches_oracle(dev):
+    """Full width with 8 query / 4 KV heads at B1 x S128: the Q/K/V GEMM
+    (N = 2096) takes four split partials, so qkv_post's four-split form runs
+    (C2's own shapes give it two); loss and every adapter gradient against
+    the oracle (vocabulary 8192 keeps the CPU oracle to seconds)."""
+    print("case: H 2048, 8/4 heads, 2 layers, B1 S128, V 8192", flush=True)
+    d = ref.Dims(n_layers=2, n_heads=8, n_kv_heads=4, vocab=8192)
+    W, ad, tok, tgt, _ = config_model(d, batch=1, seq_len=128, seed=1021)
+    loss_ref, grads_ref, _ = oracle_grads(W, ad, tok, tgt, d)
+    ctx = llmt.Context(llmt.make_dims(d), 1, 128)
+    try:
+        upload_model(ctx, W, dev)
+        ctx.lora_set("param", llmt.flatten_adapters(ad).to(dev))
+        loss = ctx.forward_backward(tok.to(dev), tgt.to(dev))
+        assert abs(loss - float(loss_ref)) < LOSS_TOL
+        errs = grad_errors(ctx.lora_get("grad"), grads_ref, d)
+        print("8/4 heads worst", max(errs.items(), key=lambda kv: kv[1]), flush=True)
+        assert max(errs.values()) < GRAD_TOL
+    finally:
+        ctx.close()
+
+
 def test_c4_int8_large_tile_full_width_matches_oracle(dev):
     """C4's token count (B8 x S512 = 4096 rows) on the large-tile path
     (gemm_dma_kernel with per-row and per-k int8 scales, the fused SwiGLU
